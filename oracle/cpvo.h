@@ -1,0 +1,170 @@
+/*
+ * cpvo — CPU oracle for the codpiece verify step.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker: tests/, the smoke
+ * entry point and bench.py's cpu_baseline leg may load it; the product path
+ * (codpiece_amd/, libcpv.so) never links, loads or calls it.
+ *
+ * It restates, in plain C, the arithmetic the reference's verify step relies
+ * on.  The reference runs that arithmetic in ggml b10423 (not vendored, so not
+ * buildable here) driven from Rust (no Rust toolchain here), so every
+ * function below cites the reference call site it follows and states the
+ * exact float contract it implements.  The GPU kernels implement the same
+ * contracts; parity tests compare the two bit for bit where the contract is
+ * exact, and against a tolerance where it is not (attention).
+ *
+ * Contracts (one line each; details at each function):
+ *  - fp16 <-> fp32: IEEE binary16, round-to-nearest-even.
+ *  - weights: ggml block formats Q8_0 / Q4_K / Q6_K (GGUF type ids 8/12/14).
+ *  - activations: quantized as ggml's CPU vec_dot_type does — Q8_0 for Q8_0
+ *    weights, Q8_K for K-quants.
+ *  - qgemm: per block integer dots (exact), per block f64 scale products,
+ *    summed EXACTLY in an int64 fixed-point window, rounded once per output.
+ *    The result is independent of any summation order.
+ *  - rms_norm: exact fixed-point sum of f32 squares, then ggml's f32 tail.
+ *  - rope: NEOX pairs with ggml's f32 theta recurrence; cos/sin from libm.
+ *  - attention: Q rounded to f16 (ggml CPU FA), scores/softmax/output in f64.
+ *  - sampler: bit-faithful restatement of crates/codpiece-sample/src/lib.rs.
+ *  - exp: cpvo_expf, a restatement of libm's expf equal to it on every input.
+ *  - Philox4x64-10 (Salmon et al., SC'11) for explicit uniforms.
+ */
+#ifndef CPVO_H
+#define CPVO_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGUF tensor type ids (crates/codpiece-gguf/src/lib.rs:173-185). */
+enum { CPVO_F32 = 0, CPVO_F16 = 1, CPVO_Q8_0 = 8, CPVO_Q4_K = 12, CPVO_Q6_K = 14, CPVO_Q8_K = 15 };
+
+#pragma pack(push, 1)
+typedef struct { uint16_t d; int8_t qs[32]; } cpvo_block_q8_0;                       /* 34 B  */
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } cpvo_block_q4_K; /* 144 B */
+typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } cpvo_block_q6_K; /* 210 B */
+typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } cpvo_block_q8_K;      /* 292 B */
+#pragma pack(pop)
+
+/* ---- scalar helpers ---------------------------------------------------- */
+uint16_t cpvo_fp32_to_fp16(float f);
+float    cpvo_fp16_to_fp32(uint16_t h);
+void     cpvo_fp32_to_fp16_n(const float* x, int64_t n, uint16_t* y);
+void     cpvo_fp16_to_fp32_n(const uint16_t* x, int64_t n, float* y);
+float    cpvo_expf(float x);
+void     cpvo_expf_n(const float* x, int64_t n, float* y);
+void     cpvo_exp_table(uint64_t out[32]);   /* the 2^(i/32) table cpvo_expf uses */
+/* count x in [lo, hi] (as float bit patterns, stepping every `stride` values)
+ * where cpvo_expf(x) != libm expf(x); returns the number of mismatches. */
+int64_t  cpvo_expf_vs_libm(float lo, float hi, int64_t stride);
+
+/* ---- RNGs --------------------------------------------------------------- */
+void     cpvo_philox4x64(const uint64_t ctr[4], const uint64_t key[2], uint64_t out[4]);
+float    cpvo_u01(uint64_t x);                       /* (x >> 40) / 2^24, as next_f32 */
+/* u[b][j][r] = cpvo_u01(philox((b, j, r, 0), (seed, 0))[0]) for j in [0,k], r in {0,1} */
+void     cpvo_philox_uniforms(uint64_t seed, int B, int k, float* u);
+/* xoshiro256++ seeded by splitmix64 (crates/codpiece-sample/src/lib.rs:88-130) */
+void     cpvo_rng_seed(uint64_t seed, uint64_t s[4]);
+uint64_t cpvo_rng_next_u64(uint64_t s[4]);
+float    cpvo_rng_next_f32(uint64_t s[4]);
+
+/* ---- block formats ------------------------------------------------------ */
+int64_t  cpvo_type_block(int type);                 /* elements per block */
+int64_t  cpvo_type_size(int type);                  /* bytes per block   */
+int64_t  cpvo_row_bytes(int type, int64_t k);       /* -1 if k not block-aligned */
+int      cpvo_quantize(int type, const float* x, int64_t n, void* out);
+int      cpvo_dequantize(int type, const void* q, int64_t n, float* y);
+/* activation quantizers (ggml quantize_row_q8_0_ref / quantize_row_q8_K_ref) */
+void     cpvo_quantize_q8_0(const float* x, int64_t n, cpvo_block_q8_0* y);
+void     cpvo_quantize_q8_K(const float* x, int64_t n, cpvo_block_q8_K* y);
+
+/* ---- GEMM --------------------------------------------------------------- */
+/* Y[M][N] = X[M][K] . dequant(W[N][K])^T in ggml's mul_mat convention
+ * (ne: [K,N] x [K,M] -> [N,M], crates/codpiece-ggml-sys/tests/smoke.rs:19).
+ * W is N rows of ggml blocks.  Returns 0, or -1 for an unsupported type / K. */
+int      cpvo_qgemm(int type, const void* w, int64_t N, int64_t K,
+                    const float* x, int64_t M, float* y, int n_threads);
+/* plain f32 mul_mat (smoke.rs known answer) */
+void     cpvo_mul_mat_f32(const float* w, int64_t N, int64_t K, const float* x,
+                          int64_t M, float* y);
+/* f64 reference of the same product over dequantized operands (no rounding
+ * beyond the quantizers) — used to bound the exact contract. */
+int      cpvo_qgemm_f64(int type, const void* w, int64_t N, int64_t K,
+                        const float* x, int64_t M, double* y, int n_threads);
+/* window exponent helpers shared with the tests */
+int      cpvo_qgemm_window(int type, int64_t K);
+
+/* ---- glue ops ----------------------------------------------------------- */
+void     cpvo_rms_norm(const float* x, int64_t n, float eps, const float* w, float* y);
+/* cs[p][i][0..1] = (cos, sin) of pos p for pair i, ggml's theta recurrence */
+void     cpvo_rope_table(int n_pos, int n_rot, float freq_base, float* cs);
+/* the same with IMROPE's interleaved sections (positions (p, p, p, 0)) */
+void     cpvo_rope_table_sections(int n_pos, int n_rot, float freq_base, const int32_t* sections,
+                                  float* cs);
+/* rotate one head vector of length hd in place (NEOX pairs over n_rot dims) */
+void     cpvo_rope_neox(float* x, int n_rot, const float* cs_row);
+
+/* masked GQA attention over an f16 cache.
+ * q: [T][H][D] f32; kc, vc: [n_ctx][Hkv*D] f16; rows [0, n_past) are context,
+ * rows n_past + t hold node t.  parent: [T] tree parents (-1 = root, i.e. a
+ * child of the context), or NULL for a linear chain.  Node t sees all context
+ * rows plus its ancestors and itself.  out: [T][H*D]. */
+void     cpvo_attn(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n_past,
+                   const int32_t* parent, int T, int H, int Hkv, int D, float scale,
+                   float* out);
+
+/* ---- sampler (crates/codpiece-sample/src/lib.rs) ------------------------ */
+typedef struct {
+    float   temp;
+    int32_t top_k;
+    float   top_p;
+    float   min_p;
+    int32_t min_keep;
+    float   penalty_repeat;
+    float   penalty_freq;
+    float   penalty_present;
+    int32_t penalty_last_n;
+} cpvo_sampler_params;
+
+/* Sampler::distribution (lib.rs:184-187, build :229-376).  hist: the penalty
+ * window, oldest first (already capped at penalty_last_n).  Writes the
+ * candidate ids and probabilities in candidate order; tlogit (optional) gets
+ * the tempered logits build() leaves behind.  Returns the candidate count. */
+int      cpvo_distribution(const cpvo_sampler_params* p, const float* logits, int V,
+                           const int32_t* hist, int n_hist,
+                           int32_t* ids, float* probs, float* tlogit);
+int32_t  cpvo_dist_draw(const int32_t* ids, const float* probs, int n, float r);
+int32_t  cpvo_dist_draw_excluding(const int32_t* ids, const float* probs, int n,
+                                  int32_t token, float r);
+float    cpvo_dist_prob_of(const int32_t* ids, const float* probs, int n, int32_t token);
+float    cpvo_dist_peak(const float* probs, int n);
+int32_t  cpvo_sample_coupled(const cpvo_sampler_params* p, const float* logits, int V,
+                             const int32_t* hist, int n_hist, const float* noise_t);
+int32_t  cpvo_argmax(const float* x, int64_t n);
+
+/* ---- acceptance (crates/codpiece-server/src/engine.rs:2326-2461) -------- */
+enum { CPVO_ACCEPT_GREEDY = 0, CPVO_ACCEPT_REJECT = 1, CPVO_ACCEPT_GUMBEL = 2 };
+/* p_logits [B][k+1][V]; q_logits [B][k][V] or NULL (point-mass drafts, the
+ * reference rule); draft [B][k]; u [B][k+1][2] uniforms by role (r0 = accept
+ * roll / bonus draw, r1 = residual draw); noise_t [B][k+1][V] (gumbel mode);
+ * hist [B][hist_len] (oldest first, -1 = empty slot).  out_tok [B][k+1],
+ * out_n [B] = number of accepted drafts; out_tok[b][0..out_n] are valid. */
+int      cpvo_spec_accept(const float* p_logits, const float* q_logits, const int32_t* draft,
+                          int B, int k, int V, const cpvo_sampler_params* p, int mode,
+                          const float* u, const float* noise_t,
+                          const int32_t* hist, int hist_len,
+                          int32_t* out_tok, int32_t* out_n);
+/* The engine loop verbatim for one sequence with the reference's sequential
+ * RNG (point-mass drafts).  Records the uniform consumed for each role in
+ * u_used [k+1][2] (NaN where none was drawn).  Returns n_accept. */
+int      cpvo_spec_accept_rng(const float* p_logits, const int32_t* draft, int k, int V,
+                              const cpvo_sampler_params* p, uint64_t rng[4],
+                              const int32_t* hist, int n_hist,
+                              int32_t* out_tok, float* u_used);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
