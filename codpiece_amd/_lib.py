@@ -1,0 +1,91 @@
+"""ctypes binding of libcpv.so — the C ABI declared in include/cpv.h.
+
+This is the binding a host maintainer would write over the library; it loads the
+in-tree build and fails loudly when it is missing.  There is no fallback path:
+every compute call goes through the HIP library.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libcpv.so")
+
+CPV_OK, CPV_EINVAL, CPV_ENOMEM, CPV_EDEVICE, CPV_EUNSUPPORTED = 0, 1, 2, 3, 4
+F32, F16, Q8_0, Q4_K, Q6_K = 0, 1, 8, 12, 14
+ACCEPT_GREEDY, ACCEPT_REJECT, ACCEPT_GUMBEL = 0, 1, 2
+
+STATUS_NAMES = {0: "CPV_OK", 1: "CPV_EINVAL", 2: "CPV_ENOMEM", 3: "CPV_EDEVICE", 4: "CPV_EUNSUPPORTED"}
+
+
+class CpvError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {msg}")
+        self.status = status
+
+
+class SamplerParams(ctypes.Structure):
+    """cpv_sampler_params: SamplerParams of crates/codpiece-sample/src/lib.rs:29-64
+    without the seed (uniforms are explicit)."""
+    _fields_ = [
+        ("temp", ctypes.c_float),
+        ("top_k", ctypes.c_int32),
+        ("top_p", ctypes.c_float),
+        ("min_p", ctypes.c_float),
+        ("min_keep", ctypes.c_int32),
+        ("penalty_repeat", ctypes.c_float),
+        ("penalty_freq", ctypes.c_float),
+        ("penalty_present", ctypes.c_float),
+        ("penalty_last_n", ctypes.c_int32),
+    ]
+
+    def __init__(self, temp=0.0, top_k=0, top_p=1.0, min_p=0.0, min_keep=1,
+                 penalty_repeat=1.0, penalty_freq=0.0, penalty_present=0.0, penalty_last_n=64):
+        super().__init__(temp, top_k, top_p, min_p, min_keep, penalty_repeat, penalty_freq,
+                         penalty_present, penalty_last_n)
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_INT = ctypes.c_int
+_F32 = ctypes.c_float
+
+# name -> (restype, argtypes); kept in the order of include/cpv.h
+SIGNATURES = {
+    "cpv_init": (_INT, [_INT, ctypes.POINTER(_P)]),
+    "cpv_free": (None, [_P]),
+    "cpv_last_error": (ctypes.c_char_p, [_P]),
+    "cpv_set_stream": (_INT, [_P, _P]),
+    "cpv_get_stream": (_P, [_P]),
+    "cpv_sync": (_INT, [_P]),
+    "cpv_weight_upload": (_INT, [_P, _INT, _P, _I64, _I64, ctypes.POINTER(_P)]),
+    "cpv_weight_from_device": (_INT, [_P, _INT, _P, _I64, _I64, ctypes.POINTER(_P)]),
+    "cpv_weight_free": (None, [_P]),
+    "cpv_weight_info": (_INT, [_P, ctypes.POINTER(_INT), ctypes.POINTER(_I64), ctypes.POINTER(_I64),
+                               ctypes.POINTER(_I64)]),
+    "cpv_get_rows": (_INT, [_P, _P, _P, _I64, _P]),
+    "cpv_qgemm": (_INT, [_P, _P, _P, _I64, _P]),
+    "cpv_attn": (_INT, [_P, _P, _P, _P, _I64, _P, _INT, _INT, _INT, _INT, _F32, _P]),
+    "cpv_argmax_rows": (_INT, [_P, _P, _P, _I64, _I64, _P]),
+    "cpv_spec_accept": (_INT, [_P, _P, _P, _P, _INT, _INT, _INT, ctypes.POINTER(SamplerParams), _INT,
+                               _P, ctypes.c_uint64, _P, _P, _INT, _P, _P]),
+}
+
+_lib = None
+
+
+def load():
+    """Load libcpv.so and bind every entry point; raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() "
+                           "or python codpiece_amd/build.py")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib

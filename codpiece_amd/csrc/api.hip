@@ -1,0 +1,478 @@
+// api.hip — context, errors, weight upload/repack, get_rows, argmax.
+//
+// Weight repack.  ggml stores a quantized row as consecutive blocks (Q4_K 144 B,
+// Q6_K 210 B, Q8_0 34 B).  The GEMM kernel gives each lane of a wave one
+// 256-element unit of one of 16 rows (lane = row r + 16 * unit q) and walks the
+// row in passes of 4 units, so the repack orders the bytes the way one wave
+// instruction reads them: for each 16-row group and pass, piece-major, then
+// lane, 16 bytes per lane.  Every 128-bit load of the kernel is then a
+// contiguous 1 KiB read, whatever the block size, and rows / units are padded
+// with zero blocks (which contribute nothing) to whole groups and passes.
+//   Q4_K : [g][p][piece 0..7][lane] qs bytes 16*piece..  | [g][p][lane] d,dmin,scales
+//   Q6_K : [g][p][piece 0..12][lane] bytes 16*piece.. (ql, qh, scales) | [g][p][lane] d
+//   Q8_0 : [g][p][piece 0..15][lane] block piece/2, qs half piece%2 | [g][p][lane] 8 x d
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "cpv_internal.h"
+
+// ---------------------------------------------------------------- errors
+cpv_status cpv_fail(cpv_ctx* ctx, cpv_status st, const char* fmt, ...)
+{
+    if (ctx) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        ctx->err = buf;
+    }
+    return st;
+}
+
+cpv_status cpv_hip_fail(cpv_ctx* ctx, hipError_t e, const char* what)
+{
+    if (e == hipErrorOutOfMemory) {
+        (void)hipGetLastError();
+        return cpv_fail(ctx, CPV_ENOMEM, "%s: out of device memory", what);
+    }
+    return cpv_fail(ctx, CPV_EDEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+int64_t cpv_type_block(int type)
+{
+    switch (type) {
+    case CPV_Q8_0: return 32;
+    case CPV_Q4_K: case CPV_Q6_K: return 256;
+    case CPV_F32: case CPV_F16: return 1;
+    default: return -1;
+    }
+}
+
+int64_t cpv_type_size(int type)
+{
+    switch (type) {
+    case CPV_Q8_0: return 34;
+    case CPV_Q4_K: return 144;
+    case CPV_Q6_K: return 210;
+    case CPV_F32: return 4;
+    case CPV_F16: return 2;
+    default: return -1;
+    }
+}
+
+// ---------------------------------------------------------------- context
+extern "C" cpv_status cpv_init(int device, cpv_ctx** out)
+{
+    if (!out) return CPV_EINVAL;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return CPV_EDEVICE;
+    if (hipSetDevice(device) != hipSuccess) return CPV_EDEVICE;
+    cpv_ctx* c = new (std::nothrow) cpv_ctx();
+    if (!c) return CPV_ENOMEM;
+    c->device = device;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) { delete c; return CPV_EDEVICE; }
+    c->cu_count = prop.multiProcessorCount;
+    c->lds_max = prop.sharedMemPerBlock;
+    if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return CPV_EDEVICE;
+    }
+    c->stream = c->own_stream;
+    *out = c;
+    return CPV_OK;
+}
+
+extern "C" void cpv_free(cpv_ctx* ctx)
+{
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+}
+
+extern "C" const char* cpv_last_error(const cpv_ctx* ctx)
+{
+    return ctx ? ctx->err.c_str() : "null context";
+}
+
+extern "C" cpv_status cpv_set_stream(cpv_ctx* ctx, void* s)
+{
+    if (!ctx) return CPV_EINVAL;
+    ctx->stream = (hipStream_t)s;
+    return CPV_OK;
+}
+
+extern "C" void* cpv_get_stream(const cpv_ctx* ctx)
+{
+    return ctx ? (void*)ctx->stream : nullptr;
+}
+
+extern "C" cpv_status cpv_sync(cpv_ctx* ctx)
+{
+    if (!ctx) return CPV_EINVAL;
+    CPV_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return CPV_OK;
+}
+
+cpv_status cpv_workspace(cpv_ctx* ctx, size_t bytes, void** out)
+{
+    if (bytes <= ctx->ws_bytes) {
+        *out = ctx->ws;
+        return CPV_OK;
+    }
+    if (ctx->ws) {
+        CPV_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        CPV_HIP(ctx, hipFree(ctx->ws));
+        ctx->ws = nullptr;
+        ctx->ws_bytes = 0;
+    }
+    size_t sz = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+    CPV_HIP(ctx, hipMalloc(&ctx->ws, sz));
+    ctx->ws_bytes = sz;
+    *out = ctx->ws;
+    return CPV_OK;
+}
+
+// ---------------------------------------------------------------- repack
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return cpv_h2f(h); }
+
+template <int TYPE>
+__global__ void repack_kernel(const uint8_t* __restrict__ aos, uint8_t* __restrict__ out, int64_t n,
+                              int64_t k, int64_t P, int64_t total)
+{
+    constexpr int PIECES = TYPE == CPV_Q4_K ? 8 : TYPE == CPV_Q6_K ? 13 : 16;
+    constexpr int BSZ = TYPE == CPV_Q4_K ? 144 : TYPE == CPV_Q6_K ? 210 : 34;
+    constexpr int BLK = TYPE == CPV_Q8_0 ? 32 : 256;
+    const int64_t nblk = k / BLK;
+    const int64_t rb = nblk * BSZ;
+    const int64_t groups = (n + 15) / 16;
+    const int64_t region_a = groups * P * PIECES * 1024;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t src = -1;
+        if (i < region_a) {
+            const int b = (int)(i & 15);
+            const int lane = (int)((i >> 4) & 63);
+            const int piece = (int)((i >> 10) % PIECES);
+            const int64_t gp = (i >> 10) / PIECES;
+            const int64_t g = gp / P, p = gp % P;
+            const int64_t row = g * 16 + (lane & 15);
+            const int64_t unit = p * 4 + (lane >> 4);       // 256-element unit
+            if (row < n) {
+                if (TYPE == CPV_Q4_K) {
+                    if (unit < nblk) src = row * rb + unit * 144 + 16 + 16 * piece + b;
+                } else if (TYPE == CPV_Q6_K) {
+                    if (unit < nblk) src = row * rb + unit * 210 + 16 * piece + b;
+                } else {
+                    const int64_t blk = unit * 8 + piece / 2;
+                    if (blk < nblk) src = row * rb + blk * 34 + 2 + 16 * (piece & 1) + b;
+                }
+            }
+        } else {
+            const int64_t j = i - region_a;
+            if (TYPE == CPV_Q6_K) {
+                const int b = (int)(j & 1);
+                const int lane = (int)((j >> 1) & 63);
+                const int64_t gp = j >> 7;
+                const int64_t g = gp / P, p = gp % P;
+                const int64_t row = g * 16 + (lane & 15);
+                const int64_t unit = p * 4 + (lane >> 4);
+                if (row < n && unit < nblk) src = row * rb + unit * 210 + 208 + b;
+            } else {
+                const int b = (int)(j & 15);
+                const int lane = (int)((j >> 4) & 63);
+                const int64_t gp = j >> 10;
+                const int64_t g = gp / P, p = gp % P;
+                const int64_t row = g * 16 + (lane & 15);
+                const int64_t unit = p * 4 + (lane >> 4);
+                if (row < n) {
+                    if (TYPE == CPV_Q4_K) {
+                        if (unit < nblk) src = row * rb + unit * 144 + b;
+                    } else {
+                        const int64_t blk = unit * 8 + b / 2;
+                        if (blk < nblk) src = row * rb + blk * 34 + (b & 1);
+                    }
+                }
+            }
+        }
+        out[i] = src >= 0 ? aos[src] : 0;
+    }
+}
+
+// Ew(row): frexp exponent of the row's largest scale magnitude (d and dmin for
+// Q4_K, d for Q6_K / Q8_0; Q6_K's int8 group scales ride in the integer sum).
+template <int TYPE>
+__global__ void row_exponent_kernel(const uint8_t* __restrict__ aos, int32_t* __restrict__ ew,
+                                    int64_t n, int64_t n_pad, int64_t k)
+{
+    constexpr int BSZ = TYPE == CPV_Q4_K ? 144 : TYPE == CPV_Q6_K ? 210 : 34;
+    constexpr int BLK = TYPE == CPV_Q8_0 ? 32 : 256;
+    const int64_t nblk = k / BLK;
+    const int64_t row = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (row >= n_pad) return;
+    if (row >= n) { ew[row] = CPV_E_EMPTY; return; }
+    const uint8_t* r = aos + row * nblk * BSZ;
+    float mx = 0.0f;
+    for (int64_t b = 0; b < nblk; b++) {
+        const uint8_t* bl = r + b * BSZ;
+        if (TYPE == CPV_Q4_K) {
+            const uint16_t d = (uint16_t)(bl[0] | (bl[1] << 8)), dm = (uint16_t)(bl[2] | (bl[3] << 8));
+            mx = fmaxf(mx, fabsf(f16_to_f32(d)));
+            mx = fmaxf(mx, fabsf(f16_to_f32(dm)));
+        } else if (TYPE == CPV_Q6_K) {
+            const uint16_t d = (uint16_t)(bl[208] | (bl[209] << 8));
+            mx = fmaxf(mx, fabsf(f16_to_f32(d)));
+        } else {
+            const uint16_t d = (uint16_t)(bl[0] | (bl[1] << 8));
+            mx = fmaxf(mx, fabsf(f16_to_f32(d)));
+        }
+    }
+    int e = CPV_E_EMPTY;
+    if (mx > 0.0f) frexpf(mx, &e);
+    ew[row] = e;
+}
+
+static void weight_geometry(cpv_weight* w)
+{
+    const int64_t blk = cpv_type_block(w->type);
+    const int64_t units256 = (w->k + 255) / 256;
+    w->units = w->k / blk;
+    w->passes = (units256 + 3) / 4;
+    w->n_pad = (w->n + 15) / 16 * 16;
+    const int64_t slots = w->n_pad * w->passes * 4;   // 256-element slots
+    switch (w->type) {
+    case CPV_Q4_K: w->data_bytes = (size_t)slots * (128 + 16); break;
+    case CPV_Q6_K: w->data_bytes = (size_t)slots * (208 + 2); break;
+    default: w->data_bytes = (size_t)slots * (256 + 16); break;
+    }
+}
+
+cpv_status cpv_repack_launch(cpv_ctx* ctx, cpv_weight* w, const void* aos_dev)
+{
+    const int64_t total = (int64_t)w->data_bytes;
+    const int threads = 256;
+    const int64_t want = (total + threads - 1) / threads;
+    const int blocks = (int)(want < 65536 ? want : 65536);
+    const uint8_t* a = (const uint8_t*)aos_dev;
+    uint8_t* o = (uint8_t*)w->data;
+    const int eblocks = (int)((w->n_pad + 255) / 256);
+    switch (w->type) {
+    case CPV_Q4_K:
+        repack_kernel<CPV_Q4_K><<<blocks, threads, 0, ctx->stream>>>(a, o, w->n, w->k, w->passes, total);
+        row_exponent_kernel<CPV_Q4_K><<<eblocks, 256, 0, ctx->stream>>>(a, w->ew, w->n, w->n_pad, w->k);
+        break;
+    case CPV_Q6_K:
+        repack_kernel<CPV_Q6_K><<<blocks, threads, 0, ctx->stream>>>(a, o, w->n, w->k, w->passes, total);
+        row_exponent_kernel<CPV_Q6_K><<<eblocks, 256, 0, ctx->stream>>>(a, w->ew, w->n, w->n_pad, w->k);
+        break;
+    default:
+        repack_kernel<CPV_Q8_0><<<blocks, threads, 0, ctx->stream>>>(a, o, w->n, w->k, w->passes, total);
+        row_exponent_kernel<CPV_Q8_0><<<eblocks, 256, 0, ctx->stream>>>(a, w->ew, w->n, w->n_pad, w->k);
+        break;
+    }
+    CPV_HIP(ctx, hipGetLastError());
+    return CPV_OK;
+}
+
+static cpv_status weight_create(cpv_ctx* ctx, int type, const void* bytes, bool on_device, int64_t n,
+                                int64_t k, cpv_weight** out)
+{
+    if (!ctx || !bytes || !out || n <= 0 || k <= 0) return cpv_fail(ctx, CPV_EINVAL, "weight: bad arguments");
+    *out = nullptr;
+    if (type != CPV_Q8_0 && type != CPV_Q4_K && type != CPV_Q6_K)
+        return cpv_fail(ctx, CPV_EUNSUPPORTED, "weight: type %d not supported (Q8_0, Q4_K, Q6_K)", type);
+    const int64_t blk = cpv_type_block(type);
+    if (k % blk) return cpv_fail(ctx, CPV_EINVAL, "weight: k=%lld not a multiple of %lld", (long long)k, (long long)blk);
+    CPV_HIP(ctx, hipSetDevice(ctx->device));
+    cpv_weight* w = new (std::nothrow) cpv_weight();
+    if (!w) return cpv_fail(ctx, CPV_ENOMEM, "weight: host allocation");
+    w->ctx = ctx;
+    w->type = type;
+    w->n = n;
+    w->k = k;
+    weight_geometry(w);
+    const size_t aos_bytes = (size_t)n * (size_t)(k / blk) * (size_t)cpv_type_size(type);
+    void* tmp = nullptr;
+    hipError_t e = hipMalloc(&w->data, w->data_bytes);
+    if (e == hipSuccess) e = hipMalloc((void**)&w->ew, sizeof(int32_t) * (size_t)w->n_pad);
+    if (e == hipSuccess && !on_device) e = hipMalloc(&tmp, aos_bytes);
+    if (e == hipSuccess && !on_device) e = hipMemcpyAsync(tmp, bytes, aos_bytes, hipMemcpyHostToDevice, ctx->stream);
+    cpv_status st = CPV_OK;
+    if (e != hipSuccess) st = cpv_hip_fail(ctx, e, "weight upload");
+    if (st == CPV_OK) st = cpv_repack_launch(ctx, w, on_device ? bytes : tmp);
+    if (tmp) {
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipFree(tmp);
+    }
+    if (st != CPV_OK) {
+        if (w->data) (void)hipFree(w->data);
+        if (w->ew) (void)hipFree(w->ew);
+        delete w;
+        return st;
+    }
+    *out = w;
+    return CPV_OK;
+}
+
+extern "C" cpv_status cpv_weight_upload(cpv_ctx* ctx, int type, const void* host_bytes, int64_t n_rows,
+                                        int64_t k, cpv_weight** out)
+{
+    return weight_create(ctx, type, host_bytes, false, n_rows, k, out);
+}
+
+extern "C" cpv_status cpv_weight_from_device(cpv_ctx* ctx, int type, const void* dev_bytes, int64_t n_rows,
+                                             int64_t k, cpv_weight** out)
+{
+    return weight_create(ctx, type, dev_bytes, true, n_rows, k, out);
+}
+
+extern "C" void cpv_weight_free(cpv_weight* w)
+{
+    if (!w) return;
+    if (w->ctx) {
+        (void)hipSetDevice(w->ctx->device);
+        (void)hipStreamSynchronize(w->ctx->stream);
+    }
+    if (w->data) (void)hipFree(w->data);
+    if (w->ew) (void)hipFree(w->ew);
+    delete w;
+}
+
+extern "C" cpv_status cpv_weight_info(const cpv_weight* w, int* type, int64_t* n_rows, int64_t* k,
+                                      int64_t* bytes)
+{
+    if (!w) return CPV_EINVAL;
+    if (type) *type = w->type;
+    if (n_rows) *n_rows = w->n;
+    if (k) *k = w->k;
+    if (bytes) *bytes = (int64_t)w->data_bytes;
+    return CPV_OK;
+}
+
+// ---------------------------------------------------------------- get_rows
+// Dequantize from the repacked layout with ggml's f32 formulas:
+//   Q8_0: q * d;  Q4_K: (d*sc)*q - (dmin*m);  Q6_K: d*sc*q, left to right.
+template <int TYPE>
+__global__ void get_rows_kernel(const uint8_t* __restrict__ data, const int32_t* __restrict__ rows,
+                                int64_t nrows, int64_t n, int64_t k, int64_t P, float* __restrict__ out)
+{
+    const int64_t r_out = blockIdx.y;
+    if (r_out >= nrows) return;
+    const int64_t row = rows[r_out];
+    const int64_t groups = (n + 15) / 16;
+    for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < k; e += (int64_t)gridDim.x * blockDim.x) {
+        float v = 0.0f;
+        if (row >= 0 && row < n) {
+            const int64_t g = row / 16, r = row % 16;
+            const int64_t unit = e / 256, p = unit / 4, q = unit % 4;
+            const int lane = (int)(r + 16 * q);
+            const int el = (int)(e % 256);
+            if (TYPE == CPV_Q4_K) {
+                const int64_t region_a = groups * P * 8 * 1024;
+                const uint8_t* meta = data + region_a + ((g * P + p) * 64 + lane) * 16;
+                const int c = el / 64, l = el % 32, hi = (el % 64) >= 32;
+                const int qsbyte = c * 32 + l;
+                const uint8_t byte = data[((g * P + p) * 8 + qsbyte / 16) * 1024 + lane * 16 + qsbyte % 16];
+                const int code = hi ? (byte >> 4) : (byte & 15);
+                const int j = el / 32;
+                const uint8_t* s = meta + 4;
+                int sc, m;
+                if (j < 4) { sc = s[j] & 63; m = s[j + 4] & 63; }
+                else { sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4); m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
+                const float d = f16_to_f32((uint16_t)(meta[0] | (meta[1] << 8)));
+                const float dm = f16_to_f32((uint16_t)(meta[2] | (meta[3] << 8)));
+                const float d1 = d * (float)sc, m1 = dm * (float)m;
+                v = d1 * (float)code - m1;
+            } else if (TYPE == CPV_Q6_K) {
+                const int64_t region_a = groups * P * 13 * 1024;
+                auto bytei = [&](int idx) {
+                    return data[((g * P + p) * 13 + idx / 16) * 1024 + lane * 16 + idx % 16];
+                };
+                const int h = el / 128, l = el % 128, l32 = l % 32, quad = l / 32;
+                const uint8_t ql = bytei(h * 64 + l32 + (quad & 1) * 32);
+                const uint8_t qh = bytei(128 + h * 32 + l32);
+                const int lo = (quad < 2) ? (ql & 15) : (ql >> 4);
+                const int code = (lo | (((qh >> (2 * quad)) & 3) << 4)) - 32;
+                const int8_t sc = (int8_t)bytei(192 + el / 16);
+                const uint8_t* dd = data + region_a + ((g * P + p) * 64 + lane) * 2;
+                const float d = f16_to_f32((uint16_t)(dd[0] | (dd[1] << 8)));
+                v = d * (float)sc * (float)code;
+            } else {
+                const int64_t region_a = groups * P * 16 * 1024;
+                const int blk = el / 32, bi = el % 32;
+                const int qsbyte = blk * 32 + bi;
+                const int8_t code = (int8_t)data[((g * P + p) * 16 + qsbyte / 16) * 1024 + lane * 16 + qsbyte % 16];
+                const uint8_t* dd = data + region_a + ((g * P + p) * 64 + lane) * 16 + blk * 2;
+                v = (float)code * f16_to_f32((uint16_t)(dd[0] | (dd[1] << 8)));
+            }
+        }
+        out[r_out * k + e] = v;
+    }
+}
+
+extern "C" cpv_status cpv_get_rows(cpv_ctx* ctx, const cpv_weight* w, const int32_t* rows_dev, int64_t n,
+                                   float* out_dev)
+{
+    if (!ctx || !w || !rows_dev || !out_dev || n < 0) return cpv_fail(ctx, CPV_EINVAL, "get_rows: bad arguments");
+    if (n == 0) return CPV_OK;
+    if (n > 65535) return cpv_fail(ctx, CPV_EINVAL, "get_rows: at most 65535 rows per call");
+    dim3 grid((unsigned)((w->k + 255) / 256), (unsigned)n);
+    const uint8_t* d = (const uint8_t*)w->data;
+    switch (w->type) {
+    case CPV_Q4_K: get_rows_kernel<CPV_Q4_K><<<grid, 256, 0, ctx->stream>>>(d, rows_dev, n, w->n, w->k, w->passes, out_dev); break;
+    case CPV_Q6_K: get_rows_kernel<CPV_Q6_K><<<grid, 256, 0, ctx->stream>>>(d, rows_dev, n, w->n, w->k, w->passes, out_dev); break;
+    default: get_rows_kernel<CPV_Q8_0><<<grid, 256, 0, ctx->stream>>>(d, rows_dev, n, w->n, w->k, w->passes, out_dev); break;
+    }
+    CPV_HIP(ctx, hipGetLastError());
+    return CPV_OK;
+}
+
+// ---------------------------------------------------------------- argmax
+// ggml_argmax: the first index of the maximum; values that are not > -inf
+// (and NaN) never win, and a row with no winner gives 0.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ x, const float* __restrict__ nz,
+                                                      int64_t n, int32_t* __restrict__ out)
+{
+    const int64_t row = blockIdx.x;
+    const float* xr = x + row * n;
+    const float* nr = nz ? nz + row * n : nullptr;
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = nr ? xr[i] + nr[i] : xr[i];
+        if (v > best) { best = v; idx = (int)i; }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ob = __shfl_xor(best, off);
+        const int oi = __shfl_xor(idx, off);
+        if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+    }
+    __shared__ float sb[16];
+    __shared__ int si[16];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) { sb[wave] = best; si[wave] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int nw = (blockDim.x + 63) / 64;
+        for (int w = 1; w < nw; w++)
+            if (sb[w] > best || (sb[w] == best && si[w] < idx)) { best = sb[w]; idx = si[w]; }
+        out[row] = idx == 0x7fffffff ? 0 : idx;
+    }
+}
+
+extern "C" cpv_status cpv_argmax_rows(cpv_ctx* ctx, const float* x_dev, const float* noise_dev, int64_t rows,
+                                      int64_t n, int32_t* out_dev)
+{
+    if (!ctx || !x_dev || !out_dev || rows < 0 || n <= 0 || n > 0x7fffffff)
+        return cpv_fail(ctx, CPV_EINVAL, "argmax: bad arguments");
+    if (rows == 0) return CPV_OK;
+    argmax_kernel<<<(unsigned)rows, 1024, 0, ctx->stream>>>(x_dev, noise_dev, n, out_dev);
+    CPV_HIP(ctx, hipGetLastError());
+    return CPV_OK;
+}

@@ -1,0 +1,157 @@
+/*
+ * cpv.h — C ABI of the MI355X verify-step library (libcpv.so).
+ *
+ * Drop-in boundary for codpiece's speculative-decoding verify step.  Today the
+ * reference reaches its arithmetic through codpiece-ggml-sys, raw bindgen
+ * bindings over ggml (crates/codpiece-ggml-sys/wrapper.h:1-9,
+ * crates/codpiece-ggml-sys/src/lib.rs:1-11), building a graph per shape in
+ * crates/codpiece-model/src/qwen35.rs:2445-3198 and running it with
+ * ggml_backend_graph_compute (qwen35.rs:3606-3620).  This header is what a
+ * thin codpiece-hip-sys crate binds instead: plain C types, device pointers
+ * owned by the caller, opaque handles owned by the library.
+ *
+ * Conventions
+ *  - Every call returns a cpv_status; on failure cpv_last_error(ctx) holds a
+ *    message.  Nothing aborts or throws across this boundary (the reference's
+ *    rule: qwen35.rs:3616-3618, crates/codpiece-model/src/meta.rs:47-49).
+ *  - A context is bound to one device and one HIP stream and is used from one
+ *    thread at a time, like the engine thread that owns every ggml object
+ *    (crates/codpiece-server/src/engine.rs:1-7).  Calls enqueue on the stream
+ *    and return; cpv_sync waits.  Distinct contexts are independent.
+ *  - Pointers named *_dev are device pointers the caller owns.
+ *  - Type ids are GGUF's (crates/codpiece-gguf/src/lib.rs:173-185).
+ */
+#ifndef CPV_H
+#define CPV_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int cpv_status;
+enum {
+    CPV_OK = 0,
+    CPV_EINVAL = 1,        /* bad argument (shape, null, range) */
+    CPV_ENOMEM = 2,        /* device allocation failed; the context stays usable */
+    CPV_EDEVICE = 3,       /* HIP runtime error */
+    CPV_EUNSUPPORTED = 4,  /* valid request this build does not implement */
+};
+
+enum { CPV_F32 = 0, CPV_F16 = 1, CPV_Q8_0 = 8, CPV_Q4_K = 12, CPV_Q6_K = 14 };
+
+typedef struct cpv_ctx cpv_ctx;
+typedef struct cpv_weight cpv_weight;
+
+/* ---- context ------------------------------------------------------------ */
+/* Replaces ggml_backend_cuda_init / the backend handle Weights::load creates
+ * (crates/codpiece-model/src/lib.rs:128-311). */
+cpv_status  cpv_init(int device, cpv_ctx** out);
+void        cpv_free(cpv_ctx* ctx);
+const char* cpv_last_error(const cpv_ctx* ctx);
+/* Enqueue on the caller's hipStream_t from now on, verbatim: NULL is HIP's
+ * default (null) stream.  A new context starts on a stream of its own. */
+cpv_status  cpv_set_stream(cpv_ctx* ctx, void* hip_stream);
+void*       cpv_get_stream(const cpv_ctx* ctx);
+cpv_status  cpv_sync(cpv_ctx* ctx);
+
+/* ---- weights ------------------------------------------------------------ */
+/* Upload n_rows rows of k elements in ggml block layout (GGUF tensor bytes,
+ * ne = [k, n_rows]) and repack them for the GEMM kernels.  Replaces
+ * ggml_backend_tensor_set of a weight tensor after ggml_backend_alloc_ctx_tensors
+ * (crates/codpiece-model/src/lib.rs:236-266).  Supported: Q8_0, Q4_K, Q6_K. */
+cpv_status  cpv_weight_upload(cpv_ctx* ctx, int type, const void* host_bytes, int64_t n_rows,
+                              int64_t k, cpv_weight** out);
+/* The same from bytes already in device memory (not retained). */
+cpv_status  cpv_weight_from_device(cpv_ctx* ctx, int type, const void* dev_bytes, int64_t n_rows,
+                                   int64_t k, cpv_weight** out);
+void        cpv_weight_free(cpv_weight* w);
+/* shape / type / device bytes held; any out pointer may be NULL */
+cpv_status  cpv_weight_info(const cpv_weight* w, int* type, int64_t* n_rows, int64_t* k,
+                            int64_t* bytes);
+/* Dequantize rows[i] of w into out_dev[i][k] (f32), as ggml_get_rows does for
+ * the token embedding and out_ids (qwen35.rs:2545,2794).  rows_dev: int32. */
+cpv_status  cpv_get_rows(cpv_ctx* ctx, const cpv_weight* w, const int32_t* rows_dev, int64_t n,
+                         float* out_dev);
+
+/* ---- kernels -------------------------------------------------------------- */
+/* y[m][n] = x[m][:] . dequant(w[n][:]) — ggml_mul_mat(w, x) with ne
+ * [k, n] x [k, m] -> [n, m] (crates/codpiece-ggml-sys/tests/smoke.rs:19),
+ * quantizing x to ggml's CPU vec_dot_type (Q8_0 for Q8_0 weights, Q8_K for
+ * K-quants).  Per block the integer dot is exact; each block's scaled term is
+ * rounded to an integer grid 2^g (g from the largest weight-row and
+ * activation-row scales) and the terms are summed exactly below 2^53, so the
+ * result does not depend on how the K loop is split.
+ * Replaces every ggml_mul_mat on the verify path (qwen35.rs:2779-2782,2797,
+ * 3029,3047,3051,3197; mtp_graph.rs:184,209-212,230).  x_dev: f32 [m][k];
+ * y_dev: f32 [m][n_rows]; 1 <= m <= 64. */
+cpv_status  cpv_qgemm(cpv_ctx* ctx, const cpv_weight* w, const float* x_dev, int64_t m,
+                      float* y_dev);
+
+/* Masked GQA attention over an f16 cache; replaces ggml_flash_attn_ext with
+ * prec F32 and an f16 mask (qwen35.rs:3182-3187, mask fill :3551-3568).
+ * q_dev: f32 [t][h][d]; k_cache_dev, v_cache_dev: f16 [n_ctx][h_kv * d], rows
+ * [0, n_past) are context and row n_past + i holds node i; parent_dev: int32
+ * [t], parent of each node (-1 = child of the context) or NULL for a linear
+ * chain (the reference's causal mask).  out_dev: f32 [t][h * d].
+ * Requires t <= 64, d in {64, 128}, h % h_kv == 0. */
+cpv_status  cpv_attn(cpv_ctx* ctx, const float* q_dev, const uint16_t* k_cache_dev,
+                     const uint16_t* v_cache_dev, int64_t n_past, const int32_t* parent_dev,
+                     int t, int h, int h_kv, int d, float scale, float* out_dev);
+
+/* Row argmax, first maximum wins: ggml_argmax (qwen35.rs:2811-2818),
+ * optionally of logits + noise (the gumbel branch).  x_dev [rows][n],
+ * noise_dev [rows][n] or NULL, out_dev int32 [rows]. */
+cpv_status  cpv_argmax_rows(cpv_ctx* ctx, const float* x_dev, const float* noise_dev, int64_t rows,
+                            int64_t n, int32_t* out_dev);
+
+/* ---- speculative acceptance ------------------------------------------------ */
+/* SamplerParams (crates/codpiece-sample/src/lib.rs:29-47) minus the seed. */
+typedef struct {
+    float   temp;
+    int32_t top_k;
+    float   top_p;
+    float   min_p;
+    int32_t min_keep;
+    float   penalty_repeat;
+    float   penalty_freq;
+    float   penalty_present;
+    int32_t penalty_last_n;
+} cpv_sampler_params;
+
+enum { CPV_ACCEPT_GREEDY = 0, CPV_ACCEPT_REJECT = 1, CPV_ACCEPT_GUMBEL = 2 };
+
+/* Decide a speculative round for b sequences on the device: the acceptance
+ * loop of crates/codpiece-server/src/engine.rs:2326-2461 with the target
+ * distribution of Sampler::distribution (crates/codpiece-sample/src/lib.rs:
+ * 184-187,229-376) and Dist::{prob_of, draw, draw_excluding} (:387-436).
+ *   p_logits_dev  f32 [b][k+1][v]   target logits at the k+1 verified rows
+ *   q_logits_dev  f32 [b][k][v] or NULL.  NULL = drafts are the draft head's
+ *                 argmax (a point mass) and the reference rule applies:
+ *                 accept with p(x), else draw from p without x.  Non-NULL =
+ *                 drafts were sampled from q: accept iff u*q(x) < p(x), else
+ *                 draw from max(0, p - q) renormalised.
+ *   draft_dev     int32 [b][k]
+ *   mode          CPV_ACCEPT_GREEDY (argmax match), _REJECT, _GUMBEL
+ *   u_dev         f32 [b][k+1][2] uniforms by role (r0 = accept roll, or the
+ *                 bonus draw at j = k; r1 = residual draw), or NULL to draw
+ *                 them from Philox4x64-10 with key (philox_seed, 0) and
+ *                 counter (b, j, r, 0), taking (x >> 40) / 2^24.
+ *   noise_dev     f32 [b][k+1][v], T-scaled gumbel noise (GUMBEL mode only)
+ *   hist_dev      int32 [b][hist_len] penalty window, oldest first, -1 empty
+ *                 (only read when a penalty is active)
+ *   out_tok_dev   int32 [b][k+1]: the accepted drafts then the next token
+ *   out_n_dev     int32 [b]: number of accepted drafts (tokens = out_n + 1)
+ * v <= 262144, k <= 15. */
+cpv_status  cpv_spec_accept(cpv_ctx* ctx, const float* p_logits_dev, const float* q_logits_dev,
+                            const int32_t* draft_dev, int b, int k, int v,
+                            const cpv_sampler_params* params, int mode, const float* u_dev,
+                            uint64_t philox_seed, const float* noise_dev, const int32_t* hist_dev,
+                            int hist_len, int32_t* out_tok_dev, int32_t* out_n_dev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -315,23 +315,25 @@ int cpvo_dequantize(int type, const void* q, int64_t n, float* y)
  * and CUDA builds, so no single ggml order exists to follow.  This contract
  * removes order from the result instead:
  *
- *   for each output (m, n) and each block unit u along K:
+ *   for each output (m, n) and each unit u along K (a Q8_0 block of 32, a
+ *   K-quant super-block of 256):
  *     isum_u   exact integer   (Q8_0: sum q_w q_a;  Q4_K: sum_j sc_j dot_j;
  *                               Q6_K: sum_g sc_g dot_g)
  *     imin_u   exact integer   (Q4_K only: sum_j m_j * bsum_j)
  *     A_u    = (double)d_w * (double)d_a * 2^-g          exact in binary64
- *     t_u    = A_u * (double)isum_u                      one binary64 rounding
- *     S     += floor(t_u)          (Q4_K: S -= floor(B_u * (double)imin_u),
- *                                   B_u = (double)dmin_w * (double)d_a * 2^-g)
- *   y = (float)((double)S * 2^g)
+ *     S     += rint(A_u * (double)isum_u)                an integer
+ *              (Q4_K: S -= rint(B_u * (double)imin_u),
+ *               B_u = (double)dmin_w * (double)d_a * 2^-g)
+ *   y = (float)(S * 2^g)
  *
- * with S an int64 and the window g = Ew(n) + Ea(m) - W, where Ew / Ea are the
- * frexp exponents of the largest weight-row / activation-row scale magnitude
- * and W = 62 - isum_bits - ceil(log2(terms + 1)) keeps |S| < 2^62.  Integer
- * sums are associative, so any split of the K loop over lanes, waves or
- * workgroups gives the same bits.  The window sits ~2^-30 below the largest
- * possible term, far below f32 resolution, so y is the correctly rounded
- * quantized dot product except within ~2^-30 relative of a rounding tie. */
+ * The window g = Ew(n) + Ea(m) - W, with Ew / Ea the frexp exponents of the
+ * largest weight-row / activation-row scale magnitude and
+ * W = 52 - isum_bits - ceil(log2(terms + 1)), bounds |S| < 2^53: S is an
+ * integer exactly representable in binary64, so it can be accumulated in
+ * int64 or in double, in any order and split any way over lanes, waves or
+ * workgroups, with the same result.  The grid sits ~2^-45 below the largest
+ * possible term; for real data y is the correctly rounded quantized dot
+ * product except within ~2^-10 ulp of a rounding tie. */
 static int isum_bits(int type) { return type == CPVO_Q8_0 ? 20 : type == CPVO_Q4_K ? 25 : 28; }
 
 static int64_t n_terms(int type, int64_t K)
@@ -348,7 +350,7 @@ static int ceil_log2(int64_t v)
 
 int cpvo_qgemm_window(int type, int64_t K)
 {
-    return 62 - isum_bits(type) - ceil_log2(n_terms(type, K) + 1);
+    return 52 - isum_bits(type) - ceil_log2(n_terms(type, K) + 1);
 }
 
 #define CPVO_E_EMPTY INT_MIN
@@ -360,7 +362,7 @@ static int exp_of(float v)
     return e;
 }
 
-static inline int64_t fx_floor(double t) { return (int64_t)floor(t); }
+static inline int64_t fx_round(double t) { return (int64_t)rint(t); }
 
 static inline int32_t dot_i8(const int8_t* a, const int8_t* b, int n)
 {
@@ -409,7 +411,7 @@ int cpvo_qgemm(int type, const void* w, int64_t N, int64_t K, const float* x, in
                 for (int64_t b = 0; b < nb; b++) {
                     const int32_t isum = dot_i8(wr[b].qs, xa[m * nb + b].qs, 32);
                     double A = ldexp((double)cpvo_fp16_to_fp32(wr[b].d) * (double)dta[m * nb + b], -g);
-                    S += fx_floor(A * (double)isum);
+                    S += fx_round(A * (double)isum);
                 }
                 y[m * N + n] = (float)ldexp((double)S, g);
             }
@@ -471,8 +473,8 @@ int cpvo_qgemm(int type, const void* w, int64_t N, int64_t K, const float* x, in
                         }
                         const double A = ldexp(dw * (double)a->d, -gm[mm]);
                         const double Bm = ldexp(dmn * (double)a->d, -gm[mm]);
-                        S[mm] += fx_floor(A * (double)isum);
-                        S[mm] -= fx_floor(Bm * (double)imin);
+                        S[mm] += fx_round(A * (double)isum);
+                        S[mm] -= fx_round(Bm * (double)imin);
                     }
                 } else {
                     const cpvo_block_q6_K* bl = (const cpvo_block_q6_K*)wr + b;
@@ -484,7 +486,7 @@ int cpvo_qgemm(int type, const void* w, int64_t N, int64_t K, const float* x, in
                         for (int g = 0; g < 16; g++)
                             isum += (int32_t)bl->scales[g] * dot_i8(q + g * 16, a->qs + g * 16, 16);
                         const double A = ldexp(dw * (double)a->d, -gm[mm]);
-                        S[mm] += fx_floor(A * (double)isum);
+                        S[mm] += fx_round(A * (double)isum);
                     }
                 }
             }
