@@ -69,4 +69,7 @@ __host__ __device__ __forceinline__ uint16_t cpv_f2h(float f)
 
 // internal launchers
 cpv_status cpv_repack_launch(cpv_ctx* ctx, cpv_weight* w, const void* aos_dev);
+cpv_status cpv_attn_launch(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
+                           int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
+                           float* out);
 cpv_status cpv_qgemm_launch(cpv_ctx* ctx, const cpv_weight* w, const float* x, int64_t m, float* y);

@@ -93,14 +93,14 @@ class Context:
         self._check(self.lib.cpv_argmax_rows(self.h, _ptr(x), _ptr(noise), rows, n, _ptr(out)))
         return out
 
-    def attn(self, q, k_cache, v_cache, n_past, parent, h_kv, scale, out=None):
-        """q [t][h][d] f32; caches [n_ctx][h_kv*d] as int16/uint16/float16 tensors."""
+    def attn(self, q, k_cache, v_cache_t, n_past, parent, h_kv, scale, out=None):
+        """q [t][h][d] f32; k_cache [n_ctx][h_kv*d] and v_cache_t [h_kv*d][v_stride], 16-bit tensors."""
         t, h, d = q.shape
         if out is None:
             out = torch.empty((t, h * d), dtype=torch.float32, device=q.device)
         par = None if parent is None else parent.to(torch.int32).contiguous()
-        self._check(self.lib.cpv_attn(self.h, _ptr(q.contiguous()), _ptr(k_cache), _ptr(v_cache), n_past,
-                                      _ptr(par), t, h, h_kv, d, scale, _ptr(out)))
+        self._check(self.lib.cpv_attn(self.h, _ptr(q.contiguous()), _ptr(k_cache), _ptr(v_cache_t),
+                                      v_cache_t.shape[1], n_past, _ptr(par), t, h, h_kv, d, scale, _ptr(out)))
         return out
 
     def spec_accept(self, p_logits, draft, params, mode, u=None, q_logits=None, noise=None, hist=None,

@@ -90,16 +90,24 @@ cpv_status  cpv_get_rows(cpv_ctx* ctx, const cpv_weight* w, const int32_t* rows_
 cpv_status  cpv_qgemm(cpv_ctx* ctx, const cpv_weight* w, const float* x_dev, int64_t m,
                       float* y_dev);
 
-/* Masked GQA attention over an f16 cache; replaces ggml_flash_attn_ext with
- * prec F32 and an f16 mask (qwen35.rs:3182-3187, mask fill :3551-3568).
- * q_dev: f32 [t][h][d]; k_cache_dev, v_cache_dev: f16 [n_ctx][h_kv * d], rows
- * [0, n_past) are context and row n_past + i holds node i; parent_dev: int32
- * [t], parent of each node (-1 = child of the context) or NULL for a linear
- * chain (the reference's causal mask).  out_dev: f32 [t][h * d].
- * Requires t <= 64, d in {64, 128}, h % h_kv == 0. */
+/* Masked GQA attention over the f16 KV cache; replaces ggml_flash_attn_ext
+ * with prec F32 and an f16 mask (qwen35.rs:3182-3187, mask fill :3551-3568).
+ *   q_dev        f32 [t][h][d]
+ *   k_cache_dev  f16 [n_ctx][h_kv * d], the FA cache layout (qwen35.rs:571-575)
+ *   v_cache_t_dev f16 [h_kv * d][v_stride], the transposed V cache the
+ *                reference keeps without FA (qwen35.rs:580-586)
+ *   rows / columns [0, n_past) are context; n_past + i holds tree node i
+ *   parent_dev   int32 [t]: parent of each node (-1 = child of the context,
+ *                parents precede children), or NULL for a linear chain (the
+ *                reference's causal mask).  Node i sees all context rows plus
+ *                its ancestors and itself.
+ *   out_dev      f32 [t][h * d]
+ * Requires t <= 64, (h / h_kv) * t <= 96, d in {64, 128}, v_stride >= n_past
+ * + t and a multiple of 8, 16-byte aligned caches. */
 cpv_status  cpv_attn(cpv_ctx* ctx, const float* q_dev, const uint16_t* k_cache_dev,
-                     const uint16_t* v_cache_dev, int64_t n_past, const int32_t* parent_dev,
-                     int t, int h, int h_kv, int d, float scale, float* out_dev);
+                     const uint16_t* v_cache_t_dev, int64_t v_stride, int64_t n_past,
+                     const int32_t* parent_dev, int t, int h, int h_kv, int d, float scale,
+                     float* out_dev);
 
 /* Row argmax, first maximum wins: ggml_argmax (qwen35.rs:2811-2818),
  * optionally of logits + noise (the gumbel branch).  x_dev [rows][n],

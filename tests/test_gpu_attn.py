@@ -1,0 +1,96 @@
+"""GPU parity of tree-masked GQA attention against the f64 oracle.
+
+Bar: the GPU evaluates q k^T with f16 MFMA products (q rounded to f16 exactly
+as the oracle does) and an f32 online softmax, so it is held to a tolerance:
+|gpu - oracle| <= 2e-5 + 2e-4 * |oracle| elementwise, for V ~ N(0, 1).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import cpvo
+
+pytestmark = pytest.mark.gpu
+
+TREE16 = [-1, -1, -1, -1, 0, 0, 0, 1, 1, 1, 4, 4, 4, 10, 10, 10]
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from codpiece_amd.runtime import Context
+    c = Context(0)
+    yield c
+    c.close()
+
+
+def make(rng, n_ctx, hkv, d, v_stride=None):
+    k = cpvo.f32_to_f16_bits(rng.normal(size=(n_ctx, hkv * d)).astype(np.float32))
+    v = cpvo.f32_to_f16_bits(rng.normal(size=(n_ctx, hkv * d)).astype(np.float32))
+    vs = v_stride or (n_ctx + 7) // 8 * 8
+    vt = np.zeros((hkv * d, vs), dtype=np.uint16)
+    vt[:, :n_ctx] = v.T
+    return k, v, vt
+
+
+def run(ctx, t, h, hkv, d, n_past, parent, seed=0, extra_rows=0):
+    rng = np.random.default_rng(seed)
+    n_ctx = n_past + t + extra_rows
+    k, v, vt = make(rng, n_ctx, hkv, d)
+    q = rng.normal(size=(t, h, d)).astype(np.float32)
+    scale = np.float32(1) / np.sqrt(np.float32(d))
+    print(f"case t={t} h={h} hkv={hkv} d={d} n_past={n_past} tree={parent is not None}", flush=True)
+    par = None if parent is None else torch.tensor(parent, dtype=torch.int32, device="cuda")
+    got = ctx.attn(torch.from_numpy(q).cuda(), torch.from_numpy(k.view(np.int16)).cuda(),
+                   torch.from_numpy(vt.view(np.int16)).cuda(), n_past, par, hkv, float(scale)).cpu().numpy()
+    ref = cpvo.attn(q, k[:n_past + t], v[:n_past + t], n_past, parent, scale)
+    return got, ref
+
+
+def close(got, ref):
+    err = np.abs(got - ref)
+    tol = 2e-5 + 2e-4 * np.abs(ref)
+    assert np.all(err <= tol), (err.max(), (err / tol).max())
+
+
+@pytest.mark.parametrize("n_past", [0, 1, 37, 300, 1000])
+def test_tiny_model_chain(ctx, n_past):
+    # 8 Q / 2 KV heads x 64, T = k+1 = 5, causal chain (the reference's mask)
+    close(*run(ctx, 5, 8, 2, 64, n_past, None))
+
+
+@pytest.mark.parametrize("n_past", [4096, 4101])
+def test_27b_class_chain(ctx, n_past):
+    close(*run(ctx, 5, 40, 8, 128, n_past, None))
+
+
+@pytest.mark.parametrize("n_ctx", [8192, 32768])
+def test_tree_verify_config(ctx, n_ctx):
+    # 40 Q / 8 KV heads x 128, a 16-node draft tree over n_ctx context rows
+    close(*run(ctx, 16, 40, 8, 128, n_ctx, TREE16, seed=n_ctx))
+
+
+def test_tree_with_linear_parents_equals_chain(ctx):
+    a, _ = run(ctx, 8, 8, 2, 64, 200, None, seed=3)
+    b, _ = run(ctx, 8, 8, 2, 64, 200, list(range(-1, 7)), seed=3)
+    assert np.array_equal(a, b)
+
+
+def test_rows_past_the_window_are_ignored(ctx):
+    # cache rows beyond n_past + t (stale rows of a rolled-back round) never count
+    a, ref = run(ctx, 5, 8, 2, 64, 100, None, seed=4, extra_rows=200)
+    close(a, ref)
+
+
+def test_wide_tree_max_nodes(ctx):
+    # 64 nodes, one query head per KV head: a bushy random tree
+    rng = np.random.default_rng(9)
+    parent = [-1] + [int(rng.integers(-1, i)) for i in range(1, 64)]
+    close(*run(ctx, 64, 2, 2, 64, 500, parent, seed=5))
+
+
+def test_bad_shapes_are_rejected(ctx):
+    from codpiece_amd import CpvError
+    q = torch.zeros((4, 8, 96), device="cuda")
+    kc = torch.zeros((16, 2 * 96), dtype=torch.int16, device="cuda")
+    with pytest.raises(CpvError):
+        ctx.attn(q, kc, kc, 4, None, 2, 0.1)
