@@ -44,6 +44,24 @@ class SamplerParams(ctypes.Structure):
                          penalty_present, penalty_last_n)
 
 
+class Hparams(ctypes.Structure):
+    """cpv_hparams: an all-attention qwen35 model (crates/codpiece-model/src/qwen35.rs:45-148)."""
+    _fields_ = [
+        ("n_layer", ctypes.c_int32), ("n_embd", ctypes.c_int32), ("n_head", ctypes.c_int32),
+        ("n_head_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("n_ff", ctypes.c_int32),
+        ("n_vocab", ctypes.c_int32), ("n_rot", ctypes.c_int32), ("rope_sections", ctypes.c_int32 * 4),
+        ("rms_eps", ctypes.c_float), ("freq_base", ctypes.c_float), ("has_mtp", ctypes.c_int32),
+    ]
+
+
+class RoundOut(ctypes.Structure):
+    """cpv_round_out: FusedOut (qwen35.rs:817-828) as device pointers."""
+    _fields_ = [
+        ("n_past", ctypes.c_int64), ("preds_dev", ctypes.c_void_p), ("chain_dev", ctypes.c_void_p),
+        ("conf_dev", ctypes.c_void_p), ("logits_dev", ctypes.c_void_p), ("hidden_dev", ctypes.c_void_p),
+    ]
+
+
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I32 = ctypes.c_int32
@@ -69,6 +87,17 @@ SIGNATURES = {
     "cpv_argmax_rows": (_INT, [_P, _P, _P, _I64, _I64, _P]),
     "cpv_spec_accept": (_INT, [_P, _P, _P, _P, _INT, _INT, _INT, ctypes.POINTER(SamplerParams), _INT,
                                _P, ctypes.c_uint64, _P, _P, _INT, _P, _P]),
+    "cpv_model_create": (_INT, [_P, ctypes.POINTER(Hparams), ctypes.POINTER(_P)]),
+    "cpv_model_set_tensor": (_INT, [_P, ctypes.c_char_p, _INT, _P, _INT, _I64, _I64]),
+    "cpv_model_ready": (_INT, [_P]),
+    "cpv_model_free": (None, [_P]),
+    "cpv_session_create": (_INT, [_P, _I64, _I32, ctypes.POINTER(_P)]),
+    "cpv_session_free": (None, [_P]),
+    "cpv_session_set_pos": (_INT, [_P, _I64, _I64]),
+    "cpv_session_get_pos": (_INT, [_P, ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
+    "cpv_session_set_attn_tap": (_INT, [_P, _P, _I64]),
+    "cpv_prefill": (_INT, [_P, _P, _INT]),
+    "cpv_verify_step": (_INT, [_P, _P, _INT, _INT, _P, ctypes.POINTER(RoundOut)]),
 }
 
 _lib = None

@@ -28,7 +28,7 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int TILE = 32;           // KV rows per MFMA tile
 constexpr int WAVES = 4;
-constexpr int MAX_ROWS = 96;       // G * T per KV head handled by one workgroup
+constexpr int MAX_ROWS = 96;       // query rows per workgroup (a row block of one KV head)
 constexpr int P_STRIDE = TILE + 8; // halves per P row in LDS (breaks bank aliasing)
 
 __device__ __forceinline__ h8 load_h8(const uint16_t* p)
@@ -46,7 +46,9 @@ __global__ __launch_bounds__(256) void attn_split_kernel(
     constexpr int DC = D / 32;     // MFMA k-steps for q k^T
     constexpr int DT = D / 16;     // output column tiles
     const int G = H / Hkv;
-    const int R = G * T;
+    const int R = G * T;                         // query rows of this KV head
+    const int row0 = blockIdx.z * MAX_ROWS;      // this workgroup's first row
+    const int Rb = R - row0 < RT * 16 ? R - row0 : RT * 16;
     const int split = blockIdx.x, kvh = blockIdx.y;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, g4 = lane >> 4;
     const int64_t n_tot = n_past + T;
@@ -59,8 +61,8 @@ __global__ __launch_bounds__(256) void attn_split_kernel(
     __shared__ uint64_t s_anc[64];
     __shared__ float s_ml[WAVES][2][RT * 16];
 
-    // ancestor-or-self bitmask per node (a linear chain when parent is null)
-    if (tid < T) {
+    // ancestor-or-self bitmask per node of a tree (a chain needs none)
+    if (parent && tid < T) {
         uint64_t m = 0;
         int a = tid;
         for (int steps = 0; a >= 0 && a < T && steps <= T; steps++) {
@@ -73,8 +75,8 @@ __global__ __launch_bounds__(256) void attn_split_kernel(
     for (int i = tid; i < RT * 16 * D; i += blockDim.x) {
         const int rho = i / D, d = i % D;
         float v = 0.0f;
-        if (rho < R) {
-            const int t = rho / G, gi = rho % G;
+        if (rho < Rb) {
+            const int t = (row0 + rho) / G, gi = (row0 + rho) % G;
             v = q[((int64_t)t * H + kvh * G + gi) * D + d];
         }
         s_q[i] = cpv_f2h(v);
@@ -128,13 +130,14 @@ __global__ __launch_bounds__(256) void attn_split_kernel(
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int rho = rt * 16 + 4 * g4 + i;
-                    const int node = rho < R ? rho / G : 0;
+                    const int node = rho < Rb ? (row0 + rho) / G : 0;
                     float sv[2];
 #pragma unroll
                     for (int ct = 0; ct < 2; ct++) {
                         const int64_t j = j0 + 16 * ct + l16;
                         bool vis = j < j_end;
-                        if (vis && j >= n_past) vis = (s_anc[node] >> (j - n_past)) & 1ull;
+                        if (vis && j >= n_past)
+                            vis = parent ? ((s_anc[node] >> (j - n_past)) & 1ull) != 0 : j - n_past <= node;
                         sv[ct] = vis ? s[ct][i] * scale : -INFINITY;
                     }
                     float mx = fmaxf(sv[0], sv[1]);
@@ -227,10 +230,10 @@ __global__ __launch_bounds__(256) void attn_split_kernel(
     }
     // partials: [split][kvh][rho] x (m, l, O[D])
     const int nsplit = gridDim.x;
-    for (int i = tid; i < R * (D + 2); i += blockDim.x) {
+    for (int i = tid; i < Rb * (D + 2); i += blockDim.x) {
         const int rho = i / (D + 2), c = i % (D + 2);
         const float v = c == 0 ? s_ml[0][0][rho] : c == 1 ? s_ml[0][1][rho] : s_o[rho * D + c - 2];
-        part[(((int64_t)kvh * nsplit + split) * R + rho) * (D + 2) + c] = v;
+        part[(((int64_t)kvh * nsplit + split) * R + row0 + rho) * (D + 2) + c] = v;
     }
 }
 
@@ -274,7 +277,7 @@ cpv_status launch(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16
     void* ws = nullptr;
     cpv_status st = cpv_workspace(ctx, (size_t)Hkv * nsplit * R * (D + 2) * sizeof(float), &ws);
     if (st != CPV_OK) return st;
-    dim3 grid((unsigned)nsplit, (unsigned)Hkv);
+    dim3 grid((unsigned)nsplit, (unsigned)Hkv, (unsigned)((R + MAX_ROWS - 1) / MAX_ROWS));
     attn_split_kernel<D, RT><<<grid, 256, 0, ctx->stream>>>(q, kc, vt, v_stride, n_past, parent, T, H, Hkv,
                                                             scale, chunk, (float*)ws);
     CPV_HIP(ctx, hipGetLastError());
@@ -304,7 +307,7 @@ cpv_status cpv_attn_launch(cpv_ctx* ctx, const float* q, const uint16_t* kc, con
                            float* out)
 {
     const int R = (h / h_kv) * t;
-    const int rt = (R + 15) / 16;
+    const int rt = ((R < MAX_ROWS ? R : MAX_ROWS) + 15) / 16;
     if (d == 128) return launch_rt<128>(ctx, rt, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out);
     return launch_rt<64>(ctx, rt, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out);
 }
@@ -316,12 +319,10 @@ extern "C" cpv_status cpv_attn(cpv_ctx* ctx, const float* q_dev, const uint16_t*
 {
     if (!ctx || !q_dev || !k_cache_dev || !v_cache_t_dev || !out_dev)
         return cpv_fail(ctx, CPV_EINVAL, "attn: null argument");
-    if (t < 1 || t > 64 || h < 1 || h_kv < 1 || h % h_kv || n_past < 0)
+    if (t < 1 || (parent_dev && t > 64) || t > 8192 || h < 1 || h_kv < 1 || h % h_kv || n_past < 0)
         return cpv_fail(ctx, CPV_EINVAL, "attn: bad shape t=%d h=%d h_kv=%d n_past=%lld", t, h, h_kv,
                         (long long)n_past);
     if (d != 64 && d != 128) return cpv_fail(ctx, CPV_EUNSUPPORTED, "attn: head dim %d (64 or 128)", d);
-    if ((h / h_kv) * t > MAX_ROWS)
-        return cpv_fail(ctx, CPV_EUNSUPPORTED, "attn: %d query rows per KV head (max %d)", (h / h_kv) * t, MAX_ROWS);
     if (v_stride < n_past + t || (v_stride % 8))
         return cpv_fail(ctx, CPV_EINVAL, "attn: v_stride %lld must be >= n_past + t and a multiple of 8",
                         (long long)v_stride);

@@ -1,0 +1,705 @@
+// model.hip — the qwen35-layout verify round on the device.
+//
+// cpv_verify_step is Qwen35::step_fused_cached (crates/codpiece-model/src/
+// qwen35.rs:1693-1948) for an all-attention qwen35 model: the trunk
+// (build_inner, :2445-2786, with build_attn_block :3000-3198), the LM head and
+// in-graph argmax (:2788-2821) and the fused MTP draft chain (:2840-2962).
+// Every op follows the ggml CPU semantics the oracle restates:
+//   rms_norm   exact sum of f32 squares, mean = (float)(sum/n),
+//              scale = 1/sqrtf(mean + eps), y = (x*scale)*w
+//   rope       NEOX pairs from a cos/sin table built on the host with ggml's
+//              f32 theta recurrence (qwen35.rs:3053-3062 with text positions)
+//   sigmoid    1/(1+expf(-x)); silu x/(1+expf(-x)); add / mul in f32
+//   mul_mat    the exact-window GEMM of qgemm.hip
+//   attention  attn.hip (f16 MFMA; within a tolerance of the f64 oracle)
+// The K cache is [n_ctx][h_kv*d] and V is kept transposed [h_kv*d][n_ctx]
+// (the reference's non-FA V layout), one pair per layer plus the MTP pair.
+#include <math.h>
+#include <string.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "cpv_internal.h"
+
+namespace {
+
+// ---------------------------------------------------------------- glue kernels
+__device__ __forceinline__ int ceil_log2_dev(int64_t v)
+{
+    int b = 0;
+    while (((int64_t)1 << b) < v) b++;
+    return b;
+}
+
+// y = rms_norm(x) * w over rows of n; exact fixed-point sum of the f32 squares
+// (order-free), then ggml's f32 tail.  One block per row.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, int64_t xs,
+                                                      const float* __restrict__ w, float* __restrict__ y,
+                                                      int64_t ys, int n, float eps)
+{
+    const float* xr = x + (int64_t)blockIdx.x * xs;
+    float* yr = y + (int64_t)blockIdx.x * ys;
+    __shared__ float s_max[4];
+    __shared__ long long s_sum[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = (blockDim.x + 63) >> 6;
+    float am = 0.0f;
+    for (int i = tid; i < n; i += blockDim.x) am = fmaxf(am, fabsf(xr[i]));
+    for (int off = 32; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));
+    if (lane == 0) s_max[wave] = am;
+    __syncthreads();
+    am = s_max[0];
+    for (int i = 1; i < nw; i++) am = fmaxf(am, s_max[i]);
+    double sum = 0.0;
+    if (am > 0.0f) {
+        int e;
+        frexpf(am, &e);
+        const int g = 2 * e - (62 - ceil_log2_dev(n + 1));
+        long long S = 0;
+        for (int i = tid; i < n; i += blockDim.x) {
+            const float sq = xr[i] * xr[i];
+            S += (long long)floor(ldexp((double)sq, -g));
+        }
+        for (int off = 32; off > 0; off >>= 1) S += __shfl_xor(S, off);
+        if (lane == 0) s_sum[wave] = S;
+        __syncthreads();
+        S = 0;
+        for (int i = 0; i < nw; i++) S += s_sum[i];
+        sum = ldexp((double)S, g);
+    }
+    const float mean = (float)(sum / (double)n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int i = tid; i < n; i += blockDim.x) {
+        const float v = xr[i] * scale;
+        yr[i] = w ? v * w[i] : v;
+    }
+}
+
+// Per token t and head: q/k RMS norm over the head, NEOX rope at position
+// rope_pos0 + t, then q to qout, k (f16) to k_cache row kv_row0 + t and v (f16)
+// to column kv_row0 + t of the transposed V cache.  Grid (T, H + Hkv), block hd.
+struct PrepArgs {
+    const float* qg;       // [T][H][2*hd]  query | output gate per head
+    const float* kk;       // [T][Hkv*hd]
+    const float* vv;       // [T][Hkv*hd]
+    const float* q_norm;   // [hd]
+    const float* k_norm;   // [hd]
+    const float* rope;     // [n_pos][n_rot/2][2]
+    float* qout;           // [T][H][hd]
+    uint16_t* k_cache;     // [n_ctx][Hkv*hd]
+    uint16_t* v_cache_t;   // [Hkv*hd][v_stride]
+    int64_t v_stride;
+    int64_t rope_pos0, kv_row0;
+    int H, Hkv, hd, n_rot, write;
+    float eps;
+};
+
+__global__ __launch_bounds__(128) void qk_prep_kernel(PrepArgs a)
+{
+    const int t = blockIdx.x, hh = blockIdx.y, i = threadIdx.x;
+    const bool is_q = hh < a.H;
+    const int kh = hh - a.H;
+    const float* src = is_q ? a.qg + ((int64_t)t * a.H + hh) * 2 * a.hd : a.kk + ((int64_t)t * a.Hkv + kh) * a.hd;
+    const float* w = is_q ? a.q_norm : a.k_norm;
+    __shared__ float s_v[128];
+    __shared__ float s_am[2];
+    __shared__ long long s_s[2];
+    const float x = src[i];
+    // rms over the head (n = hd <= 128: two waves at most)
+    float am = fabsf(x);
+    for (int off = 32; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));
+    if ((i & 63) == 0) s_am[i >> 6] = am;
+    __syncthreads();
+    am = s_am[0];
+    if (a.hd > 64) am = fmaxf(am, s_am[1]);
+    double sum = 0.0;
+    if (am > 0.0f) {
+        int e;
+        frexpf(am, &e);
+        const int g = 2 * e - (62 - ceil_log2_dev(a.hd + 1));
+        long long S = (long long)floor(ldexp((double)(x * x), -g));
+        for (int off = 32; off > 0; off >>= 1) S += __shfl_xor(S, off);
+        if ((i & 63) == 0) s_s[i >> 6] = S;
+        __syncthreads();
+        S = s_s[0] + (a.hd > 64 ? s_s[1] : 0);
+        sum = ldexp((double)S, g);
+    }
+    const float mean = (float)(sum / (double)a.hd);
+    const float scale = 1.0f / sqrtf(mean + a.eps);
+    const float v0 = x * scale;
+    const float xn = w ? v0 * w[i] : v0;
+    s_v[i] = xn;
+    __syncthreads();
+    float out = xn;
+    const int half = a.n_rot / 2;
+    if (i < a.n_rot) {
+        const int p = i < half ? i : i - half;
+        const float* cs = a.rope + (a.rope_pos0 + t) * a.n_rot + 2 * p;
+        const float c = cs[0], s = cs[1];
+        const float x0 = s_v[p], x1 = s_v[p + half];
+        if (i < half) {
+            const float m0 = x0 * c, m1 = x1 * s;
+            out = m0 - m1;
+        } else {
+            const float m0 = x0 * s, m1 = x1 * c;
+            out = m0 + m1;
+        }
+    }
+    if (is_q) {
+        a.qout[((int64_t)t * a.H + hh) * a.hd + i] = out;
+    } else if (a.write) {
+        const int64_t row = a.kv_row0 + t;
+        a.k_cache[row * a.Hkv * a.hd + (int64_t)kh * a.hd + i] = cpv_f2h(out);
+        const float vv = a.vv[((int64_t)t * a.Hkv + kh) * a.hd + i];
+        a.v_cache_t[((int64_t)kh * a.hd + i) * a.v_stride + row] = cpv_f2h(vv);
+    }
+}
+
+// out[t][h*hd + i] = attn[t][h*hd + i] * sigmoid(gate), gate = qg[t][h][hd + i]
+__global__ void gate_mul_kernel(const float* __restrict__ attn, const float* __restrict__ qg, int H, int hd,
+                                int64_t total, float* __restrict__ out)
+{
+    for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t t = e / ((int64_t)H * hd);
+        const int64_t r = e % ((int64_t)H * hd);
+        const int64_t h = r / hd, i = r % hd;
+        const float g = qg[(t * H + h) * 2 * hd + hd + i];
+        const float sig = 1.0f / (1.0f + cpv_expf(-g));
+        out[e] = attn[e] * sig;
+    }
+}
+
+__global__ void add_kernel(const float* a, const float* b, float* y, int64_t n)   // y may alias b
+{
+    for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x)
+        y[e] = a[e] + b[e];
+}
+
+// act = silu(g) * u, silu(x) = x / (1 + expf(-x))
+__global__ void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ y,
+                              int64_t n)
+{
+    for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+        const float x = g[e];
+        const float s = x / (1.0f + cpv_expf(-x));
+        y[e] = s * u[e];
+    }
+}
+
+// ggml_soft_max peak at the argmax: expf(0) * (float)(1 / sum_i expf(x_i - max)),
+// the sum taken in double as ggml_vec_soft_max_f32 does
+__global__ __launch_bounds__(1024) void peak_kernel(const float* __restrict__ x, int64_t n, float* __restrict__ out)
+{
+    const float* xr = x + (int64_t)blockIdx.x * n;
+    __shared__ float s_m[16];
+    __shared__ double s_d[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+    float mx = -INFINITY;
+    for (int64_t i = tid; i < n; i += blockDim.x) mx = fmaxf(mx, xr[i]);
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (lane == 0) s_m[wave] = mx;
+    __syncthreads();
+    mx = s_m[0];
+    for (int i = 1; i < nw; i++) mx = fmaxf(mx, s_m[i]);
+    double sum = 0.0;
+    for (int64_t i = tid; i < n; i += blockDim.x) sum += (double)cpv_expf(xr[i] - mx);
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    if (lane == 0) s_d[wave] = sum;
+    __syncthreads();
+    if (tid == 0) {
+        double tot = 0.0;
+        for (int i = 0; i < nw; i++) tot += s_d[i];
+        out[blockIdx.x] = 1.0f * (float)(1.0 / tot);
+    }
+}
+
+unsigned grid_for(int64_t n) { return (unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096); }
+
+}  // namespace
+
+// ---------------------------------------------------------------- model
+struct LayerW {
+    cpv_weight *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr;
+    cpv_weight *gate = nullptr, *up = nullptr, *down = nullptr;
+    float *attn_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+};
+
+struct cpv_model {
+    cpv_ctx* ctx = nullptr;
+    cpv_hparams hp;
+    std::vector<LayerW> layers;           // n_layer trunk layers, then the MTP layer
+    cpv_weight *tok_embd = nullptr, *output = nullptr;
+    float* output_norm = nullptr;
+    // MTP extras (blk.{n_layer}.nextn.*)
+    cpv_weight *eh_proj = nullptr, *mtp_embed = nullptr, *mtp_head = nullptr;
+    float *enorm = nullptr, *hnorm = nullptr, *mtp_head_norm = nullptr;
+    std::vector<void*> allocs;            // norm vectors
+    std::vector<cpv_weight*> weights;
+};
+
+struct cpv_session {
+    cpv_model* model = nullptr;
+    int64_t n_ctx = 0, mtp_ctx = 0, v_stride = 0, mtp_v_stride = 0;
+    int64_t n_past = 0, mtp_past = 0;
+    int max_batch = 0;
+    std::vector<uint16_t*> kc, vt;        // per layer; the last pair is the MTP cache
+    float* rope = nullptr;                // [n_ctx + 2][n_rot/2][2]
+    // activations, max_batch rows
+    float *x, *xn, *qg, *kk, *vv, *q, *att, *gated, *o, *up, *gt, *act, *h, *logits, *e, *cat, *d, *dsa;
+    float *mtp_logits, *hn, *hsrc;
+    int32_t *tok, *preds, *chain;
+    float* conf;
+    void* actbuf;                         // quantized activations
+    size_t actbuf_bytes;
+    float* tap = nullptr;                 // attention outputs of each call, when set
+    int64_t tap_cap = 0, tap_off = 0;
+    std::vector<void*> allocs;
+};
+
+static cpv_status dev_alloc(cpv_ctx* ctx, std::vector<void*>& list, size_t bytes, void** out)
+{
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 16);
+    if (e != hipSuccess) return cpv_hip_fail(ctx, e, "hipMalloc");
+    list.push_back(p);
+    *out = p;
+    return CPV_OK;
+}
+
+extern "C" cpv_status cpv_model_create(cpv_ctx* ctx, const cpv_hparams* hp, cpv_model** out)
+{
+    if (!ctx || !hp || !out) return cpv_fail(ctx, CPV_EINVAL, "model: null argument");
+    *out = nullptr;
+    if (hp->n_layer < 1 || hp->n_embd < 1 || hp->n_head < 1 || hp->n_head_kv < 1 || hp->n_head % hp->n_head_kv ||
+        (hp->head_dim != 64 && hp->head_dim != 128) || hp->n_rot < 0 || hp->n_rot > hp->head_dim ||
+        (hp->n_rot & 1) || hp->n_ff < 1 || hp->n_vocab < 1)
+        return cpv_fail(ctx, CPV_EINVAL, "model: unsupported hyper-parameters");
+    cpv_model* m = new (std::nothrow) cpv_model();
+    if (!m) return cpv_fail(ctx, CPV_ENOMEM, "model: host allocation");
+    m->ctx = ctx;
+    m->hp = *hp;
+    m->layers.resize(hp->n_layer + (hp->has_mtp ? 1 : 0));
+    *out = m;
+    return CPV_OK;
+}
+
+extern "C" void cpv_model_free(cpv_model* m)
+{
+    if (!m) return;
+    for (cpv_weight* w : m->weights) cpv_weight_free(w);
+    for (void* p : m->allocs) (void)hipFree(p);
+    delete m;
+}
+
+static bool parse_blk(const std::string& name, int* il, std::string* rest)
+{
+    if (name.rfind("blk.", 0) != 0) return false;
+    size_t dot = name.find('.', 4);
+    if (dot == std::string::npos) return false;
+    *il = atoi(name.substr(4, dot - 4).c_str());
+    *rest = name.substr(dot + 1);
+    return true;
+}
+
+extern "C" cpv_status cpv_model_set_tensor(cpv_model* m, const char* name_c, int type, const void* data,
+                                           int on_device, int64_t ne0, int64_t ne1)
+{
+    if (!m || !name_c || !data || ne0 < 1 || ne1 < 1) return cpv_fail(m ? m->ctx : nullptr, CPV_EINVAL, "set_tensor: bad arguments");
+    cpv_ctx* ctx = m->ctx;
+    const std::string name(name_c);
+    int il = -1;
+    std::string rest;
+    const bool blk = parse_blk(name, &il, &rest);
+    const int nl = m->hp.n_layer;
+    if (blk && (il < 0 || il >= (int)m->layers.size()))
+        return cpv_fail(ctx, CPV_EINVAL, "set_tensor: %s: layer out of range", name_c);
+
+    auto norm = [&](float** dst) -> cpv_status {
+        if (type != CPV_F32 || ne1 != 1) return cpv_fail(ctx, CPV_EINVAL, "set_tensor: %s must be F32 [n]", name_c);
+        void* p = nullptr;
+        cpv_status st = dev_alloc(ctx, m->allocs, (size_t)ne0 * 4, &p);
+        if (st != CPV_OK) return st;
+        CPV_HIP(ctx, hipMemcpyAsync(p, data, (size_t)ne0 * 4, on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                                    ctx->stream));
+        CPV_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        *dst = (float*)p;
+        return CPV_OK;
+    };
+    auto lin = [&](cpv_weight** dst) -> cpv_status {
+        cpv_weight* w = nullptr;
+        cpv_status st = on_device ? cpv_weight_from_device(ctx, type, data, ne1, ne0, &w)
+                                  : cpv_weight_upload(ctx, type, data, ne1, ne0, &w);
+        if (st != CPV_OK) return st;
+        m->weights.push_back(w);
+        *dst = w;
+        return CPV_OK;
+    };
+
+    if (name == "token_embd.weight") return lin(&m->tok_embd);
+    if (name == "output.weight") return lin(&m->output);
+    if (name == "output_norm.weight") return norm(&m->output_norm);
+    if (!blk) return cpv_fail(ctx, CPV_EINVAL, "set_tensor: unknown tensor %s", name_c);
+    LayerW& L = m->layers[il];
+    if (rest == "attn_norm.weight") return norm(&L.attn_norm);
+    if (rest == "post_attention_norm.weight") return norm(&L.post_norm);
+    if (rest == "attn_q_norm.weight") return norm(&L.q_norm);
+    if (rest == "attn_k_norm.weight") return norm(&L.k_norm);
+    if (rest == "attn_q.weight") return lin(&L.wq);
+    if (rest == "attn_k.weight") return lin(&L.wk);
+    if (rest == "attn_v.weight") return lin(&L.wv);
+    if (rest == "attn_output.weight") return lin(&L.wo);
+    if (rest == "ffn_gate.weight") return lin(&L.gate);
+    if (rest == "ffn_up.weight") return lin(&L.up);
+    if (rest == "ffn_down.weight") return lin(&L.down);
+    if (il == nl) {
+        if (rest == "nextn.eh_proj.weight") return lin(&m->eh_proj);
+        if (rest == "nextn.enorm.weight") return norm(&m->enorm);
+        if (rest == "nextn.hnorm.weight") return norm(&m->hnorm);
+        if (rest == "nextn.embed_tokens.weight") return lin(&m->mtp_embed);
+        if (rest == "nextn.shared_head_norm.weight") return norm(&m->mtp_head_norm);
+        if (rest == "nextn.shared_head_head.weight") return lin(&m->mtp_head);
+    }
+    return cpv_fail(ctx, CPV_EINVAL, "set_tensor: unknown tensor %s", name_c);
+}
+
+extern "C" cpv_status cpv_model_ready(cpv_model* m)
+{
+    if (!m) return CPV_EINVAL;
+    cpv_ctx* ctx = m->ctx;
+    const cpv_hparams& hp = m->hp;
+    if (!m->tok_embd || !m->output_norm) return cpv_fail(ctx, CPV_EINVAL, "model: token_embd / output_norm missing");
+    if (!m->output) m->output = m->tok_embd;           // tied head (qwen35.rs:2789)
+    const int64_t E = hp.n_embd, hd = hp.head_dim, H = hp.n_head, Hkv = hp.n_head_kv, F = hp.n_ff;
+    auto shape = [&](const cpv_weight* w, int64_t n, int64_t k, const char* what) -> cpv_status {
+        if (!w) return cpv_fail(ctx, CPV_EINVAL, "model: %s missing", what);
+        if (w->n != n || w->k != k)
+            return cpv_fail(ctx, CPV_EINVAL, "model: %s is [%lld x %lld], want [%lld x %lld]", what, (long long)w->n,
+                            (long long)w->k, (long long)n, (long long)k);
+        return CPV_OK;
+    };
+    cpv_status st;
+    if ((st = shape(m->tok_embd, hp.n_vocab, E, "token_embd")) || (st = shape(m->output, hp.n_vocab, E, "output")))
+        return st;
+    for (size_t il = 0; il < m->layers.size(); il++) {
+        const LayerW& L = m->layers[il];
+        if (!L.attn_norm || !L.post_norm || !L.q_norm || !L.k_norm)
+            return cpv_fail(ctx, CPV_EINVAL, "model: layer %zu norms missing", il);
+        if ((st = shape(L.wq, 2 * H * hd, E, "attn_q")) || (st = shape(L.wk, Hkv * hd, E, "attn_k")) ||
+            (st = shape(L.wv, Hkv * hd, E, "attn_v")) || (st = shape(L.wo, E, H * hd, "attn_output")) ||
+            (st = shape(L.gate, F, E, "ffn_gate")) || (st = shape(L.up, F, E, "ffn_up")) ||
+            (st = shape(L.down, E, F, "ffn_down")))
+            return st;
+    }
+    if (hp.has_mtp) {
+        if (!m->enorm || !m->hnorm) return cpv_fail(ctx, CPV_EINVAL, "model: nextn norms missing");
+        if ((st = shape(m->eh_proj, E, 2 * E, "nextn.eh_proj"))) return st;
+        if (!m->mtp_embed) m->mtp_embed = m->tok_embd;
+        if (!m->mtp_head) m->mtp_head = m->output;
+        if (!m->mtp_head_norm) m->mtp_head_norm = m->output_norm;
+    }
+    return CPV_OK;
+}
+
+// ---------------------------------------------------------------- session
+extern "C" void cpv_session_free(cpv_session* s)
+{
+    if (!s) return;
+    (void)hipStreamSynchronize(s->model->ctx->stream);
+    for (void* p : s->allocs) (void)hipFree(p);
+    delete s;
+}
+
+extern "C" cpv_status cpv_session_create(cpv_model* m, int64_t n_ctx, int32_t max_batch, cpv_session** out)
+{
+    if (!m || !out || n_ctx < 1 || max_batch < 1 || max_batch > 4096)
+        return cpv_fail(m ? m->ctx : nullptr, CPV_EINVAL, "session: bad arguments");
+    cpv_ctx* ctx = m->ctx;
+    *out = nullptr;
+    const cpv_hparams& hp = m->hp;
+    cpv_session* s = new (std::nothrow) cpv_session();
+    if (!s) return cpv_fail(ctx, CPV_ENOMEM, "session: host allocation");
+    s->model = m;
+    s->n_ctx = n_ctx;
+    s->mtp_ctx = n_ctx < 16384 ? n_ctx : 16384;       // mtp_ctx_cap (qwen35.rs:366-373)
+    s->v_stride = (n_ctx + 7) / 8 * 8;
+    s->mtp_v_stride = (s->mtp_ctx + 7) / 8 * 8;
+    s->max_batch = max_batch;
+    const int64_t E = hp.n_embd, hd = hp.head_dim, H = hp.n_head, Hkv = hp.n_head_kv, F = hp.n_ff, V = hp.n_vocab;
+    const int64_t T = max_batch;
+    cpv_status st = CPV_OK;
+    auto A = [&](size_t bytes, void** p) {
+        if (st == CPV_OK) st = dev_alloc(ctx, s->allocs, bytes, p);
+    };
+    const size_t layers = m->layers.size();
+    s->kc.resize(layers);
+    s->vt.resize(layers);
+    for (size_t il = 0; il < layers; il++) {
+        const bool mtp = (int)il == hp.n_layer;
+        const int64_t rows = mtp ? s->mtp_ctx : n_ctx, vs = mtp ? s->mtp_v_stride : s->v_stride;
+        A((size_t)rows * Hkv * hd * 2, (void**)&s->kc[il]);
+        A((size_t)Hkv * hd * vs * 2, (void**)&s->vt[il]);
+        if (st == CPV_OK) CPV_HIP(ctx, hipMemsetAsync(s->vt[il], 0, (size_t)Hkv * hd * vs * 2, ctx->stream));
+    }
+    A((size_t)T * E * 4, (void**)&s->x);
+    A((size_t)T * 2 * E * 4, (void**)&s->xn);
+    A((size_t)T * 2 * H * hd * 4, (void**)&s->qg);
+    A((size_t)T * Hkv * hd * 4, (void**)&s->kk);
+    A((size_t)T * Hkv * hd * 4, (void**)&s->vv);
+    A((size_t)T * H * hd * 4, (void**)&s->q);
+    A((size_t)T * H * hd * 4, (void**)&s->att);
+    A((size_t)T * H * hd * 4, (void**)&s->gated);
+    A((size_t)T * E * 4, (void**)&s->o);
+    A((size_t)T * F * 4, (void**)&s->up);
+    A((size_t)T * F * 4, (void**)&s->gt);
+    A((size_t)T * F * 4, (void**)&s->act);
+    A((size_t)T * E * 4, (void**)&s->h);
+    A((size_t)T * V * 4, (void**)&s->logits);
+    A((size_t)T * V * 4, (void**)&s->mtp_logits);
+    A((size_t)T * E * 4, (void**)&s->hn);
+    A((size_t)T * E * 4, (void**)&s->hsrc);
+    A((size_t)T * E * 4, (void**)&s->e);
+    A((size_t)T * 2 * E * 4, (void**)&s->cat);
+    A((size_t)T * E * 4, (void**)&s->d);
+    A((size_t)T * E * 4, (void**)&s->dsa);
+    A((size_t)T * 4, (void**)&s->tok);
+    A((size_t)T * 4, (void**)&s->preds);
+    A((size_t)16 * T * 4, (void**)&s->chain);
+    A((size_t)16 * T * 4, (void**)&s->conf);
+    const int64_t kmax = (2 * E > F ? 2 * E : F) > H * hd ? (2 * E > F ? 2 * E : F) : H * hd;
+    s->actbuf_bytes = cpv_act_bytes(CPV_Q4_K, kmax, T) > cpv_act_bytes(CPV_Q8_0, kmax, T)
+                    ? cpv_act_bytes(CPV_Q4_K, kmax, T) : cpv_act_bytes(CPV_Q8_0, kmax, T);
+    A(s->actbuf_bytes, &s->actbuf);
+    // rope table: positions up to n_ctx + 1 (the MTP head runs one position ahead)
+    const int64_t npos = n_ctx + 2, nrot = hp.n_rot;
+    if (st == CPV_OK && nrot > 0) {
+        std::vector<float> tab((size_t)npos * nrot);
+        const float theta_scale = powf(hp.freq_base, -2.0f / (float)nrot);
+        const int32_t* sec = hp.rope_sections;
+        const int sect = sec[0] + sec[1] + sec[2] + sec[3];
+        for (int64_t p = 0; p < npos; p++) {
+            float th_t = (float)p, th_h = (float)p, th_w = (float)p, th_e = 0.0f;
+            for (int64_t i = 0; i < nrot / 2; i++) {
+                float theta = th_t;
+                if (sect > 0) {
+                    const int sc = (int)(i % sect);
+                    if (sc % 3 == 1 && sc < 3 * sec[1]) theta = th_h;
+                    else if (sc % 3 == 2 && sc < 3 * sec[2]) theta = th_w;
+                    else if (sc % 3 == 0 && sc < 3 * sec[0]) theta = th_t;
+                    else theta = th_e;
+                }
+                tab[(size_t)p * nrot + 2 * i] = cosf(theta);
+                tab[(size_t)p * nrot + 2 * i + 1] = sinf(theta);
+                th_t *= theta_scale;
+                th_h *= theta_scale;
+                th_w *= theta_scale;
+                th_e *= theta_scale;
+            }
+        }
+        A(tab.size() * 4, (void**)&s->rope);
+        if (st == CPV_OK) {
+            CPV_HIP(ctx, hipMemcpyAsync(s->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+            CPV_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        }
+    }
+    if (st != CPV_OK) {
+        cpv_session_free(s);
+        return st;
+    }
+    *out = s;
+    return CPV_OK;
+}
+
+extern "C" cpv_status cpv_session_set_pos(cpv_session* s, int64_t n_past, int64_t mtp_past)
+{
+    if (!s || n_past < 0 || n_past > s->n_ctx || mtp_past < 0 || mtp_past > s->mtp_ctx)
+        return cpv_fail(s ? s->model->ctx : nullptr, CPV_EINVAL, "session: position out of range");
+    s->n_past = n_past;
+    s->mtp_past = mtp_past;
+    return CPV_OK;
+}
+
+extern "C" cpv_status cpv_session_set_attn_tap(cpv_session* s, float* tap_dev, int64_t capacity_floats)
+{
+    if (!s || capacity_floats < 0 || (!tap_dev && capacity_floats))
+        return cpv_fail(s ? s->model->ctx : nullptr, CPV_EINVAL, "set_attn_tap: bad arguments");
+    s->tap = tap_dev;
+    s->tap_cap = tap_dev ? capacity_floats : 0;
+    s->tap_off = 0;
+    return CPV_OK;
+}
+
+extern "C" cpv_status cpv_session_get_pos(const cpv_session* s, int64_t* n_past, int64_t* mtp_past)
+{
+    if (!s) return CPV_EINVAL;
+    if (n_past) *n_past = s->n_past;
+    if (mtp_past) *mtp_past = s->mtp_past;
+    return CPV_OK;
+}
+
+// ---------------------------------------------------------------- forward
+namespace {
+
+cpv_status rmsnorm(cpv_ctx* ctx, const float* x, int64_t xs, const float* w, float* y, int64_t ys, int64_t rows,
+                   int n, float eps)
+{
+    rmsnorm_kernel<<<(unsigned)rows, 256, 0, ctx->stream>>>(x, xs, w, y, ys, n, eps);
+    CPV_HIP(ctx, hipGetLastError());
+    return CPV_OK;
+}
+
+// one attention block + FFN block of layer L on s->x (in place), T rows
+cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_pos0, int64_t kv_row0,
+                 int64_t attn_past, uint16_t* kc, uint16_t* vt, int64_t v_stride, bool write)
+{
+    cpv_model* m = s->model;
+    cpv_ctx* ctx = m->ctx;
+    const cpv_hparams& hp = m->hp;
+    const int64_t E = hp.n_embd, hd = hp.head_dim, H = hp.n_head, Hkv = hp.n_head_kv, F = hp.n_ff;
+    cpv_status st;
+    cpv_act act;
+    // attention (build_attn_block)
+    if ((st = rmsnorm(ctx, x, E, L.attn_norm, s->xn, E, T, (int)E, hp.rms_eps))) return st;
+    if ((st = cpv_quant_act(ctx, L.wq->type, s->xn, T, E, s->actbuf, &act))) return st;
+    if ((st = cpv_qgemm_act(ctx, L.wq, &act, s->qg))) return st;
+    if (L.wk->type != L.wq->type && (st = cpv_quant_act(ctx, L.wk->type, s->xn, T, E, s->actbuf, &act))) return st;
+    if ((st = cpv_qgemm_act(ctx, L.wk, &act, s->kk))) return st;
+    if (L.wv->type != L.wk->type && (st = cpv_quant_act(ctx, L.wv->type, s->xn, T, E, s->actbuf, &act))) return st;
+    if ((st = cpv_qgemm_act(ctx, L.wv, &act, s->vv))) return st;
+    PrepArgs pa;
+    pa.qg = s->qg;
+    pa.kk = s->kk;
+    pa.vv = s->vv;
+    pa.q_norm = L.q_norm;
+    pa.k_norm = L.k_norm;
+    pa.rope = s->rope;
+    pa.qout = s->q;
+    pa.k_cache = kc;
+    pa.v_cache_t = vt;
+    pa.v_stride = v_stride;
+    pa.rope_pos0 = rope_pos0;
+    pa.kv_row0 = kv_row0;
+    pa.H = (int)H;
+    pa.Hkv = (int)Hkv;
+    pa.hd = (int)hd;
+    pa.n_rot = hp.n_rot;
+    pa.write = write ? 1 : 0;
+    pa.eps = hp.rms_eps;
+    qk_prep_kernel<<<dim3((unsigned)T, (unsigned)(H + Hkv)), (unsigned)hd, 0, ctx->stream>>>(pa);
+    CPV_HIP(ctx, hipGetLastError());
+    const float kq_scale = 1.0f / sqrtf((float)hd);
+    if ((st = cpv_attn_launch(ctx, s->q, kc, vt, v_stride, attn_past, nullptr, T, (int)H, (int)Hkv, (int)hd, kq_scale,
+                              s->att)))
+        return st;
+    if (s->tap) {
+        const int64_t n = (int64_t)T * H * hd;
+        if (s->tap_off + n <= s->tap_cap)
+            CPV_HIP(ctx, hipMemcpyAsync(s->tap + s->tap_off, s->att, (size_t)n * 4, hipMemcpyDeviceToDevice, ctx->stream));
+        s->tap_off += n;
+    }
+    gate_mul_kernel<<<grid_for(T * H * hd), 256, 0, ctx->stream>>>(s->att, s->qg, (int)H, (int)hd, T * H * hd, s->gated);
+    if ((st = cpv_quant_act(ctx, L.wo->type, s->gated, T, H * hd, s->actbuf, &act))) return st;
+    if ((st = cpv_qgemm_act(ctx, L.wo, &act, s->o))) return st;
+    add_kernel<<<grid_for(T * E), 256, 0, ctx->stream>>>(s->o, x, x, T * E);
+    // FFN
+    if ((st = rmsnorm(ctx, x, E, L.post_norm, s->xn, E, T, (int)E, hp.rms_eps))) return st;
+    if ((st = cpv_quant_act(ctx, L.up->type, s->xn, T, E, s->actbuf, &act))) return st;
+    if ((st = cpv_qgemm_act(ctx, L.up, &act, s->up))) return st;
+    if (L.gate->type != L.up->type && (st = cpv_quant_act(ctx, L.gate->type, s->xn, T, E, s->actbuf, &act))) return st;
+    if ((st = cpv_qgemm_act(ctx, L.gate, &act, s->gt))) return st;
+    swiglu_kernel<<<grid_for(T * F), 256, 0, ctx->stream>>>(s->gt, s->up, s->act, T * F);
+    if ((st = cpv_quant_act(ctx, L.down->type, s->act, T, F, s->actbuf, &act))) return st;
+    if ((st = cpv_qgemm_act(ctx, L.down, &act, s->d))) return st;
+    add_kernel<<<grid_for(T * E), 256, 0, ctx->stream>>>(s->d, x, x, T * E);
+    CPV_HIP(ctx, hipGetLastError());
+    return CPV_OK;
+}
+
+cpv_status project(cpv_session* s, const cpv_weight* w, const float* x, int T, float* y)
+{
+    cpv_act act;
+    cpv_status st = cpv_quant_act(s->model->ctx, w->type, x, T, w->k, s->actbuf, &act);
+    if (st != CPV_OK) return st;
+    return cpv_qgemm_act(s->model->ctx, w, &act, y);
+}
+
+}  // namespace
+
+extern "C" cpv_status cpv_prefill(cpv_session* s, const int32_t* tokens_dev, int t)
+{
+    if (!s || !tokens_dev || t < 1 || t > s->max_batch)
+        return cpv_fail(s ? s->model->ctx : nullptr, CPV_EINVAL, "prefill: bad arguments");
+    cpv_model* m = s->model;
+    cpv_ctx* ctx = m->ctx;
+    if (s->n_past + t > s->n_ctx) return cpv_fail(ctx, CPV_EINVAL, "prefill: context overflow");
+    cpv_status st;
+    s->tap_off = 0;
+    CPV_HIP(ctx, hipMemcpyAsync(s->tok, tokens_dev, (size_t)t * 4, hipMemcpyDeviceToDevice, ctx->stream));
+    if ((st = cpv_get_rows(ctx, m->tok_embd, s->tok, t, s->x))) return st;
+    for (int il = 0; il < m->hp.n_layer; il++)
+        if ((st = block(s, m->layers[il], s->x, t, s->n_past, s->n_past, s->n_past, s->kc[il], s->vt[il], s->v_stride, true)))
+            return st;
+    s->n_past += t;
+    return CPV_OK;
+}
+
+extern "C" cpv_status cpv_verify_step(cpv_session* s, const int32_t* tokens_dev, int t, int depth,
+                                      const float* noise_dev, cpv_round_out* out)
+{
+    if (!s || !tokens_dev || !out || t < 1 || t > s->max_batch || depth < 0 || depth > 16)
+        return cpv_fail(s ? s->model->ctx : nullptr, CPV_EINVAL, "verify_step: bad arguments");
+    cpv_model* m = s->model;
+    cpv_ctx* ctx = m->ctx;
+    const cpv_hparams& hp = m->hp;
+    const int64_t E = hp.n_embd, V = hp.n_vocab;
+    if (s->n_past + t > s->n_ctx) return cpv_fail(ctx, CPV_EINVAL, "verify_step: context overflow");  // qwen35.rs:1718-1720
+    if (depth > 0 && !hp.has_mtp) return cpv_fail(ctx, CPV_EINVAL, "verify_step: model has no MTP head");
+    // the draft head's window is bounded; when it fills, it restarts (qwen35.rs:1730-1735)
+    if (s->mtp_past + t > s->mtp_ctx) s->mtp_past = 0;
+    cpv_status st;
+    s->tap_off = 0;
+    CPV_HIP(ctx, hipMemcpyAsync(s->tok, tokens_dev, (size_t)t * 4, hipMemcpyDeviceToDevice, ctx->stream));
+    if ((st = cpv_get_rows(ctx, m->tok_embd, s->tok, t, s->x))) return st;
+    for (int il = 0; il < hp.n_layer; il++)
+        if ((st = block(s, m->layers[il], s->x, t, s->n_past, s->n_past, s->n_past, s->kc[il], s->vt[il], s->v_stride, true)))
+            return st;
+    // LM head and in-graph argmax (qwen35.rs:2788-2821)
+    if ((st = rmsnorm(ctx, s->x, E, m->output_norm, s->h, E, t, (int)E, hp.rms_eps))) return st;
+    if ((st = project(s, m->output, s->h, t, s->logits))) return st;
+    if ((st = cpv_argmax_rows(ctx, s->logits, noise_dev, t, V, s->preds))) return st;
+    // fused MTP draft chain (qwen35.rs:2840-2962)
+    if (depth > 0) {
+        const LayerW& ML = m->layers[hp.n_layer];
+        const float* h_src = s->h;
+        const int32_t* tok_src = s->preds;
+        for (int step = 0; step < depth; step++) {
+            if ((st = cpv_get_rows(ctx, m->mtp_embed, tok_src, t, s->e))) return st;
+            if ((st = rmsnorm(ctx, s->e, E, m->enorm, s->cat, 2 * E, t, (int)E, hp.rms_eps))) return st;
+            if ((st = rmsnorm(ctx, h_src, E, m->hnorm, s->cat + E, 2 * E, t, (int)E, hp.rms_eps))) return st;
+            if ((st = project(s, m->eh_proj, s->cat, t, s->dsa))) return st;
+            // positions rope_base + i + 1, rows mtp_past + i; only link 0 writes (:1858-1866, :2898-2906)
+            if ((st = block(s, ML, s->dsa, t, s->n_past + 1, s->mtp_past, s->mtp_past, s->kc[hp.n_layer],
+                            s->vt[hp.n_layer], s->mtp_v_stride, step == 0)))
+                return st;
+            // h_next = rms(d, shared_head_norm or output_norm), then the draft head
+            if ((st = rmsnorm(ctx, s->dsa, E, m->mtp_head_norm, s->hn, E, t, (int)E, hp.rms_eps))) return st;
+            if ((st = project(s, m->mtp_head, s->hn, t, s->mtp_logits))) return st;
+            int32_t* ids = s->chain + (size_t)step * t;
+            if ((st = cpv_argmax_rows(ctx, s->mtp_logits, nullptr, t, V, ids))) return st;
+            peak_kernel<<<(unsigned)t, 1024, 0, ctx->stream>>>(s->mtp_logits, V, s->conf + (size_t)step * t);
+            CPV_HIP(ctx, hipGetLastError());
+            // the next link feeds on this link's prediction and hidden
+            CPV_HIP(ctx, hipMemcpyAsync(s->hsrc, s->hn, (size_t)t * E * 4, hipMemcpyDeviceToDevice, ctx->stream));
+            h_src = s->hsrc;
+            tok_src = ids;
+        }
+    }
+    s->n_past += t;
+    out->n_past = s->n_past;
+    out->preds_dev = s->preds;
+    out->chain_dev = s->chain;
+    out->conf_dev = s->conf;
+    out->logits_dev = s->logits;
+    out->hidden_dev = s->h;
+    return CPV_OK;
+}

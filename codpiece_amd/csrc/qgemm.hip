@@ -348,36 +348,57 @@ int cpv_qgemm_window(int type, int64_t k)
     return 52 - isum_bits(type) - b;
 }
 
-cpv_status cpv_qgemm_launch(cpv_ctx* ctx, const cpv_weight* w, const float* x, int64_t m, float* y)
+size_t cpv_act_bytes(int type, int64_t k, int64_t m)
 {
-    const int U = (int)(w->passes * 4);
-    const int64_t Kp = (int64_t)U * 256;
-    const bool kq = w->type != CPV_Q8_0;
-    // workspace: codes, scales, sums
-    const size_t qa_b = (size_t)m * Kp;
-    const size_t da_b = (size_t)m * U * (kq ? 1 : 8) * 4;
+    const int64_t U = ((k + 255) / 256 + 3) / 4 * 4;
+    const bool kq = type != CPV_Q8_0;
+    const size_t qa_b = ((size_t)m * U * 256 + 255) & ~(size_t)255;
+    const size_t da_b = ((size_t)m * U * (kq ? 1 : 8) * 4 + 255) & ~(size_t)255;
     const size_t bs_b = kq ? (size_t)m * U * (8 + 16) * 4 : 0;
-    void* ws = nullptr;
-    cpv_status st = cpv_workspace(ctx, ((qa_b + 255) & ~(size_t)255) + ((da_b + 255) & ~(size_t)255) + bs_b, &ws);
-    if (st != CPV_OK) return st;
-    int8_t* qa = (int8_t*)ws;
-    float* da = (float*)((uint8_t*)ws + ((qa_b + 255) & ~(size_t)255));
-    int32_t* bs32 = (int32_t*)((uint8_t*)da + ((da_b + 255) & ~(size_t)255));
-    int32_t* bs16 = bs32 + (size_t)m * U * 8;
-    dim3 qgrid((unsigned)U, (unsigned)m);
-    if (kq) quant_q8k_kernel<<<qgrid, 256, 0, ctx->stream>>>(x, w->k, U, qa, da, bs32, bs16);
-    else quant_q80_kernel<<<qgrid, 256, 0, ctx->stream>>>(x, w->k, U, qa, da);
-    CPV_HIP(ctx, hipGetLastError());
+    return qa_b + da_b + bs_b;
+}
 
+cpv_status cpv_quant_act(cpv_ctx* ctx, int type, const float* x, int64_t m, int64_t k, void* buf, cpv_act* out)
+{
+    const int U = (int)(((k + 255) / 256 + 3) / 4 * 4);
+    const bool kq = type != CPV_Q8_0;
+    const size_t qa_b = ((size_t)m * U * 256 + 255) & ~(size_t)255;
+    const size_t da_b = ((size_t)m * U * (kq ? 1 : 8) * 4 + 255) & ~(size_t)255;
+    int8_t* qa = (int8_t*)buf;
+    float* da = (float*)((uint8_t*)buf + qa_b);
+    int32_t* bs32 = (int32_t*)((uint8_t*)buf + qa_b + da_b);
+    int32_t* bs16 = bs32 + (size_t)m * U * 8;
+    out->qa = qa;
+    out->da = da;
+    out->bs32 = bs32;
+    out->bs16 = bs16;
+    out->m = m;
+    out->k = k;
+    out->U = U;
+    out->kq = kq;
+    dim3 qgrid((unsigned)U, (unsigned)m);
+    if (kq) quant_q8k_kernel<<<qgrid, 256, 0, ctx->stream>>>(x, k, U, qa, da, bs32, bs16);
+    else quant_q80_kernel<<<qgrid, 256, 0, ctx->stream>>>(x, k, U, qa, da);
+    CPV_HIP(ctx, hipGetLastError());
+    return CPV_OK;
+}
+
+cpv_status cpv_qgemm_act(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, float* y)
+{
+    const bool kq = w->type != CPV_Q8_0;
+    if (kq != act->kq || act->k != w->k || act->U != (int)(w->passes * 4))
+        return cpv_fail(ctx, CPV_EINVAL, "qgemm: activation format does not match the weight");
+    const int U = act->U;
+    const int64_t m = act->m;
     const int P = (int)w->passes;
     const int per = (P + 7) / 8;
     const int W = (P + per - 1) / per;
     GemmArgs a;
     a.w = (const uint8_t*)w->data;
     a.ew = w->ew;
-    a.qa = qa;
-    a.da = da;
-    a.bs = w->type == CPV_Q4_K ? bs32 : bs16;
+    a.qa = act->qa;
+    a.da = act->da;
+    a.bs = w->type == CPV_Q4_K ? act->bs32 : act->bs16;
     a.y = y;
     a.N = w->n;
     a.n_pad = w->n_pad;
@@ -385,7 +406,7 @@ cpv_status cpv_qgemm_launch(cpv_ctx* ctx, const cpv_weight* w, const float* x, i
     a.U = U;
     a.Mtot = (int)m;
     a.win = cpv_qgemm_window(w->type, w->k);
-    // activation rows per launch: as many as fit the 160 KiB of LDS
+    // activation rows per launch: as many as fit the workgroup's LDS
     int chunk = m < 16 ? (int)m : 16;
     auto lds = [&](int c) {
         return w->type == CPV_Q4_K ? lds_for<CPV_Q4_K>(c, U, W)
@@ -395,8 +416,6 @@ cpv_status cpv_qgemm_launch(cpv_ctx* ctx, const cpv_weight* w, const float* x, i
     while (chunk > 1 && lds(chunk) > lds_cap) chunk--;
     if (lds(chunk) > lds_cap)
         return cpv_fail(ctx, CPV_EUNSUPPORTED, "qgemm: k=%lld needs more LDS than a CU has", (long long)w->k);
-    // the activation-side arrays are indexed from row m0 inside the kernel
-    a.qa = qa;
     for (int64_t m0 = 0; m0 < m; m0 += chunk) {
         a.m0 = (int)m0;
         a.M = (int)((m - m0) < chunk ? (m - m0) : chunk);
@@ -406,6 +425,17 @@ cpv_status cpv_qgemm_launch(cpv_ctx* ctx, const cpv_weight* w, const float* x, i
         if (s2 != CPV_OK) return s2;
     }
     return CPV_OK;
+}
+
+cpv_status cpv_qgemm_launch(cpv_ctx* ctx, const cpv_weight* w, const float* x, int64_t m, float* y)
+{
+    void* ws = nullptr;
+    cpv_status st = cpv_workspace(ctx, cpv_act_bytes(w->type, w->k, m), &ws);
+    if (st != CPV_OK) return st;
+    cpv_act act;
+    st = cpv_quant_act(ctx, w->type, x, m, w->k, ws, &act);
+    if (st != CPV_OK) return st;
+    return cpv_qgemm_act(ctx, w, &act, y);
 }
 
 extern "C" cpv_status cpv_qgemm(cpv_ctx* ctx, const cpv_weight* w, const float* x_dev, int64_t m, float* y_dev)

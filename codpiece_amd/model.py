@@ -1,0 +1,202 @@
+"""Host mirror of codpiece-model's verify-round interface over the C ABI.
+
+`Model` loads tensors by GGUF name (Weights::load, crates/codpiece-model/src/
+lib.rs:128-311); `Session` owns the KV caches and positions (Session::new_spec,
+qwen35.rs:528-649); `Session.step_fused_cached` is Qwen35::step_fused_cached
+(qwen35.rs:1693-1948) and returns a `FusedOut` (qwen35.rs:817-828);
+`fused_generate` is the CLI's fused speculative loop (crates/codpiece-cli/src/
+main.rs:643-931).  All arithmetic runs in libcpv.so.
+"""
+import ctypes
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import CpvError, Hparams, RoundOut
+
+
+def make_hparams(n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, n_rot=None,
+                 rope_sections=(0, 0, 0, 0), rms_eps=1e-6, freq_base=1e6, has_mtp=True):
+    hp = Hparams()
+    hp.n_layer, hp.n_embd, hp.n_head, hp.n_head_kv = n_layer, n_embd, n_head, n_head_kv
+    hp.head_dim, hp.n_ff, hp.n_vocab = head_dim, n_ff, n_vocab
+    hp.n_rot = head_dim if n_rot is None else n_rot
+    for i, v in enumerate(rope_sections):
+        hp.rope_sections[i] = v
+    hp.rms_eps, hp.freq_base, hp.has_mtp = rms_eps, freq_base, int(has_mtp)
+    return hp
+
+
+class Model:
+    def __init__(self, ctx, hp):
+        self.ctx, self.hp = ctx, hp
+        h = ctypes.c_void_p()
+        ctx._check(ctx.lib.cpv_model_create(ctx.h, ctypes.byref(hp), ctypes.byref(h)))
+        self.h = h
+
+    def set_tensor(self, name, qtype, data, ne0, ne1):
+        """data: numpy (host bytes) or a cuda tensor (device bytes), ggml ne order."""
+        if isinstance(data, torch.Tensor):
+            ptr, dev = ctypes.c_void_p(data.data_ptr()), 1
+        else:
+            data = np.ascontiguousarray(data)
+            ptr, dev = data.ctypes.data_as(ctypes.c_void_p), 0
+        self.ctx._check(self.ctx.lib.cpv_model_set_tensor(self.h, name.encode(), qtype, ptr, dev, ne0, ne1))
+
+    def ready(self):
+        self.ctx._check(self.ctx.lib.cpv_model_ready(self.h))
+
+    def free(self):
+        if self.h:
+            self.ctx.lib.cpv_model_free(self.h)
+            self.h = None
+
+
+@dataclass
+class FusedOut:
+    preds: list
+    chain: list = field(default_factory=list)   # [depth][t]
+    conf: list = field(default_factory=list)    # [depth][t]
+    logits: object = None                       # torch [t][V] on the device, when wanted
+    hidden: object = None                       # torch [t][E] on the device, when wanted
+
+
+class Session:
+    def __init__(self, model, n_ctx, max_batch=64):
+        self.model, self.ctx = model, model.ctx
+        h = ctypes.c_void_p()
+        self.ctx._check(self.ctx.lib.cpv_session_create(model.h, n_ctx, max_batch, ctypes.byref(h)))
+        self.h = h
+        self.max_batch = max_batch
+        self._tok = torch.empty(max_batch, dtype=torch.int32, device=self.ctx.torch_device)
+
+    @property
+    def pos(self):
+        a, b = ctypes.c_int64(), ctypes.c_int64()
+        self.ctx._check(self.ctx.lib.cpv_session_get_pos(self.h, ctypes.byref(a), ctypes.byref(b)))
+        return a.value, b.value
+
+    def set_pos(self, n_past, mtp_past):
+        self.ctx._check(self.ctx.lib.cpv_session_set_pos(self.h, n_past, mtp_past))
+
+    def set_attn_tap(self, tap):
+        """Copy every attention output of the next calls into `tap` (a float32
+        cuda tensor), blocks in call order; None clears it."""
+        if tap is None:
+            self.ctx._check(self.ctx.lib.cpv_session_set_attn_tap(self.h, None, 0))
+        else:
+            self._tap = tap
+            self.ctx._check(self.ctx.lib.cpv_session_set_attn_tap(self.h, ctypes.c_void_p(tap.data_ptr()),
+                                                                  tap.numel()))
+
+    @property
+    def n_past(self):
+        return self.pos[0]
+
+    @property
+    def mtp_past(self):
+        return self.pos[1]
+
+    def _tokens(self, tokens):
+        t = len(tokens)
+        self._tok[:t].copy_(torch.as_tensor(np.asarray(tokens, dtype=np.int32)))
+        return t
+
+    def prefill(self, tokens):
+        t = self._tokens(tokens)
+        self.ctx._check(self.ctx.lib.cpv_prefill(self.h, ctypes.c_void_p(self._tok.data_ptr()), t))
+
+    def step_fused_cached(self, tokens, depth, want_logits=False, noise=None):
+        """Verify `tokens` and chain `depth` drafts; greedy in-graph argmax,
+        gumbel argmax when `noise` ([t][V] device tensor) is given."""
+        t = self._tokens(tokens)
+        out = RoundOut()
+        nz = None if noise is None else ctypes.c_void_p(noise.data_ptr())
+        self.ctx._check(self.ctx.lib.cpv_verify_step(self.h, ctypes.c_void_p(self._tok.data_ptr()), t, depth, nz,
+                                                     ctypes.byref(out)))
+        V, E = self.model.hp.n_vocab, self.model.hp.n_embd
+        preds = _device_view(out.preds_dev, t, torch.int32, self.ctx.torch_device).cpu().tolist()
+        chain = []
+        conf = []
+        if depth:
+            ch = _device_view(out.chain_dev, depth * t, torch.int32, self.ctx.torch_device).cpu().view(depth, t)
+            cf = _device_view(out.conf_dev, depth * t, torch.float32, self.ctx.torch_device).cpu().view(depth, t)
+            chain, conf = ch.tolist(), cf.tolist()
+        logits = hidden = None
+        if want_logits:
+            logits = _device_view(out.logits_dev, t * V, torch.float32, self.ctx.torch_device).view(t, V).clone()
+            hidden = _device_view(out.hidden_dev, t * E, torch.float32, self.ctx.torch_device).view(t, E).clone()
+        return FusedOut(preds, chain, conf, logits, hidden)
+
+    def free(self):
+        if self.h:
+            self.ctx.lib.cpv_session_free(self.h)
+            self.h = None
+
+
+def _device_view(ptr, n, dtype, device):
+    """A torch view of library-owned device memory (valid until the next call)."""
+    class _Arr:
+        __cuda_array_interface__ = {
+            "shape": (n,), "typestr": {torch.int32: "<i4", torch.float32: "<f4"}[dtype],
+            "data": (ptr, False), "version": 3, "strides": None,
+        }
+    return torch.as_tensor(_Arr(), device=device)
+
+
+@dataclass
+class FusedStats:
+    accepted: int
+    proposed: int
+    rounds: int
+    prefill_s: float = 0.0
+    decode_s: float = 0.0
+
+
+def fused_generate(session, prompt, n_gen, depth, tail=64, bulk=512, timer=None):
+    """cmd_fused (crates/codpiece-cli/src/main.rs:643-931) at a fixed depth with
+    greedy acceptance; the seeded model has no tokenizer, so no EOS stop.
+    Returns (committed tokens, FusedStats)."""
+    import time
+    t0 = time.perf_counter()
+    split = max(0, len(prompt) - tail)
+    bulk = min(bulk, getattr(session, "max_batch", bulk))
+    for c in range(0, split, bulk):
+        session.prefill(prompt[c:min(split, c + bulk)])
+    out = session.step_fused_cached(prompt[split:], depth)
+    n_past, mtp_past = session.pos
+    session.set_pos(n_past, mtp_past + len(out.preds))
+    last = len(out.preds) - 1
+    committed = [out.preds[last]]
+    drafts = [out.chain[l][last] for l in range(depth)]
+    t1 = time.perf_counter()
+    accepted = proposed = rounds = 0
+    while len(committed) < n_gen:
+        batch = [committed[-1]] + drafts
+        out = session.step_fused_cached(batch, depth)
+        rounds += 1
+        proposed += len(drafts)
+        keep = 0
+        while keep < len(drafts) and out.preds[keep] == drafts[keep]:
+            keep += 1
+        accepted += keep
+        done = False
+        for d in drafts[:keep]:
+            committed.append(d)
+            if len(committed) >= n_gen:
+                done = True
+                break
+        if done:
+            break
+        committed.append(out.preds[keep])
+        drafts = [out.chain[l][keep] for l in range(depth)]
+        over = len(batch) - (keep + 1)
+        n_past, mtp_past = session.pos
+        session.set_pos(n_past - over, mtp_past + keep + 1)
+    t2 = time.perf_counter()
+    return committed, FusedStats(accepted, proposed, rounds, t1 - t0, t2 - t1)
+
+
+__all__ = ["Model", "Session", "FusedOut", "FusedStats", "make_hparams", "fused_generate", "CpvError"]

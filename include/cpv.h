@@ -102,8 +102,8 @@ cpv_status  cpv_qgemm(cpv_ctx* ctx, const cpv_weight* w, const float* x_dev, int
  *                reference's causal mask).  Node i sees all context rows plus
  *                its ancestors and itself.
  *   out_dev      f32 [t][h * d]
- * Requires t <= 64, (h / h_kv) * t <= 96, d in {64, 128}, v_stride >= n_past
- * + t and a multiple of 8, 16-byte aligned caches. */
+ * Requires d in {64, 128}, t <= 64 for a tree (t <= 8192 for a chain),
+ * v_stride >= n_past + t and a multiple of 8, 16-byte aligned caches. */
 cpv_status  cpv_attn(cpv_ctx* ctx, const float* q_dev, const uint16_t* k_cache_dev,
                      const uint16_t* v_cache_t_dev, int64_t v_stride, int64_t n_past,
                      const int32_t* parent_dev, int t, int h, int h_kv, int d, float scale,
@@ -158,6 +158,70 @@ cpv_status  cpv_spec_accept(cpv_ctx* ctx, const float* p_logits_dev, const float
                             const cpv_sampler_params* params, int mode, const float* u_dev,
                             uint64_t philox_seed, const float* noise_dev, const int32_t* hist_dev,
                             int hist_len, int32_t* out_tok_dev, int32_t* out_n_dev);
+
+/* ---- model and verify round ------------------------------------------------- */
+typedef struct cpv_model cpv_model;
+typedef struct cpv_session cpv_session;
+
+/* Hparams of an all-attention qwen35 model (qwen35.rs:45-148 with
+ * full_attention_interval = 1): n_layer trunk layers, plus the MTP layer
+ * blk.{n_layer} when has_mtp. */
+typedef struct {
+    int32_t n_layer;
+    int32_t n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab;
+    int32_t n_rot;               /* rotary dims of head_dim */
+    int32_t rope_sections[4];    /* IMROPE sections; text positions use streams (p, p, p, 0) */
+    float   rms_eps, freq_base;
+    int32_t has_mtp;
+} cpv_hparams;
+
+/* Weights::load (crates/codpiece-model/src/lib.rs:128-311): create a model,
+ * hand it every tensor by its GGUF name (ggml ne order: ne0 = row length,
+ * ne1 = rows; host or device bytes), then check it with cpv_model_ready.
+ * Linear weights: Q8_0 / Q4_K / Q6_K; norms: F32. */
+cpv_status  cpv_model_create(cpv_ctx* ctx, const cpv_hparams* hp, cpv_model** out);
+cpv_status  cpv_model_set_tensor(cpv_model* m, const char* name, int type, const void* data, int on_device,
+                                 int64_t ne0, int64_t ne1);
+cpv_status  cpv_model_ready(cpv_model* m);
+void        cpv_model_free(cpv_model* m);
+
+/* Session::new_spec (qwen35.rs:528-649): f16 K caches [n_ctx][h_kv*d] and
+ * transposed V caches per layer, plus the MTP cache (min(n_ctx, 16384)
+ * rows); max_batch bounds t of every call. */
+cpv_status  cpv_session_create(cpv_model* m, int64_t n_ctx, int32_t max_batch, cpv_session** out);
+void        cpv_session_free(cpv_session* s);
+/* n_past / mtp_past, the round bookkeeping of engine.rs:2533-2540: a caller
+ * rewinds a rejected tail with set_pos(n_past - over, mtp_past + n_keep + 1). */
+cpv_status  cpv_session_set_pos(cpv_session* s, int64_t n_past, int64_t mtp_past);
+cpv_status  cpv_session_get_pos(const cpv_session* s, int64_t* n_past, int64_t* mtp_past);
+/* No counterpart in the reference: a debugging tap.  While set, every
+ * attention call of cpv_prefill / cpv_verify_step also copies its output
+ * ([t][n_head][head_dim] f32, before the output gate) to tap_dev, blocks
+ * back to back in call order (trunk layers, then each MTP link), restarting
+ * at offset 0 with each call; blocks past capacity_floats are dropped.
+ * NULL clears it. */
+cpv_status  cpv_session_set_attn_tap(cpv_session* s, float* tap_dev, int64_t capacity_floats);
+
+/* Trunk only over t prompt tokens (step_greedy's bulk prefill, main.rs:776-781):
+ * writes the KV cache and advances n_past by t. */
+cpv_status  cpv_prefill(cpv_session* s, const int32_t* tokens_dev, int t);
+
+/* FusedOut (qwen35.rs:817-828).  Device pointers owned by the session, valid
+ * until its next call. */
+typedef struct {
+    int64_t  n_past;        /* after the round (advanced by t, as the reference) */
+    int32_t* preds_dev;     /* [t] argmax of each verified row (of logits + noise) */
+    int32_t* chain_dev;     /* [depth][t] draft ids, link-major */
+    float*   conf_dev;      /* [depth][t] softmax peak of each link */
+    float*   logits_dev;    /* [t][n_vocab] trunk logits */
+    float*   hidden_dev;    /* [t][n_embd] normed trunk hidden */
+} cpv_round_out;
+
+/* Qwen35::step_fused_cached (qwen35.rs:1693-1948) for t tokens with a draft
+ * chain of `depth` links (0 = verify only): trunk, LM head, argmax (of
+ * logits + noise_dev when noise is given, the gumbel branch), MTP chain. */
+cpv_status  cpv_verify_step(cpv_session* s, const int32_t* tokens_dev, int t, int depth,
+                            const float* noise_dev, cpv_round_out* out);
 
 #ifdef __cplusplus
 }

@@ -164,6 +164,42 @@ int      cpvo_spec_accept_rng(const float* p_logits, const int32_t* draft, int k
                               const int32_t* hist, int n_hist,
                               int32_t* out_tok, float* u_used);
 
+/* ---- model restatement (crates/codpiece-model/src/qwen35.rs) ------------ */
+typedef struct {
+    int32_t n_layer;
+    int32_t n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab;
+    int32_t n_rot;
+    int32_t rope_sections[4];
+    float   rms_eps, freq_base;
+    int32_t has_mtp;
+} cpvo_hparams;
+typedef struct cpvo_model cpvo_model;
+typedef struct cpvo_session cpvo_session;
+cpvo_model*   cpvo_model_create(const cpvo_hparams* hp);
+void          cpvo_model_free(cpvo_model* m);
+/* tensors by GGUF name, ggml ne order (ne0 = row length, ne1 = rows) */
+int           cpvo_model_set(cpvo_model* m, const char* name, int type, const void* data, int64_t ne0, int64_t ne1);
+cpvo_session* cpvo_session_create(cpvo_model* m, int64_t n_ctx);
+void          cpvo_session_free(cpvo_session* s);
+void          cpvo_session_set_pos(cpvo_session* s, int64_t n_past, int64_t mtp_past);
+/* Inject the attention outputs of another implementation (consecutive
+ * [T][H][head_dim] f32 blocks, one per attention call, in call order): each
+ * block() checks its own attention against the injected block and continues
+ * with the injected values, so every op outside attention can be compared
+ * exactly.  NULL turns it off.  inject_ratio = max |inj - ref| / (2e-5 +
+ * 2e-4|ref|) seen since the last set (inf when the blocks ran out). */
+void          cpvo_session_set_attn_inject(cpvo_session* s, const float* att, int64_t n_floats);
+double        cpvo_session_inject_ratio(const cpvo_session* s);
+void          cpvo_session_get_pos(const cpvo_session* s, int64_t* n_past, int64_t* mtp_past);
+int           cpvo_prefill(cpvo_session* s, const int32_t* tok, int t);
+/* step_fused_cached: preds [t], chain [depth][t], conf [depth][t] (nullable),
+ * logits [t][V] and hidden [t][E] (nullable); noise [t][V] or NULL */
+int           cpvo_verify_step(cpvo_session* s, const int32_t* tok, int t, int depth, const float* noise,
+                               int32_t* preds, int32_t* chain, float* conf, float* logits, float* hidden);
+/* cmd_fused: returns the number of committed tokens; stats = {accepted, proposed, rounds} */
+int           cpvo_fused_generate(cpvo_session* s, const int32_t* prompt, int n_prompt, int n_gen, int depth,
+                                  int tail, int bulk, int32_t* committed, int64_t* stats);
+
 #ifdef __cplusplus
 }
 #endif

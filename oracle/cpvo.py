@@ -93,6 +93,19 @@ def lib():
                                                 P, ctypes.c_int, P, P, P, ctypes.c_int, P, P]),
             "cpvo_spec_accept_rng": (ctypes.c_int, [P, P, ctypes.c_int, ctypes.c_int, P, P, P,
                                                     ctypes.c_int, P, P]),
+            "cpvo_model_create": (P, [P]),
+            "cpvo_model_free": (None, [P]),
+            "cpvo_model_set": (ctypes.c_int, [P, ctypes.c_char_p, ctypes.c_int, P, i64, i64]),
+            "cpvo_session_create": (P, [P, i64]),
+            "cpvo_session_free": (None, [P]),
+            "cpvo_session_set_pos": (None, [P, i64, i64]),
+            "cpvo_session_get_pos": (None, [P, P, P]),
+            "cpvo_session_set_attn_inject": (None, [P, P, i64]),
+            "cpvo_session_inject_ratio": (ctypes.c_double, [P]),
+            "cpvo_prefill": (ctypes.c_int, [P, P, ctypes.c_int]),
+            "cpvo_verify_step": (ctypes.c_int, [P, P, ctypes.c_int, ctypes.c_int, P, P, P, P, P, P]),
+            "cpvo_fused_generate": (ctypes.c_int, [P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                   ctypes.c_int, ctypes.c_int, P, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -362,3 +375,90 @@ def spec_accept_rng(p_logits, draft, params, rng, hist=None):
     n = lib().cpvo_spec_accept_rng(_p(p_logits), _p(draft), k, V, ctypes.byref(params),
                                    _p(rng.s), _p(h), 0 if h is None else h.size, _p(tok), _p(used))
     return tok, n, used
+
+
+class Hparams(ctypes.Structure):
+    _fields_ = [
+        ("n_layer", ctypes.c_int32), ("n_embd", ctypes.c_int32), ("n_head", ctypes.c_int32),
+        ("n_head_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("n_ff", ctypes.c_int32),
+        ("n_vocab", ctypes.c_int32), ("n_rot", ctypes.c_int32), ("rope_sections", ctypes.c_int32 * 4),
+        ("rms_eps", ctypes.c_float), ("freq_base", ctypes.c_float), ("has_mtp", ctypes.c_int32),
+    ]
+
+
+class Model:
+    """The oracle's restatement of the qwen35 verify round (cpvo_model.c)."""
+
+    def __init__(self, hp_fields):
+        self.hp = Hparams()
+        for k, v in hp_fields.items():
+            if k == "rope_sections":
+                for i, x in enumerate(v):
+                    self.hp.rope_sections[i] = x
+            else:
+                setattr(self.hp, k, v)
+        self.h = lib().cpvo_model_create(ctypes.byref(self.hp))
+
+    def set_tensor(self, name, qtype, data, ne0, ne1):
+        data = np.ascontiguousarray(data)
+        assert lib().cpvo_model_set(self.h, name.encode(), qtype, _p(data), ne0, ne1) == 0, name
+
+    def free(self):
+        if self.h:
+            lib().cpvo_model_free(self.h)
+            self.h = None
+
+
+class Session:
+    def __init__(self, model, n_ctx):
+        self.model = model
+        self.h = lib().cpvo_session_create(model.h, n_ctx)
+
+    @property
+    def pos(self):
+        a, b = np.zeros(1, np.int64), np.zeros(1, np.int64)
+        lib().cpvo_session_get_pos(self.h, _p(a), _p(b))
+        return int(a[0]), int(b[0])
+
+    def set_pos(self, n_past, mtp_past):
+        lib().cpvo_session_set_pos(self.h, n_past, mtp_past)
+
+    def inject_attention(self, att):
+        """Continue the next call with these attention outputs (float32 blocks
+        in call order, or None); returns nothing, see inject_ratio."""
+        self._inj = None if att is None else np.ascontiguousarray(att, dtype=np.float32).ravel()
+        lib().cpvo_session_set_attn_inject(self.h, _p(self._inj), 0 if att is None else self._inj.size)
+
+    @property
+    def inject_ratio(self):
+        return lib().cpvo_session_inject_ratio(self.h)
+
+    def prefill(self, tokens):
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        assert lib().cpvo_prefill(self.h, _p(t), t.size) == 0
+
+    def step_fused_cached(self, tokens, depth, want_logits=False, noise=None):
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        T, V, E = t.size, self.model.hp.n_vocab, self.model.hp.n_embd
+        preds = np.empty(T, np.int32)
+        chain = np.empty((max(depth, 1), T), np.int32)
+        conf = np.empty((max(depth, 1), T), np.float32)
+        logits = np.empty((T, V), np.float32) if want_logits else None
+        hidden = np.empty((T, E), np.float32) if want_logits else None
+        nz = None if noise is None else np.ascontiguousarray(noise, dtype=np.float32)
+        assert lib().cpvo_verify_step(self.h, _p(t), T, depth, _p(nz), _p(preds), _p(chain), _p(conf),
+                                      _p(logits), _p(hidden)) == 0
+        return preds, chain[:depth], conf[:depth], logits, hidden
+
+    def fused_generate(self, prompt, n_gen, depth, tail=64, bulk=512):
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.empty(n_gen, np.int32)
+        stats = np.zeros(3, np.int64)
+        n = lib().cpvo_fused_generate(self.h, _p(p), p.size, n_gen, depth, tail, bulk, _p(out), _p(stats))
+        assert n >= 0
+        return out[:n].tolist(), stats.tolist()
+
+    def free(self):
+        if self.h:
+            lib().cpvo_session_free(self.h)
+            self.h = None

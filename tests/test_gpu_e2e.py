@@ -1,0 +1,190 @@
+"""End-to-end parity of the verify round on the config-1 model (device vs oracle).
+
+Two bars.  (1) Lockstep: each device call runs with its attention tap on and
+the oracle continues from the device's attention outputs, after checking them
+against its own f64 attention (|dev - ref| <= 2e-5 + 2e-4|ref|); everything
+else -- embeddings, norms, rope, the exact-window GEMMs, gates, SwiGLU, the LM
+head, argmax, the MTP chain, the KV writes and the round bookkeeping -- must
+then agree bit for bit (logits, hidden, preds, chain), the peak confidence to
+1e-6.  (2) Free-running: without injection the device's attention differs from the
+oracle's by ~1e-6 relative, and the Q8 activation rounding that follows
+(a discontinuous function) turns that into 1e-2-level logit differences and
+diverging greedy streams after a few tokens; these tests are expected to fail
+until attention is made order-free and exact on both sides.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import cpvo
+
+import model_fixtures as mf
+
+pytestmark = pytest.mark.gpu
+
+V = mf.TINY["n_vocab"]
+
+
+@pytest.fixture(scope="module")
+def models():
+    from codpiece_amd.model import Model, make_hparams
+    from codpiece_amd.runtime import Context
+    ctx = Context(0)
+    hp = make_hparams(**mf.TINY)
+    tensors = mf.make_tensors(mf.TINY, seed=0)
+    gm = Model(ctx, hp)
+    mf.load_into(gm, tensors)
+    gm.ready()
+    om = cpvo.Model(mf.TINY)
+    mf.load_into(om, tensors)
+    yield ctx, gm, om
+    gm.free()
+    om.free()
+    ctx.close()
+
+
+def sessions(models, n_ctx=512):
+    from codpiece_amd.model import Session
+    ctx, gm, om = models
+    return Session(gm, n_ctx), cpvo.Session(om, n_ctx)
+
+
+def paired(models, n_ctx=512, max_t=160, depth=4):
+    g, o = sessions(models, n_ctx)
+    hp = mf.TINY
+    n = (hp["n_layer"] + depth) * max_t * hp["n_head"] * hp["head_dim"]
+    return mf.PairedSession(g, o, n), g, o
+
+
+def test_lockstep_single_round(models):
+    ps, g, o = paired(models)
+    rng = np.random.default_rng(11)
+    prompt = rng.integers(0, V, size=70).tolist()
+    print("lockstep: prefill 64 + round of 6 at depth 4", flush=True)
+    ps.prefill(prompt[:64])
+    ps.step_fused_cached(prompt[64:], 4)
+    assert ps.pos == (70, 0)
+    print("worst attention ratio", ps.worst, flush=True)
+    g.free()
+    o.free()
+
+
+def test_lockstep_fused_loop_config1(models):
+    # config 1: 128 random prompt ids, greedy fused speculation at depth 4, 64 new tokens,
+    # driven by the host loop; the paired session checks every call
+    from codpiece_amd.model import fused_generate
+    ps, g, o = paired(models)
+    rng = np.random.default_rng(1)
+    prompt = rng.integers(0, V, size=128).tolist()
+    print("lockstep fused generate 64 at depth 4", flush=True)
+    toks, st = fused_generate(ps, prompt, 64, 4)
+    assert len(toks) == 64 and st.rounds > 0
+    print("rounds", st.rounds, "accepted", st.accepted, "worst ratio", ps.worst, flush=True)
+    g.free()
+    o.free()
+
+
+def test_lockstep_all_drafts_accepted(models):
+    # drafts = the trunk's own greedy continuation, so every draft is kept:
+    # the multi-accept path that random MTP drafts never reach
+    from codpiece_amd.model import fused_generate  # noqa: F401  (same loop rules below)
+    ps, g, o = paired(models)
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(0, V, size=40).tolist()
+    ps.prefill(prompt[:-1])
+    n0 = ps.pos[0]
+    cont = [prompt[-1]]
+    for _ in range(5):
+        out = ps.step_fused_cached(cont[-1:], 0)
+        cont.append(out.preds[0])
+    ps.set_pos(n0, 0)
+    out = ps.step_fused_cached(cont[:5], 4)
+    assert out.preds[:4] == cont[1:5]
+    assert out.preds[4] == cont[5]
+    g.free()
+    o.free()
+
+
+def test_lockstep_gumbel_noise(models):
+    # stochastic argmax: logits + per-token noise, same noise on both sides
+    ps, g, o = paired(models)
+    rng = np.random.default_rng(8)
+    prompt = rng.integers(0, V, size=30).tolist()
+    ps.prefill(prompt[:25])
+    u = rng.random(size=(5, V)).astype(np.float32)
+    noise = torch.from_numpy(-np.log(-np.log(np.maximum(u, 1e-12))).astype(np.float32)).cuda()
+    ps.step_fused_cached(prompt[25:], 2, noise=noise)
+    g.free()
+    o.free()
+
+
+FREE_RUNNING = pytest.mark.xfail(reason="attention is within tolerance, not bit-exact; Q8 activation "
+                                        "rounding amplifies the difference", strict=False)
+
+
+@FREE_RUNNING
+def test_free_running_round_within_tolerance(models):
+    g, o = sessions(models)
+    rng = np.random.default_rng(11)
+    prompt = rng.integers(0, V, size=70).tolist()
+    g.prefill(prompt[:64])
+    o.prefill(prompt[:64])
+    a = g.step_fused_cached(prompt[64:], 4, want_logits=True)
+    p, chain, conf, logits, hidden = o.step_fused_cached(prompt[64:], 4, want_logits=True)
+    err = np.abs(a.logits.cpu().numpy() - logits).max() / np.abs(logits).max()
+    print("free-running max logit error (relative to max |logit|)", err, flush=True)
+    assert err <= 1e-3
+    g.free()
+    o.free()
+
+
+@FREE_RUNNING
+def test_free_running_fused_loop_streams(models):
+    from codpiece_amd.model import fused_generate
+    g, o = sessions(models)
+    rng = np.random.default_rng(1)
+    prompt = rng.integers(0, V, size=128).tolist()
+    toks, st = fused_generate(g, prompt, 64, 4)
+    otoks, ost = o.fused_generate(prompt, 64, 4)
+    same = next((i for i, (x, y) in enumerate(zip(toks, otoks)) if x != y), len(toks))
+    print("free-running streams agree on the first", same, "of", len(toks), "tokens", flush=True)
+    assert toks == otoks
+    assert [st.accepted, st.proposed, st.rounds] == ost
+    g.free()
+    o.free()
+
+
+def test_rewind_then_redo_is_deterministic(models):
+    g, _ = sessions(models)
+    rng = np.random.default_rng(7)
+    prompt = rng.integers(0, V, size=20).tolist()
+    g.prefill(prompt[:15])
+    a = g.step_fused_cached(prompt[15:], 4, want_logits=True)
+    la = a.logits.cpu()
+    g.set_pos(15, 0)
+    b = g.step_fused_cached(prompt[15:], 4, want_logits=True)
+    assert a.preds == b.preds and a.chain == b.chain
+    assert torch.equal(la, b.logits.cpu())
+    g.free()
+
+
+def test_context_overflow_is_an_error(models):
+    from codpiece_amd import CpvError
+    g, _ = sessions(models, n_ctx=16)
+    g.prefill(list(range(12)))
+    with pytest.raises(CpvError):
+        g.step_fused_cached([1, 2, 3, 4, 5], 4)
+    g.free()
+
+
+def test_lockstep_mtp_window_restart(models):
+    # mtp_past + t > min(n_ctx, 16384): the draft head's window restarts at row 0
+    ps, g, o = paired(models)
+    rng = np.random.default_rng(12)
+    prompt = rng.integers(0, V, size=25).tolist()
+    ps.prefill(prompt[:20])
+    ps.set_pos(20, 509)
+    ps.step_fused_cached(prompt[20:], 3)
+    assert ps.pos == (25, 0)
+    g.free()
+    o.free()
