@@ -1,0 +1,339 @@
+#!/usr/bin/env python3
+"""Verify-step latency and accepted tokens/s: 27B-class Q4_K model, draft k=4, one MI355X.
+
+Workload: the end-to-end 27B-class configuration -- 64 layers, d_model 5120,
+40 Q / 8 KV heads x 128, SwiGLU FFN 17408, vocab 151,936, qwen35 layout (attn_q
+packs Q and the per-head output gate, q/k norms), every linear weight Q4_K,
+token embedding and output head Q6_K, norms 1, one MTP (nextn) layer; random
+weights generated on the device (no checkpoint); a 4096-token uniform random
+prompt; context 32768; greedy speculative decoding with k=4 drafts from the
+4-link MTP chain.
+
+A step is one round of the fused loop (crates/codpiece-cli/src/main.rs:
+803-913): [last] + 4 drafts through the trunk, the LM head argmax, the MTP
+chain, greedy acceptance and the KV rewind.  `value` is committed tokens per
+second over the timed rounds (host loop included); `ms_per_step` the wall
+time of a round.  With random weights the drafts are almost never accepted,
+so a round commits ~1 token, as the reference would on the same weights.
+
+Beside the line's required fields: `detail` holds the device time of a
+round and of a verify-only round (depth 0) from HIP events, and the per-class
+kernel timing that `roofline` is computed from: extra rounds run with
+cpv_profile_start/stop, which records every GEMM and attention launch, and
+cpv_profile_replay launches each class's recorded launches again back to back
+between one pair of HIP events on the library's stream (per-launch events
+would add the dispatch gaps); `roofline.achieved` = the dominant class's mean
+algorithmic bytes per launch / its mean replayed launch time.  `cpu_baseline`
+times the oracle (the C restatement under oracle/, all host cores given)
+on one layer sample scaled to a round -- a reported baseline, not the target.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+HP = dict(n_layer=64, n_embd=5120, n_head=40, n_head_kv=8, head_dim=128, n_ff=17408, n_vocab=151936,
+          n_rot=128, rope_sections=(22, 22, 20, 0), rms_eps=1e-6, freq_base=1e6, has_mtp=True)
+HBM_PEAK_GBS = 8000.0
+Q4_K, Q6_K, F32 = 12, 14, 0
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=16, help="timed rounds")
+    ap.add_argument("--warmup", type=int, default=3, help="untimed rounds before the timed ones")
+    ap.add_argument("--layers", type=int, default=HP["n_layer"], help="trunk layers (64 = the workload)")
+    ap.add_argument("--prompt", type=int, default=4096)
+    ap.add_argument("--n-ctx", type=int, default=32768)
+    ap.add_argument("--depth", type=int, default=4, help="drafts per round (k)")
+    ap.add_argument("--profile-rounds", type=int, default=4)
+    ap.add_argument("--cpu-baseline", type=int, default=1, help="0 skips the oracle timing")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU sample budget (seconds)")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--calibrate-copy", type=int, default=0,
+                    help="first copy 1 GiB on the device 3 times (a known-size kernel for HBM counters)")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------- synthetic weights
+def _fp16_bytes(torch, vals):
+    return vals.to(torch.float16).view(torch.uint8).view(-1, 2)
+
+
+def synth_quant(torch, qtype, n_rows, k, gen, device):
+    """Random ggml blocks with plausible scales: weights roughly N(0, 0.02)-sized."""
+    nb = n_rows * (k // 256)
+    if qtype == Q4_K:
+        raw = torch.randint(0, 256, (nb, 144), dtype=torch.uint8, device=device, generator=gen)
+        u = torch.rand(nb, device=device, generator=gen)
+        raw[:, 0:2] = _fp16_bytes(torch, 1.5e-4 + 1e-4 * u)          # d
+        raw[:, 2:4] = _fp16_bytes(torch, 1.2e-3 + 6e-4 * u)          # dmin (keeps the mean near 0)
+    else:
+        raw = torch.randint(0, 256, (nb, 210), dtype=torch.uint8, device=device, generator=gen)
+        u = torch.rand(nb, device=device, generator=gen)
+        raw[:, 208:210] = _fp16_bytes(torch, 1.2e-5 + 6e-6 * u)      # d (scales are int8)
+    return raw.view(-1)
+
+
+def tensor_specs(hp):
+    E, H, Hkv, hd, F, V = hp["n_embd"], hp["n_head"], hp["n_head_kv"], hp["head_dim"], hp["n_ff"], hp["n_vocab"]
+    specs = [("token_embd.weight", Q6_K, E, V), ("output.weight", Q6_K, E, V), ("output_norm.weight", F32, E, 1)]
+    for il in range(hp["n_layer"] + (1 if hp["has_mtp"] else 0)):
+        b = f"blk.{il}."
+        specs += [(b + "attn_norm.weight", F32, E, 1), (b + "post_attention_norm.weight", F32, E, 1),
+                  (b + "attn_q_norm.weight", F32, hd, 1), (b + "attn_k_norm.weight", F32, hd, 1),
+                  (b + "attn_q.weight", Q4_K, E, 2 * H * hd), (b + "attn_k.weight", Q4_K, E, Hkv * hd),
+                  (b + "attn_v.weight", Q4_K, E, Hkv * hd), (b + "attn_output.weight", Q4_K, H * hd, E),
+                  (b + "ffn_gate.weight", Q4_K, E, F), (b + "ffn_up.weight", Q4_K, E, F),
+                  (b + "ffn_down.weight", Q4_K, F, E)]
+    if hp["has_mtp"]:
+        b = f"blk.{hp['n_layer']}.nextn."
+        specs += [(b + "eh_proj.weight", Q4_K, 2 * E, E), (b + "enorm.weight", F32, E, 1),
+                  (b + "hnorm.weight", F32, E, 1)]
+    return specs
+
+
+def build_model(torch, ctx, hp, seed):
+    from codpiece_amd.model import Model, make_hparams
+    m = Model(ctx, make_hparams(**hp))
+    gen = torch.Generator(device=ctx.torch_device)
+    gen.manual_seed(seed)
+    nbytes = 0
+    for name, t, ne0, ne1 in tensor_specs(hp):
+        if t == F32:
+            data = torch.ones(ne0, dtype=torch.float32, device=ctx.torch_device)
+        else:
+            data = synth_quant(torch, t, ne1, ne0, gen, ctx.torch_device)
+            nbytes += data.numel()
+        m.set_tensor(name, t, data, ne0, ne1)
+        del data
+    m.ready()
+    return m, nbytes
+
+
+# ---------------------------------------------------------------- the fused loop
+class Loop:
+    """The fused loop's state (main.rs:803-913): last committed token and drafts."""
+
+    def __init__(self, session, depth):
+        self.s, self.depth = session, depth
+        self.committed = 0
+        self.accepted = self.proposed = self.rounds = 0
+
+    def start(self, prompt, tail=64, bulk=64):
+        split = max(0, len(prompt) - tail)
+        for c in range(0, split, bulk):
+            self.s.prefill(prompt[c:min(split, c + bulk)])
+        out = self.s.step_fused_cached(prompt[split:], self.depth)
+        n_past, mtp_past = self.s.pos
+        self.s.set_pos(n_past, mtp_past + len(out.preds))
+        last = len(out.preds) - 1
+        self.last = out.preds[last]
+        self.drafts = [out.chain[l][last] for l in range(self.depth)]
+
+    def round(self):
+        batch = [self.last] + self.drafts
+        out = self.s.step_fused_cached(batch, self.depth)
+        keep = 0
+        while keep < len(self.drafts) and out.preds[keep] == self.drafts[keep]:
+            keep += 1
+        self.rounds += 1
+        self.proposed += len(self.drafts)
+        self.accepted += keep
+        self.committed += keep + 1
+        self.last = out.preds[keep]
+        self.drafts = [out.chain[l][keep] for l in range(self.depth)]
+        over = len(batch) - (keep + 1)
+        n_past, mtp_past = self.s.pos
+        self.s.set_pos(n_past - over, mtp_past + keep + 1)
+
+
+# ---------------------------------------------------------------- CPU baseline
+def cpu_baseline(hp, layers, budget_s, tokens_per_round, depth, seed):
+    """Time the oracle on one layer's GEMMs + attention at the round's shapes
+    and the Q6_K head, then scale to a full round (trunk layers + head +
+    `depth` MTP links of layer + eh_proj + head)."""
+    import numpy as np
+    from oracle import cpvo
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    rng = np.random.default_rng(seed)
+    E, H, Hkv, hd, F, V = hp["n_embd"], hp["n_head"], hp["n_head_kv"], hp["head_dim"], hp["n_ff"], hp["n_vocab"]
+    T = depth + 1
+
+    def w(t, n, k):
+        raw = rng.integers(0, 256, size=n * cpvo.row_bytes(t, k), dtype=np.uint8)
+        if t == Q4_K:
+            b = raw.reshape(-1, 144)
+            b[:, 0:2] = np.frombuffer(np.float16(2e-4).tobytes(), np.uint8)
+            b[:, 2:4] = np.frombuffer(np.float16(1.5e-3).tobytes(), np.uint8)
+        else:
+            b = raw.reshape(-1, 210)
+            b[:, 208:210] = np.frombuffer(np.float16(1.5e-5).tobytes(), np.uint8)
+        return raw
+
+    layer_w = [(w(Q4_K, n, k), k) for n, k in ((2 * H * hd, E), (Hkv * hd, E), (Hkv * hd, E), (E, H * hd),
+                                                (F, E), (F, E), (E, F))]
+    head = w(Q6_K, V, E)
+    eh = w(Q4_K, E, 2 * E)
+    n_past = 4096
+    kc = cpvo.f32_to_f16_bits(rng.normal(size=(n_past + T, Hkv * hd)).astype(np.float32))
+    q = rng.normal(size=(T, H, hd)).astype(np.float32)
+
+    def x(k):
+        return rng.normal(size=(T, k)).astype(np.float32)
+
+    def layer():
+        for wb, k in layer_w:
+            cpvo.qgemm(Q4_K, wb, x(k), cores)
+        cpvo.attn(q, kc, kc, n_past, None, np.float32(1 / np.sqrt(hd)))
+
+    def timed(fn, budget):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return el / reps, reps
+
+    t_layer, r_layer = timed(layer, budget_s * 0.7)
+    t_head, r_head = timed(lambda: cpvo.qgemm(Q6_K, head, x(E), cores), budget_s * 0.25)
+    t_eh, _ = timed(lambda: cpvo.qgemm(Q4_K, eh, x(2 * E), cores), budget_s * 0.05)
+    round_s = layers * t_layer + t_head + depth * (t_layer + t_eh + t_head)
+    return {
+        "value": tokens_per_round / round_s, "unit": "tok/s", "cores": cores, "kind": "port",
+        "sample": (f"oracle (exact-window GEMMs, f64 attention) on one trunk layer at t={T}, n_past={n_past} "
+                   f"({r_layer} reps, {t_layer * 1e3:.1f} ms), the Q6_K head ({r_head} reps, {t_head * 1e3:.1f} ms) "
+                   f"and eh_proj, scaled to a round of {layers} layers + head + {depth} MTP links "
+                   f"= {round_s:.2f} s, at the GPU run's {tokens_per_round:.3f} committed tokens per round"),
+    }
+
+
+# ---------------------------------------------------------------- main
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X: the verify step runs on a single GPU (the 27B-class "
+              f"model is resident in one GPU's HBM); --gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from codpiece_amd.model import Session
+    from codpiece_amd.runtime import Context
+
+    hp = dict(HP, n_layer=args.layers)
+    torch.cuda.set_device(0)
+    ctx = Context(0)
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=ctx.torch_device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    t0 = time.perf_counter()
+    model, wbytes = build_model(torch, ctx, hp, args.seed)
+    torch.cuda.synchronize()
+    print(f"[bench] model built: {wbytes / 1e9:.2f} GB quantized weights in {time.perf_counter() - t0:.1f} s",
+          file=sys.stderr, flush=True)
+    sess = Session(model, args.n_ctx, max_batch=64)
+    g = torch.Generator().manual_seed(args.seed + 1)
+    prompt = torch.randint(0, hp["n_vocab"], (args.prompt,), generator=g).tolist()
+    loop = Loop(sess, args.depth)
+    t0 = time.perf_counter()
+    loop.start(prompt)
+    torch.cuda.synchronize()
+    print(f"[bench] prefill of {args.prompt} tokens: {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+
+    for _ in range(args.warmup):
+        loop.round()
+    # timed rounds: device time of each round by events on the library's stream
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    c0 = loop.committed
+    acc0, prop0 = loop.accepted, loop.proposed
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        evs[i][0].record(stream)
+        loop.round()
+        evs[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    committed = loop.committed - c0
+    dev_ms = sorted(a.elapsed_time(b) for a, b in evs)
+    print(f"[bench] {args.steps} rounds in {wall:.3f} s, {committed} tokens", file=sys.stderr, flush=True)
+
+    # verify-only rounds (depth 0), rewound afterwards
+    n_past, mtp_past = sess.pos
+    vo = []
+    for _ in range(max(3, args.steps // 4)):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        sess.step_fused_cached([loop.last] + loop.drafts, 0)
+        b.record(stream)
+        torch.cuda.synchronize()
+        vo.append(a.elapsed_time(b))
+        sess.set_pos(n_past, mtp_past)
+    vo.sort()
+
+    # per-class kernel timing over extra rounds (events between launches: not in the timed region)
+    ctx.profile_start()
+    for _ in range(args.profile_rounds):
+        loop.round()
+    prof = ctx.profile_stop()
+    dom = max(prof, key=lambda k: prof[k][1])
+    # the recorded launches of each class, replayed back to back between one event pair
+    replay = {k: ctx.profile_replay(k, reps=3) for k, v in prof.items() if v[0]}
+    rep_ms, rep_bytes = replay[dom]
+    achieved = rep_bytes / (rep_ms * 1e-3) / 1e9
+
+    traffic = None
+    tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get(dom)
+
+    cpu = None
+    if args.cpu_baseline:
+        cpu = cpu_baseline(hp, args.layers, args.cpu_seconds, committed / args.steps, args.depth, args.seed)
+
+    value = committed / wall
+    line = {
+        "metric": "verify-step µs + accepted tok/s, 27B-class Q4_K, draft k=4, 1 MI355X",
+        "value": round(value, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic (random-init weights and prompt)",
+        "config": {"workload": (f"27B-class qwen35-layout random-init model: {hp['n_layer']} layers, d_model 5120, "
+                                f"40/8 heads x 128, FFN 17408, vocab 151936, Q4_K linears, Q6_K embedding/output, "
+                                f"1 MTP layer; {args.prompt}-token random prompt, context {args.n_ctx}; "
+                                f"greedy speculative decode, k={args.depth}"),
+                   "k": args.depth, "context": args.n_ctx, "prompt": args.prompt},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+        "detail": {
+            "round_device_us_median": round(dev_ms[len(dev_ms) // 2] * 1e3, 1),
+            "verify_only_device_us_median": round(vo[len(vo) // 2] * 1e3, 1),
+            "acceptance": round((loop.accepted - acc0) / max(1, loop.proposed - prop0), 4),
+            "tokens_per_round": round(committed / args.steps, 3),
+            "kernel_classes": {k: {"launches_per_round": v[0] / args.profile_rounds,
+                                   "GB_per_launch": round(v[2] / v[0] / 1e9, 5),
+                                   "us_per_launch_replayed": round(replay[k][0] * 1e3, 2),
+                                   "GB_s_replayed": round(replay[k][1] / (replay[k][0] * 1e-3) / 1e9, 1),
+                                   "us_per_launch_event_bracketed": round(v[1] / v[0] * 1e3, 2)}
+                               for k, v in prof.items() if v[0]},
+            "profiled_rounds": args.profile_rounds,
+        },
+    }
+    print(json.dumps(line), flush=True)
+    sess.free()
+    model.free()
+    ctx.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

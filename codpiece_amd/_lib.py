@@ -62,6 +62,14 @@ class RoundOut(ctypes.Structure):
     ]
 
 
+PROF_Q4_K, PROF_Q6_K, PROF_Q8_0, PROF_ATTN, PROF_CLASSES = 0, 1, 2, 3, 4
+PROF_NAMES = ("qgemm_q4_k", "qgemm_q6_k", "qgemm_q8_0", "attention")
+
+
+class ProfStat(ctypes.Structure):
+    _fields_ = [("launches", ctypes.c_int64), ("ms", ctypes.c_double), ("bytes", ctypes.c_double)]
+
+
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I32 = ctypes.c_int32
@@ -75,6 +83,9 @@ SIGNATURES = {
     "cpv_last_error": (ctypes.c_char_p, [_P]),
     "cpv_set_stream": (_INT, [_P, _P]),
     "cpv_get_stream": (_P, [_P]),
+    "cpv_profile_start": (_INT, [_P]),
+    "cpv_profile_stop": (_INT, [_P, _P]),
+    "cpv_profile_replay": (_INT, [_P, _INT, _INT, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
     "cpv_sync": (_INT, [_P]),
     "cpv_weight_upload": (_INT, [_P, _INT, _P, _I64, _I64, ctypes.POINTER(_P)]),
     "cpv_weight_from_device": (_INT, [_P, _INT, _P, _I64, _I64, ctypes.POINTER(_P)]),

@@ -92,6 +92,7 @@ extern "C" void cpv_free(cpv_ctx* ctx)
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
+    for (hipEvent_t e : ctx->prof_ev) (void)hipEventDestroy(e);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
 }
@@ -120,6 +121,97 @@ extern "C" cpv_status cpv_sync(cpv_ctx* ctx)
     return CPV_OK;
 }
 
+// ---------------------------------------------------------------- timing
+int cpv_prof_mark(cpv_ctx* ctx)
+{
+    if (!ctx->prof) return -1;
+    if (ctx->prof_used == ctx->prof_ev.size()) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) {
+            ctx->prof = false;               // out of events: stop timing, keep computing
+            return -1;
+        }
+        ctx->prof_ev.push_back(e);
+    }
+    if (hipEventRecord(ctx->prof_ev[ctx->prof_used], ctx->stream) != hipSuccess) return -1;
+    return (int)ctx->prof_used++;
+}
+
+void cpv_prof_add(cpv_ctx* ctx, int ev0, int cls, double bytes)
+{
+    const int ev1 = cpv_prof_mark(ctx);
+    if (ev0 >= 0 && ev1 >= 0) ctx->prof_recs.push_back({cls, ev0, ev1, bytes});
+}
+
+void cpv_prof_keep(cpv_ctx* ctx, int cls, double bytes, std::function<void()> go)
+{
+    ctx->prof_launches.push_back({cls, bytes, ctx->ws_gen, std::move(go)});
+}
+
+extern "C" cpv_status cpv_profile_start(cpv_ctx* ctx)
+{
+    if (!ctx) return CPV_EINVAL;
+    ctx->prof = true;
+    ctx->prof_used = 0;
+    ctx->prof_recs.clear();
+    ctx->prof_launches.clear();
+    return CPV_OK;
+}
+
+extern "C" cpv_status cpv_profile_replay(cpv_ctx* ctx, int cls, int reps, double* ms_per_launch,
+                                         double* bytes_per_launch)
+{
+    if (!ctx || cls < 0 || cls >= CPV_PROF_CLASSES || reps < 1 || !ms_per_launch)
+        return cpv_fail(ctx, CPV_EINVAL, "profile_replay: bad arguments");
+    if (ctx->prof) return cpv_fail(ctx, CPV_EINVAL, "profile_replay: stop the profile first");
+    std::vector<const cpv_ctx::prof_launch*> sel;
+    double bytes = 0.0;
+    for (const auto& l : ctx->prof_launches)
+        if (l.cls == cls) {
+            if (l.ws_gen != ctx->ws_gen)
+                return cpv_fail(ctx, CPV_EINVAL, "profile_replay: the workspace moved since the profile");
+            sel.push_back(&l);
+            bytes += l.bytes;
+        }
+    if (sel.empty()) return cpv_fail(ctx, CPV_EINVAL, "profile_replay: no launches of class %d recorded", cls);
+    hipEvent_t e0, e1;
+    CPV_HIP(ctx, hipEventCreate(&e0));
+    CPV_HIP(ctx, hipEventCreate(&e1));
+    CPV_HIP(ctx, hipEventRecord(e0, ctx->stream));
+    for (int r = 0; r < reps; r++)
+        for (const auto* l : sel) l->go();
+    CPV_HIP(ctx, hipEventRecord(e1, ctx->stream));
+    CPV_HIP(ctx, hipEventSynchronize(e1));
+    float ms = 0.0f;
+    CPV_HIP(ctx, hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    CPV_HIP(ctx, hipGetLastError());
+    *ms_per_launch = (double)ms / ((double)reps * (double)sel.size());
+    if (bytes_per_launch) *bytes_per_launch = bytes / (double)sel.size();
+    return CPV_OK;
+}
+
+extern "C" cpv_status cpv_profile_stop(cpv_ctx* ctx, cpv_prof_stat* out)
+{
+    if (!ctx || !out) return cpv_fail(ctx, CPV_EINVAL, "profile_stop: null argument");
+    const bool was = ctx->prof;
+    ctx->prof = false;
+    for (int c = 0; c < CPV_PROF_CLASSES; c++) out[c] = cpv_prof_stat{0, 0.0, 0.0};
+    if (!was) return cpv_fail(ctx, CPV_EINVAL, "profile_stop: no profile running");
+    CPV_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    for (const auto& r : ctx->prof_recs) {
+        float ms = 0.0f;
+        CPV_HIP(ctx, hipEventElapsedTime(&ms, ctx->prof_ev[r.ev0], ctx->prof_ev[r.ev1]));
+        out[r.cls].launches++;
+        out[r.cls].ms += ms;
+        out[r.cls].bytes += r.bytes;
+    }
+    ctx->prof_recs.clear();
+    ctx->prof_used = 0;
+    return CPV_OK;
+}
+
 cpv_status cpv_workspace(cpv_ctx* ctx, size_t bytes, void** out)
 {
     if (bytes <= ctx->ws_bytes) {
@@ -135,6 +227,7 @@ cpv_status cpv_workspace(cpv_ctx* ctx, size_t bytes, void** out)
     size_t sz = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
     CPV_HIP(ctx, hipMalloc(&ctx->ws, sz));
     ctx->ws_bytes = sz;
+    ctx->ws_gen++;
     *out = ctx->ws;
     return CPV_OK;
 }

@@ -308,8 +308,18 @@ cpv_status cpv_attn_launch(cpv_ctx* ctx, const float* q, const uint16_t* kc, con
 {
     const int R = (h / h_kv) * t;
     const int rt = ((R < MAX_ROWS ? R : MAX_ROWS) + 15) / 16;
-    if (d == 128) return launch_rt<128>(ctx, rt, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out);
-    return launch_rt<64>(ctx, rt, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out);
+    auto go = [=]() {
+        return d == 128 ? launch_rt<128>(ctx, rt, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out)
+                        : launch_rt<64>(ctx, rt, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out);
+    };
+    const int ev = cpv_prof_mark(ctx);
+    const cpv_status st = go();
+    if (st == CPV_OK && ev >= 0) {  // algorithmic bytes: K and V rows once, q in, out
+        const double bytes = 2.0 * 2.0 * (double)(n_past + t) * h_kv * d + 2.0 * 4.0 * t * h * d;
+        cpv_prof_add(ctx, ev, CPV_PROF_ATTN, bytes);
+        cpv_prof_keep(ctx, CPV_PROF_ATTN, bytes, [go]() { (void)go(); });
+    }
+    return st;
 }
 
 extern "C" cpv_status cpv_attn(cpv_ctx* ctx, const float* q_dev, const uint16_t* k_cache_dev,

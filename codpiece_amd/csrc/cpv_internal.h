@@ -3,7 +3,9 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <functional>
 #include <string>
+#include <vector>
 
 #include "../../include/cpv.h"
 
@@ -17,7 +19,25 @@ struct cpv_ctx {
     // scratch owned by the context, grown on demand (never inside a capture)
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    uint64_t ws_gen = 0;      // bumped whenever ws is reallocated
+    // kernel timing (cpv_profile_start / _stop): event pairs around launches,
+    // and each launch kept for cpv_profile_replay
+    struct prof_rec { int cls, ev0, ev1; double bytes; };
+    struct prof_launch { int cls; double bytes; uint64_t ws_gen; std::function<void()> go; };
+    bool prof = false;
+    std::vector<hipEvent_t> prof_ev;      // reused from one profile to the next
+    std::vector<prof_rec> prof_recs;
+    std::vector<prof_launch> prof_launches;
+    size_t prof_used = 0;
 };
+
+// kernel timing: cpv_prof_mark records an event on the context's stream and
+// returns its index (-1 when not profiling); cpv_prof_add closes a launch of
+// class `cls` that moved `bytes` algorithmic bytes, opened by mark `ev0`
+int  cpv_prof_mark(cpv_ctx* ctx);
+void cpv_prof_add(cpv_ctx* ctx, int ev0, int cls, double bytes);
+// keep a launch (its kernel and arguments) for cpv_profile_replay
+void cpv_prof_keep(cpv_ctx* ctx, int cls, double bytes, std::function<void()> go);
 
 struct cpv_weight {
     cpv_ctx* ctx = nullptr;

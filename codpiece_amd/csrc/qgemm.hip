@@ -304,25 +304,35 @@ __global__ __launch_bounds__(512) void qgemm_kernel(GemmArgs a)
     }
 }
 
+// one launch of the GEMM; k and wbytes (the weight's row length and bytes)
+// only feed the kernel timing
 template <int TYPE, int MT>
-cpv_status launch_mt(cpv_ctx* ctx, GemmArgs a, int W)
+cpv_status launch_mt(cpv_ctx* ctx, GemmArgs a, int W, int64_t k, double wbytes)
 {
     const size_t lds = gemm_lds_bytes<TYPE, MT>(a.U, W);
-    qgemm_kernel<TYPE, MT><<<(unsigned)(a.n_pad / 16), W * 64, lds, ctx->stream>>>(a);
+    auto go = [=]() { qgemm_kernel<TYPE, MT><<<(unsigned)(a.n_pad / 16), W * 64, lds, ctx->stream>>>(a); };
+    const int ev = cpv_prof_mark(ctx);
+    go();
     CPV_HIP(ctx, hipGetLastError());
+    if (ev >= 0) {  // algorithmic bytes: the weight, f32 activations in, f32 outputs
+        const int cls = TYPE == CPV_Q4_K ? CPV_PROF_Q4_K : TYPE == CPV_Q6_K ? CPV_PROF_Q6_K : CPV_PROF_Q8_0;
+        const double bytes = wbytes + 4.0 * a.M * (double)k + 4.0 * a.M * (double)a.N;
+        cpv_prof_add(ctx, ev, cls, bytes);
+        cpv_prof_keep(ctx, cls, bytes, go);
+    }
     return CPV_OK;
 }
 
 template <int TYPE>
-cpv_status launch_type(cpv_ctx* ctx, GemmArgs a, int W)
+cpv_status launch_type(cpv_ctx* ctx, GemmArgs a, int W, int64_t k, double wbytes)
 {
     // the register tile MT is the smallest instantiated size >= M
-    if (a.M <= 1) return launch_mt<TYPE, 1>(ctx, a, W);
-    if (a.M <= 2) return launch_mt<TYPE, 2>(ctx, a, W);
-    if (a.M <= 4) return launch_mt<TYPE, 4>(ctx, a, W);
-    if (a.M <= 5) return launch_mt<TYPE, 5>(ctx, a, W);
-    if (a.M <= 8) return launch_mt<TYPE, 8>(ctx, a, W);
-    return launch_mt<TYPE, 16>(ctx, a, W);
+    if (a.M <= 1) return launch_mt<TYPE, 1>(ctx, a, W, k, wbytes);
+    if (a.M <= 2) return launch_mt<TYPE, 2>(ctx, a, W, k, wbytes);
+    if (a.M <= 4) return launch_mt<TYPE, 4>(ctx, a, W, k, wbytes);
+    if (a.M <= 5) return launch_mt<TYPE, 5>(ctx, a, W, k, wbytes);
+    if (a.M <= 8) return launch_mt<TYPE, 8>(ctx, a, W, k, wbytes);
+    return launch_mt<TYPE, 16>(ctx, a, W, k, wbytes);
 }
 
 template <int TYPE>
@@ -419,9 +429,10 @@ cpv_status cpv_qgemm_act(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, 
     for (int64_t m0 = 0; m0 < m; m0 += chunk) {
         a.m0 = (int)m0;
         a.M = (int)((m - m0) < chunk ? (m - m0) : chunk);
-        cpv_status s2 = w->type == CPV_Q4_K ? launch_type<CPV_Q4_K>(ctx, a, W)
-                      : w->type == CPV_Q6_K ? launch_type<CPV_Q6_K>(ctx, a, W)
-                                            : launch_type<CPV_Q8_0>(ctx, a, W);
+        const double wb = (double)w->n * (double)(w->k / cpv_type_block(w->type)) * (double)cpv_type_size(w->type);
+        cpv_status s2 = w->type == CPV_Q4_K ? launch_type<CPV_Q4_K>(ctx, a, W, w->k, wb)
+                      : w->type == CPV_Q6_K ? launch_type<CPV_Q6_K>(ctx, a, W, w->k, wb)
+                                            : launch_type<CPV_Q8_0>(ctx, a, W, w->k, wb);
         if (s2 != CPV_OK) return s2;
     }
     return CPV_OK;

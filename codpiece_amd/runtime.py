@@ -44,6 +44,24 @@ class Context:
     def sync(self):
         self._check(self.lib.cpv_sync(self.h))
 
+    def profile_start(self):
+        """Time every GEMM / attention launch with HIP events until profile_stop."""
+        self._check(self.lib.cpv_profile_start(self.h))
+
+    def profile_stop(self):
+        """{class name: (launches, ms, algorithmic bytes)} since profile_start."""
+        out = (_lib.ProfStat * _lib.PROF_CLASSES)()
+        self._check(self.lib.cpv_profile_stop(self.h, out))
+        return {name: (out[i].launches, out[i].ms, out[i].bytes) for i, name in enumerate(_lib.PROF_NAMES)}
+
+    def profile_replay(self, cls_name, reps=5):
+        """(ms per launch, algorithmic bytes per launch) of the class's recorded
+        launches replayed back to back."""
+        ms, b = ctypes.c_double(), ctypes.c_double()
+        self._check(self.lib.cpv_profile_replay(self.h, _lib.PROF_NAMES.index(cls_name), reps, ctypes.byref(ms),
+                                                ctypes.byref(b)))
+        return ms.value, b.value
+
     def close(self):
         if getattr(self, "h", None):
             self.lib.cpv_free(self.h)

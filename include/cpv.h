@@ -223,6 +223,27 @@ typedef struct {
 cpv_status  cpv_verify_step(cpv_session* s, const int32_t* tokens_dev, int t, int depth,
                             const float* noise_dev, cpv_round_out* out);
 
+/* ---- kernel timing -------------------------------------------------------
+ * No counterpart in the reference (which times whole rounds with
+ * Instant::now, crates/codpiece-server/src/engine.rs:2295,2324).  Between
+ * start and stop, every GEMM and attention launch on the context is bracketed
+ * by a pair of HIP events on its stream; stop waits for the stream and sums,
+ * per kernel class, the launches, their event-timed milliseconds and their
+ * algorithmic bytes (GEMM: the quantized weight + 4*m*k + 4*m*n; attention:
+ * the K and V rows read once + q and the output in f32).  The events add
+ * a little time between launches: time throughput without them. */
+enum { CPV_PROF_Q4_K = 0, CPV_PROF_Q6_K = 1, CPV_PROF_Q8_0 = 2, CPV_PROF_ATTN = 3, CPV_PROF_CLASSES = 4 };
+typedef struct { int64_t launches; double ms; double bytes; } cpv_prof_stat;
+cpv_status  cpv_profile_start(cpv_ctx* ctx);
+cpv_status  cpv_profile_stop(cpv_ctx* ctx, cpv_prof_stat* out /* [CPV_PROF_CLASSES] */);
+/* Launch again, back to back, every launch of class `cls` the last profile
+ * recorded (same kernels, grids and arguments), `reps` times between one pair
+ * of events: *ms_per_launch = elapsed / (reps * launches), free of the gaps
+ * the per-launch events add; *bytes_per_launch (may be NULL) their mean
+ * algorithmic bytes.  The buffers of the recorded calls (weights, sessions)
+ * must still be allocated; their outputs are overwritten. */
+cpv_status  cpv_profile_replay(cpv_ctx* ctx, int cls, int reps, double* ms_per_launch, double* bytes_per_launch);
+
 #ifdef __cplusplus
 }
 #endif

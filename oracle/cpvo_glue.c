@@ -110,29 +110,47 @@ void cpvo_rope_neox(float* x, int n_rot, const float* cs)
  * kernel converts Q to f16 before the dot with the f16 cache; that rounding
  * is kept.  Everything after it is evaluated in binary64, which makes this
  * the closed-form reference the GPU kernel is held to within a tolerance. */
+static float f16_tab[65536];
+static int f16_tab_ready;
+
+static void f16_tab_init(void)
+{
+    if (f16_tab_ready) return;
+#pragma omp critical(cpvo_f16_tab)
+    if (!f16_tab_ready) {
+        for (int i = 0; i < 65536; i++) f16_tab[i] = cpvo_fp16_to_fp32((uint16_t)i);
+        f16_tab_ready = 1;
+    }
+}
+
 void cpvo_attn(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n_past,
                const int32_t* parent, int T, int H, int Hkv, int D, float scale, float* out)
 {
     const int g = H / Hkv;
     const int64_t row = (int64_t)Hkv * D;
     const int64_t nmax = n_past + T;
-    double* s = malloc(sizeof(double) * (size_t)nmax);
-    char* vis = malloc((size_t)T);
-    double* qd = malloc(sizeof(double) * (size_t)D);
-    double* o = malloc(sizeof(double) * (size_t)D);
-    for (int t = 0; t < T; t++) {
-        memset(vis, 0, (size_t)T);
-        for (int a = t; a >= 0; a = parent ? parent[a] : a - 1) vis[a] = 1;
-        for (int h = 0; h < H; h++) {
+    f16_tab_init();
+    /* each (t, h) row is independent: the result does not depend on the thread count */
+#pragma omp parallel
+    {
+        double* s = malloc(sizeof(double) * (size_t)nmax);
+        char* vis = malloc((size_t)T);
+        double* qd = malloc(sizeof(double) * (size_t)D);
+        double* o = malloc(sizeof(double) * (size_t)D);
+#pragma omp for schedule(dynamic)
+        for (int th = 0; th < T * H; th++) {
+            const int t = th / H, h = th % H;
+            memset(vis, 0, (size_t)T);
+            for (int a = t; a >= 0; a = parent ? parent[a] : a - 1) vis[a] = 1;
             const int kh = h / g;
             for (int d = 0; d < D; d++)
-                qd[d] = (double)cpvo_fp16_to_fp32(cpvo_fp32_to_fp16(q[((int64_t)t * H + h) * D + d]));
+                qd[d] = (double)f16_tab[cpvo_fp32_to_fp16(q[((int64_t)t * H + h) * D + d])];
             double mx = -INFINITY;
             for (int64_t r = 0; r < nmax; r++) {
                 if (r >= n_past && !vis[r - n_past]) { s[r] = -INFINITY; continue; }
                 const uint16_t* kr = kc + r * row + (int64_t)kh * D;
                 double acc = 0.0;
-                for (int d = 0; d < D; d++) acc += qd[d] * (double)cpvo_fp16_to_fp32(kr[d]);
+                for (int d = 0; d < D; d++) acc += qd[d] * (double)f16_tab[kr[d]];
                 s[r] = acc * (double)scale;
                 if (s[r] > mx) mx = s[r];
             }
@@ -143,10 +161,10 @@ void cpvo_attn(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n
                 const double p = exp(s[r] - mx);
                 z += p;
                 const uint16_t* vr = vc + r * row + (int64_t)kh * D;
-                for (int d = 0; d < D; d++) o[d] += p * (double)cpvo_fp16_to_fp32(vr[d]);
+                for (int d = 0; d < D; d++) o[d] += p * (double)f16_tab[vr[d]];
             }
             for (int d = 0; d < D; d++) out[((int64_t)t * H + h) * D + d] = (float)(o[d] / z);
         }
+        free(s); free(vis); free(qd); free(o);
     }
-    free(s); free(vis); free(qd); free(o);
 }
