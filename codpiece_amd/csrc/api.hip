@@ -1,16 +1,12 @@
 // api.hip — context, errors, weight upload/repack, get_rows, argmax.
 //
 // Weight repack.  ggml stores a quantized row as consecutive blocks (Q4_K 144 B,
-// Q6_K 210 B, Q8_0 34 B).  The GEMM kernel gives each lane of a wave one
-// 256-element unit of one of 16 rows (lane = row r + 16 * unit q) and walks the
-// row in passes of 4 units, so the repack orders the bytes the way one wave
-// instruction reads them: for each 16-row group and pass, piece-major, then
-// lane, 16 bytes per lane.  Every 128-bit load of the kernel is then a
-// contiguous 1 KiB read, whatever the block size, and rows / units are padded
-// with zero blocks (which contribute nothing) to whole groups and passes.
-//   Q4_K : [g][p][piece 0..7][lane] qs bytes 16*piece..  | [g][p][lane] d,dmin,scales
-//   Q6_K : [g][p][piece 0..12][lane] bytes 16*piece.. (ql, qh, scales) | [g][p][lane] d
-//   Q8_0 : [g][p][piece 0..15][lane] block piece/2, qs half piece%2 | [g][p][lane] 8 x d
+// Q6_K 210 B, Q8_0 34 B).  The GEMM kernel gives each lane of a wave one row of
+// a 64-row tile and walks the row one 256-element unit at a time, so the
+// repack orders the bytes the way one wave instruction reads them: per (tile,
+// unit), piece-major, then lane, 16 bytes per lane (see repack_kernel).  Every
+// 128-bit load of the kernel is then a contiguous 1 KiB read, and the total
+// size equals ggml's (plus zero padding of the last tile).
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -92,6 +88,7 @@ extern "C" void cpv_free(cpv_ctx* ctx)
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->gsum) (void)hipFree(ctx->gsum);
     for (hipEvent_t e : ctx->prof_ev) (void)hipEventDestroy(e);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
@@ -235,17 +232,26 @@ cpv_status cpv_workspace(cpv_ctx* ctx, size_t bytes, void** out)
 // ---------------------------------------------------------------- repack
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return cpv_h2f(h); }
 
+// Tile layout of a repacked weight.  Rows are padded to tiles of 64; for
+// tile t and 256-element unit u the slab (t*U + u) holds PIECES x 64 lanes x
+// 16 bytes, lane = row within the tile, so the wave that owns the tile reads
+// each piece as one contiguous KiB:
+//   Q4_K  pieces 0-7 = qs (block bytes 16..143), piece 8 = d, dmin, scales[12]
+//   Q6_K  pieces 0-12 = ql, qh, scales (block bytes 0..207); the f16 d of
+//         every (row, unit) follows all slabs as [t*U + u][lane] u16
+//   Q8_0  pieces 0-15 = the codes of the unit's 8 blocks, piece 16 = their 8 d
+// Missing rows and units are zero (their Ew is empty, so they contribute 0).
 template <int TYPE>
 __global__ void repack_kernel(const uint8_t* __restrict__ aos, uint8_t* __restrict__ out, int64_t n,
-                              int64_t k, int64_t P, int64_t total)
+                              int64_t k, int64_t U, int64_t total)
 {
-    constexpr int PIECES = TYPE == CPV_Q4_K ? 8 : TYPE == CPV_Q6_K ? 13 : 16;
+    constexpr int PIECES = TYPE == CPV_Q4_K ? 9 : TYPE == CPV_Q6_K ? 13 : 17;
     constexpr int BSZ = TYPE == CPV_Q4_K ? 144 : TYPE == CPV_Q6_K ? 210 : 34;
     constexpr int BLK = TYPE == CPV_Q8_0 ? 32 : 256;
     const int64_t nblk = k / BLK;
     const int64_t rb = nblk * BSZ;
-    const int64_t groups = (n + 15) / 16;
-    const int64_t region_a = groups * P * PIECES * 1024;
+    const int64_t tiles = (n + 63) / 64;
+    const int64_t region_a = tiles * U * PIECES * 1024;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * blockDim.x) {
         int64_t src = -1;
@@ -253,46 +259,31 @@ __global__ void repack_kernel(const uint8_t* __restrict__ aos, uint8_t* __restri
             const int b = (int)(i & 15);
             const int lane = (int)((i >> 4) & 63);
             const int piece = (int)((i >> 10) % PIECES);
-            const int64_t gp = (i >> 10) / PIECES;
-            const int64_t g = gp / P, p = gp % P;
-            const int64_t row = g * 16 + (lane & 15);
-            const int64_t unit = p * 4 + (lane >> 4);       // 256-element unit
+            const int64_t slab = (i >> 10) / PIECES;
+            const int64_t t = slab / U, u = slab % U;
+            const int64_t row = t * 64 + lane;
             if (row < n) {
                 if (TYPE == CPV_Q4_K) {
-                    if (unit < nblk) src = row * rb + unit * 144 + 16 + 16 * piece + b;
+                    if (u < nblk) src = row * rb + u * 144 + (piece < 8 ? 16 + 16 * piece : 0) + b;
                 } else if (TYPE == CPV_Q6_K) {
-                    if (unit < nblk) src = row * rb + unit * 210 + 16 * piece + b;
-                } else {
-                    const int64_t blk = unit * 8 + piece / 2;
+                    if (u < nblk) src = row * rb + u * 210 + 16 * piece + b;
+                } else if (piece < 16) {
+                    const int64_t blk = u * 8 + piece / 2;
                     if (blk < nblk) src = row * rb + blk * 34 + 2 + 16 * (piece & 1) + b;
+                } else {
+                    const int64_t blk = u * 8 + b / 2;
+                    if (blk < nblk) src = row * rb + blk * 34 + (b & 1);
                 }
             }
         } else {
+            // Q6_K d region
             const int64_t j = i - region_a;
-            if (TYPE == CPV_Q6_K) {
-                const int b = (int)(j & 1);
-                const int lane = (int)((j >> 1) & 63);
-                const int64_t gp = j >> 7;
-                const int64_t g = gp / P, p = gp % P;
-                const int64_t row = g * 16 + (lane & 15);
-                const int64_t unit = p * 4 + (lane >> 4);
-                if (row < n && unit < nblk) src = row * rb + unit * 210 + 208 + b;
-            } else {
-                const int b = (int)(j & 15);
-                const int lane = (int)((j >> 4) & 63);
-                const int64_t gp = j >> 10;
-                const int64_t g = gp / P, p = gp % P;
-                const int64_t row = g * 16 + (lane & 15);
-                const int64_t unit = p * 4 + (lane >> 4);
-                if (row < n) {
-                    if (TYPE == CPV_Q4_K) {
-                        if (unit < nblk) src = row * rb + unit * 144 + b;
-                    } else {
-                        const int64_t blk = unit * 8 + b / 2;
-                        if (blk < nblk) src = row * rb + blk * 34 + (b & 1);
-                    }
-                }
-            }
+            const int b = (int)(j & 1);
+            const int lane = (int)((j >> 1) & 63);
+            const int64_t slab = j >> 7;
+            const int64_t t = slab / U, u = slab % U;
+            const int64_t row = t * 64 + lane;
+            if (row < n && u < nblk) src = row * rb + u * 210 + 208 + b;
         }
         out[i] = src >= 0 ? aos[src] : 0;
     }
@@ -333,14 +324,11 @@ __global__ void row_exponent_kernel(const uint8_t* __restrict__ aos, int32_t* __
 
 static void weight_geometry(cpv_weight* w)
 {
-    const int64_t blk = cpv_type_block(w->type);
-    const int64_t units256 = (w->k + 255) / 256;
-    w->units = w->k / blk;
-    w->passes = (units256 + 3) / 4;
-    w->n_pad = (w->n + 15) / 16 * 16;
-    const int64_t slots = w->n_pad * w->passes * 4;   // 256-element slots
+    w->units = (w->k + 255) / 256;
+    w->n_pad = (w->n + 63) / 64 * 64;
+    const int64_t slots = w->n_pad * w->units;          // (row, unit) pairs
     switch (w->type) {
-    case CPV_Q4_K: w->data_bytes = (size_t)slots * (128 + 16); break;
+    case CPV_Q4_K: w->data_bytes = (size_t)slots * 144; break;
     case CPV_Q6_K: w->data_bytes = (size_t)slots * (208 + 2); break;
     default: w->data_bytes = (size_t)slots * (256 + 16); break;
     }
@@ -357,15 +345,15 @@ cpv_status cpv_repack_launch(cpv_ctx* ctx, cpv_weight* w, const void* aos_dev)
     const int eblocks = (int)((w->n_pad + 255) / 256);
     switch (w->type) {
     case CPV_Q4_K:
-        repack_kernel<CPV_Q4_K><<<blocks, threads, 0, ctx->stream>>>(a, o, w->n, w->k, w->passes, total);
+        repack_kernel<CPV_Q4_K><<<blocks, threads, 0, ctx->stream>>>(a, o, w->n, w->k, w->units, total);
         row_exponent_kernel<CPV_Q4_K><<<eblocks, 256, 0, ctx->stream>>>(a, w->ew, w->n, w->n_pad, w->k);
         break;
     case CPV_Q6_K:
-        repack_kernel<CPV_Q6_K><<<blocks, threads, 0, ctx->stream>>>(a, o, w->n, w->k, w->passes, total);
+        repack_kernel<CPV_Q6_K><<<blocks, threads, 0, ctx->stream>>>(a, o, w->n, w->k, w->units, total);
         row_exponent_kernel<CPV_Q6_K><<<eblocks, 256, 0, ctx->stream>>>(a, w->ew, w->n, w->n_pad, w->k);
         break;
     default:
-        repack_kernel<CPV_Q8_0><<<blocks, threads, 0, ctx->stream>>>(a, o, w->n, w->k, w->passes, total);
+        repack_kernel<CPV_Q8_0><<<blocks, threads, 0, ctx->stream>>>(a, o, w->n, w->k, w->units, total);
         row_exponent_kernel<CPV_Q8_0><<<eblocks, 256, 0, ctx->stream>>>(a, w->ew, w->n, w->n_pad, w->k);
         break;
     }
@@ -425,6 +413,63 @@ extern "C" cpv_status cpv_weight_from_device(cpv_ctx* ctx, int type, const void*
     return weight_create(ctx, type, dev_bytes, true, n_rows, k, out);
 }
 
+// Rows of several weights stacked into one (same type and k; every part but
+// the last a whole number of 64-row tiles, so the tiles just follow each
+// other): the tile slabs of the parts in order, then, for Q6_K, their d
+// regions in order, and their row exponents.  The parts stay as they are.
+cpv_status cpv_weight_concat(cpv_ctx* ctx, cpv_weight* const* parts, int np, cpv_weight** out)
+{
+    *out = nullptr;
+    if (np < 1) return cpv_fail(ctx, CPV_EINVAL, "weight_concat: no parts");
+    const int type = parts[0]->type;
+    const int64_t k = parts[0]->k;
+    int64_t n = 0;
+    for (int i = 0; i < np; i++) {
+        if (parts[i]->type != type || parts[i]->k != k)
+            return cpv_fail(ctx, CPV_EINVAL, "weight_concat: parts differ in type or k");
+        if (i + 1 < np && parts[i]->n % 64)
+            return cpv_fail(ctx, CPV_EINVAL, "weight_concat: part %d has %lld rows, not whole tiles", i,
+                            (long long)parts[i]->n);
+        n += parts[i]->n;
+    }
+    cpv_weight* w = new (std::nothrow) cpv_weight();
+    if (!w) return cpv_fail(ctx, CPV_ENOMEM, "weight_concat: host allocation");
+    w->ctx = ctx;
+    w->type = type;
+    w->n = n;
+    w->k = k;
+    weight_geometry(w);
+    hipError_t e = hipMalloc(&w->data, w->data_bytes);
+    if (e == hipSuccess) e = hipMalloc((void**)&w->ew, sizeof(int32_t) * (size_t)w->n_pad);
+    const size_t slab = (size_t)w->units * (type == CPV_Q4_K ? 9 : type == CPV_Q6_K ? 13 : 17) * 1024;
+    size_t off_a = 0, off_d = (size_t)(w->n_pad / 64) * slab, off_e = 0;
+    for (int i = 0; i < np && e == hipSuccess; i++) {
+        const cpv_weight* q = parts[i];
+        const size_t ra = (size_t)(q->n_pad / 64) * slab;
+        e = hipMemcpyAsync((uint8_t*)w->data + off_a, q->data, ra, hipMemcpyDeviceToDevice, ctx->stream);
+        off_a += ra;
+        if (e == hipSuccess && type == CPV_Q6_K) {
+            const size_t rd = (size_t)(q->n_pad / 64) * w->units * 64 * 2;
+            e = hipMemcpyAsync((uint8_t*)w->data + off_d, (const uint8_t*)q->data + ra, rd, hipMemcpyDeviceToDevice,
+                               ctx->stream);
+            off_d += rd;
+        }
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(w->ew + off_e, q->ew, sizeof(int32_t) * (size_t)q->n_pad, hipMemcpyDeviceToDevice,
+                               ctx->stream);
+        off_e += (size_t)q->n_pad;
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        if (w->data) (void)hipFree(w->data);
+        if (w->ew) (void)hipFree(w->ew);
+        delete w;
+        return cpv_hip_fail(ctx, e, "weight_concat");
+    }
+    *out = w;
+    return CPV_OK;
+}
+
 extern "C" void cpv_weight_free(cpv_weight* w)
 {
     if (!w) return;
@@ -453,27 +498,28 @@ extern "C" cpv_status cpv_weight_info(const cpv_weight* w, int* type, int64_t* n
 //   Q8_0: q * d;  Q4_K: (d*sc)*q - (dmin*m);  Q6_K: d*sc*q, left to right.
 template <int TYPE>
 __global__ void get_rows_kernel(const uint8_t* __restrict__ data, const int32_t* __restrict__ rows,
-                                int64_t nrows, int64_t n, int64_t k, int64_t P, float* __restrict__ out)
+                                int64_t nrows, int64_t n, int64_t k, int64_t U, float* __restrict__ out)
 {
+    constexpr int PIECES = TYPE == CPV_Q4_K ? 9 : TYPE == CPV_Q6_K ? 13 : 17;
     const int64_t r_out = blockIdx.y;
     if (r_out >= nrows) return;
     const int64_t row = rows[r_out];
-    const int64_t groups = (n + 15) / 16;
+    const int64_t tiles = (n + 63) / 64;
     for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < k; e += (int64_t)gridDim.x * blockDim.x) {
         float v = 0.0f;
         if (row >= 0 && row < n) {
-            const int64_t g = row / 16, r = row % 16;
-            const int64_t unit = e / 256, p = unit / 4, q = unit % 4;
-            const int lane = (int)(r + 16 * q);
+            const int64_t t = row / 64;
+            const int lane = (int)(row % 64);
+            const int64_t u = e / 256;
             const int el = (int)(e % 256);
+            const uint8_t* slab = data + (t * U + u) * PIECES * 1024 + lane * 16;
+            auto byte_at = [&](int idx) { return slab[(idx / 16) * 1024 + idx % 16]; };   // block byte idx of the piece run
             if (TYPE == CPV_Q4_K) {
-                const int64_t region_a = groups * P * 8 * 1024;
-                const uint8_t* meta = data + region_a + ((g * P + p) * 64 + lane) * 16;
-                const int c = el / 64, l = el % 32, hi = (el % 64) >= 32;
-                const int qsbyte = c * 32 + l;
-                const uint8_t byte = data[((g * P + p) * 8 + qsbyte / 16) * 1024 + lane * 16 + qsbyte % 16];
-                const int code = hi ? (byte >> 4) : (byte & 15);
-                const int j = el / 32;
+                const uint8_t* meta = slab + 8 * 1024;
+                const int j = el / 32, l = el % 32;
+                const int qsbyte = (j / 2) * 32 + l;
+                const uint8_t byte = byte_at(qsbyte);
+                const int code = (j & 1) ? (byte >> 4) : (byte & 15);
                 const uint8_t* s = meta + 4;
                 int sc, m;
                 if (j < 4) { sc = s[j] & 63; m = s[j + 4] & 63; }
@@ -483,25 +529,19 @@ __global__ void get_rows_kernel(const uint8_t* __restrict__ data, const int32_t*
                 const float d1 = d * (float)sc, m1 = dm * (float)m;
                 v = d1 * (float)code - m1;
             } else if (TYPE == CPV_Q6_K) {
-                const int64_t region_a = groups * P * 13 * 1024;
-                auto bytei = [&](int idx) {
-                    return data[((g * P + p) * 13 + idx / 16) * 1024 + lane * 16 + idx % 16];
-                };
                 const int h = el / 128, l = el % 128, l32 = l % 32, quad = l / 32;
-                const uint8_t ql = bytei(h * 64 + l32 + (quad & 1) * 32);
-                const uint8_t qh = bytei(128 + h * 32 + l32);
+                const uint8_t ql = byte_at(h * 64 + l32 + (quad & 1) * 32);
+                const uint8_t qh = byte_at(128 + h * 32 + l32);
                 const int lo = (quad < 2) ? (ql & 15) : (ql >> 4);
                 const int code = (lo | (((qh >> (2 * quad)) & 3) << 4)) - 32;
-                const int8_t sc = (int8_t)bytei(192 + el / 16);
-                const uint8_t* dd = data + region_a + ((g * P + p) * 64 + lane) * 2;
+                const int8_t sc = (int8_t)byte_at(192 + el / 16);
+                const uint8_t* dd = data + tiles * U * 13 * 1024 + ((t * U + u) * 64 + lane) * 2;
                 const float d = f16_to_f32((uint16_t)(dd[0] | (dd[1] << 8)));
                 v = d * (float)sc * (float)code;
             } else {
-                const int64_t region_a = groups * P * 16 * 1024;
-                const int blk = el / 32, bi = el % 32;
-                const int qsbyte = blk * 32 + bi;
-                const int8_t code = (int8_t)data[((g * P + p) * 16 + qsbyte / 16) * 1024 + lane * 16 + qsbyte % 16];
-                const uint8_t* dd = data + region_a + ((g * P + p) * 64 + lane) * 16 + blk * 2;
+                const int blk = el / 32;
+                const int8_t code = (int8_t)byte_at(el);
+                const uint8_t* dd = slab + 16 * 1024 + blk * 2;
                 v = (float)code * f16_to_f32((uint16_t)(dd[0] | (dd[1] << 8)));
             }
         }
@@ -518,9 +558,9 @@ extern "C" cpv_status cpv_get_rows(cpv_ctx* ctx, const cpv_weight* w, const int3
     dim3 grid((unsigned)((w->k + 255) / 256), (unsigned)n);
     const uint8_t* d = (const uint8_t*)w->data;
     switch (w->type) {
-    case CPV_Q4_K: get_rows_kernel<CPV_Q4_K><<<grid, 256, 0, ctx->stream>>>(d, rows_dev, n, w->n, w->k, w->passes, out_dev); break;
-    case CPV_Q6_K: get_rows_kernel<CPV_Q6_K><<<grid, 256, 0, ctx->stream>>>(d, rows_dev, n, w->n, w->k, w->passes, out_dev); break;
-    default: get_rows_kernel<CPV_Q8_0><<<grid, 256, 0, ctx->stream>>>(d, rows_dev, n, w->n, w->k, w->passes, out_dev); break;
+    case CPV_Q4_K: get_rows_kernel<CPV_Q4_K><<<grid, 256, 0, ctx->stream>>>(d, rows_dev, n, w->n, w->k, w->units, out_dev); break;
+    case CPV_Q6_K: get_rows_kernel<CPV_Q6_K><<<grid, 256, 0, ctx->stream>>>(d, rows_dev, n, w->n, w->k, w->units, out_dev); break;
+    default: get_rows_kernel<CPV_Q8_0><<<grid, 256, 0, ctx->stream>>>(d, rows_dev, n, w->n, w->k, w->units, out_dev); break;
     }
     CPV_HIP(ctx, hipGetLastError());
     return CPV_OK;

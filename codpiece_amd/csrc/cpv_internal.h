@@ -19,7 +19,11 @@ struct cpv_ctx {
     // scratch owned by the context, grown on demand (never inside a capture)
     void* ws = nullptr;
     size_t ws_bytes = 0;
-    uint64_t ws_gen = 0;      // bumped whenever ws is reallocated
+    uint64_t ws_gen = 0;      // bumped whenever ws (or the GEMM accumulator) is reallocated
+    // the split-K GEMM accumulator [16][n_pad] f64: zero between launches
+    // (each finalize leaves it as it found it)
+    double* gsum = nullptr;
+    size_t gsum_bytes = 0;
     // kernel timing (cpv_profile_start / _stop): event pairs around launches,
     // and each launch kept for cpv_profile_replay
     struct prof_rec { int cls, ev0, ev1; double bytes; };
@@ -43,13 +47,10 @@ struct cpv_weight {
     cpv_ctx* ctx = nullptr;
     int type = 0;
     int64_t n = 0, k = 0;     // logical rows and row length
-    int64_t n_pad = 0;        // rows padded to the 16-row groups of the GEMM
-    int64_t units = 0;        // super-blocks (K-quants) or 32-blocks (Q8_0) per row
-    int64_t passes = 0;       // 256-element passes per row (padded)
-    void* data = nullptr;     // repacked blocks, layout per type (qgemm.hip)
+    int64_t n_pad = 0;        // rows padded to the 64-row tiles of the GEMM
+    int64_t units = 0;        // 256-element units per row (a super-block, or 8 Q8_0 blocks)
+    void* data = nullptr;     // repacked tiles, layout per type (api.hip)
     size_t data_bytes = 0;
-    void* aos = nullptr;      // ggml row layout, kept for get_rows
-    size_t aos_bytes = 0;
     int32_t* ew = nullptr;    // [n_pad] frexp exponent of the row's largest scale
 };
 
@@ -138,6 +139,10 @@ struct cpv_act {
 size_t cpv_act_bytes(int type, int64_t k, int64_t m);
 cpv_status cpv_quant_act(cpv_ctx* ctx, int type, const float* x, int64_t m, int64_t k, void* buf, cpv_act* out);
 cpv_status cpv_qgemm_act(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, float* y);
+
+// rows of several weights stacked into a new weight (same type and k, every
+// part but the last in whole 64-row tiles)
+cpv_status cpv_weight_concat(cpv_ctx* ctx, cpv_weight* const* parts, int np, cpv_weight** out);
 
 // internal launchers
 cpv_status cpv_repack_launch(cpv_ctx* ctx, cpv_weight* w, const void* aos_dev);

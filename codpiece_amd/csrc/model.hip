@@ -34,18 +34,32 @@ __device__ __forceinline__ int ceil_log2_dev(int64_t v)
 }
 
 // y = rms_norm(x) * w over rows of n; exact fixed-point sum of the f32 squares
-// (order-free), then ggml's f32 tail.  One block per row.
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, int64_t xs,
-                                                      const float* __restrict__ w, float* __restrict__ y,
-                                                      int64_t ys, int n, float eps)
+// (order-free), then ggml's f32 tail.  One block of 1024 threads per row; the
+// row is read once into registers (n <= RMS_PER * 1024), else re-read.
+constexpr int RMS_PER = 24;
+
+__global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__ x, int64_t xs,
+                                                       const float* __restrict__ w, float* __restrict__ y,
+                                                       int64_t ys, int n, float eps)
 {
     const float* xr = x + (int64_t)blockIdx.x * xs;
     float* yr = y + (int64_t)blockIdx.x * ys;
-    __shared__ float s_max[4];
-    __shared__ long long s_sum[4];
+    __shared__ float s_max[16];
+    __shared__ long long s_sum[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = (blockDim.x + 63) >> 6;
+    const bool cached = n <= RMS_PER * (int)blockDim.x;
+    float v[RMS_PER];
     float am = 0.0f;
-    for (int i = tid; i < n; i += blockDim.x) am = fmaxf(am, fabsf(xr[i]));
+    if (cached) {
+#pragma unroll
+        for (int j = 0; j < RMS_PER; j++) {
+            const int i = tid + j * blockDim.x;
+            v[j] = i < n ? xr[i] : 0.0f;
+            am = fmaxf(am, fabsf(v[j]));
+        }
+    } else {
+        for (int i = tid; i < n; i += blockDim.x) am = fmaxf(am, fabsf(xr[i]));
+    }
     for (int off = 32; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));
     if (lane == 0) s_max[wave] = am;
     __syncthreads();
@@ -57,9 +71,14 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
         frexpf(am, &e);
         const int g = 2 * e - (62 - ceil_log2_dev(n + 1));
         long long S = 0;
-        for (int i = tid; i < n; i += blockDim.x) {
-            const float sq = xr[i] * xr[i];
-            S += (long long)floor(ldexp((double)sq, -g));
+        if (cached) {
+#pragma unroll
+            for (int j = 0; j < RMS_PER; j++) S += (long long)floor(ldexp((double)(v[j] * v[j]), -g));
+        } else {
+            for (int i = tid; i < n; i += blockDim.x) {
+                const float sq = xr[i] * xr[i];
+                S += (long long)floor(ldexp((double)sq, -g));
+            }
         }
         for (int off = 32; off > 0; off >>= 1) S += __shfl_xor(S, off);
         if (lane == 0) s_sum[wave] = S;
@@ -70,9 +89,20 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
     }
     const float mean = (float)(sum / (double)n);
     const float scale = 1.0f / sqrtf(mean + eps);
-    for (int i = tid; i < n; i += blockDim.x) {
-        const float v = xr[i] * scale;
-        yr[i] = w ? v * w[i] : v;
+    if (cached) {
+#pragma unroll
+        for (int j = 0; j < RMS_PER; j++) {
+            const int i = tid + j * blockDim.x;
+            if (i < n) {
+                const float t = v[j] * scale;
+                yr[i] = w ? t * w[i] : t;
+            }
+        }
+    } else {
+        for (int i = tid; i < n; i += blockDim.x) {
+            const float t = xr[i] * scale;
+            yr[i] = w ? t * w[i] : t;
+        }
     }
 }
 
@@ -80,9 +110,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
 // rope_pos0 + t, then q to qout, k (f16) to k_cache row kv_row0 + t and v (f16)
 // to column kv_row0 + t of the transposed V cache.  Grid (T, H + Hkv), block hd.
 struct PrepArgs {
-    const float* qg;       // [T][H][2*hd]  query | output gate per head
-    const float* kk;       // [T][Hkv*hd]
-    const float* vv;       // [T][Hkv*hd]
+    const float* qg;       // [T] rows of qs floats: [H][2*hd] query | output gate per head
+    const float* kk;       // [T] rows of ks floats: [Hkv*hd]
+    const float* vv;       // [T] rows of ks floats: [Hkv*hd]
+    int64_t qs, ks;        // row strides (a fused q|k|v output shares one)
     const float* q_norm;   // [hd]
     const float* k_norm;   // [hd]
     const float* rope;     // [n_pos][n_rot/2][2]
@@ -100,7 +131,7 @@ __global__ __launch_bounds__(128) void qk_prep_kernel(PrepArgs a)
     const int t = blockIdx.x, hh = blockIdx.y, i = threadIdx.x;
     const bool is_q = hh < a.H;
     const int kh = hh - a.H;
-    const float* src = is_q ? a.qg + ((int64_t)t * a.H + hh) * 2 * a.hd : a.kk + ((int64_t)t * a.Hkv + kh) * a.hd;
+    const float* src = is_q ? a.qg + (int64_t)t * a.qs + (int64_t)hh * 2 * a.hd : a.kk + (int64_t)t * a.ks + (int64_t)kh * a.hd;
     const float* w = is_q ? a.q_norm : a.k_norm;
     __shared__ float s_v[128];
     __shared__ float s_am[2];
@@ -151,20 +182,20 @@ __global__ __launch_bounds__(128) void qk_prep_kernel(PrepArgs a)
     } else if (a.write) {
         const int64_t row = a.kv_row0 + t;
         a.k_cache[row * a.Hkv * a.hd + (int64_t)kh * a.hd + i] = cpv_f2h(out);
-        const float vv = a.vv[((int64_t)t * a.Hkv + kh) * a.hd + i];
+        const float vv = a.vv[(int64_t)t * a.ks + (int64_t)kh * a.hd + i];
         a.v_cache_t[((int64_t)kh * a.hd + i) * a.v_stride + row] = cpv_f2h(vv);
     }
 }
 
-// out[t][h*hd + i] = attn[t][h*hd + i] * sigmoid(gate), gate = qg[t][h][hd + i]
-__global__ void gate_mul_kernel(const float* __restrict__ attn, const float* __restrict__ qg, int H, int hd,
-                                int64_t total, float* __restrict__ out)
+// out[t][h*hd + i] = attn[t][h*hd + i] * sigmoid(gate), gate = qg[t*qs + h*2hd + hd + i]
+__global__ void gate_mul_kernel(const float* __restrict__ attn, const float* __restrict__ qg, int64_t qs, int H,
+                                int hd, int64_t total, float* __restrict__ out)
 {
     for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
         const int64_t t = e / ((int64_t)H * hd);
         const int64_t r = e % ((int64_t)H * hd);
         const int64_t h = r / hd, i = r % hd;
-        const float g = qg[(t * H + h) * 2 * hd + hd + i];
+        const float g = qg[t * qs + h * 2 * hd + hd + i];
         const float sig = 1.0f / (1.0f + cpv_expf(-g));
         out[e] = attn[e] * sig;
     }
@@ -176,14 +207,15 @@ __global__ void add_kernel(const float* a, const float* b, float* y, int64_t n) 
         y[e] = a[e] + b[e];
 }
 
-// act = silu(g) * u, silu(x) = x / (1 + expf(-x))
-__global__ void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ y,
-                              int64_t n)
+// act[t][i] = silu(g[t*gs + i]) * u[t*gs + i], silu(x) = x / (1 + expf(-x)); F per row
+__global__ void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u, int64_t gs, int64_t F,
+                              float* __restrict__ y, int64_t n)
 {
     for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
-        const float x = g[e];
+        const int64_t t = e / F, i = e % F;
+        const float x = g[t * gs + i];
         const float s = x / (1.0f + cpv_expf(-x));
-        y[e] = s * u[e];
+        y[e] = s * u[t * gs + i];
     }
 }
 
@@ -222,6 +254,7 @@ unsigned grid_for(int64_t n) { return (unsigned)((n + 255) / 256 < 4096 ? (n + 2
 struct LayerW {
     cpv_weight *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr;
     cpv_weight *gate = nullptr, *up = nullptr, *down = nullptr;
+    cpv_weight *qkv = nullptr, *gate_up = nullptr;   // stacked copies when the parts allow it
     float *attn_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
 };
 
@@ -248,6 +281,7 @@ struct cpv_session {
     // activations, max_batch rows
     float *x, *xn, *qg, *kk, *vv, *q, *att, *gated, *o, *up, *gt, *act, *h, *logits, *e, *cat, *d, *dsa;
     float *mtp_logits, *hn, *hsrc;
+    float *qkv, *gu;                      // outputs of the stacked q|k|v and gate|up GEMMs
     int32_t *tok, *preds, *chain;
     float* conf;
     void* actbuf;                         // quantized activations
@@ -385,9 +419,10 @@ extern "C" cpv_status cpv_model_ready(cpv_model* m)
         const LayerW& L = m->layers[il];
         if (!L.attn_norm || !L.post_norm || !L.q_norm || !L.k_norm)
             return cpv_fail(ctx, CPV_EINVAL, "model: layer %zu norms missing", il);
-        if ((st = shape(L.wq, 2 * H * hd, E, "attn_q")) || (st = shape(L.wk, Hkv * hd, E, "attn_k")) ||
-            (st = shape(L.wv, Hkv * hd, E, "attn_v")) || (st = shape(L.wo, E, H * hd, "attn_output")) ||
-            (st = shape(L.gate, F, E, "ffn_gate")) || (st = shape(L.up, F, E, "ffn_up")) ||
+        if ((!L.qkv && ((st = shape(L.wq, 2 * H * hd, E, "attn_q")) || (st = shape(L.wk, Hkv * hd, E, "attn_k")) ||
+                        (st = shape(L.wv, Hkv * hd, E, "attn_v")))) ||
+            (st = shape(L.wo, E, H * hd, "attn_output")) ||
+            (!L.gate_up && ((st = shape(L.gate, F, E, "ffn_gate")) || (st = shape(L.up, F, E, "ffn_up")))) ||
             (st = shape(L.down, E, F, "ffn_down")))
             return st;
     }
@@ -397,6 +432,36 @@ extern "C" cpv_status cpv_model_ready(cpv_model* m)
         if (!m->mtp_embed) m->mtp_embed = m->tok_embd;
         if (!m->mtp_head) m->mtp_head = m->output;
         if (!m->mtp_head_norm) m->mtp_head_norm = m->output_norm;
+    }
+    // Stack q|k|v and gate|up into one weight each where the parts allow it
+    // (same type, whole 64-row tiles): one activation pass and one GEMM launch
+    // instead of three / two.  The parts are freed.
+    auto release = [&](cpv_weight* w) {
+        for (size_t i = 0; i < m->weights.size(); i++)
+            if (m->weights[i] == w) {
+                cpv_weight_free(w);
+                m->weights.erase(m->weights.begin() + (long)i);
+                return;
+            }
+    };
+    for (LayerW& L : m->layers) {
+        if (!L.qkv && L.wq->type == L.wk->type && L.wk->type == L.wv->type && L.wq->n % 64 == 0 && L.wk->n % 64 == 0) {
+            cpv_weight* parts[3] = {L.wq, L.wk, L.wv};
+            if ((st = cpv_weight_concat(ctx, parts, 3, &L.qkv))) return st;
+            m->weights.push_back(L.qkv);
+            release(L.wq);
+            release(L.wk);
+            release(L.wv);
+            L.wq = L.wk = L.wv = nullptr;
+        }
+        if (!L.gate_up && L.gate->type == L.up->type && L.gate->n % 64 == 0) {
+            cpv_weight* parts[2] = {L.gate, L.up};
+            if ((st = cpv_weight_concat(ctx, parts, 2, &L.gate_up))) return st;
+            m->weights.push_back(L.gate_up);
+            release(L.gate);
+            release(L.up);
+            L.gate = L.up = nullptr;
+        }
     }
     return CPV_OK;
 }
@@ -453,6 +518,8 @@ extern "C" cpv_status cpv_session_create(cpv_model* m, int64_t n_ctx, int32_t ma
     A((size_t)T * F * 4, (void**)&s->up);
     A((size_t)T * F * 4, (void**)&s->gt);
     A((size_t)T * F * 4, (void**)&s->act);
+    A((size_t)T * (2 * H + 2 * Hkv) * hd * 4, (void**)&s->qkv);
+    A((size_t)T * 2 * F * 4, (void**)&s->gu);
     A((size_t)T * E * 4, (void**)&s->h);
     A((size_t)T * V * 4, (void**)&s->logits);
     A((size_t)T * V * 4, (void**)&s->mtp_logits);
@@ -543,7 +610,7 @@ namespace {
 cpv_status rmsnorm(cpv_ctx* ctx, const float* x, int64_t xs, const float* w, float* y, int64_t ys, int64_t rows,
                    int n, float eps)
 {
-    rmsnorm_kernel<<<(unsigned)rows, 256, 0, ctx->stream>>>(x, xs, w, y, ys, n, eps);
+    rmsnorm_kernel<<<(unsigned)rows, 1024, 0, ctx->stream>>>(x, xs, w, y, ys, n, eps);
     CPV_HIP(ctx, hipGetLastError());
     return CPV_OK;
 }
@@ -560,16 +627,28 @@ cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_
     cpv_act act;
     // attention (build_attn_block)
     if ((st = rmsnorm(ctx, x, E, L.attn_norm, s->xn, E, T, (int)E, hp.rms_eps))) return st;
-    if ((st = cpv_quant_act(ctx, L.wq->type, s->xn, T, E, s->actbuf, &act))) return st;
-    if ((st = cpv_qgemm_act(ctx, L.wq, &act, s->qg))) return st;
-    if (L.wk->type != L.wq->type && (st = cpv_quant_act(ctx, L.wk->type, s->xn, T, E, s->actbuf, &act))) return st;
-    if ((st = cpv_qgemm_act(ctx, L.wk, &act, s->kk))) return st;
-    if (L.wv->type != L.wk->type && (st = cpv_quant_act(ctx, L.wv->type, s->xn, T, E, s->actbuf, &act))) return st;
-    if ((st = cpv_qgemm_act(ctx, L.wv, &act, s->vv))) return st;
     PrepArgs pa;
-    pa.qg = s->qg;
-    pa.kk = s->kk;
-    pa.vv = s->vv;
+    if (L.qkv) {
+        // one GEMM for q|gate, k and v: row stride 2*H*hd + 2*Hkv*hd
+        if ((st = cpv_quant_act(ctx, L.qkv->type, s->xn, T, E, s->actbuf, &act))) return st;
+        if ((st = cpv_qgemm_act(ctx, L.qkv, &act, s->qkv))) return st;
+        pa.qg = s->qkv;
+        pa.kk = s->qkv + 2 * H * hd;
+        pa.vv = pa.kk + Hkv * hd;
+        pa.qs = pa.ks = L.qkv->n;
+    } else {
+        if ((st = cpv_quant_act(ctx, L.wq->type, s->xn, T, E, s->actbuf, &act))) return st;
+        if ((st = cpv_qgemm_act(ctx, L.wq, &act, s->qg))) return st;
+        if (L.wk->type != L.wq->type && (st = cpv_quant_act(ctx, L.wk->type, s->xn, T, E, s->actbuf, &act))) return st;
+        if ((st = cpv_qgemm_act(ctx, L.wk, &act, s->kk))) return st;
+        if (L.wv->type != L.wk->type && (st = cpv_quant_act(ctx, L.wv->type, s->xn, T, E, s->actbuf, &act))) return st;
+        if ((st = cpv_qgemm_act(ctx, L.wv, &act, s->vv))) return st;
+        pa.qg = s->qg;
+        pa.kk = s->kk;
+        pa.vv = s->vv;
+        pa.qs = 2 * H * hd;
+        pa.ks = Hkv * hd;
+    }
     pa.q_norm = L.q_norm;
     pa.k_norm = L.k_norm;
     pa.rope = s->rope;
@@ -597,17 +676,26 @@ cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_
             CPV_HIP(ctx, hipMemcpyAsync(s->tap + s->tap_off, s->att, (size_t)n * 4, hipMemcpyDeviceToDevice, ctx->stream));
         s->tap_off += n;
     }
-    gate_mul_kernel<<<grid_for(T * H * hd), 256, 0, ctx->stream>>>(s->att, s->qg, (int)H, (int)hd, T * H * hd, s->gated);
+    gate_mul_kernel<<<grid_for(T * H * hd), 256, 0, ctx->stream>>>(s->att, pa.qg, pa.qs, (int)H, (int)hd, T * H * hd,
+                                                                  s->gated);
     if ((st = cpv_quant_act(ctx, L.wo->type, s->gated, T, H * hd, s->actbuf, &act))) return st;
     if ((st = cpv_qgemm_act(ctx, L.wo, &act, s->o))) return st;
     add_kernel<<<grid_for(T * E), 256, 0, ctx->stream>>>(s->o, x, x, T * E);
     // FFN
     if ((st = rmsnorm(ctx, x, E, L.post_norm, s->xn, E, T, (int)E, hp.rms_eps))) return st;
-    if ((st = cpv_quant_act(ctx, L.up->type, s->xn, T, E, s->actbuf, &act))) return st;
-    if ((st = cpv_qgemm_act(ctx, L.up, &act, s->up))) return st;
-    if (L.gate->type != L.up->type && (st = cpv_quant_act(ctx, L.gate->type, s->xn, T, E, s->actbuf, &act))) return st;
-    if ((st = cpv_qgemm_act(ctx, L.gate, &act, s->gt))) return st;
-    swiglu_kernel<<<grid_for(T * F), 256, 0, ctx->stream>>>(s->gt, s->up, s->act, T * F);
+    if (L.gate_up) {
+        // one GEMM for gate|up: row stride 2F
+        if ((st = cpv_quant_act(ctx, L.gate_up->type, s->xn, T, E, s->actbuf, &act))) return st;
+        if ((st = cpv_qgemm_act(ctx, L.gate_up, &act, s->gu))) return st;
+        swiglu_kernel<<<grid_for(T * F), 256, 0, ctx->stream>>>(s->gu, s->gu + F, 2 * F, F, s->act, T * F);
+    } else {
+        if ((st = cpv_quant_act(ctx, L.up->type, s->xn, T, E, s->actbuf, &act))) return st;
+        if ((st = cpv_qgemm_act(ctx, L.up, &act, s->up))) return st;
+        if (L.gate->type != L.up->type && (st = cpv_quant_act(ctx, L.gate->type, s->xn, T, E, s->actbuf, &act)))
+            return st;
+        if ((st = cpv_qgemm_act(ctx, L.gate, &act, s->gt))) return st;
+        swiglu_kernel<<<grid_for(T * F), 256, 0, ctx->stream>>>(s->gt, s->up, F, F, s->act, T * F);
+    }
     if ((st = cpv_quant_act(ctx, L.down->type, s->act, T, F, s->actbuf, &act))) return st;
     if ((st = cpv_qgemm_act(ctx, L.down, &act, s->d))) return st;
     add_kernel<<<grid_for(T * E), 256, 0, ctx->stream>>>(s->d, x, x, T * E);

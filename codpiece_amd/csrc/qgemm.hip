@@ -14,24 +14,28 @@
 //    are summed in binary64, exactly because the window g keeps every partial
 //    sum below 2^53.  Any split of the K loop gives the same bits.
 //
-// Mapping.  A workgroup owns 16 weight rows and all of K.  Lane = r + 16 q of
-// a wave handles row r and unit q of each pass of 4 units; the waves of the
-// group take passes round-robin.  Activation codes for all of K are staged in
-// LDS once per group; the 16 lanes of a q share every LDS read (broadcast).
-// Weights come in through 128-bit loads that are contiguous per wave (see the
-// repack in api.hip).  Partial sums reduce across q with shuffles and across
-// waves through LDS, then one rounding to f32 per output.
+// Mapping.  Weights are repacked in tiles of 64 rows: a wave works on one
+// tile at a time, lane = row, and reads each 256-element unit of its row as
+// 16-byte pieces, so every load instruction of the wave is one contiguous
+// KiB (api.hip).  The integer dots run on the 16-block 4x4x4 int8 MFMA:
+// block b of lanes 4b..4b+3 multiplies 4 activation rows (A, from LDS) by the
+// 4 weight rows of its lanes (B), so each lane receives the dots of its own
+// row with 4 activation rows; a launch takes up to 8 rows (2 row groups).  The
+// per-unit scale work and the binary64 rounding then run lane-locally, with
+// no cross-lane traffic.  The grid is persistent (one workgroup per CU) and
+// the (tile, unit) items are dealt out to waves in consecutive runs, so K is
+// split wherever a run starts or ends: the partial sums are exact integers
+// below 2^53 and add in any order, through f64 atomics into an accumulator
+// that a small finalize kernel turns into y and leaves zeroed for the next
+// launch (no device-scope fence in the GEMM: on gfx950 one would write back a
+// whole L2 per workgroup).
 #include <math.h>
 
 #include "cpv_internal.h"
 
 namespace {
 
-constexpr int UNIT_STRIDE = 272;   // LDS bytes per 256 codes (+16 breaks bank aliasing)
-
 __device__ __forceinline__ float h2f(uint32_t h) { return cpv_h2f((uint16_t)h); }
-
-__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 __device__ __forceinline__ int byte_of(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xffu); }
 
@@ -100,223 +104,346 @@ __global__ __launch_bounds__(256) void quant_q80_kernel(const float* __restrict_
 }
 
 // ---------------------------------------------------------------- GEMM
-struct GemmArgs {
-    const uint8_t* w;      // repacked weight
-    const int32_t* ew;     // [n_pad] row exponents
-    const int8_t* qa;      // [M][Kp] codes
-    const float* da;       // [M][U] (K-quants) or [M][U*8] (Q8_0)
-    const int32_t* bs;     // [M][U*8] (Q4_K) or [M][U*16] (Q6_K)
-    float* y;              // [M][N]
-    int64_t N, n_pad;
-    int P, U, M, m0, Mtot, win;
-};
+typedef int v4i __attribute__((ext_vector_type(4)));
 
 template <int TYPE>
-struct Layout {
-    static constexpr int PIECES = TYPE == CPV_Q4_K ? 8 : TYPE == CPV_Q6_K ? 13 : 16;
-    static constexpr int DA_PER_UNIT = TYPE == CPV_Q8_0 ? 8 : 1;
-    static constexpr int BS_PER_UNIT = TYPE == CPV_Q4_K ? 8 : TYPE == CPV_Q6_K ? 16 : 0;
+struct Fmt {
+    // 16-byte pieces per (row, unit) in the repacked tile, activation scales
+    // per unit, activation code sums per unit
+    static constexpr int PIECES = TYPE == CPV_Q4_K ? 9 : TYPE == CPV_Q6_K ? 13 : 17;
+    static constexpr int DA = TYPE == CPV_Q8_0 ? 8 : 1;
+    static constexpr int BS = TYPE == CPV_Q4_K ? 8 : TYPE == CPV_Q6_K ? 16 : 0;
 };
 
-template <int TYPE, int MT>
-__host__ __device__ inline size_t gemm_lds_bytes(int U, int W)
+struct GemmArgs {
+    const uint8_t* w;      // repacked weight: [tile][unit][piece][lane][16 B] (+ Q6_K d region)
+    const int32_t* ew;     // [n_pad] row exponents
+    const int8_t* qa;      // [Mtot][U*256] activation codes
+    const float* da;       // [Mtot][U*DA]
+    const int32_t* bs;     // [Mtot][U*BS]
+    double* gsum;          // [16][n_pad] accumulator, zero between launches
+    int64_t n_pad;
+    int64_t items;         // tiles * U (tile-major)
+    int U, M, m0, win, chunk;   // chunk: consecutive items per wave
+};
+
+constexpr int GEMM_WAVES = 8;   // waves per workgroup (one workgroup per CU)
+
+__device__ __forceinline__ v4i mfma4(int a, int b, v4i c)
 {
-    using L = Layout<TYPE>;
-    return (size_t)MT * U * UNIT_STRIDE + (size_t)MT * U * L::DA_PER_UNIT * 8 +
-           (size_t)MT * U * L::BS_PER_UNIT * 4 + (size_t)W * 16 * MT * 8;
+    return __builtin_amdgcn_mfma_i32_4x4x4i8(a, b, c, 0, 0, 0);
 }
 
-template <int TYPE, int MT>
-__global__ __launch_bounds__(512) void qgemm_kernel(GemmArgs a)
+// LDS bytes of one workgroup: all M x U activation units, their scales and sums
+template <int TYPE>
+__host__ __device__ inline size_t gemm_lds(int M, int U)
 {
-    using L = Layout<TYPE>;
+    using F = Fmt<TYPE>;
+    const size_t codes = (size_t)M * ((size_t)U * 256 + 16);
+    const size_t da = (size_t)M * U * F::DA * 4;
+    const size_t bs = (size_t)M * U * F::BS * 4;
+    return ((codes + 15) & ~(size_t)15) + ((da + 15) & ~(size_t)15) + bs;
+}
+
+// One (tile, unit) item: the unit's integer dots for all MC rows and its
+// binary64 terms, added to S.  pcu: the lane's pieces of the unit.
+template <int TYPE, int MC>
+__device__ __forceinline__ void gemm_unit(const v4i* pcu, uint16_t d6, int er, int u, int M, int U,
+                                          const uint8_t* const* arow, const int* mrow, const double* sm,
+                                          const float* s_da, const int32_t* s_bs, double* S)
+{
+    constexpr int RG = (MC + 3) / 4;
+    using F = Fmt<TYPE>;
+    if constexpr (TYPE == CPV_Q4_K) {
+        const uint32_t h0 = (uint32_t)pcu[8][0], hy = (uint32_t)pcu[8][1], hz = (uint32_t)pcu[8][2],
+                       hw = (uint32_t)pcu[8][3];
+        const double dws = ldexp((double)h2f(h0 & 0xffffu), -er);
+        const double dms = ldexp((double)h2f(h0 >> 16), -er);
+        const uint32_t sc_lo = hy & 0x3f3f3f3fu, mn_lo = hz & 0x3f3f3f3fu;
+        const uint32_t sc_hi = (hw & 0x0f0f0f0fu) | (((hy >> 6) & 0x03030303u) << 4);
+        const uint32_t mn_hi = ((hw >> 4) & 0x0f0f0f0fu) | (((hz >> 6) & 0x03030303u) << 4);
+        int isum[MC], imin[MC];
+#pragma unroll
+        for (int m = 0; m < MC; m++) {
+            // imin = sum_j m_j * (code sum of sub-block j); 6-bit mins times |sums| <= 32*127
+            const v4i b0 = *(const v4i*)(s_bs + (mrow[m] * U + u) * 8);
+            const v4i b1 = *(const v4i*)(s_bs + (mrow[m] * U + u) * 8 + 4);
+            imin[m] = __mul24(byte_of(mn_lo, 0), b0[0]) + __mul24(byte_of(mn_lo, 1), b0[1]) +
+                      __mul24(byte_of(mn_lo, 2), b0[2]) + __mul24(byte_of(mn_lo, 3), b0[3]) +
+                      __mul24(byte_of(mn_hi, 0), b1[0]) + __mul24(byte_of(mn_hi, 1), b1[1]) +
+                      __mul24(byte_of(mn_hi, 2), b1[2]) + __mul24(byte_of(mn_hi, 3), b1[3]);
+            isum[m] = 0;
+        }
+#pragma unroll
+        for (int pr = 0; pr < 4; pr++) {
+            // sub-blocks 2pr (low nibbles) and 2pr+1 (high nibbles) of qs dwords 8pr..8pr+7: two chains
+            v4i De[RG], Do[RG];
+#pragma unroll
+            for (int r = 0; r < RG; r++) { De[r] = v4i{0, 0, 0, 0}; Do[r] = v4i{0, 0, 0, 0}; }
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                v4i Ae[RG], Ao[RG];
+#pragma unroll
+                for (int r = 0; r < RG; r++) {
+                    Ae[r] = *(const v4i*)(arow[r] + u * 256 + pr * 64 + h * 16);
+                    Ao[r] = *(const v4i*)(arow[r] + u * 256 + pr * 64 + 32 + h * 16);
+                }
+#pragma unroll
+                for (int d = 0; d < 4; d++) {
+                    const uint32_t wv = (uint32_t)pcu[pr * 2 + h][d];
+                    const int be = (int)(wv & 0x0f0f0f0fu), bo = (int)((wv >> 4) & 0x0f0f0f0fu);
+#pragma unroll
+                    for (int r = 0; r < RG; r++) {
+                        De[r] = mfma4(Ae[r][d], be, De[r]);
+                        Do[r] = mfma4(Ao[r][d], bo, Do[r]);
+                    }
+                }
+            }
+            const uint32_t scw = pr < 2 ? sc_lo : sc_hi;
+            const int sce = byte_of(scw, (2 * pr) & 3), sco = byte_of(scw, (2 * pr + 1) & 3);
+#pragma unroll
+            for (int m = 0; m < MC; m++)   // 6-bit scales times |dots| <= 32*15*127: 24-bit products
+                isum[m] += __mul24(sce, De[m >> 2][m & 3]) + __mul24(sco, Do[m >> 2][m & 3]);
+        }
+#pragma unroll
+        for (int m = 0; m < MC; m++) {
+            const double da = (double)s_da[mrow[m] * U + u] * sm[m];
+            S[m] += rint(dws * da * (double)isum[m]) - rint(dms * da * (double)imin[m]);
+        }
+    } else if constexpr (TYPE == CPV_Q6_K) {
+        const double dws = ldexp((double)h2f(d6), -er);
+        int isum[MC];
+#pragma unroll
+        for (int m = 0; m < MC; m++) isum[m] = 0;
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++) {
+#pragma unroll
+            for (int quad = 0; quad < 4; quad++) {
+                // 32 elements hf*128 + quad*32 ..: groups g0 = 2(hf*4 + quad) and g0 + 1, two chains
+                const int g0 = (hf * 4 + quad) * 2;
+                v4i A0[RG], A1[RG], D0[RG], D1[RG];
+#pragma unroll
+                for (int r = 0; r < RG; r++) {
+                    A0[r] = *(const v4i*)(arow[r] + u * 256 + g0 * 16);
+                    A1[r] = *(const v4i*)(arow[r] + u * 256 + g0 * 16 + 16);
+                    D0[r] = v4i{0, 0, 0, 0};
+                    D1[r] = v4i{0, 0, 0, 0};
+                }
+#pragma unroll
+                for (int d = 0; d < 4; d++) {
+                    const uint32_t l0 = (uint32_t)pcu[hf * 4 + (quad & 1) * 2][d];
+                    const uint32_t l1 = (uint32_t)pcu[hf * 4 + (quad & 1) * 2 + 1][d];
+                    const uint32_t q0 = (uint32_t)pcu[8 + hf * 2][d], q1 = (uint32_t)pcu[8 + hf * 2 + 1][d];
+                    const uint32_t lo0 = quad < 2 ? (l0 & 0x0f0f0f0fu) : ((l0 >> 4) & 0x0f0f0f0fu);
+                    const uint32_t lo1 = quad < 2 ? (l1 & 0x0f0f0f0fu) : ((l1 >> 4) & 0x0f0f0f0fu);
+                    const int b0 = (int)(lo0 | (((q0 >> (2 * quad)) & 0x03030303u) << 4));
+                    const int b1 = (int)(lo1 | (((q1 >> (2 * quad)) & 0x03030303u) << 4));
+#pragma unroll
+                    for (int r = 0; r < RG; r++) {
+                        D0[r] = mfma4(A0[r][d], b0, D0[r]);
+                        D1[r] = mfma4(A1[r][d], b1, D1[r]);
+                    }
+                }
+                const int sc0 = (int)(int8_t)byte_of((uint32_t)pcu[12][g0 >> 2], g0 & 3);
+                const int sc1 = (int)(int8_t)byte_of((uint32_t)pcu[12][(g0 + 1) >> 2], (g0 + 1) & 3);
+#pragma unroll
+                for (int m = 0; m < MC; m++) {
+                    // int8 scales times |dot - 32 * code sum| < 2^18: 24-bit products
+                    const int32_t* bs = s_bs + (mrow[m] * U + u) * 16 + g0;
+                    isum[m] += __mul24(sc0, D0[m >> 2][m & 3] - 32 * bs[0]) +
+                               __mul24(sc1, D1[m >> 2][m & 3] - 32 * bs[1]);
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MC; m++) S[m] += rint(dws * ((double)s_da[mrow[m] * U + u] * sm[m]) * (double)isum[m]);
+    } else {
+        const uint32_t dw[4] = {(uint32_t)pcu[16][0], (uint32_t)pcu[16][1], (uint32_t)pcu[16][2],
+                                (uint32_t)pcu[16][3]};
+#pragma unroll
+        for (int b2 = 0; b2 < 4; b2++) {
+            // blocks 2 b2 and 2 b2 + 1: two chains
+            v4i D0[RG], D1[RG];
+#pragma unroll
+            for (int r = 0; r < RG; r++) { D0[r] = v4i{0, 0, 0, 0}; D1[r] = v4i{0, 0, 0, 0}; }
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                v4i A0[RG], A1[RG];
+#pragma unroll
+                for (int r = 0; r < RG; r++) {
+                    A0[r] = *(const v4i*)(arow[r] + u * 256 + b2 * 64 + h * 16);
+                    A1[r] = *(const v4i*)(arow[r] + u * 256 + b2 * 64 + 32 + h * 16);
+                }
+#pragma unroll
+                for (int d = 0; d < 4; d++)
+#pragma unroll
+                    for (int r = 0; r < RG; r++) {
+                        D0[r] = mfma4(A0[r][d], pcu[b2 * 4 + h][d], D0[r]);
+                        D1[r] = mfma4(A1[r][d], pcu[b2 * 4 + 2 + h][d], D1[r]);
+                    }
+            }
+            const double dw0 = ldexp((double)h2f(dw[b2] & 0xffffu), -er);
+            const double dw1 = ldexp((double)h2f(dw[b2] >> 16), -er);
+#pragma unroll
+            for (int m = 0; m < MC; m++) {
+                const float* dam = s_da + (mrow[m] * U + u) * 8 + 2 * b2;
+                S[m] += rint(dw0 * ((double)dam[0] * sm[m]) * (double)D0[m >> 2][m & 3]) +
+                        rint(dw1 * ((double)dam[1] * sm[m]) * (double)D1[m >> 2][m & 3]);
+            }
+        }
+    }
+    (void)M;
+}
+
+// Persistent streaming GEMM: one workgroup of GEMM_WAVES waves per CU stages
+// every activation unit in LDS once; then each wave walks its own run of
+// `chunk` consecutive (tile, unit) items with the next item's weights in
+// flight while it computes the current one, keeps the partial sums of its
+// current tile in registers, and adds them to the accumulator (f64 atomics,
+// exact) whenever the tile changes and at the end.  No barrier after staging.
+// MC: a compile-time bound on the activation rows (rows M..MC-1 repeat row
+// M-1 and are never stored), so every loop over rows unrolls without branches.
+template <int TYPE, int MC>
+__global__ __launch_bounds__(64 * GEMM_WAVES) void qgemm_kernel(GemmArgs a)
+{
+    using F = Fmt<TYPE>;
+    constexpr int RG = (MC + 3) / 4;           // 4-row groups of the MFMA
+    constexpr int NT = 64 * GEMM_WAVES;
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ int s_ea[MT];
-    const int U = a.U, P = a.P, M = a.M;
-    const int tid = threadIdx.x, nthr = blockDim.x, W = nthr >> 6;
-    uint8_t* s_qa = smem;
-    double* s_da = (double*)(smem + (size_t)MT * U * UNIT_STRIDE);
-    int32_t* s_bs = (int32_t*)(s_da + (size_t)MT * U * L::DA_PER_UNIT);
-    double* s_red = (double*)(s_bs + (size_t)MT * U * L::BS_PER_UNIT);
+    __shared__ int s_ea[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int M = a.M, U = a.U;
+    const int cstride = U * 256 + 16;          // LDS bytes per activation row (+16: 4 rows, 4 bank groups)
+    uint8_t* s_codes = smem;
+    float* s_da = (float*)(smem + ((M * cstride + 15) & ~15));
+    int32_t* s_bs = (int32_t*)((uint8_t*)s_da + ((M * U * F::DA * 4 + 15) & ~15));
     const int64_t Kp = (int64_t)U * 256;
 
-    // stage codes (16 B at a time) and code sums
-    for (int i = tid; i < M * U * 16; i += nthr) {
-        const int m = i / (U * 16), rest = i % (U * 16), u = rest >> 4, c = rest & 15;
-        const uint4 v = *(const uint4*)(a.qa + (int64_t)(a.m0 + m) * Kp + (int64_t)u * 256 + c * 16);
-        *(uint4*)(s_qa + ((size_t)m * U + u) * UNIT_STRIDE + c * 16) = v;
+    // this wave's items
+    const int64_t i0 = ((int64_t)blockIdx.x * GEMM_WAVES + wave) * a.chunk;
+    const int64_t i1 = i0 + a.chunk < a.items ? i0 + a.chunk : a.items;
+    const uint16_t* d6base = (const uint16_t*)(a.w + (a.n_pad / 64) * (int64_t)U * 13 * 1024);
+    auto load = [&](int64_t it, v4i* pcu, uint16_t& d6, int& er) {
+        const int64_t tile = it / U;
+        const v4i* src = (const v4i*)(a.w + it * F::PIECES * 1024 + lane * 16);
+#pragma unroll
+        for (int p = 0; p < F::PIECES; p++) pcu[p] = src[p * 64];
+        if (TYPE == CPV_Q6_K) d6 = d6base[it * 64 + lane];
+        er = a.ew[tile * 64 + lane];
+    };
+    v4i bufA[F::PIECES], bufB[F::PIECES];
+    uint16_t dA = 0, dB = 0;
+    int eA = 0, eB = 0;
+    // two items in flight before the staging below
+    if (i0 < i1) load(i0, bufA, dA, eA);
+    if (i0 + 1 < i1) load(i0 + 1, bufB, dB, eB);
+
+    // ---- stage every activation unit, its scale and code sums; Ea(m) over the row
+    for (int i = tid; i < M * U * 16; i += NT) {
+        const int m = i / (U * 16), c = i - m * (U * 16);
+        const v4i v = *(const v4i*)(a.qa + (int64_t)(a.m0 + m) * Kp + c * 16);
+        *(v4i*)(s_codes + m * cstride + c * 16) = v;
     }
-    if (L::BS_PER_UNIT)
-        for (int i = tid; i < M * U * L::BS_PER_UNIT; i += nthr)
-            s_bs[i] = a.bs[(int64_t)a.m0 * U * L::BS_PER_UNIT + i];
-    // Ea(m): exponent of the row's largest activation scale
-    if (tid < 64) {
-        for (int m = 0; m < M; m++) {
-            float mx = 0.0f;
-            for (int i = tid; i < U * L::DA_PER_UNIT; i += 64)
-                mx = fmaxf(mx, fabsf(a.da[(int64_t)(a.m0 + m) * U * L::DA_PER_UNIT + i]));
-            for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-            if (tid == 0) {
-                int e = CPV_E_EMPTY;
-                if (mx > 0.0f) frexpf(mx, &e);
-                s_ea[m] = e;
-            }
+    for (int i = tid; i < M * U * F::DA; i += NT) s_da[i] = a.da[(int64_t)a.m0 * U * F::DA + i];
+    if (F::BS)
+        for (int i = tid; i < M * U * F::BS; i += NT) s_bs[i] = a.bs[(int64_t)a.m0 * U * F::BS + i];
+    for (int m = wave; m < M; m += GEMM_WAVES) {
+        float mx = 0.0f;
+        for (int i = lane; i < U * F::DA; i += 64) mx = fmaxf(mx, fabsf(a.da[(int64_t)(a.m0 + m) * U * F::DA + i]));
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        if (lane == 0) {
+            int e = CPV_E_EMPTY;
+            if (mx > 0.0f) frexpf(mx, &e);
+            s_ea[m] = e;
         }
     }
     __syncthreads();
-    // activation scales pre-multiplied by 2^(win - Ea(m)) (exact)
-    for (int i = tid; i < M * U * L::DA_PER_UNIT; i += nthr) {
-        const int m = i / (U * L::DA_PER_UNIT);
-        const int e = s_ea[m];
-        const double v = (double)a.da[(int64_t)a.m0 * U * L::DA_PER_UNIT + i];
-        s_da[i] = e == CPV_E_EMPTY ? 0.0 : ldexp(v, a.win - e);
+    if (i0 >= i1) return;
+
+    // per row: the MFMA feed of this lane (row group r takes row 4r + lane%4) and 2^(win - Ea)
+    const uint8_t* arow[RG];
+#pragma unroll
+    for (int r = 0; r < RG; r++) {
+        const int m = 4 * r + (lane & 3);
+        arow[r] = s_codes + (m < M ? m : M - 1) * cstride;
     }
-    __syncthreads();
+    int mrow[MC];
+    double sm[MC];
+#pragma unroll
+    for (int m = 0; m < MC; m++) {
+        mrow[m] = m < M ? m : M - 1;
+        const int e = s_ea[mrow[m]];
+        sm[m] = e == CPV_E_EMPTY ? 0.0 : ldexp(1.0, a.win - e);
+    }
 
-    const int wave = tid >> 6, lane = tid & 63, r = lane & 15, q = lane >> 4;
-    const int64_t g = blockIdx.x;
-    const int er = a.ew[g * 16 + r];
-    const uint4* wq = (const uint4*)a.w;
-    const int64_t groups = a.n_pad / 16;
-    const int64_t region_a = groups * P * L::PIECES * 64;      // in uint4
-
-    double acc[MT];
+    double S[MC];
 #pragma unroll
-    for (int m = 0; m < MT; m++) acc[m] = 0.0;
-
-    for (int p = wave; p < P; p += W) {
-        const int u = p * 4 + q;
-        const uint4* src = wq + (g * P + p) * L::PIECES * 64 + lane;
-        uint4 pc[L::PIECES];
+    for (int m = 0; m < MC; m++) S[m] = 0.0;
+    int64_t tile = i0 / U;
+    auto flush = [&]() {
+        // partial sums of this tile's units: exact, so the order of the adds does not matter
 #pragma unroll
-        for (int i = 0; i < L::PIECES; i++) pc[i] = src[i * 64];
-
-        if constexpr (TYPE == CPV_Q4_K) {
-            const uint4 meta = wq[region_a + (g * P + p) * 64 + lane];
-            const double dws = ldexp((double)h2f(meta.x & 0xffffu), -er);
-            const double dms = ldexp((double)h2f(meta.x >> 16), -er);
-            const uint32_t sc_lo = meta.y & 0x3f3f3f3fu, mn_lo = meta.z & 0x3f3f3f3fu;
-            const uint32_t sc_hi = (meta.w & 0x0f0f0f0fu) | (((meta.y >> 6) & 0x03030303u) << 4);
-            const uint32_t mn_hi = ((meta.w >> 4) & 0x0f0f0f0fu) | (((meta.z >> 6) & 0x03030303u) << 4);
-            const uint32_t* nw = (const uint32_t*)pc;     // 32 dwords, chunk c = dwords 8c..8c+7
-#pragma unroll
-            for (int m = 0; m < MT; m++) {
-                if (m < M) {
-                    const int* av = (const int*)(s_qa + ((size_t)m * U + u) * UNIT_STRIDE);
-                    int isum = 0, imin = 0;
-#pragma unroll
-                    for (int c = 0; c < 4; c++) {
-                        int dlo = 0, dhi = 0;
-#pragma unroll
-                        for (int dd = 0; dd < 8; dd++) {
-                            const uint32_t wv = nw[c * 8 + dd];
-                            dlo = sdot4((int)(wv & 0x0f0f0f0fu), av[c * 16 + dd], dlo);
-                            dhi = sdot4((int)((wv >> 4) & 0x0f0f0f0fu), av[c * 16 + 8 + dd], dhi);
-                        }
-                        const uint32_t scw = c < 2 ? sc_lo : sc_hi, mnw = c < 2 ? mn_lo : mn_hi;
-                        const int j0 = (2 * c) & 3, j1 = (2 * c + 1) & 3;
-                        isum += byte_of(scw, j0) * dlo + byte_of(scw, j1) * dhi;
-                        const int32_t* bsu = s_bs + ((size_t)m * U + u) * 8;
-                        imin += byte_of(mnw, j0) * bsu[2 * c] + byte_of(mnw, j1) * bsu[2 * c + 1];
-                    }
-                    const double das = s_da[(size_t)m * U + u];
-                    acc[m] += rint(dws * das * (double)isum) - rint(dms * das * (double)imin);
-                }
+        for (int m = 0; m < MC; m++)
+            if (m < M) {
+                unsafeAtomicAdd(&a.gsum[(int64_t)m * a.n_pad + tile * 64 + lane], S[m]);
+                S[m] = 0.0;
             }
-        } else if constexpr (TYPE == CPV_Q6_K) {
-            const uint16_t dbits = *((const uint16_t*)(wq + region_a) + (g * P + p) * 64 + lane);
-            const double dws = ldexp((double)h2f(dbits), -er);
-            const uint32_t* ql = (const uint32_t*)pc;         // 32 dwords
-            const uint32_t* qh = ql + 32;                     // 16 dwords
-            const uint32_t* scw = ql + 48;                    // 4 dwords, 16 int8 scales
-            // unsigned 6-bit codes, element order, 64 dwords
-            uint32_t code[64];
-#pragma unroll
-            for (int h = 0; h < 2; h++)
-#pragma unroll
-                for (int dd = 0; dd < 8; dd++) {
-                    const uint32_t l0 = ql[h * 16 + dd], l1 = ql[h * 16 + 8 + dd], hb = qh[h * 8 + dd];
-                    code[h * 32 + 0 + dd] = (l0 & 0x0f0f0f0fu) | ((hb & 0x03030303u) << 4);
-                    code[h * 32 + 8 + dd] = (l1 & 0x0f0f0f0fu) | (((hb >> 2) & 0x03030303u) << 4);
-                    code[h * 32 + 16 + dd] = ((l0 >> 4) & 0x0f0f0f0fu) | (((hb >> 4) & 0x03030303u) << 4);
-                    code[h * 32 + 24 + dd] = ((l1 >> 4) & 0x0f0f0f0fu) | (((hb >> 6) & 0x03030303u) << 4);
-                }
-#pragma unroll
-            for (int m = 0; m < MT; m++) {
-                if (m < M) {
-                    const int* av = (const int*)(s_qa + ((size_t)m * U + u) * UNIT_STRIDE);
-                    const int32_t* bsu = s_bs + ((size_t)m * U + u) * 16;
-                    int isum = 0;
-#pragma unroll
-                    for (int gi = 0; gi < 16; gi++) {
-                        int dg = 0;
-#pragma unroll
-                        for (int dd = 0; dd < 4; dd++) dg = sdot4((int)code[gi * 4 + dd], av[gi * 4 + dd], dg);
-                        const int sc = (int)(int8_t)byte_of(scw[gi >> 2], gi & 3);
-                        isum += sc * (dg - 32 * bsu[gi]);
-                    }
-                    acc[m] += rint(dws * s_da[(size_t)m * U + u] * (double)isum);
-                }
-            }
-        } else {
-            const uint4 dq = wq[region_a + (g * P + p) * 64 + lane];
-            const uint32_t dw4[4] = {dq.x, dq.y, dq.z, dq.w};
-            const uint32_t* qs = (const uint32_t*)pc;         // 64 dwords, block b = 8b..8b+7
-#pragma unroll
-            for (int m = 0; m < MT; m++) {
-                if (m < M) {
-                    const int* av = (const int*)(s_qa + ((size_t)m * U + u) * UNIT_STRIDE);
-                    const double* das = s_da + ((size_t)m * U + u) * 8;
-#pragma unroll
-                    for (int b = 0; b < 8; b++) {
-                        int isum = 0;
-#pragma unroll
-                        for (int dd = 0; dd < 8; dd++) isum = sdot4((int)qs[b * 8 + dd], av[b * 8 + dd], isum);
-                        const uint32_t hb = (dw4[b >> 1] >> (16 * (b & 1))) & 0xffffu;
-                        const double dws = ldexp((double)h2f(hb), -er);
-                        acc[m] += rint(dws * das[b] * (double)isum);
-                    }
-                }
-            }
-        }
+    };
+    for (int64_t it = i0; it < i1; it += 2) {
+        if (it > i0 && it + 1 < i1) load(it + 1, bufB, dB, eB);
+        if (it / U != tile) { flush(); tile = it / U; }
+        gemm_unit<TYPE, MC>(bufA, dA, eA, (int)(it % U), M, U, arow, mrow, sm, s_da, s_bs, S);
+        if (it + 1 >= i1) break;
+        if (it + 2 < i1) load(it + 2, bufA, dA, eA);
+        if ((it + 1) / U != tile) { flush(); tile = (it + 1) / U; }
+        gemm_unit<TYPE, MC>(bufB, dB, eB, (int)((it + 1) % U), M, U, arow, mrow, sm, s_da, s_bs, S);
     }
-
-    // exact reduction: over the 4 units of a row, then over waves
-#pragma unroll
-    for (int m = 0; m < MT; m++) {
-        acc[m] += __shfl_xor(acc[m], 16);
-        acc[m] += __shfl_xor(acc[m], 32);
-    }
-    if (q == 0)
-#pragma unroll
-        for (int m = 0; m < MT; m++) s_red[((size_t)wave * 16 + r) * MT + m] = acc[m];
-    __syncthreads();
-    for (int t = tid; t < 16 * M; t += nthr) {
-        const int rr = t & 15, m = t >> 4;
-        const int64_t row = g * 16 + rr;
-        if (row >= a.N) continue;
-        double s = 0.0;
-        for (int w = 0; w < W; w++) s += s_red[((size_t)w * 16 + rr) * MT + m];
-        const int ew = a.ew[row], ea = s_ea[m];
-        float out = 0.0f;
-        if (ew != CPV_E_EMPTY && ea != CPV_E_EMPTY) out = (float)ldexp(s, ew + ea - a.win);
-        a.y[(int64_t)(a.m0 + m) * a.N + row] = out;
-    }
+    flush();
 }
 
-// one launch of the GEMM; k and wbytes (the weight's row length and bytes)
-// only feed the kernel timing
-template <int TYPE, int MT>
-cpv_status launch_mt(cpv_ctx* ctx, GemmArgs a, int W, int64_t k, double wbytes)
+// y = the accumulated split-K sums scaled by 2^(Ew + Ea - win); leaves the
+// accumulator zero.  One block per 256 outputs of one activation row; Ea(m)
+// is recomputed from the row's scales.
+__global__ __launch_bounds__(256) void qgemm_finalize_kernel(double* __restrict__ gsum, int64_t n_pad,
+                                                             const int32_t* __restrict__ ew,
+                                                             const float* __restrict__ da, int nda, int m0,
+                                                             int win, float* __restrict__ y, int64_t N)
 {
-    const size_t lds = gemm_lds_bytes<TYPE, MT>(a.U, W);
-    auto go = [=]() { qgemm_kernel<TYPE, MT><<<(unsigned)(a.n_pad / 16), W * 64, lds, ctx->stream>>>(a); };
+    const int m = blockIdx.y, tid = threadIdx.x;
+    __shared__ float s_mx[4];
+    float mx = 0.0f;
+    for (int i = tid; i < nda; i += 256) mx = fmaxf(mx, fabsf(da[(int64_t)(m0 + m) * nda + i]));
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if ((tid & 63) == 0) s_mx[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(s_mx[0], s_mx[1]), fmaxf(s_mx[2], s_mx[3]));
+    int ea = CPV_E_EMPTY;
+    if (mx > 0.0f) frexpf(mx, &ea);
+    const int64_t n = (int64_t)blockIdx.x * 256 + tid;
+    if (n >= N) return;
+    double* g = gsum + (int64_t)m * n_pad + n;
+    const double tot = *g;
+    *g = 0.0;
+    const int e = ew[n];
+    y[(int64_t)(m0 + m) * N + n] = (e == CPV_E_EMPTY || ea == CPV_E_EMPTY) ? 0.0f : (float)ldexp(tot, e + ea - win);
+}
+
+template <int TYPE, int MC>
+cpv_status launch_mc(cpv_ctx* ctx, const GemmArgs& a, float* y, int64_t N, int64_t k, double wbytes)
+{
+    const size_t lds = gemm_lds<TYPE>(a.M, a.U);
+    const unsigned grid = (unsigned)ctx->cu_count;
+    auto go = [=]() {
+        qgemm_kernel<TYPE, MC><<<grid, 64 * GEMM_WAVES, lds, ctx->stream>>>(a);
+        qgemm_finalize_kernel<<<dim3((unsigned)((N + 255) / 256), (unsigned)a.M), 256, 0, ctx->stream>>>(
+            a.gsum, a.n_pad, a.ew, a.da, a.U * Fmt<TYPE>::DA, a.m0, a.win, y, N);
+    };
     const int ev = cpv_prof_mark(ctx);
     go();
     CPV_HIP(ctx, hipGetLastError());
     if (ev >= 0) {  // algorithmic bytes: the weight, f32 activations in, f32 outputs
         const int cls = TYPE == CPV_Q4_K ? CPV_PROF_Q4_K : TYPE == CPV_Q6_K ? CPV_PROF_Q6_K : CPV_PROF_Q8_0;
-        const double bytes = wbytes + 4.0 * a.M * (double)k + 4.0 * a.M * (double)a.N;
+        const double bytes = wbytes + 4.0 * a.M * (double)k + 4.0 * a.M * (double)N;
         cpv_prof_add(ctx, ev, cls, bytes);
         cpv_prof_keep(ctx, cls, bytes, go);
     }
@@ -324,29 +451,39 @@ cpv_status launch_mt(cpv_ctx* ctx, GemmArgs a, int W, int64_t k, double wbytes)
 }
 
 template <int TYPE>
-cpv_status launch_type(cpv_ctx* ctx, GemmArgs a, int W, int64_t k, double wbytes)
+cpv_status launch_type(cpv_ctx* ctx, const GemmArgs& a, float* y, int64_t N, int64_t k, double wbytes)
 {
-    // the register tile MT is the smallest instantiated size >= M
-    if (a.M <= 1) return launch_mt<TYPE, 1>(ctx, a, W, k, wbytes);
-    if (a.M <= 2) return launch_mt<TYPE, 2>(ctx, a, W, k, wbytes);
-    if (a.M <= 4) return launch_mt<TYPE, 4>(ctx, a, W, k, wbytes);
-    if (a.M <= 5) return launch_mt<TYPE, 5>(ctx, a, W, k, wbytes);
-    if (a.M <= 8) return launch_mt<TYPE, 8>(ctx, a, W, k, wbytes);
-    return launch_mt<TYPE, 16>(ctx, a, W, k, wbytes);
+    // the smallest instantiated row bound >= M
+    if (a.M <= 1) return launch_mc<TYPE, 1>(ctx, a, y, N, k, wbytes);
+    if (a.M <= 2) return launch_mc<TYPE, 2>(ctx, a, y, N, k, wbytes);
+    if (a.M <= 4) return launch_mc<TYPE, 4>(ctx, a, y, N, k, wbytes);
+    if (a.M <= 5) return launch_mc<TYPE, 5>(ctx, a, y, N, k, wbytes);
+    return launch_mc<TYPE, 8>(ctx, a, y, N, k, wbytes);
 }
 
 template <int TYPE>
-size_t lds_for(int M, int U, int W)
-{
-    if (M <= 1) return gemm_lds_bytes<TYPE, 1>(U, W);
-    if (M <= 2) return gemm_lds_bytes<TYPE, 2>(U, W);
-    if (M <= 4) return gemm_lds_bytes<TYPE, 4>(U, W);
-    if (M <= 5) return gemm_lds_bytes<TYPE, 5>(U, W);
-    if (M <= 8) return gemm_lds_bytes<TYPE, 8>(U, W);
-    return gemm_lds_bytes<TYPE, 16>(U, W);
-}
+size_t lds_of(int M, int U) { return gemm_lds<TYPE>(M, U); }
 
 static int isum_bits(int type) { return type == CPV_Q8_0 ? 20 : type == CPV_Q4_K ? 25 : 28; }
+
+// the cross-group accumulator: zeroed once when (re)allocated, left zero by every finalize
+static cpv_status gemm_accumulator(cpv_ctx* ctx, int64_t n_pad, double** gsum)
+{
+    const size_t need = (size_t)16 * n_pad * sizeof(double);
+    if (need > ctx->gsum_bytes) {
+        CPV_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (ctx->gsum) (void)hipFree(ctx->gsum);
+        ctx->gsum = nullptr;
+        ctx->gsum_bytes = 0;
+        const size_t bs = need > ((size_t)16 << 20) ? need : ((size_t)16 << 20);
+        CPV_HIP(ctx, hipMalloc((void**)&ctx->gsum, bs));
+        CPV_HIP(ctx, hipMemsetAsync(ctx->gsum, 0, bs, ctx->stream));
+        ctx->gsum_bytes = bs;
+        ctx->ws_gen++;
+    }
+    *gsum = ctx->gsum;
+    return CPV_OK;
+}
 
 }  // namespace
 
@@ -358,9 +495,11 @@ int cpv_qgemm_window(int type, int64_t k)
     return 52 - isum_bits(type) - b;
 }
 
+static int act_units(int64_t k) { return (int)((k + 255) / 256); }
+
 size_t cpv_act_bytes(int type, int64_t k, int64_t m)
 {
-    const int64_t U = ((k + 255) / 256 + 3) / 4 * 4;
+    const int64_t U = act_units(k);
     const bool kq = type != CPV_Q8_0;
     const size_t qa_b = ((size_t)m * U * 256 + 255) & ~(size_t)255;
     const size_t da_b = ((size_t)m * U * (kq ? 1 : 8) * 4 + 255) & ~(size_t)255;
@@ -370,7 +509,7 @@ size_t cpv_act_bytes(int type, int64_t k, int64_t m)
 
 cpv_status cpv_quant_act(cpv_ctx* ctx, int type, const float* x, int64_t m, int64_t k, void* buf, cpv_act* out)
 {
-    const int U = (int)(((k + 255) / 256 + 3) / 4 * 4);
+    const int U = act_units(k);
     const bool kq = type != CPV_Q8_0;
     const size_t qa_b = ((size_t)m * U * 256 + 255) & ~(size_t)255;
     const size_t da_b = ((size_t)m * U * (kq ? 1 : 8) * 4 + 255) & ~(size_t)255;
@@ -396,44 +535,46 @@ cpv_status cpv_quant_act(cpv_ctx* ctx, int type, const float* x, int64_t m, int6
 cpv_status cpv_qgemm_act(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, float* y)
 {
     const bool kq = w->type != CPV_Q8_0;
-    if (kq != act->kq || act->k != w->k || act->U != (int)(w->passes * 4))
+    if (kq != act->kq || act->k != w->k || act->U != (int)w->units)
         return cpv_fail(ctx, CPV_EINVAL, "qgemm: activation format does not match the weight");
     const int U = act->U;
     const int64_t m = act->m;
-    const int P = (int)w->passes;
-    const int per = (P + 7) / 8;
-    const int W = (P + per - 1) / per;
+    const int64_t tiles = w->n_pad / 64;
     GemmArgs a;
     a.w = (const uint8_t*)w->data;
     a.ew = w->ew;
     a.qa = act->qa;
     a.da = act->da;
     a.bs = w->type == CPV_Q4_K ? act->bs32 : act->bs16;
-    a.y = y;
-    a.N = w->n;
     a.n_pad = w->n_pad;
-    a.P = P;
     a.U = U;
-    a.Mtot = (int)m;
+    a.items = tiles * U;
     a.win = cpv_qgemm_window(w->type, w->k);
-    // activation rows per launch: as many as fit the workgroup's LDS
-    int chunk = m < 16 ? (int)m : 16;
-    auto lds = [&](int c) {
-        return w->type == CPV_Q4_K ? lds_for<CPV_Q4_K>(c, U, W)
-             : w->type == CPV_Q6_K ? lds_for<CPV_Q6_K>(c, U, W) : lds_for<CPV_Q8_0>(c, U, W);
+    {
+        // consecutive items per wave: all waves of one workgroup per CU
+        const int64_t waves = (int64_t)ctx->cu_count * GEMM_WAVES;
+        a.chunk = (int)((a.items + waves - 1) / waves);
+    }
+    cpv_status st = gemm_accumulator(ctx, w->n_pad, &a.gsum);
+    if (st != CPV_OK) return st;
+    const double wb = (double)w->n * (double)(w->k / cpv_type_block(w->type)) * (double)cpv_type_size(w->type);
+    auto lds = [&](int M) {
+        return w->type == CPV_Q4_K ? lds_of<CPV_Q4_K>(M, U) : w->type == CPV_Q6_K ? lds_of<CPV_Q6_K>(M, U)
+                                                                                 : lds_of<CPV_Q8_0>(M, U);
     };
-    const size_t lds_cap = ctx->lds_max - 1024;    // less the static shared words
-    while (chunk > 1 && lds(chunk) > lds_cap) chunk--;
-    if (lds(chunk) > lds_cap)
-        return cpv_fail(ctx, CPV_EUNSUPPORTED, "qgemm: k=%lld needs more LDS than a CU has", (long long)w->k);
-    for (int64_t m0 = 0; m0 < m; m0 += chunk) {
+    const size_t lds_cap = ctx->lds_max - 1024;
+    for (int64_t m0 = 0; m0 < m;) {
+        int M = (int)((m - m0) < 8 ? (m - m0) : 8);
+        while (M > 1 && lds(M) > lds_cap) M--;      // rows per launch: up to 8, as many as LDS holds
+        if (lds(M) > lds_cap)
+            return cpv_fail(ctx, CPV_EUNSUPPORTED, "qgemm: k=%lld needs more LDS than a CU has", (long long)w->k);
         a.m0 = (int)m0;
-        a.M = (int)((m - m0) < chunk ? (m - m0) : chunk);
-        const double wb = (double)w->n * (double)(w->k / cpv_type_block(w->type)) * (double)cpv_type_size(w->type);
-        cpv_status s2 = w->type == CPV_Q4_K ? launch_type<CPV_Q4_K>(ctx, a, W, w->k, wb)
-                      : w->type == CPV_Q6_K ? launch_type<CPV_Q6_K>(ctx, a, W, w->k, wb)
-                                            : launch_type<CPV_Q8_0>(ctx, a, W, w->k, wb);
+        a.M = M;
+        cpv_status s2 = w->type == CPV_Q4_K ? launch_type<CPV_Q4_K>(ctx, a, y, w->n, w->k, wb)
+                      : w->type == CPV_Q6_K ? launch_type<CPV_Q6_K>(ctx, a, y, w->n, w->k, wb)
+                                            : launch_type<CPV_Q8_0>(ctx, a, y, w->n, w->k, wb);
         if (s2 != CPV_OK) return s2;
+        m0 += M;
     }
     return CPV_OK;
 }
