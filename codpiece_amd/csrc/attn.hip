@@ -1,303 +1,358 @@
-// attn.hip — tree-masked GQA attention over the f16 KV cache (split-KV, MFMA).
+// attn.hip — tree-masked GQA attention over the f16 KV cache, exact and
+// order-free: the same bits whatever the grid, the split of the KV axis or
+// the number of query rows in a call.
 //
-// Replaces ggml_flash_attn_ext with prec F32 (crates/codpiece-model/src/
-// qwen35.rs:3182-3187): out = softmax(scale * q k^T + mask) v, where a query
-// node sees every context row and the rows of its ancestors and itself.
+// Replaces the attention of build_attn_block (crates/codpiece-model/src/
+// qwen35.rs:3182-3199): ggml_flash_attn_ext with prec F32 by default (the
+// session's fa flag, qwen35.rs:534), or mul_mat(k, q) -> soft_max_ext(scale,
+// mask) -> mul_mat(v, p).  Both ggml CPU paths round q to f16 (the f16
+// cache's vec_dot_type) and sum in an order set by the SIMD width (and the
+// FA kernel accumulates p.v in f16).  The contract here keeps the f16 q and
+// makes every sum exact or fixed-order (the oracle's cpvo_attn states it):
+//  1. scores: q16 and each cache row k16 become 15-bit fixed point relative
+//     to their own largest element (qf = rint(q16 2^(14-Eq)), kf likewise);
+//     s = (float)(sum_d qf kf * 2^(Eq+Ek-28)), the sum exact -- here on the
+//     int8 MFMA with two signed 8-bit limbs per operand.
+//  2. w = s * scale, mx = max over visible rows, e = expf(w - mx).
+//  3. Z = sum rint(e 2^G) exactly (G = 62 - ceil_log2(n_vis + 1)),
+//     inv = (float)(1 / (Z 2^-G)), p = f16(e * inv).
+//  4. per 256-row chunk of the cache (absolute rows) P_c = fma chain over its
+//     rows in increasing order; out = ((0 + P_0) + P_1) + ... in f32.
 //
-// Layout.  K is the FA cache layout [n_ctx][h_kv * d] (qwen35.rs:571-575).  V
-// is the transposed cache [h_kv * d][v_stride] the reference uses without FA
-// (qwen35.rs:580-586): the KV axis is contiguous, which is what the PV product
-// needs as its reduction axis.
+// Kernels: scores (grid: chunk x KV head x 32-row query block), softmax (one
+// block per query row), pv (chunk x KV head x 8-row groups; lane = d), fold
+// (per output element).  Scratch in the context workspace: w [T*H][n] f32,
+// p [h_kv][n][LRp] f16 (LRp = query rows of a KV head, padded to 8),
+// partials [chunks][T*H][D] f32.
 //
-// Mapping.  Grid = (splits of the KV axis, h_kv).  A workgroup stages the
-// G*T query rows of its KV head (G = h / h_kv) in LDS as f16 (ggml's CPU FA
-// also converts q to f16), and its 4 waves walk 32-row KV tiles round-robin:
-//   S  = Q K^T      v_mfma_f32_16x16x32_f16, K fragments straight from HBM
-//   online softmax  f32, per query row, rows spread as the MFMA D layout
-//   O += P V        v_mfma_f32_16x16x32_f16 twice, with P = P_hi + P_lo in f16
-// Each wave keeps its own (m, l, O); the waves merge through LDS, each split
-// writes (m, l, O) partials, and a second kernel combines the splits.
+// Layout.  K is [n_ctx][h_kv * d]; V is the transposed cache [h_kv * d][v_stride]
+// (the reference's non-FA V layout, qwen35.rs:580-586): the KV axis is
+// contiguous, the reduction axis of P V.
 #include <math.h>
 
 #include "cpv_internal.h"
 
 namespace {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef float f4 __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int TILE = 32;           // KV rows per MFMA tile
-constexpr int WAVES = 4;
-constexpr int MAX_ROWS = 96;       // query rows per workgroup (a row block of one KV head)
-constexpr int P_STRIDE = TILE + 8; // halves per P row in LDS (breaks bank aliasing)
+constexpr int CHUNK = 256;          // cache rows per chunk (the fold unit of the contract)
+constexpr int QB = 32;              // query rows per scores workgroup
+constexpr int E_EMPTY = -100000;    // exponent of an all-zero vector
 
-__device__ __forceinline__ h8 load_h8(const uint16_t* p)
+__device__ __forceinline__ int ceil_log2_dev(int64_t v)
 {
-    const uint4 v = *(const uint4*)p;
-    return __builtin_bit_cast(h8, v);
+    int b = 0;
+    while (((int64_t)1 << b) < v) b++;
+    return b;
 }
 
-template <int D, int RT>
-__global__ __launch_bounds__(256) void attn_split_kernel(
-    const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vt,
-    int64_t v_stride, int64_t n_past, const int32_t* __restrict__ parent, int T, int H, int Hkv, float scale,
-    int64_t chunk, float* __restrict__ part)
+// visibility of cache row j for node t: context rows, then the node's
+// ancestors and itself (tree, bit mask anc) or every node up to t (chain)
+__device__ __forceinline__ bool visible(int64_t j, int64_t n_past, int t, bool tree, uint64_t anc)
 {
-    constexpr int DC = D / 32;     // MFMA k-steps for q k^T
-    constexpr int DT = D / 16;     // output column tiles
-    const int G = H / Hkv;
-    const int R = G * T;                         // query rows of this KV head
-    const int row0 = blockIdx.z * MAX_ROWS;      // this workgroup's first row
-    const int Rb = R - row0 < RT * 16 ? R - row0 : RT * 16;
-    const int split = blockIdx.x, kvh = blockIdx.y;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, g4 = lane >> 4;
-    const int64_t n_tot = n_past + T;
-    const int64_t j_begin = (int64_t)split * chunk;
-    const int64_t j_end = j_begin + chunk < n_tot ? j_begin + chunk : n_tot;
-    const int ntiles = (int)((j_end - j_begin + TILE - 1) / TILE);
+    if (j < n_past) return true;
+    const int64_t node = j - n_past;
+    return tree ? ((anc >> node) & 1ull) != 0 : node <= t;
+}
 
-    __shared__ __align__(16) uint16_t s_q[RT * 16 * D];                      // f16 queries
-    __shared__ __align__(16) uint16_t s_p[WAVES][2][RT * 16 * P_STRIDE];     // P hi / lo
-    __shared__ uint64_t s_anc[64];
-    __shared__ float s_ml[WAVES][2][RT * 16];
+__device__ __forceinline__ uint64_t ancestors(const int32_t* parent, int t)
+{
+    uint64_t m = 0;
+    for (int a = t; a >= 0; a = parent[a]) m |= 1ull << a;
+    return m;
+}
 
-    // ancestor-or-self bitmask per node of a tree (a chain needs none)
-    if (parent && tid < T) {
-        uint64_t m = 0;
-        int a = tid;
-        for (int steps = 0; a >= 0 && a < T && steps <= T; steps++) {
-            m |= 1ull << a;
-            a = parent ? parent[a] : a - 1;
+// 15-bit fixed point of an f16 value at exponent e, split into two signed
+// 8-bit limbs: f = 256 hi + lo, lo in [-128, 127], |hi| <= 64
+__device__ __forceinline__ void limbs(float v, int e, int8_t* hi, int8_t* lo)
+{
+    int f = 0;
+    if (e != E_EMPTY) f = (int)rintf(ldexpf(v, 14 - e));
+    const int h = (f + 128) >> 8;
+    *hi = (int8_t)h;
+    *lo = (int8_t)(f - 256 * h);
+}
+
+struct ScoreArgs {
+    const float* q;           // [T][H][D]
+    const uint16_t* kc;       // [n_ctx][Hkv*D]
+    const int32_t* parent;    // [T] or null
+    float* w;                 // [T*H][n]  scaled scores, -inf where invisible
+    int64_t n_past, n;        // n = n_past + T rows in play
+    int T, H, Hkv;
+    float scale;
+};
+
+// scores of 32 query rows (of one KV head) against one 256-row chunk
+template <int D>
+__global__ __launch_bounds__(256) void attn_scores_kernel(ScoreArgs a)
+{
+    constexpr int TPR = D / 16;                // threads per row when converting (16 values each)
+    constexpr int RPP = 256 / TPR;             // rows per pass
+    __shared__ __align__(16) int8_t s_qh[QB][D], s_ql[QB][D];
+    __shared__ __align__(16) int8_t s_kh[CHUNK][D], s_kl[CHUNK][D];
+    __shared__ int s_eq[QB], s_ek[CHUNK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = blockIdx.x, kh = blockIdx.y;
+    const int G = a.H / a.Hkv, LR = G * a.T;
+    const int64_t j0 = (int64_t)c * CHUNK;
+    const int sub = tid % TPR;
+
+    // ---- query rows lr = blockIdx.z * 32 + r: t = lr / G, head kh * G + lr % G
+    for (int r = tid / TPR; r < QB; r += RPP) {
+        const int lr = blockIdx.z * QB + r;
+        float v[16];
+        float mx = 0.0f;
+        if (lr < LR) {
+            const int t = lr / G, h = kh * G + lr % G;
+            const float* src = a.q + ((int64_t)t * a.H + h) * D + sub * 16;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                v[i] = cpv_h2f(cpv_f2h(src[i]));
+                mx = fmaxf(mx, fabsf(v[i]));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) v[i] = 0.0f;
         }
-        s_anc[tid] = m;
+        for (int off = 1; off < TPR; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        int e = E_EMPTY;
+        if (mx > 0.0f) frexpf(mx, &e);
+#pragma unroll
+        for (int i = 0; i < 16; i++) limbs(v[i], e, &s_qh[r][sub * 16 + i], &s_ql[r][sub * 16 + i]);
+        if (sub == 0) s_eq[r] = e;
     }
-    // query rows rho = t * G + gi of head kvh * G + gi, rounded to f16
-    for (int i = tid; i < RT * 16 * D; i += blockDim.x) {
-        const int rho = i / D, d = i % D;
-        float v = 0.0f;
-        if (rho < Rb) {
-            const int t = (row0 + rho) / G, gi = (row0 + rho) % G;
-            v = q[((int64_t)t * H + kvh * G + gi) * D + d];
+    // ---- the chunk's cache rows of this KV head
+    for (int r = tid / TPR; r < CHUNK; r += RPP) {
+        const int64_t j = j0 + r;
+        float v[16];
+        float mx = 0.0f;
+        if (j < a.n) {
+            const uint16_t* src = a.kc + j * (int64_t)a.Hkv * D + (int64_t)kh * D + sub * 16;
+            const uint4 p0 = *(const uint4*)src, p1 = *(const uint4*)(src + 8);
+            const uint32_t wds[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                v[i] = cpv_h2f((uint16_t)(wds[i >> 1] >> (16 * (i & 1))));
+                mx = fmaxf(mx, fabsf(v[i]));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) v[i] = 0.0f;
         }
-        s_q[i] = cpv_f2h(v);
+        for (int off = 1; off < TPR; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        int e = E_EMPTY;
+        if (mx > 0.0f) frexpf(mx, &e);
+#pragma unroll
+        for (int i = 0; i < 16; i++) limbs(v[i], e, &s_kh[r][sub * 16 + i], &s_kl[r][sub * 16 + i]);
+        if (sub == 0) s_ek[r] = e;
     }
     __syncthreads();
 
-    float m_run[RT][4], l_run[RT][4];
-    f4 o[RT][DT];
+    // ---- 2 x 16 output blocks of 16 x 16 (query rows x cache rows); 4 waves, 8 blocks each
+    const bool tree = a.parent != nullptr;
+    for (int blk = wave; blk < 2 * (CHUNK / 16); blk += 4) {
+        const int qb = blk & 1, jb = blk >> 1;
+        v4i hh = {0, 0, 0, 0}, mix = {0, 0, 0, 0}, ll = {0, 0, 0, 0};
+        const int ar = qb * 16 + (lane & 15), bc = jb * 16 + (lane & 15), kg = (lane >> 4) * 16;
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) { m_run[rt][i] = -INFINITY; l_run[rt][i] = 0.0f; }
-#pragma unroll
-    for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) o[rt][dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    const uint16_t* kh = kc + (int64_t)kvh * D;
-    const int64_t k_row = (int64_t)Hkv * D;
-    const int steps = (ntiles + WAVES - 1) / WAVES;
-    for (int step = 0; step < steps; step++) {
-        const int tile = step * WAVES + wave;
-        const bool active = tile < ntiles;
-        const int64_t j0 = j_begin + (int64_t)tile * TILE;
-        if (active) {
-            // K fragments for both 16-row column tiles: row j0 + 16 ct + l16, d = 32 dc + 8 g4
-            h8 kf[2][DC];
-#pragma unroll
-            for (int ct = 0; ct < 2; ct++) {
-                const int64_t j = j0 + 16 * ct + l16;
-#pragma unroll
-                for (int dc = 0; dc < DC; dc++) {
-                    if (j < j_end) kf[ct][dc] = load_h8(kh + j * k_row + 32 * dc + 8 * g4);
-                    else kf[ct][dc] = h8{0, 0, 0, 0, 0, 0, 0, 0};
-                }
-            }
-#pragma unroll
-            for (int rt = 0; rt < RT; rt++) {
-                f4 s[2];
-#pragma unroll
-                for (int ct = 0; ct < 2; ct++) {
-                    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                    for (int dc = 0; dc < DC; dc++) {
-                        const h8 a = load_h8(s_q + (rt * 16 + l16) * D + 32 * dc + 8 * g4);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, kf[ct][dc], acc, 0, 0, 0);
-                    }
-                    s[ct] = acc;
-                }
-                // scale, mask, online softmax for rows rt*16 + 4 g4 + i
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int rho = rt * 16 + 4 * g4 + i;
-                    const int node = rho < Rb ? (row0 + rho) / G : 0;
-                    float sv[2];
-#pragma unroll
-                    for (int ct = 0; ct < 2; ct++) {
-                        const int64_t j = j0 + 16 * ct + l16;
-                        bool vis = j < j_end;
-                        if (vis && j >= n_past)
-                            vis = parent ? ((s_anc[node] >> (j - n_past)) & 1ull) != 0 : j - n_past <= node;
-                        sv[ct] = vis ? s[ct][i] * scale : -INFINITY;
-                    }
-                    float mx = fmaxf(sv[0], sv[1]);
-#pragma unroll
-                    for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-                    const float m_new = fmaxf(m_run[rt][i], mx);
-                    float p0 = 0.0f, p1 = 0.0f, alpha = 1.0f;
-                    if (m_new != -INFINITY) {
-                        alpha = expf(m_run[rt][i] - m_new);
-                        p0 = expf(sv[0] - m_new);
-                        p1 = expf(sv[1] - m_new);
-                    }
-                    float sum = p0 + p1;
-#pragma unroll
-                    for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off);
-                    l_run[rt][i] = l_run[rt][i] * alpha + sum;
-                    m_run[rt][i] = m_new;
-#pragma unroll
-                    for (int dt = 0; dt < DT; dt++) o[rt][dt][i] *= alpha;
-                    // P for the PV product, split exactly into two f16 parts
-                    const uint16_t h0 = cpv_f2h(p0), h1 = cpv_f2h(p1);
-                    const uint16_t lo0 = cpv_f2h(p0 - cpv_h2f(h0)), lo1 = cpv_f2h(p1 - cpv_h2f(h1));
-                    uint16_t* ph = s_p[wave][0] + (rt * 16 + 4 * g4 + i) * P_STRIDE;
-                    uint16_t* pl = s_p[wave][1] + (rt * 16 + 4 * g4 + i) * P_STRIDE;
-                    ph[l16] = h0;
-                    ph[16 + l16] = h1;
-                    pl[l16] = lo0;
-                    pl[16 + l16] = lo1;
-                }
-            }
+        for (int ks = 0; ks < D / 64; ks++) {
+            const v4i qhv = *(const v4i*)&s_qh[ar][ks * 64 + kg], qlv = *(const v4i*)&s_ql[ar][ks * 64 + kg];
+            const v4i khv = *(const v4i*)&s_kh[bc][ks * 64 + kg], klv = *(const v4i*)&s_kl[bc][ks * 64 + kg];
+            hh = __builtin_amdgcn_mfma_i32_16x16x64_i8(qhv, khv, hh, 0, 0, 0);
+            mix = __builtin_amdgcn_mfma_i32_16x16x64_i8(qhv, klv, mix, 0, 0, 0);
+            mix = __builtin_amdgcn_mfma_i32_16x16x64_i8(qlv, khv, mix, 0, 0, 0);
+            ll = __builtin_amdgcn_mfma_i32_16x16x64_i8(qlv, klv, ll, 0, 0, 0);
         }
-        __syncthreads();
-        if (active) {
-            // V^T fragments: column d = 16 dt + l16, KV rows j0 + 8 g4 .. + 8
-            h8 vf[DT];
-            const int64_t jv = j0 + 8 * g4;
+        // lane holds rows 4 (lane/16) + i of the query block, cache row bc
+        const int64_t j = j0 + bc;
+        if (j >= a.n) continue;
+        const int ek = s_ek[bc];
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++) {
-                const uint16_t* src = vt + ((int64_t)kvh * D + 16 * dt + l16) * v_stride + jv;
-                if (jv + 8 <= j_end) {
-                    vf[dt] = load_h8(src);
-                } else {
-                    h8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-                    for (int e = 0; e < 8; e++)
-                        if (jv + e < j_end) v[e] = __builtin_bit_cast(_Float16, src[e]);
-                    vf[dt] = v;
+        for (int i = 0; i < 4; i++) {
+            const int r = qb * 16 + 4 * (lane >> 4) + i;
+            const int lr = blockIdx.z * QB + r;
+            if (lr >= LR) continue;
+            const int t = lr / G, h = kh * G + lr % G;
+            const uint64_t anc = tree ? ancestors(a.parent, t) : 0;
+            float w = -INFINITY;
+            if (visible(j, a.n_past, t, tree, anc)) {
+                const int eq = s_eq[r];
+                float s = 0.0f;
+                if (eq != E_EMPTY && ek != E_EMPTY) {
+                    const int64_t S = (int64_t)hh[i] * 65536 + (int64_t)mix[i] * 256 + (int64_t)ll[i];
+                    s = (float)ldexp((double)S, eq + ek - 28);
                 }
+                w = s * a.scale;
             }
-#pragma unroll
-            for (int rt = 0; rt < RT; rt++) {
-                const h8 ahi = load_h8(s_p[wave][0] + (rt * 16 + l16) * P_STRIDE + 8 * g4);
-                const h8 alo = load_h8(s_p[wave][1] + (rt * 16 + l16) * P_STRIDE + 8 * g4);
-#pragma unroll
-                for (int dt = 0; dt < DT; dt++) {
-                    o[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, vf[dt], o[rt][dt], 0, 0, 0);
-                    o[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, vf[dt], o[rt][dt], 0, 0, 0);
-                }
-            }
+            a.w[((int64_t)t * a.H + h) * a.n + j] = w;
         }
-        __syncthreads();
-    }
-
-    // merge the waves' (m, l, O) through LDS, reusing the P buffers for O
-    float* s_o = (float*)&s_p[0][0][0];          // RT*16 x D floats
-    static_assert(sizeof(s_p) >= sizeof(float) * RT * 16 * D, "merge buffer");
-    for (int w = 0; w < WAVES; w++) {
-        if (wave == w) {
-#pragma unroll
-            for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int row = rt * 16 + 4 * g4 + i;
-                    float scale_old = 0.0f, scale_new = 1.0f, m_tot = m_run[rt][i], l_tot = l_run[rt][i];
-                    if (w > 0) {
-                        const float mo = s_ml[0][0][row], lo = s_ml[0][1][row];
-                        m_tot = fmaxf(mo, m_run[rt][i]);
-                        scale_old = m_tot == -INFINITY ? 0.0f : expf(mo - m_tot);
-                        scale_new = m_tot == -INFINITY ? 0.0f : expf(m_run[rt][i] - m_tot);
-                        l_tot = lo * scale_old + l_run[rt][i] * scale_new;
-                    }
-#pragma unroll
-                    for (int dt = 0; dt < DT; dt++) {
-                        float* dst = s_o + row * D + 16 * dt + l16;
-                        *dst = (w > 0 ? *dst * scale_old : 0.0f) + o[rt][dt][i] * scale_new;
-                    }
-                    if (l16 == 0) { s_ml[0][0][row] = m_tot; s_ml[0][1][row] = l_tot; }
-                }
-        }
-        __syncthreads();
-    }
-    // partials: [split][kvh][rho] x (m, l, O[D])
-    const int nsplit = gridDim.x;
-    for (int i = tid; i < Rb * (D + 2); i += blockDim.x) {
-        const int rho = i / (D + 2), c = i % (D + 2);
-        const float v = c == 0 ? s_ml[0][0][rho] : c == 1 ? s_ml[0][1][rho] : s_o[rho * D + c - 2];
-        part[(((int64_t)kvh * nsplit + split) * R + row0 + rho) * (D + 2) + c] = v;
     }
 }
 
-// combine the splits of one query row: out = sum_s e^{m_s-M} O_s / sum_s e^{m_s-M} l_s
-__global__ void attn_combine_kernel(const float* __restrict__ part, int nsplit, int T, int H, int Hkv, int D,
-                                    float* __restrict__ out)
+// one query row: max, exact normaliser, f16 probabilities (transposed per KV head)
+__global__ __launch_bounds__(256) void attn_softmax_kernel(const float* __restrict__ w, int64_t n, int T, int H,
+                                                           int Hkv, int LRp, uint16_t* __restrict__ p)
 {
-    const int G = H / Hkv, R = G * T;
-    const int rho = blockIdx.x % R, kvh = blockIdx.x / R;
-    const float* base = part + ((int64_t)kvh * nsplit * R + rho) * (D + 2);
-    const int64_t sstride = (int64_t)R * (D + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, base[s * sstride]);
-    const int t = rho / G, gi = rho % G;
-    float* o = out + ((int64_t)t * H + kvh * G + gi) * D;
-    for (int d = threadIdx.x; d < D; d += blockDim.x) {
-        float num = 0.0f, den = 0.0f;
-        for (int s = 0; s < nsplit; s++) {
-            const float* p = base + s * sstride;
-            const float w = p[0] == -INFINITY ? 0.0f : expf(p[0] - M);
-            num += w * p[2 + d];
-            den += w * p[1];
-        }
-        o[d] = num / den;
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t = row / H, h = row % H, G = H / Hkv, kh = h / G, lr = t * G + h % G;
+    const float* wr = w + (int64_t)row * n;
+    __shared__ float s_m[4];
+    __shared__ long long s_z[4];
+    __shared__ int s_c[4];
+    float mx = -INFINITY;
+    int cnt = 0;
+    for (int64_t j = tid; j < n; j += 256) {
+        const float v = wr[j];
+        if (v != -INFINITY) { mx = fmaxf(mx, v); cnt++; }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, off));
+        cnt += __shfl_xor(cnt, off);
+    }
+    if (lane == 0) { s_m[wave] = mx; s_c[wave] = cnt; }
+    __syncthreads();
+    mx = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+    const int nvis = s_c[0] + s_c[1] + s_c[2] + s_c[3];
+    const int Gz = 62 - ceil_log2_dev(nvis + 1);
+    long long Z = 0;
+    for (int64_t j = tid; j < n; j += 256) {
+        const float v = wr[j];
+        if (v != -INFINITY) Z += (long long)rint(ldexp((double)cpv_expf(v - mx), Gz));
+    }
+    for (int off = 32; off > 0; off >>= 1) Z += __shfl_xor(Z, off);
+    if (lane == 0) s_z[wave] = Z;
+    __syncthreads();
+    Z = s_z[0] + s_z[1] + s_z[2] + s_z[3];
+    const float inv = (float)(1.0 / ldexp((double)Z, -Gz));
+    uint16_t* pr = p + (int64_t)kh * n * LRp + lr;
+    for (int64_t j = tid; j < n; j += 256) {
+        const float v = wr[j];
+        pr[j * LRp] = v == -INFINITY ? (uint16_t)0 : cpv_f2h(cpv_expf(v - mx) * inv);
     }
 }
 
-template <int D, int RT>
-cpv_status launch(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
-                  int64_t n_past, const int32_t* parent, int T, int H, int Hkv, float scale, float* out)
+// P_c for 8 query rows x D of one KV head and one chunk: lane = d, an fma chain over
+// the chunk's rows in increasing order; the p of the 8 rows at a cache row is one
+// uniform 16-byte load
+template <int D>
+__global__ __launch_bounds__(256) void attn_pv_kernel(const uint16_t* __restrict__ vt, int64_t v_stride,
+                                                      const uint16_t* __restrict__ p, int64_t n, int LR, int LRp,
+                                                      int T, int H, int Hkv, float* __restrict__ part)
 {
-    const int G = H / Hkv, R = G * T;
-    const int64_t n_tot = n_past + T;
-    // enough splits for ~4 workgroups per CU, chunks a whole number of wave-steps
-    int64_t want = (int64_t)ctx->cu_count * 4 / Hkv;
-    if (want < 1) want = 1;
-    int64_t chunk = (n_tot + want - 1) / want;
-    const int64_t step_rows = (int64_t)TILE * WAVES;
-    chunk = (chunk + step_rows - 1) / step_rows * step_rows;
-    const int nsplit = (int)((n_tot + chunk - 1) / chunk);
+    constexpr int WPR = D / 64;                // waves per 8-row group
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = blockIdx.x, kh = blockIdx.y;
+    const int grp = blockIdx.z * (4 / WPR) + wave / WPR;   // 8-row group of this wave
+    const int lr0 = grp * 8;
+    if (lr0 >= LR) return;
+    const int d = (wave % WPR) * 64 + lane;
+    const int64_t j0 = (int64_t)c * CHUNK, j1 = j0 + CHUNK < n ? j0 + CHUNK : n;
+    const uint16_t* vrow = vt + ((int64_t)kh * D + d) * v_stride;
+    const uint16_t* pb = p + (int64_t)kh * n * LRp + lr0;
+    float acc[8];
+#pragma unroll
+    for (int r = 0; r < 8; r++) acc[r] = 0.0f;
+    int64_t j = j0;
+    for (; j + 8 <= j1; j += 8) {
+        const uint4 vv = *(const uint4*)(vrow + j);
+        const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+        for (int jj = 0; jj < 8; jj++) {
+            const float v = cpv_h2f((uint16_t)(vw[jj >> 1] >> (16 * (jj & 1))));
+            const uint4 pp = *(const uint4*)(pb + (j + jj) * LRp);
+            const uint32_t pw[4] = {pp.x, pp.y, pp.z, pp.w};
+#pragma unroll
+            for (int r = 0; r < 8; r++) acc[r] = fmaf(cpv_h2f((uint16_t)(pw[r >> 1] >> (16 * (r & 1)))), v, acc[r]);
+        }
+    }
+    for (; j < j1; j++) {
+        const float v = cpv_h2f(vrow[j]);
+        const uint4 pp = *(const uint4*)(pb + j * LRp);
+        const uint32_t pw[4] = {pp.x, pp.y, pp.z, pp.w};
+#pragma unroll
+        for (int r = 0; r < 8; r++) acc[r] = fmaf(cpv_h2f((uint16_t)(pw[r >> 1] >> (16 * (r & 1)))), v, acc[r]);
+    }
+    const int G = H / Hkv;
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        const int lr = lr0 + r;
+        if (lr >= LR) break;
+        const int t = lr / G, h = kh * G + lr % G;
+        part[((int64_t)c * T * H + (int64_t)t * H + h) * D + d] = acc[r];
+    }
+}
+
+// out = ((0 + P_0) + P_1) + ... in chunk order
+__global__ __launch_bounds__(256) void attn_fold_kernel(const float* __restrict__ part, int nchunk, int64_t total,
+                                                        float* __restrict__ out)
+{
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= total) return;
+    float o = 0.0f;
+    for (int c = 0; c < nchunk; c++) o = o + part[(int64_t)c * total + e];
+    out[e] = o;
+}
+
+// one call over T query tokens (the scratch holds T*H rows)
+template <int D>
+cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
+                      int64_t n_past, const int32_t* parent, int T, int H, int Hkv, float scale, float* out)
+{
+    const int64_t n = n_past + T;
+    const int G = H / Hkv, LR = G * T, LRp = (LR + 7) / 8 * 8;
+    const int nchunk = (int)((n + CHUNK - 1) / CHUNK);
+    const size_t w_b = ((size_t)T * H * n * 4 + 255) & ~(size_t)255;
+    const size_t p_b = ((size_t)Hkv * n * LRp * 2 + 255) & ~(size_t)255;
+    const size_t part_b = (size_t)nchunk * T * H * D * 4;
     void* ws = nullptr;
-    cpv_status st = cpv_workspace(ctx, (size_t)Hkv * nsplit * R * (D + 2) * sizeof(float), &ws);
+    cpv_status st = cpv_workspace(ctx, w_b + p_b + part_b, &ws);
     if (st != CPV_OK) return st;
-    dim3 grid((unsigned)nsplit, (unsigned)Hkv, (unsigned)((R + MAX_ROWS - 1) / MAX_ROWS));
-    attn_split_kernel<D, RT><<<grid, 256, 0, ctx->stream>>>(q, kc, vt, v_stride, n_past, parent, T, H, Hkv,
-                                                            scale, chunk, (float*)ws);
-    CPV_HIP(ctx, hipGetLastError());
-    attn_combine_kernel<<<(unsigned)(Hkv * R), D, 0, ctx->stream>>>((const float*)ws, nsplit, T, H, Hkv, D, out);
+    float* w = (float*)ws;
+    uint16_t* p = (uint16_t*)((uint8_t*)ws + w_b);
+    float* part = (float*)((uint8_t*)ws + w_b + p_b);
+    ScoreArgs sa;
+    sa.q = q;
+    sa.kc = kc;
+    sa.parent = parent;
+    sa.w = w;
+    sa.n_past = n_past;
+    sa.n = n;
+    sa.T = T;
+    sa.H = H;
+    sa.Hkv = Hkv;
+    sa.scale = scale;
+    attn_scores_kernel<D><<<dim3((unsigned)nchunk, (unsigned)Hkv, (unsigned)((LR + QB - 1) / QB)), 256, 0,
+                            ctx->stream>>>(sa);
+    attn_softmax_kernel<<<(unsigned)(T * H), 256, 0, ctx->stream>>>(w, n, T, H, Hkv, LRp, p);
+    const int rows_per_block = 8 * (4 / (D / 64));
+    attn_pv_kernel<D><<<dim3((unsigned)nchunk, (unsigned)Hkv, (unsigned)((LR + rows_per_block - 1) / rows_per_block)),
+                        256, 0, ctx->stream>>>(vt, v_stride, p, n, LR, LRp, T, H, Hkv, part);
+    const int64_t total = (int64_t)T * H * D;
+    attn_fold_kernel<<<(unsigned)((total + 255) / 256), 256, 0, ctx->stream>>>(part, nchunk, total, out);
     CPV_HIP(ctx, hipGetLastError());
     return CPV_OK;
 }
 
 template <int D>
-cpv_status launch_rt(cpv_ctx* ctx, int rt, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t vs,
-                     int64_t n_past, const int32_t* parent, int T, int H, int Hkv, float scale, float* out)
+cpv_status attn_run(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
+                    int64_t n_past, const int32_t* parent, int t, int h, int h_kv, float scale, float* out)
 {
-    switch (rt) {
-    case 1: return launch<D, 1>(ctx, q, kc, vt, vs, n_past, parent, T, H, Hkv, scale, out);
-    case 2: return launch<D, 2>(ctx, q, kc, vt, vs, n_past, parent, T, H, Hkv, scale, out);
-    case 3: return launch<D, 3>(ctx, q, kc, vt, vs, n_past, parent, T, H, Hkv, scale, out);
-    case 4: return launch<D, 4>(ctx, q, kc, vt, vs, n_past, parent, T, H, Hkv, scale, out);
-    case 5: return launch<D, 5>(ctx, q, kc, vt, vs, n_past, parent, T, H, Hkv, scale, out);
-    default: return launch<D, 6>(ctx, q, kc, vt, vs, n_past, parent, T, H, Hkv, scale, out);
+    if (parent) return attn_block<D>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out);
+    // a long chain runs in token blocks to bound the scratch: node t of a chain sees
+    // the rows <= n_past + t, which is what a block starting at t0 sees with n_past + t0
+    const int64_t n = n_past + t;
+    int64_t tb = ((int64_t)192 << 20) / ((int64_t)h * n * 4 + 1);
+    if (tb < 1) tb = 1;
+    if (tb > t) tb = t;
+    for (int t0 = 0; t0 < t; t0 += (int)tb) {
+        const int tn = t - t0 < (int)tb ? t - t0 : (int)tb;
+        cpv_status st = attn_block<D>(ctx, q + (int64_t)t0 * h * D, kc, vt, v_stride, n_past + t0, nullptr, tn, h,
+                                      h_kv, scale, out + (int64_t)t0 * h * D);
+        if (st != CPV_OK) return st;
     }
+    return CPV_OK;
 }
 
 }  // namespace
@@ -306,11 +361,9 @@ cpv_status cpv_attn_launch(cpv_ctx* ctx, const float* q, const uint16_t* kc, con
                            int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
                            float* out)
 {
-    const int R = (h / h_kv) * t;
-    const int rt = ((R < MAX_ROWS ? R : MAX_ROWS) + 15) / 16;
     auto go = [=]() {
-        return d == 128 ? launch_rt<128>(ctx, rt, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out)
-                        : launch_rt<64>(ctx, rt, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out);
+        return d == 128 ? attn_run<128>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out)
+                        : attn_run<64>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out);
     };
     const int ev = cpv_prof_mark(ctx);
     const cpv_status st = go();

@@ -78,14 +78,26 @@ constexpr int CPV_E_EMPTY = -100000;
 // exact-window constants shared by the launcher and the kernels
 int cpv_qgemm_window(int type, int64_t k);
 
-// IEEE binary16 <-> binary32 (exact / round-to-nearest-even)
+// IEEE binary16 <-> binary32 (exact / round-to-nearest-even).  The narrowing
+// is done on the bits: a plain (_Float16) conversion lets the compiler fuse a
+// preceding f32 multiply or add into one v_fma_mix (a single rounding to f16
+// instead of f32 then f16), which differs at f32 ties.
 __host__ __device__ __forceinline__ float cpv_h2f(uint16_t h)
 {
     return (float)__builtin_bit_cast(_Float16, h);
 }
 __host__ __device__ __forceinline__ uint16_t cpv_f2h(float f)
 {
-    return __builtin_bit_cast(uint16_t, (_Float16)f);
+    const uint32_t x = __builtin_bit_cast(uint32_t, f);
+    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (uint16_t)(sign | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u));   // NaN, inf
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);           // |f| >= 65520 rounds to inf
+    if (ax < 0x38800000u) {                                               // below 2^-14: subnormal or zero
+        const float m = rintf(__builtin_bit_cast(float, ax) * 16777216.0f);   // exact scaling by 2^24, RNE
+        return (uint16_t)(sign | (uint32_t)m);
+    }
+    const uint32_t r = ax + 0x0fffu + ((ax >> 13) & 1u);                  // round the 13 dropped bits, ties to even
+    return (uint16_t)(sign | ((r - 0x38000000u) >> 13));
 }
 
 // expf evaluated as glibc (>= 2.27) evaluates it, which is the libm expf the

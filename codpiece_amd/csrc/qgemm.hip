@@ -153,7 +153,6 @@ __device__ __forceinline__ void gemm_unit(const v4i* pcu, uint16_t d6, int er, i
                                           const float* s_da, const int32_t* s_bs, double* S)
 {
     constexpr int RG = (MC + 3) / 4;
-    using F = Fmt<TYPE>;
     if constexpr (TYPE == CPV_Q4_K) {
         const uint32_t h0 = (uint32_t)pcu[8][0], hy = (uint32_t)pcu[8][1], hz = (uint32_t)pcu[8][2],
                        hw = (uint32_t)pcu[8][3];

@@ -110,10 +110,17 @@ void     cpvo_rope_neox(float* x, int n_rot, const float* cs_row);
  * q: [T][H][D] f32; kc, vc: [n_ctx][Hkv*D] f16; rows [0, n_past) are context,
  * rows n_past + t hold node t.  parent: [T] tree parents (-1 = root, i.e. a
  * child of the context), or NULL for a linear chain.  Node t sees all context
- * rows plus its ancestors and itself.  out: [T][H*D]. */
+ * rows plus its ancestors and itself.  out: [T][H*D].
+ * cpvo_attn is the exact-window contract (cpvo_glue.c), order-free;
+ * cpvo_attn_f64 the same attention in binary64 (q rounded to f16), the
+ * accuracy reference. */
+#define CPVO_ATTN_CHUNK 256
 void     cpvo_attn(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n_past,
                    const int32_t* parent, int T, int H, int Hkv, int D, float scale,
                    float* out);
+void     cpvo_attn_f64(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n_past,
+                       const int32_t* parent, int T, int H, int Hkv, int D, float scale,
+                       float* out);
 
 /* ---- sampler (crates/codpiece-sample/src/lib.rs) ------------------------ */
 typedef struct {

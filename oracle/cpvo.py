@@ -82,6 +82,8 @@ def lib():
             "cpvo_rope_neox": (None, [P, ctypes.c_int, P]),
             "cpvo_attn": (None, [P, P, P, i64, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                  ctypes.c_int, f32, P]),
+            "cpvo_attn_f64": (None, [P, P, P, i64, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                 ctypes.c_int, f32, P]),
             "cpvo_distribution": (ctypes.c_int, [P, P, ctypes.c_int, P, ctypes.c_int, P, P, P]),
             "cpvo_dist_draw": (i32, [P, P, ctypes.c_int, f32]),
             "cpvo_dist_draw_excluding": (i32, [P, P, ctypes.c_int, i32, f32]),
@@ -260,8 +262,12 @@ def rope_neox(x, n_rot, cs_row):
     return x
 
 
-def attn(q, kc, vc, n_past, parent, scale):
-    """q [T][H][D] f32; kc/vc [n_ctx][Hkv*D] uint16 (f16 bits)."""
+ATTN_CHUNK = 256
+
+
+def attn(q, kc, vc, n_past, parent, scale, f64=False):
+    """q [T][H][D] f32; kc/vc [n_ctx][Hkv*D] uint16 (f16 bits).  The
+    exact-window contract, or (f64=True) binary64 attention."""
     q = np.ascontiguousarray(q, dtype=np.float32)
     T, H, D = q.shape
     kc = np.ascontiguousarray(kc, dtype=np.uint16)
@@ -269,7 +275,8 @@ def attn(q, kc, vc, n_past, parent, scale):
     Hkv = kc.shape[1] // D
     par = None if parent is None else np.ascontiguousarray(parent, dtype=np.int32)
     out = np.empty((T, H * D), dtype=np.float32)
-    lib().cpvo_attn(_p(q), _p(kc), _p(vc), n_past, _p(par), T, H, Hkv, D, scale, _p(out))
+    fn = lib().cpvo_attn_f64 if f64 else lib().cpvo_attn
+    fn(_p(q), _p(kc), _p(vc), n_past, _p(par), T, H, Hkv, D, scale, _p(out))
     return out
 
 

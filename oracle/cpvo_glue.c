@@ -123,7 +123,7 @@ static void f16_tab_init(void)
     }
 }
 
-void cpvo_attn(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n_past,
+void cpvo_attn_f64(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n_past,
                const int32_t* parent, int T, int H, int Hkv, int D, float scale, float* out)
 {
     const int g = H / Hkv;
@@ -166,5 +166,108 @@ void cpvo_attn(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n
             for (int d = 0; d < D; d++) out[((int64_t)t * H + h) * D + d] = (float)(o[d] / z);
         }
         free(s); free(vis); free(qd); free(o);
+    }
+}
+
+/* The exact-window attention contract (what the device computes, bit for
+ * bit, in any launch configuration).  ggml's CPU path (the reference's
+ * build_attn_block, qwen35.rs:3100-3140: mul_mat(k, q), soft_max_ext with
+ * the kq scale and the mask, mul_mat(v^T, kq)) rounds q and the
+ * probabilities to f16 (vec_dot_type of an f16 cache) and sums in an order
+ * set by its SIMD width; this restatement keeps those roundings and fixes the
+ * sums so that any order gives the same bits:
+ *  1. q16 = f16(q).  Per query head, Eq = frexp exponent of max|q16|,
+ *     qf = rint(q16 * 2^(14 - Eq)) (|qf| <= 2^14).  Per cache row j and KV
+ *     head, Ek = exponent of max|k16|, kf = rint(k16 * 2^(14 - Ek)).  The
+ *     score is s_j = (float)(sum_d qf*kf * 2^(Eq + Ek - 28)), the integer sum
+ *     exact (|sum| < 2^36).  An all-zero q head or k row scores 0.
+ *  2. w_j = s_j * scale (f32) for visible rows; mx = max w; e_j = expf(w_j -
+ *     mx) with the glibc expf restatement.
+ *  3. Z = sum over visible j of rint(e_j * 2^G), G = 62 - ceil_log2(n_vis + 1),
+ *     exact in int64; inv = (float)(1 / (Z * 2^-G)); p_j = f16(e_j * inv).
+ *  4. out_d: for each chunk of CPVO_ATTN_CHUNK consecutive cache rows (by
+ *     absolute row index) P_c = fmaf(p_j, v_jd, P_c) over its rows in
+ *     increasing order from +0 (invisible rows have p = 0); then
+ *     out_d = (((0 + P_0) + P_1) + ...) in f32.
+ * The f64 attention above is the accuracy reference this is tested against. */
+static int64_t ipow_exp(const uint16_t* h, int n)
+{
+    float mx = 0.0f;
+    for (int i = 0; i < n; i++) {
+        const float a = fabsf(f16_tab[h[i]]);
+        if (a > mx) mx = a;
+    }
+    int e = INT_MIN;
+    if (mx > 0.0f) frexpf(mx, &e);
+    return e;
+}
+
+void cpvo_attn(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n_past,
+               const int32_t* parent, int T, int H, int Hkv, int D, float scale, float* out)
+{
+    const int g = H / Hkv;
+    const int64_t row = (int64_t)Hkv * D;
+    const int64_t nmax = n_past + T;
+    const int64_t nchunk = (nmax + CPVO_ATTN_CHUNK - 1) / CPVO_ATTN_CHUNK;
+    f16_tab_init();
+#pragma omp parallel
+    {
+        float* w = malloc(sizeof(float) * (size_t)nmax);
+        float* p = malloc(sizeof(float) * (size_t)nmax);
+        char* vis = malloc((size_t)T);
+        uint16_t* q16 = malloc(sizeof(uint16_t) * (size_t)D);
+        int64_t* qf = malloc(sizeof(int64_t) * (size_t)D);
+        float* P = malloc(sizeof(float) * (size_t)D);
+#pragma omp for schedule(dynamic)
+        for (int th = 0; th < T * H; th++) {
+            const int t = th / H, h = th % H, kh = h / g;
+            memset(vis, 0, (size_t)T);
+            for (int a = t; a >= 0; a = parent ? parent[a] : a - 1) vis[a] = 1;
+            for (int d = 0; d < D; d++) q16[d] = cpvo_fp32_to_fp16(q[((int64_t)t * H + h) * D + d]);
+            const int64_t eq = ipow_exp(q16, D);
+            for (int d = 0; d < D; d++)
+                qf[d] = eq == INT_MIN ? 0 : (int64_t)rint(ldexp((double)f16_tab[q16[d]], 14 - (int)eq));
+            /* 1-2: scores, scaled; max over visible rows */
+            float mx = -INFINITY;
+            int64_t nvis = 0;
+            for (int64_t r = 0; r < nmax; r++) {
+                if (r >= n_past && !vis[r - n_past]) { w[r] = -INFINITY; continue; }
+                const uint16_t* kr = kc + r * row + (int64_t)kh * D;
+                const int64_t ek = ipow_exp(kr, D);
+                float s = 0.0f;
+                if (eq != INT_MIN && ek != INT_MIN) {
+                    int64_t S = 0;
+                    for (int d = 0; d < D; d++)
+                        S += qf[d] * (int64_t)rint(ldexp((double)f16_tab[kr[d]], 14 - (int)ek));
+                    s = (float)ldexp((double)S, (int)(eq + ek) - 28);
+                }
+                w[r] = s * scale;
+                if (w[r] > mx) mx = w[r];
+                nvis++;
+            }
+            /* 3: exact normaliser, f16 probabilities */
+            const int G = 62 - ceil_log2_i(nvis + 1);
+            int64_t Z = 0;
+            for (int64_t r = 0; r < nmax; r++) {
+                if (w[r] == -INFINITY) { p[r] = 0.0f; continue; }
+                p[r] = cpvo_expf(w[r] - mx);
+                Z += (int64_t)rint(ldexp((double)p[r], G));
+            }
+            const float inv = (float)(1.0 / ldexp((double)Z, -G));
+            for (int64_t r = 0; r < nmax; r++) p[r] = f16_tab[cpvo_fp32_to_fp16(p[r] * inv)];
+            /* 4: chunked fixed-order fma chains, chunks folded in order */
+            float* o = out + ((int64_t)t * H + h) * D;
+            for (int d = 0; d < D; d++) o[d] = 0.0f;
+            for (int64_t c = 0; c < nchunk; c++) {
+                for (int d = 0; d < D; d++) P[d] = 0.0f;
+                const int64_t r1 = (c + 1) * CPVO_ATTN_CHUNK < nmax ? (c + 1) * CPVO_ATTN_CHUNK : nmax;
+                for (int64_t r = c * CPVO_ATTN_CHUNK; r < r1; r++) {
+                    const uint16_t* vr = vc + r * row + (int64_t)kh * D;
+                    for (int d = 0; d < D; d++) P[d] = fmaf(p[r], f16_tab[vr[d]], P[d]);
+                }
+                for (int d = 0; d < D; d++) o[d] = o[d] + P[d];
+            }
+        }
+        free(w); free(p); free(vis); free(q16); free(qf); free(P);
     }
 }

@@ -102,8 +102,9 @@ class PairedSession:
         self.o.inject_attention(self.tap.cpu().numpy())
 
     def _check(self):
+        # the device attention follows the oracle's exact contract: no difference at all
         r = self.o.inject_ratio
-        assert r <= 1.0, f"attention beyond tolerance (ratio {r}) in call {self.calls}"
+        assert r == 0.0, f"attention differs from the oracle (ratio {r}) in call {self.calls}"
         self.worst = max(self.worst, r)
         self.calls += 1
 

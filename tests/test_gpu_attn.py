@@ -1,8 +1,11 @@
-"""GPU parity of tree-masked GQA attention against the f64 oracle.
+"""GPU parity of tree-masked GQA attention against the oracle.
 
-Bar: the GPU evaluates q k^T with f16 MFMA products (q rounded to f16 exactly
-as the oracle does) and an f32 online softmax, so it is held to a tolerance:
-|gpu - oracle| <= 2e-5 + 2e-4 * |oracle| elementwise, for V ~ N(0, 1).
+Bar: bit-exact.  Both sides implement the exact-window attention contract
+(fixed-point scores with exact integer sums, an exact softmax normaliser, f16
+probabilities and fixed-order f32 accumulation), so the device result does
+not depend on its grid, KV split or the number of query rows per call.  The
+contract itself is held within 2^-10 max|v| of binary64 attention by the
+oracle's own tests.
 """
 import numpy as np
 import pytest
@@ -47,9 +50,7 @@ def run(ctx, t, h, hkv, d, n_past, parent, seed=0, extra_rows=0):
 
 
 def close(got, ref):
-    err = np.abs(got - ref)
-    tol = 2e-5 + 2e-4 * np.abs(ref)
-    assert np.all(err <= tol), (err.max(), (err / tol).max())
+    assert np.array_equal(got, ref), (np.abs(got - ref).max(), np.count_nonzero(got != ref))
 
 
 @pytest.mark.parametrize("n_past", [0, 1, 37, 300, 1000])
@@ -94,3 +95,21 @@ def test_bad_shapes_are_rejected(ctx):
     kc = torch.zeros((16, 2 * 96), dtype=torch.int16, device="cuda")
     with pytest.raises(CpvError):
         ctx.attn(q, kc, kc, 4, None, 2, 0.1)
+
+
+@pytest.mark.parametrize("split", [1, 7, 40])
+def test_chain_in_pieces_equals_whole(ctx, split):
+    rng = np.random.default_rng(21)
+    n_past, t, h, hkv, d = 600, 40, 8, 2, 64
+    k, v, vt = make(rng, n_past + t, hkv, d)
+    qn = rng.normal(size=(t, h, d)).astype(np.float32)
+    kc = torch.from_numpy(k.view(np.int16)).cuda()
+    vtc = torch.from_numpy(vt.view(np.int16)).cuda()
+    outs = []
+    for t0 in range(0, t, split):
+        tn = min(split, t - t0)
+        q = torch.from_numpy(qn[t0:t0 + tn]).cuda()
+        outs.append(ctx.attn(q, kc, vtc, n_past + t0, None, hkv, 0.125).cpu().numpy())
+    got = np.concatenate(outs)
+    ref = cpvo.attn(qn, k, v, n_past, None, np.float32(0.125))
+    close(got, ref)

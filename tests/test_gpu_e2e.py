@@ -6,11 +6,9 @@ against its own f64 attention (|dev - ref| <= 2e-5 + 2e-4|ref|); everything
 else -- embeddings, norms, rope, the exact-window GEMMs, gates, SwiGLU, the LM
 head, argmax, the MTP chain, the KV writes and the round bookkeeping -- must
 then agree bit for bit (logits, hidden, preds, chain), the peak confidence to
-1e-6.  (2) Free-running: without injection the device's attention differs from the
-oracle's by ~1e-6 relative, and the Q8 activation rounding that follows
-(a discontinuous function) turns that into 1e-2-level logit differences and
-diverging greedy streams after a few tokens; these tests are expected to fail
-until attention is made order-free and exact on both sides.
+1e-6.  (2) Free-running: attention follows the same exact, order-free contract on
+both sides, so without any injection the logits, the greedy streams and the
+acceptance counts are bit-identical to the oracle's.
 """
 import numpy as np
 import pytest
@@ -118,12 +116,7 @@ def test_lockstep_gumbel_noise(models):
     o.free()
 
 
-FREE_RUNNING = pytest.mark.xfail(reason="attention is within tolerance, not bit-exact; Q8 activation "
-                                        "rounding amplifies the difference", strict=False)
-
-
-@FREE_RUNNING
-def test_free_running_round_within_tolerance(models):
+def test_free_running_round_is_bit_exact(models):
     g, o = sessions(models)
     rng = np.random.default_rng(11)
     prompt = rng.integers(0, V, size=70).tolist()
@@ -131,14 +124,13 @@ def test_free_running_round_within_tolerance(models):
     o.prefill(prompt[:64])
     a = g.step_fused_cached(prompt[64:], 4, want_logits=True)
     p, chain, conf, logits, hidden = o.step_fused_cached(prompt[64:], 4, want_logits=True)
-    err = np.abs(a.logits.cpu().numpy() - logits).max() / np.abs(logits).max()
-    print("free-running max logit error (relative to max |logit|)", err, flush=True)
-    assert err <= 1e-3
+    assert np.array_equal(a.logits.cpu().numpy(), logits)
+    assert np.array_equal(a.hidden.cpu().numpy(), hidden)
+    assert a.preds == p.tolist() and a.chain == chain.tolist()
     g.free()
     o.free()
 
 
-@FREE_RUNNING
 def test_free_running_fused_loop_streams(models):
     from codpiece_amd.model import fused_generate
     g, o = sessions(models)

@@ -95,16 +95,52 @@ def _brute(q, k, v, n_past, parent, scale, H, Hkv, D):
 TREE = [-1, -1, -1, -1, 0, 0, 0, 1, 1, 1, 4, 4, 4, 10, 10, 10]
 
 
-def test_attention_matches_dense_masked_softmax():
+def test_attention_f64_matches_dense_masked_softmax():
     rng = np.random.default_rng(2)
     H, Hkv, D, n_past = 8, 2, 64, 300
     T = len(TREE)
     k, v = _cache(rng, n_past + T, Hkv, D)
     q = rng.normal(size=(T, H, D)).astype(np.float32)
     scale = np.float32(1) / np.sqrt(np.float32(D))
-    got = cpvo.attn(q, k, v, n_past, TREE, scale)
+    got = cpvo.attn(q, k, v, n_past, TREE, scale, f64=True)
     ref = _brute(q, k, v, n_past, TREE, float(scale), H, Hkv, D)
     np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("n_past,qmul", [(0, 1.0), (1, 3.0), (300, 1.0), (700, 3.0), (4096, 1.0)])
+def test_exact_contract_is_attention_up_to_f16_probabilities(n_past, qmul):
+    # the contract rounds every probability to f16 (relative error <= 2^-11,
+    # as ggml's f16 vec_dot_type does) and the scores to 15-bit fixed point:
+    # |exact - f64| <= 2^-10 * max|v| bounds both (sum of p is 1)
+    rng = np.random.default_rng(n_past + 7)
+    H, Hkv, D = 8, 2, 64
+    T = len(TREE)
+    k, v = _cache(rng, n_past + T, Hkv, D)
+    q = (qmul * rng.normal(size=(T, H, D))).astype(np.float32)
+    scale = np.float32(1) / np.sqrt(np.float32(D))
+    a = cpvo.attn(q, k, v, n_past, TREE, scale)
+    b = cpvo.attn(q, k, v, n_past, TREE, scale, f64=True)
+    bound = 2.0 ** -10 * np.abs(cpvo.f16_bits_to_f32(v)).max()
+    assert np.abs(a - b).max() <= bound
+
+
+@pytest.mark.parametrize("n_past", [0, 255, 256, 700, 2047])
+def test_exact_contract_uniform_weights_closed_form(n_past):
+    # q = 0: every visible score is 0, so e = 1, Z = n 2^G, inv = (float)(1/n) and
+    # p = f16(inv); with v = 1 every chunk's fma chain and the chunk fold are
+    # exact sums of p, so out = n * f16((float)(1/n)) exactly.  A dropped or
+    # repeated row or chunk, or a missing f16 rounding of p, breaks the equality.
+    rng = np.random.default_rng(n_past)
+    H, Hkv, D, T = 4, 2, 32, 3
+    n = n_past + T
+    k = cpvo.f32_to_f16_bits(rng.normal(size=(n, Hkv * D)).astype(np.float32))
+    v = cpvo.f32_to_f16_bits(np.ones((n, Hkv * D), np.float32))
+    q = np.zeros((T, H, D), np.float32)
+    out = cpvo.attn(q, k, v, n_past, None, 0.5)
+    for t in range(T):
+        nv = n_past + t + 1
+        p16 = float(cpvo.f16_bits_to_f32(cpvo.f32_to_f16_bits(np.array([1.0 / nv], np.float32)))[0])
+        assert np.all(out[t] == np.float32(nv * p16)), (t, out[t][:3], nv * p16)
 
 
 def test_linear_chain_equals_tree_with_linear_parents():
@@ -140,3 +176,4 @@ def test_single_visible_row_returns_its_value():
     out = cpvo.attn(q, k, v, 0, None, 0.3)
     vv = cpvo.f16_bits_to_f32(v)[0]
     assert np.array_equal(out[0, :D], vv) and np.array_equal(out[0, D:], vv)
+
