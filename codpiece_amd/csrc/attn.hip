@@ -1,29 +1,26 @@
 // attn.hip — tree-masked GQA attention over the f16 KV cache, exact and
-// order-free: the same bits whatever the grid, the split of the KV axis or
-// the number of query rows in a call.
+// order-free: the same bits whatever the grid or the number of query rows in
+// a call (the oracle's cpvo_attn states the contract).
 //
 // Replaces the attention of build_attn_block (crates/codpiece-model/src/
-// qwen35.rs:3182-3199): ggml_flash_attn_ext with prec F32 by default (the
-// session's fa flag, qwen35.rs:534), or mul_mat(k, q) -> soft_max_ext(scale,
-// mask) -> mul_mat(v, p).  Both ggml CPU paths round q to f16 (the f16
-// cache's vec_dot_type) and sum in an order set by the SIMD width (and the
-// FA kernel accumulates p.v in f16).  The contract here keeps the f16 q and
-// makes every sum exact or fixed-order (the oracle's cpvo_attn states it):
+// qwen35.rs:3182-3199), by default ggml_flash_attn_ext with prec F32 (the
+// session's fa flag, qwen35.rs:534): q rounded to f16, weights expf(s - max),
+// the normalisation deferred to the end.  Here every sum is exact or in a
+// fixed order:
 //  1. scores: q16 and each cache row k16 become 15-bit fixed point relative
 //     to their own largest element (qf = rint(q16 2^(14-Eq)), kf likewise);
 //     s = (float)(sum_d qf kf * 2^(Eq+Ek-28)), the sum exact -- here on the
-//     int8 MFMA with two signed 8-bit limbs per operand.
-//  2. w = s * scale, mx = max over visible rows, e = expf(w - mx).
-//  3. Z = sum rint(e 2^G) exactly (G = 62 - ceil_log2(n_vis + 1)),
-//     inv = (float)(1 / (Z 2^-G)), p = f16(e * inv).
-//  4. per 256-row chunk of the cache (absolute rows) P_c = fma chain over its
-//     rows in increasing order; out = ((0 + P_0) + P_1) + ... in f32.
+//     int8 MFMA with two signed 8-bit limbs per operand; w = s * scale.
+//  2. per chunk c of 128 cache rows (absolute rows), over its visible rows:
+//     m_c = max w, e = expf(w - m_c), p = f16(e), P_c = fma chain of p v in
+//     row order, Z_c = sum rint(e 2^54) exactly.
+//  3. M = max m_c, f_c = expf(m_c - M); in chunk order Zt += (Z_c 2^-54) f_c
+//     (binary64) and O = fma(P_c, f_c, O) (f32); out = O * (float)(1 / Zt).
 //
-// Kernels: scores (grid: chunk x KV head x 32-row query block), softmax (one
-// block per query row), pv (chunk x KV head x 8-row groups; lane = d), fold
-// (per output element).  Scratch in the context workspace: w [T*H][n] f32,
-// p [h_kv][n][LRp] f16 (LRp = query rows of a KV head, padded to 8),
-// partials [chunks][T*H][D] f32.
+// Kernels: chunk (grid: chunk x KV head x 32-row query block; scores on the
+// MFMA, then the chunk's softmax and its P_c in the same workgroup) and fold
+// (one block per query row).  Scratch in the context workspace: P [chunks][T*H][D]
+// f32, m [chunks][T*H] f32, Z [chunks][T*H] int64.
 //
 // Layout.  K is [n_ctx][h_kv * d]; V is the transposed cache [h_kv * d][v_stride]
 // (the reference's non-FA V layout, qwen35.rs:580-586): the KV axis is
@@ -36,7 +33,8 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int CHUNK = 256;          // cache rows per chunk (the fold unit of the contract)
+constexpr int CHUNK = 128;          // cache rows per chunk (the unit of the contract)
+constexpr int ZBITS = 54;           // 62 - ceil_log2(CHUNK + 1)
 constexpr int QB = 32;              // query rows per scores workgroup
 constexpr int E_EMPTY = -100000;    // exponent of an all-zero vector
 
@@ -74,85 +72,113 @@ __device__ __forceinline__ void limbs(float v, int e, int8_t* hi, int8_t* lo)
     *lo = (int8_t)(f - 256 * h);
 }
 
-struct ScoreArgs {
+struct ChunkArgs {
     const float* q;           // [T][H][D]
     const uint16_t* kc;       // [n_ctx][Hkv*D]
+    const uint16_t* vt;       // [Hkv*D][v_stride]
     const int32_t* parent;    // [T] or null
-    float* w;                 // [T*H][n]  scaled scores, -inf where invisible
-    int64_t n_past, n;        // n = n_past + T rows in play
+    float* P;                 // [chunks][T*H][D]
+    float* mc;                // [chunks][T*H]
+    long long* zc;            // [chunks][T*H]
+    int64_t n_past, n, v_stride;   // n = n_past + T rows in play
     int T, H, Hkv;
     float scale;
 };
 
-// scores of 32 query rows (of one KV head) against one 256-row chunk
+// pack 16 limbs of one kind into 4 dwords and store them as one 16-byte LDS write
+__device__ __forceinline__ void store16(int8_t* dst, const int8_t* v)
+{
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        w[i] = (uint32_t)(uint8_t)v[4 * i] | ((uint32_t)(uint8_t)v[4 * i + 1] << 8) |
+               ((uint32_t)(uint8_t)v[4 * i + 2] << 16) | ((uint32_t)(uint8_t)v[4 * i + 3] << 24);
+    *(uint4*)dst = uint4{w[0], w[1], w[2], w[3]};
+}
+
+// the limbs of 16 f16-exact values at the exponent of the largest |value| of
+// their row (a row spans TPR consecutive lanes)
+template <int TPR>
+__device__ __forceinline__ int row_limbs(const float* v, int8_t* hi, int8_t* lo)
+{
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(v[i]));
+    for (int off = 1; off < TPR; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    int e = E_EMPTY;
+    if (mx > 0.0f) frexpf(mx, &e);
+#pragma unroll
+    for (int i = 0; i < 16; i++) limbs(v[i], e, &hi[i], &lo[i]);
+    return e;
+}
+
+// one 128-row chunk of the cache against 32 query rows of one KV head
+constexpr int CT = 512;             // threads of a chunk workgroup (8 waves)
+
 template <int D>
-__global__ __launch_bounds__(256) void attn_scores_kernel(ScoreArgs a)
+__global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
 {
     constexpr int TPR = D / 16;                // threads per row when converting (16 values each)
-    constexpr int RPP = 256 / TPR;             // rows per pass
+    constexpr int RPP = CT / TPR;              // rows per pass
     __shared__ __align__(16) int8_t s_qh[QB][D], s_ql[QB][D];
     __shared__ __align__(16) int8_t s_kh[CHUNK][D], s_kl[CHUNK][D];
+    __shared__ __align__(16) float s_w[QB][CHUNK];     // scores
+    __shared__ __align__(16) float s_pt[CHUNK][QB];    // the f16-rounded weights (as f32), row-minor
     __shared__ int s_eq[QB], s_ek[CHUNK];
+    __shared__ unsigned long long s_anc[QB];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = blockIdx.x, kh = blockIdx.y;
     const int G = a.H / a.Hkv, LR = G * a.T;
     const int64_t j0 = (int64_t)c * CHUNK;
+    const int nj = (int)(a.n - j0 < CHUNK ? a.n - j0 : CHUNK);
     const int sub = tid % TPR;
+    const bool tree = a.parent != nullptr;
 
-    // ---- query rows lr = blockIdx.z * 32 + r: t = lr / G, head kh * G + lr % G
+    // ---- query rows lr = blockIdx.z * 32 + r: token t = lr / G, head kh * G + lr % G
     for (int r = tid / TPR; r < QB; r += RPP) {
         const int lr = blockIdx.z * QB + r;
         float v[16];
-        float mx = 0.0f;
         if (lr < LR) {
             const int t = lr / G, h = kh * G + lr % G;
             const float* src = a.q + ((int64_t)t * a.H + h) * D + sub * 16;
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                v[i] = cpv_h2f(cpv_f2h(src[i]));
-                mx = fmaxf(mx, fabsf(v[i]));
-            }
+            for (int i = 0; i < 16; i++) v[i] = cpv_h2f(cpv_f2h(src[i]));
         } else {
 #pragma unroll
             for (int i = 0; i < 16; i++) v[i] = 0.0f;
         }
-        for (int off = 1; off < TPR; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-        int e = E_EMPTY;
-        if (mx > 0.0f) frexpf(mx, &e);
-#pragma unroll
-        for (int i = 0; i < 16; i++) limbs(v[i], e, &s_qh[r][sub * 16 + i], &s_ql[r][sub * 16 + i]);
-        if (sub == 0) s_eq[r] = e;
+        int8_t hi[16], lo[16];
+        const int e = row_limbs<TPR>(v, hi, lo);
+        store16(&s_qh[r][sub * 16], hi);
+        store16(&s_ql[r][sub * 16], lo);
+        if (sub == 0) {
+            s_eq[r] = e;
+            s_anc[r] = (tree && lr < LR) ? ancestors(a.parent, lr / G) : 0ull;
+        }
     }
     // ---- the chunk's cache rows of this KV head
     for (int r = tid / TPR; r < CHUNK; r += RPP) {
-        const int64_t j = j0 + r;
         float v[16];
-        float mx = 0.0f;
-        if (j < a.n) {
-            const uint16_t* src = a.kc + j * (int64_t)a.Hkv * D + (int64_t)kh * D + sub * 16;
+        if (r < nj) {
+            const uint16_t* src = a.kc + (j0 + r) * (int64_t)a.Hkv * D + (int64_t)kh * D + sub * 16;
             const uint4 p0 = *(const uint4*)src, p1 = *(const uint4*)(src + 8);
             const uint32_t wds[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                v[i] = cpv_h2f((uint16_t)(wds[i >> 1] >> (16 * (i & 1))));
-                mx = fmaxf(mx, fabsf(v[i]));
-            }
+            for (int i = 0; i < 16; i++) v[i] = cpv_h2f((uint16_t)(wds[i >> 1] >> (16 * (i & 1))));
         } else {
 #pragma unroll
             for (int i = 0; i < 16; i++) v[i] = 0.0f;
         }
-        for (int off = 1; off < TPR; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-        int e = E_EMPTY;
-        if (mx > 0.0f) frexpf(mx, &e);
-#pragma unroll
-        for (int i = 0; i < 16; i++) limbs(v[i], e, &s_kh[r][sub * 16 + i], &s_kl[r][sub * 16 + i]);
+        int8_t hi[16], lo[16];
+        const int e = row_limbs<TPR>(v, hi, lo);
+        store16(&s_kh[r][sub * 16], hi);
+        store16(&s_kl[r][sub * 16], lo);
         if (sub == 0) s_ek[r] = e;
     }
     __syncthreads();
 
-    // ---- 2 x 16 output blocks of 16 x 16 (query rows x cache rows); 4 waves, 8 blocks each
-    const bool tree = a.parent != nullptr;
-    for (int blk = wave; blk < 2 * (CHUNK / 16); blk += 4) {
+    // ---- scores: 2 x 8 blocks of 16 x 16 (query rows x cache rows), 2 per wave
+    for (int blk = wave; blk < 2 * (CHUNK / 16); blk += CT / 64) {
         const int qb = blk & 1, jb = blk >> 1;
         v4i hh = {0, 0, 0, 0}, mix = {0, 0, 0, 0}, ll = {0, 0, 0, 0};
         const int ar = qb * 16 + (lane & 15), bc = jb * 16 + (lane & 15), kg = (lane >> 4) * 16;
@@ -165,172 +191,183 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(ScoreArgs a)
             mix = __builtin_amdgcn_mfma_i32_16x16x64_i8(qlv, khv, mix, 0, 0, 0);
             ll = __builtin_amdgcn_mfma_i32_16x16x64_i8(qlv, klv, ll, 0, 0, 0);
         }
-        // lane holds rows 4 (lane/16) + i of the query block, cache row bc
-        const int64_t j = j0 + bc;
-        if (j >= a.n) continue;
+        // lane holds query rows 4 (lane/16) + i of the block, cache row bc
         const int ek = s_ek[bc];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int r = qb * 16 + 4 * (lane >> 4) + i;
             const int lr = blockIdx.z * QB + r;
-            if (lr >= LR) continue;
-            const int t = lr / G, h = kh * G + lr % G;
-            const uint64_t anc = tree ? ancestors(a.parent, t) : 0;
             float w = -INFINITY;
-            if (visible(j, a.n_past, t, tree, anc)) {
+            if (lr < LR && bc < nj && visible(j0 + bc, a.n_past, lr / G, tree, s_anc[r])) {
                 const int eq = s_eq[r];
-                float s = 0.0f;
+                float sc = 0.0f;
                 if (eq != E_EMPTY && ek != E_EMPTY) {
                     const int64_t S = (int64_t)hh[i] * 65536 + (int64_t)mix[i] * 256 + (int64_t)ll[i];
-                    s = (float)ldexp((double)S, eq + ek - 28);
+                    sc = (float)ldexp((double)S, eq + ek - 28);
                 }
-                w = s * a.scale;
+                w = sc * a.scale;
             }
-            a.w[((int64_t)t * a.H + h) * a.n + j] = w;
+            s_w[r][bc] = w;
         }
     }
-}
-
-// one query row: max, exact normaliser, f16 probabilities (transposed per KV head)
-__global__ __launch_bounds__(256) void attn_softmax_kernel(const float* __restrict__ w, int64_t n, int T, int H,
-                                                           int Hkv, int LRp, uint16_t* __restrict__ p)
-{
-    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t = row / H, h = row % H, G = H / Hkv, kh = h / G, lr = t * G + h % G;
-    const float* wr = w + (int64_t)row * n;
-    __shared__ float s_m[4];
-    __shared__ long long s_z[4];
-    __shared__ int s_c[4];
-    float mx = -INFINITY;
-    int cnt = 0;
-    for (int64_t j = tid; j < n; j += 256) {
-        const float v = wr[j];
-        if (v != -INFINITY) { mx = fmaxf(mx, v); cnt++; }
-    }
-    for (int off = 32; off > 0; off >>= 1) {
-        mx = fmaxf(mx, __shfl_xor(mx, off));
-        cnt += __shfl_xor(cnt, off);
-    }
-    if (lane == 0) { s_m[wave] = mx; s_c[wave] = cnt; }
     __syncthreads();
-    mx = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
-    const int nvis = s_c[0] + s_c[1] + s_c[2] + s_c[3];
-    const int Gz = 62 - ceil_log2_dev(nvis + 1);
-    long long Z = 0;
-    for (int64_t j = tid; j < n; j += 256) {
-        const float v = wr[j];
-        if (v != -INFINITY) Z += (long long)rint(ldexp((double)cpv_expf(v - mx), Gz));
-    }
-    for (int off = 32; off > 0; off >>= 1) Z += __shfl_xor(Z, off);
-    if (lane == 0) s_z[wave] = Z;
-    __syncthreads();
-    Z = s_z[0] + s_z[1] + s_z[2] + s_z[3];
-    const float inv = (float)(1.0 / ldexp((double)Z, -Gz));
-    uint16_t* pr = p + (int64_t)kh * n * LRp + lr;
-    for (int64_t j = tid; j < n; j += 256) {
-        const float v = wr[j];
-        pr[j * LRp] = v == -INFINITY ? (uint16_t)0 : cpv_f2h(cpv_expf(v - mx) * inv);
-    }
-}
 
-// P_c for 8 query rows x D of one KV head and one chunk: lane = d, an fma chain over
-// the chunk's rows in increasing order; the p of the 8 rows at a cache row is one
-// uniform 16-byte load
-template <int D>
-__global__ __launch_bounds__(256) void attn_pv_kernel(const uint16_t* __restrict__ vt, int64_t v_stride,
-                                                      const uint16_t* __restrict__ p, int64_t n, int LR, int LRp,
-                                                      int T, int H, int Hkv, float* __restrict__ part)
-{
+    // ---- the chunk's softmax: 16 threads per query row, 8 cache rows each
+    {
+        const int r = tid >> 4, part = tid & 15;
+        const int lr = blockIdx.z * QB + r;
+        float m = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 8; i++) m = fmaxf(m, s_w[r][part * 8 + i]);
+        for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+        long long z = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int jl = part * 8 + i;
+            const float w = s_w[r][jl];
+            float p = 0.0f;
+            if (w != -INFINITY) {
+                const float e = cpv_expf(w - m);
+                p = cpv_h2f(cpv_f2h(e));
+                z += (long long)rint(ldexp((double)e, ZBITS));
+            }
+            s_pt[jl][r] = p;
+        }
+        for (int off = 1; off < 16; off <<= 1) z += __shfl_xor(z, off);
+        if (part == 0 && lr < LR) {
+            const int t = lr / G, h = kh * G + lr % G;
+            const int64_t row = (int64_t)c * a.T * a.H + (int64_t)t * a.H + h;
+            a.mc[row] = m;
+            a.zc[row] = z;
+        }
+    }
+    __syncthreads();
+
+    // ---- P_c: 8 query rows x 64 d per wave (lane = d), fma chain over the chunk's rows in order
     constexpr int WPR = D / 64;                // waves per 8-row group
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int c = blockIdx.x, kh = blockIdx.y;
-    const int grp = blockIdx.z * (4 / WPR) + wave / WPR;   // 8-row group of this wave
-    const int lr0 = grp * 8;
-    if (lr0 >= LR) return;
-    const int d = (wave % WPR) * 64 + lane;
-    const int64_t j0 = (int64_t)c * CHUNK, j1 = j0 + CHUNK < n ? j0 + CHUNK : n;
-    const uint16_t* vrow = vt + ((int64_t)kh * D + d) * v_stride;
-    const uint16_t* pb = p + (int64_t)kh * n * LRp + lr0;
-    float acc[8];
+    for (int g8 = wave / WPR; g8 < QB / 8; g8 += (CT / 64) / WPR) {
+        const int r0 = g8 * 8;
+        if (blockIdx.z * QB + r0 >= LR) break;
+        const int d = (wave % WPR) * 64 + lane;
+        const uint16_t* vrow = a.vt + ((int64_t)kh * D + d) * a.v_stride + j0;
+        float acc[8];
 #pragma unroll
-    for (int r = 0; r < 8; r++) acc[r] = 0.0f;
-    int64_t j = j0;
-    for (; j + 8 <= j1; j += 8) {
-        const uint4 vv = *(const uint4*)(vrow + j);
-        const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+        for (int i = 0; i < 8; i++) acc[i] = 0.0f;
+        int jl = 0;
+        for (; jl + 8 <= nj; jl += 8) {
+            const uint4 vv = *(const uint4*)(vrow + jl);
+            const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
-        for (int jj = 0; jj < 8; jj++) {
-            const float v = cpv_h2f((uint16_t)(vw[jj >> 1] >> (16 * (jj & 1))));
-            const uint4 pp = *(const uint4*)(pb + (j + jj) * LRp);
-            const uint32_t pw[4] = {pp.x, pp.y, pp.z, pp.w};
+            for (int jj = 0; jj < 8; jj++) {
+                const float v = cpv_h2f((uint16_t)(vw[jj >> 1] >> (16 * (jj & 1))));
+                const float4 p0 = *(const float4*)&s_pt[jl + jj][r0], p1 = *(const float4*)&s_pt[jl + jj][r0 + 4];
+                const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
-            for (int r = 0; r < 8; r++) acc[r] = fmaf(cpv_h2f((uint16_t)(pw[r >> 1] >> (16 * (r & 1)))), v, acc[r]);
+                for (int i = 0; i < 8; i++) acc[i] = fmaf(pv[i], v, acc[i]);
+            }
+        }
+        for (; jl < nj; jl++) {
+            const float v = cpv_h2f(vrow[jl]);
+            const float4 p0 = *(const float4*)&s_pt[jl][r0], p1 = *(const float4*)&s_pt[jl][r0 + 4];
+            const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[i] = fmaf(pv[i], v, acc[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int lr = blockIdx.z * QB + r0 + i;
+            if (lr >= LR) break;
+            const int t = lr / G, h = kh * G + lr % G;
+            a.P[(((int64_t)c * a.T + t) * a.H + h) * D + d] = acc[i];
         }
     }
-    for (; j < j1; j++) {
-        const float v = cpv_h2f(vrow[j]);
-        const uint4 pp = *(const uint4*)(pb + j * LRp);
-        const uint32_t pw[4] = {pp.x, pp.y, pp.z, pp.w};
-#pragma unroll
-        for (int r = 0; r < 8; r++) acc[r] = fmaf(cpv_h2f((uint16_t)(pw[r >> 1] >> (16 * (r & 1)))), v, acc[r]);
-    }
-    const int G = H / Hkv;
-#pragma unroll
-    for (int r = 0; r < 8; r++) {
-        const int lr = lr0 + r;
-        if (lr >= LR) break;
-        const int t = lr / G, h = kh * G + lr % G;
-        part[((int64_t)c * T * H + (int64_t)t * H + h) * D + d] = acc[r];
-    }
 }
 
-// out = ((0 + P_0) + P_1) + ... in chunk order
-__global__ __launch_bounds__(256) void attn_fold_kernel(const float* __restrict__ part, int nchunk, int64_t total,
-                                                        float* __restrict__ out)
+// one query row: the chunks folded in order, then the normalisation.  The
+// chunk maxima, sums and factors are staged in LDS; empty chunks (no visible
+// row) carry factor 0 and zero partials, which leave both folds unchanged.
+template <int D>
+__global__ __launch_bounds__(D) void attn_fold_kernel(const float* __restrict__ P, const float* __restrict__ mc,
+                                                      const long long* __restrict__ zc, int nchunk, int rows,
+                                                      float* __restrict__ out)
 {
-    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (e >= total) return;
+    extern __shared__ double s_dyn[];          // [nchunk] Z_c 2^-ZBITS, then [nchunk] factors f_c
+    double* s_z = s_dyn;
+    float* s_f = (float*)(s_dyn + nchunk);
+    __shared__ float s_red[D / 64];
+    __shared__ float s_inv;
+    const int row = blockIdx.x, d = threadIdx.x, lane = d & 63, wave = d >> 6;
+    float M = -INFINITY;
+    for (int c = d; c < nchunk; c += D) {
+        const float m = mc[(int64_t)c * rows + row];
+        s_f[c] = m;
+        s_z[c] = ldexp((double)zc[(int64_t)c * rows + row], -ZBITS);
+        M = fmaxf(M, m);
+    }
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+    if (lane == 0) s_red[wave] = M;
+    __syncthreads();
+    M = s_red[0];
+    for (int i = 1; i < D / 64; i++) M = fmaxf(M, s_red[i]);
+    for (int c = d; c < nchunk; c += D) {
+        const float m = s_f[c];
+        s_f[c] = m == -INFINITY ? 0.0f : cpv_expf(m - M);
+    }
+    __syncthreads();
+    if (d == 0) {
+        double Zt = 0.0;
+        for (int c = 0; c < nchunk; c++) Zt = Zt + s_z[c] * (double)s_f[c];
+        s_inv = (float)(1.0 / Zt);
+    }
     float o = 0.0f;
-    for (int c = 0; c < nchunk; c++) o = o + part[(int64_t)c * total + e];
-    out[e] = o;
+    const float* pr = P + (int64_t)row * D + d;
+    const int64_t cs = (int64_t)rows * D;
+    int c = 0;
+    for (; c + 8 <= nchunk; c += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = pr[(c + i) * cs];
+#pragma unroll
+        for (int i = 0; i < 8; i++) o = fmaf(v[i], s_f[c + i], o);
+    }
+    for (; c < nchunk; c++) o = fmaf(pr[c * cs], s_f[c], o);
+    __syncthreads();
+    out[(int64_t)row * D + d] = o * s_inv;
 }
 
-// one call over T query tokens (the scratch holds T*H rows)
+// one call over T query tokens (the scratch holds T*H rows per chunk)
 template <int D>
 cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                       int64_t n_past, const int32_t* parent, int T, int H, int Hkv, float scale, float* out)
 {
     const int64_t n = n_past + T;
-    const int G = H / Hkv, LR = G * T, LRp = (LR + 7) / 8 * 8;
+    const int G = H / Hkv, LR = G * T, rows = T * H;
     const int nchunk = (int)((n + CHUNK - 1) / CHUNK);
-    const size_t w_b = ((size_t)T * H * n * 4 + 255) & ~(size_t)255;
-    const size_t p_b = ((size_t)Hkv * n * LRp * 2 + 255) & ~(size_t)255;
-    const size_t part_b = (size_t)nchunk * T * H * D * 4;
+    const size_t P_b = ((size_t)nchunk * rows * D * 4 + 255) & ~(size_t)255;
+    const size_t m_b = ((size_t)nchunk * rows * 4 + 255) & ~(size_t)255;
+    const size_t z_b = (size_t)nchunk * rows * 8;
     void* ws = nullptr;
-    cpv_status st = cpv_workspace(ctx, w_b + p_b + part_b, &ws);
+    cpv_status st = cpv_workspace(ctx, P_b + m_b + z_b, &ws);
     if (st != CPV_OK) return st;
-    float* w = (float*)ws;
-    uint16_t* p = (uint16_t*)((uint8_t*)ws + w_b);
-    float* part = (float*)((uint8_t*)ws + w_b + p_b);
-    ScoreArgs sa;
-    sa.q = q;
-    sa.kc = kc;
-    sa.parent = parent;
-    sa.w = w;
-    sa.n_past = n_past;
-    sa.n = n;
-    sa.T = T;
-    sa.H = H;
-    sa.Hkv = Hkv;
-    sa.scale = scale;
-    attn_scores_kernel<D><<<dim3((unsigned)nchunk, (unsigned)Hkv, (unsigned)((LR + QB - 1) / QB)), 256, 0,
-                            ctx->stream>>>(sa);
-    attn_softmax_kernel<<<(unsigned)(T * H), 256, 0, ctx->stream>>>(w, n, T, H, Hkv, LRp, p);
-    const int rows_per_block = 8 * (4 / (D / 64));
-    attn_pv_kernel<D><<<dim3((unsigned)nchunk, (unsigned)Hkv, (unsigned)((LR + rows_per_block - 1) / rows_per_block)),
-                        256, 0, ctx->stream>>>(vt, v_stride, p, n, LR, LRp, T, H, Hkv, part);
-    const int64_t total = (int64_t)T * H * D;
-    attn_fold_kernel<<<(unsigned)((total + 255) / 256), 256, 0, ctx->stream>>>(part, nchunk, total, out);
+    ChunkArgs ca;
+    ca.q = q;
+    ca.kc = kc;
+    ca.vt = vt;
+    ca.parent = parent;
+    ca.P = (float*)ws;
+    ca.mc = (float*)((uint8_t*)ws + P_b);
+    ca.zc = (long long*)((uint8_t*)ws + P_b + m_b);
+    ca.n_past = n_past;
+    ca.n = n;
+    ca.v_stride = v_stride;
+    ca.T = T;
+    ca.H = H;
+    ca.Hkv = Hkv;
+    ca.scale = scale;
+    attn_chunk_kernel<D><<<dim3((unsigned)nchunk, (unsigned)Hkv, (unsigned)((LR + QB - 1) / QB)), CT, 0,
+                           ctx->stream>>>(ca);
+    attn_fold_kernel<D><<<(unsigned)rows, D, (size_t)nchunk * 12, ctx->stream>>>(ca.P, ca.mc, ca.zc, nchunk, rows,
+                                                                              out);
     CPV_HIP(ctx, hipGetLastError());
     return CPV_OK;
 }
@@ -343,7 +380,8 @@ cpv_status attn_run(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint
     // a long chain runs in token blocks to bound the scratch: node t of a chain sees
     // the rows <= n_past + t, which is what a block starting at t0 sees with n_past + t0
     const int64_t n = n_past + t;
-    int64_t tb = ((int64_t)192 << 20) / ((int64_t)h * n * 4 + 1);
+    const int64_t per_token = (int64_t)h * ((n + CHUNK - 1) / CHUNK) * (D * 4 + 12);
+    int64_t tb = ((int64_t)192 << 20) / (per_token + 1);
     if (tb < 1) tb = 1;
     if (tb > t) tb = t;
     for (int t0 = 0; t0 < t; t0 += (int)tb) {

@@ -114,7 +114,8 @@ void     cpvo_rope_neox(float* x, int n_rot, const float* cs_row);
  * cpvo_attn is the exact-window contract (cpvo_glue.c), order-free;
  * cpvo_attn_f64 the same attention in binary64 (q rounded to f16), the
  * accuracy reference. */
-#define CPVO_ATTN_CHUNK 256
+#define CPVO_ATTN_CHUNK 128
+#define CPVO_ATTN_ZBITS 54   /* 62 - ceil_log2(CHUNK + 1): a chunk's sum stays below 2^62 */
 void     cpvo_attn(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n_past,
                    const int32_t* parent, int T, int H, int Hkv, int D, float scale,
                    float* out);

@@ -262,7 +262,7 @@ def rope_neox(x, n_rot, cs_row):
     return x
 
 
-ATTN_CHUNK = 256
+ATTN_CHUNK = 128
 
 
 def attn(q, kc, vc, n_past, parent, scale, f64=False):

@@ -170,25 +170,27 @@ void cpvo_attn_f64(const float* q, const uint16_t* kc, const uint16_t* vc, int64
 }
 
 /* The exact-window attention contract (what the device computes, bit for
- * bit, in any launch configuration).  ggml's CPU path (the reference's
- * build_attn_block, qwen35.rs:3100-3140: mul_mat(k, q), soft_max_ext with
- * the kq scale and the mask, mul_mat(v^T, kq)) rounds q and the
- * probabilities to f16 (vec_dot_type of an f16 cache) and sums in an order
- * set by its SIMD width; this restatement keeps those roundings and fixes the
- * sums so that any order gives the same bits:
+ * bit, in any launch configuration).  The reference's default attention is
+ * ggml_flash_attn_ext with prec F32 (qwen35.rs:534, 3182-3187), whose CPU
+ * kernel rounds q to f16 (the f16 cache's vec_dot_type), keeps a running
+ * max, weights V by expf(s - max) and divides by the sum of the weights at
+ * the end, summing in an order set by its SIMD width (and, for an f16 cache,
+ * accumulating V in f16).  This restatement keeps the f16 q and the deferred
+ * normalisation and fixes every sum, chunk by chunk:
  *  1. q16 = f16(q).  Per query head, Eq = frexp exponent of max|q16|,
  *     qf = rint(q16 * 2^(14 - Eq)) (|qf| <= 2^14).  Per cache row j and KV
  *     head, Ek = exponent of max|k16|, kf = rint(k16 * 2^(14 - Ek)).  The
  *     score is s_j = (float)(sum_d qf*kf * 2^(Eq + Ek - 28)), the integer sum
- *     exact (|sum| < 2^36).  An all-zero q head or k row scores 0.
- *  2. w_j = s_j * scale (f32) for visible rows; mx = max w; e_j = expf(w_j -
- *     mx) with the glibc expf restatement.
- *  3. Z = sum over visible j of rint(e_j * 2^G), G = 62 - ceil_log2(n_vis + 1),
- *     exact in int64; inv = (float)(1 / (Z * 2^-G)); p_j = f16(e_j * inv).
- *  4. out_d: for each chunk of CPVO_ATTN_CHUNK consecutive cache rows (by
- *     absolute row index) P_c = fmaf(p_j, v_jd, P_c) over its rows in
- *     increasing order from +0 (invisible rows have p = 0); then
- *     out_d = (((0 + P_0) + P_1) + ...) in f32.
+ *     exact (|sum| < 2^36); an all-zero q head or k row scores 0.
+ *     w_j = s_j * scale (f32).
+ *  2. Chunks of CPVO_ATTN_CHUNK consecutive cache rows (absolute row index).
+ *     For each chunk c with a visible row: m_c = max of its visible w;
+ *     e_j = expf(w_j - m_c) (the glibc expf restatement); p_j = f16(e_j);
+ *     P_c[d] = fmaf(p_j, v_jd, P_c[d]) over its visible rows in increasing
+ *     order from +0; Z_c = sum rint(e_j * 2^CPVO_ATTN_ZBITS), exact in int64.
+ *  3. M = max m_c; f_c = expf(m_c - M); over the chunks in increasing order
+ *     Zt = Zt + (Z_c * 2^-ZBITS) * f_c in binary64 from 0, and
+ *     O[d] = fmaf(P_c[d], f_c, O[d]) in f32 from +0; out[d] = O[d] * (float)(1 / Zt).
  * The f64 attention above is the accuracy reference this is tested against. */
 static int64_t ipow_exp(const uint16_t* h, int n)
 {
@@ -213,11 +215,12 @@ void cpvo_attn(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n
 #pragma omp parallel
     {
         float* w = malloc(sizeof(float) * (size_t)nmax);
-        float* p = malloc(sizeof(float) * (size_t)nmax);
         char* vis = malloc((size_t)T);
         uint16_t* q16 = malloc(sizeof(uint16_t) * (size_t)D);
         int64_t* qf = malloc(sizeof(int64_t) * (size_t)D);
-        float* P = malloc(sizeof(float) * (size_t)D);
+        float* P = malloc(sizeof(float) * (size_t)nchunk * D);
+        float* mc = malloc(sizeof(float) * (size_t)nchunk);
+        int64_t* Zc = malloc(sizeof(int64_t) * (size_t)nchunk);
 #pragma omp for schedule(dynamic)
         for (int th = 0; th < T * H; th++) {
             const int t = th / H, h = th % H, kh = h / g;
@@ -227,9 +230,7 @@ void cpvo_attn(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n
             const int64_t eq = ipow_exp(q16, D);
             for (int d = 0; d < D; d++)
                 qf[d] = eq == INT_MIN ? 0 : (int64_t)rint(ldexp((double)f16_tab[q16[d]], 14 - (int)eq));
-            /* 1-2: scores, scaled; max over visible rows */
-            float mx = -INFINITY;
-            int64_t nvis = 0;
+            /* 1: scores, scaled; -inf marks an invisible row */
             for (int64_t r = 0; r < nmax; r++) {
                 if (r >= n_past && !vis[r - n_past]) { w[r] = -INFINITY; continue; }
                 const uint16_t* kr = kc + r * row + (int64_t)kh * D;
@@ -242,32 +243,41 @@ void cpvo_attn(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n
                     s = (float)ldexp((double)S, (int)(eq + ek) - 28);
                 }
                 w[r] = s * scale;
-                if (w[r] > mx) mx = w[r];
-                nvis++;
             }
-            /* 3: exact normaliser, f16 probabilities */
-            const int G = 62 - ceil_log2_i(nvis + 1);
-            int64_t Z = 0;
-            for (int64_t r = 0; r < nmax; r++) {
-                if (w[r] == -INFINITY) { p[r] = 0.0f; continue; }
-                p[r] = cpvo_expf(w[r] - mx);
-                Z += (int64_t)rint(ldexp((double)p[r], G));
+            /* 2: per chunk */
+            float M = -INFINITY;
+            for (int64_t c = 0; c < nchunk; c++) {
+                const int64_t r0 = c * CPVO_ATTN_CHUNK;
+                const int64_t r1 = r0 + CPVO_ATTN_CHUNK < nmax ? r0 + CPVO_ATTN_CHUNK : nmax;
+                float m = -INFINITY;
+                for (int64_t r = r0; r < r1; r++) if (w[r] > m) m = w[r];
+                mc[c] = m;
+                Zc[c] = 0;
+                for (int d = 0; d < D; d++) P[c * D + d] = 0.0f;
+                if (m == -INFINITY) continue;
+                if (m > M) M = m;
+                for (int64_t r = r0; r < r1; r++) {
+                    if (w[r] == -INFINITY) continue;
+                    const float e = cpvo_expf(w[r] - m);
+                    const float p = f16_tab[cpvo_fp32_to_fp16(e)];
+                    Zc[c] += (int64_t)rint(ldexp((double)e, CPVO_ATTN_ZBITS));
+                    const uint16_t* vr = vc + r * row + (int64_t)kh * D;
+                    for (int d = 0; d < D; d++) P[c * D + d] = fmaf(p, f16_tab[vr[d]], P[c * D + d]);
+                }
             }
-            const float inv = (float)(1.0 / ldexp((double)Z, -G));
-            for (int64_t r = 0; r < nmax; r++) p[r] = f16_tab[cpvo_fp32_to_fp16(p[r] * inv)];
-            /* 4: chunked fixed-order fma chains, chunks folded in order */
+            /* 3: fold the chunks in order, normalise once */
             float* o = out + ((int64_t)t * H + h) * D;
+            double Zt = 0.0;
             for (int d = 0; d < D; d++) o[d] = 0.0f;
             for (int64_t c = 0; c < nchunk; c++) {
-                for (int d = 0; d < D; d++) P[d] = 0.0f;
-                const int64_t r1 = (c + 1) * CPVO_ATTN_CHUNK < nmax ? (c + 1) * CPVO_ATTN_CHUNK : nmax;
-                for (int64_t r = c * CPVO_ATTN_CHUNK; r < r1; r++) {
-                    const uint16_t* vr = vc + r * row + (int64_t)kh * D;
-                    for (int d = 0; d < D; d++) P[d] = fmaf(p[r], f16_tab[vr[d]], P[d]);
-                }
-                for (int d = 0; d < D; d++) o[d] = o[d] + P[d];
+                if (mc[c] == -INFINITY) continue;
+                const float f = cpvo_expf(mc[c] - M);
+                Zt = Zt + ldexp((double)Zc[c], -CPVO_ATTN_ZBITS) * (double)f;
+                for (int d = 0; d < D; d++) o[d] = fmaf(P[c * D + d], f, o[d]);
             }
+            const float inv = (float)(1.0 / Zt);
+            for (int d = 0; d < D; d++) o[d] = o[d] * inv;
         }
-        free(w); free(p); free(vis); free(q16); free(qf); free(P);
+        free(w); free(vis); free(q16); free(qf); free(P); free(mc); free(Zc);
     }
 }

@@ -124,12 +124,13 @@ def test_exact_contract_is_attention_up_to_f16_probabilities(n_past, qmul):
     assert np.abs(a - b).max() <= bound
 
 
-@pytest.mark.parametrize("n_past", [0, 255, 256, 700, 2047])
+@pytest.mark.parametrize("n_past", [0, 127, 128, 700, 2047])
 def test_exact_contract_uniform_weights_closed_form(n_past):
-    # q = 0: every visible score is 0, so e = 1, Z = n 2^G, inv = (float)(1/n) and
-    # p = f16(inv); with v = 1 every chunk's fma chain and the chunk fold are
-    # exact sums of p, so out = n * f16((float)(1/n)) exactly.  A dropped or
-    # repeated row or chunk, or a missing f16 rounding of p, breaks the equality.
+    # q = 0: every visible score is 0, so in every chunk m = 0, e = 1, p = 1,
+    # Z_c = (rows) 2^ZBITS and the chunk factors are 1; with v = 1 each chunk's
+    # fma chain is its row count and the fold their sum, so
+    # out = (float)n * (float)(1/n) exactly.  A dropped or repeated row or
+    # chunk, a wrong factor or a missing normalisation breaks the equality.
     rng = np.random.default_rng(n_past)
     H, Hkv, D, T = 4, 2, 32, 3
     n = n_past + T
@@ -139,8 +140,8 @@ def test_exact_contract_uniform_weights_closed_form(n_past):
     out = cpvo.attn(q, k, v, n_past, None, 0.5)
     for t in range(T):
         nv = n_past + t + 1
-        p16 = float(cpvo.f16_bits_to_f32(cpvo.f32_to_f16_bits(np.array([1.0 / nv], np.float32)))[0])
-        assert np.all(out[t] == np.float32(nv * p16)), (t, out[t][:3], nv * p16)
+        want = np.float32(np.float32(nv) * np.float32(1.0 / nv))
+        assert np.all(out[t] == want), (t, out[t][:3], want)
 
 
 def test_linear_chain_equals_tree_with_linear_parents():
