@@ -62,8 +62,8 @@ class RoundOut(ctypes.Structure):
     ]
 
 
-PROF_Q4_K, PROF_Q6_K, PROF_Q8_0, PROF_ATTN, PROF_CLASSES = 0, 1, 2, 3, 4
-PROF_NAMES = ("qgemm_q4_k", "qgemm_q6_k", "qgemm_q8_0", "attention")
+PROF_Q4_K, PROF_Q6_K, PROF_Q8_0, PROF_ATTN, PROF_SAMPLE, PROF_CLASSES = 0, 1, 2, 3, 4, 5
+PROF_NAMES = ("qgemm_q4_k", "qgemm_q6_k", "qgemm_q8_0", "attention", "sampler")
 
 
 class ProfStat(ctypes.Structure):
@@ -96,6 +96,7 @@ SIGNATURES = {
     "cpv_qgemm": (_INT, [_P, _P, _P, _I64, _P]),
     "cpv_attn": (_INT, [_P, _P, _P, _P, _I64, _I64, _P, _INT, _INT, _INT, _INT, _F32, _P]),
     "cpv_argmax_rows": (_INT, [_P, _P, _P, _I64, _I64, _P]),
+    "cpv_distribution": (_INT, [_P, _P, _INT, _INT, ctypes.POINTER(SamplerParams), _P, _INT, _P, _P, _P]),
     "cpv_spec_accept": (_INT, [_P, _P, _P, _P, _INT, _INT, _INT, ctypes.POINTER(SamplerParams), _INT,
                                _P, ctypes.c_uint64, _P, _P, _INT, _P, _P]),
     "cpv_model_create": (_INT, [_P, ctypes.POINTER(Hparams), ctypes.POINTER(_P)]),

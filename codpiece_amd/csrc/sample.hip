@@ -1,9 +1,1009 @@
-// sample.hip — speculative acceptance on the device.
+// sample.hip — target distributions and speculative acceptance on the device.
+//
+// The reference builds each target distribution on the host
+// (Sampler::build, crates/codpiece-sample/src/lib.rs:229-376) with f32
+// arithmetic whose sums are sequential folds in candidate order, and decides
+// a round with Dist::{prob_of, draw, draw_excluding} (:387-436) in the engine
+// loop (crates/codpiece-server/src/engine.rs:2326-2461).  Here one 1024-thread
+// workgroup builds the distribution of one verified row and a second kernel,
+// one workgroup per sequence, walks the drafts.  Results equal the CPU
+// sampler bit for bit:
+//
+//  * Sequential f32 sums without a sequential loop.  While a running sum s
+//    stays inside one binade [2^E, 2^(E+1)) every float there is a multiple
+//    of u = ulp(s), so fl(s + x) = s + u*round(x/u), where round is to
+//    nearest and a tie goes to the even multiple: the step depends on s only
+//    through the parity of s/u.  Each element is therefore a map on integers
+//    S -> S + d[S & 1], the maps compose associatively, and a block scan of
+//    them gives every prefix of the fold exactly.  The first element whose
+//    prefix would leave the binade is added in hardware f32 and the scan
+//    resumes from there in the new binade; sums of non-negative terms only
+//    climb, so there are at most ~40 such restarts.
+//  * Candidate order (logit descending, id ascending; cmp_desc, lib.rs:
+//    453-459) as a stream of sorted bands: a radix histogram over the 64-bit
+//    key (order-flipped logit bits, id) picks the next <= 16384 keys, which
+//    are gathered and bitonic-sorted in LDS.  Only as much of the order as
+//    the filter needs is produced.
+//  * exp is the glibc expf restatement (cpv_expf); divisions are IEEE; the
+//    library is built without contraction, so every a*b+c rounds twice as
+//    in the Rust source.
 #include "cpv_internal.h"
 
-extern "C" cpv_status cpv_spec_accept(cpv_ctx* ctx, const float*, const float*, const int32_t*, int, int, int,
-                                      const cpv_sampler_params*, int, const float*, uint64_t, const float*,
-                                      const int32_t*, int, int32_t*, int32_t*)
+#include <float.h>
+#include <math.h>
+
+namespace {
+
+constexpr int SB = 1024;               // threads per sampler workgroup
+constexpr int SWV = SB / 64;           // waves per workgroup
+constexpr int FIPT = 8;                // fold: elements per thread per pass
+constexpr uint32_t FTOP = 1u << 24;    // fold: ulps from 0 to the top of a binade
+constexpr uint32_t FSAT = 1u << 26;    // fold: saturation of a composed step
+constexpr int BAND = 16384;            // sorted band held in LDS as u64 keys
+constexpr int HIST_MAX = 4096;         // penalty window input limit (4 per thread)
+constexpr int VMAX = 262144;           // ids fit the low 18 bits of a key
+constexpr size_t SAMPLE_LDS_KEYS = (size_t)BAND * 8;
+
+// ------------------------------------------------------------ block scratch
+struct FMap { uint32_t d0, d1; };      // S -> S + (S even ? d0 : d1)
+
+struct Small {
+    FMap wtot[SWV];
+    unsigned long long slot[2][2];     // per pass: first binade exit, first predicate hit
+    uint32_t scan[SWV];
+    float wf[SWV];
+    int wi[SWV];
+    int iv[8];
+};
+
+// the step of m for an S of parity par (arithmetic select: a ?: on the two
+// fields lets the compiler address a register array by parity)
+__device__ __forceinline__ uint32_t fsel(FMap m, uint32_t par)
 {
-    return cpv_fail(ctx, CPV_EUNSUPPORTED, "spec_accept: not built yet");
+    return m.d0 ^ ((m.d0 ^ m.d1) & (0u - (par & 1u)));
+}
+
+// f then g
+__device__ __forceinline__ FMap fcomp(FMap f, FMap g)
+{
+    const uint32_t a = f.d0 + fsel(g, f.d0);
+    const uint32_t b = f.d1 + fsel(g, f.d1 + 1u);
+    return {a < FSAT ? a : FSAT, b < FSAT ? b : FSAT};
+}
+
+// the step x/u rounded to nearest, for x >= 0 finite and u = 2^(eb - 150)
+// (eb = the biased exponent of the binade, 1 for the subnormal range)
+__device__ __forceinline__ FMap fmap_of(float x, int eb)
+{
+    const uint32_t xb = __float_as_uint(x);
+    int xe = (int)(xb >> 23);
+    uint32_t m = xb & 0x7fffffu;
+    if (xe == 0) xe = 1;
+    else m |= 0x800000u;
+    const int sh = eb - xe;                      // x/u = m * 2^-sh
+    if (sh <= 0) {
+        if (m == 0) return {0, 0};
+        const uint32_t X = (-sh >= 3) ? FSAT : (m << (-sh));
+        return {X, X};
+    }
+    if (sh >= 26) return {0, 0};                 // below a quarter ulp
+    const uint32_t q = m >> sh, rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1);
+    if (rem != half) {
+        const uint32_t d = q + (rem > half ? 1u : 0u);
+        return {d, d};
+    }
+    return {q + (q & 1u), q + ((q & 1u) ^ 1u)};  // tie: to the even multiple
+}
+
+__device__ __forceinline__ int f_eb(float s)
+{
+    const int e = (int)(__float_as_uint(s) >> 23);
+    return e ? e : 1;
+}
+__device__ __forceinline__ uint32_t f_S(float s)
+{
+    const uint32_t b = __float_as_uint(s);
+    return (b >> 23) ? ((b & 0x7fffffu) | 0x800000u) : b;
+}
+__device__ __forceinline__ float f_make(int eb, uint32_t S)
+{
+    return __uint_as_float(((uint32_t)(eb - 1) << 23) + S);
+}
+
+enum { F_NONE = 0, F_GE = 1, F_GT = 2 };
+
+struct FoldRes {
+    float sum;    // the fold of all n elements (idx < 0), or the prefix at idx
+    int idx;      // first index whose prefix meets the predicate, or -1
+};
+
+__device__ __forceinline__ bool fpred(int mode, float v, float thr)
+{
+    return mode == F_GE ? v >= thr : v > thr;
+}
+
+// Sequential f32 fold s = s + x(i), i = 0..n-1, of non-negative finite x,
+// bit-identical to the loop, with an optional monotone predicate on the
+// running value (F_GE: s_i >= thr, F_GT: s_i > thr) whose first hit ends the
+// fold.  Called by every thread of the block with the same arguments.
+template <class X>
+__device__ FoldRes block_fold(X x_at, int n, float s, float thr, int pmode, Small* sm)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __syncthreads();
+    if (tid < 4) (&sm->slot[0][0])[tid] = ~0ull;
+    __syncthreads();
+    int start = 0, it = 0;
+    while (start < n) {
+        const int eb = f_eb(s);
+        const uint32_t S0 = f_S(s);
+        const int base = start + tid * FIPT;
+        FMap m[FIPT];
+        float xv[FIPT];
+        FMap acc = {0u, 0u};
+#pragma unroll
+        for (int q = 0; q < FIPT; q++) {
+            const int i = base + q;
+            xv[q] = i < n ? x_at(i) : 0.0f;
+            m[q] = fmap_of(xv[q], eb);
+            acc = fcomp(acc, m[q]);
+        }
+        FMap inc = acc;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            FMap o;
+            o.d0 = __shfl_up(inc.d0, off, 64);
+            o.d1 = __shfl_up(inc.d1, off, 64);
+            if (lane >= off) inc = fcomp(o, inc);
+        }
+        FMap ex;
+        ex.d0 = __shfl_up(inc.d0, 1, 64);
+        ex.d1 = __shfl_up(inc.d1, 1, 64);
+        if (lane == 0) ex = {0u, 0u};
+        if (lane == 63) sm->wtot[wave] = inc;
+        unsigned long long* slot = sm->slot[it & 1];
+        __syncthreads();
+        if (tid < 2) sm->slot[(it + 1) & 1][tid] = ~0ull;
+        FMap wp = {0u, 0u};
+        for (int w = 0; w < wave; w++) wp = fcomp(wp, sm->wtot[w]);
+        FMap tot = wp;
+        for (int w = wave; w < SWV; w++) tot = fcomp(tot, sm->wtot[w]);
+        const FMap pre = fcomp(wp, ex);
+        uint32_t S = S0 + fsel(pre, S0);
+        bool live = true;
+#pragma unroll
+        for (int q = 0; q < FIPT; q++) {
+            const int i = base + q;
+            if (live && i < n && S < FTOP) {
+                const uint32_t Sp = S;
+                S = Sp + fsel(m[q], Sp);
+                if (S >= FTOP) {
+                    // leaves the binade: this add is done in f32 by the hardware
+                    const float sn = f_make(eb, Sp) + xv[q];
+                    atomicMin(&slot[0], ((unsigned long long)i << 32) | __float_as_uint(sn));
+                    live = false;
+                } else if (pmode != F_NONE) {
+                    const float sv = f_make(eb, S);
+                    if (fpred(pmode, sv, thr)) {
+                        atomicMin(&slot[1], ((unsigned long long)i << 32) | __float_as_uint(sv));
+                        live = false;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        const unsigned long long cr = slot[0], pr = slot[1];
+        // a predicate hit can only precede the first exit: later prefixes
+        // are saturated and never tested
+        if (pr != ~0ull) return {__uint_as_float((uint32_t)pr), (int)(pr >> 32)};
+        if (cr != ~0ull) {
+            const int ci = (int)(cr >> 32);
+            const float sn = __uint_as_float((uint32_t)cr);
+            if (pmode != F_NONE && fpred(pmode, sn, thr)) return {sn, ci};
+            s = sn;
+            start = ci + 1;
+        } else {
+            s = f_make(eb, S0 + fsel(tot, S0));
+            start += SB * FIPT;
+        }
+        it++;
+    }
+    return {s, -1};
+}
+
+// ------------------------------------------------------------ block helpers
+// exclusive scan of one u32 per thread; *total gets the block sum
+__device__ uint32_t block_excl_scan(uint32_t v, Small* sm, uint32_t* total)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t inc = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_up(inc, off, 64);
+        if (lane >= off) inc += o;
+    }
+    __syncthreads();
+    if (lane == 63) sm->scan[wave] = inc;
+    __syncthreads();
+    uint32_t wp = 0, tot = 0;
+    for (int w = 0; w < SWV; w++) {
+        const uint32_t c = sm->scan[w];
+        if (w < wave) wp += c;
+        tot += c;
+    }
+    *total = tot;
+    return wp + inc - v;
+}
+
+// fmaxf over x(i), i < n (f32::max semantics: a NaN operand is ignored)
+template <class X>
+__device__ float block_max(X x_at, int n, Small* sm)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float m = -INFINITY;
+    for (int i = tid; i < n; i += SB) m = fmaxf(m, x_at(i));
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    __syncthreads();
+    if (lane == 0) sm->wf[wave] = m;
+    __syncthreads();
+    float r = -INFINITY;
+    for (int w = 0; w < SWV; w++) r = fmaxf(r, sm->wf[w]);
+    return r;
+}
+
+// index of the first strict maximum of x(i), i < n (values that are not
+// above -inf, NaN included, never win); `dflt` when nothing wins
+template <class X>
+__device__ int block_argmax(X x_at, int n, int dflt, Small* sm)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = tid; i < n; i += SB) {
+        const float v = x_at(i);
+        if (v > best) { best = v; idx = i; }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ob = __shfl_xor(best, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+    }
+    __syncthreads();
+    if (lane == 0) { sm->wf[wave] = best; sm->wi[wave] = idx; }
+    __syncthreads();
+    best = -INFINITY;
+    idx = 0x7fffffff;
+    for (int w = 0; w < SWV; w++)
+        if (sm->wf[w] > best || (sm->wf[w] == best && sm->wi[w] < idx)) { best = sm->wf[w]; idx = sm->wi[w]; }
+    return idx == 0x7fffffff ? dflt : idx;
+}
+
+// number of i < n with pred(i)
+template <class Pred>
+__device__ int block_count(Pred pred, int n, Small* sm)
+{
+    int c = 0;
+    for (int i = threadIdx.x; i < n; i += SB) c += pred(i) ? 1 : 0;
+    uint32_t tot;
+    (void)block_excl_scan((uint32_t)c, sm, &tot);
+    return (int)tot;
+}
+
+// smallest i < n with pred(i), or -1
+template <class Pred>
+__device__ int block_first(Pred pred, int n, Small* sm)
+{
+    __syncthreads();
+    if (threadIdx.x == 0) sm->iv[7] = 0x7fffffff;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += SB)
+        if (pred(i)) { atomicMin(&sm->iv[7], i); break; }
+    __syncthreads();
+    const int r = sm->iv[7];
+    return r == 0x7fffffff ? -1 : r;
+}
+
+// largest i < n with pred(i), or -1
+template <class Pred>
+__device__ int block_last(Pred pred, int n, Small* sm)
+{
+    __syncthreads();
+    if (threadIdx.x == 0) sm->iv[6] = -1;
+    __syncthreads();
+    int mine = -1;
+    for (int i = threadIdx.x; i < n; i += SB)
+        if (pred(i)) mine = i;
+    if (mine >= 0) atomicMax(&sm->iv[6], mine);
+    __syncthreads();
+    return sm->iv[6];
+}
+
+// ------------------------------------------------------------ candidate order
+// u32 that ascends as the logit descends (-0 ranks with +0)
+__device__ __forceinline__ uint32_t desc_key(float l)
+{
+    uint32_t b = __float_as_uint(l);
+    if (b == 0x80000000u) b = 0;
+    const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ~ord;
+}
+__device__ __forceinline__ unsigned long long cand_key(float l, int i)
+{
+    return ((unsigned long long)desc_key(l) << 32) | (uint32_t)i;
+}
+
+__device__ void bitonic_sort(unsigned long long* keys, int P)
+{
+    const int tid = threadIdx.x;
+    for (int k2 = 2; k2 <= P; k2 <<= 1) {
+        for (int j = k2 >> 1; j > 0; j >>= 1) {
+            for (int t = tid; t < P / 2; t += SB) {
+                const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
+                const int l = i | j;
+                const unsigned long long a = keys[i], b = keys[l];
+                const bool up = (i & k2) == 0;
+                if ((a > b) == up) { keys[i] = b; keys[l] = a; }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// The next band of the candidate order after key *last (all keys when
+// have_last is false): at most BAND keys, ending early at a histogram bin
+// boundary once `want` are in.  Writes ids and logits to sid/sl[pos...],
+// advances *last and returns the band size.
+__device__ int emit_band(const float* lg, int V, bool have_last, unsigned long long* last_io, int want,
+                         int pos, int32_t* sid, float* sl, unsigned long long* keys, Small* sm)
+{
+    const int tid = threadIdx.x;
+    const unsigned long long last = *last_io;
+    uint32_t* hist = (uint32_t*)keys;
+    unsigned long long prefix = 0, fixed = 0, hi = ~0ull;
+    // bit fields of the key: desc_key in 63..32 (12 + 12 + 8), id in 17..0 (9 + 9)
+    const int SH[5] = {52, 40, 32, 9, 0};
+    const int WD[5] = {12, 12, 8, 9, 9};
+    bool found = false;
+    for (int lev = 0; lev < 5 && !found; lev++) {
+        const int sh = SH[lev], nb = 1 << WD[lev];
+        __syncthreads();
+        for (int b = tid; b < nb; b += SB) hist[b] = 0;
+        __syncthreads();
+        for (int i = tid; i < V; i += SB) {
+            const unsigned long long key = cand_key(lg[i], i);
+            if ((have_last && key <= last) || (key & fixed) != prefix) continue;
+            atomicAdd(&hist[(key >> sh) & (unsigned long long)(nb - 1)], 1u);
+        }
+        __syncthreads();
+        uint32_t c[4], s = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int b = tid * 4 + q;
+            c[q] = b < nb ? hist[b] : 0u;
+            s += c[q];
+        }
+        uint32_t tot;
+        const uint32_t ex = block_excl_scan(s, sm, &tot);
+        if (tid == 0) { sm->iv[0] = -1; sm->iv[1] = 0x7fffffff; sm->iv[2] = 0x7fffffff; }
+        __syncthreads();
+        uint32_t run = ex;
+        int my_cap = -1, my_want = 0x7fffffff, my_first = 0x7fffffff;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int b = tid * 4 + q;
+            if (b < nb) {
+                run += c[q];
+                if (run <= (uint32_t)BAND) my_cap = b;
+                if (run >= (uint32_t)want && my_want == 0x7fffffff) my_want = b;
+                if (c[q] && my_first == 0x7fffffff) my_first = b;
+            }
+        }
+        if (my_cap >= 0) atomicMax(&sm->iv[0], my_cap);
+        if (my_want != 0x7fffffff) atomicMin(&sm->iv[1], my_want);
+        if (my_first != 0x7fffffff) atomicMin(&sm->iv[2], my_first);
+        __syncthreads();
+        const int jcap = sm->iv[0], jwant = sm->iv[1], first = sm->iv[2];
+        if (tot == 0) return 0;
+        if (jcap >= first) {
+            const int j = jwant < jcap ? jwant : jcap;
+            hi = prefix | ((unsigned long long)j << sh) | ((1ull << sh) - 1ull);
+            found = true;
+        } else {
+            // the first non-empty bin alone holds more than a band: refine it
+            prefix |= (unsigned long long)first << sh;
+            fixed |= (unsigned long long)(nb - 1) << sh;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) sm->iv[3] = 0;
+    __syncthreads();
+    for (int i = tid; i < V; i += SB) {
+        const unsigned long long key = cand_key(lg[i], i);
+        if ((have_last && key <= last) || key > hi) continue;
+        keys[atomicAdd(&sm->iv[3], 1)] = key;
+    }
+    __syncthreads();
+    const int cnt = sm->iv[3];
+    int P = 64;
+    while (P < cnt) P <<= 1;
+    for (int t = cnt + tid; t < P; t += SB) keys[t] = ~0ull;
+    __syncthreads();
+    bitonic_sort(keys, P);
+    for (int t = tid; t < cnt; t += SB) {
+        const int id = (int)(uint32_t)keys[t];
+        sid[pos + t] = id;
+        sl[pos + t] = lg[id];
+    }
+    *last_io = keys[cnt - 1];
+    __syncthreads();
+    return cnt;
+}
+
+// ------------------------------------------------------------ distributions
+struct DistArgs {
+    const float* p_logits;      // spec: [B][k+1][V]; direct: [rows][V]
+    const float* q_logits;      // spec only: [B][k][V] or NULL
+    const int32_t* draft;       // spec only: [B][k]
+    const int32_t* hist;        // [B or rows][hist_len] or NULL
+    int B, k, V, hist_len, nrow_p, direct;
+    cpv_sampler_params prm;
+    float ln_min_p;             // logf(min_p), evaluated by the host's libm
+    int pen_on;
+    float* pen;                 // [rows][V] penalised copies (pen_on)
+    int32_t* sid;               // [rows][V] candidate ids in candidate order
+    float* sl;                  // [rows][V] their (penalised, untempered) logits
+    float* pr;                  // [rows][V] their probabilities
+    int32_t* hdr;               // [rows] candidate count
+};
+
+// Penalties (lib.rs:233-266): a dense copy of the row in which every token
+// of the window carries its penalised logit.  The window is the last
+// penalty_last_n of the history (valid entries, oldest first) followed by
+// the row's preceding drafts (Sampler::accept after each kept draft,
+// engine.rs:2368-2369).
+__device__ const float* apply_penalties(const float* logits, float* pen, int V, const int32_t* hist, int hist_len,
+                                        const int32_t* drafts, int nd, const cpv_sampler_params& P, int* win,
+                                        Small* sm)
+{
+    const int tid = threadIdx.x;
+    int valid[4], c = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int a = tid * 4 + q;
+        valid[q] = (hist && a < hist_len && hist[a] >= 0) ? 1 : 0;
+        c += valid[q];
+    }
+    uint32_t L;
+    uint32_t p = block_excl_scan((uint32_t)c, sm, &L);
+    const int total = (int)L + nd, cap = P.penalty_last_n;
+    const int start = total > cap ? total - cap : 0;
+    const int wn = total - start;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        if (valid[q]) {
+            if ((int)p >= start) win[p - start] = hist[tid * 4 + q];
+            p++;
+        }
+    }
+    for (int d = tid; d < nd; d += SB) {
+        const int at = (int)L + d;
+        if (at >= start) win[at - start] = drafts[d];
+    }
+    for (int i = tid; i < V; i += SB) pen[i] = logits[i];
+    __syncthreads();
+    for (int a = tid; a < wn; a += SB) {
+        const int tok = win[a];
+        if (tok < 0 || tok >= V) continue;
+        bool first = true;
+        int count = 0;
+        for (int b = 0; b < wn; b++) {
+            if (win[b] == tok) {
+                if (b < a) first = false;
+                count++;
+            }
+        }
+        if (!first) continue;
+        float l = logits[tok];
+        if (l <= 0.0f) l *= P.penalty_repeat;
+        else l /= P.penalty_repeat;
+        const float sub = (float)count * P.penalty_freq;
+        l -= sub + P.penalty_present;
+        pen[tok] = l;
+    }
+    __syncthreads();
+    return pen;
+}
+
+// Sampler::build for one row (lib.rs:229-376), leaving the distribution as
+// n candidates (sid, sl, pr) in candidate order.
+__global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
+{
+    extern __shared__ __align__(16) unsigned char sdyn[];
+    unsigned long long* keys = (unsigned long long*)sdyn;
+    Small* sm = (Small*)(sdyn + SAMPLE_LDS_KEYS);
+    const int tid = threadIdx.x, row = blockIdx.x, V = a.V;
+    const cpv_sampler_params& P = a.prm;
+    const float* logits;
+    const int32_t* hist = nullptr;
+    const int32_t* drafts = nullptr;
+    int nd = 0;
+    if (a.direct) {
+        logits = a.p_logits + (size_t)row * V;
+        if (a.hist) hist = a.hist + (size_t)row * a.hist_len;
+    } else {
+        int b, j;
+        if (row < a.nrow_p) {
+            b = row / (a.k + 1);
+            j = row % (a.k + 1);
+            logits = a.p_logits + (size_t)row * V;
+        } else {
+            const int r = row - a.nrow_p;
+            b = r / a.k;
+            j = r % a.k;
+            logits = a.q_logits + (size_t)r * V;
+        }
+        if (a.hist) hist = a.hist + (size_t)b * a.hist_len;
+        drafts = a.draft + (size_t)b * a.k;
+        nd = j;
+    }
+    const size_t off = (size_t)row * V;
+    int32_t* sid = a.sid + off;
+    float* sl = a.sl + off;
+    float* pr = a.pr + off;
+    const float* lg = logits;
+    if (a.pen_on) lg = apply_penalties(logits, a.pen + off, V, hist, a.hist_len, drafts, nd, P, (int*)keys, sm);
+
+    if (P.temp <= 0.0f) {                                  // :324-337 point mass at the first maximum
+        const int best = block_argmax([&](int i) { return lg[i]; }, V, 0, sm);
+        if (tid == 0) {
+            sid[0] = best;
+            sl[0] = lg[best];
+            pr[0] = 1.0f;
+            a.hdr[row] = 1;
+        }
+        return;
+    }
+
+    const bool top_k = P.top_k > 0 && P.top_k < V;         // :272-280
+    const bool min_p = !top_k && P.min_p > 0.0f;           // :281-295
+    const bool top_p = !top_k && !min_p && P.top_p < 1.0f; // :296-316
+    const float mx = block_max([&](int i) { return lg[i]; }, V, sm);
+    int n;
+    if (top_k || min_p || top_p) {
+        int M = 0, emitted = 0;
+        unsigned long long last = 0;
+        if (top_k) {
+            M = P.top_k > P.min_keep ? P.top_k : P.min_keep;
+            if (M > V) M = V;
+        } else if (min_p) {
+            const float floor_l = mx + a.ln_min_p;
+            M = block_count([&](int i) { return lg[i] >= floor_l; }, V, sm);
+        } else {
+            // softmax over the vocabulary in index order, then the probe:
+            // the smallest of 1024, 8192, ... (capped at V) whose sorted
+            // prefix covers top_p, and the cut inside it (:343-358), both
+            // read off one fold of the probabilities in candidate order
+            const float sum1 = block_fold([&](int i) { return cpv_expf(lg[i] - mx); }, V, 0.0f, 0.0f, F_NONE, sm).sum;
+            float s = 0.0f;
+            int ifirst = -1;
+            while (emitted < V) {
+                const int cnt = emit_band(lg, V, emitted > 0, &last, BAND, emitted, sid, sl, keys, sm);
+                if (cnt <= 0) break;
+                const float* band = sl + emitted;
+                const FoldRes r = block_fold([&](int i) { return cpv_expf(band[i] - mx) / sum1; }, cnt, s, P.top_p,
+                                             F_GE, sm);
+                if (r.idx >= 0) ifirst = emitted + r.idx;
+                emitted += cnt;
+                if (r.idx >= 0) break;
+                s = r.sum;
+            }
+            int probe = V < 1024 ? V : 1024;
+            if (ifirst < 0) probe = V;
+            else
+                while (probe < ifirst + 1) probe = probe * 8 < V ? probe * 8 : V;
+            M = probe;
+            if (probe > 1 && ifirst >= 0) {
+                const int keep = ifirst + 1 > P.min_keep ? ifirst + 1 : P.min_keep;
+                if (keep <= probe) M = keep;
+            }
+        }
+        while (emitted < M) {
+            const int cnt = emit_band(lg, V, emitted > 0, &last, M - emitted, emitted, sid, sl, keys, sm);
+            if (cnt <= 0) break;
+            emitted += cnt;
+        }
+        n = M;
+        if (!top_p && P.top_p < 1.0f && n > 1) {           // :343-358 after a re-softmax over the survivors
+            const float l0 = sl[0];
+            const float sA = block_fold([&](int i) { return cpv_expf(sl[i] - l0); }, n, 0.0f, 0.0f, F_NONE, sm).sum;
+            const FoldRes r = block_fold([&](int i) { return cpv_expf(sl[i] - l0) / sA; }, n, 0.0f, P.top_p, F_GE, sm);
+            if (r.idx >= 0) {
+                const int keep = r.idx + 1 > P.min_keep ? r.idx + 1 : P.min_keep;
+                if (keep <= n) n = keep;
+            }
+        }
+        if (top_k && P.min_p > 0.0f && n > 1) {            // :360-369
+            const float floor_l = sl[0] + a.ln_min_p;
+            const int nn = n;
+            int keep = block_count([&](int i) { return sl[i] >= floor_l; }, nn, sm);
+            if (keep < 1) keep = 1;
+            if (keep < P.min_keep) keep = P.min_keep;
+            if (keep < n) n = keep;
+        }
+    } else {                                               // :317-322 the vocabulary in index order
+        for (int i = tid; i < V; i += SB) {
+            sid[i] = i;
+            sl[i] = lg[i];
+        }
+        __syncthreads();
+        n = V;
+    }
+    // :371-374 temperature, then softmax over the survivors (:461-471)
+    const float T = P.temp;
+    const float mx2 = (top_k || min_p || top_p ? sl[0] : mx) / T;
+    const float s2 = block_fold([&](int i) { return cpv_expf(sl[i] / T - mx2); }, n, 0.0f, 0.0f, F_NONE, sm).sum;
+    for (int i = tid; i < n; i += SB) pr[i] = cpv_expf(sl[i] / T - mx2) / s2;
+    if (tid == 0) a.hdr[row] = n;
+}
+
+// ------------------------------------------------------------ acceptance
+// Philox4x64-10 (Salmon, Moraes, Dror, Shaw, SC'11): counter (c0, c1, c2, 0),
+// key (seed, 0); the uniform is the top 24 bits of the first output word.
+__device__ float philox_u01(uint64_t seed, uint64_t c0, uint64_t c1, uint64_t c2)
+{
+    uint64_t x0 = c0, x1 = c1, x2 = c2, x3 = 0, k0 = seed, k1 = 0;
+    for (int r = 0; r < 10; r++) {
+        const uint64_t lo0 = 0xD2E7470EE14C6C93ull * x0, hi0 = __umul64hi(0xD2E7470EE14C6C93ull, x0);
+        const uint64_t lo1 = 0xCA5A826395121157ull * x2, hi1 = __umul64hi(0xCA5A826395121157ull, x2);
+        const uint64_t n0 = hi1 ^ x1 ^ k0, n2 = hi0 ^ x3 ^ k1;
+        x0 = n0;
+        x1 = lo1;
+        x2 = n2;
+        x3 = lo0;
+        k0 += 0x9E3779B97F4A7C15ull;
+        k1 += 0xBB67AE8584CAA73Bull;
+    }
+    return (float)(x0 >> 40) / 16777216.0f;
+}
+
+struct DecideArgs {
+    const int32_t* draft;       // [B][k]
+    const float* u;             // [B][k+1][2] or NULL (Philox)
+    uint64_t seed;
+    const float* noise;         // [B][k+1][V] (GUMBEL)
+    int B, k, V, mode, has_q, nrow_p;
+    float T, inv_t;
+    const int32_t* sid;
+    const float* sl;
+    const float* pr;
+    const int32_t* hdr;
+    float* qdense;              // [B][V] (has_q)
+    int32_t* out_tok;           // [B][k+1]
+    int32_t* out_n;             // [B]
+};
+
+struct Row {
+    const int32_t* sid;
+    const float* sl;
+    const float* pr;
+    int n;
+};
+
+__device__ __forceinline__ Row dist_row(const DecideArgs& a, int row)
+{
+    const size_t off = (size_t)row * a.V;
+    return {a.sid + off, a.sl + off, a.pr + off, a.hdr[row]};
+}
+
+// Dist::draw (lib.rs:395-404): the first candidate whose cumulative
+// probability exceeds r, else the last
+__device__ int dist_draw(const Row& d, float r, Small* sm)
+{
+    const FoldRes f = block_fold([&](int i) { return d.pr[i]; }, d.n, 0.0f, r, F_GT, sm);
+    return f.idx >= 0 ? d.sid[f.idx] : d.sid[d.n - 1];
+}
+
+// Dist::draw_excluding (lib.rs:408-436).  Adding 0 leaves an f32 sum
+// unchanged, so skipping x is folding it as 0.
+__device__ int dist_draw_excluding(const Row& d, int x, float r, Small* sm)
+{
+    auto val = [&](int i) { return d.sid[i] == x ? 0.0f : d.pr[i]; };
+    const float total = block_fold(val, d.n, 0.0f, 0.0f, F_NONE, sm).sum;
+    if (total <= 0.0f) return dist_draw(d, r, sm);
+    const float target = r * total;
+    const FoldRes f = block_fold(val, d.n, 0.0f, target, F_GT, sm);
+    if (f.idx >= 0) return d.sid[f.idx];
+    if (d.sid[d.n - 1] != x || d.n < 2) return d.sid[d.n - 1];
+    return d.sid[d.n - 2];
+}
+
+// the general rule's residual max(0, p - q) over p's candidates in p's order
+__device__ int dist_draw_residual(const Row& p, const Row& q, float* qd, int V, float r, Small* sm)
+{
+    for (int i = threadIdx.x; i < V; i += SB) qd[i] = 0.0f;
+    __syncthreads();
+    for (int i = threadIdx.x; i < q.n; i += SB) qd[q.sid[i]] = q.pr[i];
+    __syncthreads();
+    auto val = [&](int i) {
+        const float d = p.pr[i] - qd[p.sid[i]];
+        return d > 0.0f ? d : 0.0f;
+    };
+    const float total = block_fold(val, p.n, 0.0f, 0.0f, F_NONE, sm).sum;
+    if (total <= 0.0f) return dist_draw(p, r, sm);
+    const float target = r * total;
+    const FoldRes f = block_fold(val, p.n, 0.0f, target, F_GT, sm);
+    if (f.idx >= 0) return p.sid[f.idx];
+    const int l = block_last([&](int i) { return p.pr[i] - qd[p.sid[i]] > 0.0f; }, p.n, sm);
+    return l >= 0 ? p.sid[l] : p.sid[p.n - 1];
+}
+
+// Sampler::sample_coupled (lib.rs:197-216): the first candidate maximising
+// tempered logit + T-scaled noise / T
+__device__ int coupled_argmax(const DecideArgs& a, const Row& d, const float* noise_row, Small* sm)
+{
+    const float T = a.T, inv_t = a.inv_t;
+    const bool tempered = T > 0.0f;
+    const int i = block_argmax(
+        [&](int c) {
+            const float tl = tempered ? d.sl[c] / T : d.sl[c];
+            return tl + noise_row[d.sid[c]] * inv_t;
+        },
+        d.n, 0, sm);
+    return d.sid[i];
+}
+
+__device__ __forceinline__ float uniform(const DecideArgs& a, int b, int j, int r)
+{
+    if (a.u) return a.u[((size_t)b * (a.k + 1) + j) * 2 + r];
+    return philox_u01(a.seed, (uint64_t)b, (uint64_t)j, (uint64_t)r);
+}
+
+// engine.rs:2326-2461 for one sequence: walk the drafts, stop at the first
+// rejection, then the replacement or the bonus token
+__global__ __launch_bounds__(SB) void decide_kernel(DecideArgs a)
+{
+    __shared__ Small sm_s;
+    Small* sm = &sm_s;
+    const int b = blockIdx.x, tid = threadIdx.x, K1 = a.k + 1, V = a.V;
+    int n_keep = 0, rep = 0;
+    bool have_rep = false;
+    for (int j = 0; j < a.k; j++) {
+        const Row d = dist_row(a, b * K1 + j);
+        const int x = a.draft[(size_t)b * a.k + j];
+        bool keep;
+        if (a.mode == CPV_ACCEPT_GUMBEL) {
+            const int commit = coupled_argmax(a, d, a.noise + ((size_t)b * K1 + j) * V, sm);
+            keep = x == commit;
+            if (!keep) { rep = commit; have_rep = true; }
+        } else {
+            const float u0 = uniform(a, b, j, 0), u1 = uniform(a, b, j, 1);
+            const int pos = block_first([&](int i) { return d.sid[i] == x; }, d.n, sm);
+            const float px = pos >= 0 ? d.pr[pos] : 0.0f;
+            if (!a.has_q) {
+                keep = u0 < px;
+                if (!keep) { rep = dist_draw_excluding(d, x, u1, sm); have_rep = true; }
+            } else {
+                const Row q = dist_row(a, a.nrow_p + b * a.k + j);
+                const int qpos = block_first([&](int i) { return q.sid[i] == x; }, q.n, sm);
+                const float qx = qpos >= 0 ? q.pr[qpos] : 0.0f;
+                keep = u0 * qx < px;
+                if (!keep) { rep = dist_draw_residual(d, q, a.qdense + (size_t)b * V, V, u1, sm); have_rep = true; }
+            }
+        }
+        if (!keep) break;
+        if (tid == 0) a.out_tok[(size_t)b * K1 + n_keep] = x;
+        n_keep++;
+    }
+    int next;
+    if (have_rep) {
+        next = rep;
+    } else {
+        const Row d = dist_row(a, b * K1 + n_keep);
+        if (a.mode == CPV_ACCEPT_GUMBEL) next = coupled_argmax(a, d, a.noise + ((size_t)b * K1 + n_keep) * V, sm);
+        else next = dist_draw(d, uniform(a, b, n_keep, 0), sm);
+    }
+    if (tid == 0) {
+        a.out_tok[(size_t)b * K1 + n_keep] = next;
+        a.out_n[b] = n_keep;
+    }
+}
+
+// greedy, and gumbel when the coupling is exact: the drafts are kept while
+// they equal the row argmax (of logits + noise), and the row after the last
+// kept draft gives the next token
+__global__ void decide_argmax_kernel(const int32_t* __restrict__ am, const int32_t* __restrict__ draft, int B, int k,
+                                     int32_t* __restrict__ out_tok, int32_t* __restrict__ out_n)
+{
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    const int K1 = k + 1;
+    int n_keep = 0;
+    while (n_keep < k && am[(size_t)b * K1 + n_keep] == draft[(size_t)b * k + n_keep]) {
+        out_tok[(size_t)b * K1 + n_keep] = draft[(size_t)b * k + n_keep];
+        n_keep++;
+    }
+    out_tok[(size_t)b * K1 + n_keep] = am[(size_t)b * K1 + n_keep];
+    out_n[b] = n_keep;
+}
+
+bool penalties_on(const cpv_sampler_params* p)
+{
+    return !(p->penalty_repeat == 1.0f && p->penalty_freq == 0.0f && p->penalty_present == 0.0f);
+}
+
+bool coupling_is_exact(const cpv_sampler_params* p)       // lib.rs:70-78
+{
+    return p->temp > 0.0f && p->top_k == 0 && p->top_p >= 1.0f && p->min_p <= 0.0f && !penalties_on(p);
+}
+
+cpv_status check_params(cpv_ctx* ctx, const cpv_sampler_params* p, int hist_len)
+{
+    if (!p) return cpv_fail(ctx, CPV_EINVAL, "sampler: params is NULL");
+    if (p->top_k < 0 || p->min_keep < 0 || p->penalty_last_n < 0)
+        return cpv_fail(ctx, CPV_EINVAL, "sampler: top_k, min_keep and penalty_last_n are counts (>= 0)");
+    if (p->min_p > 1.0f)
+        return cpv_fail(ctx, CPV_EINVAL, "sampler: min_p above 1 leaves no candidate");
+    if (hist_len < 0 || hist_len > HIST_MAX)
+        return cpv_fail(ctx, CPV_EINVAL, "sampler: hist_len must be in [0, %d]", HIST_MAX);
+    return CPV_OK;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct DistBufs {
+    int32_t* hdr;
+    int32_t* sid;
+    float* sl;
+    float* pr;
+    float* pen;
+    void* tail;                 // first byte after the distribution buffers
+};
+
+size_t dist_bytes(int rows, int V, bool pen)
+{
+    const size_t rv = align256((size_t)rows * V * 4);
+    return align256((size_t)rows * 4) + 3 * rv + (pen ? rv : 0);
+}
+
+DistBufs dist_carve(void* ws, int rows, int V, bool pen)
+{
+    uint8_t* p = (uint8_t*)ws;
+    const size_t rv = align256((size_t)rows * V * 4);
+    DistBufs d;
+    d.hdr = (int32_t*)p;
+    p += align256((size_t)rows * 4);
+    d.sid = (int32_t*)p;
+    p += rv;
+    d.sl = (float*)p;
+    p += rv;
+    d.pr = (float*)p;
+    p += rv;
+    d.pen = pen ? (float*)p : nullptr;
+    if (pen) p += rv;
+    d.tail = p;
+    return d;
+}
+
+cpv_status dist_launch(cpv_ctx* ctx, DistArgs& a, int rows)
+{
+    const size_t lds = SAMPLE_LDS_KEYS + sizeof(Small);
+    if (lds > ctx->lds_max) return cpv_fail(ctx, CPV_EUNSUPPORTED, "sampler: needs %zu bytes of LDS", lds);
+    const int e0 = cpv_prof_mark(ctx);
+    dist_kernel<<<(unsigned)rows, SB, lds, ctx->stream>>>(a);
+    CPV_HIP(ctx, hipGetLastError());
+    cpv_prof_add(ctx, e0, CPV_PROF_SAMPLE, (double)rows * a.V * 4.0);
+    return CPV_OK;
+}
+
+}  // namespace
+
+extern "C" cpv_status cpv_distribution(cpv_ctx* ctx, const float* logits_dev, int rows, int v,
+                                       const cpv_sampler_params* params, const int32_t* hist_dev, int hist_len,
+                                       int32_t* ids_dev, float* probs_dev, int32_t* n_dev)
+{
+    if (!ctx) return CPV_EINVAL;
+    if (!logits_dev || !ids_dev || !probs_dev || !n_dev || rows < 0 || v < 1 || v > VMAX)
+        return cpv_fail(ctx, CPV_EINVAL, "distribution: bad arguments (1 <= v <= %d)", VMAX);
+    cpv_status st = check_params(ctx, params, hist_dev ? hist_len : 0);
+    if (st) return st;
+    if (rows == 0) return CPV_OK;
+    const bool pen = penalties_on(params) && params->penalty_last_n > 0 && hist_dev && hist_len > 0;
+    void* ws = nullptr;
+    if ((st = cpv_workspace(ctx, dist_bytes(rows, v, pen), &ws))) return st;
+    DistBufs d = dist_carve(ws, rows, v, pen);
+    DistArgs a{};
+    a.p_logits = logits_dev;
+    a.hist = hist_dev;
+    a.V = v;
+    a.hist_len = hist_dev ? hist_len : 0;
+    a.direct = 1;
+    a.prm = *params;
+    a.ln_min_p = params->min_p > 0.0f ? logf(params->min_p) : 0.0f;
+    a.pen_on = pen;
+    a.pen = d.pen;
+    a.sid = ids_dev;
+    a.sl = d.sl;
+    a.pr = probs_dev;
+    a.hdr = n_dev;
+    return dist_launch(ctx, a, rows);
+}
+
+extern "C" cpv_status cpv_spec_accept(cpv_ctx* ctx, const float* p_logits_dev, const float* q_logits_dev,
+                                      const int32_t* draft_dev, int b, int k, int v,
+                                      const cpv_sampler_params* params, int mode, const float* u_dev,
+                                      uint64_t philox_seed, const float* noise_dev, const int32_t* hist_dev,
+                                      int hist_len, int32_t* out_tok_dev, int32_t* out_n_dev)
+{
+    if (!ctx) return CPV_EINVAL;
+    if (!p_logits_dev || (k > 0 && !draft_dev) || !out_tok_dev || !out_n_dev || b < 1 || k < 0 || k > 15 || v < 1 ||
+        v > VMAX)
+        return cpv_fail(ctx, CPV_EINVAL, "spec_accept: bad arguments (b >= 1, 0 <= k <= 15, 1 <= v <= %d)", VMAX);
+    if (mode != CPV_ACCEPT_GREEDY && mode != CPV_ACCEPT_REJECT && mode != CPV_ACCEPT_GUMBEL)
+        return cpv_fail(ctx, CPV_EINVAL, "spec_accept: unknown mode %d", mode);
+    if (mode == CPV_ACCEPT_GUMBEL && !noise_dev) return cpv_fail(ctx, CPV_EINVAL, "spec_accept: gumbel needs noise");
+    cpv_status st;
+    const int K1 = k + 1, nrow_p = b * K1;
+    if (mode == CPV_ACCEPT_GREEDY || (mode == CPV_ACCEPT_GUMBEL && params && coupling_is_exact(params))) {
+        void* ws = nullptr;
+        if ((st = cpv_workspace(ctx, align256((size_t)nrow_p * 4), &ws))) return st;
+        int32_t* am = (int32_t*)ws;
+        if ((st = cpv_argmax_rows(ctx, p_logits_dev, mode == CPV_ACCEPT_GUMBEL ? noise_dev : nullptr, nrow_p, v, am)))
+            return st;
+        decide_argmax_kernel<<<(unsigned)((b + 63) / 64), 64, 0, ctx->stream>>>(am, draft_dev, b, k, out_tok_dev,
+                                                                                out_n_dev);
+        CPV_HIP(ctx, hipGetLastError());
+        return CPV_OK;
+    }
+    if ((st = check_params(ctx, params, hist_dev ? hist_len : 0))) return st;
+    const bool has_q = mode == CPV_ACCEPT_REJECT && q_logits_dev && k > 0;
+    const int rows = nrow_p + (has_q ? b * k : 0);
+    const bool pen = penalties_on(params) && params->penalty_last_n > 0;
+    const size_t db = dist_bytes(rows, v, pen);
+    const size_t qb = has_q ? align256((size_t)b * v * 4) : 0;
+    void* ws = nullptr;
+    if ((st = cpv_workspace(ctx, db + qb, &ws))) return st;
+    DistBufs d = dist_carve(ws, rows, v, pen);
+    DistArgs a{};
+    a.p_logits = p_logits_dev;
+    a.q_logits = has_q ? q_logits_dev : nullptr;
+    a.draft = draft_dev;
+    a.hist = hist_dev;
+    a.B = b;
+    a.k = k;
+    a.V = v;
+    a.hist_len = hist_dev ? hist_len : 0;
+    a.nrow_p = nrow_p;
+    a.direct = 0;
+    a.prm = *params;
+    a.ln_min_p = params->min_p > 0.0f ? logf(params->min_p) : 0.0f;
+    a.pen_on = pen;
+    a.pen = d.pen;
+    a.sid = d.sid;
+    a.sl = d.sl;
+    a.pr = d.pr;
+    a.hdr = d.hdr;
+    if ((st = dist_launch(ctx, a, rows))) return st;
+    DecideArgs c{};
+    c.draft = draft_dev;
+    c.u = u_dev;
+    c.seed = philox_seed;
+    c.noise = noise_dev;
+    c.B = b;
+    c.k = k;
+    c.V = v;
+    c.mode = mode;
+    c.has_q = has_q;
+    c.nrow_p = nrow_p;
+    c.T = params->temp;
+    c.inv_t = 1.0f / fmaxf(params->temp, FLT_MIN);
+    c.sid = d.sid;
+    c.sl = d.sl;
+    c.pr = d.pr;
+    c.hdr = d.hdr;
+    c.qdense = has_q ? (float*)d.tail : nullptr;
+    c.out_tok = out_tok_dev;
+    c.out_n = out_n_dev;
+    decide_kernel<<<(unsigned)b, SB, 0, ctx->stream>>>(c);
+    CPV_HIP(ctx, hipGetLastError());
+    return CPV_OK;
 }

@@ -121,6 +121,18 @@ class Context:
                                       v_cache_t.shape[1], n_past, _ptr(par), t, h, h_kv, d, scale, _ptr(out)))
         return out
 
+    def distribution(self, logits, params, hist=None):
+        """Sampler::distribution of each row of logits [rows][v]: (ids, probs, n) device tensors."""
+        logits = logits.contiguous()
+        rows, v = logits.shape
+        ids = torch.empty((rows, v), dtype=torch.int32, device=logits.device)
+        probs = torch.empty((rows, v), dtype=torch.float32, device=logits.device)
+        n = torch.empty(rows, dtype=torch.int32, device=logits.device)
+        h = None if hist is None else hist.to(torch.int32).contiguous()
+        self._check(self.lib.cpv_distribution(self.h, _ptr(logits), rows, v, ctypes.byref(params), _ptr(h),
+                                              0 if h is None else h.shape[1], _ptr(ids), _ptr(probs), _ptr(n)))
+        return ids, probs, n
+
     def spec_accept(self, p_logits, draft, params, mode, u=None, q_logits=None, noise=None, hist=None,
                     philox_seed=0, out_tok=None, out_n=None):
         b, k1, v = p_logits.shape

@@ -131,6 +131,25 @@ typedef struct {
 
 enum { CPV_ACCEPT_GREEDY = 0, CPV_ACCEPT_REJECT = 1, CPV_ACCEPT_GUMBEL = 2 };
 
+/* Sampler::distribution (crates/codpiece-sample/src/lib.rs:184-187, built by
+ * Sampler::build :229-376) for `rows` independent logit rows: penalties over
+ * the row's history window, then top-k / min-p / top-p narrowing, the
+ * temperature and the softmax, with the CPU sampler's f32 results bit for
+ * bit (its sums are sequential folds in candidate order).
+ *   logits_dev  f32 [rows][v]
+ *   hist_dev    int32 [rows][hist_len] history, oldest first, -1 = empty
+ *               (NULL = none); the last penalty_last_n valid entries count
+ *   ids_dev     int32 [rows][v]: candidate ids in candidate order (logit
+ *               descending, id ascending after a narrowing filter, index
+ *               order otherwise); the first n_dev[r] are the distribution
+ *   probs_dev   f32 [rows][v]: their probabilities
+ *   n_dev       int32 [rows]
+ * 1 <= v <= 262144, hist_len <= 4096, min_p <= 1 (above 1 no candidate
+ * survives and the reference panics). */
+cpv_status  cpv_distribution(cpv_ctx* ctx, const float* logits_dev, int rows, int v,
+                             const cpv_sampler_params* params, const int32_t* hist_dev, int hist_len,
+                             int32_t* ids_dev, float* probs_dev, int32_t* n_dev);
+
 /* Decide a speculative round for b sequences on the device: the acceptance
  * loop of crates/codpiece-server/src/engine.rs:2326-2461 with the target
  * distribution of Sampler::distribution (crates/codpiece-sample/src/lib.rs:
@@ -152,7 +171,8 @@ enum { CPV_ACCEPT_GREEDY = 0, CPV_ACCEPT_REJECT = 1, CPV_ACCEPT_GUMBEL = 2 };
  *                 (only read when a penalty is active)
  *   out_tok_dev   int32 [b][k+1]: the accepted drafts then the next token
  *   out_n_dev     int32 [b]: number of accepted drafts (tokens = out_n + 1)
- * v <= 262144, k <= 15. */
+ * v <= 262144, k <= 15, hist_len <= 4096; params may be NULL in GREEDY mode.
+ * Outputs equal the CPU loop's for the same uniforms, bit for bit. */
 cpv_status  cpv_spec_accept(cpv_ctx* ctx, const float* p_logits_dev, const float* q_logits_dev,
                             const int32_t* draft_dev, int b, int k, int v,
                             const cpv_sampler_params* params, int mode, const float* u_dev,
@@ -230,9 +250,11 @@ cpv_status  cpv_verify_step(cpv_session* s, const int32_t* tokens_dev, int t, in
  * by a pair of HIP events on its stream; stop waits for the stream and sums,
  * per kernel class, the launches, their event-timed milliseconds and their
  * algorithmic bytes (GEMM: the quantized weight + 4*m*k + 4*m*n; attention:
- * the K and V rows read once + q and the output in f32).  The events add
- * a little time between launches: time throughput without them. */
-enum { CPV_PROF_Q4_K = 0, CPV_PROF_Q6_K = 1, CPV_PROF_Q8_0 = 2, CPV_PROF_ATTN = 3, CPV_PROF_CLASSES = 4 };
+ * the K and V rows read once + q and the output in f32; sampler: the logit
+ * rows read once).  The events add a little time between launches: time
+ * throughput without them. */
+enum { CPV_PROF_Q4_K = 0, CPV_PROF_Q6_K = 1, CPV_PROF_Q8_0 = 2, CPV_PROF_ATTN = 3, CPV_PROF_SAMPLE = 4,
+       CPV_PROF_CLASSES = 5 };
 typedef struct { int64_t launches; double ms; double bytes; } cpv_prof_stat;
 cpv_status  cpv_profile_start(cpv_ctx* ctx);
 cpv_status  cpv_profile_stop(cpv_ctx* ctx, cpv_prof_stat* out /* [CPV_PROF_CLASSES] */);
