@@ -204,7 +204,7 @@ def cpu_baseline(hp, layers, budget_s, tokens_per_round, depth, seed):
     round_s = layers * t_layer + t_head + depth * (t_layer + t_eh + t_head)
     return {
         "value": tokens_per_round / round_s, "unit": "tok/s", "cores": cores, "kind": "port",
-        "sample": (f"oracle (exact-window GEMMs, f64 attention) on one trunk layer at t={T}, n_past={n_past} "
+        "sample": (f"oracle (exact-window GEMMs, exact-contract attention) on one trunk layer at t={T}, n_past={n_past} "
                    f"({r_layer} reps, {t_layer * 1e3:.1f} ms), the Q6_K head ({r_head} reps, {t_head * 1e3:.1f} ms) "
                    f"and eh_proj, scaled to a round of {layers} layers + head + {depth} MTP links "
                    f"= {round_s:.2f} s, at the GPU run's {tokens_per_round:.3f} committed tokens per round"),

@@ -11,7 +11,8 @@
 //              f32 theta recurrence (qwen35.rs:3053-3062 with text positions)
 //   sigmoid    1/(1+expf(-x)); silu x/(1+expf(-x)); add / mul in f32
 //   mul_mat    the exact-window GEMM of qgemm.hip
-//   attention  attn.hip (f16 MFMA; within a tolerance of the f64 oracle)
+//   attention  attn.hip (the exact chunked contract the oracle restates:
+//              fixed-point scores, exact normalisers, fixed-order sums)
 // The K cache is [n_ctx][h_kv*d] and V is kept transposed [h_kv*d][n_ctx]
 // (the reference's non-FA V layout), one pair per layer plus the MTP pair.
 #include <math.h>

@@ -193,18 +193,27 @@ def same(got, ref):
 
 
 @pytest.mark.parametrize("B", [1, 4, 16])
-def test_reject_headline_philox(ctx, B):
-    # rejection sampling against top-p 0.95 at T = 0.7, device Philox uniforms
-    print(f"case accept reject B={B}", flush=True)
+def test_headline_acceptance(ctx, B):
+    # target logits ~N(0,3) + a +8 spike, draft logits = target + N(0,1),
+    # drafts sampled from the draft distribution; T = 0.7, top-p 0.95,
+    # device Philox uniforms; rejection with the draft distribution, the
+    # one-hot rule, and greedy argmax match
+    print(f"case accept headline B={B}", flush=True)
     k = 4
     rng = np.random.default_rng(100 + B)
     pl = spiked(rng, (B, k + 1, V27))
-    draft = drafts_for(rng, pl, k)
+    ql = (pl[:, :k] + rng.normal(0, 1, size=(B, k, V27))).astype(np.float32)
     p = cpvo.SamplerParams(temp=0.7, top_p=0.95)
+    draft = np.array([[cpvo.Sampler(p).distribution(ql[b, j]).draw(np.float32(rng.random())) for j in range(k)]
+                      for b in range(B)], dtype=np.int32)
     seed = 1234 + B
-    got = accept(ctx, pl, draft, p, cpvo.ACCEPT_REJECT, seed=seed)
-    ref = cpvo.spec_accept(pl, draft, p, cpvo.ACCEPT_REJECT, u=cpvo.philox_uniforms(seed, B, k))
-    same(got, ref)
+    u = cpvo.philox_uniforms(seed, B, k)
+    same(accept(ctx, pl, draft, p, cpvo.ACCEPT_REJECT, seed=seed, q=ql),
+         cpvo.spec_accept(pl, draft, p, cpvo.ACCEPT_REJECT, u=u, q_logits=ql))
+    same(accept(ctx, pl, draft, p, cpvo.ACCEPT_REJECT, seed=seed),
+         cpvo.spec_accept(pl, draft, p, cpvo.ACCEPT_REJECT, u=u))
+    g = cpvo.SamplerParams()
+    same(accept(ctx, pl, draft, g, cpvo.ACCEPT_GREEDY), cpvo.spec_accept(pl, draft, g, cpvo.ACCEPT_GREEDY))
 
 
 def test_reject_many_rounds_small_vocab(ctx):
