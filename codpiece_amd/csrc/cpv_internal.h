@@ -20,8 +20,8 @@ struct cpv_ctx {
     void* ws = nullptr;
     size_t ws_bytes = 0;
     uint64_t ws_gen = 0;      // bumped whenever ws (or the GEMM accumulator) is reallocated
-    // the split-K GEMM accumulator [16][n_pad] f64: zero between launches
-    // (each finalize leaves it as it found it)
+    // the split-K GEMM accumulator [rows][n_pad] f64: zero between uses (each
+    // finalize, and each fused consumer of a kept result, leaves it zero)
     double* gsum = nullptr;
     size_t gsum_bytes = 0;
     // kernel timing (cpv_profile_start / _stop): event pairs around launches,
@@ -149,8 +149,48 @@ struct cpv_act {
     bool kq;                 // Q8_K (for Q4_K / Q6_K weights) or Q8_0
 };
 size_t cpv_act_bytes(int type, int64_t k, int64_t m);
+// the cpv_act views of buf for m rows of length k (no work launched)
+void cpv_act_layout(int type, int64_t m, int64_t k, void* buf, cpv_act* out);
 cpv_status cpv_quant_act(cpv_ctx* ctx, int type, const float* x, int64_t m, int64_t k, void* buf, cpv_act* out);
 cpv_status cpv_qgemm_act(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, float* y);
+
+// A GEMM result kept in the accumulator for a fused consumer: row m, output n
+// is cpv_gout_value(acc[m * n_pad + n], ew[n], Ea(m), win) with Ea(m) the
+// frexp exponent of max |da[m][0..nda)|; the consumer reads each entry once
+// and writes it back to zero.
+struct cpv_gout {
+    double* acc;
+    int64_t n_pad, n;
+    const int32_t* ew;
+    const float* da;
+    int nda, win;
+};
+cpv_status cpv_qgemm_keep(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, cpv_gout* out);
+
+// floor(sq * 2^-g) for a non-negative finite f32 sq, as an integer: sq is its
+// 24-bit mantissa times a power of two, so the floor is a shift (the same value
+// as floor(ldexp((double)sq, -g)), without binary64 arithmetic).  Callers keep
+// the result below 2^63.
+__host__ __device__ __forceinline__ long long cpv_fixed_floor(float sq, int g)
+{
+    const uint32_t b = __builtin_bit_cast(uint32_t, sq);
+    const int be = (int)(b >> 23);
+    const long long mant = (long long)((b & 0x7fffffu) | (be ? 0x800000u : 0u));
+    const int sh = (be ? be : 1) - 150 - g;                 // sq = mant * 2^(sh + g)
+    if (sh >= 0) return mant << sh;
+    return -sh >= 63 ? 0 : mant >> (-sh);
+}
+
+__host__ __device__ __forceinline__ int cpv_exp_of_max(float mx)
+{
+    int e = CPV_E_EMPTY;
+    if (mx > 0.0f) frexpf(mx, &e);
+    return e;
+}
+__host__ __device__ __forceinline__ float cpv_gout_value(double S, int ew, int ea, int win)
+{
+    return (ew == CPV_E_EMPTY || ea == CPV_E_EMPTY) ? 0.0f : (float)ldexp(S, ew + ea - win);
+}
 
 // rows of several weights stacked into a new weight (same type and k, every
 // part but the last in whole 64-row tiles)

@@ -55,7 +55,8 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__
 #pragma unroll
         for (int j = 0; j < RMS_PER; j++) {
             const int i = tid + j * blockDim.x;
-            v[j] = i < n ? xr[i] : 0.0f;
+            const float xi = xr[i < n ? i : n - 1];          // every lane loads: no wait per element
+            v[j] = i < n ? xi : 0.0f;
             am = fmaxf(am, fabsf(v[j]));
         }
     } else {
@@ -74,11 +75,11 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__
         long long S = 0;
         if (cached) {
 #pragma unroll
-            for (int j = 0; j < RMS_PER; j++) S += (long long)floor(ldexp((double)(v[j] * v[j]), -g));
+            for (int j = 0; j < RMS_PER; j++) S += cpv_fixed_floor(v[j] * v[j], g);
         } else {
             for (int i = tid; i < n; i += blockDim.x) {
                 const float sq = xr[i] * xr[i];
-                S += (long long)floor(ldexp((double)sq, -g));
+                S += cpv_fixed_floor(sq, g);
             }
         }
         for (int off = 32; off > 0; off >>= 1) S += __shfl_xor(S, off);
@@ -150,7 +151,7 @@ __global__ __launch_bounds__(128) void qk_prep_kernel(PrepArgs a)
         int e;
         frexpf(am, &e);
         const int g = 2 * e - (62 - ceil_log2_dev(a.hd + 1));
-        long long S = (long long)floor(ldexp((double)(x * x), -g));
+        long long S = cpv_fixed_floor(x * x, g);
         for (int off = 32; off > 0; off >>= 1) S += __shfl_xor(S, off);
         if ((i & 63) == 0) s_s[i >> 6] = S;
         __syncthreads();
@@ -247,6 +248,409 @@ __global__ __launch_bounds__(1024) void peak_kernel(const float* __restrict__ x,
     }
 }
 
+// ---------------------------------------------------------------- fused row kernels
+// One 1024-thread block per activation row.  Wave w holds the row's 256-element
+// units u = w, w + 16, ...; lane l holds elements u*256 + l + 64k (k < 4) of
+// each, so every per-unit step of the quantization is a wave reduction with no
+// barrier.  A row kernel produces the row (from the residual and a GEMM result
+// kept in the accumulator, or from the attention output and its gate, or from
+// the gate|up GEMM through SwiGLU), optionally RMS-normalizes it, and
+// optionally quantizes it for the next GEMM, with the same arithmetic as the
+// separate kernels it replaces (add_kernel, rmsnorm_kernel, gate_mul_kernel,
+// swiglu_kernel, quant_q8k_kernel / quant_q80_kernel).
+constexpr int RB = 1024;     // threads per row block
+constexpr int RW = RB / 64;  // waves
+constexpr int RUU = 3;       // units per wave: rows up to 3 * 16 * 256 = 12288 elements
+constexpr int RQ = RUU * 4;  // register slots per thread
+
+enum { SRC_X = 0, SRC_ADD = 1, SRC_SET = 2, SRC_GATE = 3, SRC_SWIGLU = 4 };
+
+struct RowArgs {
+    int src;
+    float* x;              // residual rows [T][xs] (SRC_X / _ADD / _SET read and write it)
+    int64_t xs;
+    cpv_gout g;            // kept GEMM result (SRC_ADD / _SET / _SWIGLU)
+    const float* att;      // SRC_GATE: attention output [T][n] and gate [T][n]
+    const float* gate;
+    int n;                 // row length
+    const float* w;        // RMS norm weight, when norm
+    int norm;
+    float eps;
+    float* y;              // optional f32 copy of the produced (normalized) row, stride ys
+    int64_t ys;
+    int quant;             // quantize the row into act (0: no)
+    cpv_act act;
+};
+
+struct RowLds {
+    float red_f[RW];
+    long long red_l[RW];
+};
+
+__device__ float row_max(float v, RowLds& L)
+{
+    const int tid = threadIdx.x;
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    __syncthreads();
+    if ((tid & 63) == 0) L.red_f[tid >> 6] = v;
+    __syncthreads();
+    float r = L.red_f[0];
+    for (int i = 1; i < RW; i++) r = fmaxf(r, L.red_f[i]);
+    return r;
+}
+
+__device__ long long row_sum(long long v, RowLds& L)
+{
+    const int tid = threadIdx.x;
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    __syncthreads();
+    if ((tid & 63) == 0) L.red_l[tid >> 6] = v;
+    __syncthreads();
+    long long r = 0;
+    for (int i = 0; i < RW; i++) r += L.red_l[i];
+    return r;
+}
+
+__device__ __forceinline__ float take(const cpv_gout& g, int m, int64_t n, int ea)
+{
+    double* p = g.acc + (int64_t)m * g.n_pad + n;
+    const double S = *p;
+    *p = 0.0;
+    return cpv_gout_value(S, g.ew[n], ea, g.win);
+}
+
+template <int SRC>
+__global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
+{
+    __shared__ RowLds L;
+    const int m = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int n = a.n, U = (n + 255) / 256;
+    constexpr bool kept = SRC == SRC_ADD || SRC == SRC_SET;
+    float* xr = a.x ? a.x + (int64_t)m * a.xs : nullptr;
+    // ---- the plain inputs go out first (every lane loads: no join before the uses)
+    float v[RQ];
+#pragma unroll
+    for (int uu = 0; uu < RUU; uu++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int j = uu * 4 + k, u = wave + RW * uu;
+            const int e = u * 256 + lane + 64 * k;
+            const int ec = e < n ? e : n - 1;
+            v[j] = (SRC == SRC_X || SRC == SRC_ADD) ? xr[ec] : 0.0f;
+        }
+    // ---- a kept result: its sums and row exponents are loaded before anything
+    // is stored (the stores below could alias them), then Ea, then y = the
+    // finalized sums, folded into x, the accumulator entries cleared
+    if (kept) {
+        double* acc = a.g.acc + (int64_t)m * a.g.n_pad;
+        double S[RQ];
+        int ew[RQ];
+#pragma unroll
+        for (int uu = 0; uu < RUU; uu++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int j = uu * 4 + k, u = wave + RW * uu;
+                const int e = u * 256 + lane + 64 * k;
+                const int ec = e < n ? e : n - 1;
+                S[j] = acc[ec];
+                ew[j] = a.g.ew[ec];
+            }
+        float mx = 0.0f;
+        for (int i = tid; i < a.g.nda; i += RB) mx = fmaxf(mx, fabsf(a.g.da[(int64_t)m * a.g.nda + i]));
+        const int ea = cpv_exp_of_max(row_max(mx, L));
+#pragma unroll
+        for (int uu = 0; uu < RUU; uu++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int j = uu * 4 + k, u = wave + RW * uu;
+                const int e = u * 256 + lane + 64 * k;
+                if (u < U && e < n) {
+                    const float gv = cpv_gout_value(S[j], ew[j], ea, a.g.win);
+                    v[j] = SRC == SRC_ADD ? gv + v[j] : gv;
+                    acc[e] = 0.0;
+                    xr[e] = v[j];
+                }
+            }
+    }
+#pragma unroll
+    for (int uu = 0; uu < RUU; uu++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int u = wave + RW * uu, e = u * 256 + lane + 64 * k;
+            if (!(u < U && e < n)) v[uu * 4 + k] = 0.0f;
+        }
+    if (a.norm) {
+        // exact fixed-point sum of the f32 squares, then ggml's f32 tail
+        float am = 0.0f;
+#pragma unroll
+        for (int j = 0; j < RQ; j++) am = fmaxf(am, fabsf(v[j]));
+        am = row_max(am, L);
+        double sum = 0.0;
+        if (am > 0.0f) {
+            int e;
+            frexpf(am, &e);
+            const int g2 = 2 * e - (62 - ceil_log2_dev(n + 1));
+            long long S = 0;
+#pragma unroll
+            for (int j = 0; j < RQ; j++) S += cpv_fixed_floor(v[j] * v[j], g2);
+            sum = ldexp((double)row_sum(S, L), g2);
+        }
+        const float mean = (float)(sum / (double)n);
+        const float scale = 1.0f / sqrtf(mean + a.eps);
+#pragma unroll
+        for (int uu = 0; uu < RUU; uu++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int j = uu * 4 + k, u = wave + RW * uu;
+                const int e = u * 256 + lane + 64 * k;
+                const float tv = v[j] * scale;
+                v[j] = (u < U && e < n) ? (a.w ? tv * a.w[e] : tv) : 0.0f;   // padding stays 0
+            }
+    }
+    if (a.y) {
+#pragma unroll
+        for (int uu = 0; uu < RUU; uu++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int u = wave + RW * uu, e = u * 256 + lane + 64 * k;
+                if (u < U && e < n) a.y[(int64_t)m * a.ys + e] = v[uu * 4 + k];
+            }
+    }
+    if (!a.quant) return;
+    const int64_t Kp = (int64_t)U * 256;
+    int8_t* qa = const_cast<int8_t*>(a.act.qa);           // cpv_act is the GEMM's read-only view
+    float* da = const_cast<float*>(a.act.da);
+    int32_t* bs16 = const_cast<int32_t*>(a.act.bs16);
+    int32_t* bs32 = const_cast<int32_t*>(a.act.bs32);
+#pragma unroll
+    for (int uu = 0; uu < RUU; uu++) {
+        const int u = wave + RW * uu;
+        if (u >= U) break;                                  // wave-uniform
+        const float* x = v + uu * 4;
+        int8_t* qrow = qa + (int64_t)m * Kp + (int64_t)u * 256;
+        if (a.act.kq) {
+            // Q8_K: the signed element of largest magnitude (first occurrence),
+            // iscale = -127/max, q = min(127, rint(iscale * x)), d = 1/iscale, code sums
+            float ax = fabsf(x[0]);
+            int ix = lane, kk = 0;
+#pragma unroll
+            for (int k = 1; k < 4; k++)
+                if (fabsf(x[k]) > ax) { ax = fabsf(x[k]); ix = lane + 64 * k; kk = k; }
+            float sx = x[kk];
+            for (int off = 32; off > 0; off >>= 1) {
+                const float oa = __shfl_xor(ax, off);
+                const int oi = __shfl_xor(ix, off);
+                const float os = __shfl_xor(sx, off);
+                if (oa > ax || (oa == ax && oi < ix)) { ax = oa; ix = oi; sx = os; }
+            }
+            int q[4];
+            float d = 0.0f;
+            if (ax > 0.0f) {
+                const float iscale = -127.0f / sx;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int vq = (int)rintf(iscale * x[k]);
+                    q[k] = vq < 127 ? vq : 127;
+                }
+                d = 1.0f / iscale;
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; k++) q[k] = 0;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                qrow[lane + 64 * k] = (int8_t)q[k];
+                int s16 = q[k];
+                for (int off = 8; off > 0; off >>= 1) s16 += __shfl_xor(s16, off);
+                const int s32 = s16 + __shfl_xor(s16, 16);
+                if ((lane & 15) == 0) bs16[((int64_t)m * U + u) * 16 + k * 4 + (lane >> 4)] = s16;
+                if ((lane & 31) == 0) bs32[((int64_t)m * U + u) * 8 + k * 2 + (lane >> 5)] = s32;
+            }
+            if (lane == 0) da[(int64_t)m * U + u] = d;
+        } else {
+            // Q8_0 per 32-element block: d = amax/127, q = roundf(x * (1/d)), d kept as fp16
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float amax = fabsf(x[k]);
+                for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+                const float d = amax / 127.0f;
+                const float id = d != 0.0f ? 1.0f / d : 0.0f;
+                qrow[lane + 64 * k] = (int8_t)(int)roundf(x[k] * id);
+                if ((lane & 31) == 0) da[((int64_t)m * U + u) * 8 + k * 2 + (lane >> 5)] = cpv_h2f(cpv_f2h(d));
+            }
+        }
+    }
+}
+
+// The same for rows that need no row-wide reduction: the gated attention
+// output (SRC_GATE) and SwiGLU of a kept gate|up result (SRC_SWIGLU), each
+// quantized for the next GEMM.  One 256-thread block per (unit, row).
+template <int SRC>
+__global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
+{
+    __shared__ float s_ax[4], s_sx[4];
+    __shared__ int s_ix[4];
+    const int u = blockIdx.x, m = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int n = a.n, U = (n + 255) / 256;
+    const int e = u * 256 + t, ec = e < n ? e : n - 1;
+    float val = 0.0f;
+    if (SRC == SRC_GATE) {
+        const float gv = a.gate[(int64_t)m * n + ec], at = a.att[(int64_t)m * n + ec];
+        const float sig = 1.0f / (1.0f + cpv_expf(-gv));
+        val = e < n ? at * sig : 0.0f;
+    } else {
+        double* acc = a.g.acc + (int64_t)m * a.g.n_pad;
+        const double S0 = acc[ec], S1 = acc[n + ec];
+        const int e0 = a.g.ew[ec], e1 = a.g.ew[n + ec];
+        float mx = 0.0f;
+        for (int i = t; i < a.g.nda; i += 256) mx = fmaxf(mx, fabsf(a.g.da[(int64_t)m * a.g.nda + i]));
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        if (lane == 0) s_ax[wave] = mx;
+        __syncthreads();
+        mx = fmaxf(fmaxf(s_ax[0], s_ax[1]), fmaxf(s_ax[2], s_ax[3]));
+        __syncthreads();
+        const int ea = cpv_exp_of_max(mx);
+        if (e < n) {
+            const float gv = cpv_gout_value(S0, e0, ea, a.g.win), uv = cpv_gout_value(S1, e1, ea, a.g.win);
+            acc[e] = 0.0;
+            acc[n + e] = 0.0;
+            const float sl = gv / (1.0f + cpv_expf(-gv));
+            val = sl * uv;
+        }
+    }
+    if (!a.quant) return;
+    int8_t* qa = const_cast<int8_t*>(a.act.qa);           // cpv_act is the GEMM's read-only view
+    float* da = const_cast<float*>(a.act.da);
+    const int64_t Kp = (int64_t)U * 256;
+    if (a.act.kq) {
+        // Q8_K: the signed element of largest magnitude (first occurrence),
+        // iscale = -127/max, q = min(127, rint(iscale * x)), d = 1/iscale, code sums
+        float ax = fabsf(val), sx = val;
+        int ix = t;
+        for (int off = 32; off > 0; off >>= 1) {
+            const float oa = __shfl_xor(ax, off), os = __shfl_xor(sx, off);
+            const int oi = __shfl_xor(ix, off);
+            if (oa > ax || (oa == ax && oi < ix)) { ax = oa; ix = oi; sx = os; }
+        }
+        if (lane == 0) { s_ax[wave] = ax; s_ix[wave] = ix; s_sx[wave] = sx; }
+        __syncthreads();
+        ax = s_ax[0];
+        ix = s_ix[0];
+        sx = s_sx[0];
+        for (int w = 1; w < 4; w++)
+            if (s_ax[w] > ax || (s_ax[w] == ax && s_ix[w] < ix)) { ax = s_ax[w]; ix = s_ix[w]; sx = s_sx[w]; }
+        int q = 0;
+        float d = 0.0f;
+        if (ax > 0.0f) {
+            const float iscale = -127.0f / sx;
+            const int vq = (int)rintf(iscale * val);
+            q = vq < 127 ? vq : 127;
+            d = 1.0f / iscale;
+        }
+        qa[(int64_t)m * Kp + e] = (int8_t)q;
+        int s16 = q;
+        for (int off = 8; off > 0; off >>= 1) s16 += __shfl_xor(s16, off);
+        const int s32 = s16 + __shfl_xor(s16, 16);
+        if ((t & 15) == 0) const_cast<int32_t*>(a.act.bs16)[((int64_t)m * U + u) * 16 + (t >> 4)] = s16;
+        if ((t & 31) == 0) const_cast<int32_t*>(a.act.bs32)[((int64_t)m * U + u) * 8 + (t >> 5)] = s32;
+        if (t == 0) da[(int64_t)m * U + u] = d;
+    } else {
+        // Q8_0 per 32-element block: d = amax/127, q = roundf(x * (1/d)), d kept as fp16
+        float amax = fabsf(val);
+        for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        qa[(int64_t)m * Kp + e] = (int8_t)(int)roundf(val * id);
+        if ((t & 31) == 0) da[((int64_t)m * U + u) * 8 + (t >> 5)] = cpv_h2f(cpv_f2h(d));
+    }
+}
+
+// qk_prep_kernel on a kept q|gate|k|v GEMM result: each value is finalized
+// (and its accumulator entry cleared) by the block that uses it; the query
+// heads also write their output gate to gate_out [T][H][hd].
+struct PrepKeptArgs {
+    PrepArgs p;
+    cpv_gout g;
+    float* gate_out;
+};
+
+__global__ __launch_bounds__(128) void qk_prep_kept_kernel(PrepKeptArgs ka)
+{
+    const PrepArgs& a = ka.p;
+    const int t = blockIdx.x, hh = blockIdx.y, i = threadIdx.x;
+    const bool is_q = hh < a.H;
+    const int kh = hh - a.H;
+    __shared__ float s_v[128];
+    __shared__ float s_am[2];
+    __shared__ long long s_s[2];
+    // Ea of this token's activation row
+    float mx = 0.0f;
+    for (int c = i; c < ka.g.nda; c += a.hd) mx = fmaxf(mx, fabsf(ka.g.da[(int64_t)t * ka.g.nda + c]));
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if ((i & 63) == 0) s_am[i >> 6] = mx;
+    __syncthreads();
+    mx = s_am[0];
+    if (a.hd > 64) mx = fmaxf(mx, s_am[1]);
+    const int ea = cpv_exp_of_max(mx);
+    __syncthreads();
+    const int64_t qoff = (int64_t)2 * a.H * a.hd;
+    float x, vv = 0.0f;
+    if (is_q) {
+        x = take(ka.g, t, (int64_t)hh * 2 * a.hd + i, ea);
+        ka.gate_out[((int64_t)t * a.H + hh) * a.hd + i] = take(ka.g, t, (int64_t)hh * 2 * a.hd + a.hd + i, ea);
+    } else {
+        x = take(ka.g, t, qoff + (int64_t)kh * a.hd + i, ea);
+        vv = take(ka.g, t, qoff + (int64_t)a.Hkv * a.hd + (int64_t)kh * a.hd + i, ea);
+    }
+    const float* w = is_q ? a.q_norm : a.k_norm;
+    float am = fabsf(x);
+    for (int off = 32; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));
+    if ((i & 63) == 0) s_am[i >> 6] = am;
+    __syncthreads();
+    am = s_am[0];
+    if (a.hd > 64) am = fmaxf(am, s_am[1]);
+    double sum = 0.0;
+    if (am > 0.0f) {
+        int e;
+        frexpf(am, &e);
+        const int g = 2 * e - (62 - ceil_log2_dev(a.hd + 1));
+        long long S = cpv_fixed_floor(x * x, g);
+        for (int off = 32; off > 0; off >>= 1) S += __shfl_xor(S, off);
+        if ((i & 63) == 0) s_s[i >> 6] = S;
+        __syncthreads();
+        S = s_s[0] + (a.hd > 64 ? s_s[1] : 0);
+        sum = ldexp((double)S, g);
+    }
+    const float mean = (float)(sum / (double)a.hd);
+    const float scale = 1.0f / sqrtf(mean + a.eps);
+    const float v0 = x * scale;
+    const float xn = w ? v0 * w[i] : v0;
+    s_v[i] = xn;
+    __syncthreads();
+    float out = xn;
+    const int half = a.n_rot / 2;
+    if (i < a.n_rot) {
+        const int p = i < half ? i : i - half;
+        const float* cs = a.rope + (a.rope_pos0 + t) * a.n_rot + 2 * p;
+        const float c = cs[0], sn = cs[1];
+        const float x0 = s_v[p], x1 = s_v[p + half];
+        if (i < half) {
+            const float m0 = x0 * c, m1 = x1 * sn;
+            out = m0 - m1;
+        } else {
+            const float m0 = x0 * sn, m1 = x1 * c;
+            out = m0 + m1;
+        }
+    }
+    if (is_q) {
+        a.qout[((int64_t)t * a.H + hh) * a.hd + i] = out;
+    } else if (a.write) {
+        const int64_t row = a.kv_row0 + t;
+        a.k_cache[row * a.Hkv * a.hd + (int64_t)kh * a.hd + i] = cpv_f2h(out);
+        a.v_cache_t[((int64_t)kh * a.hd + i) * a.v_stride + row] = cpv_f2h(vv);
+    }
+}
+
 unsigned grid_for(int64_t n) { return (unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096); }
 
 }  // namespace
@@ -285,7 +689,9 @@ struct cpv_session {
     float *qkv, *gu;                      // outputs of the stacked q|k|v and gate|up GEMMs
     int32_t *tok, *preds, *chain;
     float* conf;
-    void* actbuf;                         // quantized activations
+    void* actbuf;                         // quantized activations (two buffers, alternating:
+    void* actbuf2;                        // a kept GEMM result refers to the scales of its input
+    int act_i = 0;                        // while its consumer quantizes the next GEMM's input)
     size_t actbuf_bytes;
     float* tap = nullptr;                 // attention outputs of each call, when set
     int64_t tap_cap = 0, tap_off = 0;
@@ -538,6 +944,7 @@ extern "C" cpv_status cpv_session_create(cpv_model* m, int64_t n_ctx, int32_t ma
     s->actbuf_bytes = cpv_act_bytes(CPV_Q4_K, kmax, T) > cpv_act_bytes(CPV_Q8_0, kmax, T)
                     ? cpv_act_bytes(CPV_Q4_K, kmax, T) : cpv_act_bytes(CPV_Q8_0, kmax, T);
     A(s->actbuf_bytes, &s->actbuf);
+    A(s->actbuf_bytes, &s->actbuf2);
     // rope table: positions up to n_ctx + 1 (the MTP head runs one position ahead)
     const int64_t npos = n_ctx + 2, nrot = hp.n_rot;
     if (st == CPV_OK && nrot > 0) {
@@ -608,6 +1015,12 @@ extern "C" cpv_status cpv_session_get_pos(const cpv_session* s, int64_t* n_past,
 // ---------------------------------------------------------------- forward
 namespace {
 
+void* next_act(cpv_session* s)
+{
+    s->act_i ^= 1;
+    return s->act_i ? s->actbuf2 : s->actbuf;
+}
+
 cpv_status rmsnorm(cpv_ctx* ctx, const float* x, int64_t xs, const float* w, float* y, int64_t ys, int64_t rows,
                    int n, float eps)
 {
@@ -616,8 +1029,35 @@ cpv_status rmsnorm(cpv_ctx* ctx, const float* x, int64_t xs, const float* w, flo
     return CPV_OK;
 }
 
-// one attention block + FFN block of layer L on s->x (in place), T rows
-cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_pos0, int64_t kv_row0,
+cpv_status row_launch(cpv_ctx* ctx, const RowArgs& a, int T)
+{
+    const dim3 ugrid((unsigned)((a.n + 255) / 256), (unsigned)T);
+    switch (a.src) {
+    case SRC_X: row_kernel<SRC_X><<<(unsigned)T, RB, 0, ctx->stream>>>(a); break;
+    case SRC_ADD: row_kernel<SRC_ADD><<<(unsigned)T, RB, 0, ctx->stream>>>(a); break;
+    case SRC_SET: row_kernel<SRC_SET><<<(unsigned)T, RB, 0, ctx->stream>>>(a); break;
+    case SRC_GATE: unit_kernel<SRC_GATE><<<ugrid, 256, 0, ctx->stream>>>(a); break;
+    default: unit_kernel<SRC_SWIGLU><<<ugrid, 256, 0, ctx->stream>>>(a); break;
+    }
+    CPV_HIP(ctx, hipGetLastError());
+    return CPV_OK;
+}
+
+// fold a kept GEMM result into x (SRC_ADD: x += y, SRC_SET: x = y), nothing else
+cpv_status apply_kept(cpv_session* s, float* x, int T, const cpv_gout& g, int src)
+{
+    RowArgs r{};
+    r.src = src;
+    r.x = x;
+    r.xs = s->model->hp.n_embd;
+    r.g = g;
+    r.n = (int)s->model->hp.n_embd;
+    return row_launch(s->model->ctx, r, T);
+}
+
+// one attention block + FFN block of layer L on x (in place), T rows, one
+// kernel per op: the path for unstacked weights
+cpv_status block_unfused(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_pos0, int64_t kv_row0,
                  int64_t attn_past, uint16_t* kc, uint16_t* vt, int64_t v_stride, bool write)
 {
     cpv_model* m = s->model;
@@ -631,18 +1071,18 @@ cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_
     PrepArgs pa;
     if (L.qkv) {
         // one GEMM for q|gate, k and v: row stride 2*H*hd + 2*Hkv*hd
-        if ((st = cpv_quant_act(ctx, L.qkv->type, s->xn, T, E, s->actbuf, &act))) return st;
+        if ((st = cpv_quant_act(ctx, L.qkv->type, s->xn, T, E, next_act(s), &act))) return st;
         if ((st = cpv_qgemm_act(ctx, L.qkv, &act, s->qkv))) return st;
         pa.qg = s->qkv;
         pa.kk = s->qkv + 2 * H * hd;
         pa.vv = pa.kk + Hkv * hd;
         pa.qs = pa.ks = L.qkv->n;
     } else {
-        if ((st = cpv_quant_act(ctx, L.wq->type, s->xn, T, E, s->actbuf, &act))) return st;
+        if ((st = cpv_quant_act(ctx, L.wq->type, s->xn, T, E, next_act(s), &act))) return st;
         if ((st = cpv_qgemm_act(ctx, L.wq, &act, s->qg))) return st;
-        if (L.wk->type != L.wq->type && (st = cpv_quant_act(ctx, L.wk->type, s->xn, T, E, s->actbuf, &act))) return st;
+        if (L.wk->type != L.wq->type && (st = cpv_quant_act(ctx, L.wk->type, s->xn, T, E, next_act(s), &act))) return st;
         if ((st = cpv_qgemm_act(ctx, L.wk, &act, s->kk))) return st;
-        if (L.wv->type != L.wk->type && (st = cpv_quant_act(ctx, L.wv->type, s->xn, T, E, s->actbuf, &act))) return st;
+        if (L.wv->type != L.wk->type && (st = cpv_quant_act(ctx, L.wv->type, s->xn, T, E, next_act(s), &act))) return st;
         if ((st = cpv_qgemm_act(ctx, L.wv, &act, s->vv))) return st;
         pa.qg = s->qg;
         pa.kk = s->kk;
@@ -679,37 +1119,179 @@ cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_
     }
     gate_mul_kernel<<<grid_for(T * H * hd), 256, 0, ctx->stream>>>(s->att, pa.qg, pa.qs, (int)H, (int)hd, T * H * hd,
                                                                   s->gated);
-    if ((st = cpv_quant_act(ctx, L.wo->type, s->gated, T, H * hd, s->actbuf, &act))) return st;
+    if ((st = cpv_quant_act(ctx, L.wo->type, s->gated, T, H * hd, next_act(s), &act))) return st;
     if ((st = cpv_qgemm_act(ctx, L.wo, &act, s->o))) return st;
     add_kernel<<<grid_for(T * E), 256, 0, ctx->stream>>>(s->o, x, x, T * E);
     // FFN
     if ((st = rmsnorm(ctx, x, E, L.post_norm, s->xn, E, T, (int)E, hp.rms_eps))) return st;
     if (L.gate_up) {
         // one GEMM for gate|up: row stride 2F
-        if ((st = cpv_quant_act(ctx, L.gate_up->type, s->xn, T, E, s->actbuf, &act))) return st;
+        if ((st = cpv_quant_act(ctx, L.gate_up->type, s->xn, T, E, next_act(s), &act))) return st;
         if ((st = cpv_qgemm_act(ctx, L.gate_up, &act, s->gu))) return st;
         swiglu_kernel<<<grid_for(T * F), 256, 0, ctx->stream>>>(s->gu, s->gu + F, 2 * F, F, s->act, T * F);
     } else {
-        if ((st = cpv_quant_act(ctx, L.up->type, s->xn, T, E, s->actbuf, &act))) return st;
+        if ((st = cpv_quant_act(ctx, L.up->type, s->xn, T, E, next_act(s), &act))) return st;
         if ((st = cpv_qgemm_act(ctx, L.up, &act, s->up))) return st;
-        if (L.gate->type != L.up->type && (st = cpv_quant_act(ctx, L.gate->type, s->xn, T, E, s->actbuf, &act)))
+        if (L.gate->type != L.up->type && (st = cpv_quant_act(ctx, L.gate->type, s->xn, T, E, next_act(s), &act)))
             return st;
         if ((st = cpv_qgemm_act(ctx, L.gate, &act, s->gt))) return st;
         swiglu_kernel<<<grid_for(T * F), 256, 0, ctx->stream>>>(s->gt, s->up, F, F, s->act, T * F);
     }
-    if ((st = cpv_quant_act(ctx, L.down->type, s->act, T, F, s->actbuf, &act))) return st;
+    if ((st = cpv_quant_act(ctx, L.down->type, s->act, T, F, next_act(s), &act))) return st;
     if ((st = cpv_qgemm_act(ctx, L.down, &act, s->d))) return st;
     add_kernel<<<grid_for(T * E), 256, 0, ctx->stream>>>(s->d, x, x, T * E);
     CPV_HIP(ctx, hipGetLastError());
     return CPV_OK;
 }
 
+bool fusable(const cpv_model* m, const LayerW& L)
+{
+    const cpv_hparams& hp = m->hp;
+    // the residual rows go through row_kernel (RQ elements per thread); the
+    // gated attention output and SwiGLU rows through unit_kernel (any length)
+    return L.qkv && L.gate_up && hp.n_embd <= (int64_t)RQ * RB;
+}
+
+// One attention block + FFN block of layer L on x (in place), T rows.  pend,
+// when given, is a kept GEMM result folded into x first (pend_src: SRC_ADD or
+// SRC_SET).  On return *out holds the block's FFN down projection as a kept
+// result still to be added to x (the next block, the final norm or apply_kept
+// folds it in), or out->acc is null when the block already added it.
+// Launches per block: norm+quant, q|k|v GEMM, prep, attention (2), gate+quant,
+// wo GEMM, residual+norm+quant, gate|up GEMM, SwiGLU+quant, down GEMM.
+cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_pos0, int64_t kv_row0,
+                 int64_t attn_past, uint16_t* kc, uint16_t* vt, int64_t v_stride, bool write, const cpv_gout* pend,
+                 int pend_src, cpv_gout* out)
+{
+    cpv_model* m = s->model;
+    cpv_ctx* ctx = m->ctx;
+    const cpv_hparams& hp = m->hp;
+    const int64_t E = hp.n_embd, hd = hp.head_dim, H = hp.n_head, Hkv = hp.n_head_kv, F = hp.n_ff;
+    cpv_status st;
+    out->acc = nullptr;
+    if (!fusable(m, L)) {
+        if (pend && (st = apply_kept(s, x, T, *pend, pend_src))) return st;
+        return block_unfused(s, L, x, T, rope_pos0, kv_row0, attn_past, kc, vt, v_stride, write);
+    }
+    // attention norm (after the pending residual term) and the q|k|v input
+    RowArgs r{};
+    r.src = pend ? pend_src : SRC_X;
+    r.x = x;
+    r.xs = E;
+    if (pend) r.g = *pend;
+    r.n = (int)E;
+    r.w = L.attn_norm;
+    r.norm = 1;
+    r.eps = hp.rms_eps;
+    r.quant = 1;
+    cpv_act_layout(L.qkv->type, T, E, next_act(s), &r.act);
+    if ((st = row_launch(ctx, r, T))) return st;
+    cpv_gout g;
+    if ((st = cpv_qgemm_keep(ctx, L.qkv, &r.act, &g))) return st;
+    // q/k norm, rope, KV write, output gate
+    PrepKeptArgs pk;
+    PrepArgs& pa = pk.p;
+    pa.qg = pa.kk = pa.vv = nullptr;
+    pa.qs = pa.ks = 0;
+    pa.q_norm = L.q_norm;
+    pa.k_norm = L.k_norm;
+    pa.rope = s->rope;
+    pa.qout = s->q;
+    pa.k_cache = kc;
+    pa.v_cache_t = vt;
+    pa.v_stride = v_stride;
+    pa.rope_pos0 = rope_pos0;
+    pa.kv_row0 = kv_row0;
+    pa.H = (int)H;
+    pa.Hkv = (int)Hkv;
+    pa.hd = (int)hd;
+    pa.n_rot = hp.n_rot;
+    pa.write = write ? 1 : 0;
+    pa.eps = hp.rms_eps;
+    pk.g = g;
+    pk.gate_out = s->qg;
+    qk_prep_kept_kernel<<<dim3((unsigned)T, (unsigned)(H + Hkv)), (unsigned)hd, 0, ctx->stream>>>(pk);
+    CPV_HIP(ctx, hipGetLastError());
+    const float kq_scale = 1.0f / sqrtf((float)hd);
+    if ((st = cpv_attn_launch(ctx, s->q, kc, vt, v_stride, attn_past, nullptr, T, (int)H, (int)Hkv, (int)hd, kq_scale,
+                              s->att)))
+        return st;
+    if (s->tap) {
+        const int64_t n = (int64_t)T * H * hd;
+        if (s->tap_off + n <= s->tap_cap)
+            CPV_HIP(ctx, hipMemcpyAsync(s->tap + s->tap_off, s->att, (size_t)n * 4, hipMemcpyDeviceToDevice, ctx->stream));
+        s->tap_off += n;
+    }
+    // attention output times sigmoid(gate), the wo input
+    RowArgs r2{};
+    r2.src = SRC_GATE;
+    r2.att = s->att;
+    r2.gate = s->qg;
+    r2.n = (int)(H * hd);
+    r2.quant = 1;
+    cpv_act_layout(L.wo->type, T, H * hd, next_act(s), &r2.act);
+    if ((st = row_launch(ctx, r2, T))) return st;
+    if ((st = cpv_qgemm_keep(ctx, L.wo, &r2.act, &g))) return st;
+    // residual add, FFN norm, the gate|up input
+    RowArgs r3{};
+    r3.src = SRC_ADD;
+    r3.x = x;
+    r3.xs = E;
+    r3.g = g;
+    r3.n = (int)E;
+    r3.w = L.post_norm;
+    r3.norm = 1;
+    r3.eps = hp.rms_eps;
+    r3.quant = 1;
+    cpv_act_layout(L.gate_up->type, T, E, next_act(s), &r3.act);
+    if ((st = row_launch(ctx, r3, T))) return st;
+    if ((st = cpv_qgemm_keep(ctx, L.gate_up, &r3.act, &g))) return st;
+    // SwiGLU, the down input
+    RowArgs r4{};
+    r4.src = SRC_SWIGLU;
+    r4.g = g;
+    r4.n = (int)F;
+    r4.quant = 1;
+    cpv_act_layout(L.down->type, T, F, next_act(s), &r4.act);
+    if ((st = row_launch(ctx, r4, T))) return st;
+    return cpv_qgemm_keep(ctx, L.down, &r4.act, out);
+}
+
 cpv_status project(cpv_session* s, const cpv_weight* w, const float* x, int T, float* y)
 {
     cpv_act act;
-    cpv_status st = cpv_quant_act(s->model->ctx, w->type, x, T, w->k, s->actbuf, &act);
+    cpv_status st = cpv_quant_act(s->model->ctx, w->type, x, T, w->k, next_act(s), &act);
     if (st != CPV_OK) return st;
     return cpv_qgemm_act(s->model->ctx, w, &act, y);
+}
+
+// x (+ a kept result) -> RMS norm with w -> y (f32) and the input of head w_head,
+// whose logits go to logits
+cpv_status norm_head(cpv_session* s, float* x, int T, const cpv_gout* pend, const float* w, float* y,
+                     const cpv_weight* w_head, float* logits)
+{
+    cpv_model* m = s->model;
+    const cpv_hparams& hp = m->hp;
+    if (hp.n_embd > (int64_t)RQ * RB) {     // rows too long for row_kernel (never with a kept result)
+        cpv_status st = rmsnorm(m->ctx, x, hp.n_embd, w, y, hp.n_embd, T, (int)hp.n_embd, hp.rms_eps);
+        return st != CPV_OK ? st : project(s, w_head, y, T, logits);
+    }
+    RowArgs r{};
+    r.src = pend ? SRC_ADD : SRC_X;
+    r.x = x;
+    r.xs = hp.n_embd;
+    if (pend) r.g = *pend;
+    r.n = hp.n_embd;
+    r.w = w;
+    r.norm = 1;
+    r.eps = hp.rms_eps;
+    r.y = y;
+    r.ys = hp.n_embd;
+    r.quant = 1;
+    cpv_act_layout(w_head->type, T, hp.n_embd, next_act(s), &r.act);
+    cpv_status st = row_launch(m->ctx, r, T);
+    if (st != CPV_OK) return st;
+    return cpv_qgemm_act(m->ctx, w_head, &r.act, logits);
 }
 
 }  // namespace
@@ -725,9 +1307,14 @@ extern "C" cpv_status cpv_prefill(cpv_session* s, const int32_t* tokens_dev, int
     s->tap_off = 0;
     CPV_HIP(ctx, hipMemcpyAsync(s->tok, tokens_dev, (size_t)t * 4, hipMemcpyDeviceToDevice, ctx->stream));
     if ((st = cpv_get_rows(ctx, m->tok_embd, s->tok, t, s->x))) return st;
-    for (int il = 0; il < m->hp.n_layer; il++)
-        if ((st = block(s, m->layers[il], s->x, t, s->n_past, s->n_past, s->n_past, s->kc[il], s->vt[il], s->v_stride, true)))
+    cpv_gout pend{}, nxt{};
+    for (int il = 0; il < m->hp.n_layer; il++) {
+        if ((st = block(s, m->layers[il], s->x, t, s->n_past, s->n_past, s->n_past, s->kc[il], s->vt[il], s->v_stride,
+                        true, pend.acc ? &pend : nullptr, SRC_ADD, &nxt)))
             return st;
+        pend = nxt;
+    }
+    if (pend.acc && (st = apply_kept(s, s->x, t, pend, SRC_ADD))) return st;
     s->n_past += t;
     return CPV_OK;
 }
@@ -749,12 +1336,16 @@ extern "C" cpv_status cpv_verify_step(cpv_session* s, const int32_t* tokens_dev,
     s->tap_off = 0;
     CPV_HIP(ctx, hipMemcpyAsync(s->tok, tokens_dev, (size_t)t * 4, hipMemcpyDeviceToDevice, ctx->stream));
     if ((st = cpv_get_rows(ctx, m->tok_embd, s->tok, t, s->x))) return st;
-    for (int il = 0; il < hp.n_layer; il++)
-        if ((st = block(s, m->layers[il], s->x, t, s->n_past, s->n_past, s->n_past, s->kc[il], s->vt[il], s->v_stride, true)))
+    cpv_gout pend{}, nxt{};
+    for (int il = 0; il < hp.n_layer; il++) {
+        if ((st = block(s, m->layers[il], s->x, t, s->n_past, s->n_past, s->n_past, s->kc[il], s->vt[il], s->v_stride,
+                        true, pend.acc ? &pend : nullptr, SRC_ADD, &nxt)))
             return st;
+        pend = nxt;
+    }
     // LM head and in-graph argmax (qwen35.rs:2788-2821)
-    if ((st = rmsnorm(ctx, s->x, E, m->output_norm, s->h, E, t, (int)E, hp.rms_eps))) return st;
-    if ((st = project(s, m->output, s->h, t, s->logits))) return st;
+    if ((st = norm_head(s, s->x, t, pend.acc ? &pend : nullptr, m->output_norm, s->h, m->output, s->logits)))
+        return st;
     if ((st = cpv_argmax_rows(ctx, s->logits, noise_dev, t, V, s->preds))) return st;
     // fused MTP draft chain (qwen35.rs:2840-2962)
     if (depth > 0) {
@@ -765,14 +1356,18 @@ extern "C" cpv_status cpv_verify_step(cpv_session* s, const int32_t* tokens_dev,
             if ((st = cpv_get_rows(ctx, m->mtp_embed, tok_src, t, s->e))) return st;
             if ((st = rmsnorm(ctx, s->e, E, m->enorm, s->cat, 2 * E, t, (int)E, hp.rms_eps))) return st;
             if ((st = rmsnorm(ctx, h_src, E, m->hnorm, s->cat + E, 2 * E, t, (int)E, hp.rms_eps))) return st;
-            if ((st = project(s, m->eh_proj, s->cat, t, s->dsa))) return st;
+            cpv_act act;
+            if ((st = cpv_quant_act(ctx, m->eh_proj->type, s->cat, t, 2 * E, next_act(s), &act))) return st;
+            cpv_gout eh;
+            if ((st = cpv_qgemm_keep(ctx, m->eh_proj, &act, &eh))) return st;
             // positions rope_base + i + 1, rows mtp_past + i; only link 0 writes (:1858-1866, :2898-2906)
             if ((st = block(s, ML, s->dsa, t, s->n_past + 1, s->mtp_past, s->mtp_past, s->kc[hp.n_layer],
-                            s->vt[hp.n_layer], s->mtp_v_stride, step == 0)))
+                            s->vt[hp.n_layer], s->mtp_v_stride, step == 0, &eh, SRC_SET, &nxt)))
                 return st;
             // h_next = rms(d, shared_head_norm or output_norm), then the draft head
-            if ((st = rmsnorm(ctx, s->dsa, E, m->mtp_head_norm, s->hn, E, t, (int)E, hp.rms_eps))) return st;
-            if ((st = project(s, m->mtp_head, s->hn, t, s->mtp_logits))) return st;
+            if ((st = norm_head(s, s->dsa, t, nxt.acc ? &nxt : nullptr, m->mtp_head_norm, s->hn, m->mtp_head,
+                                s->mtp_logits)))
+                return st;
             int32_t* ids = s->chain + (size_t)step * t;
             if ((st = cpv_argmax_rows(ctx, s->mtp_logits, nullptr, t, V, ids))) return st;
             peak_kernel<<<(unsigned)t, 1024, 0, ctx->stream>>>(s->mtp_logits, V, s->conf + (size_t)step * t);

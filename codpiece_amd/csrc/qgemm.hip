@@ -121,7 +121,7 @@ struct GemmArgs {
     const int8_t* qa;      // [Mtot][U*256] activation codes
     const float* da;       // [Mtot][U*DA]
     const int32_t* bs;     // [Mtot][U*BS]
-    double* gsum;          // [16][n_pad] accumulator, zero between launches
+    double* gsum;          // [rows][n_pad] accumulator (absolute activation rows), zero between uses
     int64_t n_pad;
     int64_t items;         // tiles * U (tile-major)
     int U, M, m0, win, chunk;   // chunk: consecutive items per wave
@@ -384,7 +384,7 @@ __global__ __launch_bounds__(64 * GEMM_WAVES) void qgemm_kernel(GemmArgs a)
 #pragma unroll
         for (int m = 0; m < MC; m++)
             if (m < M) {
-                unsafeAtomicAdd(&a.gsum[(int64_t)m * a.n_pad + tile * 64 + lane], S[m]);
+                unsafeAtomicAdd(&a.gsum[(int64_t)(a.m0 + m) * a.n_pad + tile * 64 + lane], S[m]);
                 S[m] = 0.0;
             }
     };
@@ -420,7 +420,7 @@ __global__ __launch_bounds__(256) void qgemm_finalize_kernel(double* __restrict_
     if (mx > 0.0f) frexpf(mx, &ea);
     const int64_t n = (int64_t)blockIdx.x * 256 + tid;
     if (n >= N) return;
-    double* g = gsum + (int64_t)m * n_pad + n;
+    double* g = gsum + (int64_t)(m0 + m) * n_pad + n;
     const double tot = *g;
     *g = 0.0;
     const int e = ew[n];
@@ -434,8 +434,9 @@ cpv_status launch_mc(cpv_ctx* ctx, const GemmArgs& a, float* y, int64_t N, int64
     const unsigned grid = (unsigned)ctx->cu_count;
     auto go = [=]() {
         qgemm_kernel<TYPE, MC><<<grid, 64 * GEMM_WAVES, lds, ctx->stream>>>(a);
-        qgemm_finalize_kernel<<<dim3((unsigned)((N + 255) / 256), (unsigned)a.M), 256, 0, ctx->stream>>>(
-            a.gsum, a.n_pad, a.ew, a.da, a.U * Fmt<TYPE>::DA, a.m0, a.win, y, N);
+        if (y)   // else the sums stay in the accumulator for a fused consumer
+            qgemm_finalize_kernel<<<dim3((unsigned)((N + 255) / 256), (unsigned)a.M), 256, 0, ctx->stream>>>(
+                a.gsum, a.n_pad, a.ew, a.da, a.U * Fmt<TYPE>::DA, a.m0, a.win, y, N);
     };
     const int ev = cpv_prof_mark(ctx);
     go();
@@ -465,10 +466,11 @@ size_t lds_of(int M, int U) { return gemm_lds<TYPE>(M, U); }
 
 static int isum_bits(int type) { return type == CPV_Q8_0 ? 20 : type == CPV_Q4_K ? 25 : 28; }
 
-// the cross-group accumulator: zeroed once when (re)allocated, left zero by every finalize
-static cpv_status gemm_accumulator(cpv_ctx* ctx, int64_t n_pad, double** gsum)
+// the split-K accumulator [rows][n_pad]: zeroed once when (re)allocated, left
+// zero by every finalize and by every fused consumer of a kept result
+static cpv_status gemm_accumulator(cpv_ctx* ctx, int64_t rows, int64_t n_pad, double** gsum)
 {
-    const size_t need = (size_t)16 * n_pad * sizeof(double);
+    const size_t need = (size_t)rows * n_pad * sizeof(double);
     if (need > ctx->gsum_bytes) {
         CPV_HIP(ctx, hipStreamSynchronize(ctx->stream));
         if (ctx->gsum) (void)hipFree(ctx->gsum);
@@ -504,6 +506,22 @@ size_t cpv_act_bytes(int type, int64_t k, int64_t m)
     const size_t da_b = ((size_t)m * U * (kq ? 1 : 8) * 4 + 255) & ~(size_t)255;
     const size_t bs_b = kq ? (size_t)m * U * (8 + 16) * 4 : 0;
     return qa_b + da_b + bs_b;
+}
+
+void cpv_act_layout(int type, int64_t m, int64_t k, void* buf, cpv_act* out)
+{
+    const int U = act_units(k);
+    const bool kq = type != CPV_Q8_0;
+    const size_t qa_b = ((size_t)m * U * 256 + 255) & ~(size_t)255;
+    const size_t da_b = ((size_t)m * U * (kq ? 1 : 8) * 4 + 255) & ~(size_t)255;
+    out->qa = (int8_t*)buf;
+    out->da = (float*)((uint8_t*)buf + qa_b);
+    out->bs32 = (int32_t*)((uint8_t*)buf + qa_b + da_b);
+    out->bs16 = out->bs32 + (size_t)m * U * 8;
+    out->m = m;
+    out->k = k;
+    out->U = U;
+    out->kq = kq;
 }
 
 cpv_status cpv_quant_act(cpv_ctx* ctx, int type, const float* x, int64_t m, int64_t k, void* buf, cpv_act* out)
@@ -554,7 +572,7 @@ cpv_status cpv_qgemm_act(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, 
         const int64_t waves = (int64_t)ctx->cu_count * GEMM_WAVES;
         a.chunk = (int)((a.items + waves - 1) / waves);
     }
-    cpv_status st = gemm_accumulator(ctx, w->n_pad, &a.gsum);
+    cpv_status st = gemm_accumulator(ctx, m, w->n_pad, &a.gsum);
     if (st != CPV_OK) return st;
     const double wb = (double)w->n * (double)(w->k / cpv_type_block(w->type)) * (double)cpv_type_size(w->type);
     auto lds = [&](int M) {
@@ -575,6 +593,20 @@ cpv_status cpv_qgemm_act(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, 
         if (s2 != CPV_OK) return s2;
         m0 += M;
     }
+    return CPV_OK;
+}
+
+cpv_status cpv_qgemm_keep(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, cpv_gout* out)
+{
+    cpv_status st = cpv_qgemm_act(ctx, w, act, nullptr);
+    if (st != CPV_OK) return st;
+    out->acc = ctx->gsum;
+    out->n_pad = w->n_pad;
+    out->n = w->n;
+    out->ew = w->ew;
+    out->da = act->da;
+    out->nda = act->U * (act->kq ? 1 : 8);
+    out->win = cpv_qgemm_window(w->type, w->k);
     return CPV_OK;
 }
 

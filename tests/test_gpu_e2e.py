@@ -180,3 +180,48 @@ def test_lockstep_mtp_window_restart(models):
     assert ps.pos == (25, 0)
     g.free()
     o.free()
+
+
+K_MODEL = dict(mf.TINY, n_layer=2, n_vocab=4096)
+
+
+@pytest.fixture(scope="module")
+def kmodels():
+    # the 27B-class mix at small size: Q4_K linears, Q6_K embedding and head
+    from codpiece_amd.model import Model, make_hparams
+    from codpiece_amd.runtime import Context
+    ctx = Context(0)
+    tensors = mf.make_tensors(K_MODEL, seed=7, qtype=cpvo.Q4_K, head_type=cpvo.Q6_K)
+    gm = Model(ctx, make_hparams(**K_MODEL))
+    mf.load_into(gm, tensors)
+    gm.ready()
+    om = cpvo.Model(K_MODEL)
+    mf.load_into(om, tensors)
+    yield ctx, gm, om
+    gm.free()
+    om.free()
+    ctx.close()
+
+
+def test_q4k_model_rounds_and_stream_are_bit_exact(kmodels):
+    from codpiece_amd.model import Session, fused_generate
+    ctx, gm, om = kmodels
+    rng = np.random.default_rng(8)
+    prompt = rng.integers(0, K_MODEL["n_vocab"], size=70).tolist()
+    g, o = Session(gm, 256), cpvo.Session(om, 256)
+    g.prefill(prompt[:60])
+    o.prefill(prompt[:60])
+    a = g.step_fused_cached(prompt[60:65], 4, want_logits=True)
+    b = o.step_fused_cached(prompt[60:65], 4, want_logits=True)
+    assert np.array_equal(a.logits.cpu().numpy().view(np.uint32), b[3].view(np.uint32))
+    assert np.array_equal(a.hidden.cpu().numpy().view(np.uint32), b[4].view(np.uint32))
+    assert a.preds == b[0].tolist() and a.chain == b[1].tolist()
+    g.free()
+    o.free()
+    g, o = Session(gm, 256), cpvo.Session(om, 256)
+    toks, st = fused_generate(g, prompt, 24, 4, tail=16, bulk=32)
+    otoks, ost = o.fused_generate(prompt, 24, 4, tail=16, bulk=32)
+    assert toks == otoks
+    assert [st.accepted, st.proposed, st.rounds] == ost
+    g.free()
+    o.free()
