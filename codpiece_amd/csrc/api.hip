@@ -89,6 +89,7 @@ extern "C" void cpv_free(cpv_ctx* ctx)
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->gsum) (void)hipFree(ctx->gsum);
+    if (ctx->red) (void)hipFree(ctx->red);
     for (hipEvent_t e : ctx->prof_ev) (void)hipEventDestroy(e);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
@@ -568,44 +569,138 @@ extern "C" cpv_status cpv_get_rows(cpv_ctx* ctx, const cpv_weight* w, const int3
 
 // ---------------------------------------------------------------- argmax
 // ggml_argmax: the first index of the maximum; values that are not > -inf
-// (and NaN) never win, and a row with no winner gives 0.
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ x, const float* __restrict__ nz,
-                                                      int64_t n, int32_t* __restrict__ out)
+// (and NaN) never win, and a row with no winner gives 0.  Pass 1 reduces each
+// of 64 slices of a row to a key, (order-preserving bits of the value) << 32 |
+// (2^32 - 1 - index), so the integer maximum of the keys is the largest value
+// at its first index (-0 is keyed as +0, which compares equal); 0 = no winner.
+// Pass 2 reduces a row's keys.
+constexpr int AM_NB = 64;
+
+__device__ __forceinline__ unsigned long long am_key(float v, int64_t i)
 {
-    const int64_t row = blockIdx.x;
+    uint32_t b = __float_as_uint(v);
+    if (b == 0x80000000u) b = 0;
+    const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
+}
+
+__device__ __forceinline__ float am_value(unsigned long long key)
+{
+    const uint32_t ord = (uint32_t)(key >> 32);
+    return __uint_as_float((ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord);
+}
+
+__device__ unsigned long long block_max_u64(unsigned long long v, unsigned long long* s)
+{
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = __shfl_xor(v, off);
+        v = o > v ? o : v;
+    }
+    const int tid = threadIdx.x, nw = blockDim.x >> 6;
+    if ((tid & 63) == 0) s[tid >> 6] = v;
+    __syncthreads();
+    unsigned long long r = 0;
+    for (int w = 0; w < nw; w++) r = s[w] > r ? s[w] : r;
+    return r;
+}
+
+__global__ __launch_bounds__(256) void argmax_part_kernel(const float* __restrict__ x, const float* __restrict__ nz,
+                                                          int64_t n, int64_t chunk, unsigned long long* __restrict__ part)
+{
+    __shared__ unsigned long long s_k[4];
+    const int64_t row = blockIdx.y, i0 = (int64_t)blockIdx.x * chunk;
+    const int64_t i1 = i0 + chunk < n ? i0 + chunk : n;
     const float* xr = x + row * n;
     const float* nr = nz ? nz + row * n : nullptr;
-    float best = -INFINITY;
-    int idx = 0x7fffffff;
-    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+    unsigned long long best = 0;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) {
         const float v = nr ? xr[i] + nr[i] : xr[i];
-        if (v > best) { best = v; idx = (int)i; }
+        if (v > -INFINITY) {
+            const unsigned long long k = am_key(v, i);
+            best = k > best ? k : best;
+        }
     }
+    best = block_max_u64(best, s_k);
+    if (threadIdx.x == 0) part[row * AM_NB + blockIdx.x] = best;
+}
+
+__global__ __launch_bounds__(64) void argmax_fin_kernel(const unsigned long long* __restrict__ part,
+                                                        int32_t* __restrict__ out)
+{
+    const int64_t row = blockIdx.x;
+    unsigned long long v = part[row * AM_NB + threadIdx.x];
     for (int off = 32; off > 0; off >>= 1) {
-        const float ob = __shfl_xor(best, off);
-        const int oi = __shfl_xor(idx, off);
-        if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+        const unsigned long long o = __shfl_xor(v, off);
+        v = o > v ? o : v;
     }
-    __shared__ float sb[16];
-    __shared__ int si[16];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (lane == 0) { sb[wave] = best; si[wave] = idx; }
+    if (threadIdx.x == 0) out[row] = v ? (int32_t)(0xffffffffu - (uint32_t)v) : 0;
+}
+
+// softmax peak: each slice's sum of expf(x - max) in binary64 (max from the
+// argmax keys), then the row's slices added in order
+__global__ __launch_bounds__(256) void peak_part_kernel(const float* __restrict__ x, int64_t n, int64_t chunk,
+                                                        const unsigned long long* __restrict__ part,
+                                                        double* __restrict__ psum)
+{
+    __shared__ double s_d[4];
+    const int64_t row = blockIdx.y, i0 = (int64_t)blockIdx.x * chunk;
+    const int64_t i1 = i0 + chunk < n ? i0 + chunk : n;
+    unsigned long long k = part[row * AM_NB + (threadIdx.x & 63)];
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = __shfl_xor(k, off);
+        k = o > k ? o : k;
+    }
+    const float mx = k ? am_value(k) : -INFINITY;
+    const float* xr = x + row * n;
+    double sum = 0.0;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) sum += (double)cpv_expf(xr[i] - mx);
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    if ((threadIdx.x & 63) == 0) s_d[threadIdx.x >> 6] = sum;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const int nw = (blockDim.x + 63) / 64;
-        for (int w = 1; w < nw; w++)
-            if (sb[w] > best || (sb[w] == best && si[w] < idx)) { best = sb[w]; idx = si[w]; }
-        out[row] = idx == 0x7fffffff ? 0 : idx;
+    if (threadIdx.x == 0) psum[row * AM_NB + blockIdx.x] = (s_d[0] + s_d[1]) + (s_d[2] + s_d[3]);
+}
+
+__global__ void peak_fin_kernel(const double* __restrict__ psum, int64_t rows, float* __restrict__ out)
+{
+    const int64_t row = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    double tot = 0.0;
+    for (int b = 0; b < AM_NB; b++) tot += psum[row * AM_NB + b];
+    out[row] = 1.0f * (float)(1.0 / tot);
+}
+
+cpv_status cpv_argmax_peak_rows(cpv_ctx* ctx, const float* x, const float* noise, int64_t rows, int64_t n,
+                                int32_t* idx_out, float* peak_out)
+{
+    const size_t need = (size_t)rows * AM_NB * 16;
+    if (need > ctx->red_bytes) {
+        CPV_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (ctx->red) (void)hipFree(ctx->red);
+        ctx->red = nullptr;
+        ctx->red_bytes = 0;
+        const size_t bs = need > ((size_t)1 << 20) ? need : ((size_t)1 << 20);
+        CPV_HIP(ctx, hipMalloc(&ctx->red, bs));
+        ctx->red_bytes = bs;
     }
+    unsigned long long* part = (unsigned long long*)ctx->red;
+    double* psum = (double*)(part + rows * AM_NB);
+    const int64_t chunk = (n + AM_NB - 1) / AM_NB;
+    const dim3 grid(AM_NB, (unsigned)rows);
+    argmax_part_kernel<<<grid, 256, 0, ctx->stream>>>(x, noise, n, chunk, part);
+    argmax_fin_kernel<<<(unsigned)rows, 64, 0, ctx->stream>>>(part, idx_out);
+    if (peak_out) {
+        peak_part_kernel<<<grid, 256, 0, ctx->stream>>>(x, n, chunk, part, psum);
+        peak_fin_kernel<<<(unsigned)((rows + 63) / 64), 64, 0, ctx->stream>>>(psum, rows, peak_out);
+    }
+    CPV_HIP(ctx, hipGetLastError());
+    return CPV_OK;
 }
 
 extern "C" cpv_status cpv_argmax_rows(cpv_ctx* ctx, const float* x_dev, const float* noise_dev, int64_t rows,
                                       int64_t n, int32_t* out_dev)
 {
-    if (!ctx || !x_dev || !out_dev || rows < 0 || n <= 0 || n > 0x7fffffff)
+    if (!ctx || !x_dev || !out_dev || rows < 0 || n <= 0 || n > 0x7fffffff || rows > 65535)
         return cpv_fail(ctx, CPV_EINVAL, "argmax: bad arguments");
     if (rows == 0) return CPV_OK;
-    argmax_kernel<<<(unsigned)rows, 1024, 0, ctx->stream>>>(x_dev, noise_dev, n, out_dev);
-    CPV_HIP(ctx, hipGetLastError());
-    return CPV_OK;
+    return cpv_argmax_peak_rows(ctx, x_dev, noise_dev, rows, n, out_dev, nullptr);
 }

@@ -24,6 +24,9 @@ struct cpv_ctx {
     // finalize, and each fused consumer of a kept result, leaves it zero)
     double* gsum = nullptr;
     size_t gsum_bytes = 0;
+    // partial results of the row reductions (argmax / softmax peak), grown on demand
+    void* red = nullptr;
+    size_t red_bytes = 0;
     // kernel timing (cpv_profile_start / _stop): event pairs around launches,
     // and each launch kept for cpv_profile_replay
     struct prof_rec { int cls, ev0, ev1; double bytes; };
@@ -195,6 +198,12 @@ __host__ __device__ __forceinline__ float cpv_gout_value(double S, int ew, int e
 // rows of several weights stacked into a new weight (same type and k, every
 // part but the last in whole 64-row tiles)
 cpv_status cpv_weight_concat(cpv_ctx* ctx, cpv_weight* const* parts, int np, cpv_weight** out);
+
+// Row argmax (first maximum, as cpv_argmax_rows) and, when peak_out is not
+// null, the softmax peak expf(0) * (float)(1 / sum_i expf(x_i - max)) of each
+// row (the sum in binary64), in two passes over 64 slices per row.
+cpv_status cpv_argmax_peak_rows(cpv_ctx* ctx, const float* x, const float* noise, int64_t rows, int64_t n,
+                                int32_t* idx_out, float* peak_out);
 
 // internal launchers
 cpv_status cpv_repack_launch(cpv_ctx* ctx, cpv_weight* w, const void* aos_dev);

@@ -221,33 +221,6 @@ __global__ void swiglu_kernel(const float* __restrict__ g, const float* __restri
     }
 }
 
-// ggml_soft_max peak at the argmax: expf(0) * (float)(1 / sum_i expf(x_i - max)),
-// the sum taken in double as ggml_vec_soft_max_f32 does
-__global__ __launch_bounds__(1024) void peak_kernel(const float* __restrict__ x, int64_t n, float* __restrict__ out)
-{
-    const float* xr = x + (int64_t)blockIdx.x * n;
-    __shared__ float s_m[16];
-    __shared__ double s_d[16];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-    float mx = -INFINITY;
-    for (int64_t i = tid; i < n; i += blockDim.x) mx = fmaxf(mx, xr[i]);
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if (lane == 0) s_m[wave] = mx;
-    __syncthreads();
-    mx = s_m[0];
-    for (int i = 1; i < nw; i++) mx = fmaxf(mx, s_m[i]);
-    double sum = 0.0;
-    for (int64_t i = tid; i < n; i += blockDim.x) sum += (double)cpv_expf(xr[i] - mx);
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-    if (lane == 0) s_d[wave] = sum;
-    __syncthreads();
-    if (tid == 0) {
-        double tot = 0.0;
-        for (int i = 0; i < nw; i++) tot += s_d[i];
-        out[blockIdx.x] = 1.0f * (float)(1.0 / tot);
-    }
-}
-
 // ---------------------------------------------------------------- fused row kernels
 // One 1024-thread block per activation row.  Wave w holds the row's 256-element
 // units u = w, w + 16, ...; lane l holds elements u*256 + l + 64k (k < 4) of
@@ -1369,9 +1342,8 @@ extern "C" cpv_status cpv_verify_step(cpv_session* s, const int32_t* tokens_dev,
                                 s->mtp_logits)))
                 return st;
             int32_t* ids = s->chain + (size_t)step * t;
-            if ((st = cpv_argmax_rows(ctx, s->mtp_logits, nullptr, t, V, ids))) return st;
-            peak_kernel<<<(unsigned)t, 1024, 0, ctx->stream>>>(s->mtp_logits, V, s->conf + (size_t)step * t);
-            CPV_HIP(ctx, hipGetLastError());
+            if ((st = cpv_argmax_peak_rows(ctx, s->mtp_logits, nullptr, t, V, ids, s->conf + (size_t)step * t)))
+                return st;
             // the next link feeds on this link's prediction and hidden
             CPV_HIP(ctx, hipMemcpyAsync(s->hsrc, s->hn, (size_t)t * E * 4, hipMemcpyDeviceToDevice, ctx->stream));
             h_src = s->hsrc;
