@@ -91,16 +91,18 @@ __host__ __device__ __forceinline__ float cpv_h2f(uint16_t h)
 }
 __host__ __device__ __forceinline__ uint16_t cpv_f2h(float f)
 {
+    // every case is computed and selected (no branches: the conversion runs
+    // per element in divergent-free inner loops)
     const uint32_t x = __builtin_bit_cast(uint32_t, f);
     const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
-    if (ax >= 0x7f800000u) return (uint16_t)(sign | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u));   // NaN, inf
-    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);           // |f| >= 65520 rounds to inf
-    if (ax < 0x38800000u) {                                               // below 2^-14: subnormal or zero
-        const float m = rintf(__builtin_bit_cast(float, ax) * 16777216.0f);   // exact scaling by 2^24, RNE
-        return (uint16_t)(sign | (uint32_t)m);
-    }
-    const uint32_t r = ax + 0x0fffu + ((ax >> 13) & 1u);                  // round the 13 dropped bits, ties to even
-    return (uint16_t)(sign | ((r - 0x38000000u) >> 13));
+    // below 2^-14: subnormal or zero, exact scaling by 2^24 then RNE
+    const uint32_t sub = (uint32_t)rintf(__builtin_bit_cast(float, ax < 0x38800000u ? ax : 0u) * 16777216.0f);
+    // normal: round the 13 dropped bits, ties to even
+    const uint32_t nrm = ((ax + 0x0fffu + ((ax >> 13) & 1u)) - 0x38000000u) >> 13;
+    uint32_t r = ax < 0x38800000u ? sub : nrm;
+    r = ax >= 0x477ff000u ? 0x7c00u : r;                // |f| >= 65520 (and inf) rounds to inf
+    r = ax > 0x7f800000u ? 0x7e00u : r;                 // NaN
+    return (uint16_t)(sign | r);
 }
 
 // expf evaluated as glibc (>= 2.27) evaluates it, which is the libm expf the
