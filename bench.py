@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--cpu-baseline", type=int, default=1, help="0 skips the oracle timing")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU sample budget (seconds)")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--sampler", type=int, default=1, help="0 skips the acceptance-sampler microbench")
+    ap.add_argument("--sampler-only", action="store_true", help="run only the acceptance-sampler microbench")
     ap.add_argument("--calibrate-copy", type=int, default=0,
                     help="first copy 1 GiB on the device 3 times (a known-size kernel for HBM counters)")
     return ap.parse_args()
@@ -211,6 +213,54 @@ def cpu_baseline(hp, layers, budget_s, tokens_per_round, depth, seed):
     }
 
 
+# ---------------------------------------------------------------- sampler
+def sampler_bench(torch, ctx, seed, reps=20):
+    """The acceptance sampler at its headline shapes: target logits f32
+    [B][k+1 = 5][151936] ~ N(0, 3) plus a +8 spike at a random id per row,
+    draft logits = target + N(0, 1) over the k = 4 draft rows, drafts drawn
+    from the draft distribution (T = 0.7, top-p 0.95); per call, rejection
+    sampling with the draft distribution (the general rule), with one-hot
+    drafts (the reference rule) and greedy argmax match, on Philox uniforms.
+    Algorithmic bytes per call: the logit rows read once (target, plus the
+    draft rows where used)."""
+    from codpiece_amd.runtime import SamplerParams
+    V, k = 151936, 4
+    g = torch.Generator(device=ctx.torch_device).manual_seed(seed + 7)
+    p = SamplerParams(temp=0.7, top_p=0.95)
+    out = {}
+    for B in (1, 4, 16):
+        pl = torch.randn(B, k + 1, V, device=ctx.torch_device, generator=g) * 3.0
+        spike = torch.randint(0, V, (B, k + 1), device=ctx.torch_device, generator=g)
+        pl.scatter_add_(2, spike.unsqueeze(2), torch.full((B, k + 1, 1), 8.0, device=ctx.torch_device))
+        ql = (pl[:, :k] + torch.randn(B, k, V, device=ctx.torch_device, generator=g)).contiguous()
+        ids, probs, n = ctx.distribution(ql.view(B * k, V), p)
+        u = torch.rand(B * k, device=ctx.torch_device, generator=g)
+        cum = torch.cumsum(probs, dim=1)
+        pick = torch.searchsorted(cum, (u * cum.gather(1, (n - 1).long().unsqueeze(1)).squeeze(1)).unsqueeze(1))
+        pick = torch.minimum(pick.squeeze(1), (n - 1).long())
+        drafts = ids.gather(1, pick.unsqueeze(1)).view(B, k).to(torch.int32)
+        res = {}
+        for name, mode, q, bytes_ in (("reject_draft_dist", 1, ql, 4.0 * V * (B * (k + 1) + B * k)),
+                                      ("reject_one_hot", 1, None, 4.0 * V * B * (k + 1)),
+                                      ("greedy", 0, None, 4.0 * V * B * (k + 1))):
+            prm = p if mode else SamplerParams()
+            for _ in range(3):
+                ctx.spec_accept(pl, drafts, prm, mode, q_logits=q, philox_seed=seed)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(reps):
+                ctx.spec_accept(pl, drafts, prm, mode, q_logits=q, philox_seed=seed + i)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / reps * 1e3
+            res[name] = {"us_per_call": round(us, 1), "GB_s": round(bytes_ / (us * 1e-6) / 1e9, 1),
+                         "MB_per_call": round(bytes_ / 1e6, 2)}
+        out[f"B={B}"] = res
+        print(f"[bench] sampler B={B}: " + ", ".join(f"{k2} {v['us_per_call']} us" for k2, v in res.items()),
+              file=sys.stderr, flush=True)
+    return out
+
+
 # ---------------------------------------------------------------- main
 def main():
     args = parse()
@@ -226,6 +276,10 @@ def main():
     hp = dict(HP, n_layer=args.layers)
     torch.cuda.set_device(0)
     ctx = Context(0)
+    if args.sampler_only:
+        print(json.dumps({"sampler": sampler_bench(torch, ctx, args.seed)}), flush=True)
+        ctx.close()
+        return 0
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device=ctx.torch_device)
         dst = torch.empty_like(src)
@@ -300,6 +354,8 @@ def main():
     if args.cpu_baseline:
         cpu = cpu_baseline(hp, args.layers, args.cpu_seconds, committed / args.steps, args.depth, args.seed)
 
+    sampler = sampler_bench(torch, ctx, args.seed) if args.sampler else None
+
     value = committed / wall
     line = {
         "metric": "verify-step µs + accepted tok/s, 27B-class Q4_K, draft k=4, 1 MI355X",
@@ -326,6 +382,7 @@ def main():
                                    "us_per_launch_event_bracketed": round(v[1] / v[0] * 1e3, 2)}
                                for k, v in prof.items() if v[0]},
             "profiled_rounds": args.profile_rounds,
+            "acceptance_sampler": sampler,
         },
     }
     print(json.dumps(line), flush=True)

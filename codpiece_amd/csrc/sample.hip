@@ -36,7 +36,8 @@ namespace {
 
 constexpr int SB = 1024;               // threads per sampler workgroup
 constexpr int SWV = SB / 64;           // waves per workgroup
-constexpr int FIPT = 8;                // fold: elements per thread per pass
+constexpr int FIPT = 8;                // fold: elements per thread per window
+constexpr int BU = 8;                  // strided loops: loads issued ahead of their uses
 constexpr uint32_t FTOP = 1u << 24;    // fold: ulps from 0 to the top of a binade
 constexpr uint32_t FSAT = 1u << 26;    // fold: saturation of a composed step
 constexpr int BAND = 16384;            // sorted band held in LDS as u64 keys
@@ -55,6 +56,26 @@ struct Small {
     int wi[SWV];
     int iv[8];
 };
+
+// for (i = tid; i < n; i += SB) use(i, load(i)), with BU loads in flight:
+// every load of a batch is issued (at a clamped index) before the first use
+template <class L, class U>
+__device__ __forceinline__ void strided(int n, L load, U use)
+{
+    for (int i0 = threadIdx.x; i0 < n; i0 += SB * BU) {
+        decltype(load(0)) v[BU];
+#pragma unroll
+        for (int q = 0; q < BU; q++) {
+            const int i = i0 + q * SB;
+            v[q] = load(i < n ? i : n - 1);
+        }
+#pragma unroll
+        for (int q = 0; q < BU; q++) {
+            const int i = i0 + q * SB;
+            if (i < n) use(i, v[q]);
+        }
+    }
+}
 
 // the step of m for an S of parity par (arithmetic select: a ?: on the two
 // fields lets the compiler address a register array by parity)
@@ -133,80 +154,103 @@ __device__ FoldRes block_fold(X x_at, int n, float s, float thr, int pmode, Smal
     __syncthreads();
     if (tid < 4) (&sm->slot[0][0])[tid] = ~0ull;
     __syncthreads();
-    int start = 0, it = 0;
-    while (start < n) {
-        const int eb = f_eb(s);
-        const uint32_t S0 = f_S(s);
+    int it = 0;
+    for (int start = 0; start < n; start += SB * FIPT) {
         const int base = start + tid * FIPT;
-        FMap m[FIPT];
         float xv[FIPT];
-        FMap acc = {0u, 0u};
 #pragma unroll
         for (int q = 0; q < FIPT; q++) {
             const int i = base + q;
-            xv[q] = i < n ? x_at(i) : 0.0f;
-            m[q] = fmap_of(xv[q], eb);
-            acc = fcomp(acc, m[q]);
+            xv[q] = x_at(i < n ? i : n - 1);
         }
-        FMap inc = acc;
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            FMap o;
-            o.d0 = __shfl_up(inc.d0, off, 64);
-            o.d1 = __shfl_up(inc.d1, off, 64);
-            if (lane >= off) inc = fcomp(o, inc);
-        }
-        FMap ex;
-        ex.d0 = __shfl_up(inc.d0, 1, 64);
-        ex.d1 = __shfl_up(inc.d1, 1, 64);
-        if (lane == 0) ex = {0u, 0u};
-        if (lane == 63) sm->wtot[wave] = inc;
-        unsigned long long* slot = sm->slot[it & 1];
-        __syncthreads();
-        if (tid < 2) sm->slot[(it + 1) & 1][tid] = ~0ull;
-        FMap wp = {0u, 0u};
-        for (int w = 0; w < wave; w++) wp = fcomp(wp, sm->wtot[w]);
-        FMap tot = wp;
-        for (int w = wave; w < SWV; w++) tot = fcomp(tot, sm->wtot[w]);
-        const FMap pre = fcomp(wp, ex);
-        uint32_t S = S0 + fsel(pre, S0);
-        bool live = true;
+        for (int q = 0; q < FIPT; q++)
+            if (base + q >= n) xv[q] = 0.0f;
+        // passes over the window held in registers; a pass that leaves the
+        // binade is redone from the exit on, in the new binade, with the
+        // elements up to the exit masked out
+        int done = start - 1;
+        for (;;) {
+            const int eb = f_eb(s);
+            const uint32_t S0 = f_S(s);
+            FMap m[FIPT];
+            FMap acc = {0u, 0u};
 #pragma unroll
-        for (int q = 0; q < FIPT; q++) {
-            const int i = base + q;
-            if (live && i < n && S < FTOP) {
-                const uint32_t Sp = S;
-                S = Sp + fsel(m[q], Sp);
-                if (S >= FTOP) {
-                    // leaves the binade: this add is done in f32 by the hardware
-                    const float sn = f_make(eb, Sp) + xv[q];
-                    atomicMin(&slot[0], ((unsigned long long)i << 32) | __float_as_uint(sn));
-                    live = false;
-                } else if (pmode != F_NONE) {
-                    const float sv = f_make(eb, S);
-                    if (fpred(pmode, sv, thr)) {
-                        atomicMin(&slot[1], ((unsigned long long)i << 32) | __float_as_uint(sv));
+            for (int q = 0; q < FIPT; q++) {
+                m[q] = base + q > done ? fmap_of(xv[q], eb) : FMap{0u, 0u};
+                acc = fcomp(acc, m[q]);
+            }
+            FMap inc = acc;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                FMap o;
+                o.d0 = __shfl_up(inc.d0, off, 64);
+                o.d1 = __shfl_up(inc.d1, off, 64);
+                if (lane >= off) inc = fcomp(o, inc);
+            }
+            FMap ex;
+            ex.d0 = __shfl_up(inc.d0, 1, 64);
+            ex.d1 = __shfl_up(inc.d1, 1, 64);
+            if (lane == 0) ex = {0u, 0u};
+            if (lane == 63) sm->wtot[wave] = inc;
+            unsigned long long* slot = sm->slot[it & 1];
+            __syncthreads();
+            if (tid < 2) sm->slot[(it + 1) & 1][tid] = ~0ull;
+            // the waves' totals, scanned by every wave on its first SWV lanes
+            FMap wi = lane < SWV ? sm->wtot[lane] : FMap{0u, 0u};
+#pragma unroll
+            for (int off = 1; off < SWV; off <<= 1) {
+                FMap o;
+                o.d0 = __shfl_up(wi.d0, off, 64);
+                o.d1 = __shfl_up(wi.d1, off, 64);
+                if (lane >= off && lane < SWV) wi = fcomp(o, wi);
+            }
+            FMap wp = {0u, 0u}, tot;
+            const int src = wave > 0 ? wave - 1 : 0;
+            wp.d0 = __shfl(wi.d0, src, 64);
+            wp.d1 = __shfl(wi.d1, src, 64);
+            if (wave == 0) wp = {0u, 0u};
+            tot.d0 = __shfl(wi.d0, SWV - 1, 64);
+            tot.d1 = __shfl(wi.d1, SWV - 1, 64);
+            const FMap pre = fcomp(wp, ex);
+            uint32_t S = S0 + fsel(pre, S0);
+            bool live = true;
+#pragma unroll
+            for (int q = 0; q < FIPT; q++) {
+                const int i = base + q;
+                if (live && i > done && i < n && S < FTOP) {
+                    const uint32_t Sp = S;
+                    S = Sp + fsel(m[q], Sp);
+                    if (S >= FTOP) {
+                        // leaves the binade: this add is done in f32 by the hardware
+                        const float sn = f_make(eb, Sp) + xv[q];
+                        atomicMin(&slot[0], ((unsigned long long)i << 32) | __float_as_uint(sn));
                         live = false;
+                    } else if (pmode != F_NONE) {
+                        const float sv = f_make(eb, S);
+                        if (fpred(pmode, sv, thr)) {
+                            atomicMin(&slot[1], ((unsigned long long)i << 32) | __float_as_uint(sv));
+                            live = false;
+                        }
                     }
                 }
             }
-        }
-        __syncthreads();
-        const unsigned long long cr = slot[0], pr = slot[1];
-        // a predicate hit can only precede the first exit: later prefixes
-        // are saturated and never tested
-        if (pr != ~0ull) return {__uint_as_float((uint32_t)pr), (int)(pr >> 32)};
-        if (cr != ~0ull) {
+            __syncthreads();
+            const unsigned long long cr = slot[0], pr = slot[1];
+            it++;
+            // a predicate hit can only precede the first exit: later prefixes
+            // are saturated and never tested
+            if (pr != ~0ull) return {__uint_as_float((uint32_t)pr), (int)(pr >> 32)};
+            if (cr == ~0ull) {
+                s = f_make(eb, S0 + fsel(tot, S0));
+                break;
+            }
             const int ci = (int)(cr >> 32);
             const float sn = __uint_as_float((uint32_t)cr);
             if (pmode != F_NONE && fpred(pmode, sn, thr)) return {sn, ci};
             s = sn;
-            start = ci + 1;
-        } else {
-            s = f_make(eb, S0 + fsel(tot, S0));
-            start += SB * FIPT;
+            done = ci;
         }
-        it++;
     }
     return {s, -1};
 }
@@ -241,7 +285,7 @@ __device__ float block_max(X x_at, int n, Small* sm)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float m = -INFINITY;
-    for (int i = tid; i < n; i += SB) m = fmaxf(m, x_at(i));
+    strided(n, x_at, [&](int, float v) { m = fmaxf(m, v); });
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
     __syncthreads();
     if (lane == 0) sm->wf[wave] = m;
@@ -259,10 +303,9 @@ __device__ int block_argmax(X x_at, int n, int dflt, Small* sm)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float best = -INFINITY;
     int idx = 0x7fffffff;
-    for (int i = tid; i < n; i += SB) {
-        const float v = x_at(i);
+    strided(n, x_at, [&](int i, float v) {
         if (v > best) { best = v; idx = i; }
-    }
+    });
     for (int off = 32; off > 0; off >>= 1) {
         const float ob = __shfl_xor(best, off, 64);
         const int oi = __shfl_xor(idx, off, 64);
@@ -369,11 +412,11 @@ __device__ int emit_band(const float* lg, int V, bool have_last, unsigned long l
         __syncthreads();
         for (int b = tid; b < nb; b += SB) hist[b] = 0;
         __syncthreads();
-        for (int i = tid; i < V; i += SB) {
-            const unsigned long long key = cand_key(lg[i], i);
-            if ((have_last && key <= last) || (key & fixed) != prefix) continue;
+        strided(V, [&](int i) { return lg[i]; }, [&](int i, float l) {
+            const unsigned long long key = cand_key(l, i);
+            if ((have_last && key <= last) || (key & fixed) != prefix) return;
             atomicAdd(&hist[(key >> sh) & (unsigned long long)(nb - 1)], 1u);
-        }
+        });
         __syncthreads();
         uint32_t c[4], s = 0;
 #pragma unroll
@@ -417,11 +460,11 @@ __device__ int emit_band(const float* lg, int V, bool have_last, unsigned long l
     __syncthreads();
     if (tid == 0) sm->iv[3] = 0;
     __syncthreads();
-    for (int i = tid; i < V; i += SB) {
-        const unsigned long long key = cand_key(lg[i], i);
-        if ((have_last && key <= last) || key > hi) continue;
+    strided(V, [&](int i) { return lg[i]; }, [&](int i, float l) {
+        const unsigned long long key = cand_key(l, i);
+        if ((have_last && key <= last) || key > hi) return;
         keys[atomicAdd(&sm->iv[3], 1)] = key;
-    }
+    });
     __syncthreads();
     const int cnt = sm->iv[3];
     int P = 64;
@@ -489,7 +532,7 @@ __device__ const float* apply_penalties(const float* logits, float* pen, int V, 
         const int at = (int)L + d;
         if (at >= start) win[at - start] = drafts[d];
     }
-    for (int i = tid; i < V; i += SB) pen[i] = logits[i];
+    strided(V, [&](int i) { return logits[i]; }, [&](int i, float l) { pen[i] = l; });
     __syncthreads();
     for (int a = tid; a < wn; a += SB) {
         const int tok = win[a];
@@ -583,15 +626,18 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
             // the smallest of 1024, 8192, ... (capped at V) whose sorted
             // prefix covers top_p, and the cut inside it (:343-358), both
             // read off one fold of the probabilities in candidate order
-            const float sum1 = block_fold([&](int i) { return cpv_expf(lg[i] - mx); }, V, 0.0f, 0.0f, F_NONE, sm).sum;
+            // e_i = expf(l_i - max) once, by index, in the probabilities' row (the
+            // final probabilities overwrite it at the end)
+            strided(V, [&](int i) { return lg[i]; }, [&](int i, float l) { pr[i] = cpv_expf(l - mx); });
+            __syncthreads();
+            const float sum1 = block_fold([&](int i) { return pr[i]; }, V, 0.0f, 0.0f, F_NONE, sm).sum;
             float s = 0.0f;
             int ifirst = -1;
             while (emitted < V) {
                 const int cnt = emit_band(lg, V, emitted > 0, &last, BAND, emitted, sid, sl, keys, sm);
                 if (cnt <= 0) break;
-                const float* band = sl + emitted;
-                const FoldRes r = block_fold([&](int i) { return cpv_expf(band[i] - mx) / sum1; }, cnt, s, P.top_p,
-                                             F_GE, sm);
+                const int32_t* band = sid + emitted;
+                const FoldRes r = block_fold([&](int i) { return pr[band[i]] / sum1; }, cnt, s, P.top_p, F_GE, sm);
                 if (r.idx >= 0) ifirst = emitted + r.idx;
                 emitted += cnt;
                 if (r.idx >= 0) break;
@@ -615,8 +661,10 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
         n = M;
         if (!top_p && P.top_p < 1.0f && n > 1) {           // :343-358 after a re-softmax over the survivors
             const float l0 = sl[0];
-            const float sA = block_fold([&](int i) { return cpv_expf(sl[i] - l0); }, n, 0.0f, 0.0f, F_NONE, sm).sum;
-            const FoldRes r = block_fold([&](int i) { return cpv_expf(sl[i] - l0) / sA; }, n, 0.0f, P.top_p, F_GE, sm);
+            strided(n, [&](int i) { return sl[i]; }, [&](int i, float l) { pr[i] = cpv_expf(l - l0); });
+            __syncthreads();
+            const float sA = block_fold([&](int i) { return pr[i]; }, n, 0.0f, 0.0f, F_NONE, sm).sum;
+            const FoldRes r = block_fold([&](int i) { return pr[i] / sA; }, n, 0.0f, P.top_p, F_GE, sm);
             if (r.idx >= 0) {
                 const int keep = r.idx + 1 > P.min_keep ? r.idx + 1 : P.min_keep;
                 if (keep <= n) n = keep;
@@ -641,8 +689,12 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
     // :371-374 temperature, then softmax over the survivors (:461-471)
     const float T = P.temp;
     const float mx2 = (top_k || min_p || top_p ? sl[0] : mx) / T;
-    const float s2 = block_fold([&](int i) { return cpv_expf(sl[i] / T - mx2); }, n, 0.0f, 0.0f, F_NONE, sm).sum;
-    for (int i = tid; i < n; i += SB) pr[i] = cpv_expf(sl[i] / T - mx2) / s2;
+    __syncthreads();
+    strided(n, [&](int i) { return sl[i]; }, [&](int i, float l) { pr[i] = cpv_expf(l / T - mx2); });
+    __syncthreads();
+    const float s2 = block_fold([&](int i) { return pr[i]; }, n, 0.0f, 0.0f, F_NONE, sm).sum;
+    __syncthreads();
+    strided(n, [&](int i) { return pr[i]; }, [&](int i, float e) { pr[i] = e / s2; });
     if (tid == 0) a.hdr[row] = n;
 }
 
