@@ -22,13 +22,16 @@
 // 4 weight rows of its lanes (B), so each lane receives the dots of its own
 // row with 4 activation rows; a launch takes up to 8 rows (2 row groups).  The
 // per-unit scale work and the binary64 rounding then run lane-locally, with
-// no cross-lane traffic.  The grid is persistent (one workgroup per CU) and
-// the (tile, unit) items are dealt out to waves in consecutive runs, so K is
-// split wherever a run starts or ends: the partial sums are exact integers
-// below 2^53 and add in any order, through f64 atomics into an accumulator
-// that a small finalize kernel turns into y and leaves zeroed for the next
-// launch (no device-scope fence in the GEMM: on gfx950 one would write back a
-// whole L2 per workgroup).
+// no cross-lane traffic.  The grid is persistent (one workgroup per CU): the
+// (tile, unit) items are dealt out evenly to the workgroups and within each
+// to its waves in consecutive runs, so K is split wherever a run starts or
+// ends.  A workgroup stages only the activation units its items touch.  The
+// partial sums are exact integers below 2^53 and add in any order: the waves
+// add theirs into per-tile sums in LDS, and each workgroup then writes a tile
+// it covers whole and adds (f64 atomics) a tile it shares into an accumulator
+// that a small finalize kernel (or the fused consumer of a kept result) turns
+// into y and leaves zeroed for the next launch (no device-scope fence in the
+// GEMM: on gfx950 one would write back a whole L2 per workgroup).
 #include <math.h>
 
 #include "cpv_internal.h"
@@ -123,26 +126,34 @@ struct GemmArgs {
     const int32_t* bs;     // [Mtot][U*BS]
     double* gsum;          // [rows][n_pad] accumulator (absolute activation rows), zero between uses
     int64_t n_pad;
-    int64_t items;         // tiles * U (tile-major)
-    int U, M, m0, win, chunk;   // chunk: consecutive items per wave
+    int items;             // tiles * U (tile-major)
+    int U, M, m0, win;
+    int nu_max, nt_max;    // most units / tiles one workgroup's items touch
 };
 
-constexpr int GEMM_WAVES = 8;   // waves per workgroup (one workgroup per CU)
+// waves per workgroup (one workgroup per CU): 12 where the kernel fits 3
+// waves per SIMD in registers, else 8
+template <int TYPE, int MC>
+constexpr int gemm_waves() { return TYPE == CPV_Q4_K && MC <= 5 ? 12 : 8; }
 
 __device__ __forceinline__ v4i mfma4(int a, int b, v4i c)
 {
     return __builtin_amdgcn_mfma_i32_4x4x4i8(a, b, c, 0, 0, 0);
 }
 
-// LDS bytes of one workgroup: all M x U activation units, their scales and sums
+// LDS of one workgroup: its nu activation units for M rows (rows of nu*256
+// + 16 bytes: 4 rows, 4 bank groups), their scales and code sums, the
+// binary64 sums of its nt tiles, and 16 bytes that take the staging writes of
+// lanes with nothing to stage (so that the writes need no branch)
 template <int TYPE>
-__host__ __device__ inline size_t gemm_lds(int M, int U)
+__host__ __device__ inline size_t gemm_lds(int M, int nu, int nt)
 {
     using F = Fmt<TYPE>;
-    const size_t codes = (size_t)M * ((size_t)U * 256 + 16);
-    const size_t da = (size_t)M * U * F::DA * 4;
-    const size_t bs = (size_t)M * U * F::BS * 4;
-    return ((codes + 15) & ~(size_t)15) + ((da + 15) & ~(size_t)15) + bs;
+    const size_t codes = (size_t)M * ((size_t)nu * 256 + 16);
+    const size_t da = (size_t)M * nu * F::DA * 4;
+    const size_t bs = (size_t)M * nu * F::BS * 4;
+    const size_t acc = (size_t)nt * M * 64 * 8;
+    return ((codes + 15) & ~(size_t)15) + ((da + 15) & ~(size_t)15) + ((bs + 15) & ~(size_t)15) + acc + 16;
 }
 
 // One (tile, unit) item: the unit's integer dots for all MC rows and its
@@ -295,109 +306,189 @@ __device__ __forceinline__ void gemm_unit(const v4i* pcu, uint16_t d6, int er, i
 }
 
 // Persistent streaming GEMM: one workgroup of GEMM_WAVES waves per CU stages
-// every activation unit in LDS once; then each wave walks its own run of
-// `chunk` consecutive (tile, unit) items with the next item's weights in
-// flight while it computes the current one, keeps the partial sums of its
-// current tile in registers, and adds them to the accumulator (f64 atomics,
-// exact) whenever the tile changes and at the end.  No barrier after staging.
-// MC: a compile-time bound on the activation rows (rows M..MC-1 repeat row
-// M-1 and are never stored), so every loop over rows unrolls without branches.
+// the activation units of its items in LDS; then each wave walks its own run
+// of consecutive (tile, unit) items with the next item's weights in flight
+// while it computes the current one, and keeps the partial sums of its
+// current tile in registers, adding them to the tile's sums in LDS whenever
+// the tile changes and at the end.  MC: a compile-time bound on the
+// activation rows (rows M..MC-1 repeat row M-1 and are never stored), so every
+// loop over rows unrolls without branches.
 template <int TYPE, int MC>
-__global__ __launch_bounds__(64 * GEMM_WAVES) void qgemm_kernel(GemmArgs a)
+__global__ __launch_bounds__((64 * gemm_waves<TYPE, MC>())) void qgemm_kernel(GemmArgs a)
 {
     using F = Fmt<TYPE>;
+    constexpr int GEMM_WAVES = gemm_waves<TYPE, MC>();
     constexpr int RG = (MC + 3) / 4;           // 4-row groups of the MFMA
     constexpr int NT = 64 * GEMM_WAVES;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int s_ea[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int M = a.M, U = a.U;
-    const int cstride = U * 256 + 16;          // LDS bytes per activation row (+16: 4 rows, 4 bank groups)
-    uint8_t* s_codes = smem;
-    float* s_da = (float*)(smem + ((M * cstride + 15) & ~15));
-    int32_t* s_bs = (int32_t*)((uint8_t*)s_da + ((M * U * F::DA * 4 + 15) & ~15));
     const int64_t Kp = (int64_t)U * 256;
 
-    // this wave's items
-    const int64_t i0 = ((int64_t)blockIdx.x * GEMM_WAVES + wave) * a.chunk;
-    const int64_t i1 = i0 + a.chunk < a.items ? i0 + a.chunk : a.items;
+    // this workgroup's items [I0, I1), their units us, us+1, ... (mod U) and tiles t0..
+    const int I0 = (int)((int64_t)blockIdx.x * a.items / gridDim.x);
+    const int I1 = (int)((int64_t)(blockIdx.x + 1) * a.items / gridDim.x);
+    const int us = I0 % U, nu = I1 - I0 < U ? I1 - I0 : U;
+    const int t0 = I0 / U, nt = I1 > I0 ? (I1 - 1) / U - t0 + 1 : 0;
+    const int cstride = nu * 256 + 16;         // LDS bytes per activation row (+16: 4 rows, 4 bank groups)
+    uint8_t* s_codes = smem;
+    float* s_da = (float*)(smem + ((M * cstride + 15) & ~15));
+    int32_t* s_bs = (int32_t*)((uint8_t*)s_da + ((M * nu * F::DA * 4 + 15) & ~15));
+    double* s_acc = (double*)((uint8_t*)s_bs + ((M * nu * F::BS * 4 + 15) & ~15));   // [nt][M][64]
+    uint8_t* s_trash = (uint8_t*)(s_acc + nt * M * 64);
+
+    // this wave's run
+    const int n = I1 - I0;
+    const int i0 = I0 + wave * n / GEMM_WAVES, i1 = I0 + (wave + 1) * n / GEMM_WAVES;
     const uint16_t* d6base = (const uint16_t*)(a.w + (a.n_pad / 64) * (int64_t)U * 13 * 1024);
-    auto load = [&](int64_t it, v4i* pcu, uint16_t& d6, int& er) {
-        const int64_t tile = it / U;
-        const v4i* src = (const v4i*)(a.w + it * F::PIECES * 1024 + lane * 16);
+    auto load = [&](int it, v4i* pcu, uint16_t& d6, int& er) {
+        const int tile = it / U;
+        const v4i* src = (const v4i*)(a.w + (int64_t)it * F::PIECES * 1024 + lane * 16);
 #pragma unroll
         for (int p = 0; p < F::PIECES; p++) pcu[p] = src[p * 64];
-        if (TYPE == CPV_Q6_K) d6 = d6base[it * 64 + lane];
+        if (TYPE == CPV_Q6_K) d6 = d6base[(int64_t)it * 64 + lane];
         er = a.ew[tile * 64 + lane];
     };
+    // ---- staging: the first batch of activation loads goes out before any
+    // weight load, so that it is not queued behind them; the LDS writes then
+    // wait for these loads only
+    constexpr int BC = 4, BD = 2, BB = 4;      // per thread: code pieces, scales, code sums
+    const int ncode = M * nu * 16, nda = M * nu * F::DA, nbs = M * nu * F::BS;
+    auto code_src = [&](int i) {
+        const int m = i / (nu * 16), c = i - m * (nu * 16), j = c >> 4;
+        const int u = us + j < U ? us + j : us + j - U;
+        return (const v4i*)(a.qa + (int64_t)(a.m0 + m) * Kp + u * 256 + (c & 15) * 16);
+    };
+    auto code_dst = [&](int i) {
+        const int m = i / (nu * 16), c = i - m * (nu * 16);
+        return (v4i*)(s_codes + m * cstride + c * 16);
+    };
+    auto da_src = [&](int i) {
+        const int m = i / (nu * F::DA), c = i - m * (nu * F::DA), j = c / F::DA;
+        const int u = us + j < U ? us + j : us + j - U;
+        return a.da + ((int64_t)(a.m0 + m) * U + u) * F::DA + (c - j * F::DA);
+    };
+    auto bs_src = [&](int i) {
+        const int m = i / (nu * F::BS), c = i - m * (nu * F::BS), j = c / F::BS;
+        const int u = us + j < U ? us + j : us + j - U;
+        return a.bs + ((int64_t)(a.m0 + m) * U + u) * F::BS + (c - j * F::BS);
+    };
+    v4i cv[BC];
+    float dv[BD];
+    int32_t bv[BB];
+#pragma unroll
+    for (int q = 0; q < BC; q++) cv[q] = *code_src(tid + q * NT < ncode ? tid + q * NT : 0);
+#pragma unroll
+    for (int q = 0; q < BD; q++) dv[q] = *da_src(tid + q * NT < nda ? tid + q * NT : 0);
+    if constexpr (F::BS > 0)
+#pragma unroll
+        for (int q = 0; q < BB; q++) bv[q] = *bs_src(tid + q * NT < nbs ? tid + q * NT : 0);
+    // Ea(m): the exponent of the row's largest |scale|, one wave per row (first two loads per lane here)
+    const int m_ea = wave < M ? wave : 0, nrow = U * F::DA;
+    const float* dr = a.da + (int64_t)(a.m0 + m_ea) * nrow;
+    float ev0 = dr[lane < nrow ? lane : 0], ev1 = dr[lane + 64 < nrow ? lane + 64 : 0];
+
+    // then two items of weights in flight
     v4i bufA[F::PIECES], bufB[F::PIECES];
     uint16_t dA = 0, dB = 0;
     int eA = 0, eB = 0;
-    // two items in flight before the staging below
-    if (i0 < i1) load(i0, bufA, dA, eA);
-    if (i0 + 1 < i1) load(i0 + 1, bufB, dB, eB);
+    // (unconditional: a wave without items, or with one, reloads a valid item;
+    // branches here would make the compiler wait for every load at the join)
+    const int ia = i0 < i1 ? i0 : 0, ib = i0 + 1 < i1 ? i0 + 1 : ia;
+    load(ia, bufA, dA, eA);
+    load(ib, bufB, dB, eB);
 
-    // ---- stage every activation unit, its scale and code sums; Ea(m) over the row
-    for (int i = tid; i < M * U * 16; i += NT) {
-        const int m = i / (U * 16), c = i - m * (U * 16);
-        const v4i v = *(const v4i*)(a.qa + (int64_t)(a.m0 + m) * Kp + c * 16);
-        *(v4i*)(s_codes + m * cstride + c * 16) = v;
+#pragma unroll
+    for (int q = 0; q < BC; q++) {
+        const int i = tid + q * NT;
+        *(i < ncode ? code_dst(i) : (v4i*)s_trash) = cv[q];
     }
-    for (int i = tid; i < M * U * F::DA; i += NT) s_da[i] = a.da[(int64_t)a.m0 * U * F::DA + i];
-    if (F::BS)
-        for (int i = tid; i < M * U * F::BS; i += NT) s_bs[i] = a.bs[(int64_t)a.m0 * U * F::BS + i];
-    for (int m = wave; m < M; m += GEMM_WAVES) {
-        float mx = 0.0f;
-        for (int i = lane; i < U * F::DA; i += 64) mx = fmaxf(mx, fabsf(a.da[(int64_t)(a.m0 + m) * U * F::DA + i]));
+#pragma unroll
+    for (int q = 0; q < BD; q++) {
+        const int i = tid + q * NT;
+        *(i < nda ? s_da + i : (float*)s_trash) = dv[q];
+    }
+    if constexpr (F::BS > 0)
+#pragma unroll
+        for (int q = 0; q < BB; q++) {
+            const int i = tid + q * NT;
+            *(i < nbs ? s_bs + i : (int32_t*)s_trash) = bv[q];
+        }
+    for (int i = tid + BC * NT; i < ncode; i += NT) *code_dst(i) = *code_src(i);
+    for (int i = tid + BD * NT; i < nda; i += NT) s_da[i] = *da_src(i);
+    if constexpr (F::BS > 0)
+        for (int i = tid + BB * NT; i < nbs; i += NT) s_bs[i] = *bs_src(i);
+    for (int i = tid; i < nt * M * 64; i += NT) s_acc[i] = 0.0;
+    if (wave < M) {
+        float mx = fmaxf(lane < nrow ? fabsf(ev0) : 0.0f, lane + 64 < nrow ? fabsf(ev1) : 0.0f);
+        for (int i = lane + 128; i < nrow; i += 64) mx = fmaxf(mx, fabsf(dr[i]));
         for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
         if (lane == 0) {
             int e = CPV_E_EMPTY;
             if (mx > 0.0f) frexpf(mx, &e);
-            s_ea[m] = e;
+            s_ea[wave] = e;
         }
     }
     __syncthreads();
-    if (i0 >= i1) return;
 
-    // per row: the MFMA feed of this lane (row group r takes row 4r + lane%4) and 2^(win - Ea)
-    const uint8_t* arow[RG];
+    if (i0 < i1) {
+        // per row: the MFMA feed of this lane (row group r takes row 4r + lane%4) and 2^(win - Ea)
+        const uint8_t* arow[RG];
 #pragma unroll
-    for (int r = 0; r < RG; r++) {
-        const int m = 4 * r + (lane & 3);
-        arow[r] = s_codes + (m < M ? m : M - 1) * cstride;
-    }
-    int mrow[MC];
-    double sm[MC];
+        for (int r = 0; r < RG; r++) {
+            const int m = 4 * r + (lane & 3);
+            arow[r] = s_codes + (m < M ? m : M - 1) * cstride;
+        }
+        int mrow[MC];
+        double sm[MC];
 #pragma unroll
-    for (int m = 0; m < MC; m++) {
-        mrow[m] = m < M ? m : M - 1;
-        const int e = s_ea[mrow[m]];
-        sm[m] = e == CPV_E_EMPTY ? 0.0 : ldexp(1.0, a.win - e);
-    }
+        for (int m = 0; m < MC; m++) {
+            mrow[m] = m < M ? m : M - 1;
+            const int e = s_ea[mrow[m]];
+            sm[m] = e == CPV_E_EMPTY ? 0.0 : ldexp(1.0, a.win - e);
+        }
 
-    double S[MC];
+        double S[MC];
 #pragma unroll
-    for (int m = 0; m < MC; m++) S[m] = 0.0;
-    int64_t tile = i0 / U;
-    auto flush = [&]() {
-        // partial sums of this tile's units: exact, so the order of the adds does not matter
+        for (int m = 0; m < MC; m++) S[m] = 0.0;
+        int tile = i0 / U;
+        auto flush = [&]() {
+            // partial sums of this tile's units into its LDS sums: exact, in any order
+            double* acc = s_acc + ((tile - t0) * M) * 64 + lane;
 #pragma unroll
-        for (int m = 0; m < MC; m++)
-            if (m < M) {
-                unsafeAtomicAdd(&a.gsum[(int64_t)(a.m0 + m) * a.n_pad + tile * 64 + lane], S[m]);
-                S[m] = 0.0;
-            }
-    };
-    for (int64_t it = i0; it < i1; it += 2) {
-        if (it > i0 && it + 1 < i1) load(it + 1, bufB, dB, eB);
-        if (it / U != tile) { flush(); tile = it / U; }
-        gemm_unit<TYPE, MC>(bufA, dA, eA, (int)(it % U), M, U, arow, mrow, sm, s_da, s_bs, S);
-        if (it + 1 >= i1) break;
-        if (it + 2 < i1) load(it + 2, bufA, dA, eA);
-        if ((it + 1) / U != tile) { flush(); tile = (it + 1) / U; }
-        gemm_unit<TYPE, MC>(bufB, dB, eB, (int)((it + 1) % U), M, U, arow, mrow, sm, s_da, s_bs, S);
+            for (int m = 0; m < MC; m++)
+                if (m < M) {
+                    __hip_atomic_fetch_add(acc + m * 64, S[m], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    S[m] = 0.0;
+                }
+        };
+        // the item's unit as an LDS slot
+        auto slot = [&](int it) {
+            const int u = it - (it / U) * U;
+            return u >= us ? u - us : u - us + U;
+        };
+        // loads are unconditional (past the run they reload its last item)
+        for (int it = i0; it < i1; it += 2) {
+            if (it / U != tile) { flush(); tile = it / U; }
+            gemm_unit<TYPE, MC>(bufA, dA, eA, slot(it), M, nu, arow, mrow, sm, s_da, s_bs, S);
+            load(it + 2 < i1 ? it + 2 : i1 - 1, bufA, dA, eA);
+            if (it + 1 >= i1) break;
+            if ((it + 1) / U != tile) { flush(); tile = (it + 1) / U; }
+            gemm_unit<TYPE, MC>(bufB, dB, eB, slot(it + 1), M, nu, arow, mrow, sm, s_da, s_bs, S);
+            load(it + 3 < i1 ? it + 3 : i1 - 1, bufB, dB, eB);
+        }
+        flush();
     }
-    flush();
+    __syncthreads();
+    // the tile sums: stored where this workgroup covers the whole tile, else added
+    for (int i = tid; i < nt * M * 64; i += NT) {
+        const int t = i / (M * 64), r = i - t * (M * 64), m = r >> 6, l = r & 63;
+        const int tile = t0 + t;
+        double* g = a.gsum + (int64_t)(a.m0 + m) * a.n_pad + (int64_t)tile * 64 + l;
+        if (tile * U >= I0 && (tile + 1) * U <= I1) *g = s_acc[i];
+        else unsafeAtomicAdd(g, s_acc[i]);
+    }
 }
 
 // y = the accumulated split-K sums scaled by 2^(Ew + Ea - win); leaves the
@@ -430,10 +521,10 @@ __global__ __launch_bounds__(256) void qgemm_finalize_kernel(double* __restrict_
 template <int TYPE, int MC>
 cpv_status launch_mc(cpv_ctx* ctx, const GemmArgs& a, float* y, int64_t N, int64_t k, double wbytes)
 {
-    const size_t lds = gemm_lds<TYPE>(a.M, a.U);
+    const size_t lds = gemm_lds<TYPE>(a.M, a.nu_max, a.nt_max);
     const unsigned grid = (unsigned)ctx->cu_count;
     auto go = [=]() {
-        qgemm_kernel<TYPE, MC><<<grid, 64 * GEMM_WAVES, lds, ctx->stream>>>(a);
+        qgemm_kernel<TYPE, MC><<<grid, 64 * gemm_waves<TYPE, MC>(), lds, ctx->stream>>>(a);
         if (y)   // else the sums stay in the accumulator for a fused consumer
             qgemm_finalize_kernel<<<dim3((unsigned)((N + 255) / 256), (unsigned)a.M), 256, 0, ctx->stream>>>(
                 a.gsum, a.n_pad, a.ew, a.da, a.U * Fmt<TYPE>::DA, a.m0, a.win, y, N);
@@ -462,7 +553,7 @@ cpv_status launch_type(cpv_ctx* ctx, const GemmArgs& a, float* y, int64_t N, int
 }
 
 template <int TYPE>
-size_t lds_of(int M, int U) { return gemm_lds<TYPE>(M, U); }
+size_t lds_of(int M, int nu, int nt) { return gemm_lds<TYPE>(M, nu, nt); }
 
 static int isum_bits(int type) { return type == CPV_Q8_0 ? 20 : type == CPV_Q4_K ? 25 : 28; }
 
@@ -565,19 +656,24 @@ cpv_status cpv_qgemm_act(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, 
     a.bs = w->type == CPV_Q4_K ? act->bs32 : act->bs16;
     a.n_pad = w->n_pad;
     a.U = U;
-    a.items = tiles * U;
+    if (tiles * U > INT32_MAX / 2)
+        return cpv_fail(ctx, CPV_EUNSUPPORTED, "qgemm: %lld tiles of %d units", (long long)tiles, U);
+    a.items = (int)(tiles * U);
     a.win = cpv_qgemm_window(w->type, w->k);
     {
-        // consecutive items per wave: all waves of one workgroup per CU
-        const int64_t waves = (int64_t)ctx->cu_count * GEMM_WAVES;
-        a.chunk = (int)((a.items + waves - 1) / waves);
+        // one workgroup's items: at most ceil(items / CUs), spanning at most that
+        // many units and one tile more than they fill
+        const int per = (a.items + ctx->cu_count - 1) / ctx->cu_count;
+        a.nu_max = per < U ? per : U;
+        a.nt_max = (per + U - 1) / U + 1;
     }
     cpv_status st = gemm_accumulator(ctx, m, w->n_pad, &a.gsum);
     if (st != CPV_OK) return st;
     const double wb = (double)w->n * (double)(w->k / cpv_type_block(w->type)) * (double)cpv_type_size(w->type);
     auto lds = [&](int M) {
-        return w->type == CPV_Q4_K ? lds_of<CPV_Q4_K>(M, U) : w->type == CPV_Q6_K ? lds_of<CPV_Q6_K>(M, U)
-                                                                                 : lds_of<CPV_Q8_0>(M, U);
+        return w->type == CPV_Q4_K   ? lds_of<CPV_Q4_K>(M, a.nu_max, a.nt_max)
+               : w->type == CPV_Q6_K ? lds_of<CPV_Q6_K>(M, a.nu_max, a.nt_max)
+                                     : lds_of<CPV_Q8_0>(M, a.nu_max, a.nt_max);
     };
     const size_t lds_cap = ctx->lds_max - 1024;
     for (int64_t m0 = 0; m0 < m;) {
