@@ -179,11 +179,13 @@ cpv_status cpv_qgemm_keep(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act,
 __host__ __device__ __forceinline__ long long cpv_fixed_floor(float sq, int g)
 {
     const uint32_t b = __builtin_bit_cast(uint32_t, sq);
-    const int be = (int)(b >> 23);
+    const uint32_t be = b >> 23;
     const long long mant = (long long)((b & 0x7fffffu) | (be ? 0x800000u : 0u));
-    const int sh = (be ? be : 1) - 150 - g;                 // sq = mant * 2^(sh + g)
-    if (sh >= 0) return mant << sh;
-    return -sh >= 63 ? 0 : mant >> (-sh);
+    const int sh = (int)(be ? be : 1u) - 150 - g;           // sq = mant * 2^(sh + g)
+    // one of the two shifts is zero; no branch (a right shift by 24 or more clears mant)
+    const int ls = sh > 0 ? (sh < 63 ? sh : 63) : 0;
+    const int rs = sh < 0 ? (-sh < 63 ? -sh : 63) : 0;
+    return (mant << ls) >> rs;
 }
 
 __host__ __device__ __forceinline__ int cpv_exp_of_max(float mx)

@@ -223,14 +223,16 @@ __global__ void swiglu_kernel(const float* __restrict__ g, const float* __restri
 
 // ---------------------------------------------------------------- fused row kernels
 // One 1024-thread block per activation row.  Wave w holds the row's 256-element
-// units u = w, w + 16, ...; lane l holds elements u*256 + l + 64k (k < 4) of
-// each, so every per-unit step of the quantization is a wave reduction with no
-// barrier.  A row kernel produces the row (from the residual and a GEMM result
-// kept in the accumulator, or from the attention output and its gate, or from
-// the gate|up GEMM through SwiGLU), optionally RMS-normalizes it, and
-// optionally quantizes it for the next GEMM, with the same arithmetic as the
-// separate kernels it replaces (add_kernel, rmsnorm_kernel, gate_mul_kernel,
-// swiglu_kernel, quant_q8k_kernel / quant_q80_kernel).
+// units u = w, w + 16, ...; lane l holds elements u*256 + 4l .. 4l + 3 of each,
+// so every load and store is 16 (or 4) bytes wide and every per-unit step of
+// the quantization is a wave reduction with no barrier.  A row kernel
+// produces the row (from the residual and a GEMM result kept in the
+// accumulator, or from the attention output and its gate, or from the
+// gate|up GEMM through SwiGLU), optionally RMS-normalizes it, and optionally
+// quantizes it for the next GEMM, with the same arithmetic as the separate
+// kernels it replaces (add_kernel, rmsnorm_kernel, gate_mul_kernel,
+// swiglu_kernel, quant_q8k_kernel / quant_q80_kernel).  Row lengths are
+// multiples of 4.
 constexpr int RB = 1024;     // threads per row block
 constexpr int RW = RB / 64;  // waves
 constexpr int RUU = 3;       // units per wave: rows up to 3 * 16 * 256 = 12288 elements
@@ -299,59 +301,79 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
     const int m = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int n = a.n, U = (n + 255) / 256;
     constexpr bool kept = SRC == SRC_ADD || SRC == SRC_SET;
-    float* xr = a.x ? a.x + (int64_t)m * a.xs : nullptr;
-    // ---- the plain inputs go out first (every lane loads: no join before the uses)
-    float v[RQ];
+    float* xr = a.x + (int64_t)m * a.xs;
+    // this lane's four elements of each of its units (clamped to element 0 when out of range)
+    int e0[RUU];
+    bool ok[RUU];
 #pragma unroll
-    for (int uu = 0; uu < RUU; uu++)
+    for (int uu = 0; uu < RUU; uu++) {
+        const int u = wave + RW * uu, e = u * 256 + 4 * lane;
+        ok[uu] = u < U && e < n;
+        e0[uu] = ok[uu] ? e : 0;
+    }
+    // ---- every input goes out first, unconditionally (a branch would make
+    // the compiler wait for all of them at the join): x, the norm weight, a
+    // kept result's sums and row exponents, and the scales that give Ea
+    float v[RQ], wv[RQ];
+    const float* wsrc = a.w ? a.w : xr;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int j = uu * 4 + k, u = wave + RW * uu;
-            const int e = u * 256 + lane + 64 * k;
-            const int ec = e < n ? e : n - 1;
-            v[j] = (SRC == SRC_X || SRC == SRC_ADD) ? xr[ec] : 0.0f;
-        }
-    // ---- a kept result: its sums and row exponents are loaded before anything
-    // is stored (the stores below could alias them), then Ea, then y = the
-    // finalized sums, folded into x, the accumulator entries cleared
+    for (int uu = 0; uu < RUU; uu++) {
+        const float4 xv = *(const float4*)(xr + e0[uu]);
+        const float4 ww = *(const float4*)(wsrc + e0[uu]);
+        const bool use_x = SRC == SRC_X || SRC == SRC_ADD;
+        v[uu * 4 + 0] = use_x ? xv.x : 0.0f;
+        v[uu * 4 + 1] = use_x ? xv.y : 0.0f;
+        v[uu * 4 + 2] = use_x ? xv.z : 0.0f;
+        v[uu * 4 + 3] = use_x ? xv.w : 0.0f;
+        wv[uu * 4 + 0] = ww.x;
+        wv[uu * 4 + 1] = ww.y;
+        wv[uu * 4 + 2] = ww.z;
+        wv[uu * 4 + 3] = ww.w;
+    }
     if (kept) {
+        // its sums and row exponents are loaded before anything is stored (the
+        // stores below could alias them), then Ea, then y = the finalized sums,
+        // folded into x, the accumulator entries cleared
         double* acc = a.g.acc + (int64_t)m * a.g.n_pad;
         double S[RQ];
         int ew[RQ];
 #pragma unroll
-        for (int uu = 0; uu < RUU; uu++)
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int j = uu * 4 + k, u = wave + RW * uu;
-                const int e = u * 256 + lane + 64 * k;
-                const int ec = e < n ? e : n - 1;
-                S[j] = acc[ec];
-                ew[j] = a.g.ew[ec];
-            }
-        float mx = 0.0f;
-        for (int i = tid; i < a.g.nda; i += RB) mx = fmaxf(mx, fabsf(a.g.da[(int64_t)m * a.g.nda + i]));
+        for (int uu = 0; uu < RUU; uu++) {
+            const double2 s0 = *(const double2*)(acc + e0[uu]);
+            const double2 s1 = *(const double2*)(acc + e0[uu] + 2);
+            const int4 ev = *(const int4*)(a.g.ew + e0[uu]);
+            S[uu * 4 + 0] = s0.x;
+            S[uu * 4 + 1] = s0.y;
+            S[uu * 4 + 2] = s1.x;
+            S[uu * 4 + 3] = s1.y;
+            ew[uu * 4 + 0] = ev.x;
+            ew[uu * 4 + 1] = ev.y;
+            ew[uu * 4 + 2] = ev.z;
+            ew[uu * 4 + 3] = ev.w;
+        }
+        const float* dar = a.g.da + (int64_t)m * a.g.nda;
+        float mx = fabsf(dar[tid < a.g.nda ? tid : 0]);
+        if (tid >= a.g.nda) mx = 0.0f;
+        for (int i = tid + RB; i < a.g.nda; i += RB) mx = fmaxf(mx, fabsf(dar[i]));
         const int ea = cpv_exp_of_max(row_max(mx, L));
 #pragma unroll
-        for (int uu = 0; uu < RUU; uu++)
+        for (int j = 0; j < RQ; j++) {
+            const float gv = cpv_gout_value(S[j], ew[j], ea, a.g.win);
+            v[j] = SRC == SRC_ADD ? gv + v[j] : gv;
+        }
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int j = uu * 4 + k, u = wave + RW * uu;
-                const int e = u * 256 + lane + 64 * k;
-                if (u < U && e < n) {
-                    const float gv = cpv_gout_value(S[j], ew[j], ea, a.g.win);
-                    v[j] = SRC == SRC_ADD ? gv + v[j] : gv;
-                    acc[e] = 0.0;
-                    xr[e] = v[j];
-                }
+        for (int uu = 0; uu < RUU; uu++)
+            if (ok[uu]) {
+                *(float4*)(xr + e0[uu]) = make_float4(v[uu * 4], v[uu * 4 + 1], v[uu * 4 + 2], v[uu * 4 + 3]);
+                *(double2*)(acc + e0[uu]) = make_double2(0.0, 0.0);
+                *(double2*)(acc + e0[uu] + 2) = make_double2(0.0, 0.0);
             }
     }
 #pragma unroll
     for (int uu = 0; uu < RUU; uu++)
+        if (!ok[uu])
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int u = wave + RW * uu, e = u * 256 + lane + 64 * k;
-            if (!(u < U && e < n)) v[uu * 4 + k] = 0.0f;
-        }
+            for (int k = 0; k < 4; k++) v[uu * 4 + k] = 0.0f;
     if (a.norm) {
         // exact fixed-point sum of the f32 squares, then ggml's f32 tail
         float am = 0.0f;
@@ -374,20 +396,17 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
         for (int uu = 0; uu < RUU; uu++)
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const int j = uu * 4 + k, u = wave + RW * uu;
-                const int e = u * 256 + lane + 64 * k;
+                const int j = uu * 4 + k;
                 const float tv = v[j] * scale;
-                v[j] = (u < U && e < n) ? (a.w ? tv * a.w[e] : tv) : 0.0f;   // padding stays 0
+                v[j] = ok[uu] ? (a.w ? tv * wv[j] : tv) : 0.0f;   // padding stays 0
             }
     }
     if (a.y) {
 #pragma unroll
         for (int uu = 0; uu < RUU; uu++)
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int u = wave + RW * uu, e = u * 256 + lane + 64 * k;
-                if (u < U && e < n) a.y[(int64_t)m * a.ys + e] = v[uu * 4 + k];
-            }
+            if (ok[uu])
+                *(float4*)(a.y + (int64_t)m * a.ys + e0[uu]) =
+                    make_float4(v[uu * 4], v[uu * 4 + 1], v[uu * 4 + 2], v[uu * 4 + 3]);
     }
     if (!a.quant) return;
     const int64_t Kp = (int64_t)U * 256;
@@ -400,23 +419,22 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
         const int u = wave + RW * uu;
         if (u >= U) break;                                  // wave-uniform
         const float* x = v + uu * 4;
-        int8_t* qrow = qa + (int64_t)m * Kp + (int64_t)u * 256;
+        uint32_t* qw = (uint32_t*)(qa + (int64_t)m * Kp + (int64_t)u * 256) + lane;
+        int q[4];
         if (a.act.kq) {
             // Q8_K: the signed element of largest magnitude (first occurrence),
             // iscale = -127/max, q = min(127, rint(iscale * x)), d = 1/iscale, code sums
-            float ax = fabsf(x[0]);
-            int ix = lane, kk = 0;
+            float ax = fabsf(x[0]), sx = x[0];
+            int ix = 4 * lane;
 #pragma unroll
             for (int k = 1; k < 4; k++)
-                if (fabsf(x[k]) > ax) { ax = fabsf(x[k]); ix = lane + 64 * k; kk = k; }
-            float sx = x[kk];
+                if (fabsf(x[k]) > ax) { ax = fabsf(x[k]); ix = 4 * lane + k; sx = x[k]; }
             for (int off = 32; off > 0; off >>= 1) {
                 const float oa = __shfl_xor(ax, off);
                 const int oi = __shfl_xor(ix, off);
                 const float os = __shfl_xor(sx, off);
                 if (oa > ax || (oa == ax && oi < ix)) { ax = oa; ix = oi; sx = os; }
             }
-            int q[4];
             float d = 0.0f;
             if (ax > 0.0f) {
                 const float iscale = -127.0f / sx;
@@ -430,27 +448,27 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
 #pragma unroll
                 for (int k = 0; k < 4; k++) q[k] = 0;
             }
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                qrow[lane + 64 * k] = (int8_t)q[k];
-                int s16 = q[k];
-                for (int off = 8; off > 0; off >>= 1) s16 += __shfl_xor(s16, off);
-                const int s32 = s16 + __shfl_xor(s16, 16);
-                if ((lane & 15) == 0) bs16[((int64_t)m * U + u) * 16 + k * 4 + (lane >> 4)] = s16;
-                if ((lane & 31) == 0) bs32[((int64_t)m * U + u) * 8 + k * 2 + (lane >> 5)] = s32;
-            }
+            *qw = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
+                  ((uint32_t)(q[3] & 0xff) << 24);
+            // code sums of 16 (4 lanes) and 32 (8 lanes) elements
+            int s16 = q[0] + q[1] + q[2] + q[3];
+            s16 += __shfl_xor(s16, 1);
+            s16 += __shfl_xor(s16, 2);
+            const int s32 = s16 + __shfl_xor(s16, 4);
+            if ((lane & 3) == 0) bs16[((int64_t)m * U + u) * 16 + (lane >> 2)] = s16;
+            if ((lane & 7) == 0) bs32[((int64_t)m * U + u) * 8 + (lane >> 3)] = s32;
             if (lane == 0) da[(int64_t)m * U + u] = d;
         } else {
-            // Q8_0 per 32-element block: d = amax/127, q = roundf(x * (1/d)), d kept as fp16
+            // Q8_0 per 32-element block (8 lanes): d = amax/127, q = roundf(x * (1/d)), d kept as fp16
+            float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+            for (int off = 4; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                float amax = fabsf(x[k]);
-                for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
-                const float d = amax / 127.0f;
-                const float id = d != 0.0f ? 1.0f / d : 0.0f;
-                qrow[lane + 64 * k] = (int8_t)(int)roundf(x[k] * id);
-                if ((lane & 31) == 0) da[((int64_t)m * U + u) * 8 + k * 2 + (lane >> 5)] = cpv_h2f(cpv_f2h(d));
-            }
+            for (int k = 0; k < 4; k++) q[k] = (int)roundf(x[k] * id);
+            *qw = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
+                  ((uint32_t)(q[3] & 0xff) << 24);
+            if ((lane & 7) == 0) da[((int64_t)m * U + u) * 8 + (lane >> 3)] = cpv_h2f(cpv_f2h(d));
         }
     }
 }
@@ -1005,6 +1023,15 @@ cpv_status rmsnorm(cpv_ctx* ctx, const float* x, int64_t xs, const float* w, flo
 cpv_status row_launch(cpv_ctx* ctx, const RowArgs& a, int T)
 {
     const dim3 ugrid((unsigned)((a.n + 255) / 256), (unsigned)T);
+    if (a.src <= SRC_SET) {
+        // row_kernel: 16-byte accesses of every row it reads or writes
+        auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+        const bool kept = a.src != SRC_X;
+        if (a.n % 4 || a.xs % 4 || !a.x || !al(a.x) || (a.w && !al(a.w)) || (a.y && (a.ys % 4 || !al(a.y))) ||
+            (kept && (!al(a.g.acc) || a.g.n_pad % 4 || !al(a.g.ew))))
+            return cpv_fail(ctx, CPV_EUNSUPPORTED, "row kernel: rows of %d need 16-byte aligned rows of a multiple of 4",
+                            a.n);
+    }
     switch (a.src) {
     case SRC_X: row_kernel<SRC_X><<<(unsigned)T, RB, 0, ctx->stream>>>(a); break;
     case SRC_ADD: row_kernel<SRC_ADD><<<(unsigned)T, RB, 0, ctx->stream>>>(a); break;

@@ -131,10 +131,10 @@ struct GemmArgs {
     int nu_max, nt_max;    // most units / tiles one workgroup's items touch
 };
 
-// waves per workgroup (one workgroup per CU): 12 where the kernel fits 3
-// waves per SIMD in registers, else 8
+// waves per workgroup (one workgroup per CU; 12 waves, where registers
+// allow 3 per SIMD, measured slower)
 template <int TYPE, int MC>
-constexpr int gemm_waves() { return TYPE == CPV_Q4_K && MC <= 5 ? 12 : 8; }
+constexpr int gemm_waves() { return 8; }
 
 __device__ __forceinline__ v4i mfma4(int a, int b, v4i c)
 {
@@ -370,9 +370,10 @@ __global__ __launch_bounds__((64 * gemm_waves<TYPE, MC>())) void qgemm_kernel(Ge
         return a.da + ((int64_t)(a.m0 + m) * U + u) * F::DA + (c - j * F::DA);
     };
     auto bs_src = [&](int i) {
-        const int m = i / (nu * F::BS), c = i - m * (nu * F::BS), j = c / F::BS;
+        constexpr int BS = F::BS > 0 ? F::BS : 1;   // (not called without code sums)
+        const int m = i / (nu * BS), c = i - m * (nu * BS), j = c / BS;
         const int u = us + j < U ? us + j : us + j - U;
-        return a.bs + ((int64_t)(a.m0 + m) * U + u) * F::BS + (c - j * F::BS);
+        return a.bs + ((int64_t)(a.m0 + m) * U + u) * BS + (c - j * BS);
     };
     v4i cv[BC];
     float dv[BD];

@@ -225,3 +225,37 @@ def test_q4k_model_rounds_and_stream_are_bit_exact(kmodels):
     assert [st.accepted, st.proposed, st.rounds] == ost
     g.free()
     o.free()
+
+
+W_MODEL = dict(mf.TINY, n_layer=1, n_embd=5120, n_head=40, n_head_kv=8, head_dim=128, n_rot=128,
+               rope_sections=[22, 22, 20, 0], n_ff=1536, n_vocab=2048)
+
+
+@pytest.mark.gpu
+def test_wide_rows_round_is_bit_exact():
+    # d_model 5120: 20 units per row, so the row kernels' waves take a second
+    # unit (the widths above all fit one pass); the 27B-class head layout
+    from codpiece_amd.model import Model, Session, make_hparams
+    from codpiece_amd.runtime import Context
+    ctx = Context(0)
+    tensors = mf.make_tensors(W_MODEL, seed=11, qtype=cpvo.Q4_K, head_type=cpvo.Q6_K)
+    gm = Model(ctx, make_hparams(**W_MODEL))
+    mf.load_into(gm, tensors)
+    gm.ready()
+    om = cpvo.Model(W_MODEL)
+    mf.load_into(om, tensors)
+    rng = np.random.default_rng(12)
+    prompt = rng.integers(0, W_MODEL["n_vocab"], size=45).tolist()
+    g, o = Session(gm, 128), cpvo.Session(om, 128)
+    g.prefill(prompt[:40])
+    o.prefill(prompt[:40])
+    a = g.step_fused_cached(prompt[40:45], 4, want_logits=True)
+    b = o.step_fused_cached(prompt[40:45], 4, want_logits=True)
+    assert np.array_equal(a.hidden.cpu().numpy().view(np.uint32), b[4].view(np.uint32))
+    assert np.array_equal(a.logits.cpu().numpy().view(np.uint32), b[3].view(np.uint32))
+    assert a.preds == b[0].tolist() and a.chain == b[1].tolist()
+    g.free()
+    o.free()
+    gm.free()
+    om.free()
+    ctx.close()
