@@ -335,10 +335,13 @@ __global__ __launch_bounds__(D) void attn_fold_kernel(const float* __restrict__ 
     out[(int64_t)row * D + d] = o * s_inv;
 }
 
-// one call over T query tokens (the scratch holds T*H rows per chunk)
+// one call over T query tokens (the scratch holds T*H rows per chunk); with
+// out null only the chunk partials are produced (into *part), for a consumer
+// that folds them itself
 template <int D>
 cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
-                      int64_t n_past, const int32_t* parent, int T, int H, int Hkv, float scale, float* out)
+                      int64_t n_past, const int32_t* parent, int T, int H, int Hkv, float scale, float* out,
+                      cpv_attn_part* part = nullptr)
 {
     const int64_t n = n_past + T;
     const int G = H / Hkv, LR = G * T, rows = T * H;
@@ -366,10 +369,28 @@ cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const ui
     ca.scale = scale;
     attn_chunk_kernel<D><<<dim3((unsigned)nchunk, (unsigned)Hkv, (unsigned)((LR + QB - 1) / QB)), CT, 0,
                            ctx->stream>>>(ca);
-    attn_fold_kernel<D><<<(unsigned)rows, D, (size_t)nchunk * 12, ctx->stream>>>(ca.P, ca.mc, ca.zc, nchunk, rows,
-                                                                              out);
+    if (out)
+        attn_fold_kernel<D><<<(unsigned)rows, D, (size_t)nchunk * 12, ctx->stream>>>(ca.P, ca.mc, ca.zc, nchunk,
+                                                                                  rows, out);
     CPV_HIP(ctx, hipGetLastError());
+    if (part) {
+        part->P = ca.P;
+        part->mc = ca.mc;
+        part->zc = ca.zc;
+        part->nchunk = nchunk;
+        part->rows = rows;
+        part->zbits = ZBITS;
+    }
     return CPV_OK;
+}
+
+// the chain's scratch per token, and whether T tokens run as one block
+template <int D>
+bool attn_one_block(int64_t n_past, int t, int h)
+{
+    const int64_t n = n_past + t;
+    const int64_t per_token = (int64_t)h * ((n + CHUNK - 1) / CHUNK) * (D * 4 + 12);
+    return ((int64_t)192 << 20) / (per_token + 1) >= t;
 }
 
 template <int D>
@@ -380,7 +401,7 @@ cpv_status attn_run(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint
     // a long chain runs in token blocks to bound the scratch: node t of a chain sees
     // the rows <= n_past + t, which is what a block starting at t0 sees with n_past + t0
     const int64_t n = n_past + t;
-    const int64_t per_token = (int64_t)h * ((n + CHUNK - 1) / CHUNK) * (D * 4 + 12);
+    const int64_t per_token = (int64_t)h * ((n + CHUNK - 1) / CHUNK) * (D * 4 + 12);   // (attn_one_block)
     int64_t tb = ((int64_t)192 << 20) / (per_token + 1);
     if (tb < 1) tb = 1;
     if (tb > t) tb = t;
@@ -407,6 +428,25 @@ cpv_status cpv_attn_launch(cpv_ctx* ctx, const float* q, const uint16_t* kc, con
     const cpv_status st = go();
     if (st == CPV_OK && ev >= 0) {  // algorithmic bytes: K and V rows once, q in, out
         const double bytes = 2.0 * 2.0 * (double)(n_past + t) * h_kv * d + 2.0 * 4.0 * t * h * d;
+        cpv_prof_add(ctx, ev, CPV_PROF_ATTN, bytes);
+        cpv_prof_keep(ctx, CPV_PROF_ATTN, bytes, [go]() { (void)go(); });
+    }
+    return st;
+}
+
+cpv_status cpv_attn_partials(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
+                             int64_t n_past, int t, int h, int h_kv, int d, float scale, cpv_attn_part* part)
+{
+    if ((d != 64 && d != 128) || !(d == 128 ? attn_one_block<128>(n_past, t, h) : attn_one_block<64>(n_past, t, h)))
+        return CPV_EUNSUPPORTED;   // (no message: the caller takes the unfused path)
+    auto go = [=]() {
+        return d == 128 ? attn_block<128>(ctx, q, kc, vt, v_stride, n_past, nullptr, t, h, h_kv, scale, nullptr, part)
+                        : attn_block<64>(ctx, q, kc, vt, v_stride, n_past, nullptr, t, h, h_kv, scale, nullptr, part);
+    };
+    const int ev = cpv_prof_mark(ctx);
+    const cpv_status st = go();
+    if (st == CPV_OK && ev >= 0) {  // algorithmic bytes: K and V rows once, q in (the fold is the consumer's)
+        const double bytes = 2.0 * 2.0 * (double)(n_past + t) * h_kv * d + 4.0 * t * h * d;
         cpv_prof_add(ctx, ev, CPV_PROF_ATTN, bytes);
         cpv_prof_keep(ctx, CPV_PROF_ATTN, bytes, [go]() { (void)go(); });
     }

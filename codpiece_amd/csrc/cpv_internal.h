@@ -215,3 +215,17 @@ cpv_status cpv_attn_launch(cpv_ctx* ctx, const float* q, const uint16_t* kc, con
                            int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
                            float* out);
 cpv_status cpv_qgemm_launch(cpv_ctx* ctx, const cpv_weight* w, const float* x, int64_t m, float* y);
+
+// the attention's chunk partials for a consumer that folds them itself (chains
+// only, when t tokens run as one block; else CPV_EUNSUPPORTED, nothing launched):
+// P [nchunk][rows][d] f32, mc [nchunk][rows] f32, zc [nchunk][rows] int64 in
+// the context workspace, rows = t * h, row = token * h + head
+struct cpv_attn_part {
+    const float* P;
+    const float* mc;
+    const long long* zc;
+    int nchunk, rows;
+    int zbits;            // zc holds Z_c 2^zbits
+};
+cpv_status cpv_attn_partials(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
+                             int64_t n_past, int t, int h, int h_kv, int d, float scale, cpv_attn_part* part);

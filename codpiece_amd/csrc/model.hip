@@ -238,7 +238,8 @@ constexpr int RW = RB / 64;  // waves
 constexpr int RUU = 3;       // units per wave: rows up to 3 * 16 * 256 = 12288 elements
 constexpr int RQ = RUU * 4;  // register slots per thread
 
-enum { SRC_X = 0, SRC_ADD = 1, SRC_SET = 2, SRC_GATE = 3, SRC_SWIGLU = 4 };
+enum { SRC_X = 0, SRC_ADD = 1, SRC_SET = 2, SRC_GATE = 3, SRC_SWIGLU = 4, SRC_GATE_FOLD = 5 };
+constexpr int FOLD_MAX = 512;   // attention chunks a SRC_GATE_FOLD row kernel folds (contexts to 64k)
 
 struct RowArgs {
     int src;
@@ -247,6 +248,8 @@ struct RowArgs {
     cpv_gout g;            // kept GEMM result (SRC_ADD / _SET / _SWIGLU)
     const float* att;      // SRC_GATE: attention output [T][n] and gate [T][n]
     const float* gate;
+    cpv_attn_part part;    // SRC_GATE_FOLD: the attention's chunk partials (rows = T * n / hd)
+    int hd;                // SRC_GATE_FOLD: head dim
     int n;                 // row length
     const float* w;        // RMS norm weight, when norm
     int norm;
@@ -485,7 +488,59 @@ __global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
     const int n = a.n, U = (n + 255) / 256;
     const int e = u * 256 + t, ec = e < n ? e : n - 1;
     float val = 0.0f;
-    if (SRC == SRC_GATE) {
+    if (SRC == SRC_GATE_FOLD) {
+        // the attention output of this element's head (the fold of
+        // attn_fold_kernel: chunks in order, factors expf(m_c - M), the
+        // binary64 sum of the Z_c, one fma chain per element), times
+        // sigmoid(gate).  A unit holds 256 / hd heads; hd threads per head.
+        __shared__ float s_f[4][FOLD_MAX];
+        __shared__ double s_z[4][FOLD_MAX];
+        __shared__ float s_m[4][2], s_inv[4];
+        const int hd = a.hd, nch = a.part.nchunk, rows = a.part.rows, H = n / hd;
+        const int lh = t / hd, tl = t - lh * hd;             // head within the unit, thread within the head
+        const int h = ec / hd, rr = m * H + h;                // (clamped: a thread past n reads a valid head)
+        const int wph = hd / 64;                              // waves per head
+        float M = -INFINITY;
+        for (int c = tl; c < nch; c += hd) {
+            const float mc = a.part.mc[(int64_t)c * rows + rr];
+            s_f[lh][c] = mc;
+            s_z[lh][c] = ldexp((double)a.part.zc[(int64_t)c * rows + rr], -a.part.zbits);
+            M = fmaxf(M, mc);
+        }
+        for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+        if (lane == 0) s_m[lh][wave - lh * wph] = M;
+        __syncthreads();
+        M = s_m[lh][0];
+        for (int i = 1; i < wph; i++) M = fmaxf(M, s_m[lh][i]);
+        for (int c = tl; c < nch; c += hd) {
+            const float mc = s_f[lh][c];
+            s_f[lh][c] = mc == -INFINITY ? 0.0f : cpv_expf(mc - M);
+        }
+        __syncthreads();
+        if (tl == 0) {
+            double Zt = 0.0;
+            for (int c = 0; c < nch; c++) Zt = Zt + s_z[lh][c] * (double)s_f[lh][c];
+            s_inv[lh] = (float)(1.0 / Zt);
+        }
+        // the element's fma chain, loads issued eight at a time
+        const float* pr = a.part.P + (int64_t)rr * hd + (ec - h * hd);
+        const int64_t cs = (int64_t)rows * hd;
+        float o = 0.0f;
+        int c = 0;
+        for (; c + 8 <= nch; c += 8) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = pr[(c + i) * cs];
+#pragma unroll
+            for (int i = 0; i < 8; i++) o = fmaf(v[i], s_f[lh][c + i], o);
+        }
+        for (; c < nch; c++) o = fmaf(pr[c * cs], s_f[lh][c], o);
+        __syncthreads();
+        const float at = o * s_inv[lh];
+        const float gv = a.gate[(int64_t)m * n + ec];
+        const float sig = 1.0f / (1.0f + cpv_expf(-gv));
+        val = e < n ? at * sig : 0.0f;
+    } else if (SRC == SRC_GATE) {
         const float gv = a.gate[(int64_t)m * n + ec], at = a.att[(int64_t)m * n + ec];
         const float sig = 1.0f / (1.0f + cpv_expf(-gv));
         val = e < n ? at * sig : 0.0f;
@@ -1037,6 +1092,11 @@ cpv_status row_launch(cpv_ctx* ctx, const RowArgs& a, int T)
     case SRC_ADD: row_kernel<SRC_ADD><<<(unsigned)T, RB, 0, ctx->stream>>>(a); break;
     case SRC_SET: row_kernel<SRC_SET><<<(unsigned)T, RB, 0, ctx->stream>>>(a); break;
     case SRC_GATE: unit_kernel<SRC_GATE><<<ugrid, 256, 0, ctx->stream>>>(a); break;
+    case SRC_GATE_FOLD:
+        if (a.hd % 64 || 256 % a.hd || a.n % a.hd || a.part.nchunk > FOLD_MAX)
+            return cpv_fail(ctx, CPV_EUNSUPPORTED, "gate fold: head dim %d, %d chunks", a.hd, a.part.nchunk);
+        unit_kernel<SRC_GATE_FOLD><<<ugrid, 256, 0, ctx->stream>>>(a);
+        break;
     default: unit_kernel<SRC_SWIGLU><<<ugrid, 256, 0, ctx->stream>>>(a); break;
     }
     CPV_HIP(ctx, hipGetLastError());
@@ -1213,22 +1273,36 @@ cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_
     qk_prep_kept_kernel<<<dim3((unsigned)T, (unsigned)(H + Hkv)), (unsigned)hd, 0, ctx->stream>>>(pk);
     CPV_HIP(ctx, hipGetLastError());
     const float kq_scale = 1.0f / sqrtf((float)hd);
-    if ((st = cpv_attn_launch(ctx, s->q, kc, vt, v_stride, attn_past, nullptr, T, (int)H, (int)Hkv, (int)hd, kq_scale,
-                              s->att)))
-        return st;
-    if (s->tap) {
-        const int64_t n = (int64_t)T * H * hd;
-        if (s->tap_off + n <= s->tap_cap)
-            CPV_HIP(ctx, hipMemcpyAsync(s->tap + s->tap_off, s->att, (size_t)n * 4, hipMemcpyDeviceToDevice, ctx->stream));
-        s->tap_off += n;
-    }
-    // attention output times sigmoid(gate), the wo input
+    // attention output times sigmoid(gate), the wo input: the gate kernel folds
+    // the attention's chunk partials itself, unless the tap wants the output or
+    // the partials do not come in one block
     RowArgs r2{};
-    r2.src = SRC_GATE;
-    r2.att = s->att;
     r2.gate = s->qg;
     r2.n = (int)(H * hd);
     r2.quant = 1;
+    cpv_attn_part part{};
+    const int64_t nch = (attn_past + T + 127) / 128;         // the attention's 128-row chunks
+    const bool fold = !s->tap && hd % 64 == 0 && 256 % hd == 0 && nch <= FOLD_MAX &&
+                      cpv_attn_partials(ctx, s->q, kc, vt, v_stride, attn_past, T, (int)H, (int)Hkv, (int)hd, kq_scale,
+                                        &part) == CPV_OK;
+    if (fold) {
+        r2.src = SRC_GATE_FOLD;
+        r2.part = part;
+        r2.hd = (int)hd;
+    } else {
+        if ((st = cpv_attn_launch(ctx, s->q, kc, vt, v_stride, attn_past, nullptr, T, (int)H, (int)Hkv, (int)hd,
+                                  kq_scale, s->att)))
+            return st;
+        if (s->tap) {
+            const int64_t n = (int64_t)T * H * hd;
+            if (s->tap_off + n <= s->tap_cap)
+                CPV_HIP(ctx,
+                        hipMemcpyAsync(s->tap + s->tap_off, s->att, (size_t)n * 4, hipMemcpyDeviceToDevice, ctx->stream));
+            s->tap_off += n;
+        }
+        r2.src = SRC_GATE;
+        r2.att = s->att;
+    }
     cpv_act_layout(L.wo->type, T, H * hd, next_act(s), &r2.act);
     if ((st = row_launch(ctx, r2, T))) return st;
     if ((st = cpv_qgemm_keep(ctx, L.wo, &r2.act, &g))) return st;
