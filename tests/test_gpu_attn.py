@@ -59,8 +59,9 @@ def test_tiny_model_chain(ctx, n_past):
     close(*run(ctx, 5, 8, 2, 64, n_past, None))
 
 
-@pytest.mark.parametrize("n_past", [4096, 4101])
+@pytest.mark.parametrize("n_past", [4096, 4101, 4123, 4124])
 def test_27b_class_chain(ctx, n_past):
+    # n = n_past + 5 rows: a final chunk of 5, 10, 32 and 33 rows
     close(*run(ctx, 5, 40, 8, 128, n_past, None))
 
 
