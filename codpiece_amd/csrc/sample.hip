@@ -22,8 +22,9 @@
 //  * Candidate order (logit descending, id ascending; cmp_desc, lib.rs:
 //    453-459) as a stream of sorted bands: a radix histogram over the 64-bit
 //    key (order-flipped logit bits, id) picks the next <= 16384 keys, which
-//    are gathered and bitonic-sorted in LDS.  Only as much of the order as
-//    the filter needs is produced.
+//    are gathered, packed into 50 bits (key << 18 | id) and radix-sorted in
+//    LDS by rocPRIM's block sort.  Only as much of the order as the filter
+//    needs is produced.
 //  * exp is the glibc expf restatement (cpv_expf); divisions are IEEE; the
 //    library is built without contraction, so every a*b+c rounds twice as
 //    in the Rust source.
@@ -31,6 +32,8 @@
 
 #include <float.h>
 #include <math.h>
+
+#include <rocprim/block/block_radix_sort.hpp>
 
 namespace {
 
@@ -43,7 +46,13 @@ constexpr uint32_t FSAT = 1u << 26;    // fold: saturation of a composed step
 constexpr int BAND = 16384;            // sorted band held in LDS as u64 keys
 constexpr int HIST_MAX = 4096;         // penalty window input limit (4 per thread)
 constexpr int VMAX = 262144;           // ids fit the low 18 bits of a key
-constexpr size_t SAMPLE_LDS_KEYS = (size_t)BAND * 8;
+// a band in candidate order: a block radix sort of 16 keys per thread, each
+// key (desc_key, id) packed into 50 bits; its storage overlays the key buffer
+using band_sort_t = rocprim::block_radix_sort<unsigned long long, SB, BAND / SB>;
+constexpr int KEY_BITS = 50;
+constexpr size_t SAMPLE_LDS_KEYS =
+    (((size_t)BAND * 8 > sizeof(band_sort_t::storage_type) ? (size_t)BAND * 8 : sizeof(band_sort_t::storage_type)) +
+     255) & ~(size_t)255;
 
 // ------------------------------------------------------------ block scratch
 struct FMap { uint32_t d0, d1; };      // S -> S + (S even ? d0 : d1)
@@ -55,6 +64,7 @@ struct Small {
     float wf[SWV];
     int wi[SWV];
     int iv[8];
+    unsigned long long last;           // the last key of a band
 };
 
 // for (i = tid; i < n; i += SB) use(i, load(i)), with BU loads in flight:
@@ -375,28 +385,11 @@ __device__ __forceinline__ unsigned long long cand_key(float l, int i)
     return ((unsigned long long)desc_key(l) << 32) | (uint32_t)i;
 }
 
-__device__ void bitonic_sort(unsigned long long* keys, int P)
-{
-    const int tid = threadIdx.x;
-    for (int k2 = 2; k2 <= P; k2 <<= 1) {
-        for (int j = k2 >> 1; j > 0; j >>= 1) {
-            for (int t = tid; t < P / 2; t += SB) {
-                const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
-                const int l = i | j;
-                const unsigned long long a = keys[i], b = keys[l];
-                const bool up = (i & k2) == 0;
-                if ((a > b) == up) { keys[i] = b; keys[l] = a; }
-            }
-            __syncthreads();
-        }
-    }
-}
-
 // The next band of the candidate order after key *last (all keys when
 // have_last is false): at most BAND keys, ending early at a histogram bin
 // boundary once `want` are in.  Writes ids and logits to sid/sl[pos...],
 // advances *last and returns the band size.
-__device__ int emit_band(const float* lg, int V, bool have_last, unsigned long long* last_io, int want,
+__device__ __noinline__ int emit_band(const float* lg, int V, bool have_last, unsigned long long* last_io, int want,
                          int pos, int32_t* sid, float* sl, unsigned long long* keys, Small* sm)
 {
     const int tid = threadIdx.x;
@@ -467,17 +460,29 @@ __device__ int emit_band(const float* lg, int V, bool have_last, unsigned long l
     });
     __syncthreads();
     const int cnt = sm->iv[3];
-    int P = 64;
-    while (P < cnt) P <<= 1;
-    for (int t = cnt + tid; t < P; t += SB) keys[t] = ~0ull;
-    __syncthreads();
-    bitonic_sort(keys, P);
-    for (int t = tid; t < cnt; t += SB) {
-        const int id = (int)(uint32_t)keys[t];
-        sid[pos + t] = id;
-        sl[pos + t] = lg[id];
+    constexpr int IPT = BAND / SB;
+    unsigned long long k[IPT];
+#pragma unroll
+    for (int q = 0; q < IPT; q++) {
+        const int t = tid * IPT + q;
+        const unsigned long long key = t < cnt ? keys[t] : ~0ull;
+        k[q] = key == ~0ull ? (1ull << KEY_BITS) - 1 : ((key >> 32) << 18) | (key & 0x3ffffull);
     }
-    *last_io = keys[cnt - 1];
+    __syncthreads();                           // the key buffer becomes the sort's storage
+    band_sort_t().sort(k, *reinterpret_cast<band_sort_t::storage_type*>(keys), 0, KEY_BITS);
+    // thread t now holds positions t*IPT .. t*IPT + IPT-1 of the band
+#pragma unroll
+    for (int q = 0; q < IPT; q++) {
+        const int t = tid * IPT + q;
+        if (t < cnt) {
+            const int id = (int)(k[q] & 0x3ffffull);
+            sid[pos + t] = id;
+            sl[pos + t] = lg[id];
+            if (t == cnt - 1) sm->last = ((k[q] >> 18) << 32) | (k[q] & 0x3ffffull);
+        }
+    }
+    __syncthreads();
+    *last_io = sm->last;
     __syncthreads();
     return cnt;
 }
