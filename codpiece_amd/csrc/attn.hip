@@ -126,55 +126,92 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     __shared__ __align__(16) float s_pt[CHUNK][QB];    // the f16-rounded weights (as f32), row-minor
     __shared__ int s_eq[QB], s_ek[CHUNK];
     __shared__ unsigned long long s_anc[QB];
+    __shared__ uint64_t s_etab[32];                     // the expf table
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int c = blockIdx.x, kh = blockIdx.y;
+    if (tid < 32) {
+        constexpr uint64_t etab[32] = CPV_EXP2F_TAB;
+        s_etab[tid] = etab[tid];
+    }
+    // KV head fastest: the last blocks dispatched are the heads' last chunk,
+    // the only one that can be short, and a short chunk costs little below
+    const int c = blockIdx.x / a.Hkv, kh = blockIdx.x % a.Hkv;
     const int G = a.H / a.Hkv, LR = G * a.T;
     const int64_t j0 = (int64_t)c * CHUNK;
     const int nj = (int)(a.n - j0 < CHUNK ? a.n - j0 : CHUNK);
     const int sub = tid % TPR;
     const bool tree = a.parent != nullptr;
 
+    // ---- q and K go out first, at clamped (in-bounds) rows, with no branch
+    // around a load (a branch makes the compiler wait for every load at the join)
+    constexpr int KP = CHUNK / RPP > 0 ? CHUNK / RPP : 1;   // K passes
+    const int rq = tid / TPR;                  // query row converted by this thread (if < QB)
+    const int lrq = blockIdx.z * QB + rq;
+    const bool qok = rq < QB && lrq < LR;
+    const int lrc = qok ? lrq : 0;
+    float4 qv[4];
+    {
+        const float* src = a.q + ((int64_t)(lrc / G) * a.H + kh * G + lrc % G) * D + sub * 16;
+#pragma unroll
+        for (int i = 0; i < 4; i++) qv[i] = ((const float4*)src)[i];
+    }
+    uint4 kv[KP][2];
+#pragma unroll
+    for (int p = 0; p < KP; p++) {
+        const int r = rq + p * RPP, rc = r < nj ? r : nj - 1;
+        const uint16_t* src = a.kc + (j0 + rc) * (int64_t)a.Hkv * D + (int64_t)kh * D + sub * 16;
+        kv[p][0] = *(const uint4*)src;
+        kv[p][1] = *(const uint4*)(src + 8);
+    }
     // ---- query rows lr = blockIdx.z * 32 + r: token t = lr / G, head kh * G + lr % G
-    for (int r = tid / TPR; r < QB; r += RPP) {
-        const int lr = blockIdx.z * QB + r;
+    if (rq < QB) {
         float v[16];
-        if (lr < LR) {
-            const int t = lr / G, h = kh * G + lr % G;
-            const float* src = a.q + ((int64_t)t * a.H + h) * D + sub * 16;
 #pragma unroll
-            for (int i = 0; i < 16; i++) v[i] = cpv_h2f(cpv_f2h(src[i]));
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; i++) v[i] = 0.0f;
+        for (int i = 0; i < 4; i++) {
+            v[4 * i + 0] = qok ? cpv_h2f(cpv_f2h(qv[i].x)) : 0.0f;
+            v[4 * i + 1] = qok ? cpv_h2f(cpv_f2h(qv[i].y)) : 0.0f;
+            v[4 * i + 2] = qok ? cpv_h2f(cpv_f2h(qv[i].z)) : 0.0f;
+            v[4 * i + 3] = qok ? cpv_h2f(cpv_f2h(qv[i].w)) : 0.0f;
         }
         int8_t hi[16], lo[16];
         const int e = row_limbs<TPR>(v, hi, lo);
-        store16(&s_qh[r][sub * 16], hi);
-        store16(&s_ql[r][sub * 16], lo);
+        store16(&s_qh[rq][sub * 16], hi);
+        store16(&s_ql[rq][sub * 16], lo);
         if (sub == 0) {
-            s_eq[r] = e;
-            s_anc[r] = (tree && lr < LR) ? ancestors(a.parent, lr / G) : 0ull;
+            s_eq[rq] = e;
+            s_anc[rq] = (tree && qok) ? ancestors(a.parent, lrq / G) : 0ull;
         }
     }
     // ---- the chunk's cache rows of this KV head
-    for (int r = tid / TPR; r < CHUNK; r += RPP) {
-        float v[16];
-        if (r < nj) {
-            const uint16_t* src = a.kc + (j0 + r) * (int64_t)a.Hkv * D + (int64_t)kh * D + sub * 16;
-            const uint4 p0 = *(const uint4*)src, p1 = *(const uint4*)(src + 8);
-            const uint32_t wds[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+    for (int p = 0; p < KP; p++) {
+        const int r = rq + p * RPP;
+        if (r >= CHUNK) break;                 // (threads past the chunk when d = 64)
+        const uint32_t wds[8] = {kv[p][0].x, kv[p][0].y, kv[p][0].z, kv[p][0].w,
+                                 kv[p][1].x, kv[p][1].y, kv[p][1].z, kv[p][1].w};
+        int8_t hi[16], lo[16];
+        int e = E_EMPTY;
+        if (r < nj) {                          // the same for the TPR lanes of a row
+            float v[16];
 #pragma unroll
             for (int i = 0; i < 16; i++) v[i] = cpv_h2f((uint16_t)(wds[i >> 1] >> (16 * (i & 1))));
-        } else {
+            e = row_limbs<TPR>(v, hi, lo);
+        } else {                               // what row_limbs gives an all-zero row
 #pragma unroll
-            for (int i = 0; i < 16; i++) v[i] = 0.0f;
+            for (int i = 0; i < 16; i++) hi[i] = lo[i] = 0;
         }
-        int8_t hi[16], lo[16];
-        const int e = row_limbs<TPR>(v, hi, lo);
         store16(&s_kh[r][sub * 16], hi);
         store16(&s_kl[r][sub * 16], lo);
         if (sub == 0) s_ek[r] = e;
     }
+    // ---- the first V groups of this thread's P_c lane (d, chunk rows 8g..8g+7),
+    // in flight through the scores and the softmax; the loop below keeps four
+    // groups ahead.  Groups past the chunk's end re-read its last group.
+    constexpr int WPR = D / 64;                // waves per 8-row group of P_c
+    const int dv = (wave % WPR) * 64 + lane;
+    const uint16_t* vrow = a.vt + ((int64_t)kh * D + dv) * a.v_stride + j0;
+    const int gl = (nj - 1) >> 3;
+    uint4 vq0 = *(const uint4*)(vrow + 8 * min(0, gl)), vq1 = *(const uint4*)(vrow + 8 * min(1, gl)),
+          vq2 = *(const uint4*)(vrow + 8 * min(2, gl)), vq3 = *(const uint4*)(vrow + 8 * min(3, gl));
     __syncthreads();
 
     // ---- scores: 2 x 8 blocks of 16 x 16 (query rows x cache rows), 2 per wave
@@ -184,6 +221,7 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
         const int ar = qb * 16 + (lane & 15), bc = jb * 16 + (lane & 15), kg = (lane >> 4) * 16;
 #pragma unroll
         for (int ks = 0; ks < D / 64; ks++) {
+            if (jb * 16 >= nj) break;          // a block past the chunk's end: every score is -inf
             const v4i qhv = *(const v4i*)&s_qh[ar][ks * 64 + kg], qlv = *(const v4i*)&s_ql[ar][ks * 64 + kg];
             const v4i khv = *(const v4i*)&s_kh[bc][ks * 64 + kg], klv = *(const v4i*)&s_kl[bc][ks * 64 + kg];
             hh = __builtin_amdgcn_mfma_i32_16x16x64_i8(qhv, khv, hh, 0, 0, 0);
@@ -212,28 +250,29 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     }
     __syncthreads();
 
-    // ---- the chunk's softmax: 16 threads per query row, 8 cache rows each
+    // ---- the chunk's softmax: SPR threads per query row, EPT cache rows each
     {
-        const int r = tid >> 4, part = tid & 15;
+        constexpr int SPR = CT / QB, EPT = CHUNK / SPR;
+        const int r = tid / SPR, part = tid % SPR;
         const int lr = blockIdx.z * QB + r;
         float m = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 8; i++) m = fmaxf(m, s_w[r][part * 8 + i]);
-        for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+        for (int i = 0; i < EPT; i++) m = fmaxf(m, s_w[r][part * EPT + i]);
+        for (int off = 1; off < SPR; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
         long long z = 0;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int jl = part * 8 + i;
+        for (int i = 0; i < EPT; i++) {
+            const int jl = part * EPT + i;
             const float w = s_w[r][jl];
             float p = 0.0f;
             if (w != -INFINITY) {
-                const float e = cpv_expf(w - m);
+                const float e = cpv_expf_t(w - m, s_etab);
                 p = cpv_h2f(cpv_f2h(e));
                 z += (long long)rint(ldexp((double)e, ZBITS));
             }
             s_pt[jl][r] = p;
         }
-        for (int off = 1; off < 16; off <<= 1) z += __shfl_xor(z, off);
+        for (int off = 1; off < SPR; off <<= 1) z += __shfl_xor(z, off);
         if (part == 0 && lr < LR) {
             const int t = lr / G, h = kh * G + lr % G;
             const int64_t row = (int64_t)c * a.T * a.H + (int64_t)t * a.H + h;
@@ -243,42 +282,76 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     }
     __syncthreads();
 
-    // ---- P_c: 8 query rows x 64 d per wave (lane = d), fma chain over the chunk's rows in order
-    constexpr int WPR = D / 64;                // waves per 8-row group
-    for (int g8 = wave / WPR; g8 < QB / 8; g8 += (CT / 64) / WPR) {
-        const int r0 = g8 * 8;
-        if (blockIdx.z * QB + r0 >= LR) break;
-        const int d = (wave % WPR) * 64 + lane;
-        const uint16_t* vrow = a.vt + ((int64_t)kh * D + d) * a.v_stride + j0;
-        float acc[8];
+    // ---- P_c: RPW query rows x 64 d per wave (lane = d), fma chain over the
+    // chunk's rows in order.  In the last group, rows past the chunk's end have
+    // p = 0 (their score is -inf) and get v = 0, so they add exact zeros and
+    // leave the chain as it is over the chunk's own rows; later groups are
+    // skipped.
+    constexpr int RPW = QB * WPR * 64 / CT;    // query rows per wave
+    static_assert(RPW == 2 || RPW == 4 || RPW == 8, "P_c rows per wave");
+    const int r0 = (wave / WPR) * RPW;
+    if (blockIdx.z * QB + r0 < LR) {
+        float acc[RPW];
 #pragma unroll
-        for (int i = 0; i < 8; i++) acc[i] = 0.0f;
-        int jl = 0;
-        for (; jl + 8 <= nj; jl += 8) {
-            const uint4 vv = *(const uint4*)(vrow + jl);
-            const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+        for (int i = 0; i < RPW; i++) acc[i] = 0.0f;
+        // rows 8g..8g+7 with their v in vw
+        auto rows8 = [&](int g, uint4 vq) {
+            uint32_t vw[4] = {vq.x, vq.y, vq.z, vq.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int j = 8 * g + 2 * k;
+                vw[k] = j + 1 < nj ? vw[k] : (j < nj ? (vw[k] & 0xffffu) : 0u);
+            }
 #pragma unroll
             for (int jj = 0; jj < 8; jj++) {
+                const int jl = 8 * g + jj;
                 const float v = cpv_h2f((uint16_t)(vw[jj >> 1] >> (16 * (jj & 1))));
-                const float4 p0 = *(const float4*)&s_pt[jl + jj][r0], p1 = *(const float4*)&s_pt[jl + jj][r0 + 4];
-                const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                float pv[RPW];
+                if constexpr (RPW == 2) {
+                    const float2 p0 = *(const float2*)&s_pt[jl][r0];
+                    pv[0] = p0.x;
+                    pv[1] = p0.y;
+                } else {
 #pragma unroll
-                for (int i = 0; i < 8; i++) acc[i] = fmaf(pv[i], v, acc[i]);
+                    for (int i = 0; i < RPW; i += 4) {
+                        const float4 p0 = *(const float4*)&s_pt[jl][r0 + i];
+                        pv[i] = p0.x;
+                        pv[i + 1] = p0.y;
+                        pv[i + 2] = p0.z;
+                        pv[i + 3] = p0.w;
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < RPW; i++) acc[i] = fmaf(pv[i], v, acc[i]);
             }
-        }
-        for (; jl < nj; jl++) {
-            const float v = cpv_h2f(vrow[jl]);
-            const float4 p0 = *(const float4*)&s_pt[jl][r0], p1 = *(const float4*)&s_pt[jl][r0 + 4];
-            const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        };
+        if (nj == CHUNK) {
+            // a whole chunk: each group's registers then take the group four ahead
+            auto group = [&](int g, uint4& vq) {
+                const uint4 cur = vq;
+                vq = *(const uint4*)(vrow + 8 * min(g + 4, gl));
+                rows8(g, cur);
+            };
 #pragma unroll
-            for (int i = 0; i < 8; i++) acc[i] = fmaf(pv[i], v, acc[i]);
+            for (int g = 0; g < CHUNK / 8; g += 4) {
+                group(g, vq0);
+                group(g + 1, vq1);
+                group(g + 2, vq2);
+                group(g + 3, vq3);
+            }
+        } else {
+            // the short last chunk: its groups only
+            for (int g = 0; g <= gl; g++) rows8(g, *(const uint4*)(vrow + 8 * g));
         }
+        // finish every chain here (otherwise they are sunk into the stores below)
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
+        for (int i = 0; i < RPW; i++) asm volatile("" : "+v"(acc[i]));
+#pragma unroll
+        for (int i = 0; i < RPW; i++) {
             const int lr = blockIdx.z * QB + r0 + i;
             if (lr >= LR) break;
             const int t = lr / G, h = kh * G + lr % G;
-            a.P[(((int64_t)c * a.T + t) * a.H + h) * D + d] = acc[i];
+            a.P[(((int64_t)c * a.T + t) * a.H + h) * D + dv] = acc[i];
         }
     }
 }
@@ -367,7 +440,7 @@ cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const ui
     ca.H = H;
     ca.Hkv = Hkv;
     ca.scale = scale;
-    attn_chunk_kernel<D><<<dim3((unsigned)nchunk, (unsigned)Hkv, (unsigned)((LR + QB - 1) / QB)), CT, 0,
+    attn_chunk_kernel<D><<<dim3((unsigned)(nchunk * Hkv), 1u, (unsigned)((LR + QB - 1) / QB)), CT, 0,
                            ctx->stream>>>(ca);
     if (out)
         attn_fold_kernel<D><<<(unsigned)rows, D, (size_t)nchunk * 12, ctx->stream>>>(ca.P, ca.mc, ca.zc, nchunk,

@@ -105,24 +105,26 @@ __host__ __device__ __forceinline__ uint16_t cpv_f2h(float f)
     return (uint16_t)(sign | r);
 }
 
+// 2^(i/32) in binary64, stored minus i << 47
+#define CPV_EXP2F_TAB { \
+        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull, \
+        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull, \
+        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull, \
+        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull, \
+        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull, \
+        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull, \
+        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull, \
+        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull }
+
 // expf evaluated as glibc (>= 2.27) evaluates it, which is the libm expf the
 // reference's Rust f32::exp calls: k = round(x * 32/ln2), e^x = 2^(k/32) * p(r)
 // with a 32-entry table of 2^(i/32) (stored minus i<<47) and the published
 // cubic, in binary64 with fused multiply-adds, rounded once to f32.  Used
 // wherever the reference applies exp on the verify path (sigmoid, SiLU, the
-// sampler), so results match the CPU bit for bit.
-__host__ __device__ __forceinline__ float cpv_expf(float x)
+// sampler), so results match the CPU bit for bit.  cpv_expf_t takes the table
+// from the caller (a copy in LDS keeps global loads out of a kernel's phase).
+__host__ __device__ __forceinline__ float cpv_expf_t(float x, const uint64_t* tab)
 {
-    constexpr uint64_t tab[32] = {
-        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
-        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
-        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
-        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
-        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
-        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
-        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
-        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
-    };
     if (x != x) return x + x;
     if (x > 0x1.62e42ep6f) return __builtin_huge_valf();
     if (x < -0x1.9fe368p6f) return 0.0f;
@@ -141,6 +143,11 @@ __host__ __device__ __forceinline__ float cpv_expf(float x)
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     return (float)(y * s);
+}
+__host__ __device__ __forceinline__ float cpv_expf(float x)
+{
+    constexpr uint64_t tab[32] = CPV_EXP2F_TAB;
+    return cpv_expf_t(x, tab);
 }
 
 // quantized activations shared by every GEMM that reads the same input
