@@ -150,6 +150,64 @@ __host__ __device__ __forceinline__ float cpv_expf(float x)
     return cpv_expf_t(x, tab);
 }
 
+// ---- reductions across lanes through DPP row permutations (no LDS round
+// trip, unlike a shuffle).  Every lane of the wave must be active.  The
+// operations used with them (max, integer sums, a strict total order) give
+// the same result in any order.
+//   XOR1 = quad_perm [1,0,3,2], XOR2 = quad_perm [2,3,0,1]: lane ^ 1, lane ^ 2;
+//   HMIRROR = row_half_mirror (i <-> 7 - i in 8 lanes), MIRROR = row_mirror
+//   (i <-> 15 - i in 16): once the quads (eights) agree on a value, each pairs
+//   them with the other quad (eight) of the group.
+enum { CPV_DPP_XOR1 = 0xb1, CPV_DPP_XOR2 = 0x4e, CPV_DPP_MIRROR = 0x140, CPV_DPP_HMIRROR = 0x141 };
+
+template <int C>
+__device__ __forceinline__ int cpv_dpp(int v)
+{
+    return __builtin_amdgcn_update_dpp(0, v, C, 0xf, 0xf, false);
+}
+template <int C>
+__device__ __forceinline__ float cpv_dpp(float v)
+{
+    return __builtin_bit_cast(float, cpv_dpp<C>(__builtin_bit_cast(int, v)));
+}
+template <int C>
+__device__ __forceinline__ long long cpv_dpp(long long v)
+{
+    const int lo = cpv_dpp<C>((int)(uint32_t)v), hi = cpv_dpp<C>((int)(v >> 32));
+    return (long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+__device__ __forceinline__ int cpv_readlane(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ float cpv_readlane(float v, int l)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ __forceinline__ long long cpv_readlane(long long v, int l)
+{
+    const int lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l), hi = __builtin_amdgcn_readlane((int)(v >> 32), l);
+    return (long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+// op over each group of N consecutive lanes (N = 2, 4, 8, 16), in every lane of the group
+template <int N, class T, class Op>
+__device__ __forceinline__ T cpv_group_reduce(T v, Op op)
+{
+    static_assert(N == 2 || N == 4 || N == 8 || N == 16, "group of 2, 4, 8 or 16 lanes");
+    v = op(v, cpv_dpp<CPV_DPP_XOR1>(v));
+    if constexpr (N >= 4) v = op(v, cpv_dpp<CPV_DPP_XOR2>(v));
+    if constexpr (N >= 8) v = op(v, cpv_dpp<CPV_DPP_HMIRROR>(v));
+    if constexpr (N >= 16) v = op(v, cpv_dpp<CPV_DPP_MIRROR>(v));
+    return v;
+}
+// op over the whole wave (a wave-uniform value)
+template <class T, class Op>
+__device__ __forceinline__ T cpv_wave_reduce(T v, Op op)
+{
+    v = cpv_group_reduce<16>(v, op);
+    return op(op(cpv_readlane(v, 0), cpv_readlane(v, 16)), op(cpv_readlane(v, 32), cpv_readlane(v, 48)));
+}
+struct cpv_op_max { __device__ float operator()(float a, float b) const { return fmaxf(a, b); } };
+struct cpv_op_add { template <class T> __device__ T operator()(T a, T b) const { return a + b; } };
+
 // quantized activations shared by every GEMM that reads the same input
 struct cpv_act {
     const int8_t* qa;        // [m][U*256] codes

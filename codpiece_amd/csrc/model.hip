@@ -62,7 +62,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__
     } else {
         for (int i = tid; i < n; i += blockDim.x) am = fmaxf(am, fabsf(xr[i]));
     }
-    for (int off = 32; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));
+    am = cpv_wave_reduce(am, cpv_op_max());
     if (lane == 0) s_max[wave] = am;
     __syncthreads();
     am = s_max[0];
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__
                 S += cpv_fixed_floor(sq, g);
             }
         }
-        for (int off = 32; off > 0; off >>= 1) S += __shfl_xor(S, off);
+        S = cpv_wave_reduce(S, cpv_op_add());
         if (lane == 0) s_sum[wave] = S;
         __syncthreads();
         S = 0;
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(128) void qk_prep_kernel(PrepArgs a)
     const float x = src[i];
     // rms over the head (n = hd <= 128: two waves at most)
     float am = fabsf(x);
-    for (int off = 32; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));
+    am = cpv_wave_reduce(am, cpv_op_max());
     if ((i & 63) == 0) s_am[i >> 6] = am;
     __syncthreads();
     am = s_am[0];
@@ -152,7 +152,7 @@ __global__ __launch_bounds__(128) void qk_prep_kernel(PrepArgs a)
         frexpf(am, &e);
         const int g = 2 * e - (62 - ceil_log2_dev(a.hd + 1));
         long long S = cpv_fixed_floor(x * x, g);
-        for (int off = 32; off > 0; off >>= 1) S += __shfl_xor(S, off);
+        S = cpv_wave_reduce(S, cpv_op_add());
         if ((i & 63) == 0) s_s[i >> 6] = S;
         __syncthreads();
         S = s_s[0] + (a.hd > 64 ? s_s[1] : 0);
@@ -260,32 +260,62 @@ struct RowArgs {
     cpv_act act;
 };
 
+// the signed element of largest magnitude over the wave, the lowest index
+// among equal magnitudes (a strict order, so any reduction order agrees);
+// every lane ends with it
+__device__ __forceinline__ void amax_take(float& ax, int& ix, float& sx, float oa, int oi, float os)
+{
+    if (oa > ax || (oa == ax && oi < ix)) {
+        ax = oa;
+        ix = oi;
+        sx = os;
+    }
+}
+template <int C>
+__device__ __forceinline__ void amax_dpp(float& ax, int& ix, float& sx)
+{
+    amax_take(ax, ix, sx, cpv_dpp<C>(ax), cpv_dpp<C>(ix), cpv_dpp<C>(sx));
+}
+__device__ __forceinline__ void wave_amax(float& ax, int& ix, float& sx)
+{
+    amax_dpp<CPV_DPP_XOR1>(ax, ix, sx);
+    amax_dpp<CPV_DPP_XOR2>(ax, ix, sx);
+    amax_dpp<CPV_DPP_HMIRROR>(ax, ix, sx);
+    amax_dpp<CPV_DPP_MIRROR>(ax, ix, sx);
+    float a0 = cpv_readlane(ax, 0), s0 = cpv_readlane(sx, 0);
+    int i0 = cpv_readlane(ix, 0);
+#pragma unroll
+    for (int l = 16; l < 64; l += 16) amax_take(a0, i0, s0, cpv_readlane(ax, l), cpv_readlane(ix, l), cpv_readlane(sx, l));
+    ax = a0;
+    ix = i0;
+    sx = s0;
+}
+
+// each block-wide reduction has its own LDS slots, so one barrier suffices
 struct RowLds {
-    float red_f[RW];
-    long long red_l[RW];
+    float red_ea[RW], red_am[RW];
+    long long red_s[RW];
 };
 
-__device__ float row_max(float v, RowLds& L)
+__device__ float row_max(float v, float* slot)
 {
     const int tid = threadIdx.x;
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    v = cpv_wave_reduce(v, cpv_op_max());
+    if ((tid & 63) == 0) slot[tid >> 6] = v;
     __syncthreads();
-    if ((tid & 63) == 0) L.red_f[tid >> 6] = v;
-    __syncthreads();
-    float r = L.red_f[0];
-    for (int i = 1; i < RW; i++) r = fmaxf(r, L.red_f[i]);
+    float r = slot[0];
+    for (int i = 1; i < RW; i++) r = fmaxf(r, slot[i]);
     return r;
 }
 
-__device__ long long row_sum(long long v, RowLds& L)
+__device__ long long row_sum(long long v, long long* slot)
 {
     const int tid = threadIdx.x;
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    __syncthreads();
-    if ((tid & 63) == 0) L.red_l[tid >> 6] = v;
+    v = cpv_wave_reduce(v, cpv_op_add());
+    if ((tid & 63) == 0) slot[tid >> 6] = v;
     __syncthreads();
     long long r = 0;
-    for (int i = 0; i < RW; i++) r += L.red_l[i];
+    for (int i = 0; i < RW; i++) r += slot[i];
     return r;
 }
 
@@ -358,7 +388,7 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
         float mx = fabsf(dar[tid < a.g.nda ? tid : 0]);
         if (tid >= a.g.nda) mx = 0.0f;
         for (int i = tid + RB; i < a.g.nda; i += RB) mx = fmaxf(mx, fabsf(dar[i]));
-        const int ea = cpv_exp_of_max(row_max(mx, L));
+        const int ea = cpv_exp_of_max(row_max(mx, L.red_ea));
 #pragma unroll
         for (int j = 0; j < RQ; j++) {
             const float gv = cpv_gout_value(S[j], ew[j], ea, a.g.win);
@@ -382,7 +412,7 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
         float am = 0.0f;
 #pragma unroll
         for (int j = 0; j < RQ; j++) am = fmaxf(am, fabsf(v[j]));
-        am = row_max(am, L);
+        am = row_max(am, L.red_am);
         double sum = 0.0;
         if (am > 0.0f) {
             int e;
@@ -391,7 +421,7 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
             long long S = 0;
 #pragma unroll
             for (int j = 0; j < RQ; j++) S += cpv_fixed_floor(v[j] * v[j], g2);
-            sum = ldexp((double)row_sum(S, L), g2);
+            sum = ldexp((double)row_sum(S, L.red_s), g2);
         }
         const float mean = (float)(sum / (double)n);
         const float scale = 1.0f / sqrtf(mean + a.eps);
@@ -432,12 +462,7 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
 #pragma unroll
             for (int k = 1; k < 4; k++)
                 if (fabsf(x[k]) > ax) { ax = fabsf(x[k]); ix = 4 * lane + k; sx = x[k]; }
-            for (int off = 32; off > 0; off >>= 1) {
-                const float oa = __shfl_xor(ax, off);
-                const int oi = __shfl_xor(ix, off);
-                const float os = __shfl_xor(sx, off);
-                if (oa > ax || (oa == ax && oi < ix)) { ax = oa; ix = oi; sx = os; }
-            }
+            wave_amax(ax, ix, sx);
             float d = 0.0f;
             if (ax > 0.0f) {
                 const float iscale = -127.0f / sx;
@@ -454,17 +479,15 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
             *qw = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
                   ((uint32_t)(q[3] & 0xff) << 24);
             // code sums of 16 (4 lanes) and 32 (8 lanes) elements
-            int s16 = q[0] + q[1] + q[2] + q[3];
-            s16 += __shfl_xor(s16, 1);
-            s16 += __shfl_xor(s16, 2);
-            const int s32 = s16 + __shfl_xor(s16, 4);
+            const int s16 = cpv_group_reduce<4>(q[0] + q[1] + q[2] + q[3], cpv_op_add());
+            const int s32 = s16 + cpv_dpp<CPV_DPP_HMIRROR>(s16);
             if ((lane & 3) == 0) bs16[((int64_t)m * U + u) * 16 + (lane >> 2)] = s16;
             if ((lane & 7) == 0) bs32[((int64_t)m * U + u) * 8 + (lane >> 3)] = s32;
             if (lane == 0) da[(int64_t)m * U + u] = d;
         } else {
             // Q8_0 per 32-element block (8 lanes): d = amax/127, q = roundf(x * (1/d)), d kept as fp16
             float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
-            for (int off = 4; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+            amax = cpv_group_reduce<8>(amax, cpv_op_max());
             const float d = amax / 127.0f;
             const float id = d != 0.0f ? 1.0f / d : 0.0f;
 #pragma unroll
@@ -507,7 +530,7 @@ __global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
             s_z[lh][c] = ldexp((double)a.part.zc[(int64_t)c * rows + rr], -a.part.zbits);
             M = fmaxf(M, mc);
         }
-        for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+        M = cpv_wave_reduce(M, cpv_op_max());
         if (lane == 0) s_m[lh][wave - lh * wph] = M;
         __syncthreads();
         M = s_m[lh][0];
@@ -550,7 +573,7 @@ __global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
         const int e0 = a.g.ew[ec], e1 = a.g.ew[n + ec];
         float mx = 0.0f;
         for (int i = t; i < a.g.nda; i += 256) mx = fmaxf(mx, fabsf(a.g.da[(int64_t)m * a.g.nda + i]));
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        mx = cpv_wave_reduce(mx, cpv_op_max());
         if (lane == 0) s_ax[wave] = mx;
         __syncthreads();
         mx = fmaxf(fmaxf(s_ax[0], s_ax[1]), fmaxf(s_ax[2], s_ax[3]));
@@ -573,11 +596,7 @@ __global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
         // iscale = -127/max, q = min(127, rint(iscale * x)), d = 1/iscale, code sums
         float ax = fabsf(val), sx = val;
         int ix = t;
-        for (int off = 32; off > 0; off >>= 1) {
-            const float oa = __shfl_xor(ax, off), os = __shfl_xor(sx, off);
-            const int oi = __shfl_xor(ix, off);
-            if (oa > ax || (oa == ax && oi < ix)) { ax = oa; ix = oi; sx = os; }
-        }
+        wave_amax(ax, ix, sx);
         if (lane == 0) { s_ax[wave] = ax; s_ix[wave] = ix; s_sx[wave] = sx; }
         __syncthreads();
         ax = s_ax[0];
@@ -594,8 +613,7 @@ __global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
             d = 1.0f / iscale;
         }
         qa[(int64_t)m * Kp + e] = (int8_t)q;
-        int s16 = q;
-        for (int off = 8; off > 0; off >>= 1) s16 += __shfl_xor(s16, off);
+        const int s16 = cpv_group_reduce<16>(q, cpv_op_add());
         const int s32 = s16 + __shfl_xor(s16, 16);
         if ((t & 15) == 0) const_cast<int32_t*>(a.act.bs16)[((int64_t)m * U + u) * 16 + (t >> 4)] = s16;
         if ((t & 31) == 0) const_cast<int32_t*>(a.act.bs32)[((int64_t)m * U + u) * 8 + (t >> 5)] = s32;
@@ -603,7 +621,8 @@ __global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
     } else {
         // Q8_0 per 32-element block: d = amax/127, q = roundf(x * (1/d)), d kept as fp16
         float amax = fabsf(val);
-        for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+        amax = cpv_group_reduce<16>(amax, cpv_op_max());
+        amax = fmaxf(amax, __shfl_xor(amax, 16));
         const float d = amax / 127.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         qa[(int64_t)m * Kp + e] = (int8_t)(int)roundf(val * id);
@@ -632,7 +651,7 @@ __global__ __launch_bounds__(128) void qk_prep_kept_kernel(PrepKeptArgs ka)
     // Ea of this token's activation row
     float mx = 0.0f;
     for (int c = i; c < ka.g.nda; c += a.hd) mx = fmaxf(mx, fabsf(ka.g.da[(int64_t)t * ka.g.nda + c]));
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    mx = cpv_wave_reduce(mx, cpv_op_max());
     if ((i & 63) == 0) s_am[i >> 6] = mx;
     __syncthreads();
     mx = s_am[0];
@@ -650,7 +669,7 @@ __global__ __launch_bounds__(128) void qk_prep_kept_kernel(PrepKeptArgs ka)
     }
     const float* w = is_q ? a.q_norm : a.k_norm;
     float am = fabsf(x);
-    for (int off = 32; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));
+    am = cpv_wave_reduce(am, cpv_op_max());
     if ((i & 63) == 0) s_am[i >> 6] = am;
     __syncthreads();
     am = s_am[0];
@@ -661,7 +680,7 @@ __global__ __launch_bounds__(128) void qk_prep_kept_kernel(PrepKeptArgs ka)
         frexpf(am, &e);
         const int g = 2 * e - (62 - ceil_log2_dev(a.hd + 1));
         long long S = cpv_fixed_floor(x * x, g);
-        for (int off = 32; off > 0; off >>= 1) S += __shfl_xor(S, off);
+        S = cpv_wave_reduce(S, cpv_op_add());
         if ((i & 63) == 0) s_s[i >> 6] = S;
         __syncthreads();
         S = s_s[0] + (a.hd > 64 ? s_s[1] : 0);
