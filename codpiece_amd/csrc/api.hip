@@ -592,10 +592,7 @@ __device__ __forceinline__ float am_value(unsigned long long key)
 
 __device__ unsigned long long block_max_u64(unsigned long long v, unsigned long long* s)
 {
-    for (int off = 32; off > 0; off >>= 1) {
-        const unsigned long long o = __shfl_xor(v, off);
-        v = o > v ? o : v;
-    }
+    v = cpv_wave_reduce(v, cpv_op_umax());
     const int tid = threadIdx.x, nw = blockDim.x >> 6;
     if ((tid & 63) == 0) s[tid >> 6] = v;
     __syncthreads();
@@ -628,11 +625,7 @@ __global__ __launch_bounds__(64) void argmax_fin_kernel(const unsigned long long
                                                         int32_t* __restrict__ out)
 {
     const int64_t row = blockIdx.x;
-    unsigned long long v = part[row * AM_NB + threadIdx.x];
-    for (int off = 32; off > 0; off >>= 1) {
-        const unsigned long long o = __shfl_xor(v, off);
-        v = o > v ? o : v;
-    }
+    const unsigned long long v = cpv_wave_reduce(part[row * AM_NB + threadIdx.x], cpv_op_umax());
     if (threadIdx.x == 0) out[row] = v ? (int32_t)(0xffffffffu - (uint32_t)v) : 0;
 }
 
@@ -645,11 +638,7 @@ __global__ __launch_bounds__(256) void peak_part_kernel(const float* __restrict_
     __shared__ double s_d[4];
     const int64_t row = blockIdx.y, i0 = (int64_t)blockIdx.x * chunk;
     const int64_t i1 = i0 + chunk < n ? i0 + chunk : n;
-    unsigned long long k = part[row * AM_NB + (threadIdx.x & 63)];
-    for (int off = 32; off > 0; off >>= 1) {
-        const unsigned long long o = __shfl_xor(k, off);
-        k = o > k ? o : k;
-    }
+    const unsigned long long k = cpv_wave_reduce(part[row * AM_NB + (threadIdx.x & 63)], cpv_op_umax());
     const float mx = k ? am_value(k) : -INFINITY;
     const float* xr = x + row * n;
     double sum = 0.0;

@@ -104,7 +104,7 @@ __device__ __forceinline__ int row_limbs(const float* v, int8_t* hi, int8_t* lo)
     float mx = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(v[i]));
-    for (int off = 1; off < TPR; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    mx = cpv_group_reduce<TPR>(mx, cpv_op_max());   // a row's lanes are all active or all idle
     int e = E_EMPTY;
     if (mx > 0.0f) frexpf(mx, &e);
 #pragma unroll
@@ -258,7 +258,7 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
         float m = -INFINITY;
 #pragma unroll
         for (int i = 0; i < EPT; i++) m = fmaxf(m, s_w[r][part * EPT + i]);
-        for (int off = 1; off < SPR; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+        m = cpv_group_reduce<SPR>(m, cpv_op_max());
         long long z = 0;
 #pragma unroll
         for (int i = 0; i < EPT; i++) {
@@ -272,7 +272,7 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
             }
             s_pt[jl][r] = p;
         }
-        for (int off = 1; off < SPR; off <<= 1) z += __shfl_xor(z, off);
+        z = cpv_group_reduce<SPR>(z, cpv_op_add());
         if (part == 0 && lr < LR) {
             const int t = lr / G, h = kh * G + lr % G;
             const int64_t row = (int64_t)c * a.T * a.H + (int64_t)t * a.H + h;
@@ -377,7 +377,7 @@ __global__ __launch_bounds__(D) void attn_fold_kernel(const float* __restrict__ 
         s_z[c] = ldexp((double)zc[(int64_t)c * rows + row], -ZBITS);
         M = fmaxf(M, m);
     }
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+    M = cpv_wave_reduce(M, cpv_op_max());
     if (lane == 0) s_red[wave] = M;
     __syncthreads();
     M = s_red[0];

@@ -176,6 +176,11 @@ __device__ __forceinline__ long long cpv_dpp(long long v)
     const int lo = cpv_dpp<C>((int)(uint32_t)v), hi = cpv_dpp<C>((int)(v >> 32));
     return (long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
 }
+template <int C>
+__device__ __forceinline__ unsigned long long cpv_dpp(unsigned long long v)
+{
+    return (unsigned long long)cpv_dpp<C>((long long)v);
+}
 __device__ __forceinline__ int cpv_readlane(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
 __device__ __forceinline__ float cpv_readlane(float v, int l)
 {
@@ -185,6 +190,11 @@ __device__ __forceinline__ long long cpv_readlane(long long v, int l)
 {
     const int lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l), hi = __builtin_amdgcn_readlane((int)(v >> 32), l);
     return (long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+__device__ __forceinline__ unsigned long long cpv_readlane(unsigned long long v, int l)
+{
+    return (unsigned long long)cpv_readlane((long long)v, l);
 }
 
 // op over each group of N consecutive lanes (N = 2, 4, 8, 16), in every lane of the group
@@ -206,7 +216,41 @@ __device__ __forceinline__ T cpv_wave_reduce(T v, Op op)
     return op(op(cpv_readlane(v, 0), cpv_readlane(v, 16)), op(cpv_readlane(v, 32), cpv_readlane(v, 48)));
 }
 struct cpv_op_max { __device__ float operator()(float a, float b) const { return fmaxf(a, b); } };
+struct cpv_op_umax {
+    __device__ unsigned long long operator()(unsigned long long a, unsigned long long b) const { return a > b ? a : b; }
+};
 struct cpv_op_add { template <class T> __device__ T operator()(T a, T b) const { return a + b; } };
+
+// the signed element of largest magnitude over the wave, the lowest index
+// among equal magnitudes (a strict order, so any reduction order agrees);
+// every lane ends with it
+__device__ __forceinline__ void cpv_amax_take(float& ax, int& ix, float& sx, float oa, int oi, float os)
+{
+    if (oa > ax || (oa == ax && oi < ix)) {
+        ax = oa;
+        ix = oi;
+        sx = os;
+    }
+}
+template <int C>
+__device__ __forceinline__ void cpv_amax_dpp(float& ax, int& ix, float& sx)
+{
+    cpv_amax_take(ax, ix, sx, cpv_dpp<C>(ax), cpv_dpp<C>(ix), cpv_dpp<C>(sx));
+}
+__device__ __forceinline__ void cpv_wave_amax(float& ax, int& ix, float& sx)
+{
+    cpv_amax_dpp<CPV_DPP_XOR1>(ax, ix, sx);
+    cpv_amax_dpp<CPV_DPP_XOR2>(ax, ix, sx);
+    cpv_amax_dpp<CPV_DPP_HMIRROR>(ax, ix, sx);
+    cpv_amax_dpp<CPV_DPP_MIRROR>(ax, ix, sx);
+    float a0 = cpv_readlane(ax, 0), s0 = cpv_readlane(sx, 0);
+    int i0 = cpv_readlane(ix, 0);
+#pragma unroll
+    for (int l = 16; l < 64; l += 16) cpv_amax_take(a0, i0, s0, cpv_readlane(ax, l), cpv_readlane(ix, l), cpv_readlane(sx, l));
+    ax = a0;
+    ix = i0;
+    sx = s0;
+}
 
 // quantized activations shared by every GEMM that reads the same input
 struct cpv_act {

@@ -260,37 +260,6 @@ struct RowArgs {
     cpv_act act;
 };
 
-// the signed element of largest magnitude over the wave, the lowest index
-// among equal magnitudes (a strict order, so any reduction order agrees);
-// every lane ends with it
-__device__ __forceinline__ void amax_take(float& ax, int& ix, float& sx, float oa, int oi, float os)
-{
-    if (oa > ax || (oa == ax && oi < ix)) {
-        ax = oa;
-        ix = oi;
-        sx = os;
-    }
-}
-template <int C>
-__device__ __forceinline__ void amax_dpp(float& ax, int& ix, float& sx)
-{
-    amax_take(ax, ix, sx, cpv_dpp<C>(ax), cpv_dpp<C>(ix), cpv_dpp<C>(sx));
-}
-__device__ __forceinline__ void wave_amax(float& ax, int& ix, float& sx)
-{
-    amax_dpp<CPV_DPP_XOR1>(ax, ix, sx);
-    amax_dpp<CPV_DPP_XOR2>(ax, ix, sx);
-    amax_dpp<CPV_DPP_HMIRROR>(ax, ix, sx);
-    amax_dpp<CPV_DPP_MIRROR>(ax, ix, sx);
-    float a0 = cpv_readlane(ax, 0), s0 = cpv_readlane(sx, 0);
-    int i0 = cpv_readlane(ix, 0);
-#pragma unroll
-    for (int l = 16; l < 64; l += 16) amax_take(a0, i0, s0, cpv_readlane(ax, l), cpv_readlane(ix, l), cpv_readlane(sx, l));
-    ax = a0;
-    ix = i0;
-    sx = s0;
-}
-
 // each block-wide reduction has its own LDS slots, so one barrier suffices
 struct RowLds {
     float red_ea[RW], red_am[RW];
@@ -462,7 +431,7 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
 #pragma unroll
             for (int k = 1; k < 4; k++)
                 if (fabsf(x[k]) > ax) { ax = fabsf(x[k]); ix = 4 * lane + k; sx = x[k]; }
-            wave_amax(ax, ix, sx);
+            cpv_wave_amax(ax, ix, sx);
             float d = 0.0f;
             if (ax > 0.0f) {
                 const float iscale = -127.0f / sx;
@@ -596,7 +565,7 @@ __global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
         // iscale = -127/max, q = min(127, rint(iscale * x)), d = 1/iscale, code sums
         float ax = fabsf(val), sx = val;
         int ix = t;
-        wave_amax(ax, ix, sx);
+        cpv_wave_amax(ax, ix, sx);
         if (lane == 0) { s_ax[wave] = ax; s_ix[wave] = ix; s_sx[wave] = sx; }
         __syncthreads();
         ax = s_ax[0];

@@ -57,13 +57,9 @@ __global__ __launch_bounds__(256) void quant_q8k_kernel(const float* __restrict_
     __shared__ float s_ax[4];
     __shared__ int s_ix[4];
     sx[t] = v;
-    float ax = fabsf(v);
+    float ax = fabsf(v), sv = v;
     int ix = t;
-    for (int off = 32; off > 0; off >>= 1) {
-        const float oa = __shfl_xor(ax, off);
-        const int oi = __shfl_xor(ix, off);
-        if (oa > ax || (oa == ax && oi < ix)) { ax = oa; ix = oi; }
-    }
+    cpv_wave_amax(ax, ix, sv);
     if ((t & 63) == 0) { s_ax[t >> 6] = ax; s_ix[t >> 6] = ix; }
     __syncthreads();
     float amax = s_ax[0];
@@ -80,9 +76,8 @@ __global__ __launch_bounds__(256) void quant_q8k_kernel(const float* __restrict_
     }
     const int64_t Kp = (int64_t)U * 256;
     qa[(int64_t)m * Kp + e] = (int8_t)q;
-    int s16 = q;
-    for (int off = 8; off > 0; off >>= 1) s16 += __shfl_xor(s16, off);
-    int s32 = s16 + __shfl_xor(s16, 16);
+    const int s16 = cpv_group_reduce<16>(q, cpv_op_add());
+    const int s32 = s16 + __shfl_xor(s16, 16);
     if ((t & 15) == 0) bs16[((int64_t)m * U + u) * 16 + (t >> 4)] = s16;
     if ((t & 31) == 0) bs32[((int64_t)m * U + u) * 8 + (t >> 5)] = s32;
     if (t == 0) da[(int64_t)m * U + u] = d;
@@ -97,7 +92,8 @@ __global__ __launch_bounds__(256) void quant_q80_kernel(const float* __restrict_
     const int64_t e = (int64_t)u * 256 + t;
     const float v = e < K ? x[(int64_t)m * K + e] : 0.0f;
     float amax = fabsf(v);
-    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    amax = cpv_group_reduce<16>(amax, cpv_op_max());
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
     const float d = amax / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
     const int q = (int)roundf(v * id);
@@ -424,7 +420,7 @@ __global__ __launch_bounds__((64 * gemm_waves<TYPE, MC>())) void qgemm_kernel(Ge
     if (wave < M) {
         float mx = fmaxf(lane < nrow ? fabsf(ev0) : 0.0f, lane + 64 < nrow ? fabsf(ev1) : 0.0f);
         for (int i = lane + 128; i < nrow; i += 64) mx = fmaxf(mx, fabsf(dr[i]));
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        mx = cpv_wave_reduce(mx, cpv_op_max());
         if (lane == 0) {
             int e = CPV_E_EMPTY;
             if (mx > 0.0f) frexpf(mx, &e);
@@ -504,7 +500,7 @@ __global__ __launch_bounds__(256) void qgemm_finalize_kernel(double* __restrict_
     __shared__ float s_mx[4];
     float mx = 0.0f;
     for (int i = tid; i < nda; i += 256) mx = fmaxf(mx, fabsf(da[(int64_t)(m0 + m) * nda + i]));
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    mx = cpv_wave_reduce(mx, cpv_op_max());
     if ((tid & 63) == 0) s_mx[tid >> 6] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(s_mx[0], s_mx[1]), fmaxf(s_mx[2], s_mx[3]));

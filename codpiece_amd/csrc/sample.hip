@@ -296,7 +296,7 @@ __device__ float block_max(X x_at, int n, Small* sm)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float m = -INFINITY;
     strided(n, x_at, [&](int, float v) { m = fmaxf(m, v); });
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    m = cpv_wave_reduce(m, cpv_op_max());
     __syncthreads();
     if (lane == 0) sm->wf[wave] = m;
     __syncthreads();
@@ -316,10 +316,9 @@ __device__ int block_argmax(X x_at, int n, int dflt, Small* sm)
     strided(n, x_at, [&](int i, float v) {
         if (v > best) { best = v; idx = i; }
     });
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ob = __shfl_xor(best, off, 64);
-        const int oi = __shfl_xor(idx, off, 64);
-        if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+    {
+        float unused = 0.0f;
+        cpv_wave_amax(best, idx, unused);   // (best, lowest index) is a strict order
     }
     __syncthreads();
     if (lane == 0) { sm->wf[wave] = best; sm->wi[wave] = idx; }
