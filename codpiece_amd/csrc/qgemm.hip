@@ -123,9 +123,34 @@ struct GemmArgs {
     double* gsum;          // [rows][n_pad] accumulator (absolute activation rows), zero between uses
     int64_t n_pad;
     int items;             // tiles * U (tile-major)
+    int iq, ir;            // items / grid and items % grid: workgroup b takes iq items, one more if b < ir
+    double rU;             // 1.0 / U
     int U, M, m0, win;
     int nu_max, nt_max;    // most units / tiles one workgroup's items touch
 };
+
+// q = a / d and *r = a % d for 0 <= a < 2^31 and 0 < d < 2^31, with rd the
+// binary64 1.0 / d: the estimate is off by at most one, then corrected (no
+// integer division, which the scalar unit would run for every wave)
+__device__ __forceinline__ int divmod_pos(int a, int d, double rd, int* r)
+{
+    int q = (int)((double)a * rd);
+    int rr = a - q * d;
+    if (rr < 0) { q--; rr += d; }
+    else if (rr >= d) { q++; rr -= d; }
+    *r = rr;
+    return q;
+}
+// the same for 0 <= a < 2^23 and 0 < d < 2^23, with rf an f32 estimate of 1 / d
+__device__ __forceinline__ int divmod_small(int a, int d, float rf, int* r)
+{
+    int q = (int)((float)a * rf);
+    int rr = a - q * d;
+    if (rr < 0) { q--; rr += d; }
+    else if (rr >= d) { q++; rr -= d; }
+    *r = rr;
+    return q;
+}
 
 // waves per workgroup (one workgroup per CU; 12 waves, where registers
 // allow 3 per SIMD, measured slower)
@@ -318,15 +343,17 @@ __global__ __launch_bounds__((64 * gemm_waves<TYPE, MC>())) void qgemm_kernel(Ge
     constexpr int NT = 64 * GEMM_WAVES;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int s_ea[16];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // (the wave index read as a scalar: the run's bounds and positions stay in SGPRs)
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int M = a.M, U = a.U;
     const int64_t Kp = (int64_t)U * 256;
 
     // this workgroup's items [I0, I1), their units us, us+1, ... (mod U) and tiles t0..
-    const int I0 = (int)((int64_t)blockIdx.x * a.items / gridDim.x);
-    const int I1 = (int)((int64_t)(blockIdx.x + 1) * a.items / gridDim.x);
-    const int us = I0 % U, nu = I1 - I0 < U ? I1 - I0 : U;
-    const int t0 = I0 / U, nt = I1 > I0 ? (I1 - 1) / U - t0 + 1 : 0;
+    const int b = blockIdx.x;
+    const int I0 = b * a.iq + (b < a.ir ? b : a.ir), I1 = I0 + a.iq + (b < a.ir ? 1 : 0);
+    int us, ul;
+    const int t0 = divmod_pos(I0, U, a.rU, &us), nu = I1 - I0 < U ? I1 - I0 : U;
+    const int nt = I1 > I0 ? divmod_pos(I1 - 1, U, a.rU, &ul) - t0 + 1 : 0;
     const int cstride = nu * 256 + 16;         // LDS bytes per activation row (+16: 4 rows, 4 bank groups)
     uint8_t* s_codes = smem;
     float* s_da = (float*)(smem + ((M * cstride + 15) & ~15));
@@ -338,36 +365,52 @@ __global__ __launch_bounds__((64 * gemm_waves<TYPE, MC>())) void qgemm_kernel(Ge
     const int n = I1 - I0;
     const int i0 = I0 + wave * n / GEMM_WAVES, i1 = I0 + (wave + 1) * n / GEMM_WAVES;
     const uint16_t* d6base = (const uint16_t*)(a.w + (a.n_pad / 64) * (int64_t)U * 13 * 1024);
-    auto load = [&](int it, v4i* pcu, uint16_t& d6, int& er) {
-        const int tile = it / U;
-        const v4i* src = (const v4i*)(a.w + (int64_t)it * F::PIECES * 1024 + lane * 16);
+    // an item with its tile and unit; step() moves to the next item of the run
+    // and stays on its last (a wave without items walks item 0)
+    struct Pos { int it, tile, u; };
+    const int ilast = i0 < i1 ? i1 - 1 : 0;
+    auto step = [&](Pos p) {
+        if (p.it < ilast) {
+            p.it++;
+            if (++p.u == U) { p.u = 0; p.tile++; }
+        }
+        return p;
+    };
+    auto load = [&](const Pos& p, v4i* pcu, uint16_t& d6, int& er) {
+        const v4i* src = (const v4i*)(a.w + (int64_t)p.it * F::PIECES * 1024 + lane * 16);
 #pragma unroll
-        for (int p = 0; p < F::PIECES; p++) pcu[p] = src[p * 64];
-        if (TYPE == CPV_Q6_K) d6 = d6base[(int64_t)it * 64 + lane];
-        er = a.ew[tile * 64 + lane];
+        for (int q = 0; q < F::PIECES; q++) pcu[q] = src[q * 64];
+        if (TYPE == CPV_Q6_K) d6 = d6base[(int64_t)p.it * 64 + lane];
+        er = a.ew[p.tile * 64 + lane];
     };
     // ---- staging: the first batch of activation loads goes out before any
     // weight load, so that it is not queued behind them; the LDS writes then
     // wait for these loads only
     constexpr int BC = 4, BD = 2, BB = 4;      // per thread: code pieces, scales, code sums
     const int ncode = M * nu * 16, nda = M * nu * F::DA, nbs = M * nu * F::BS;
+    constexpr int BS = F::BS > 0 ? F::BS : 1;   // (code sums are not staged without them)
+    const float rc = __builtin_amdgcn_rcpf((float)(nu * 16)), rd = __builtin_amdgcn_rcpf((float)(nu * F::DA)),
+                rb = __builtin_amdgcn_rcpf((float)(nu * BS));
     auto code_src = [&](int i) {
-        const int m = i / (nu * 16), c = i - m * (nu * 16), j = c >> 4;
+        int c;
+        const int m = divmod_small(i, nu * 16, rc, &c), j = c >> 4;
         const int u = us + j < U ? us + j : us + j - U;
         return (const v4i*)(a.qa + (int64_t)(a.m0 + m) * Kp + u * 256 + (c & 15) * 16);
     };
     auto code_dst = [&](int i) {
-        const int m = i / (nu * 16), c = i - m * (nu * 16);
+        int c;
+        const int m = divmod_small(i, nu * 16, rc, &c);
         return (v4i*)(s_codes + m * cstride + c * 16);
     };
     auto da_src = [&](int i) {
-        const int m = i / (nu * F::DA), c = i - m * (nu * F::DA), j = c / F::DA;
+        int c;
+        const int m = divmod_small(i, nu * F::DA, rd, &c), j = c / F::DA;
         const int u = us + j < U ? us + j : us + j - U;
         return a.da + ((int64_t)(a.m0 + m) * U + u) * F::DA + (c - j * F::DA);
     };
     auto bs_src = [&](int i) {
-        constexpr int BS = F::BS > 0 ? F::BS : 1;   // (not called without code sums)
-        const int m = i / (nu * BS), c = i - m * (nu * BS), j = c / BS;
+        int c;
+        const int m = divmod_small(i, nu * BS, rb, &c), j = c / BS;
         const int u = us + j < U ? us + j : us + j - U;
         return a.bs + ((int64_t)(a.m0 + m) * U + u) * BS + (c - j * BS);
     };
@@ -392,9 +435,13 @@ __global__ __launch_bounds__((64 * gemm_waves<TYPE, MC>())) void qgemm_kernel(Ge
     int eA = 0, eB = 0;
     // (unconditional: a wave without items, or with one, reloads a valid item;
     // branches here would make the compiler wait for every load at the join)
-    const int ia = i0 < i1 ? i0 : 0, ib = i0 + 1 < i1 ? i0 + 1 : ia;
-    load(ia, bufA, dA, eA);
-    load(ib, bufB, dB, eB);
+    Pos cur;
+    cur.it = i0 < i1 ? i0 : 0;
+    cur.tile = divmod_pos(cur.it, U, a.rU, &cur.u);
+    Pos nl = step(cur);
+    load(cur, bufA, dA, eA);
+    load(nl, bufB, dB, eB);
+    nl = step(nl);
 
 #pragma unroll
     for (int q = 0; q < BC; q++) {
@@ -449,7 +496,7 @@ __global__ __launch_bounds__((64 * gemm_waves<TYPE, MC>())) void qgemm_kernel(Ge
         double S[MC];
 #pragma unroll
         for (int m = 0; m < MC; m++) S[m] = 0.0;
-        int tile = i0 / U;
+        int tile = cur.tile;
         auto flush = [&]() {
             // partial sums of this tile's units into its LDS sums: exact, in any order
             double* acc = s_acc + ((tile - t0) * M) * 64 + lane;
@@ -461,26 +508,29 @@ __global__ __launch_bounds__((64 * gemm_waves<TYPE, MC>())) void qgemm_kernel(Ge
                 }
         };
         // the item's unit as an LDS slot
-        auto slot = [&](int it) {
-            const int u = it - (it / U) * U;
-            return u >= us ? u - us : u - us + U;
-        };
+        auto slot = [&](int u) { return u >= us ? u - us : u - us + U; };
         // loads are unconditional (past the run they reload its last item)
         for (int it = i0; it < i1; it += 2) {
-            if (it / U != tile) { flush(); tile = it / U; }
-            gemm_unit<TYPE, MC>(bufA, dA, eA, slot(it), M, nu, arow, mrow, sm, s_da, s_bs, S);
-            load(it + 2 < i1 ? it + 2 : i1 - 1, bufA, dA, eA);
+            if (cur.tile != tile) { flush(); tile = cur.tile; }
+            gemm_unit<TYPE, MC>(bufA, dA, eA, slot(cur.u), M, nu, arow, mrow, sm, s_da, s_bs, S);
+            load(nl, bufA, dA, eA);
+            nl = step(nl);
             if (it + 1 >= i1) break;
-            if ((it + 1) / U != tile) { flush(); tile = (it + 1) / U; }
-            gemm_unit<TYPE, MC>(bufB, dB, eB, slot(it + 1), M, nu, arow, mrow, sm, s_da, s_bs, S);
-            load(it + 3 < i1 ? it + 3 : i1 - 1, bufB, dB, eB);
+            cur = step(cur);
+            if (cur.tile != tile) { flush(); tile = cur.tile; }
+            gemm_unit<TYPE, MC>(bufB, dB, eB, slot(cur.u), M, nu, arow, mrow, sm, s_da, s_bs, S);
+            load(nl, bufB, dB, eB);
+            nl = step(nl);
+            cur = step(cur);
         }
         flush();
     }
     __syncthreads();
     // the tile sums: stored where this workgroup covers the whole tile, else added
+    const float rM = __builtin_amdgcn_rcpf((float)M);
     for (int i = tid; i < nt * M * 64; i += NT) {
-        const int t = i / (M * 64), r = i - t * (M * 64), m = r >> 6, l = r & 63;
+        int m;
+        const int t = divmod_small(i >> 6, M, rM, &m), l = i & 63;
         const int tile = t0 + t;
         double* g = a.gsum + (int64_t)(a.m0 + m) * a.n_pad + (int64_t)tile * 64 + l;
         if (tile * U >= I0 && (tile + 1) * U <= I1) *g = s_acc[i];
@@ -656,6 +706,9 @@ cpv_status cpv_qgemm_act(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, 
     if (tiles * U > INT32_MAX / 2)
         return cpv_fail(ctx, CPV_EUNSUPPORTED, "qgemm: %lld tiles of %d units", (long long)tiles, U);
     a.items = (int)(tiles * U);
+    a.iq = a.items / ctx->cu_count;
+    a.ir = a.items % ctx->cu_count;
+    a.rU = 1.0 / U;
     a.win = cpv_qgemm_window(w->type, w->k);
     {
         // one workgroup's items: at most ceil(items / CUs), spanning at most that
