@@ -333,6 +333,25 @@ def main():
         sess.set_pos(n_past, mtp_past)
     vo.sort()
 
+    # draft trees: the canonical 16-node tree (widths 4, 6, 3, 3) verified, then
+    # its deepest leftmost path committed; rewound afterwards
+    tree = [-1, -1, -1, -1, 0, 0, 0, 1, 1, 1, 4, 4, 4, 10, 10, 10]
+    ttoks = torch.randint(0, hp["n_vocab"], (len(tree),), generator=g).tolist()
+    tv, tc = [], []
+    for _ in range(max(3, args.steps // 4)):
+        a, b, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        a.record(stream)
+        sess.verify_tree(ttoks, tree)
+        b.record(stream)
+        sess.commit_branch([0, 4, 10, 13])
+        c.record(stream)
+        torch.cuda.synchronize()
+        tv.append(a.elapsed_time(b))
+        tc.append(b.elapsed_time(c))
+        sess.set_pos(n_past, mtp_past)
+    tv.sort()
+    tc.sort()
+
     # per-class kernel timing over extra rounds (events between launches: not in the timed region)
     ctx.profile_start()
     for _ in range(args.profile_rounds):
@@ -373,6 +392,8 @@ def main():
         "detail": {
             "round_device_us_median": round(dev_ms[len(dev_ms) // 2] * 1e3, 1),
             "verify_only_device_us_median": round(vo[len(vo) // 2] * 1e3, 1),
+            "tree_verify_16_device_us_median": round(tv[len(tv) // 2] * 1e3, 1),
+            "tree_commit_4_device_us_median": round(tc[len(tc) // 2] * 1e3, 1),
             "acceptance": round((loop.accepted - acc0) / max(1, loop.proposed - prop0), 4),
             "tokens_per_round": round(committed / args.steps, 3),
             "kernel_classes": {k: {"launches_per_round": v[0] / args.profile_rounds,

@@ -54,10 +54,17 @@ __device__ __forceinline__ bool visible(int64_t j, int64_t n_past, int t, bool t
     return tree ? ((anc >> node) & 1ull) != 0 : node <= t;
 }
 
+// node t and its ancestors; a link that does not point to an earlier node
+// ends the walk (so a malformed array cannot loop)
 __device__ __forceinline__ uint64_t ancestors(const int32_t* parent, int t)
 {
     uint64_t m = 0;
-    for (int a = t; a >= 0; a = parent[a]) m |= 1ull << a;
+    for (int a = t; a >= 0 && a < 64;) {
+        m |= 1ull << a;
+        const int p = parent[a];
+        if (p >= a) break;
+        a = p;
+    }
     return m;
 }
 
@@ -508,13 +515,15 @@ cpv_status cpv_attn_launch(cpv_ctx* ctx, const float* q, const uint16_t* kc, con
 }
 
 cpv_status cpv_attn_partials(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
-                             int64_t n_past, int t, int h, int h_kv, int d, float scale, cpv_attn_part* part)
+                             int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
+                             cpv_attn_part* part)
 {
-    if ((d != 64 && d != 128) || !(d == 128 ? attn_one_block<128>(n_past, t, h) : attn_one_block<64>(n_past, t, h)))
+    if ((d != 64 && d != 128) || (parent && t > 64) ||
+        !(d == 128 ? attn_one_block<128>(n_past, t, h) : attn_one_block<64>(n_past, t, h)))
         return CPV_EUNSUPPORTED;   // (no message: the caller takes the unfused path)
     auto go = [=]() {
-        return d == 128 ? attn_block<128>(ctx, q, kc, vt, v_stride, n_past, nullptr, t, h, h_kv, scale, nullptr, part)
-                        : attn_block<64>(ctx, q, kc, vt, v_stride, n_past, nullptr, t, h, h_kv, scale, nullptr, part);
+        return d == 128 ? attn_block<128>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, nullptr, part)
+                        : attn_block<64>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, nullptr, part);
     };
     const int ev = cpv_prof_mark(ctx);
     const cpv_status st = go();

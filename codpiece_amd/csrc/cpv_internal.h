@@ -337,4 +337,5 @@ struct cpv_attn_part {
     int zbits;            // zc holds Z_c 2^zbits
 };
 cpv_status cpv_attn_partials(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
-                             int64_t n_past, int t, int h, int h_kv, int d, float scale, cpv_attn_part* part);
+                             int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
+                             cpv_attn_part* part);

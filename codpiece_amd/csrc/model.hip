@@ -124,6 +124,7 @@ struct PrepArgs {
     uint16_t* v_cache_t;   // [Hkv*hd][v_stride]
     int64_t v_stride;
     int64_t rope_pos0, kv_row0;
+    const int32_t* pos_off;   // [T] position of token t = rope_pos0 + pos_off[t] (a tree's depths), or null: + t
     int H, Hkv, hd, n_rot, write;
     float eps;
 };
@@ -168,7 +169,7 @@ __global__ __launch_bounds__(128) void qk_prep_kernel(PrepArgs a)
     const int half = a.n_rot / 2;
     if (i < a.n_rot) {
         const int p = i < half ? i : i - half;
-        const float* cs = a.rope + (a.rope_pos0 + t) * a.n_rot + 2 * p;
+        const float* cs = a.rope + (a.rope_pos0 + (a.pos_off ? a.pos_off[t] : t)) * a.n_rot + 2 * p;
         const float c = cs[0], s = cs[1];
         const float x0 = s_v[p], x1 = s_v[p + half];
         if (i < half) {
@@ -665,7 +666,7 @@ __global__ __launch_bounds__(128) void qk_prep_kept_kernel(PrepKeptArgs ka)
     const int half = a.n_rot / 2;
     if (i < a.n_rot) {
         const int p = i < half ? i : i - half;
-        const float* cs = a.rope + (a.rope_pos0 + t) * a.n_rot + 2 * p;
+        const float* cs = a.rope + (a.rope_pos0 + (a.pos_off ? a.pos_off[t] : t)) * a.n_rot + 2 * p;
         const float c = cs[0], sn = cs[1];
         const float x0 = s_v[p], x1 = s_v[p + half];
         if (i < half) {
@@ -729,6 +730,10 @@ struct cpv_session {
     size_t actbuf_bytes;
     float* tap = nullptr;                 // attention outputs of each call, when set
     int64_t tap_cap = 0, tap_off = 0;
+    int32_t* tree_dev = nullptr;          // the last tree verify: parent [64], then depth [64]
+    uint16_t** caches_dev = nullptr;      // the trunk's K caches [n_layer], then its V caches [n_layer]
+    std::vector<int32_t> tree_parent;     // (host copy, to check a committed path)
+    int64_t tree_base = -1;               // n_past before that verify; -1 when no tree is pending
     std::vector<void*> allocs;
 };
 
@@ -974,6 +979,18 @@ extern "C" cpv_status cpv_session_create(cpv_model* m, int64_t n_ctx, int32_t ma
     A((size_t)T * 4, (void**)&s->preds);
     A((size_t)16 * T * 4, (void**)&s->chain);
     A((size_t)16 * T * 4, (void**)&s->conf);
+    A((size_t)2 * CPV_TREE_MAX * 4, (void**)&s->tree_dev);
+    A((size_t)2 * hp.n_layer * sizeof(uint16_t*), (void**)&s->caches_dev);
+    if (st == CPV_OK) {
+        std::vector<uint16_t*> cp(2 * hp.n_layer);
+        for (int il = 0; il < hp.n_layer; il++) {
+            cp[il] = s->kc[il];
+            cp[hp.n_layer + il] = s->vt[il];
+        }
+        // (synchronous: the host vector goes away on return)
+        hipError_t e = hipMemcpy(s->caches_dev, cp.data(), cp.size() * sizeof(uint16_t*), hipMemcpyHostToDevice);
+        if (e != hipSuccess) st = cpv_hip_fail(ctx, e, "hipMemcpy");
+    }
     const int64_t kmax = (2 * E > F ? 2 * E : F) > H * hd ? (2 * E > F ? 2 * E : F) : H * hd;
     s->actbuf_bytes = cpv_act_bytes(CPV_Q4_K, kmax, T) > cpv_act_bytes(CPV_Q8_0, kmax, T)
                     ? cpv_act_bytes(CPV_Q4_K, kmax, T) : cpv_act_bytes(CPV_Q8_0, kmax, T);
@@ -1025,6 +1042,7 @@ extern "C" cpv_status cpv_session_set_pos(cpv_session* s, int64_t n_past, int64_
         return cpv_fail(s ? s->model->ctx : nullptr, CPV_EINVAL, "session: position out of range");
     s->n_past = n_past;
     s->mtp_past = mtp_past;
+    s->tree_base = -1;
     return CPV_OK;
 }
 
@@ -1105,9 +1123,18 @@ cpv_status apply_kept(cpv_session* s, float* x, int T, const cpv_gout& g, int sr
 
 // one attention block + FFN block of layer L on x (in place), T rows, one
 // kernel per op: the path for unstacked weights
+// a draft tree on the device: parent[i] (-1: a child of the context) and the
+// depth of node i, whose position is the round's base position + depth
+struct Tree {
+    const int32_t* parent;
+    const int32_t* depth;
+};
+
 cpv_status block_unfused(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_pos0, int64_t kv_row0,
-                 int64_t attn_past, uint16_t* kc, uint16_t* vt, int64_t v_stride, bool write)
+                 int64_t attn_past, uint16_t* kc, uint16_t* vt, int64_t v_stride, bool write,
+                 const Tree* tree = nullptr)
 {
+    const int32_t* parent = tree ? tree->parent : nullptr;
     cpv_model* m = s->model;
     cpv_ctx* ctx = m->ctx;
     const cpv_hparams& hp = m->hp;
@@ -1147,6 +1174,7 @@ cpv_status block_unfused(cpv_session* s, const LayerW& L, float* x, int T, int64
     pa.v_stride = v_stride;
     pa.rope_pos0 = rope_pos0;
     pa.kv_row0 = kv_row0;
+    pa.pos_off = tree ? tree->depth : nullptr;
     pa.H = (int)H;
     pa.Hkv = (int)Hkv;
     pa.hd = (int)hd;
@@ -1156,7 +1184,7 @@ cpv_status block_unfused(cpv_session* s, const LayerW& L, float* x, int T, int64
     qk_prep_kernel<<<dim3((unsigned)T, (unsigned)(H + Hkv)), (unsigned)hd, 0, ctx->stream>>>(pa);
     CPV_HIP(ctx, hipGetLastError());
     const float kq_scale = 1.0f / sqrtf((float)hd);
-    if ((st = cpv_attn_launch(ctx, s->q, kc, vt, v_stride, attn_past, nullptr, T, (int)H, (int)Hkv, (int)hd, kq_scale,
+    if ((st = cpv_attn_launch(ctx, s->q, kc, vt, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd, kq_scale,
                               s->att)))
         return st;
     if (s->tap) {
@@ -1209,8 +1237,9 @@ bool fusable(const cpv_model* m, const LayerW& L)
 // wo GEMM, residual+norm+quant, gate|up GEMM, SwiGLU+quant, down GEMM.
 cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_pos0, int64_t kv_row0,
                  int64_t attn_past, uint16_t* kc, uint16_t* vt, int64_t v_stride, bool write, const cpv_gout* pend,
-                 int pend_src, cpv_gout* out)
+                 int pend_src, cpv_gout* out, const Tree* tree = nullptr)
 {
+    const int32_t* parent = tree ? tree->parent : nullptr;
     cpv_model* m = s->model;
     cpv_ctx* ctx = m->ctx;
     const cpv_hparams& hp = m->hp;
@@ -1219,7 +1248,7 @@ cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_
     out->acc = nullptr;
     if (!fusable(m, L)) {
         if (pend && (st = apply_kept(s, x, T, *pend, pend_src))) return st;
-        return block_unfused(s, L, x, T, rope_pos0, kv_row0, attn_past, kc, vt, v_stride, write);
+        return block_unfused(s, L, x, T, rope_pos0, kv_row0, attn_past, kc, vt, v_stride, write, tree);
     }
     // attention norm (after the pending residual term) and the q|k|v input
     RowArgs r{};
@@ -1250,6 +1279,7 @@ cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_
     pa.v_stride = v_stride;
     pa.rope_pos0 = rope_pos0;
     pa.kv_row0 = kv_row0;
+    pa.pos_off = tree ? tree->depth : nullptr;
     pa.H = (int)H;
     pa.Hkv = (int)Hkv;
     pa.hd = (int)hd;
@@ -1271,14 +1301,14 @@ cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_
     cpv_attn_part part{};
     const int64_t nch = (attn_past + T + 127) / 128;         // the attention's 128-row chunks
     const bool fold = !s->tap && hd % 64 == 0 && 256 % hd == 0 && nch <= FOLD_MAX &&
-                      cpv_attn_partials(ctx, s->q, kc, vt, v_stride, attn_past, T, (int)H, (int)Hkv, (int)hd, kq_scale,
+                      cpv_attn_partials(ctx, s->q, kc, vt, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd, kq_scale,
                                         &part) == CPV_OK;
     if (fold) {
         r2.src = SRC_GATE_FOLD;
         r2.part = part;
         r2.hd = (int)hd;
     } else {
-        if ((st = cpv_attn_launch(ctx, s->q, kc, vt, v_stride, attn_past, nullptr, T, (int)H, (int)Hkv, (int)hd,
+        if ((st = cpv_attn_launch(ctx, s->q, kc, vt, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd,
                                   kq_scale, s->att)))
             return st;
         if (s->tap) {
@@ -1367,6 +1397,7 @@ extern "C" cpv_status cpv_prefill(cpv_session* s, const int32_t* tokens_dev, int
     if (s->n_past + t > s->n_ctx) return cpv_fail(ctx, CPV_EINVAL, "prefill: context overflow");
     cpv_status st;
     s->tap_off = 0;
+    s->tree_base = -1;
     CPV_HIP(ctx, hipMemcpyAsync(s->tok, tokens_dev, (size_t)t * 4, hipMemcpyDeviceToDevice, ctx->stream));
     if ((st = cpv_get_rows(ctx, m->tok_embd, s->tok, t, s->x))) return st;
     cpv_gout pend{}, nxt{};
@@ -1396,6 +1427,7 @@ extern "C" cpv_status cpv_verify_step(cpv_session* s, const int32_t* tokens_dev,
     if (s->mtp_past + t > s->mtp_ctx) s->mtp_past = 0;
     cpv_status st;
     s->tap_off = 0;
+    s->tree_base = -1;
     CPV_HIP(ctx, hipMemcpyAsync(s->tok, tokens_dev, (size_t)t * 4, hipMemcpyDeviceToDevice, ctx->stream));
     if ((st = cpv_get_rows(ctx, m->tok_embd, s->tok, t, s->x))) return st;
     cpv_gout pend{}, nxt{};
@@ -1446,5 +1478,155 @@ extern "C" cpv_status cpv_verify_step(cpv_session* s, const int32_t* tokens_dev,
     out->conf_dev = s->conf;
     out->logits_dev = s->logits;
     out->hidden_dev = s->h;
+    return CPV_OK;
+}
+
+// ---------------------------------------------------------------- draft trees
+// A tree verify is step_verify over a draft tree rather than a chain: no
+// counterpart in the reference, whose rounds verify a linear draft and rewind
+// it (engine.rs:2533-2540).  Node i is written at KV row n_past + i, placed at
+// position n_past + depth(i) and sees the context and its ancestors; a commit
+// then keeps one root-to-node path as contiguous context rows.
+
+namespace {
+
+struct TreeSetup {
+    int8_t parent[CPV_TREE_MAX], depth[CPV_TREE_MAX];
+    int t;
+};
+
+// the host-checked tree, passed by value, into the session's device copy
+__global__ void tree_setup_kernel(TreeSetup ts, int32_t* __restrict__ tree)
+{
+    const int i = threadIdx.x;
+    if (i < ts.t) {
+        tree[i] = ts.parent[i];
+        tree[CPV_TREE_MAX + i] = ts.depth[i];
+    }
+}
+
+struct CompactArgs {
+    uint16_t* const* caches;   // K caches [n_layer], then V caches [n_layer]
+    int64_t base, v_stride;
+    int n_layer, width, n;     // width: h_kv * head_dim halves per row
+    int8_t path[CPV_TREE_MAX];
+};
+
+// rows base + path[j] -> base + j of every trunk K cache (16-byte pieces of a
+// row) and columns likewise of every V cache (one V row per thread).  Since
+// path[j] >= j, writing row j never touches a source of a later j: each thread
+// moves its slice in order, eight rows at a time (all eight read before any is
+// written).
+__global__ __launch_bounds__(256) void compact_kernel(CompactArgs a)
+{
+    const int layer = blockIdx.y;
+    const int g = blockIdx.x * 256 + threadIdx.x, npiece = a.width / 8;
+    if (g < npiece) {
+        uint16_t* kc = a.caches[layer];
+        for (int j0 = 0; j0 < a.n; j0 += 8) {
+            uint4 v[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                if (j0 + q < a.n) v[q] = *(const uint4*)(kc + (a.base + a.path[j0 + q]) * a.width + g * 8);
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                if (j0 + q < a.n) *(uint4*)(kc + (a.base + j0 + q) * a.width + g * 8) = v[q];
+        }
+    } else if (g < npiece + a.width) {
+        uint16_t* vrow = a.caches[a.n_layer + layer] + (int64_t)(g - npiece) * a.v_stride + a.base;
+        for (int j0 = 0; j0 < a.n; j0 += 8) {
+            uint16_t v[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                if (j0 + q < a.n) v[q] = vrow[a.path[j0 + q]];
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                if (j0 + q < a.n) vrow[j0 + q] = v[q];
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" cpv_status cpv_verify_tree(cpv_session* s, const int32_t* tokens_dev, const int32_t* parent_host, int t,
+                                      const float* noise_dev, cpv_round_out* out)
+{
+    if (!s || !tokens_dev || !parent_host || !out || t < 1 || t > CPV_TREE_MAX || t > s->max_batch)
+        return cpv_fail(s ? s->model->ctx : nullptr, CPV_EINVAL, "verify_tree: bad arguments");
+    cpv_model* m = s->model;
+    cpv_ctx* ctx = m->ctx;
+    const cpv_hparams& hp = m->hp;
+    const int64_t V = hp.n_vocab;
+    if (s->n_past + t > s->n_ctx) return cpv_fail(ctx, CPV_EINVAL, "verify_tree: context overflow");
+    TreeSetup ts{};
+    ts.t = t;
+    for (int i = 0; i < t; i++) {
+        const int p = parent_host[i];
+        if (p < -1 || p >= i)
+            return cpv_fail(ctx, CPV_EINVAL, "verify_tree: parent[%d] = %d (parents precede their children)", i, p);
+        ts.parent[i] = (int8_t)p;
+        ts.depth[i] = (int8_t)(p < 0 ? 0 : ts.depth[p] + 1);
+    }
+    s->tap_off = 0;
+    s->tree_base = -1;
+    cpv_status st;
+    tree_setup_kernel<<<1, CPV_TREE_MAX, 0, ctx->stream>>>(ts, s->tree_dev);
+    CPV_HIP(ctx, hipGetLastError());
+    const Tree tree{s->tree_dev, s->tree_dev + CPV_TREE_MAX};
+    CPV_HIP(ctx, hipMemcpyAsync(s->tok, tokens_dev, (size_t)t * 4, hipMemcpyDeviceToDevice, ctx->stream));
+    if ((st = cpv_get_rows(ctx, m->tok_embd, s->tok, t, s->x))) return st;
+    cpv_gout pend{}, nxt{};
+    for (int il = 0; il < hp.n_layer; il++) {
+        if ((st = block(s, m->layers[il], s->x, t, s->n_past, s->n_past, s->n_past, s->kc[il], s->vt[il], s->v_stride,
+                        true, pend.acc ? &pend : nullptr, SRC_ADD, &nxt, &tree)))
+            return st;
+        pend = nxt;
+    }
+    if ((st = norm_head(s, s->x, t, pend.acc ? &pend : nullptr, m->output_norm, s->h, m->output, s->logits)))
+        return st;
+    if ((st = cpv_argmax_rows(ctx, s->logits, noise_dev, t, V, s->preds))) return st;
+    s->tree_parent.assign(parent_host, parent_host + t);
+    s->tree_base = s->n_past;
+    s->n_past += t;
+    out->n_past = s->n_past;
+    out->preds_dev = s->preds;
+    out->chain_dev = s->chain;
+    out->conf_dev = s->conf;
+    out->logits_dev = s->logits;
+    out->hidden_dev = s->h;
+    return CPV_OK;
+}
+
+extern "C" cpv_status cpv_session_commit_branch(cpv_session* s, const int32_t* path_host, int n)
+{
+    if (!s || (n > 0 && !path_host) || n < 0)
+        return cpv_fail(s ? s->model->ctx : nullptr, CPV_EINVAL, "commit_branch: bad arguments");
+    cpv_ctx* ctx = s->model->ctx;
+    const cpv_hparams& hp = s->model->hp;
+    if (s->tree_base < 0) return cpv_fail(ctx, CPV_EINVAL, "commit_branch: no tree verify to commit");
+    const int t = (int)s->tree_parent.size();
+    if (n > t) return cpv_fail(ctx, CPV_EINVAL, "commit_branch: path of %d nodes in a tree of %d", n, t);
+    CompactArgs a{};
+    bool moved = false;
+    for (int j = 0; j < n; j++) {
+        const int v = path_host[j];
+        if (v < 0 || v >= t || s->tree_parent[v] != (j == 0 ? -1 : path_host[j - 1]))
+            return cpv_fail(ctx, CPV_EINVAL, "commit_branch: path[%d] = %d does not continue a root-to-node path", j, v);
+        a.path[j] = (int8_t)v;
+        moved |= v != j;
+    }
+    if (moved) {
+        a.caches = s->caches_dev;
+        a.base = s->tree_base;
+        a.v_stride = s->v_stride;
+        a.n_layer = hp.n_layer;
+        a.width = (int)(hp.n_head_kv * hp.head_dim);
+        a.n = n;
+        const int threads = a.width / 8 + a.width;
+        compact_kernel<<<dim3((unsigned)((threads + 255) / 256), (unsigned)hp.n_layer), 256, 0, ctx->stream>>>(a);
+        CPV_HIP(ctx, hipGetLastError());
+    }
+    s->n_past = s->tree_base + n;
+    s->tree_base = -1;
     return CPV_OK;
 }

@@ -130,6 +130,31 @@ class Session:
             hidden = _device_view(out.hidden_dev, t * E, torch.float32, self.ctx.torch_device).view(t, E).clone()
         return FusedOut(preds, chain, conf, logits, hidden)
 
+    def verify_tree(self, tokens, parent, want_logits=False, noise=None):
+        """Verify a draft tree: tokens[i] with parent[i] (-1: a child of the
+        context; parents precede children).  Returns the argmax of each node's
+        logits (and the logits and hidden rows when asked)."""
+        t = self._tokens(tokens)
+        par = (ctypes.c_int32 * t)(*[int(p) for p in parent])
+        out = RoundOut()
+        nz = None if noise is None else ctypes.c_void_p(noise.data_ptr())
+        self.ctx._check(self.ctx.lib.cpv_verify_tree(self.h, ctypes.c_void_p(self._tok.data_ptr()), par, t, nz,
+                                                     ctypes.byref(out)))
+        V, E = self.model.hp.n_vocab, self.model.hp.n_embd
+        preds = _device_view(out.preds_dev, t, torch.int32, self.ctx.torch_device).cpu().tolist()
+        logits = hidden = None
+        if want_logits:
+            logits = _device_view(out.logits_dev, t * V, torch.float32, self.ctx.torch_device).view(t, V).clone()
+            hidden = _device_view(out.hidden_dev, t * E, torch.float32, self.ctx.torch_device).view(t, E).clone()
+        return FusedOut(preds, [], [], logits, hidden)
+
+    def commit_branch(self, path):
+        """Keep the root-to-node path `path` (node indices) of the last tree
+        verify as context rows; the other nodes are dropped."""
+        n = len(path)
+        arr = (ctypes.c_int32 * max(n, 1))(*[int(v) for v in path])
+        self.ctx._check(self.ctx.lib.cpv_session_commit_branch(self.h, arr, n))
+
     def free(self):
         if self.h:
             self.ctx.lib.cpv_session_free(self.h)

@@ -243,6 +243,32 @@ typedef struct {
 cpv_status  cpv_verify_step(cpv_session* s, const int32_t* tokens_dev, int t, int depth,
                             const float* noise_dev, cpv_round_out* out);
 
+/* ---- draft trees ----------------------------------------------------------
+ * No counterpart in the reference: its rounds verify a linear draft and rewind
+ * the rejected tail (crates/codpiece-server/src/engine.rs:2533-2540,
+ * Qwen35::step_verify qwen35.rs:1568-1674).  These extend that round to a
+ * draft tree, with the same trunk, head and argmax.
+ *
+ * cpv_verify_tree: step_verify over t <= CPV_TREE_MAX nodes.  parent_host[i]
+ * is node i's parent (-1: a child of the context), and parents precede their
+ * children.  Node i is written at KV row n_past + i, placed at position
+ * n_past + depth(i), and attends to the context plus its ancestors and itself
+ * (the tree mask of cpv_attn).  preds_dev[i] is the argmax of node i's logits
+ * (of logits + noise when noise_dev is given).  n_past advances by t, as
+ * verify_step does.  No draft chain is produced.
+ *
+ * cpv_session_commit_branch: after a tree verify, keeps path_host[0..n), a
+ * root-to-node path of that tree.  Its nodes become context rows
+ * n_past0 .. n_past0 + n - 1 in every trunk layer's K and V caches, where
+ * n_past0 is n_past before the verify, and n_past becomes n_past0 + n.  The
+ * other nodes are dropped (n = 0 drops the tree).  Every later row is the same
+ * as if the path had been verified as a chain.  Any other call that moves n_past
+ * (prefill, verify_step, set_pos) ends the pending tree. */
+#define CPV_TREE_MAX 64
+cpv_status  cpv_verify_tree(cpv_session* s, const int32_t* tokens_dev, const int32_t* parent_host, int t,
+                            const float* noise_dev, cpv_round_out* out);
+cpv_status  cpv_session_commit_branch(cpv_session* s, const int32_t* path_host, int n);
+
 /* ---- kernel timing -------------------------------------------------------
  * No counterpart in the reference (which times whole rounds with
  * Instant::now, crates/codpiece-server/src/engine.rs:2295,2324).  Between
