@@ -54,6 +54,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--sampler", type=int, default=1, help="0 skips the acceptance-sampler microbench")
     ap.add_argument("--sampler-only", action="store_true", help="run only the acceptance-sampler microbench")
+    ap.add_argument("--gguf-load-only", type=int, default=0, metavar="LAYERS",
+                    help="only time loading a seeded 27B-class GGUF file of LAYERS trunk layers")
     ap.add_argument("--calibrate-copy", type=int, default=0,
                     help="first copy 1 GiB on the device 3 times (a known-size kernel for HBM counters)")
     return ap.parse_args()
@@ -262,6 +264,31 @@ def sampler_bench(torch, ctx, seed, reps=20):
 
 
 # ---------------------------------------------------------------- main
+def gguf_load_bench(ctx, layers, seed):
+    """Weights::load of a seeded 27B-class qwen35 file (Q4_K linears, Q6_K
+    embedding and head, `layers` trunk layers and the MTP layer): the file is
+    written to a temporary directory, then loaded (file read, host-to-device
+    copy and repack of every tensor) and timed end to end."""
+    import tempfile
+    from codpiece_amd import gguf
+    from codpiece_amd.model import Model
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "m.gguf")
+        t0 = time.perf_counter()
+        gguf.write_seeded_model(path, layers, HP["n_embd"], HP["n_head"], HP["n_head_kv"], HP["head_dim"],
+                                HP["n_ff"], HP["n_vocab"], n_rot=HP["n_rot"], rope_sections=HP["rope_sections"],
+                                seed=seed, qtype=gguf.Q4_K, head_type=gguf.Q6_K)
+        size = os.path.getsize(path)
+        print(f"[bench] wrote {size / 1e9:.2f} GB in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+        ctx.sync()
+        t0 = time.perf_counter()
+        m = Model.from_gguf(ctx, path)
+        ctx.sync()
+        s = time.perf_counter() - t0
+        m.free()
+    return {"layers": layers, "file_GB": round(size / 1e9, 3), "seconds": round(s, 3), "GB_s": round(size / 1e9 / s, 2)}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -278,6 +305,10 @@ def main():
     ctx = Context(0)
     if args.sampler_only:
         print(json.dumps({"sampler": sampler_bench(torch, ctx, args.seed)}), flush=True)
+        ctx.close()
+        return 0
+    if args.gguf_load_only:
+        print(json.dumps({"gguf_load": gguf_load_bench(ctx, args.gguf_load_only, args.seed)}), flush=True)
         ctx.close()
         return 0
     if args.calibrate_copy:

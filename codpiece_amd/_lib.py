@@ -62,6 +62,14 @@ class RoundOut(ctypes.Structure):
     ]
 
 
+class GgufInfo(ctypes.Structure):
+    """cpv_gguf_info: what GgufFile::open reads (crates/codpiece-gguf/src/lib.rs:345-458)."""
+    _fields_ = [
+        ("version", ctypes.c_int32), ("n_tensors", ctypes.c_int64), ("n_kv", ctypes.c_int64),
+        ("alignment", ctypes.c_uint64), ("data_start", ctypes.c_uint64), ("tensor_bytes", ctypes.c_uint64),
+    ]
+
+
 PROF_Q4_K, PROF_Q6_K, PROF_Q8_0, PROF_ATTN, PROF_SAMPLE, PROF_CLASSES = 0, 1, 2, 3, 4, 5
 PROF_NAMES = ("qgemm_q4_k", "qgemm_q6_k", "qgemm_q8_0", "attention", "sampler")
 
@@ -103,6 +111,9 @@ SIGNATURES = {
     "cpv_model_set_tensor": (_INT, [_P, ctypes.c_char_p, _INT, _P, _INT, _I64, _I64]),
     "cpv_model_ready": (_INT, [_P]),
     "cpv_model_free": (None, [_P]),
+    "cpv_gguf_scan": (_INT, [ctypes.c_char_p, ctypes.POINTER(GgufInfo), ctypes.c_char_p, _INT]),
+    "cpv_gguf_hparams": (_INT, [ctypes.c_char_p, ctypes.POINTER(Hparams), ctypes.c_char_p, _INT]),
+    "cpv_model_load_gguf": (_INT, [_P, ctypes.c_char_p, ctypes.POINTER(_P)]),
     "cpv_session_create": (_INT, [_P, _I64, _I32, ctypes.POINTER(_P)]),
     "cpv_session_free": (None, [_P]),
     "cpv_session_set_pos": (_INT, [_P, _I64, _I64]),

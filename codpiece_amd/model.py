@@ -36,6 +36,17 @@ class Model:
         ctx._check(ctx.lib.cpv_model_create(ctx.h, ctypes.byref(hp), ctypes.byref(h)))
         self.h = h
 
+    @classmethod
+    def from_gguf(cls, ctx, path):
+        """Weights::load of a qwen35 GGUF file (all-attention layout)."""
+        self = cls.__new__(cls)
+        h = ctypes.c_void_p()
+        ctx._check(ctx.lib.cpv_model_load_gguf(ctx.h, str(path).encode(), ctypes.byref(h)))
+        self.ctx, self.h = ctx, h
+        from .gguf import hparams
+        self.hp = hparams(path)
+        return self
+
     def set_tensor(self, name, qtype, data, ne0, ne1):
         """data: numpy (host bytes) or a cuda tensor (device bytes), ggml ne order."""
         if isinstance(data, torch.Tensor):

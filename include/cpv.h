@@ -205,6 +205,35 @@ cpv_status  cpv_model_set_tensor(cpv_model* m, const char* name, int type, const
 cpv_status  cpv_model_ready(cpv_model* m);
 void        cpv_model_free(cpv_model* m);
 
+/* ---- the model file (GGUF) -------------------------------------------------
+ * cpv_gguf_scan: GgufFile::open and its validation
+ * (crates/codpiece-gguf/src/lib.rs:345-458).  It reads the header, the
+ * metadata and the tensor directory of a GGUF v1-v3 file.  Counts and lengths
+ * are capped.  The alignment must be a power of two.  Tensor offsets must be
+ * aligned, in file order without overlap, and inside the data section.
+ * tensor_bytes is the sum of the sized tensors (tensor_bytes, :453-456).  No
+ * GPU is used.  On failure errbuf (may be NULL) gets the reason.
+ *
+ * cpv_gguf_hparams: Hparams::from_gguf (crates/codpiece-model/src/qwen35.rs:
+ * 75-130) for an all-attention qwen35 file.  n_layer = block_count -
+ * nextn_predict_layers, n_vocab = the length of tokenizer.ggml.tokens, and
+ * the same defaults for the optional keys.  full_attention_interval must be 1
+ * and there is at most one nextn layer (else CPV_EUNSUPPORTED).  No GPU is
+ * used.
+ *
+ * cpv_model_load_gguf: Weights::load (crates/codpiece-model/src/lib.rs:
+ * 128-311) on one device.  It creates the model from the file's
+ * hyper-parameters, hands every tensor to cpv_model_set_tensor by name (one
+ * whole-tensor read and upload each), then calls cpv_model_ready. */
+typedef struct {
+    int32_t  version;
+    int64_t  n_tensors, n_kv;
+    uint64_t alignment, data_start, tensor_bytes;
+} cpv_gguf_info;
+cpv_status  cpv_gguf_scan(const char* path, cpv_gguf_info* info, char* errbuf, int errlen);
+cpv_status  cpv_gguf_hparams(const char* path, cpv_hparams* hp, char* errbuf, int errlen);
+cpv_status  cpv_model_load_gguf(cpv_ctx* ctx, const char* path, cpv_model** out);
+
 /* Session::new_spec (qwen35.rs:528-649): f16 K caches [n_ctx][h_kv*d] and
  * transposed V caches per layer, plus the MTP cache (min(n_ctx, 16384)
  * rows); max_batch bounds t of every call. */
