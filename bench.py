@@ -33,6 +33,8 @@ import os
 import sys
 import time
 
+import numpy as np
+
 HP = dict(n_layer=64, n_embd=5120, n_head=40, n_head_kv=8, head_dim=128, n_ff=17408, n_vocab=151936,
           n_rot=128, rope_sections=(22, 22, 20, 0), rms_eps=1e-6, freq_base=1e6, has_mtp=True)
 HBM_PEAK_GBS = 8000.0
@@ -364,6 +366,19 @@ def main():
         sess.set_pos(n_past, mtp_past)
     vo.sort()
 
+    # full rounds with the draft head over an 8192-token shortlist, rewound afterwards
+    cands = np.arange(8192, dtype=np.int32)
+    sl = []
+    for _ in range(max(3, args.steps // 4)):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        sess.step_fused_cached([loop.last] + loop.drafts, args.depth, cands=cands)
+        b.record(stream)
+        torch.cuda.synchronize()
+        sl.append(a.elapsed_time(b))
+        sess.set_pos(n_past, mtp_past)
+    sl.sort()
+
     # draft trees: the canonical 16-node tree (widths 4, 6, 3, 3) verified, then
     # its deepest leftmost path committed; rewound afterwards
     tree = [-1, -1, -1, -1, 0, 0, 0, 1, 1, 1, 4, 4, 4, 10, 10, 10]
@@ -423,6 +438,7 @@ def main():
         "detail": {
             "round_device_us_median": round(dev_ms[len(dev_ms) // 2] * 1e3, 1),
             "verify_only_device_us_median": round(vo[len(vo) // 2] * 1e3, 1),
+            "round_shortlist_8192_device_us_median": round(sl[len(sl) // 2] * 1e3, 1),
             "tree_verify_16_device_us_median": round(tv[len(tv) // 2] * 1e3, 1),
             "tree_commit_4_device_us_median": round(tc[len(tc) // 2] * 1e3, 1),
             "acceptance": round((loop.accepted - acc0) / max(1, loop.proposed - prop0), 4),

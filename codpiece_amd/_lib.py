@@ -121,6 +121,8 @@ SIGNATURES = {
     "cpv_session_set_attn_tap": (_INT, [_P, _P, _I64]),
     "cpv_prefill": (_INT, [_P, _P, _INT]),
     "cpv_verify_step": (_INT, [_P, _P, _INT, _INT, _P, ctypes.POINTER(RoundOut)]),
+    "cpv_verify_step_cands": (_INT, [_P, _P, _INT, _INT, _P, ctypes.POINTER(ctypes.c_int32), _INT,
+                                     ctypes.POINTER(RoundOut)]),
     "cpv_verify_tree": (_INT, [_P, _P, ctypes.POINTER(ctypes.c_int32), _INT, _P, ctypes.POINTER(RoundOut)]),
     "cpv_session_commit_branch": (_INT, [_P, ctypes.POINTER(ctypes.c_int32), _INT]),
 }

@@ -414,6 +414,97 @@ extern "C" cpv_status cpv_weight_from_device(cpv_ctx* ctx, int type, const void*
     return weight_create(ctx, type, dev_bytes, true, n_rows, k, out);
 }
 
+// Rows `rows[0..n)` of a repacked weight as a new one of n rows (get_rows on
+// a quantized weight, as a draft head's shortlist takes it, qwen35.rs:2929):
+// the 16-byte pieces of every (tile, unit) slab move lane by lane, then the
+// Q6_K d region and the row exponents; rows past n are empty.
+template <int TYPE>
+__global__ void gather_kernel(const uint8_t* __restrict__ src, const int32_t* __restrict__ ew_s, int64_t n_pad_s,
+                              const int32_t* __restrict__ rows, int64_t n, int64_t U, uint8_t* __restrict__ dst,
+                              int32_t* __restrict__ ew_d, int64_t n_pad_d)
+{
+    constexpr int PIECES = TYPE == CPV_Q4_K ? 9 : TYPE == CPV_Q6_K ? 13 : 17;
+    const int64_t tiles_d = n_pad_d / 64;
+    const int64_t npieces = tiles_d * U * PIECES * 64;
+    const int64_t nd6 = TYPE == CPV_Q6_K ? tiles_d * U * 64 : 0;
+    const int64_t total = npieces + nd6 + n_pad_d;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        if (i < npieces) {
+            const int lane = (int)(i & 63);
+            const int64_t sp = i >> 6, piece = sp % PIECES, slab = sp / PIECES;
+            const int64_t row = (slab / U) * 64 + lane, u = slab % U;
+            uint4 v = {0u, 0u, 0u, 0u};
+            if (row < n) {
+                const int64_t r = rows[row];
+                v = *(const uint4*)(src + (((r / 64) * U + u) * PIECES + piece) * 1024 + (r % 64) * 16);
+            }
+            *(uint4*)(dst + (slab * PIECES + piece) * 1024 + lane * 16) = v;
+        } else if (i < npieces + nd6) {
+            const int64_t j = i - npieces;
+            const int lane = (int)(j & 63);
+            const int64_t slab = j >> 6, row = (slab / U) * 64 + lane, u = slab % U;
+            const uint16_t* d6s = (const uint16_t*)(src + (n_pad_s / 64) * U * PIECES * 1024);
+            uint16_t* d6d = (uint16_t*)(dst + tiles_d * U * PIECES * 1024);
+            uint16_t v = 0;
+            if (row < n) {
+                const int64_t r = rows[row];
+                v = d6s[((r / 64) * U + u) * 64 + r % 64];
+            }
+            d6d[slab * 64 + lane] = v;
+        } else {
+            const int64_t row = i - npieces - nd6;
+            ew_d[row] = row < n ? ew_s[rows[row]] : CPV_E_EMPTY;
+        }
+    }
+}
+
+cpv_status cpv_weight_gather(cpv_ctx* ctx, const cpv_weight* src, const int32_t* rows_dev, int64_t n,
+                             cpv_weight** out)
+{
+    *out = nullptr;
+    cpv_weight* w = new (std::nothrow) cpv_weight();
+    if (!w) return cpv_fail(ctx, CPV_ENOMEM, "gather: host allocation");
+    w->ctx = ctx;
+    w->type = src->type;
+    w->n = n;
+    w->k = src->k;
+    weight_geometry(w);
+    hipError_t e = hipMalloc(&w->data, w->data_bytes);
+    if (e == hipSuccess) e = hipMalloc((void**)&w->ew, sizeof(int32_t) * (size_t)w->n_pad);
+    if (e != hipSuccess) {
+        if (w->data) (void)hipFree(w->data);
+        delete w;
+        return cpv_hip_fail(ctx, e, "gather: hipMalloc");
+    }
+    const int64_t pieces = (int64_t)(w->data_bytes / 16) + w->n_pad;
+    const unsigned blocks = (unsigned)((pieces + 255) / 256 < 4096 ? (pieces + 255) / 256 : 4096);
+    const uint8_t* s = (const uint8_t*)src->data;
+    uint8_t* d = (uint8_t*)w->data;
+    switch (w->type) {
+    case CPV_Q4_K:
+        gather_kernel<CPV_Q4_K><<<blocks, 256, 0, ctx->stream>>>(s, src->ew, src->n_pad, rows_dev, n, w->units, d, w->ew,
+                                                                 w->n_pad);
+        break;
+    case CPV_Q6_K:
+        gather_kernel<CPV_Q6_K><<<blocks, 256, 0, ctx->stream>>>(s, src->ew, src->n_pad, rows_dev, n, w->units, d, w->ew,
+                                                                 w->n_pad);
+        break;
+    default:
+        gather_kernel<CPV_Q8_0><<<blocks, 256, 0, ctx->stream>>>(s, src->ew, src->n_pad, rows_dev, n, w->units, d, w->ew,
+                                                                 w->n_pad);
+        break;
+    }
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+        (void)hipFree(w->data);
+        (void)hipFree(w->ew);
+        delete w;
+        return cpv_hip_fail(ctx, e, "gather");
+    }
+    *out = w;
+    return CPV_OK;
+}
+
 // Rows of several weights stacked into one (same type and k; every part but
 // the last a whole number of 64-row tiles, so the tiles just follow each
 // other): the tile slabs of the parts in order, then, for Q6_K, their d

@@ -57,6 +57,10 @@ struct cpv_weight {
     int32_t* ew = nullptr;    // [n_pad] frexp exponent of the row's largest scale
 };
 
+// rows[0..n) (device, each < src->n) of a repacked weight as a new weight
+cpv_status cpv_weight_gather(cpv_ctx* ctx, const cpv_weight* src, const int32_t* rows_dev, int64_t n,
+                             cpv_weight** out);
+
 // error helpers: record a message on the context and return the status
 cpv_status cpv_fail(cpv_ctx* ctx, cpv_status st, const char* fmt, ...);
 cpv_status cpv_hip_fail(cpv_ctx* ctx, hipError_t e, const char* what);

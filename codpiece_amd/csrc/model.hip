@@ -18,6 +18,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <string>
 #include <vector>
@@ -734,6 +735,11 @@ struct cpv_session {
     uint16_t** caches_dev = nullptr;      // the trunk's K caches [n_layer], then its V caches [n_layer]
     std::vector<int32_t> tree_parent;     // (host copy, to check a committed path)
     int64_t tree_base = -1;               // n_past before that verify; -1 when no tree is pending
+    std::vector<int32_t> cand_host;       // the draft head's shortlist (host copy of cand_dev)
+    int32_t* cand_dev = nullptr;          // [cand_cap]
+    int64_t cand_cap = 0;
+    cpv_weight* cand_head = nullptr;      // the draft head's rows cand_host
+    int32_t* cand_idx = nullptr;          // [max_batch] a link's argmax within the shortlist
     std::vector<void*> allocs;
 };
 
@@ -918,6 +924,8 @@ extern "C" void cpv_session_free(cpv_session* s)
     if (!s) return;
     (void)hipStreamSynchronize(s->model->ctx->stream);
     for (void* p : s->allocs) (void)hipFree(p);
+    if (s->cand_dev) (void)hipFree(s->cand_dev);
+    if (s->cand_head) cpv_weight_free(s->cand_head);
     delete s;
 }
 
@@ -980,6 +988,7 @@ extern "C" cpv_status cpv_session_create(cpv_model* m, int64_t n_ctx, int32_t ma
     A((size_t)16 * T * 4, (void**)&s->chain);
     A((size_t)16 * T * 4, (void**)&s->conf);
     A((size_t)2 * CPV_TREE_MAX * 4, (void**)&s->tree_dev);
+    A((size_t)T * 4, (void**)&s->cand_idx);
     A((size_t)2 * hp.n_layer * sizeof(uint16_t*), (void**)&s->caches_dev);
     if (st == CPV_OK) {
         std::vector<uint16_t*> cp(2 * hp.n_layer);
@@ -1412,17 +1421,73 @@ extern "C" cpv_status cpv_prefill(cpv_session* s, const int32_t* tokens_dev, int
     return CPV_OK;
 }
 
+namespace {
+
+// a shortlist link's drafts: ids[i] = cands[idx[i]]
+__global__ void map_cands_kernel(const int32_t* __restrict__ idx, const int32_t* __restrict__ cands, int t,
+                                 int32_t* __restrict__ ids)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < t) ids[i] = cands[idx[i]];
+}
+
+// the draft head over `cands` (host, ids < V): uploaded and gathered when they
+// differ from the last shortlist; the device buffers a previous round may still
+// read are replaced only after the stream drains
+cpv_status set_cands(cpv_session* s, const int32_t* cands, int n)
+{
+    cpv_model* m = s->model;
+    cpv_ctx* ctx = m->ctx;
+    if ((size_t)n == s->cand_host.size() && std::equal(cands, cands + n, s->cand_host.begin())) return CPV_OK;
+    for (int j = 0; j < n; j++)
+        if (cands[j] < 0 || cands[j] >= m->hp.n_vocab)
+            return cpv_fail(ctx, CPV_EINVAL, "verify_step: candidate %d = %d outside the vocabulary", j, cands[j]);
+    CPV_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    s->cand_host.clear();
+    if (s->cand_head) {
+        cpv_weight_free(s->cand_head);
+        s->cand_head = nullptr;
+    }
+    if (n > s->cand_cap) {
+        if (s->cand_dev) (void)hipFree(s->cand_dev);
+        s->cand_dev = nullptr;
+        s->cand_cap = 0;
+        CPV_HIP(ctx, hipMalloc((void**)&s->cand_dev, (size_t)n * 4));
+        s->cand_cap = n;
+    }
+    CPV_HIP(ctx, hipMemcpy(s->cand_dev, cands, (size_t)n * 4, hipMemcpyHostToDevice));
+    cpv_status st = cpv_weight_gather(ctx, m->mtp_head, s->cand_dev, n, &s->cand_head);
+    if (st != CPV_OK) return st;
+    s->cand_host.assign(cands, cands + n);
+    return CPV_OK;
+}
+
+}  // namespace
+
 extern "C" cpv_status cpv_verify_step(cpv_session* s, const int32_t* tokens_dev, int t, int depth,
                                       const float* noise_dev, cpv_round_out* out)
 {
-    if (!s || !tokens_dev || !out || t < 1 || t > s->max_batch || depth < 0 || depth > 16)
+    return cpv_verify_step_cands(s, tokens_dev, t, depth, noise_dev, nullptr, 0, out);
+}
+
+extern "C" cpv_status cpv_verify_step_cands(cpv_session* s, const int32_t* tokens_dev, int t, int depth,
+                                            const float* noise_dev, const int32_t* cands_host, int n_cand,
+                                            cpv_round_out* out)
+{
+    if (!s || !tokens_dev || !out || t < 1 || t > s->max_batch || depth < 0 || depth > 16 || n_cand < 0 ||
+        (n_cand > 0 && !cands_host))
         return cpv_fail(s ? s->model->ctx : nullptr, CPV_EINVAL, "verify_step: bad arguments");
     cpv_model* m = s->model;
     cpv_ctx* ctx = m->ctx;
     const cpv_hparams& hp = m->hp;
     const int64_t E = hp.n_embd, V = hp.n_vocab;
+    if (n_cand > V) return cpv_fail(ctx, CPV_EINVAL, "verify_step: %d candidates for a vocabulary of %lld", n_cand,
+                                    (long long)V);
     if (s->n_past + t > s->n_ctx) return cpv_fail(ctx, CPV_EINVAL, "verify_step: context overflow");  // qwen35.rs:1718-1720
     if (depth > 0 && !hp.has_mtp) return cpv_fail(ctx, CPV_EINVAL, "verify_step: model has no MTP head");
+    const bool shortlist = depth > 0 && n_cand > 0;
+    cpv_status st0;
+    if (shortlist && (st0 = set_cands(s, cands_host, n_cand)) != CPV_OK) return st0;
     // the draft head's window is bounded; when it fills, it restarts (qwen35.rs:1730-1735)
     if (s->mtp_past + t > s->mtp_ctx) s->mtp_past = 0;
     cpv_status st;
@@ -1458,17 +1523,25 @@ extern "C" cpv_status cpv_verify_step(cpv_session* s, const int32_t* tokens_dev,
             if ((st = block(s, ML, s->dsa, t, s->n_past + 1, s->mtp_past, s->mtp_past, s->kc[hp.n_layer],
                             s->vt[hp.n_layer], s->mtp_v_stride, step == 0, &eh, SRC_SET, &nxt)))
                 return st;
-            // h_next = rms(d, shared_head_norm or output_norm), then the draft head
-            if ((st = norm_head(s, s->dsa, t, nxt.acc ? &nxt : nullptr, m->mtp_head_norm, s->hn, m->mtp_head,
-                                s->mtp_logits)))
+            // h_next = rms(d, shared_head_norm or output_norm), then the draft head,
+            // over the shortlist when one is given (qwen35.rs:2925-2931)
+            if ((st = norm_head(s, s->dsa, t, nxt.acc ? &nxt : nullptr, m->mtp_head_norm, s->hn,
+                                shortlist ? s->cand_head : m->mtp_head, s->mtp_logits)))
                 return st;
             int32_t* ids = s->chain + (size_t)step * t;
-            if ((st = cpv_argmax_peak_rows(ctx, s->mtp_logits, nullptr, t, V, ids, s->conf + (size_t)step * t)))
+            if ((st = cpv_argmax_peak_rows(ctx, s->mtp_logits, nullptr, t, shortlist ? n_cand : V,
+                                           shortlist ? s->cand_idx : ids, s->conf + (size_t)step * t)))
                 return st;
+            if (shortlist) {
+                // drafts are candidates; the next link embeds the argmax itself, as the
+                // graph does (tok_src = ids, qwen35.rs:2958; the ids map back on the host, :1904-1910)
+                map_cands_kernel<<<(unsigned)((t + 255) / 256), 256, 0, ctx->stream>>>(s->cand_idx, s->cand_dev, t, ids);
+                CPV_HIP(ctx, hipGetLastError());
+            }
             // the next link feeds on this link's prediction and hidden
             CPV_HIP(ctx, hipMemcpyAsync(s->hsrc, s->hn, (size_t)t * E * 4, hipMemcpyDeviceToDevice, ctx->stream));
             h_src = s->hsrc;
-            tok_src = ids;
+            tok_src = shortlist ? s->cand_idx : ids;
         }
     }
     s->n_past += t;

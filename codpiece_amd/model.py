@@ -119,14 +119,21 @@ class Session:
         t = self._tokens(tokens)
         self.ctx._check(self.ctx.lib.cpv_prefill(self.h, ctypes.c_void_p(self._tok.data_ptr()), t))
 
-    def step_fused_cached(self, tokens, depth, want_logits=False, noise=None):
+    def step_fused_cached(self, tokens, depth, want_logits=False, noise=None, cands=None):
         """Verify `tokens` and chain `depth` drafts; greedy in-graph argmax,
-        gumbel argmax when `noise` ([t][V] device tensor) is given."""
+        gumbel argmax when `noise` ([t][V] device tensor) is given; the draft
+        head over the shortlist `cands` (token ids) when given."""
         t = self._tokens(tokens)
         out = RoundOut()
         nz = None if noise is None else ctypes.c_void_p(noise.data_ptr())
-        self.ctx._check(self.ctx.lib.cpv_verify_step(self.h, ctypes.c_void_p(self._tok.data_ptr()), t, depth, nz,
-                                                     ctypes.byref(out)))
+        if cands is None:
+            self.ctx._check(self.ctx.lib.cpv_verify_step(self.h, ctypes.c_void_p(self._tok.data_ptr()), t, depth,
+                                                         nz, ctypes.byref(out)))
+        else:
+            c = np.ascontiguousarray(cands, dtype=np.int32)
+            self.ctx._check(self.ctx.lib.cpv_verify_step_cands(
+                self.h, ctypes.c_void_p(self._tok.data_ptr()), t, depth, nz,
+                c.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), int(c.size), ctypes.byref(out)))
         V, E = self.model.hp.n_vocab, self.model.hp.n_embd
         preds = _device_view(out.preds_dev, t, torch.int32, self.ctx.torch_device).cpu().tolist()
         chain = []

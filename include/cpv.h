@@ -271,6 +271,18 @@ typedef struct {
  * logits + noise_dev when noise is given, the gumbel branch), MTP chain. */
 cpv_status  cpv_verify_step(cpv_session* s, const int32_t* tokens_dev, int t, int depth,
                             const float* noise_dev, cpv_round_out* out);
+/* The same with the draft head over a shortlist: step_fused_cached's `cands`
+ * (MtpTail::n_cand, qwen35.rs:208-216, :1698-1707).  Each link projects onto
+ * the head's rows cands_host[0..n_cand) (get_rows then mul_mat,
+ * :2925-2931).  Its draft is cands[argmax] and its confidence the softmax
+ * peak over those n_cand logits.  As in the reference graph, the next link
+ * embeds the argmax itself (tok_src = ids, :2958); the reported chain holds
+ * the mapped ids (:1904-1910).  Verification keeps the full vocabulary.
+ * Candidates are host ids < n_vocab.  The gathered head is kept while the
+ * shortlist stays the same.  n_cand = 0 is cpv_verify_step. */
+cpv_status  cpv_verify_step_cands(cpv_session* s, const int32_t* tokens_dev, int t, int depth,
+                                  const float* noise_dev, const int32_t* cands_host, int n_cand,
+                                  cpv_round_out* out);
 
 /* ---- draft trees ----------------------------------------------------------
  * No counterpart in the reference: its rounds verify a linear draft and rewind

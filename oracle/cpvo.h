@@ -204,6 +204,9 @@ int           cpvo_prefill(cpvo_session* s, const int32_t* tok, int t);
  * logits [t][V] and hidden [t][E] (nullable); noise [t][V] or NULL */
 int           cpvo_verify_step(cpvo_session* s, const int32_t* tok, int t, int depth, const float* noise,
                                int32_t* preds, int32_t* chain, float* conf, float* logits, float* hidden);
+int           cpvo_verify_step_cands(cpvo_session* s, const int32_t* tok, int t, int depth, const float* noise,
+                                     const int32_t* cands, int n_cand, int32_t* preds, int32_t* chain, float* conf,
+                                     float* logits_out, float* hidden_out);
 /* cmd_fused: returns the number of committed tokens; stats = {accepted, proposed, rounds} */
 int           cpvo_fused_generate(cpvo_session* s, const int32_t* prompt, int n_prompt, int n_gen, int depth,
                                   int tail, int bulk, int32_t* committed, int64_t* stats);

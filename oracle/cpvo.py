@@ -106,6 +106,8 @@ def lib():
             "cpvo_session_inject_ratio": (ctypes.c_double, [P]),
             "cpvo_prefill": (ctypes.c_int, [P, P, ctypes.c_int]),
             "cpvo_verify_step": (ctypes.c_int, [P, P, ctypes.c_int, ctypes.c_int, P, P, P, P, P, P]),
+            "cpvo_verify_step_cands": (ctypes.c_int, [P, P, ctypes.c_int, ctypes.c_int, P, P, ctypes.c_int, P, P, P,
+                                                      P, P]),
             "cpvo_fused_generate": (ctypes.c_int, [P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                                    ctypes.c_int, ctypes.c_int, P, P]),
         }
@@ -444,7 +446,7 @@ class Session:
         t = np.ascontiguousarray(tokens, dtype=np.int32)
         assert lib().cpvo_prefill(self.h, _p(t), t.size) == 0
 
-    def step_fused_cached(self, tokens, depth, want_logits=False, noise=None):
+    def step_fused_cached(self, tokens, depth, want_logits=False, noise=None, cands=None):
         t = np.ascontiguousarray(tokens, dtype=np.int32)
         T, V, E = t.size, self.model.hp.n_vocab, self.model.hp.n_embd
         preds = np.empty(T, np.int32)
@@ -453,8 +455,9 @@ class Session:
         logits = np.empty((T, V), np.float32) if want_logits else None
         hidden = np.empty((T, E), np.float32) if want_logits else None
         nz = None if noise is None else np.ascontiguousarray(noise, dtype=np.float32)
-        assert lib().cpvo_verify_step(self.h, _p(t), T, depth, _p(nz), _p(preds), _p(chain), _p(conf),
-                                      _p(logits), _p(hidden)) == 0
+        c = None if cands is None else np.ascontiguousarray(cands, dtype=np.int32)
+        assert lib().cpvo_verify_step_cands(self.h, _p(t), T, depth, _p(nz), _p(c), 0 if c is None else c.size,
+                                            _p(preds), _p(chain), _p(conf), _p(logits), _p(hidden)) == 0
         return preds, chain[:depth], conf[:depth], logits, hidden
 
     def fused_generate(self, prompt, n_gen, depth, tail=64, bulk=512):

@@ -280,8 +280,25 @@ static float peak(const float* l, int64_t V)
     return 1.0f * (float)(1.0 / sum);
 }
 
+/* The draft head over a shortlist (MtpTail::n_cand, qwen35.rs:208-216): each
+ * link's logits are the head's rows `cands` (get_rows then mul_mat,
+ * :2925-2931; the same values as the full head's columns, rows being
+ * independent), its argmax and softmax peak are over those n_cand logits, the
+ * reported draft is cands[argmax] (:1904-1910) and, as in the graph, the next
+ * link embeds the argmax itself (`tok_src = ids`, :2958). */
+int cpvo_verify_step_cands(cpvo_session* s, const int32_t* tok, int T, int depth, const float* noise,
+                           const int32_t* cands, int n_cand, int32_t* preds, int32_t* chain, float* conf,
+                           float* logits_out, float* hidden_out);
+
 int cpvo_verify_step(cpvo_session* s, const int32_t* tok, int T, int depth, const float* noise, int32_t* preds,
                      int32_t* chain, float* conf, float* logits_out, float* hidden_out)
+{
+    return cpvo_verify_step_cands(s, tok, T, depth, noise, NULL, 0, preds, chain, conf, logits_out, hidden_out);
+}
+
+int cpvo_verify_step_cands(cpvo_session* s, const int32_t* tok, int T, int depth, const float* noise,
+                           const int32_t* cands, int n_cand, int32_t* preds, int32_t* chain, float* conf,
+                           float* logits_out, float* hidden_out)
 {
     const cpvo_model* m = s->m;
     const cpvo_hparams* hp = &m->hp;
@@ -330,9 +347,19 @@ int cpvo_verify_step(cpvo_session* s, const int32_t* tok, int T, int depth, cons
             rms_rows(d, T, (int)E, E, mtp_head_norm(m), hp->rms_eps, hsrc, E);
             mm(mtp_head_w(m), hsrc, T, logits);
             for (int t = 0; t < T; t++) {
-                chain[step * T + t] = cpvo_argmax(logits + t * V, V);
-                if (conf) conf[step * T + t] = peak(logits + t * V, V);
-                tsrc[t] = chain[step * T + t];
+                if (cands && n_cand > 0) {
+                    float* lc = malloc(sizeof(float) * (size_t)n_cand);
+                    for (int j = 0; j < n_cand; j++) lc[j] = logits[t * V + cands[j]];
+                    const int32_t idx = cpvo_argmax(lc, n_cand);
+                    chain[step * T + t] = cands[idx];
+                    if (conf) conf[step * T + t] = peak(lc, n_cand);
+                    tsrc[t] = idx;
+                    free(lc);
+                } else {
+                    chain[step * T + t] = cpvo_argmax(logits + t * V, V);
+                    if (conf) conf[step * T + t] = peak(logits + t * V, V);
+                    tsrc[t] = chain[step * T + t];
+                }
             }
         }
         free(hsrc); free(e); free(cat); free(d); free(tsrc);
