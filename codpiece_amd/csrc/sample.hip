@@ -102,6 +102,52 @@ __device__ __forceinline__ FMap fcomp(FMap f, FMap g)
     return {a < FSAT ? a : FSAT, b < FSAT ? b : FSAT};
 }
 
+// Scans through DPP (no LDS round trip): row_shr:1,2,4,8 within each row of 16
+// lanes, then row_bcast:15 (rows 1 and 3 take the last lane of the row before)
+// and row_bcast:31 (rows 2 and 3 take lane 31).  A lane without a source keeps
+// `old` = the identity, and every step combines the earlier lanes' value
+// first, so a non-commutative composition scans in lane order.
+template <int C, int RM>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, C, RM, 0xf, false);
+}
+template <int C, int RM>
+__device__ __forceinline__ FMap dpp_map(FMap f)
+{
+    return {dpp_u32<C, RM>(f.d0), dpp_u32<C, RM>(f.d1)};
+}
+// inclusive scan of the wave's maps (lane i: lanes 0..i composed in order)
+__device__ __forceinline__ FMap wave_scan_maps(FMap v)
+{
+    v = fcomp(dpp_map<0x111, 0xf>(v), v);
+    v = fcomp(dpp_map<0x112, 0xf>(v), v);
+    v = fcomp(dpp_map<0x114, 0xf>(v), v);
+    v = fcomp(dpp_map<0x118, 0xf>(v), v);
+    v = fcomp(dpp_map<0x142, 0xa>(v), v);
+    v = fcomp(dpp_map<0x143, 0xc>(v), v);
+    return v;
+}
+// inclusive scan of the first 16 lanes (the lanes past them are not used)
+__device__ __forceinline__ FMap row_scan_maps(FMap v)
+{
+    v = fcomp(dpp_map<0x111, 0xf>(v), v);
+    v = fcomp(dpp_map<0x112, 0xf>(v), v);
+    v = fcomp(dpp_map<0x114, 0xf>(v), v);
+    v = fcomp(dpp_map<0x118, 0xf>(v), v);
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_scan_add(uint32_t v)
+{
+    v += dpp_u32<0x111, 0xf>(v);
+    v += dpp_u32<0x112, 0xf>(v);
+    v += dpp_u32<0x114, 0xf>(v);
+    v += dpp_u32<0x118, 0xf>(v);
+    v += dpp_u32<0x142, 0xa>(v);
+    v += dpp_u32<0x143, 0xc>(v);
+    return v;
+}
+
 // the step x/u rounded to nearest, for x >= 0 finite and u = 2^(eb - 150)
 // (eb = the biased exponent of the binade, 1 for the subnormal range)
 __device__ __forceinline__ FMap fmap_of(float x, int eb)
@@ -190,38 +236,22 @@ __device__ FoldRes block_fold(X x_at, int n, float s, float thr, int pmode, Smal
                 m[q] = base + q > done ? fmap_of(xv[q], eb) : FMap{0u, 0u};
                 acc = fcomp(acc, m[q]);
             }
-            FMap inc = acc;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                FMap o;
-                o.d0 = __shfl_up(inc.d0, off, 64);
-                o.d1 = __shfl_up(inc.d1, off, 64);
-                if (lane >= off) inc = fcomp(o, inc);
-            }
-            FMap ex;
-            ex.d0 = __shfl_up(inc.d0, 1, 64);
-            ex.d1 = __shfl_up(inc.d1, 1, 64);
-            if (lane == 0) ex = {0u, 0u};
+            const FMap inc = wave_scan_maps(acc);
+            const FMap ex = dpp_map<0x138, 0xf>(inc);      // wave_shr:1 (lane 0: the identity)
             if (lane == 63) sm->wtot[wave] = inc;
             unsigned long long* slot = sm->slot[it & 1];
             __syncthreads();
             if (tid < 2) sm->slot[(it + 1) & 1][tid] = ~0ull;
             // the waves' totals, scanned by every wave on its first SWV lanes
-            FMap wi = lane < SWV ? sm->wtot[lane] : FMap{0u, 0u};
-#pragma unroll
-            for (int off = 1; off < SWV; off <<= 1) {
-                FMap o;
-                o.d0 = __shfl_up(wi.d0, off, 64);
-                o.d1 = __shfl_up(wi.d1, off, 64);
-                if (lane >= off && lane < SWV) wi = fcomp(o, wi);
-            }
+            static_assert(SWV == 16, "one DPP row holds the wave totals");
+            const FMap wi = row_scan_maps(lane < SWV ? sm->wtot[lane] : FMap{0u, 0u});
             FMap wp = {0u, 0u}, tot;
-            const int src = wave > 0 ? wave - 1 : 0;
-            wp.d0 = __shfl(wi.d0, src, 64);
-            wp.d1 = __shfl(wi.d1, src, 64);
+            const int src = __builtin_amdgcn_readfirstlane(wave > 0 ? wave - 1 : 0);
+            wp.d0 = (uint32_t)__builtin_amdgcn_readlane((int)wi.d0, src);
+            wp.d1 = (uint32_t)__builtin_amdgcn_readlane((int)wi.d1, src);
             if (wave == 0) wp = {0u, 0u};
-            tot.d0 = __shfl(wi.d0, SWV - 1, 64);
-            tot.d1 = __shfl(wi.d1, SWV - 1, 64);
+            tot.d0 = (uint32_t)__builtin_amdgcn_readlane((int)wi.d0, SWV - 1);
+            tot.d1 = (uint32_t)__builtin_amdgcn_readlane((int)wi.d1, SWV - 1);
             const FMap pre = fcomp(wp, ex);
             uint32_t S = S0 + fsel(pre, S0);
             bool live = true;
@@ -270,12 +300,7 @@ __device__ FoldRes block_fold(X x_at, int n, float s, float thr, int pmode, Smal
 __device__ uint32_t block_excl_scan(uint32_t v, Small* sm, uint32_t* total)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    uint32_t inc = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t o = __shfl_up(inc, off, 64);
-        if (lane >= off) inc += o;
-    }
+    const uint32_t inc = wave_scan_add(v);
     __syncthreads();
     if (lane == 63) sm->scan[wave] = inc;
     __syncthreads();
