@@ -38,6 +38,7 @@ import numpy as np
 HP = dict(n_layer=64, n_embd=5120, n_head=40, n_head_kv=8, head_dim=128, n_ff=17408, n_vocab=151936,
           n_rot=128, rope_sections=(22, 22, 20, 0), rms_eps=1e-6, freq_base=1e6, has_mtp=True)
 HBM_PEAK_GBS = 8000.0
+INT8_MFMA_PEAK_TOPS = 5000.0   # dense int8 MFMA, TOP/s
 Q4_K, Q6_K, F32 = 12, 14, 0
 
 
@@ -48,6 +49,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3, help="untimed rounds before the timed ones")
     ap.add_argument("--layers", type=int, default=HP["n_layer"], help="trunk layers (64 = the workload)")
     ap.add_argument("--prompt", type=int, default=4096)
+    ap.add_argument("--prefill-chunk", type=int, default=256, help="prompt tokens per prefill call")
     ap.add_argument("--n-ctx", type=int, default=32768)
     ap.add_argument("--depth", type=int, default=4, help="drafts per round (k)")
     ap.add_argument("--profile-rounds", type=int, default=4)
@@ -265,6 +267,24 @@ def sampler_bench(torch, ctx, seed, reps=20):
     return out
 
 
+def prefill_gemm_stats(ctx, prof, hp, rows):
+    """The wide Q4_K GEMM of one prefill chunk: launches, replayed time per
+    launch, and int8 throughput against the dense MFMA peak (multiply-adds
+    per token and layer: the q|gate|k|v, wo, gate|up and down projections)."""
+    n, ms, _ = prof.get("qgemm_q4_k_wide", (0, 0.0, 0.0))
+    if not n:
+        return None
+    rep_ms, rep_bytes = ctx.profile_replay("qgemm_q4_k_wide", reps=3)
+    E, F = hp["n_embd"], hp["n_ff"]
+    attn = 2 * hp["n_head"] * hp["head_dim"] + 2 * hp["n_head_kv"] * hp["head_dim"]
+    macs = rows * hp["n_layer"] * E * (attn + E + 2 * F + F)
+    tops = 2.0 * macs / (n * rep_ms * 1e-3) / 1e12
+    return {"rows": rows, "launches": n, "us_per_launch_replayed": round(rep_ms * 1e3, 2),
+            "us_per_launch_event_bracketed": round(ms / n * 1e3, 2),
+            "int8_TOP_s": round(tops, 1), "roofline": {"bound": "mfma", "peak": INT8_MFMA_PEAK_TOPS,
+                                                       "unit": "TOP/s", "frac": round(tops / INT8_MFMA_PEAK_TOPS, 4)}}
+
+
 # ---------------------------------------------------------------- main
 def gguf_load_bench(ctx, layers, seed):
     """Weights::load of a seeded 27B-class qwen35 file (Q4_K linears, Q6_K
@@ -325,14 +345,31 @@ def main():
     torch.cuda.synchronize()
     print(f"[bench] model built: {wbytes / 1e9:.2f} GB quantized weights in {time.perf_counter() - t0:.1f} s",
           file=sys.stderr, flush=True)
-    sess = Session(model, args.n_ctx, max_batch=64)
+    chunk = max(64, min(args.prefill_chunk, 256))
+    sess = Session(model, args.n_ctx, max_batch=chunk)
     g = torch.Generator().manual_seed(args.seed + 1)
     prompt = torch.randint(0, hp["n_vocab"], (args.prompt,), generator=g).tolist()
+    # the prefill's GEMMs over one chunk, each launch timed, then rewound
+    pchunk = min(chunk, args.prompt)
+    sess.prefill(prompt[:pchunk])      # (sizes the workspaces the profiled launches keep using)
+    sess.set_pos(0, 0)
+    ctx.profile_start()
+    sess.prefill(prompt[:pchunk])
+    pprof = ctx.profile_stop()
+    sess.set_pos(0, 0)
+    prefill_gemm = prefill_gemm_stats(ctx, pprof, hp, pchunk)
     loop = Loop(sess, args.depth)
-    t0 = time.perf_counter()
-    loop.start(prompt)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    print(f"[bench] prefill of {args.prompt} tokens: {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    e0.record()
+    loop.start(prompt, bulk=chunk)
+    e1.record()
+    torch.cuda.synchronize()
+    prefill_wall = time.perf_counter() - t0
+    prefill_dev = e0.elapsed_time(e1) * 1e-3
+    print(f"[bench] prefill of {args.prompt} tokens in {chunk}-token chunks: {prefill_wall:.2f} s "
+          f"({prefill_dev:.2f} s device, {args.prompt / prefill_dev:.0f} tok/s)", file=sys.stderr, flush=True)
 
     for _ in range(args.warmup):
         loop.round()
@@ -450,6 +487,9 @@ def main():
                                    "us_per_launch_event_bracketed": round(v[1] / v[0] * 1e3, 2)}
                                for k, v in prof.items() if v[0]},
             "profiled_rounds": args.profile_rounds,
+            "prefill": {"tokens": args.prompt, "chunk": chunk, "wall_s": round(prefill_wall, 3),
+                        "device_s": round(prefill_dev, 3), "tokens_per_s": round(args.prompt / prefill_dev, 1),
+                        "gemm_q4_k_wide": prefill_gemm},
             "acceptance_sampler": sampler,
         },
     }

@@ -185,6 +185,12 @@ extern "C" cpv_status cpv_profile_replay(cpv_ctx* ctx, int cls, int reps, double
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     CPV_HIP(ctx, hipGetLastError());
+    // a replayed GEMM without its consumer leaves sums in the split-K
+    // accumulator, which every GEMM expects to find zero
+    if (ctx->gsum) {
+        CPV_HIP(ctx, hipMemsetAsync(ctx->gsum, 0, ctx->gsum_bytes, ctx->stream));
+        CPV_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    }
     *ms_per_launch = (double)ms / ((double)reps * (double)sel.size());
     if (bytes_per_launch) *bytes_per_launch = bytes / (double)sel.size();
     return CPV_OK;

@@ -725,6 +725,14 @@ cpv_status cpv_qgemm_act(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, 
                : w->type == CPV_Q6_K ? lds_of<CPV_Q6_K>(M, a.nu_max, a.nt_max)
                                      : lds_of<CPV_Q8_0>(M, a.nu_max, a.nt_max);
     };
+    if (cpv_qgemm_wide_ok(w, m)) {
+        if ((st = cpv_qgemm_wide(ctx, w, act, a.gsum, a.win)) != CPV_OK) return st;
+        if (y)
+            qgemm_finalize_kernel<<<dim3((unsigned)((w->n + 255) / 256), (unsigned)m), 256, 0, ctx->stream>>>(
+                a.gsum, a.n_pad, a.ew, a.da, U, 0, a.win, y, w->n);
+        CPV_HIP(ctx, hipGetLastError());
+        return CPV_OK;
+    }
     const size_t lds_cap = ctx->lds_max - 1024;
     for (int64_t m0 = 0; m0 < m;) {
         int M = (int)((m - m0) < 8 ? (m - m0) : 8);
@@ -770,7 +778,7 @@ cpv_status cpv_qgemm_launch(cpv_ctx* ctx, const cpv_weight* w, const float* x, i
 extern "C" cpv_status cpv_qgemm(cpv_ctx* ctx, const cpv_weight* w, const float* x_dev, int64_t m, float* y_dev)
 {
     if (!ctx || !w || !x_dev || !y_dev) return cpv_fail(ctx, CPV_EINVAL, "qgemm: null argument");
-    if (m < 1 || m > 64) return cpv_fail(ctx, CPV_EINVAL, "qgemm: m=%lld outside [1, 64]", (long long)m);
+    if (m < 1 || m > 256) return cpv_fail(ctx, CPV_EINVAL, "qgemm: m=%lld outside [1, 256]", (long long)m);
     if (w->ctx != ctx) return cpv_fail(ctx, CPV_EINVAL, "qgemm: weight belongs to another context");
     return cpv_qgemm_launch(ctx, w, x_dev, m, y_dev);
 }

@@ -86,7 +86,8 @@ cpv_status  cpv_get_rows(cpv_ctx* ctx, const cpv_weight* w, const int32_t* rows_
  * result does not depend on how the K loop is split.
  * Replaces every ggml_mul_mat on the verify path (qwen35.rs:2779-2782,2797,
  * 3029,3047,3051,3197; mtp_graph.rs:184,209-212,230).  x_dev: f32 [m][k];
- * y_dev: f32 [m][n_rows]; 1 <= m <= 64. */
+ * y_dev: f32 [m][n_rows]; 1 <= m <= 256 (Q4_K from 32 rows on: the wide
+ * prefill kernel, the same sums). */
 cpv_status  cpv_qgemm(cpv_ctx* ctx, const cpv_weight* w, const float* x_dev, int64_t m,
                       float* y_dev);
 
@@ -321,7 +322,7 @@ cpv_status  cpv_session_commit_branch(cpv_session* s, const int32_t* path_host, 
  * rows read once).  The events add a little time between launches: time
  * throughput without them. */
 enum { CPV_PROF_Q4_K = 0, CPV_PROF_Q6_K = 1, CPV_PROF_Q8_0 = 2, CPV_PROF_ATTN = 3, CPV_PROF_SAMPLE = 4,
-       CPV_PROF_CLASSES = 5 };
+       CPV_PROF_Q4_K_WIDE = 5, CPV_PROF_CLASSES = 6 };
 typedef struct { int64_t launches; double ms; double bytes; } cpv_prof_stat;
 cpv_status  cpv_profile_start(cpv_ctx* ctx);
 cpv_status  cpv_profile_stop(cpv_ctx* ctx, cpv_prof_stat* out /* [CPV_PROF_CLASSES] */);
@@ -330,7 +331,8 @@ cpv_status  cpv_profile_stop(cpv_ctx* ctx, cpv_prof_stat* out /* [CPV_PROF_CLASS
  * of events: *ms_per_launch = elapsed / (reps * launches), free of the gaps
  * the per-launch events add; *bytes_per_launch (may be NULL) their mean
  * algorithmic bytes.  The buffers of the recorded calls (weights, sessions)
- * must still be allocated; their outputs are overwritten. */
+ * must still be allocated; their outputs are overwritten, and the GEMM
+ * accumulator is left zero (as every GEMM expects it). */
 cpv_status  cpv_profile_replay(cpv_ctx* ctx, int cls, int reps, double* ms_per_launch, double* bytes_per_launch);
 
 #ifdef __cplusplus

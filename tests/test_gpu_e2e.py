@@ -227,6 +227,27 @@ def test_q4k_model_rounds_and_stream_are_bit_exact(kmodels):
     o.free()
 
 
+def test_q4k_long_prefill_chunks_are_bit_exact(kmodels):
+    # the prompt prefill at the chunk sizes the wide Q4_K GEMM takes: 256 rows
+    # (four full row blocks), then 37 (a partial one), then a round on top
+    from codpiece_amd.model import Session
+    ctx, gm, om = kmodels
+    rng = np.random.default_rng(9)
+    prompt = rng.integers(0, K_MODEL["n_vocab"], size=300).tolist()
+    g, o = Session(gm, 512, max_batch=256), cpvo.Session(om, 512)
+    for c0, c1 in ((0, 256), (256, 293)):
+        print(f"prefill {c0}:{c1}", flush=True)
+        g.prefill(prompt[c0:c1])
+        o.prefill(prompt[c0:c1])
+    a = g.step_fused_cached(prompt[293:298], 4, want_logits=True)
+    b = o.step_fused_cached(prompt[293:298], 4, want_logits=True)
+    assert np.array_equal(a.logits.cpu().numpy().view(np.uint32), b[3].view(np.uint32))
+    assert np.array_equal(a.hidden.cpu().numpy().view(np.uint32), b[4].view(np.uint32))
+    assert a.preds == b[0].tolist() and a.chain == b[1].tolist()
+    g.free()
+    o.free()
+
+
 W_MODEL = dict(mf.TINY, n_layer=1, n_embd=5120, n_head=40, n_head_kv=8, head_dim=128, n_rot=128,
                rope_sections=[22, 22, 20, 0], n_ff=1536, n_vocab=2048)
 

@@ -91,10 +91,60 @@ def test_qgemm_extreme_scales_and_zero_rows(ctx):
     assert np.all(y[1] == 0) and np.all(y[:, 5] == 0)
 
 
+# ---- the wide Q4_K kernel (32 rows and more: the prompt prefill)
+
+@pytest.mark.parametrize("n,k", [(64, 256), (1000, 768), (33, 1024), (160, 4096)])
+@pytest.mark.parametrize("m", [32, 37, 64, 100, 256])
+def test_qgemm_wide_bit_exact_small(ctx, n, k, m):
+    y, ref = run_case(ctx, cpvo.Q4_K, n, k, m)
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), np.abs(y - ref).max()
+
+
+@pytest.mark.parametrize("k,n", [(5120, 7168), (5120, 5120), (5120, 17408), (17408, 5120)])
+@pytest.mark.parametrize("m", [64, 256])
+def test_qgemm_wide_bit_exact_prefill_shapes(ctx, k, n, m):
+    y, ref = run_case(ctx, cpvo.Q4_K, n, k, m)
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), np.abs(y - ref).max()
+
+
+def test_qgemm_wide_rows_match_the_skinny_kernel(ctx):
+    # a row's outputs do not depend on the rows batched with it: the wide
+    # launch over 96 rows against the skinny kernel on 8-row slices
+    n, k = 5120, 17408
+    wq = weights(cpvo.Q4_K, n, k)
+    x = torch.from_numpy(np.random.default_rng(11).normal(0, 1, size=(96, k)).astype(np.float32)).cuda()
+    w = ctx.upload_weight(cpvo.Q4_K, wq, n, k)
+    yw = ctx.qgemm(w, x).cpu().numpy()
+    for r in range(0, 96, 8):
+        ys = ctx.qgemm(w, x[r:r + 8].contiguous()).cpu().numpy()
+        assert np.array_equal(yw[r:r + 8].view(np.uint32), ys.view(np.uint32)), r
+    w.free()
+
+
+def test_qgemm_wide_extreme_scales_and_zero_rows(ctx):
+    t = cpvo.Q4_K
+    n, k = 96, 1280
+    rng = np.random.default_rng(4)
+    wf = rng.normal(0, 0.02, size=(n, k)).astype(np.float32)
+    wf[5] = 0.0
+    wf[70] *= 1e3
+    wq = cpvo.quantize(t, wf)
+    x = rng.normal(0, 1, size=(70, k)).astype(np.float32)
+    x[1] = 0.0
+    x[2] *= 1e-6
+    x[65] *= 1e4
+    w = ctx.upload_weight(t, wq, n, k)
+    y = ctx.qgemm(w, torch.from_numpy(x).cuda()).cpu().numpy()
+    ref = cpvo.qgemm(t, wq, x)
+    w.free()
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+    assert np.all(y[1] == 0) and np.all(y[:, 5] == 0)
+
+
 def test_qgemm_rejects_bad_shapes(ctx):
     from codpiece_amd import CpvError
     w = ctx.upload_weight(cpvo.Q8_0, weights(cpvo.Q8_0, 16, 64), 16, 64)
-    x = torch.zeros((65, 64), dtype=torch.float32, device="cuda")
+    x = torch.zeros((257, 64), dtype=torch.float32, device="cuda")
     with pytest.raises(CpvError):
         ctx.qgemm(w, x)
     with pytest.raises(CpvError):
