@@ -512,6 +512,16 @@ __device__ __noinline__ int emit_band(const float* lg, int V, bool have_last, un
 }
 
 // ------------------------------------------------------------ distributions
+// the split top-p build's state per row: the row maximum in EXP_SPLIT
+// parts, then what its first launch leaves for the second
+constexpr int EXP_SPLIT = 32;
+struct DistState {
+    float sum1;                 // the index-order sum of exp(l - max)
+    int cnt;                    // size of the first band
+    unsigned long long last;    // its last key
+    float pmax[EXP_SPLIT];      // fmaxf over each part of the row
+};
+
 struct DistArgs {
     const float* p_logits;      // spec: [B][k+1][V]; direct: [rows][V]
     const float* q_logits;      // spec only: [B][k][V] or NULL
@@ -526,6 +536,9 @@ struct DistArgs {
     float* sl;                  // [rows][V] their (penalised, untempered) logits
     float* pr;                  // [rows][V] their probabilities
     int32_t* hdr;               // [rows] candidate count
+    int phase;                  // 0: the whole build; top-p split: 1 (two workgroups per row), then 2
+    int pre_exp;                // top-p: pr already holds expf(l - max) (exp_kernel)
+    DistState* st;              // [rows] (phases 1 and 2)
 };
 
 // Penalties (lib.rs:233-266): a dense copy of the row in which every token
@@ -586,6 +599,41 @@ __device__ const float* apply_penalties(const float* logits, float* pen, int V, 
     return pen;
 }
 
+// the logits row `row` of the build (penalties off)
+__device__ __forceinline__ const float* row_logits(const DistArgs& a, int row)
+{
+    if (a.direct || row < a.nrow_p) return a.p_logits + (size_t)row * a.V;
+    return a.q_logits + (size_t)(row - a.nrow_p) * a.V;
+}
+
+// The split top-p build's first two launches, EXP_SPLIT workgroups per row:
+// the row maximum in parts (fmaxf is order-free), then pr[i] = expf(l - max)
+// by index, as the one-workgroup build computes them.
+__global__ __launch_bounds__(256) void rowmax_part_kernel(DistArgs a)
+{
+    const int part = blockIdx.x, row = blockIdx.y, V = a.V, tid = threadIdx.x;
+    const float* lg = row_logits(a, row);
+    const int per = (V + EXP_SPLIT - 1) / EXP_SPLIT, i0 = part * per, i1 = min(V, i0 + per);
+    float m = -INFINITY;
+    for (int i = i0 + tid; i < i1; i += 256) m = fmaxf(m, lg[i]);
+    m = cpv_wave_reduce(m, cpv_op_max());
+    __shared__ float s_m[4];
+    if ((tid & 63) == 0) s_m[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0) a.st[row].pmax[part] = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+}
+
+__global__ __launch_bounds__(256) void exp_kernel(DistArgs a)
+{
+    const int part = blockIdx.x, row = blockIdx.y, V = a.V, tid = threadIdx.x;
+    const float* lg = row_logits(a, row);
+    float mx = -INFINITY;
+    for (int q = 0; q < EXP_SPLIT; q++) mx = fmaxf(mx, a.st[row].pmax[q]);
+    float* pr = a.pr + (size_t)row * V;
+    const int per = (V + EXP_SPLIT - 1) / EXP_SPLIT, i0 = part * per, i1 = min(V, i0 + per);
+    for (int i = i0 + tid; i < i1; i += 256) pr[i] = cpv_expf(lg[i] - mx);
+}
+
 // Sampler::build for one row (lib.rs:229-376), leaving the distribution as
 // n candidates (sid, sl, pr) in candidate order.
 __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
@@ -593,7 +641,12 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
     extern __shared__ __align__(16) unsigned char sdyn[];
     unsigned long long* keys = (unsigned long long*)sdyn;
     Small* sm = (Small*)(sdyn + SAMPLE_LDS_KEYS);
-    const int tid = threadIdx.x, row = blockIdx.x, V = a.V;
+    // the split top-p build: after rowmax_part_kernel and exp_kernel, in
+    // phase 1 workgroup 2 r sums row r's exponentials in index order while
+    // workgroup 2 r + 1 emits its first band (the two need nothing from each
+    // other); phase 2 goes on from both
+    const int tid = threadIdx.x, row = a.phase == 1 ? (int)(blockIdx.x >> 1) : (int)blockIdx.x, V = a.V;
+    const int role = a.phase == 1 ? (int)(blockIdx.x & 1) : 0;
     const cpv_sampler_params& P = a.prm;
     const float* logits;
     const int32_t* hist = nullptr;
@@ -639,7 +692,9 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
     const bool top_k = P.top_k > 0 && P.top_k < V;         // :272-280
     const bool min_p = !top_k && P.min_p > 0.0f;           // :281-295
     const bool top_p = !top_k && !min_p && P.top_p < 1.0f; // :296-316
-    const float mx = block_max([&](int i) { return lg[i]; }, V, sm);
+    // (the split build needs no maximum here: exp_kernel has used it, and
+    // top-p's final softmax is relative to the first candidate)
+    const float mx = a.phase != 0 || a.pre_exp ? 0.0f : block_max([&](int i) { return lg[i]; }, V, sm);
     int n;
     if (top_k || min_p || top_p) {
         int M = 0, emitted = 0;
@@ -657,20 +712,44 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
             // read off one fold of the probabilities in candidate order
             // e_i = expf(l_i - max) once, by index, in the probabilities' row (the
             // final probabilities overwrite it at the end)
-            strided(V, [&](int i) { return lg[i]; }, [&](int i, float l) { pr[i] = cpv_expf(l - mx); });
-            __syncthreads();
-            const float sum1 = block_fold([&](int i) { return pr[i]; }, V, 0.0f, 0.0f, F_NONE, sm).sum;
+            float sum1 = 0.0f;
+            int cnt;
+            if (a.phase == 2) {
+                sum1 = a.st[row].sum1;
+                cnt = a.st[row].cnt;
+                last = a.st[row].last;
+            } else {
+                if (role == 0) {
+                    if (!a.pre_exp) {   // (else they come from exp_kernel)
+                        strided(V, [&](int i) { return lg[i]; }, [&](int i, float l) { pr[i] = cpv_expf(l - mx); });
+                        __syncthreads();
+                    }
+                    sum1 = block_fold([&](int i) { return pr[i]; }, V, 0.0f, 0.0f, F_NONE, sm).sum;
+                    if (a.phase == 1) {
+                        if (tid == 0) a.st[row].sum1 = sum1;
+                        return;
+                    }
+                }
+                cnt = emit_band(lg, V, false, &last, BAND, 0, sid, sl, keys, sm);
+                if (a.phase == 1) {
+                    if (tid == 0) {
+                        a.st[row].cnt = cnt;
+                        a.st[row].last = last;
+                    }
+                    return;
+                }
+            }
             float s = 0.0f;
             int ifirst = -1;
-            while (emitted < V) {
-                const int cnt = emit_band(lg, V, emitted > 0, &last, BAND, emitted, sid, sl, keys, sm);
-                if (cnt <= 0) break;
+            while (cnt > 0) {
                 const int32_t* band = sid + emitted;
                 const FoldRes r = block_fold([&](int i) { return pr[band[i]] / sum1; }, cnt, s, P.top_p, F_GE, sm);
                 if (r.idx >= 0) ifirst = emitted + r.idx;
                 emitted += cnt;
                 if (r.idx >= 0) break;
                 s = r.sum;
+                if (emitted >= V) break;
+                cnt = emit_band(lg, V, true, &last, BAND, emitted, sid, sl, keys, sm);
             }
             int probe = V < 1024 ? V : 1024;
             if (ifirst < 0) probe = V;
@@ -933,6 +1012,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct DistBufs {
     int32_t* hdr;
+    DistState* st;
     int32_t* sid;
     float* sl;
     float* pr;
@@ -943,7 +1023,7 @@ struct DistBufs {
 size_t dist_bytes(int rows, int V, bool pen)
 {
     const size_t rv = align256((size_t)rows * V * 4);
-    return align256((size_t)rows * 4) + 3 * rv + (pen ? rv : 0);
+    return align256((size_t)rows * 4) + align256((size_t)rows * sizeof(DistState)) + 3 * rv + (pen ? rv : 0);
 }
 
 DistBufs dist_carve(void* ws, int rows, int V, bool pen)
@@ -953,6 +1033,8 @@ DistBufs dist_carve(void* ws, int rows, int V, bool pen)
     DistBufs d;
     d.hdr = (int32_t*)p;
     p += align256((size_t)rows * 4);
+    d.st = (DistState*)p;
+    p += align256((size_t)rows * sizeof(DistState));
     d.sid = (int32_t*)p;
     p += rv;
     d.sl = (float*)p;
@@ -970,7 +1052,26 @@ cpv_status dist_launch(cpv_ctx* ctx, DistArgs& a, int rows)
     const size_t lds = SAMPLE_LDS_KEYS + sizeof(Small);
     if (lds > ctx->lds_max) return cpv_fail(ctx, CPV_EUNSUPPORTED, "sampler: needs %zu bytes of LDS", lds);
     const int e0 = cpv_prof_mark(ctx);
-    dist_kernel<<<(unsigned)rows, SB, lds, ctx->stream>>>(a);
+    // top-p without penalties: the maximum and the exponentials over
+    // EXP_SPLIT workgroups per row; then, when two workgroups per row fit the
+    // CUs, the index-order sum and the first band side by side (two
+    // workgroups per row), then the rest
+    const cpv_sampler_params& P = a.prm;
+    const bool top_k = P.top_k > 0 && P.top_k < a.V;
+    a.pre_exp = P.temp > 0.0f && !top_k && !(P.min_p > 0.0f) && P.top_p < 1.0f && !a.pen_on;
+    if (a.pre_exp) {
+        rowmax_part_kernel<<<dim3(EXP_SPLIT, (unsigned)rows), 256, 0, ctx->stream>>>(a);
+        exp_kernel<<<dim3(EXP_SPLIT, (unsigned)rows), 256, 0, ctx->stream>>>(a);
+    }
+    if (a.pre_exp && 2 * rows <= ctx->cu_count) {
+        a.phase = 1;
+        dist_kernel<<<(unsigned)(2 * rows), SB, lds, ctx->stream>>>(a);
+        a.phase = 2;
+        dist_kernel<<<(unsigned)rows, SB, lds, ctx->stream>>>(a);
+    } else {
+        a.phase = 0;
+        dist_kernel<<<(unsigned)rows, SB, lds, ctx->stream>>>(a);
+    }
     CPV_HIP(ctx, hipGetLastError());
     cpv_prof_add(ctx, e0, CPV_PROF_SAMPLE, (double)rows * a.V * 4.0);
     return CPV_OK;
@@ -1006,6 +1107,7 @@ extern "C" cpv_status cpv_distribution(cpv_ctx* ctx, const float* logits_dev, in
     a.sl = d.sl;
     a.pr = probs_dev;
     a.hdr = n_dev;
+    a.st = d.st;
     return dist_launch(ctx, a, rows);
 }
 
@@ -1063,6 +1165,7 @@ extern "C" cpv_status cpv_spec_accept(cpv_ctx* ctx, const float* p_logits_dev, c
     a.sl = d.sl;
     a.pr = d.pr;
     a.hdr = d.hdr;
+    a.st = d.st;
     if ((st = dist_launch(ctx, a, rows))) return st;
     DecideArgs c{};
     c.draft = draft_dev;

@@ -80,6 +80,17 @@ def test_distribution_headline_rows(ctx, name):
     check_dist(ctx, logits, cpvo.SamplerParams(**DIST_CASES[name]))
 
 
+@pytest.mark.parametrize("rows", [60, 140])
+def test_distribution_top_p_row_counts(ctx, rows):
+    # top-p builds: the maximum and exponentials over many workgroups per
+    # row, then the index-order sum and the first band side by side when two
+    # workgroups per row fit the 256 CUs (60 rows), else one per row (140)
+    print(f"case dist top-p rows={rows}", flush=True)
+    rng = np.random.default_rng(rows)
+    logits = spiked(rng, (rows, 8192))
+    check_dist(ctx, logits, cpvo.SamplerParams(temp=0.7, top_p=0.95))
+
+
 def test_distribution_penalties_with_history(ctx):
     print("case dist penalties", flush=True)
     rng = np.random.default_rng(7)
