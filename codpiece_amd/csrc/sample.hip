@@ -43,6 +43,7 @@ constexpr int FIPT = 8;                // fold: elements per thread per window
 constexpr int BU = 8;                  // strided loops: loads issued ahead of their uses
 constexpr uint32_t FTOP = 1u << 24;    // fold: ulps from 0 to the top of a binade
 constexpr uint32_t FSAT = 1u << 26;    // fold: saturation of a composed step
+constexpr int FOLD_SEQ = 1024;         // index-order sums: leading elements added by one thread
 constexpr int BAND = 16384;            // sorted band held in LDS as u64 keys
 constexpr int HIST_MAX = 4096;         // penalty window input limit (4 per thread)
 constexpr int VMAX = 262144;           // ids fit the low 18 bits of a key
@@ -202,16 +203,32 @@ __device__ __forceinline__ bool fpred(int mode, float v, float thr)
 // Sequential f32 fold s = s + x(i), i = 0..n-1, of non-negative finite x,
 // bit-identical to the loop, with an optional monotone predicate on the
 // running value (F_GE: s_i >= thr, F_GT: s_i > thr) whose first hit ends the
-// fold.  Called by every thread of the block with the same arguments.
+// fold.  Called by every thread of the block with the same arguments.  With
+// seq > 0 (no predicate) one thread adds the first seq elements itself, in
+// order: a sum that starts small leaves a binade every time it doubles, and
+// each exit costs a block pass, so a fold from 0 over values of one size
+// meets most of its exits in its first few hundred elements.
 template <class X>
-__device__ FoldRes block_fold(X x_at, int n, float s, float thr, int pmode, Small* sm)
+__device__ FoldRes block_fold(X x_at, int n, float s, float thr, int pmode, Small* sm, int seq = 0)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     __syncthreads();
     if (tid < 4) (&sm->slot[0][0])[tid] = ~0ull;
+    int start0 = 0;
+    if (seq > 0 && pmode == F_NONE) {
+        start0 = seq < n ? seq : n;
+        if (tid == 0) {
+            float t = s;
+#pragma unroll 16
+            for (int i = 0; i < start0; i++) t = t + x_at(i);
+            sm->wf[0] = t;
+        }
+        __syncthreads();
+        s = sm->wf[0];
+    }
     __syncthreads();
     int it = 0;
-    for (int start = 0; start < n; start += SB * FIPT) {
+    for (int start = start0; start < n; start += SB * FIPT) {
         const int base = start + tid * FIPT;
         float xv[FIPT];
 #pragma unroll
@@ -724,7 +741,7 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
                         strided(V, [&](int i) { return lg[i]; }, [&](int i, float l) { pr[i] = cpv_expf(l - mx); });
                         __syncthreads();
                     }
-                    sum1 = block_fold([&](int i) { return pr[i]; }, V, 0.0f, 0.0f, F_NONE, sm).sum;
+                    sum1 = block_fold([&](int i) { return pr[i]; }, V, 0.0f, 0.0f, F_NONE, sm, FOLD_SEQ).sum;
                     if (a.phase == 1) {
                         if (tid == 0) a.st[row].sum1 = sum1;
                         return;
