@@ -88,6 +88,39 @@ __device__ __forceinline__ void strided(int n, L load, U use)
     }
 }
 
+// use(i, x[i]) for every i < n in some order, for a row x of floats: 16-byte
+// loads, BU of them in flight per thread (4x the bytes of strided, for the
+// latency-bound passes over a whole vocabulary row); rows that are not
+// 16-byte aligned, or whose length is not a multiple of 4, take strided
+template <class U>
+__device__ __forceinline__ void row_pass(const float* x, int n, U use)
+{
+    if ((n & 3) || ((uintptr_t)x & 15)) {
+        strided(n, [&](int i) { return x[i]; }, use);
+        return;
+    }
+    const int n4 = n >> 2;
+    const float4* x4 = (const float4*)x;
+    for (int j0 = threadIdx.x; j0 < n4; j0 += SB * BU) {
+        float4 v[BU];
+#pragma unroll
+        for (int q = 0; q < BU; q++) {
+            const int j = j0 + q * SB;
+            v[q] = x4[j < n4 ? j : n4 - 1];
+        }
+#pragma unroll
+        for (int q = 0; q < BU; q++) {
+            const int j = j0 + q * SB;
+            if (j < n4) {
+                use(4 * j, v[q].x);
+                use(4 * j + 1, v[q].y);
+                use(4 * j + 2, v[q].z);
+                use(4 * j + 3, v[q].w);
+            }
+        }
+    }
+}
+
 // the step of m for an S of parity par (arithmetic select: a ?: on the two
 // fields lets the compiler address a register array by parity)
 __device__ __forceinline__ uint32_t fsel(FMap m, uint32_t par)
@@ -446,7 +479,7 @@ __device__ __noinline__ int emit_band(const float* lg, int V, bool have_last, un
         __syncthreads();
         for (int b = tid; b < nb; b += SB) hist[b] = 0;
         __syncthreads();
-        strided(V, [&](int i) { return lg[i]; }, [&](int i, float l) {
+        row_pass(lg, V, [&](int i, float l) {
             const unsigned long long key = cand_key(l, i);
             if ((have_last && key <= last) || (key & fixed) != prefix) return;
             atomicAdd(&hist[(key >> sh) & (unsigned long long)(nb - 1)], 1u);
@@ -494,10 +527,10 @@ __device__ __noinline__ int emit_band(const float* lg, int V, bool have_last, un
     __syncthreads();
     if (tid == 0) sm->iv[3] = 0;
     __syncthreads();
-    strided(V, [&](int i) { return lg[i]; }, [&](int i, float l) {
+    row_pass(lg, V, [&](int i, float l) {
         const unsigned long long key = cand_key(l, i);
         if ((have_last && key <= last) || key > hi) return;
-        keys[atomicAdd(&sm->iv[3], 1)] = key;
+        keys[atomicAdd(&sm->iv[3], 1)] = key;   // (the band is sorted below: any order)
     });
     __syncthreads();
     const int cnt = sm->iv[3];
@@ -510,15 +543,25 @@ __device__ __noinline__ int emit_band(const float* lg, int V, bool have_last, un
         k[q] = key == ~0ull ? (1ull << KEY_BITS) - 1 : ((key >> 32) << 18) | (key & 0x3ffffull);
     }
     __syncthreads();                           // the key buffer becomes the sort's storage
-    band_sort_t().sort(k, *reinterpret_cast<band_sort_t::storage_type*>(keys), 0, KEY_BITS);
-    // thread t now holds positions t*IPT .. t*IPT + IPT-1 of the band
+    band_sort_t().sort_to_striped(k, *reinterpret_cast<band_sort_t::storage_type*>(keys), 0, KEY_BITS);
+    // thread t now holds positions t, t + SB, ... of the band (striped: the
+    // stores coalesce); every logit load goes out before the first store
+    // (padding keys read id 0).  The positions are formed anew here: values
+    // kept across the sort were spilled and reloaded one store at a time.
+    int tb = tid;
+    asm volatile("" : "+v"(tb));
+    float lv[IPT];
 #pragma unroll
     for (int q = 0; q < IPT; q++) {
-        const int t = tid * IPT + q;
+        const int t = tb + q * SB;
+        lv[q] = lg[t < cnt ? (int)(k[q] & 0x3ffffull) : 0];
+    }
+#pragma unroll
+    for (int q = 0; q < IPT; q++) {
+        const int t = tb + q * SB;
         if (t < cnt) {
-            const int id = (int)(k[q] & 0x3ffffull);
-            sid[pos + t] = id;
-            sl[pos + t] = lg[id];
+            sid[pos + t] = (int)(k[q] & 0x3ffffull);
+            sl[pos + t] = lv[q];
             if (t == cnt - 1) sm->last = ((k[q] >> 18) << 32) | (k[q] & 0x3ffffull);
         }
     }
