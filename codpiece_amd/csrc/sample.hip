@@ -43,7 +43,7 @@ constexpr int FIPT = 8;                // fold: elements per thread per window
 constexpr int BU = 8;                  // strided loops: loads issued ahead of their uses
 constexpr uint32_t FTOP = 1u << 24;    // fold: ulps from 0 to the top of a binade
 constexpr uint32_t FSAT = 1u << 26;    // fold: saturation of a composed step
-constexpr int FOLD_SEQ = 1024;         // index-order sums: leading elements added by one thread
+constexpr int FOLD_SEQ = 1024;         // folds: leading elements added by one thread
 constexpr int BAND = 16384;            // sorted band held in LDS as u64 keys
 constexpr int HIST_MAX = 4096;         // penalty window input limit (4 per thread)
 constexpr int VMAX = 262144;           // ids fit the low 18 bits of a key
@@ -237,10 +237,11 @@ __device__ __forceinline__ bool fpred(int mode, float v, float thr)
 // bit-identical to the loop, with an optional monotone predicate on the
 // running value (F_GE: s_i >= thr, F_GT: s_i > thr) whose first hit ends the
 // fold.  Called by every thread of the block with the same arguments.  With
-// seq > 0 (no predicate) one thread adds the first seq elements itself, in
-// order: a sum that starts small leaves a binade every time it doubles, and
-// each exit costs a block pass, so a fold from 0 over values of one size
-// meets most of its exits in its first few hundred elements.
+// seq > 0 (no predicate; x_at a plain load, so that the loop can issue its
+// loads ahead) one thread adds the first seq elements itself, in order: a sum
+// leaves a binade every time it doubles and each exit costs a block pass, so
+// a fold from 0 over values of one size, or over values sorted largest first
+// from 1, meets most of its exits in its first few hundred elements.
 template <class X>
 __device__ FoldRes block_fold(X x_at, int n, float s, float thr, int pmode, Small* sm, int seq = 0)
 {
@@ -860,7 +861,7 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
     __syncthreads();
     strided(n, [&](int i) { return sl[i]; }, [&](int i, float l) { pr[i] = cpv_expf(l / T - mx2); });
     __syncthreads();
-    const float s2 = block_fold([&](int i) { return pr[i]; }, n, 0.0f, 0.0f, F_NONE, sm).sum;
+    const float s2 = block_fold([&](int i) { return pr[i]; }, n, 0.0f, 0.0f, F_NONE, sm, FOLD_SEQ).sum;
     __syncthreads();
     strided(n, [&](int i) { return pr[i]; }, [&](int i, float e) { pr[i] = e / s2; });
     if (tid == 0) a.hdr[row] = n;
