@@ -248,6 +248,25 @@ def test_q4k_long_prefill_chunks_are_bit_exact(kmodels):
     o.free()
 
 
+def test_q4k_prefill_of_600_rows_is_bit_exact(kmodels):
+    # one prefill call past the cpv_qgemm row limit: ten 64-row blocks of the
+    # wide GEMM, the last one partial (24 rows)
+    from codpiece_amd.model import Session
+    ctx, gm, om = kmodels
+    rng = np.random.default_rng(10)
+    prompt = rng.integers(0, K_MODEL["n_vocab"], size=605).tolist()
+    g, o = Session(gm, 1024, max_batch=600), cpvo.Session(om, 1024)
+    g.prefill(prompt[:600])
+    o.prefill(prompt[:600])
+    a = g.step_fused_cached(prompt[600:605], 4, want_logits=True)
+    b = o.step_fused_cached(prompt[600:605], 4, want_logits=True)
+    assert np.array_equal(a.logits.cpu().numpy().view(np.uint32), b[3].view(np.uint32))
+    assert np.array_equal(a.hidden.cpu().numpy().view(np.uint32), b[4].view(np.uint32))
+    assert a.preds == b[0].tolist() and a.chain == b[1].tolist()
+    g.free()
+    o.free()
+
+
 W_MODEL = dict(mf.TINY, n_layer=1, n_embd=5120, n_head=40, n_head_kv=8, head_dim=128, n_rot=128,
                rope_sections=[22, 22, 20, 0], n_ff=1536, n_vocab=2048)
 
