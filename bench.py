@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3, help="untimed rounds before the timed ones")
     ap.add_argument("--layers", type=int, default=HP["n_layer"], help="trunk layers (64 = the workload)")
     ap.add_argument("--prompt", type=int, default=4096)
-    ap.add_argument("--prefill-chunk", type=int, default=256, help="prompt tokens per prefill call")
+    ap.add_argument("--prefill-chunk", type=int, default=512, help="prompt tokens per prefill call")
     ap.add_argument("--n-ctx", type=int, default=32768)
     ap.add_argument("--depth", type=int, default=4, help="drafts per round (k)")
     ap.add_argument("--profile-rounds", type=int, default=4)
@@ -345,7 +345,7 @@ def main():
     torch.cuda.synchronize()
     print(f"[bench] model built: {wbytes / 1e9:.2f} GB quantized weights in {time.perf_counter() - t0:.1f} s",
           file=sys.stderr, flush=True)
-    chunk = max(64, min(args.prefill_chunk, 256))
+    chunk = max(64, min(args.prefill_chunk, 4096))
     sess = Session(model, args.n_ctx, max_batch=chunk)
     g = torch.Generator().manual_seed(args.seed + 1)
     prompt = torch.randint(0, hp["n_vocab"], (args.prompt,), generator=g).tolist()
