@@ -670,13 +670,33 @@ __device__ __forceinline__ const float* row_logits(const DistArgs& a, int row)
 // The split top-p build's first two launches, EXP_SPLIT workgroups per row:
 // the row maximum in parts (fmaxf is order-free), then pr[i] = expf(l - max)
 // by index, as the one-workgroup build computes them.
+// the part's element range, in whole float4s (parts start at multiples of 4)
+__device__ __forceinline__ void exp_part(int V, int part, int* i0, int* i1)
+{
+    const int per = (((V + EXP_SPLIT - 1) / EXP_SPLIT) + 3) & ~3;
+    *i0 = min(V, part * per);
+    *i1 = min(V, *i0 + per);
+}
+
+// 16-byte accesses when the row allows them
+__device__ __forceinline__ bool vec4_ok(const void* p, int V) { return !(V & 3) && !((uintptr_t)p & 15); }
+
 __global__ __launch_bounds__(256) void rowmax_part_kernel(DistArgs a)
 {
     const int part = blockIdx.x, row = blockIdx.y, V = a.V, tid = threadIdx.x;
     const float* lg = row_logits(a, row);
-    const int per = (V + EXP_SPLIT - 1) / EXP_SPLIT, i0 = part * per, i1 = min(V, i0 + per);
+    int i0, i1;
+    exp_part(V, part, &i0, &i1);
     float m = -INFINITY;
-    for (int i = i0 + tid; i < i1; i += 256) m = fmaxf(m, lg[i]);
+    if (vec4_ok(lg, V)) {
+        const float4* l4 = (const float4*)lg;
+        for (int j = (i0 >> 2) + tid; j < (i1 >> 2); j += 256) {
+            const float4 v = l4[j];
+            m = fmaxf(m, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+        }
+    } else {
+        for (int i = i0 + tid; i < i1; i += 256) m = fmaxf(m, lg[i]);
+    }
     m = cpv_wave_reduce(m, cpv_op_max());
     __shared__ float s_m[4];
     if ((tid & 63) == 0) s_m[tid >> 6] = m;
@@ -691,8 +711,18 @@ __global__ __launch_bounds__(256) void exp_kernel(DistArgs a)
     float mx = -INFINITY;
     for (int q = 0; q < EXP_SPLIT; q++) mx = fmaxf(mx, a.st[row].pmax[q]);
     float* pr = a.pr + (size_t)row * V;
-    const int per = (V + EXP_SPLIT - 1) / EXP_SPLIT, i0 = part * per, i1 = min(V, i0 + per);
-    for (int i = i0 + tid; i < i1; i += 256) pr[i] = cpv_expf(lg[i] - mx);
+    int i0, i1;
+    exp_part(V, part, &i0, &i1);
+    if (vec4_ok(lg, V) && vec4_ok(pr, V)) {
+        const float4* l4 = (const float4*)lg;
+        float4* p4 = (float4*)pr;
+        for (int j = (i0 >> 2) + tid; j < (i1 >> 2); j += 256) {
+            const float4 v = l4[j];
+            p4[j] = make_float4(cpv_expf(v.x - mx), cpv_expf(v.y - mx), cpv_expf(v.z - mx), cpv_expf(v.w - mx));
+        }
+    } else {
+        for (int i = i0 + tid; i < i1; i += 256) pr[i] = cpv_expf(lg[i] - mx);
+    }
 }
 
 // Sampler::build for one row (lib.rs:229-376), leaving the distribution as
