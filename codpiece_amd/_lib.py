@@ -102,6 +102,7 @@ SIGNATURES = {
                                ctypes.POINTER(_I64)]),
     "cpv_get_rows": (_INT, [_P, _P, _P, _I64, _P]),
     "cpv_qgemm": (_INT, [_P, _P, _P, _I64, _P]),
+    "cpv_qgemm_noalloc": (_INT, [_P, _P, _P, _I64, _P]),
     "cpv_attn": (_INT, [_P, _P, _P, _P, _I64, _I64, _P, _INT, _INT, _INT, _INT, _F32, _P]),
     "cpv_argmax_rows": (_INT, [_P, _P, _P, _I64, _I64, _P]),
     "cpv_distribution": (_INT, [_P, _P, _INT, _INT, ctypes.POINTER(SamplerParams), _P, _INT, _P, _P, _P]),

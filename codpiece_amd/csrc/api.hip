@@ -78,6 +78,11 @@ extern "C" cpv_status cpv_init(int device, cpv_ctx** out)
         return CPV_EDEVICE;
     }
     c->stream = c->own_stream;
+    if (cpv_noalloc_setup(c) != CPV_OK) {
+        (void)hipStreamDestroy(c->own_stream);
+        delete c;
+        return CPV_EDEVICE;
+    }
     *out = c;
     return CPV_OK;
 }

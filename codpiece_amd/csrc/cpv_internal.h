@@ -27,6 +27,8 @@ struct cpv_ctx {
     // partial results of the row reductions (argmax / softmax peak), grown on demand
     void* red = nullptr;
     size_t red_bytes = 0;
+    // this device's address of the file-scope scratch of cpv_qgemm_noalloc
+    void* scratch = nullptr;
     // kernel timing (cpv_profile_start / _stop): event pairs around launches,
     // and each launch kept for cpv_profile_replay
     struct prof_rec { int cls, ev0, ev1; double bytes; };
@@ -70,6 +72,10 @@ cpv_status cpv_hip_fail(cpv_ctx* ctx, hipError_t e, const char* what);
         hipError_t e_ = (expr);                                        \
         if (e_ != hipSuccess) return cpv_hip_fail((ctx), e_, #expr);   \
     } while (0)
+
+// look up this device's address of cpv_qgemm_noalloc's scratch (once per
+// device; ctx->device must be current)
+cpv_status cpv_noalloc_setup(cpv_ctx* ctx);
 
 // grow the context workspace to at least `bytes` (synchronises the stream
 // before freeing an old buffer the queued work may still use)

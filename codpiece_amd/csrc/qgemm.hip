@@ -34,6 +34,8 @@
 // GEMM: on gfx950 one would write back a whole L2 per workgroup).
 #include <math.h>
 
+#include <mutex>
+
 #include "cpv_internal.h"
 
 namespace {
@@ -692,7 +694,9 @@ cpv_status cpv_quant_act(cpv_ctx* ctx, int type, const float* x, int64_t m, int6
     return CPV_OK;
 }
 
-cpv_status cpv_qgemm_act(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, float* y)
+// the GEMM of quantized activations into the split-K accumulator gsum
+// ([act->m][w->n_pad] f64, zero on entry and, when y is given, on return)
+static cpv_status qgemm_into(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, float* y, double* gsum)
 {
     const bool kq = w->type != CPV_Q8_0;
     if (kq != act->kq || act->k != w->k || act->U != (int)w->units)
@@ -722,8 +726,8 @@ cpv_status cpv_qgemm_act(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, 
         a.nu_max = per < U ? per : U;
         a.nt_max = (per + U - 1) / U + 1;
     }
-    cpv_status st = gemm_accumulator(ctx, m, w->n_pad, &a.gsum);
-    if (st != CPV_OK) return st;
+    a.gsum = gsum;
+    cpv_status st = CPV_OK;
     const double wb = (double)w->n * (double)(w->k / cpv_type_block(w->type)) * (double)cpv_type_size(w->type);
     auto lds = [&](int M) {
         return w->type == CPV_Q4_K   ? lds_of<CPV_Q4_K>(M, a.nu_max, a.nt_max)
@@ -753,6 +757,14 @@ cpv_status cpv_qgemm_act(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, 
         m0 += M;
     }
     return CPV_OK;
+}
+
+cpv_status cpv_qgemm_act(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, float* y)
+{
+    double* gsum = nullptr;
+    cpv_status st = gemm_accumulator(ctx, act->m, w->n_pad, &gsum);
+    if (st != CPV_OK) return st;
+    return qgemm_into(ctx, w, act, y, gsum);
 }
 
 cpv_status cpv_qgemm_keep(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, cpv_gout* out)
@@ -786,4 +798,80 @@ extern "C" cpv_status cpv_qgemm(cpv_ctx* ctx, const cpv_weight* w, const float* 
     if (m < 1 || m > 256) return cpv_fail(ctx, CPV_EINVAL, "qgemm: m=%lld outside [1, 256]", (long long)m);
     if (w->ctx != ctx) return cpv_fail(ctx, CPV_EINVAL, "qgemm: weight belongs to another context");
     return cpv_qgemm_launch(ctx, w, x_dev, m, y_dev);
+}
+
+// ---------------------------------------------------------------- without allocation
+// cpv_qgemm_noalloc keeps its quantized activations and its split-K
+// accumulator in one file-scope device array instead of the context's
+// workspace.  Each GPU holds its own copy until the process ends.  Host code
+// must not use the array's name as an address (on the host it is a stand-in,
+// not device memory): cpv_noalloc_setup looks up each device's address once,
+// with that device current, and every launch takes that pointer.
+namespace {
+
+constexpr size_t NOALLOC_ACT_BYTES = (size_t)2 << 20;    // quantized activations (Q8_K / Q8_0 layout)
+constexpr size_t NOALLOC_ACC_BYTES = (size_t)8 << 20;    // [m][n_pad] f64 accumulator
+constexpr int NOALLOC_MAX_ROWS = 16;
+constexpr int NOALLOC_MAX_DEVICES = 64;
+
+static __device__ __align__(256) uint8_t scratch[NOALLOC_ACT_BYTES + NOALLOC_ACC_BYTES];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+__global__ __launch_bounds__(256) void zero_f64_kernel(double* __restrict__ p, int64_t n)
+{
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0.0;
+}
+
+}  // namespace
+
+cpv_status cpv_noalloc_setup(cpv_ctx* ctx)
+{
+    if (ctx->device < 0 || ctx->device >= NOALLOC_MAX_DEVICES)
+        return cpv_fail(ctx, CPV_EUNSUPPORTED, "noalloc: device %d beyond the scratch table", ctx->device);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[ctx->device]) {
+        // the caller (cpv_init) has made ctx->device current
+        void* p = nullptr;
+        CPV_HIP(ctx, hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        g_scratch_ptr[ctx->device] = p;
+    }
+    ctx->scratch = g_scratch_ptr[ctx->device];
+    return CPV_OK;
+}
+
+extern "C" cpv_status cpv_qgemm_noalloc(cpv_ctx* ctx, const cpv_weight* w, const float* x_dev, int64_t m,
+                                        float* y_dev)
+{
+    if (!ctx || !w || !x_dev || !y_dev) return cpv_fail(ctx, CPV_EINVAL, "qgemm_noalloc: null argument");
+    if (w->ctx != ctx) return cpv_fail(ctx, CPV_EINVAL, "qgemm_noalloc: weight belongs to another context");
+    if (!ctx->scratch) return cpv_fail(ctx, CPV_EDEVICE, "qgemm_noalloc: no scratch address for this device");
+    if (m < 1 || m > NOALLOC_MAX_ROWS)
+        return cpv_fail(ctx, CPV_EINVAL, "qgemm_noalloc: m=%lld outside [1, %d]", (long long)m, NOALLOC_MAX_ROWS);
+    const size_t act_b = cpv_act_bytes(w->type, w->k, m);
+    const size_t acc_b = (size_t)m * (size_t)w->n_pad * sizeof(double);
+    if (act_b > NOALLOC_ACT_BYTES)
+        return cpv_fail(ctx, CPV_EINVAL, "qgemm_noalloc: k=%lld at m=%lld needs %zu activation bytes, above %zu",
+                        (long long)w->k, (long long)m, act_b, NOALLOC_ACT_BYTES);
+    if (acc_b > NOALLOC_ACC_BYTES)
+        return cpv_fail(ctx, CPV_EINVAL, "qgemm_noalloc: %lld rows at m=%lld need %zu accumulator bytes, above %zu",
+                        (long long)w->n, (long long)m, acc_b, NOALLOC_ACC_BYTES);
+    uint8_t* base = (uint8_t*)ctx->scratch;
+    double* acc = (double*)(base + NOALLOC_ACT_BYTES);
+    // the previous call on this device left the accumulator zero unless it
+    // failed part-way; clear it with a kernel (no memset node, so the call can
+    // be captured into a graph)
+    const int64_t n_acc = m * w->n_pad;
+    const int64_t zb = (n_acc + 255) / 256;
+    zero_f64_kernel<<<(unsigned)(zb < 1024 ? zb : 1024), 256, 0, ctx->stream>>>(acc, n_acc);
+    CPV_HIP(ctx, hipGetLastError());
+    // no kernel timing here: it creates events and keeps launches
+    const bool prof = ctx->prof;
+    ctx->prof = false;
+    cpv_act act;
+    cpv_status st = cpv_quant_act(ctx, w->type, x_dev, m, w->k, base, &act);
+    if (st == CPV_OK) st = qgemm_into(ctx, w, &act, y_dev, acc);
+    ctx->prof = prof;
+    return st;
 }

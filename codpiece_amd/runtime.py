@@ -96,6 +96,14 @@ class Context:
         self._check(self.lib.cpv_qgemm(self.h, w.h, _ptr(x), x.shape[0], _ptr(y)))
         return y
 
+    def qgemm_noalloc(self, w, x, y):
+        """qgemm into a caller-allocated y through the allocation-free entry
+        point (per-device scratch; m <= 16)."""
+        assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous() and x.shape[1] == w.k
+        assert y.is_cuda and y.dtype == torch.float32 and y.is_contiguous() and y.shape == (x.shape[0], w.n)
+        self._check(self.lib.cpv_qgemm_noalloc(self.h, w.h, _ptr(x), x.shape[0], _ptr(y)))
+        return y
+
     def get_rows(self, w, rows, out=None):
         rows = rows.to(torch.int32).contiguous()
         if out is None:

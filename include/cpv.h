@@ -91,6 +91,19 @@ cpv_status  cpv_get_rows(cpv_ctx* ctx, const cpv_weight* w, const int32_t* rows_
 cpv_status  cpv_qgemm(cpv_ctx* ctx, const cpv_weight* w, const float* x_dev, int64_t m,
                       float* y_dev);
 
+/* No counterpart in the reference: cpv_qgemm for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops and
+ * harnesses that forbid hipMalloc).  The same kernels and the same results
+ * as cpv_qgemm, with the quantized activations and the split-K accumulator in
+ * a fixed per-device scratch array (10 MiB, held until the process ends)
+ * instead of the context's workspace; the call allocates nothing.  Limits:
+ * 1 <= m <= 16, the quantized activations within 2 MiB (k up to 65536 at
+ * m = 16) and m * (n_rows rounded up to 64) <= 1048576 (else CPV_EINVAL).
+ * Every call on one device shares that device's scratch: calls that overlap
+ * on one device (two streams, two contexts) race. */
+cpv_status  cpv_qgemm_noalloc(cpv_ctx* ctx, const cpv_weight* w, const float* x_dev, int64_t m,
+                              float* y_dev);
+
 /* Masked GQA attention over the f16 KV cache; replaces ggml_flash_attn_ext
  * with prec F32 and an f16 mask (qwen35.rs:3182-3187, mask fill :3551-3568).
  *   q_dev        f32 [t][h][d]
