@@ -199,6 +199,24 @@ void          cpvo_session_set_pos(cpvo_session* s, int64_t n_past, int64_t mtp_
 void          cpvo_session_set_attn_inject(cpvo_session* s, const float* att, int64_t n_floats);
 double        cpvo_session_inject_ratio(const cpvo_session* s);
 void          cpvo_session_get_pos(const cpvo_session* s, int64_t* n_past, int64_t* mtp_past);
+/* Planted mistakes, for tests that show the independent f64 forward catches a
+ * wrong composition (0 = none, the faithful restatement):
+ *   1 Q and the output gate swapped in their attn_q slots
+ *   2 the sigmoid gate applied after wo instead of before it
+ *   3 the MTP concat in the wrong order, [hnorm(h) ; enorm(e)]
+ *   4 the MTP link hands on its hidden before shared_head_norm
+ *   5 the post-attention norm dropped (the FFN reads the raw residual)
+ *   6 enorm and hnorm weights swapped in the MTP concat */
+void          cpvo_set_fault(int code);
+/* The round's attention in binary64 (cpvo_attn_f64) instead of the chunked
+ * contract, so that a composition check is not blurred by the contract's
+ * f16 probabilities (0 = the contract, the default). */
+void          cpvo_set_attn_f64(int on);
+/* Every mul_mat of the round on the f32 activation rows as they are (no
+ * activation quantization), summed in binary64: with cpvo_set_attn_f64 the
+ * round becomes a smooth function of its inputs, for composition checks
+ * against a float64 forward (0 = ggml's quantized activations, the default). */
+void          cpvo_set_smooth(int on);
 int           cpvo_prefill(cpvo_session* s, const int32_t* tok, int t);
 /* step_fused_cached: preds [t], chain [depth][t], conf [depth][t] (nullable),
  * logits [t][V] and hidden [t][E] (nullable); noise [t][V] or NULL */

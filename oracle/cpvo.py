@@ -104,6 +104,9 @@ def lib():
             "cpvo_session_get_pos": (None, [P, P, P]),
             "cpvo_session_set_attn_inject": (None, [P, P, i64]),
             "cpvo_session_inject_ratio": (ctypes.c_double, [P]),
+            "cpvo_set_fault": (None, [ctypes.c_int]),
+            "cpvo_set_attn_f64": (None, [ctypes.c_int]),
+            "cpvo_set_smooth": (None, [ctypes.c_int]),
             "cpvo_prefill": (ctypes.c_int, [P, P, ctypes.c_int]),
             "cpvo_verify_step": (ctypes.c_int, [P, P, ctypes.c_int, ctypes.c_int, P, P, P, P, P, P]),
             "cpvo_verify_step_cands": (ctypes.c_int, [P, P, ctypes.c_int, ctypes.c_int, P, P, ctypes.c_int, P, P, P,
@@ -384,6 +387,21 @@ def spec_accept_rng(p_logits, draft, params, rng, hist=None):
     n = lib().cpvo_spec_accept_rng(_p(p_logits), _p(draft), k, V, ctypes.byref(params),
                                    _p(rng.s), _p(h), 0 if h is None else h.size, _p(tok), _p(used))
     return tok, n, used
+
+
+def set_fault(code):
+    """Plant one of the oracle's listed composition mistakes (cpvo.h), or 0."""
+    lib().cpvo_set_fault(int(code))
+
+
+def set_attn_f64(on):
+    """Run the model round's attention in binary64 instead of the contract."""
+    lib().cpvo_set_attn_f64(1 if on else 0)
+
+
+def set_smooth(on):
+    """Run the model round's mul_mats on unquantized activations (binary64 sums)."""
+    lib().cpvo_set_smooth(1 if on else 0)
 
 
 class Hparams(ctypes.Structure):

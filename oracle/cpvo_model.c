@@ -14,6 +14,16 @@
 
 typedef struct { int type; uint8_t* data; int64_t ne0, ne1; } wt_t;
 
+/* a planted mistake (cpvo.h), 0 in every normal use */
+static int g_fault = 0;
+void cpvo_set_fault(int code) { g_fault = code; }
+/* attention in binary64 (cpvo_attn_f64) instead of the exact chunked contract */
+static int g_attn_f64 = 0;
+void cpvo_set_attn_f64(int on) { g_attn_f64 = on; }
+/* mul_mat on the unquantized f32 activation rows, summed in binary64 */
+static int g_smooth = 0;
+void cpvo_set_smooth(int on) { g_smooth = on; }
+
 typedef struct {
     wt_t wq, wk, wv, wo, gate, up, down;
     float *attn_norm, *post_norm, *q_norm, *k_norm;
@@ -165,7 +175,22 @@ void cpvo_session_get_pos(const cpvo_session* s, int64_t* n_past, int64_t* mtp_p
 
 static void mm(const wt_t* w, const float* x, int T, float* y)
 {
-    cpvo_qgemm(w->type, w->data, w->ne1, w->ne0, x, T, y, 8);
+    if (!g_smooth) {
+        cpvo_qgemm(w->type, w->data, w->ne1, w->ne0, x, T, y, 8);
+        return;
+    }
+    const int64_t K = w->ne0, rb = cpvo_row_bytes(w->type, K);
+    #pragma omp parallel for num_threads(8)
+    for (int64_t n = 0; n < w->ne1; n++) {
+        float* wr = malloc(sizeof(float) * (size_t)K);
+        cpvo_dequantize(w->type, w->data + n * rb, K, wr);
+        for (int t = 0; t < T; t++) {
+            double acc = 0.0;
+            for (int64_t k = 0; k < K; k++) acc += (double)wr[k] * (double)x[(int64_t)t * K + k];
+            y[(int64_t)t * w->ne1 + n] = (float)acc;
+        }
+        free(wr);
+    }
 }
 
 static void rms_rows(const float* x, int T, int n, int64_t xs, const float* w, float eps, float* y, int64_t ys)
@@ -197,7 +222,8 @@ static void block(cpvo_session* s, const layer_t* L, float* x, int T, int64_t ro
         const float* cs = s->rope ? s->rope + (rope_pos0 + t) * hp->n_rot : NULL;
         for (int h = 0; h < H; h++) {
             /* Q is the first hd of each head's 2*hd slot; the gate the second (:3029-3045) */
-            cpvo_rms_norm(qg + ((int64_t)t * H + h) * 2 * hd, hd, hp->rms_eps, L->q_norm, tmp);
+            cpvo_rms_norm(qg + ((int64_t)t * H + h) * 2 * hd + (g_fault == 1 ? hd : 0), hd, hp->rms_eps, L->q_norm,
+                          tmp);
             if (cs) cpvo_rope_neox(tmp, hp->n_rot, cs);
             memcpy(q + ((int64_t)t * H + h) * hd, tmp, sizeof(float) * (size_t)hd);
         }
@@ -214,7 +240,7 @@ static void block(cpvo_session* s, const layer_t* L, float* x, int T, int64_t ro
         }
     }
     const float scale = 1.0f / sqrtf((float)hd);
-    cpvo_attn(q, kc, vc, attn_past, NULL, T, H, Hkv, hd, scale, att);
+    (g_attn_f64 ? cpvo_attn_f64 : cpvo_attn)(q, kc, vc, attn_past, NULL, T, H, Hkv, hd, scale, att);
     if (s->inj) {
         const int64_t n = (int64_t)T * H * hd;
         if (s->inj_off + n <= s->inj_cap) {
@@ -233,13 +259,20 @@ static void block(cpvo_session* s, const layer_t* L, float* x, int T, int64_t ro
     for (int t = 0; t < T; t++)
         for (int h = 0; h < H; h++)
             for (int i = 0; i < hd; i++) {
-                const float g = qg[((int64_t)t * H + h) * 2 * hd + hd + i];
+                const float g = qg[((int64_t)t * H + h) * 2 * hd + (g_fault == 1 ? 0 : hd) + i];
                 const float sig = 1.0f / (1.0f + cpvo_expf(-g));
-                att[((int64_t)t * H + h) * hd + i] *= sig;
+                if (g_fault != 2) att[((int64_t)t * H + h) * hd + i] *= sig;
             }
     mm(&L->wo, att, T, o);
+    if (g_fault == 2 && H * hd == E)
+        for (int t = 0; t < T; t++)
+            for (int i = 0; i < H * hd; i++) {
+                const float g = qg[((int64_t)t * H + i / hd) * 2 * hd + hd + i % hd];
+                o[(int64_t)t * E + i] *= 1.0f / (1.0f + cpvo_expf(-g));
+            }
     for (int64_t e = 0; e < (int64_t)T * E; e++) x[e] = o[e] + x[e];
-    rms_rows(x, T, E, E, L->post_norm, hp->rms_eps, xn, E);
+    if (g_fault == 5) memcpy(xn, x, sizeof(float) * (size_t)T * E);
+    else rms_rows(x, T, E, E, L->post_norm, hp->rms_eps, xn, E);
     mm(&L->up, xn, T, up);
     mm(&L->gate, xn, T, gt);
     for (int64_t e = 0; e < (int64_t)T * F; e++) {
@@ -339,13 +372,15 @@ int cpvo_verify_step_cands(cpvo_session* s, const int32_t* tok, int T, int depth
         memcpy(tsrc, preds, sizeof(int32_t) * (size_t)T);
         for (int step = 0; step < depth; step++) {
             embed(mtp_embed_w(m), tsrc, T, e);
-            rms_rows(e, T, (int)E, E, m->enorm, hp->rms_eps, cat, 2 * E);
-            rms_rows(hsrc, T, (int)E, E, m->hnorm, hp->rms_eps, cat + E, 2 * E);
+            const int64_t eo = g_fault == 3 ? E : 0;
+            rms_rows(e, T, (int)E, E, g_fault == 6 ? m->hnorm : m->enorm, hp->rms_eps, cat + eo, 2 * E);
+            rms_rows(hsrc, T, (int)E, E, g_fault == 6 ? m->enorm : m->hnorm, hp->rms_eps, cat + E - eo, 2 * E);
             mm(&m->eh_proj, cat, T, d);
             block(s, ML, d, T, s->n_past + 1, s->mtp_past, s->mtp_past, s->kc[hp->n_layer], s->vc[hp->n_layer],
                   step == 0);
             rms_rows(d, T, (int)E, E, mtp_head_norm(m), hp->rms_eps, hsrc, E);
             mm(mtp_head_w(m), hsrc, T, logits);
+            if (g_fault == 4) memcpy(hsrc, d, sizeof(float) * (size_t)(T * E));
             for (int t = 0; t < T; t++) {
                 if (cands && n_cand > 0) {
                     float* lc = malloc(sizeof(float) * (size_t)n_cand);
