@@ -4,10 +4,13 @@
 lib.rs:128-311); `Session` owns the KV caches and positions (Session::new_spec,
 qwen35.rs:528-649); `Session.step_fused_cached` is Qwen35::step_fused_cached
 (qwen35.rs:1693-1948) and returns a `FusedOut` (qwen35.rs:817-828);
-`fused_generate` is the CLI's fused speculative loop (crates/codpiece-cli/src/
-main.rs:643-931).  All arithmetic runs in libcpv.so.
+`fused_generate` is the CLI's fused greedy speculative loop (crates/codpiece-
+cli/src/main.rs:643-931); `sampled_generate` is the engine's sampled
+speculative loop (crates/codpiece-server/src/engine.rs:1922-2039,
+2212-2542).  All arithmetic runs in libcpv.so.
 """
 import ctypes
+from collections import deque
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -125,6 +128,8 @@ class Session:
         head over the shortlist `cands` (token ids) when given."""
         t = self._tokens(tokens)
         out = RoundOut()
+        if noise is not None:
+            noise = _as_device(noise, self.ctx.torch_device)
         nz = None if noise is None else ctypes.c_void_p(noise.data_ptr())
         if cands is None:
             self.ctx._check(self.ctx.lib.cpv_verify_step(self.h, ctypes.c_void_p(self._tok.data_ptr()), t, depth,
@@ -166,6 +171,23 @@ class Session:
             hidden = _device_view(out.hidden_dev, t * E, torch.float32, self.ctx.torch_device).view(t, E).clone()
         return FusedOut(preds, [], [], logits, hidden)
 
+    def accept_round(self, out, drafts, params, mode, noise=None, hist=None, key=0):
+        """Decide a verified round on the device (cpv_spec_accept over the
+        round's logits, out.logits [t][V] with t = len(drafts) + 1): returns
+        (the accepted drafts then the next token, the number accepted).
+        Uniforms are Philox4x64-10 with key (key, 0), counter (0, j, role, 0);
+        `noise` ([t][V], T-scaled gumbel) for the gumbel mode; `hist` the
+        penalty window, oldest first."""
+        t, V = out.logits.shape
+        dev = self.ctx.torch_device
+        dr = torch.tensor(list(drafts), dtype=torch.int32, device=dev).view(1, len(drafts))
+        h = None if not hist else torch.tensor(list(hist), dtype=torch.int32, device=dev).view(1, -1)
+        nz = None if noise is None else _as_device(noise, dev).view(1, t, V)
+        tok, n = self.ctx.spec_accept(out.logits.view(1, t, V), dr, params, mode, noise=nz, hist=h,
+                                      philox_seed=int(key))
+        n = int(n.cpu()[0])
+        return tok[0, :n + 1].cpu().tolist(), n
+
     def commit_branch(self, path):
         """Keep the root-to-node path `path` (node indices) of the last tree
         verify as context rows; the other nodes are dropped."""
@@ -177,6 +199,13 @@ class Session:
         if self.h:
             self.ctx.lib.cpv_session_free(self.h)
             self.h = None
+
+
+def _as_device(x, device):
+    """A float32 cuda tensor of x (numpy or torch), contiguous."""
+    if not isinstance(x, torch.Tensor):
+        x = torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32))
+    return x.to(device=device, dtype=torch.float32).contiguous()
 
 
 def _device_view(ptr, n, dtype, device):
@@ -198,9 +227,14 @@ class FusedStats:
     decode_s: float = 0.0
 
 
-def fused_generate(session, prompt, n_gen, depth, tail=64, bulk=512, timer=None):
+def fused_generate(session, prompt, n_gen, depth, tail=64, bulk=512, timer=None, drafter=None):
     """cmd_fused (crates/codpiece-cli/src/main.rs:643-931) at a fixed depth with
     greedy acceptance; the seeded model has no tokenizer, so no EOS stop.
+    drafter(committed, chain_drafts) -> drafts, when given, supplies each
+    round's drafts instead of the MTP chain (an external drafter, as the
+    engine's verify-only rounds take DFlash drafts, engine.rs:2291-2293); the
+    chain is still computed at `depth`.  depth 0 with no drafter is plain
+    greedy decoding, one token per round.
     Returns (committed tokens, FusedStats)."""
     import time
     t0 = time.perf_counter()
@@ -214,6 +248,8 @@ def fused_generate(session, prompt, n_gen, depth, tail=64, bulk=512, timer=None)
     last = len(out.preds) - 1
     committed = [out.preds[last]]
     drafts = [out.chain[l][last] for l in range(depth)]
+    if drafter is not None:
+        drafts = list(drafter(committed, drafts))
     t1 = time.perf_counter()
     accepted = proposed = rounds = 0
     while len(committed) < n_gen:
@@ -235,6 +271,8 @@ def fused_generate(session, prompt, n_gen, depth, tail=64, bulk=512, timer=None)
             break
         committed.append(out.preds[keep])
         drafts = [out.chain[l][keep] for l in range(depth)]
+        if drafter is not None:
+            drafts = list(drafter(committed, drafts))
         over = len(batch) - (keep + 1)
         n_past, mtp_past = session.pos
         session.set_pos(n_past - over, mtp_past + keep + 1)
@@ -242,4 +280,108 @@ def fused_generate(session, prompt, n_gen, depth, tail=64, bulk=512, timer=None)
     return committed, FusedStats(accepted, proposed, rounds, t1 - t0, t2 - t1)
 
 
-__all__ = ["Model", "Session", "FusedOut", "FusedStats", "make_hparams", "fused_generate", "CpvError"]
+def _penalties_on(p):
+    return p.penalty_last_n > 0 and (p.penalty_repeat != 1.0 or p.penalty_freq != 0.0 or p.penalty_present != 0.0)
+
+
+def sampled_generate(session, prompt, n_gen, depth, params, mode=_lib.ACCEPT_REJECT, seed=0, tail=64, bulk=512,
+                     noise=None, chain_pmin=0.0, drafter=None):
+    """The engine's sampled speculative loop for one request (crates/codpiece-
+    server/src/engine.rs), at a fixed draft depth, without EOS, stop strings,
+    JSON or forced tokens:
+      * the prompt seeds the penalty window (sampler.accept_all, :1764); all
+        but the last `tail` tokens are prefilled in `bulk` chunks (:1922-1953);
+      * the tail runs as a fused round; the first token is a draw from the
+        distribution at the last position, and the drafts are the chain there
+        (:1958-2012, :2039);
+      * each round verifies [next] + drafts with the chain at `depth`
+        (:2291-2305) and decides them on the device (cpv_spec_accept):
+        REJECT accepts draft j with probability p(x_j), else draws the
+        replacement excluding x_j (:2351-2359); GUMBEL accepts a draft iff it
+        is the gumbel-coupled sample (:2336-2349); the next token is the
+        replacement, or else a draw at the first unverified position (:2400-
+        2461); every committed token enters the penalty window (:2368, :2497);
+      * the next drafts are the chain at n_keep, cut at the first link whose
+        confidence is below chain_pmin (:2508-2517), and dropped when the next
+        token is not the trunk's argmax there (:2527-2529); the rejected rows
+        are rewound (:2533-2540).
+    Randomness is explicit: the reference's sequential xoshiro stream becomes
+    Philox4x64-10 uniforms by role, round r (the tail round is 0) using key
+    (seed + r, 0) with counter (0, j, role, 0).  In GUMBEL mode noise(r, rows)
+    supplies round r's T-scaled gumbel noise [rows][V] (the engine's noise
+    thread, :2080-2118): the verify argmaxes logits + noise in the graph, and
+    the acceptance couples on the same noise.  drafter(committed, drafts), when
+    given, replaces each round's drafts after those rules (an external
+    drafter, as fused_generate takes).  Returns (committed tokens,
+    FusedStats)."""
+    import time
+    if mode == _lib.ACCEPT_GUMBEL and noise is None:
+        raise ValueError("sampled_generate: the gumbel mode needs a noise source")
+    t0 = time.perf_counter()
+    window = deque(maxlen=params.penalty_last_n) if _penalties_on(params) else None
+
+    def seen(tok):
+        if window is not None:
+            window.append(int(tok))
+
+    def hist():
+        return list(window) if window else None
+
+    for tok in prompt:
+        seen(tok)
+    split = max(0, len(prompt) - tail)
+    bulk = min(bulk, getattr(session, "max_batch", bulk))
+    for c in range(0, split, bulk):
+        session.prefill(prompt[c:min(split, c + bulk)])
+    out = session.step_fused_cached(prompt[split:], depth, want_logits=True)
+    n_past, mtp_past = session.pos
+    session.set_pos(n_past, mtp_past + len(out.preds))
+    at = len(out.preds) - 1
+    first = FusedOut(out.preds[at:], [], [], out.logits[at:at + 1], None)
+    toks, _ = session.accept_round(first, [], params, _lib.ACCEPT_REJECT, hist=hist(), key=seed)
+    nxt = toks[0]
+    seen(nxt)
+    committed = [nxt]
+    drafts = [out.chain[l][at] for l in range(depth)]
+    if drafter is not None:
+        drafts = list(drafter(committed, drafts))
+    t1 = time.perf_counter()
+    accepted = proposed = rounds = 0
+    while len(committed) < n_gen:
+        rounds += 1
+        batch = [nxt] + drafts
+        nz = noise(rounds, len(batch)) if mode == _lib.ACCEPT_GUMBEL else None
+        out = session.step_fused_cached(batch, depth, want_logits=True, noise=nz)
+        proposed += len(drafts)
+        toks, keep = session.accept_round(out, drafts, params, mode, noise=nz, hist=hist(), key=seed + rounds)
+        accepted += keep
+        done = False
+        for d in drafts[:keep]:
+            seen(d)
+            committed.append(d)
+            if len(committed) >= n_gen:
+                done = True
+                break
+        if done:
+            break
+        nxt = toks[keep]
+        seen(nxt)
+        committed.append(nxt)
+        drafts = []
+        for l in range(depth):
+            if out.conf[l][keep] < chain_pmin:
+                break
+            drafts.append(out.chain[l][keep])
+        if nxt != out.preds[keep]:
+            drafts = []
+        if drafter is not None:
+            drafts = list(drafter(committed, drafts))
+        over = len(batch) - (keep + 1)
+        n_past, mtp_past = session.pos
+        session.set_pos(n_past - over, mtp_past + keep + 1)
+    t2 = time.perf_counter()
+    return committed, FusedStats(accepted, proposed, rounds, t1 - t0, t2 - t1)
+
+
+__all__ = ["Model", "Session", "FusedOut", "FusedStats", "make_hparams", "fused_generate", "sampled_generate",
+           "CpvError"]

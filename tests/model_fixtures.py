@@ -69,8 +69,33 @@ class OracleSession:
 
     def step_fused_cached(self, tokens, depth, want_logits=False, noise=None):
         from codpiece_amd.model import FusedOut
-        p, ch, cf, lg, hd = self.s.step_fused_cached(tokens, depth, want_logits, noise)
+        p, ch, cf, lg, hd = self.s.step_fused_cached(tokens, depth, want_logits, _host(noise))
         return FusedOut(p.tolist(), ch.tolist(), cf.tolist(), lg, hd)
+
+    def accept_round(self, out, drafts, params, mode, noise=None, hist=None, key=0):
+        """The oracle's acceptance (cpvo_spec_accept) with the device's Philox
+        uniforms for `key`: the same contract as Session.accept_round."""
+        t, V = out.logits.shape
+        u = cpvo.philox_uniforms(int(key), 1, t - 1)
+        nz = None if noise is None else _host(noise).reshape(1, t, V)
+        h = None if not hist else np.asarray(list(hist), dtype=np.int32).reshape(1, -1)
+        tok, n = cpvo.spec_accept(np.asarray(out.logits).reshape(1, t, V), np.asarray(drafts, np.int32).reshape(1, t - 1),
+                                  oracle_params(params), mode, u=u, noise_t=nz, hist=h)
+        return tok[0, :n[0] + 1].tolist(), int(n[0])
+
+
+def _host(x):
+    """numpy float32 of x (numpy, torch on any device, or None)."""
+    if x is None:
+        return None
+    if hasattr(x, "detach"):
+        x = x.detach().cpu().numpy()
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def oracle_params(p):
+    return cpvo.SamplerParams(p.temp, p.top_k, p.top_p, p.min_p, p.min_keep, p.penalty_repeat, p.penalty_freq,
+                              p.penalty_present, p.penalty_last_n)
 
 
 class PairedSession:

@@ -1,0 +1,200 @@
+"""The sampled speculative loop and the losslessness gate, on the CPU.
+
+(1) codpiece_amd.model.sampled_generate, driven over the oracle session (whose
+acceptance is cpvo_spec_accept), commits the same tokens and counts as an
+independent restatement of the engine's loop written here from
+crates/codpiece-server/src/engine.rs:1958-2039 and 2212-2542 with the
+codpiece-sample primitives (Sampler::distribution, Dist::prob_of / draw /
+draw_excluding, sample_coupled), draft by draft, on the same uniforms by role
+(Philox4x64-10, key seed + round, counter (0, j, role)) and the same gumbel
+noise.  Rejection, gumbel coupling with and without filters, and penalties.
+(2) The losslessness gate of scripts/final-verify.sh:15-30: greedy streams at
+draft depths 1-4 equal plain greedy decoding (depth 0).  Random MTP drafts are
+almost never accepted, so the drafts are taken from the plain greedy stream
+itself (every round fully accepted) and, in every third round, with one wrong
+token (a partial accept and a rewind); the stream must not change.
+"""
+import numpy as np
+import pytest
+
+from oracle import cpvo
+
+import model_fixtures as mf
+
+SMALL = dict(mf.TINY, n_layer=2, n_vocab=4096)
+REJECT, GUMBEL = cpvo.ACCEPT_REJECT, cpvo.ACCEPT_GUMBEL
+
+
+@pytest.fixture(scope="module")
+def om():
+    m = cpvo.Model(SMALL)
+    mf.load_into(m, mf.make_tensors(SMALL, seed=3))
+    yield m
+    m.free()
+
+
+def gumbel_noise(seed, temp, V):
+    """T-scaled gumbel noise for round r (the engine's noise thread,
+    engine.rs:2098-2114: -ln(-ln(max(u, 1e-12))) * T), from numpy."""
+    def noise(r, rows):
+        u = np.random.default_rng([seed, r]).random((rows, V), dtype=np.float32)
+        u = np.maximum(u, np.float32(1e-12))
+        return (-np.log(-np.log(u)) * np.float32(temp)).astype(np.float32)
+    return noise
+
+
+def engine_restatement(osess, prompt, n_gen, depth, params, mode, seed, tail, bulk, noise=None):
+    """engine.rs's single-request sampled loop, draft by draft."""
+    sampler = cpvo.Sampler(params)
+    plain = (params.temp > 0 and params.top_k == 0 and params.top_p >= 1.0 and params.min_p <= 0.0
+             and params.penalty_repeat == 1.0 and params.penalty_freq == 0.0 and params.penalty_present == 0.0)
+    for t in prompt:                                   # sampler.accept_all(text_ids)
+        sampler.accept(t)
+    split = max(0, len(prompt) - tail)
+    for c in range(0, split, bulk):
+        osess.prefill(prompt[c:min(split, c + bulk)])
+    P, C, CF, L, _ = osess.step_fused_cached(prompt[split:], depth, want_logits=True)
+    n_past, mtp_past = osess.pos
+    osess.set_pos(n_past, mtp_past + len(P))          # session.mtp_past += preds.len()
+    at = len(P) - 1
+    u0 = cpvo.philox_uniforms(seed, 1, 0)[0]
+    nxt = sampler.distribution(L[at]).draw(u0[0][0])   # sampler.draw_from(&d)
+    drafts = [int(C[l][at]) for l in range(depth)]
+    sampler.accept(nxt)
+    committed = [int(nxt)]
+    acc = prop = rounds = 0
+    while len(committed) < n_gen:
+        rounds += 1
+        batch = [committed[-1]] + drafts
+        k = len(drafts)
+        nz = noise(rounds, len(batch)) if mode == GUMBEL else None
+        P, C, CF, L, _ = osess.step_fused_cached(batch, depth, want_logits=True, noise=nz)
+        prop += k
+        u = cpvo.philox_uniforms(seed + rounds, 1, k)[0]
+        n_keep, repl = 0, None
+        for j, d in enumerate(drafts):
+            if mode == GUMBEL:
+                commit = int(P[j]) if plain else sampler.sample_coupled(L[j], nz[j])
+                keep = d == commit
+                if not keep:
+                    repl = commit
+            else:
+                dist = sampler.distribution(L[j])
+                keep = u[j][0] < dist.prob_of(d)
+                if not keep:
+                    repl = dist.draw_excluding(d, u[j][1])
+            if not keep:
+                break
+            n_keep += 1
+            sampler.accept(d)
+        acc += n_keep
+        done = False
+        for d in drafts[:n_keep]:
+            committed.append(int(d))
+            if len(committed) >= n_gen:
+                done = True
+                break
+        if done:
+            break
+        if repl is not None:
+            nxt = repl
+        elif mode == GUMBEL:
+            nxt = int(P[n_keep]) if plain else sampler.sample_coupled(L[n_keep], nz[n_keep])
+        else:
+            nxt = sampler.distribution(L[n_keep]).draw(u[k][0])
+        sampler.accept(nxt)
+        committed.append(int(nxt))
+        drafts = [int(C[l][n_keep]) for l in range(depth)]
+        if nxt != P[n_keep]:
+            drafts = []
+        over = len(batch) - (n_keep + 1)
+        n_past, mtp_past = osess.pos
+        osess.set_pos(n_past - over, mtp_past + n_keep + 1)
+    return committed, (acc, prop, rounds)
+
+
+CASES = [
+    ("reject", REJECT, dict(temp=0.7, top_p=0.95)),
+    ("reject_penalties", REJECT, dict(temp=0.9, top_k=40, penalty_repeat=1.3, penalty_present=0.4,
+                                      penalty_last_n=16)),
+    ("gumbel_plain", GUMBEL, dict(temp=0.7)),
+    ("gumbel_top_p", GUMBEL, dict(temp=0.7, top_p=0.95)),
+]
+
+
+@pytest.mark.parametrize("name,mode,pk", CASES, ids=[c[0] for c in CASES])
+def test_sampled_loop_matches_engine_restatement(om, name, mode, pk):
+    from codpiece_amd.model import sampled_generate
+    params = cpvo.SamplerParams(**pk)
+    prompt = np.random.default_rng(5).integers(0, SMALL["n_vocab"], size=60).tolist()
+    noise = gumbel_noise(11, params.temp, SMALL["n_vocab"])
+    a, b = cpvo.Session(om, 256), cpvo.Session(om, 256)
+    toks, st = sampled_generate(mf.OracleSession(a), prompt, 40, 3, params, mode, seed=9, tail=16, bulk=32,
+                                noise=noise)
+    rtoks, rst = engine_restatement(b, prompt, 40, 3, params, mode, 9, 16, 32, noise)
+    assert toks == rtoks
+    assert (st.accepted, st.proposed, st.rounds) == rst
+    assert a.pos == b.pos
+    a.free()
+    b.free()
+
+
+def test_sampled_loop_accepts_drafts_with_a_peaked_target(om):
+    # at a very low temperature the target is nearly one-hot on the argmax:
+    # the plain gumbel commit is the trunk's argmax, drafts from the greedy
+    # stream are kept, and the sampled stream is the greedy one
+    from codpiece_amd.model import fused_generate, sampled_generate
+    prompt = np.random.default_rng(6).integers(0, SMALL["n_vocab"], size=40).tolist()
+    g0 = cpvo.Session(om, 256)
+    greedy, _ = fused_generate(mf.OracleSession(g0), prompt, 24, 0, tail=8, bulk=32)
+    s = cpvo.Session(om, 256)
+    params = cpvo.SamplerParams(temp=1e-4)
+    noise = gumbel_noise(3, params.temp, SMALL["n_vocab"])
+    toks, st = sampled_generate(mf.OracleSession(s), prompt, 24, 3, params, GUMBEL, seed=1, tail=8, bulk=32,
+                                noise=noise, drafter=_lossless_drafter(greedy, 3, spoil_every=10 ** 9))
+    assert toks == greedy
+    assert st.accepted == st.proposed > 0
+    g0.free()
+    s.free()
+
+
+def _lossless_drafter(stream, depth, spoil_every=3):
+    state = {"round": 0}
+
+    def drafter(committed, chain):
+        state["round"] += 1
+        n = len(committed)
+        d = [stream[i] for i in range(n, min(n + depth, len(stream)))]
+        if d and state["round"] % spoil_every == 0:
+            j = state["round"] % len(d)
+            d[j] = (d[j] + 1) % SMALL["n_vocab"]
+        return d
+    return drafter
+
+
+@pytest.mark.parametrize("depth", [1, 2, 3, 4])
+def test_losslessness_gate_fused_depths_equal_plain_greedy(om, depth):
+    from codpiece_amd.model import fused_generate
+    prompt = np.random.default_rng(7).integers(0, SMALL["n_vocab"], size=50).tolist()
+    s0 = cpvo.Session(om, 256)
+    plain, st0 = fused_generate(mf.OracleSession(s0), prompt, 40, 0, tail=10, bulk=32)
+    assert st0.accepted == 0 and st0.rounds == 39
+    s = cpvo.Session(om, 256)
+    toks, st = fused_generate(mf.OracleSession(s), prompt, 40, depth, tail=10, bulk=32,
+                              drafter=_lossless_drafter(plain, depth))
+    assert toks == plain
+    assert st.accepted > st.rounds // 2          # multi-accept rounds happened
+    assert st.accepted < st.proposed             # and rejected drafts were rewound
+    # positions: every committed token but the last is in the trunk cache,
+    # and the MTP rows are the tail round's plus n_keep + 1 per round, unless
+    # the last round ended inside its accepted drafts (no rewind then)
+    if s.pos[0] == len(prompt) + len(plain) - 1:
+        assert s.pos[1] == 10 + st.accepted + st.rounds
+    else:
+        assert len(prompt) + len(plain) - 1 < s.pos[0] <= len(prompt) + len(plain) - 1 + depth
+    # the MTP drafts of the same loop (never accepted on random weights) give the same stream
+    s2 = cpvo.Session(om, 256)
+    toks2, _ = fused_generate(mf.OracleSession(s2), prompt, 40, depth, tail=10, bulk=32)
+    assert toks2 == plain
+    for x in (s0, s, s2):
+        x.free()
