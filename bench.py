@@ -16,16 +16,30 @@ second over the timed rounds (host loop included); `ms_per_step` the wall
 time of a round.  With random weights the drafts are almost never accepted,
 so a round commits ~1 token, as the reference would on the same weights.
 
-Beside the line's required fields: `detail` holds the device time of a
-round and of a verify-only round (depth 0) from HIP events, and the per-class
-kernel timing that `roofline` is computed from: extra rounds run with
-cpv_profile_start/stop, which records every GEMM and attention launch, and
-cpv_profile_replay launches each class's recorded launches again back to back
-between one pair of HIP events on the library's stream (per-launch events
-would add the dispatch gaps); `roofline.achieved` = the dominant class's mean
-algorithmic bytes per launch / its mean replayed launch time.  `cpu_baseline`
-times the oracle (the C restatement under oracle/, all host cores given)
-on one layer sample scaled to a round -- a reported baseline, not the target.
+Beside the line's required fields, `detail` holds:
+  * the device time of a round and of a verify-only round (depth 0), of a
+    round with the 8192-token shortlist head, and of the 16-node tree verify
+    and its branch commit, from HIP events on the library's stream;
+  * kernel_classes: extra rounds run with cpv_profile_start/stop, which
+    records every GEMM and attention launch; cpv_profile_replay launches
+    each class's recorded launches again back to back between one pair of
+    HIP events on the library's stream (per-launch events would add the
+    dispatch gaps); `roofline.achieved` = the dominant class's mean
+    algorithmic bytes per launch / its mean replayed launch time;
+  * step_cost_us: verify-only device time at T = 1, 2, 4, 8, 16 tokens
+    (main.rs:549-629);
+  * oracle_drafts: the fused loop with drafts from the plain greedy stream
+    (acceptance 1.0), accepted tok/s when every draft is right;
+  * sampled_T0.7_top_p0.95: the sampled loop's leg;
+  * gemm: the Q4_K and Q8_0 GEMMs at the four verify shapes x M in
+    {1, 5, 8, 16}, weights rotated over >= 512 MB;
+  * attention_tree16: tree attention at context 8192 and 32768;
+  * acceptance_sampler: the acceptance sampler at B = 1, 4, 16;
+  * prefill: the prompt's prefill and its wide GEMM.
+`cpu_baseline` runs whole verify rounds of the oracle (the C restatement of
+the reference's CPU path under oracle/) on the host threads this process is
+given, median of 5 -- a reported baseline, not the target; cpu_configs times
+the oracle's functions at the microbench shapes.
 """
 import argparse
 import json
@@ -38,8 +52,12 @@ import numpy as np
 HP = dict(n_layer=64, n_embd=5120, n_head=40, n_head_kv=8, head_dim=128, n_ff=17408, n_vocab=151936,
           n_rot=128, rope_sections=(22, 22, 20, 0), rms_eps=1e-6, freq_base=1e6, has_mtp=True)
 HBM_PEAK_GBS = 8000.0
+# the verify GEMM shapes (k, n): q|k|v of the gateless layout, wo, gate (= up), down
+GEMM_SHAPES = ((5120, 7168), (5120, 5120), (5120, 17408), (17408, 5120))
+# the canonical 16-node draft tree (widths 4, 6, 3, 3)
+TREE16 = [-1, -1, -1, -1, 0, 0, 0, 1, 1, 1, 4, 4, 4, 10, 10, 10]
 INT8_MFMA_PEAK_TOPS = 5000.0   # dense int8 MFMA, TOP/s
-Q4_K, Q6_K, F32 = 12, 14, 0
+Q8_0, Q4_K, Q6_K, F32 = 8, 12, 14, 0
 
 
 def parse():
@@ -54,7 +72,12 @@ def parse():
     ap.add_argument("--depth", type=int, default=4, help="drafts per round (k)")
     ap.add_argument("--profile-rounds", type=int, default=4)
     ap.add_argument("--cpu-baseline", type=int, default=1, help="0 skips the oracle timing")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU sample budget (seconds)")
+    ap.add_argument("--cpu-rounds", type=int, default=5, help="timed whole oracle rounds of the CPU baseline")
+    ap.add_argument("--cpu-configs", type=int, default=1, help="0 skips the oracle at configs 2-4's shapes")
+    ap.add_argument("--gemm", type=int, default=1, help="0 skips the GEMM microbench (4 shapes x M)")
+    ap.add_argument("--attn", type=int, default=1, help="0 skips the tree attention microbench")
+    ap.add_argument("--legs", type=int, default=1,
+                    help="0 skips the step-cost sweep, the oracle-drafts and the T = 0.7 legs")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--sampler", type=int, default=1, help="0 skips the acceptance-sampler microbench")
     ap.add_argument("--sampler-only", action="store_true", help="run only the acceptance-sampler microbench")
@@ -78,11 +101,20 @@ def synth_quant(torch, qtype, n_rows, k, gen, device):
         u = torch.rand(nb, device=device, generator=gen)
         raw[:, 0:2] = _fp16_bytes(torch, 1.5e-4 + 1e-4 * u)          # d
         raw[:, 2:4] = _fp16_bytes(torch, 1.2e-3 + 6e-4 * u)          # dmin (keeps the mean near 0)
+    elif qtype == Q8_0:
+        nb = n_rows * (k // 32)
+        raw = torch.randint(0, 256, (nb, 34), dtype=torch.uint8, device=device, generator=gen)
+        u = torch.rand(nb, device=device, generator=gen)
+        raw[:, 0:2] = _fp16_bytes(torch, 1.2e-4 + 6e-5 * u)          # d (codes are int8)
     else:
         raw = torch.randint(0, 256, (nb, 210), dtype=torch.uint8, device=device, generator=gen)
         u = torch.rand(nb, device=device, generator=gen)
         raw[:, 208:210] = _fp16_bytes(torch, 1.2e-5 + 6e-6 * u)      # d (scales are int8)
     return raw.view(-1)
+
+
+def row_bytes(qtype, k):
+    return k // 256 * 144 if qtype == Q4_K else k // 32 * 34 if qtype == Q8_0 else k // 256 * 210
 
 
 def tensor_specs(hp):
@@ -159,64 +191,134 @@ class Loop:
 
 
 # ---------------------------------------------------------------- CPU baseline
-def cpu_baseline(hp, layers, budget_s, tokens_per_round, depth, seed):
-    """Time the oracle on one layer's GEMMs + attention at the round's shapes
-    and the Q6_K head, then scale to a full round (trunk layers + head +
-    `depth` MTP links of layer + eh_proj + head)."""
-    import numpy as np
-    from oracle import cpvo
-    cores = min(len(os.sched_getaffinity(0)), 16)
-    rng = np.random.default_rng(seed)
-    E, H, Hkv, hd, F, V = hp["n_embd"], hp["n_head"], hp["n_head_kv"], hp["head_dim"], hp["n_ff"], hp["n_vocab"]
-    T = depth + 1
+def physical_cores():
+    """Physical cores of the host (distinct core/socket pairs in lscpu -p), or None."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu", "-p=CORE,SOCKET"], capture_output=True, text=True, timeout=20).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    cores = {line.strip() for line in out.splitlines() if line.strip() and not line.startswith("#")}
+    return len(cores) or None
 
-    def w(t, n, k):
-        raw = rng.integers(0, 256, size=n * cpvo.row_bytes(t, k), dtype=np.uint8)
-        if t == Q4_K:
-            b = raw.reshape(-1, 144)
-            b[:, 0:2] = np.frombuffer(np.float16(2e-4).tobytes(), np.uint8)
-            b[:, 2:4] = np.frombuffer(np.float16(1.5e-3).tobytes(), np.uint8)
+
+def cpu_threads():
+    """Host threads the CPU legs use: the process's CPU share (OMP_NUM_THREADS
+    when the launcher sets one, else the affinity mask)."""
+    aff = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(aff, int(env))) if env.isdigit() and int(env) > 0 else aff
+
+
+def _host_pool(rng, pools, qtype, nbytes):
+    """Random block bytes with fixed plausible scales, shared by every tensor
+    of a type (each tensor's copy in the oracle model is its own memory)."""
+    if qtype not in pools or pools[qtype].size < nbytes:
+        raw = rng.integers(0, 2 ** 63, size=(nbytes + 7) // 8, dtype=np.uint64).view(np.uint8)[:nbytes].copy()
+        if qtype == Q4_K:
+            blk = raw.reshape(-1, 144)
+            blk[:, 0:2] = np.frombuffer(np.float16(2e-4).tobytes(), np.uint8)
+            blk[:, 2:4] = np.frombuffer(np.float16(1.5e-3).tobytes(), np.uint8)
+        elif qtype == Q8_0:
+            blk = raw.reshape(-1, 34)
+            blk[:, 0:2] = np.frombuffer(np.float16(1.5e-4).tobytes(), np.uint8)
         else:
-            b = raw.reshape(-1, 210)
-            b[:, 208:210] = np.frombuffer(np.float16(1.5e-5).tobytes(), np.uint8)
-        return raw
+            blk = raw.reshape(-1, 210)
+            blk[:, 208:210] = np.frombuffer(np.float16(1.5e-5).tobytes(), np.uint8)
+        pools[qtype] = raw
+    return pools[qtype][:nbytes]
 
-    layer_w = [(w(Q4_K, n, k), k) for n, k in ((2 * H * hd, E), (Hkv * hd, E), (Hkv * hd, E), (E, H * hd),
-                                                (F, E), (F, E), (E, F))]
-    head = w(Q6_K, V, E)
-    eh = w(Q4_K, E, 2 * E)
-    n_past = 4096
-    kc = cpvo.f32_to_f16_bits(rng.normal(size=(n_past + T, Hkv * hd)).astype(np.float32))
-    q = rng.normal(size=(T, H, hd)).astype(np.float32)
 
-    def x(k):
-        return rng.normal(size=(T, k)).astype(np.float32)
-
-    def layer():
-        for wb, k in layer_w:
-            cpvo.qgemm(Q4_K, wb, x(k), cores)
-        cpvo.attn(q, kc, kc, n_past, None, np.float32(1 / np.sqrt(hd)))
-
-    def timed(fn, budget):
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            fn()
-            reps += 1
-            el = time.perf_counter() - t0
-            if el >= budget:
-                return el / reps, reps
-
-    t_layer, r_layer = timed(layer, budget_s * 0.7)
-    t_head, r_head = timed(lambda: cpvo.qgemm(Q6_K, head, x(E), cores), budget_s * 0.25)
-    t_eh, _ = timed(lambda: cpvo.qgemm(Q4_K, eh, x(2 * E), cores), budget_s * 0.05)
-    round_s = layers * t_layer + t_head + depth * (t_layer + t_eh + t_head)
+def cpu_baseline(hp, threads, tokens_per_round, depth, seed, reps=5):
+    """Whole verify rounds of the oracle (the C restatement of the reference's
+    CPU ggml semantics under oracle/, not ggml itself) on the host: the
+    27B-class model with synthetic weights in host memory, the session at
+    n_past 4096 over a zero-filled KV cache (attention's cost does not depend
+    on the values), rounds of [last] + `depth` drafts with the MTP chain,
+    rewound after each; the median of `reps` rounds after one untimed."""
+    from oracle import cpvo
+    rng = np.random.default_rng(seed)
+    t0 = time.perf_counter()
+    m = cpvo.Model(hp)
+    pools = {}
+    for name, t, ne0, ne1 in tensor_specs(hp):
+        if t == F32:
+            m.set_tensor(name, t, np.ones(ne0, np.float32), ne0, ne1)
+        else:
+            m.set_tensor(name, t, _host_pool(rng, pools, t, ne1 * row_bytes(t, ne0)), ne0, ne1)
+    pools.clear()
+    build_s = time.perf_counter() - t0
+    cpvo.set_threads(threads)
+    n_past, mtp_past = 4096, 64
+    s = cpvo.Session(m, n_past + 64)
+    toks = rng.integers(0, hp["n_vocab"], size=depth + 1).tolist()
+    times = []
+    for r in range(reps + 1):
+        s.set_pos(n_past, mtp_past)
+        t1 = time.perf_counter()
+        s.step_fused_cached(toks, depth)
+        if r:
+            times.append(time.perf_counter() - t1)
+        print(f"[bench] cpu round {r}: {time.perf_counter() - t1:.2f} s", file=sys.stderr, flush=True)
+    s.free()
+    m.free()
+    times.sort()
+    round_s = times[len(times) // 2]
     return {
-        "value": tokens_per_round / round_s, "unit": "tok/s", "cores": cores, "kind": "port",
-        "sample": (f"oracle (exact-window GEMMs, exact-contract attention) on one trunk layer at t={T}, n_past={n_past} "
-                   f"({r_layer} reps, {t_layer * 1e3:.1f} ms), the Q6_K head ({r_head} reps, {t_head * 1e3:.1f} ms) "
-                   f"and eh_proj, scaled to a round of {layers} layers + head + {depth} MTP links "
-                   f"= {round_s:.2f} s, at the GPU run's {tokens_per_round:.3f} committed tokens per round"),
+        "value": round(tokens_per_round / round_s, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+        "physical_cores_lscpu": physical_cores(), "round_s_median": round(round_s, 3),
+        "round_s_all": [round(x, 3) for x in times],
+        "sample": (f"the oracle (the repo's C restatement of the reference's CPU ggml path: exact-window GEMMs, "
+                   f"exact-contract attention; not ggml, which is not vendored) timing {reps} whole verify rounds "
+                   f"(median, one untimed first) of the same 27B-class model ({hp['n_layer']} layers, synthetic "
+                   f"weights in host memory, built in {build_s:.0f} s) at n_past {n_past} over a zero-filled KV "
+                   f"cache, {depth + 1} tokens + a {depth}-link MTP chain per round, on {threads} threads, at "
+                   f"the GPU run's {tokens_per_round:.3f} committed tokens per round"),
     }
+
+
+def cpu_configs(threads, seed):
+    """The oracle's functions at configs 2-4's shapes on the host: the
+    acceptance decision at B = 1 (T = 0.7, top-p 0.95, draft distribution),
+    the Q4_K and Q8_0 GEMMs at M = 5 and the 16-node tree attention at
+    context 8192; median of 3 timed calls each."""
+    from oracle import cpvo
+    rng = np.random.default_rng(seed + 5)
+    pools = {}
+
+    def med(fn, n=3):
+        fn()
+        ts = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[n // 2]
+
+    out = {"threads": threads, "gemm_m5": {}}
+    for qt, name in ((Q4_K, "q4_k"), (Q8_0, "q8_0")):
+        for k, n in GEMM_SHAPES:
+            wb = _host_pool(rng, pools, qt, n * row_bytes(qt, k))
+            x = rng.normal(size=(5, k)).astype(np.float32)
+            sec = med(lambda: cpvo.qgemm(qt, wb, x, threads))
+            out["gemm_m5"][f"{name}_{k}x{n}"] = {"us": round(sec * 1e6, 1),
+                                                 "GB_s": round(n * row_bytes(qt, k) / sec / 1e9, 2)}
+    pools.clear()
+    H, Hkv, hd, n_past = 40, 8, 128, 8192
+    kc = cpvo.f32_to_f16_bits(rng.normal(size=(n_past + 16, Hkv * hd)).astype(np.float32))
+    q = rng.normal(size=(16, H, hd)).astype(np.float32)
+    sec = med(lambda: cpvo.attn(q, kc, kc, n_past, TREE16, np.float32(1 / np.sqrt(hd))))
+    out["attention_tree16_ctx8192"] = {"us": round(sec * 1e6, 1),
+                                       "GB_s": round(2 * kc.nbytes / sec / 1e9, 2)}
+    V, k = 151936, 4
+    pl = (rng.normal(size=(1, k + 1, V)) * 3).astype(np.float32)
+    ql = (pl[:, :k] + rng.normal(size=(1, k, V))).astype(np.float32)
+    dr = rng.integers(0, V, size=(1, k)).astype(np.int32)
+    prm = cpvo.SamplerParams(temp=0.7, top_p=0.95)
+    sec = med(lambda: cpvo.spec_accept(pl, dr, prm, cpvo.ACCEPT_REJECT, u=cpvo.philox_uniforms(seed, 1, k),
+                                       q_logits=ql))
+    out["acceptance_reject_draft_dist_b1"] = {"us": round(sec * 1e6, 1), "threads": 1}
+    return out
 
 
 # ---------------------------------------------------------------- sampler
@@ -265,6 +367,156 @@ def sampler_bench(torch, ctx, seed, reps=20):
         print(f"[bench] sampler B={B}: " + ", ".join(f"{k2} {v['us_per_call']} us" for k2, v in res.items()),
               file=sys.stderr, flush=True)
     return out
+
+
+def gemm_bench(torch, ctx, seed, rotate_bytes=512e6):
+    """The verify GEMM at its shapes: Q4_K and Q8_0 weights (random blocks
+    with plausible scales) x f32 activations ~N(0, 1) of M rows, for each of
+    GEMM_SHAPES and M in {1, 5, 8, 16}.  Each shape's weights are uploaded in
+    enough copies to cover `rotate_bytes` (more than the 256 MB last-level
+    cache), and consecutive calls rotate through them, so every call streams
+    its weights from HBM.  `us` is the GEMM kernels' time per call (the
+    recorded launches replayed back to back between one event pair, as for
+    the roofline); `us_call` adds the activation quantization and the
+    finalize kernel (whole calls back to back, one event pair).  Algorithmic
+    bytes per call: the weight blocks, the quantized activations and the f32
+    outputs."""
+    gen = torch.Generator(device=ctx.torch_device).manual_seed(seed + 11)
+    dev = ctx.torch_device
+    out = {}
+    for qt, name in ((Q4_K, "q4_k"), (Q8_0, "q8_0")):
+        cls = "qgemm_" + name
+        for k, n in GEMM_SHAPES:
+            wbytes = n * row_bytes(qt, k)
+            copies = max(2, int(np.ceil(rotate_bytes / wbytes)))
+            ws = []
+            for _ in range(copies):
+                raw = synth_quant(torch, qt, n, k, gen, dev)
+                ws.append(ctx.upload_weight(qt, raw, n, k))
+                del raw
+            res = {"weights_MB": round(wbytes / 1e6, 2), "copies_rotated": copies}
+            for M in (1, 5, 8, 16):
+                x = torch.randn(M, k, device=dev, generator=gen)
+                y = torch.empty(M, n, device=dev)
+                for w in ws[:2]:
+                    ctx.qgemm(w, x, y)
+                ctx.profile_start()
+                for w in ws:
+                    ctx.qgemm(w, x, y)
+                prof = ctx.profile_stop()
+                launches = prof[cls][0]
+                ms, b = ctx.profile_replay(cls, reps=3)
+                per = launches / copies
+                us = ms * 1e3 * per
+                gbs = b * per / (us * 1e-6) / 1e9
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for w in ws:
+                    ctx.qgemm(w, x, y)
+                e1.record()
+                torch.cuda.synchronize()
+                res[f"M={M}"] = {"us": round(us, 2), "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                                 "MB": round(b * per / 1e6, 2), "launches": per,
+                                 "us_call": round(e0.elapsed_time(e1) * 1e3 / copies, 2)}
+            out[f"{name} {k}x{n}"] = res
+            print(f"[bench] gemm {name} {k}x{n}: " + ", ".join(f"{m} {v['us']} us ({v['frac']:.2f})"
+                                                              for m, v in res.items() if m.startswith("M=")),
+                  file=sys.stderr, flush=True)
+            for w in ws:
+                w.free()
+    return out
+
+
+def attn_bench(torch, ctx, seed, reps=10):
+    """Tree-verify attention: 40 Q / 8 KV heads x 128 over an f16 KV cache
+    ~N(0, 1) of n_ctx rows plus the 16 nodes of TREE16 (ancestor-only mask),
+    at n_ctx 8192 and 32768; each call replayed `reps` times between one
+    event pair.  Algorithmic bytes: K and V rows once, q in and the output."""
+    gen = torch.Generator(device=ctx.torch_device).manual_seed(seed + 13)
+    dev = ctx.torch_device
+    H, Hkv, hd, t = 40, 8, 128, len(TREE16)
+    par = torch.tensor(TREE16, dtype=torch.int32, device=dev)
+    out = {}
+    for n_ctx in (8192, 32768):
+        rows = n_ctx + t
+        kc = torch.randn(rows, Hkv * hd, device=dev, generator=gen).half().view(torch.int16)
+        vt = torch.zeros(Hkv * hd, (rows + 7) // 8 * 8, dtype=torch.float16, device=dev)
+        vt[:, :rows] = torch.randn(Hkv * hd, rows, device=dev, generator=gen).half()
+        vt = vt.view(torch.int16)
+        q = torch.randn(t, H, hd, device=dev, generator=gen)
+        o = torch.empty(t, H * hd, device=dev)
+        scale = 1.0 / float(np.sqrt(hd))
+        ctx.attn(q, kc, vt, n_ctx, par, Hkv, scale, out=o)
+        ctx.profile_start()
+        ctx.attn(q, kc, vt, n_ctx, par, Hkv, scale, out=o)
+        ctx.profile_stop()
+        ms, b = ctx.profile_replay("attention", reps=reps)
+        gbs = b / (ms * 1e-3) / 1e9
+        out[f"ctx={n_ctx}"] = {"us": round(ms * 1e3, 2), "MB": round(b / 1e6, 2), "GB_s": round(gbs, 1),
+                               "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        print(f"[bench] attention tree16 ctx {n_ctx}: {ms * 1e3:.1f} us ({gbs:.0f} GB/s)", file=sys.stderr,
+              flush=True)
+        del kc, vt
+    return out
+
+
+def step_cost_sweep(torch, sess, stream, toks, reps=5):
+    """The verify step's device time against the tokens it carries
+    (crates/codpiece-cli/src/main.rs:549-629, stepcost): verify-only rounds
+    (no MTP chain) of T tokens in a chain, median of `reps`, rewound after
+    each."""
+    n_past, mtp_past = sess.pos
+    out = {}
+    for T in (1, 2, 4, 8, 16):
+        ts = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            sess.step_fused_cached(toks[:T], 0)
+            b.record(stream)
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+            sess.set_pos(n_past, mtp_past)
+        ts.sort()
+        out[f"T={T}"] = round(ts[len(ts) // 2] * 1e3, 1)
+    print("[bench] step cost (us): " + ", ".join(f"{k} {v}" for k, v in out.items()), file=sys.stderr, flush=True)
+    return out
+
+
+def oracle_drafts_leg(sess, prompt, depth, chunk, n_gen=64):
+    """Accepted tokens/s when every draft is right: the plain greedy stream
+    (depth 0) is generated first, then the fused loop runs with drafts taken
+    from that stream (an oracle drafter), so each round accepts all `depth`
+    drafts and commits depth + 1 tokens.  The committed stream must equal the
+    plain one (losslessness)."""
+    from codpiece_amd.model import fused_generate
+    sess.set_pos(0, 0)
+    plain, _ = fused_generate(sess, prompt, n_gen, 0, tail=64, bulk=chunk)
+
+    def drafter(committed, chain):
+        n = len(committed)
+        return plain[n:n + depth]
+
+    sess.set_pos(0, 0)
+    toks, st = fused_generate(sess, prompt, n_gen, depth, tail=64, bulk=chunk, drafter=drafter)
+    return {"tokens": len(toks), "rounds": st.rounds, "acceptance": round(st.accepted / max(1, st.proposed), 4),
+            "tokens_per_round": round((len(toks) - 1) / max(1, st.rounds), 3),
+            "decode_s": round(st.decode_s, 4), "tok_s": round((len(toks) - 1) / st.decode_s, 2),
+            "stream_equals_plain_greedy": toks == plain}
+
+
+def sampled_leg(sess, prompt, depth, chunk, seed, n_gen=64):
+    """The T = 0.7 / top-p 0.95 leg: the sampled speculative loop (rejection
+    rule on the device with Philox uniforms, MTP drafts) at the workload."""
+    from codpiece_amd import _lib
+    from codpiece_amd.model import sampled_generate
+    from codpiece_amd.runtime import SamplerParams
+    sess.set_pos(0, 0)
+    toks, st = sampled_generate(sess, prompt, n_gen, depth, SamplerParams(temp=0.7, top_p=0.95),
+                                _lib.ACCEPT_REJECT, seed=seed, tail=64, bulk=chunk)
+    return {"tokens": len(toks), "rounds": st.rounds, "acceptance": round(st.accepted / max(1, st.proposed), 4),
+            "tokens_per_round": round((len(toks) - 1) / max(1, st.rounds), 3),
+            "decode_s": round(st.decode_s, 4), "tok_s": round((len(toks) - 1) / st.decode_s, 2)}
 
 
 def prefill_gemm_stats(ctx, prof, hp, rows):
@@ -435,6 +687,12 @@ def main():
     tv.sort()
     tc.sort()
 
+    step_cost = None
+    if args.legs:
+        sweep_toks = [loop.last] + loop.drafts
+        sweep_toks += torch.randint(0, hp["n_vocab"], (16 - len(sweep_toks),), generator=g).tolist()
+        step_cost = step_cost_sweep(torch, sess, stream, sweep_toks)
+
     # per-class kernel timing over extra rounds (events between launches: not in the timed region)
     ctx.profile_start()
     for _ in range(args.profile_rounds):
@@ -452,11 +710,22 @@ def main():
         with open(tpath) as f:
             traffic = json.load(f).get(dom)
 
-    cpu = None
-    if args.cpu_baseline:
-        cpu = cpu_baseline(hp, args.layers, args.cpu_seconds, committed / args.steps, args.depth, args.seed)
-
+    oracle_drafts = sampled = None
+    if args.legs:
+        oracle_drafts = oracle_drafts_leg(sess, prompt, args.depth, chunk)
+        print(f"[bench] oracle drafts: {oracle_drafts}", file=sys.stderr, flush=True)
+        sampled = sampled_leg(sess, prompt, args.depth, chunk, args.seed)
+        print(f"[bench] T=0.7 leg: {sampled}", file=sys.stderr, flush=True)
+    gemm = gemm_bench(torch, ctx, args.seed) if args.gemm else None
+    attn = attn_bench(torch, ctx, args.seed) if args.attn else None
     sampler = sampler_bench(torch, ctx, args.seed) if args.sampler else None
+
+    threads = cpu_threads()
+    cpu = cpu_cfg = None
+    if args.cpu_baseline:
+        cpu = cpu_baseline(hp, threads, committed / args.steps, args.depth, args.seed, reps=args.cpu_rounds)
+    if args.cpu_configs:
+        cpu_cfg = cpu_configs(threads, args.seed)
 
     value = committed / wall
     line = {
@@ -491,6 +760,12 @@ def main():
                         "device_s": round(prefill_dev, 3), "tokens_per_s": round(args.prompt / prefill_dev, 1),
                         "gemm_q4_k_wide": prefill_gemm},
             "acceptance_sampler": sampler,
+            "step_cost_us": step_cost,
+            "oracle_drafts": oracle_drafts,
+            "sampled_T0.7_top_p0.95": sampled,
+            "gemm": gemm,
+            "attention_tree16": attn,
+            "cpu_configs": cpu_cfg,
         },
     }
     print(json.dumps(line), flush=True)

@@ -217,6 +217,8 @@ void          cpvo_set_attn_f64(int on);
  * round becomes a smooth function of its inputs, for composition checks
  * against a float64 forward (0 = ggml's quantized activations, the default). */
 void          cpvo_set_smooth(int on);
+/* threads of the model round's GEMMs and attention (default 8) */
+void          cpvo_set_threads(int n);
 int           cpvo_prefill(cpvo_session* s, const int32_t* tok, int t);
 /* step_fused_cached: preds [t], chain [depth][t], conf [depth][t] (nullable),
  * logits [t][V] and hidden [t][E] (nullable); noise [t][V] or NULL */

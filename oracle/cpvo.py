@@ -107,6 +107,7 @@ def lib():
             "cpvo_set_fault": (None, [ctypes.c_int]),
             "cpvo_set_attn_f64": (None, [ctypes.c_int]),
             "cpvo_set_smooth": (None, [ctypes.c_int]),
+            "cpvo_set_threads": (None, [ctypes.c_int]),
             "cpvo_prefill": (ctypes.c_int, [P, P, ctypes.c_int]),
             "cpvo_verify_step": (ctypes.c_int, [P, P, ctypes.c_int, ctypes.c_int, P, P, P, P, P, P]),
             "cpvo_verify_step_cands": (ctypes.c_int, [P, P, ctypes.c_int, ctypes.c_int, P, P, ctypes.c_int, P, P, P,
@@ -402,6 +403,11 @@ def set_attn_f64(on):
 def set_smooth(on):
     """Run the model round's mul_mats on unquantized activations (binary64 sums)."""
     lib().cpvo_set_smooth(1 if on else 0)
+
+
+def set_threads(n):
+    """Threads of the model round's GEMMs and attention."""
+    lib().cpvo_set_threads(int(n))
 
 
 class Hparams(ctypes.Structure):

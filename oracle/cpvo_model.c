@@ -8,6 +8,7 @@
  * and crates/codpiece-cli/src/main.rs:643-931 (cmd_fused) for the loop. */
 #include "cpvo.h"
 #include <math.h>
+#include <omp.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -23,6 +24,13 @@ void cpvo_set_attn_f64(int on) { g_attn_f64 = on; }
 /* mul_mat on the unquantized f32 activation rows, summed in binary64 */
 static int g_smooth = 0;
 void cpvo_set_smooth(int on) { g_smooth = on; }
+/* threads of the round's GEMMs and attention */
+static int g_threads = 8;
+void cpvo_set_threads(int n)
+{
+    g_threads = n > 0 ? n : 1;
+    omp_set_num_threads(g_threads);
+}
 
 typedef struct {
     wt_t wq, wk, wv, wo, gate, up, down;
@@ -176,11 +184,11 @@ void cpvo_session_get_pos(const cpvo_session* s, int64_t* n_past, int64_t* mtp_p
 static void mm(const wt_t* w, const float* x, int T, float* y)
 {
     if (!g_smooth) {
-        cpvo_qgemm(w->type, w->data, w->ne1, w->ne0, x, T, y, 8);
+        cpvo_qgemm(w->type, w->data, w->ne1, w->ne0, x, T, y, g_threads);
         return;
     }
     const int64_t K = w->ne0, rb = cpvo_row_bytes(w->type, K);
-    #pragma omp parallel for num_threads(8)
+    #pragma omp parallel for num_threads(g_threads)
     for (int64_t n = 0; n < w->ne1; n++) {
         float* wr = malloc(sizeof(float) * (size_t)K);
         cpvo_dequantize(w->type, w->data + n * rb, K, wr);
