@@ -127,10 +127,17 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
 {
     constexpr int TPR = D / 16;                // threads per row when converting (16 values each)
     constexpr int RPP = CT / TPR;              // rows per pass
-    __shared__ __align__(16) int8_t s_qh[QB][D], s_ql[QB][D];
-    __shared__ __align__(16) int8_t s_kh[CHUNK][D], s_kl[CHUNK][D];
-    __shared__ __align__(16) float s_w[QB][CHUNK];     // scores
-    __shared__ __align__(16) float s_pt[CHUNK][QB];    // the f16-rounded weights (as f32), row-minor
+    // rows padded by 16 bytes (limbs, scores) and 4 floats (weights): the
+    // MFMA operand reads, the score writes and the transposed weight writes
+    // then fall on distinct LDS banks.  The weights take the K limbs' place
+    // once the scores are done.
+    __shared__ __align__(16) int8_t s_qh[QB][D + 16], s_ql[QB][D + 16];
+    __shared__ __align__(16) int8_t s_kbuf[2][CHUNK][D + 16];
+    __shared__ __align__(16) float s_w[QB][CHUNK + 4];     // scores
+    static_assert(sizeof(float) * CHUNK * (QB + 4) <= sizeof(s_kbuf), "weights fit the K limbs' space");
+    int8_t(*s_kh)[D + 16] = s_kbuf[0];
+    int8_t(*s_kl)[D + 16] = s_kbuf[1];
+    float(*s_pt)[QB + 4] = (float(*)[QB + 4]) & s_kbuf[0][0][0];   // the f16-rounded weights (as f32), row-minor
     __shared__ int s_eq[QB], s_ek[CHUNK];
     __shared__ unsigned long long s_anc[QB];
     __shared__ uint64_t s_etab[32];                     // the expf table
@@ -257,19 +264,20 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     }
     __syncthreads();
 
-    // ---- the chunk's softmax: SPR threads per query row, EPT cache rows each
+    // ---- the chunk's softmax: SPR threads per query row, EPT cache rows
+    // each (rows part, part + SPR, ...: consecutive lanes, consecutive rows)
     {
         constexpr int SPR = CT / QB, EPT = CHUNK / SPR;
         const int r = tid / SPR, part = tid % SPR;
         const int lr = blockIdx.z * QB + r;
         float m = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < EPT; i++) m = fmaxf(m, s_w[r][part * EPT + i]);
+        for (int i = 0; i < EPT; i++) m = fmaxf(m, s_w[r][part + SPR * i]);
         m = cpv_group_reduce<SPR>(m, cpv_op_max());
         long long z = 0;
 #pragma unroll
         for (int i = 0; i < EPT; i++) {
-            const int jl = part * EPT + i;
+            const int jl = part + SPR * i;
             const float w = s_w[r][jl];
             float p = 0.0f;
             if (w != -INFINITY) {
@@ -399,18 +407,8 @@ __global__ __launch_bounds__(D) void attn_fold_kernel(const float* __restrict__ 
         for (int c = 0; c < nchunk; c++) Zt = Zt + s_z[c] * (double)s_f[c];
         s_inv = (float)(1.0 / Zt);
     }
-    float o = 0.0f;
     const float* pr = P + (int64_t)row * D + d;
-    const int64_t cs = (int64_t)rows * D;
-    int c = 0;
-    for (; c + 8 <= nchunk; c += 8) {
-        float v[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = pr[(c + i) * cs];
-#pragma unroll
-        for (int i = 0; i < 8; i++) o = fmaf(v[i], s_f[c + i], o);
-    }
-    for (; c < nchunk; c++) o = fmaf(pr[c * cs], s_f[c], o);
+    const float o = cpv_fold_chain(pr, (int64_t)rows * D, s_f, nchunk);
     __syncthreads();
     out[(int64_t)row * D + d] = o * s_inv;
 }

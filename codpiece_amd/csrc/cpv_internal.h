@@ -354,6 +354,35 @@ struct cpv_attn_part {
     int nchunk, rows;
     int zbits;            // zc holds Z_c 2^zbits
 };
+// o = fmaf(p[c * cs], f[c], o) for c = 0 .. n-1 in order from +0 (the
+// attention's fold over its chunk partials, n >= 1): each batch of loads goes
+// out, at clamped in-bounds indexes and without a branch, one batch ahead of
+// the chain that consumes it
+__device__ __forceinline__ float cpv_fold_chain(const float* p, int64_t cs, const float* f, int n)
+{
+    constexpr int B = 16;
+    float cur[B];
+#pragma unroll
+    for (int i = 0; i < B; i++) cur[i] = p[(int64_t)(i < n ? i : n - 1) * cs];
+    float o = 0.0f;
+    int c = 0;
+    for (; c + B <= n; c += B) {
+        float nxt[B];
+#pragma unroll
+        for (int i = 0; i < B; i++) {
+            const int k = c + B + i;
+            nxt[i] = p[(int64_t)(k < n ? k : n - 1) * cs];
+        }
+#pragma unroll
+        for (int i = 0; i < B; i++) o = fmaf(cur[i], f[c + i], o);
+#pragma unroll
+        for (int i = 0; i < B; i++) cur[i] = nxt[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B; i++)
+        if (c + i < n) o = fmaf(cur[i], f[c + i], o);
+    return o;
+}
 cpv_status cpv_attn_partials(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                              int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
                              cpv_attn_part* part);

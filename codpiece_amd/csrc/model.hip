@@ -516,19 +516,9 @@ __global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
             for (int c = 0; c < nch; c++) Zt = Zt + s_z[lh][c] * (double)s_f[lh][c];
             s_inv[lh] = (float)(1.0 / Zt);
         }
-        // the element's fma chain, loads issued eight at a time
+        // the element's fma chain over the chunks
         const float* pr = a.part.P + (int64_t)rr * hd + (ec - h * hd);
-        const int64_t cs = (int64_t)rows * hd;
-        float o = 0.0f;
-        int c = 0;
-        for (; c + 8 <= nch; c += 8) {
-            float v[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) v[i] = pr[(c + i) * cs];
-#pragma unroll
-            for (int i = 0; i < 8; i++) o = fmaf(v[i], s_f[lh][c + i], o);
-        }
-        for (; c < nch; c++) o = fmaf(pr[c * cs], s_f[lh][c], o);
+        const float o = cpv_fold_chain(pr, (int64_t)rows * hd, s_f[lh], nch);
         __syncthreads();
         const float at = o * s_inv[lh];
         const float gv = a.gate[(int64_t)m * n + ec];
