@@ -155,9 +155,10 @@ __device__ __forceinline__ int divmod_small(int a, int d, float rf, int* r)
 }
 
 // waves per workgroup (one workgroup per CU; 12 waves, where registers
-// allow 3 per SIMD, measured slower)
+// allow 3 per SIMD, measured slower).  Q8_0 above 8 rows: one wave per SIMD,
+// the whole register file per wave (its 17-piece items do not fit two).
 template <int TYPE, int MC>
-constexpr int gemm_waves() { return 8; }
+constexpr int gemm_waves() { return MC > 8 && TYPE == CPV_Q8_0 ? 4 : 8; }
 
 __device__ __forceinline__ v4i mfma4(int a, int b, v4i c)
 {
@@ -471,14 +472,21 @@ __global__ __launch_bounds__((64 * gemm_waves<TYPE, MC>())) void qgemm_kernel(Ge
     if constexpr (F::BS > 0)
         for (int i = tid + BB * NT; i < nbs; i += NT) s_bs[i] = *bs_src(i);
     for (int i = tid; i < nt * M * 64; i += NT) s_acc[i] = 0.0;
-    if (wave < M) {
-        float mx = fmaxf(lane < nrow ? fabsf(ev0) : 0.0f, lane + 64 < nrow ? fabsf(ev1) : 0.0f);
-        for (int i = lane + 128; i < nrow; i += 64) mx = fmaxf(mx, fabsf(dr[i]));
+    // (rows past the waves, when there are more rows than waves, in further passes)
+    for (int r = wave; r < M; r += GEMM_WAVES) {
+        const float* drr = a.da + (int64_t)(a.m0 + r) * nrow;
+        float mx = 0.0f;
+        int ib = lane;
+        if (r == wave) {
+            mx = fmaxf(lane < nrow ? fabsf(ev0) : 0.0f, lane + 64 < nrow ? fabsf(ev1) : 0.0f);
+            ib = lane + 128;
+        }
+        for (int i = ib; i < nrow; i += 64) mx = fmaxf(mx, fabsf(drr[i]));
         mx = cpv_wave_reduce(mx, cpv_op_max());
         if (lane == 0) {
             int e = CPV_E_EMPTY;
             if (mx > 0.0f) frexpf(mx, &e);
-            s_ea[wave] = e;
+            s_ea[r] = e;
         }
     }
     __syncthreads();
@@ -491,13 +499,22 @@ __global__ __launch_bounds__((64 * gemm_waves<TYPE, MC>())) void qgemm_kernel(Ge
             const int m = 4 * r + (lane & 3);
             arow[r] = s_codes + (m < M ? m : M - 1) * cstride;
         }
+        // 2^(win - Ea) of each row; above 8 rows built from its bits out of the
+        // wave-uniform exponent (the same value), so that it stays in scalar
+        // registers (win - Ea + 1023 lies in [1, 2046] for every f32 Ea)
         int mrow[MC];
         double sm[MC];
 #pragma unroll
         for (int m = 0; m < MC; m++) {
             mrow[m] = m < M ? m : M - 1;
-            const int e = s_ea[mrow[m]];
-            sm[m] = e == CPV_E_EMPTY ? 0.0 : ldexp(1.0, a.win - e);
+            if constexpr (MC > 8) {
+                const int e = __builtin_amdgcn_readfirstlane(s_ea[mrow[m]]);
+                const uint64_t bits = e == CPV_E_EMPTY ? 0ull : (uint64_t)(1023 + a.win - e) << 52;
+                sm[m] = __builtin_bit_cast(double, bits);
+            } else {
+                const int e = s_ea[mrow[m]];
+                sm[m] = e == CPV_E_EMPTY ? 0.0 : ldexp(1.0, a.win - e);
+            }
         }
 
         double S[MC];
@@ -516,16 +533,29 @@ __global__ __launch_bounds__((64 * gemm_waves<TYPE, MC>())) void qgemm_kernel(Ge
         };
         // the item's unit as an LDS slot
         auto slot = [&](int u) { return u >= us ? u - us : u - us + U; };
-        // loads are unconditional (past the run they reload its last item)
+        // one item for all rows: above 8 rows, in passes of 8 over the same
+        // weight registers (each pass's working set alone fits the register file)
+        auto unit = [&](const v4i* buf, uint16_t d6, int er, int su) {
+            if constexpr (MC <= 8) {
+                gemm_unit<TYPE, MC>(buf, d6, er, su, M, nu, arow, mrow, sm, s_da, s_bs, S);
+            } else {
+#pragma unroll
+                for (int h = 0; h < MC / 8; h++) {
+                    gemm_unit<TYPE, 8>(buf, d6, er, su, M, nu, arow + 2 * h, mrow + 8 * h, sm + 8 * h, s_da, s_bs,
+                                       S + 8 * h);
+                    asm volatile("" ::: "memory");   // (keeps the passes apart in the schedule)
+                }
+            }
+        };
         for (int it = i0; it < i1; it += 2) {
             if (cur.tile != tile) { flush(); tile = cur.tile; }
-            gemm_unit<TYPE, MC>(bufA, dA, eA, slot(cur.u), M, nu, arow, mrow, sm, s_da, s_bs, S);
+            unit(bufA, dA, eA, slot(cur.u));
             load(nl, bufA, dA, eA);
             nl = step(nl);
             if (it + 1 >= i1) break;
             cur = step(cur);
             if (cur.tile != tile) { flush(); tile = cur.tile; }
-            gemm_unit<TYPE, MC>(bufB, dB, eB, slot(cur.u), M, nu, arow, mrow, sm, s_da, s_bs, S);
+            unit(bufB, dB, eB, slot(cur.u));
             load(nl, bufB, dB, eB);
             nl = step(nl);
             cur = step(cur);
@@ -603,7 +633,11 @@ cpv_status launch_type(cpv_ctx* ctx, const GemmArgs& a, float* y, int64_t N, int
     if (a.M <= 2) return launch_mc<TYPE, 2>(ctx, a, y, N, k, wbytes);
     if (a.M <= 4) return launch_mc<TYPE, 4>(ctx, a, y, N, k, wbytes);
     if (a.M <= 5) return launch_mc<TYPE, 5>(ctx, a, y, N, k, wbytes);
-    return launch_mc<TYPE, 8>(ctx, a, y, N, k, wbytes);
+    if constexpr (TYPE == CPV_Q6_K) return launch_mc<TYPE, 8>(ctx, a, y, N, k, wbytes);
+    else {
+        if (a.M <= 8) return launch_mc<TYPE, 8>(ctx, a, y, N, k, wbytes);
+        return launch_mc<TYPE, 16>(ctx, a, y, N, k, wbytes);
+    }
 }
 
 template <int TYPE>
@@ -744,8 +778,11 @@ static cpv_status qgemm_into(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* a
     }
     const size_t lds_cap = ctx->lds_max - 1024;
     for (int64_t m0 = 0; m0 < m;) {
-        int M = (int)((m - m0) < 8 ? (m - m0) : 8);
-        while (M > 1 && lds(M) > lds_cap) M--;      // rows per launch: up to 8, as many as LDS holds
+        // rows per launch: up to 16 (Q6_K: 8, whose 16-row pass measured slower
+        // than two 8-row ones: 397 vs 333 us for the 151,936-row head), as many as LDS holds
+        const int cap = w->type == CPV_Q6_K ? 8 : 16;
+        int M = (int)((m - m0) < cap ? (m - m0) : cap);
+        while (M > 1 && lds(M) > lds_cap) M--;
         if (lds(M) > lds_cap)
             return cpv_fail(ctx, CPV_EUNSUPPORTED, "qgemm: k=%lld needs more LDS than a CU has", (long long)w->k);
         a.m0 = (int)m0;

@@ -3,7 +3,8 @@
 Bar: bit-exact.  The GEMM contract sums exact integers, so the HIP kernel must
 reproduce the oracle's f32 outputs bit for bit at every shape, including the
 27B-class verify shapes (K, N) in {(5120, 7168), (5120, 5120), (5120, 17408),
-(17408, 5120)} with M in {1, 5, 8, 16}.
+(17408, 5120)} with M in {1, 5, 8, 16}; up to 16 rows share one pass over
+the weights (12 and 24 rows check the partial and split launches).
 """
 import numpy as np
 import pytest
@@ -50,7 +51,7 @@ def run_case(ctx, t, n, k, m, seed=0, xscale=1.0):
 
 @pytest.mark.parametrize("tname", list(TYPES))
 @pytest.mark.parametrize("n,k", [(64, 256), (48, 512), (1000, 768), (33, 1024), (160, 4096)])
-@pytest.mark.parametrize("m", [1, 3, 5, 16])
+@pytest.mark.parametrize("m", [1, 3, 5, 12, 16, 24])
 def test_qgemm_bit_exact_small(ctx, tname, n, k, m):
     t = TYPES[tname]
     y, ref = run_case(ctx, t, n, k, m)
@@ -66,10 +67,12 @@ def test_qgemm_bit_exact_verify_shapes(ctx, tname, k, n, m):
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), np.abs(y - ref).max()
 
 
-def test_qgemm_lm_head_q6_k(ctx):
+@pytest.mark.parametrize("m", [5, 16])
+def test_qgemm_lm_head_q6_k(ctx, m):
     # the output projection of the 27B-class layout: Q6_K, K = 5120, a slice of
-    # the 151,936 vocabulary rows (full vocab is covered by the e2e test)
-    y, ref = run_case(ctx, cpvo.Q6_K, 4096, 5120, 5)
+    # the 151,936 vocabulary rows (full vocab is covered by the e2e test); 16
+    # rows are a draft tree's
+    y, ref = run_case(ctx, cpvo.Q6_K, 4096, 5120, m)
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
 
 
