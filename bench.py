@@ -83,6 +83,7 @@ def parse():
     ap.add_argument("--sampler-only", action="store_true", help="run only the acceptance-sampler microbench")
     ap.add_argument("--gguf-load-only", type=int, default=0, metavar="LAYERS",
                     help="only time loading a seeded 27B-class GGUF file of LAYERS trunk layers")
+    ap.add_argument("--replay", type=int, default=1, help="0: every round launches its kernels (no graph replay)")
     ap.add_argument("--calibrate-copy", type=int, default=0,
                     help="first copy 1 GiB on the device 3 times (a known-size kernel for HBM counters)")
     return ap.parse_args()
@@ -599,6 +600,7 @@ def main():
           file=sys.stderr, flush=True)
     chunk = max(64, min(args.prefill_chunk, 4096))
     sess = Session(model, args.n_ctx, max_batch=chunk)
+    sess.set_replay(bool(args.replay))
     g = torch.Generator().manual_seed(args.seed + 1)
     prompt = torch.randint(0, hp["n_vocab"], (args.prompt,), generator=g).tolist()
     # the prefill's GEMMs over one chunk, each launch timed, then rewound
@@ -749,6 +751,7 @@ def main():
             "tree_commit_4_device_us_median": round(tc[len(tc) // 2] * 1e3, 1),
             "acceptance": round((loop.accepted - acc0) / max(1, loop.proposed - prop0), 4),
             "tokens_per_round": round(committed / args.steps, 3),
+            "replay": {"on": bool(args.replay), "captured": sess.replay_stats[0], "replayed": sess.replay_stats[1]},
             "kernel_classes": {k: {"launches_per_round": v[0] / args.profile_rounds,
                                    "GB_per_launch": round(v[2] / v[0] / 1e9, 5),
                                    "us_per_launch_replayed": round(replay[k][0] * 1e3, 2),

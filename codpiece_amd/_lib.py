@@ -120,6 +120,8 @@ SIGNATURES = {
     "cpv_session_set_pos": (_INT, [_P, _I64, _I64]),
     "cpv_session_get_pos": (_INT, [_P, ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
     "cpv_session_set_attn_tap": (_INT, [_P, _P, _I64]),
+    "cpv_session_set_replay": (_INT, [_P, _INT]),
+    "cpv_session_replay_stats": (_INT, [_P, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]),
     "cpv_prefill": (_INT, [_P, _P, _INT]),
     "cpv_verify_step": (_INT, [_P, _P, _INT, _INT, _P, ctypes.POINTER(RoundOut)]),
     "cpv_verify_step_cands": (_INT, [_P, _P, _INT, _INT, _P, ctypes.POINTER(ctypes.c_int32), _INT,

@@ -97,6 +97,7 @@ extern "C" void cpv_free(cpv_ctx* ctx)
     if (ctx->red) (void)hipFree(ctx->red);
     for (hipEvent_t e : ctx->prof_ev) (void)hipEventDestroy(e);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+    if (ctx->cap_stream) (void)hipStreamDestroy(ctx->cap_stream);
     delete ctx;
 }
 
@@ -772,6 +773,7 @@ cpv_status cpv_argmax_peak_rows(cpv_ctx* ctx, const float* x, const float* noise
         const size_t bs = need > ((size_t)1 << 20) ? need : ((size_t)1 << 20);
         CPV_HIP(ctx, hipMalloc(&ctx->red, bs));
         ctx->red_bytes = bs;
+        ctx->ws_gen++;
     }
     unsigned long long* part = (unsigned long long*)ctx->red;
     double* psum = (double*)(part + rows * AM_NB);

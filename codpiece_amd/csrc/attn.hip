@@ -90,6 +90,9 @@ struct ChunkArgs {
     int64_t n_past, n, v_stride;   // n = n_past + T rows in play
     int T, H, Hkv;
     float scale;
+    const int64_t* pos;       // when set, n_past is pos[pos_sel] (device memory, read at run
+    int pos_sel;              // time) and the grid may hold chunks past the end, which exit
+    int64_t kv_rows;          // rows the K cache holds (loads stay below it; v_stride for V)
 };
 
 // pack 16 limbs of one kind into 4 dwords and store them as one 16-byte LDS write
@@ -149,9 +152,8 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     // KV head fastest: the last blocks dispatched are the heads' last chunk,
     // the only one that can be short, and a short chunk costs little below
     const int c = blockIdx.x / a.Hkv, kh = blockIdx.x % a.Hkv;
-    const int G = a.H / a.Hkv, LR = G * a.T;
     const int64_t j0 = (int64_t)c * CHUNK;
-    const int nj = (int)(a.n - j0 < CHUNK ? a.n - j0 : CHUNK);
+    const int G = a.H / a.Hkv, LR = G * a.T;
     const int sub = tid % TPR;
     const bool tree = a.parent != nullptr;
 
@@ -168,14 +170,18 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
 #pragma unroll
         for (int i = 0; i < 4; i++) qv[i] = ((const float4*)src)[i];
     }
+    // (rows clamped to the cache's: the chunk's end is known once n_past is)
     uint4 kv[KP][2];
 #pragma unroll
     for (int p = 0; p < KP; p++) {
-        const int r = rq + p * RPP, rc = r < nj ? r : nj - 1;
-        const uint16_t* src = a.kc + (j0 + rc) * (int64_t)a.Hkv * D + (int64_t)kh * D + sub * 16;
+        const int64_t row = j0 + rq + p * RPP, rc = row < a.kv_rows ? row : a.kv_rows - 1;
+        const uint16_t* src = a.kc + rc * (int64_t)a.Hkv * D + (int64_t)kh * D + sub * 16;
         kv[p][0] = *(const uint4*)src;
         kv[p][1] = *(const uint4*)(src + 8);
     }
+    const int64_t n_past = a.pos ? a.pos[a.pos_sel] : a.n_past, n_all = n_past + a.T;
+    if (j0 >= n_all) return;                   // a chunk past the end (the whole workgroup, before any barrier)
+    const int nj = (int)(n_all - j0 < CHUNK ? n_all - j0 : CHUNK);
     // ---- query rows lr = blockIdx.z * 32 + r: token t = lr / G, head kh * G + lr % G
     if (rq < QB) {
         float v[16];
@@ -250,7 +256,7 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
             const int r = qb * 16 + 4 * (lane >> 4) + i;
             const int lr = blockIdx.z * QB + r;
             float w = -INFINITY;
-            if (lr < LR && bc < nj && visible(j0 + bc, a.n_past, lr / G, tree, s_anc[r])) {
+            if (lr < LR && bc < nj && visible(j0 + bc, n_past, lr / G, tree, s_anc[r])) {
                 const int eq = s_eq[r];
                 float sc = 0.0f;
                 if (eq != E_EMPTY && ek != E_EMPTY) {
@@ -416,14 +422,20 @@ __global__ __launch_bounds__(D) void attn_fold_kernel(const float* __restrict__ 
 // one call over T query tokens (the scratch holds T*H rows per chunk); with
 // out null only the chunk partials are produced (into *part), for a consumer
 // that folds them itself
+// With pos set (partials only), the grid and the scratch are sized for
+// nchunk_grid chunks, at least the call's, and n_past is read on the device.
 template <int D>
 cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                       int64_t n_past, const int32_t* parent, int T, int H, int Hkv, float scale, float* out,
-                      cpv_attn_part* part = nullptr)
+                      cpv_attn_part* part = nullptr, const int64_t* pos = nullptr, int pos_sel = 0,
+                      int nchunk_grid = 0, int64_t kv_rows = 0)
 {
     const int64_t n = n_past + T;
     const int G = H / Hkv, LR = G * T, rows = T * H;
-    const int nchunk = (int)((n + CHUNK - 1) / CHUNK);
+    int nchunk = (int)((n + CHUNK - 1) / CHUNK);
+    if (pos && (out || kv_rows < n))
+        return cpv_fail(ctx, CPV_EINVAL, "attention: device positions are for partials over a cache of >= n rows");
+    if (pos && nchunk_grid > nchunk) nchunk = nchunk_grid;
     const size_t P_b = ((size_t)nchunk * rows * D * 4 + 255) & ~(size_t)255;
     const size_t m_b = ((size_t)nchunk * rows * 4 + 255) & ~(size_t)255;
     const size_t z_b = (size_t)nchunk * rows * 8;
@@ -445,6 +457,9 @@ cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const ui
     ca.H = H;
     ca.Hkv = Hkv;
     ca.scale = scale;
+    ca.pos = pos;
+    ca.pos_sel = pos_sel;
+    ca.kv_rows = pos ? kv_rows : n;
     attn_chunk_kernel<D><<<dim3((unsigned)(nchunk * Hkv), 1u, (unsigned)((LR + QB - 1) / QB)), CT, 0,
                            ctx->stream>>>(ca);
     if (out)
@@ -458,6 +473,9 @@ cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const ui
         part->nchunk = nchunk;
         part->rows = rows;
         part->zbits = ZBITS;
+        part->pos = pos;
+        part->pos_sel = pos_sel;
+        part->t = T;
     }
     return CPV_OK;
 }
@@ -514,14 +532,17 @@ cpv_status cpv_attn_launch(cpv_ctx* ctx, const float* q, const uint16_t* kc, con
 
 cpv_status cpv_attn_partials(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                              int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
-                             cpv_attn_part* part)
+                             cpv_attn_part* part, const int64_t* pos, int pos_sel, int nchunk_grid, int64_t kv_rows)
 {
+    const int64_t grid_past = pos && (int64_t)nchunk_grid * CHUNK - t > n_past ? (int64_t)nchunk_grid * CHUNK - t : n_past;
     if ((d != 64 && d != 128) || (parent && t > 64) ||
-        !(d == 128 ? attn_one_block<128>(n_past, t, h) : attn_one_block<64>(n_past, t, h)))
+        !(d == 128 ? attn_one_block<128>(grid_past, t, h) : attn_one_block<64>(grid_past, t, h)))
         return CPV_EUNSUPPORTED;   // (no message: the caller takes the unfused path)
     auto go = [=]() {
-        return d == 128 ? attn_block<128>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, nullptr, part)
-                        : attn_block<64>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, nullptr, part);
+        return d == 128 ? attn_block<128>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, nullptr, part,
+                                          pos, pos_sel, nchunk_grid, kv_rows)
+                        : attn_block<64>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, nullptr, part,
+                                         pos, pos_sel, nchunk_grid, kv_rows);
     };
     const int ev = cpv_prof_mark(ctx);
     const cpv_status st = go();

@@ -15,6 +15,7 @@ struct cpv_ctx {
     size_t lds_max = 0;       // shared memory per workgroup (bytes)
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
+    hipStream_t cap_stream = nullptr;   // graph captures (the caller's stream may be the null stream)
     std::string err;
     // scratch owned by the context, grown on demand (never inside a capture)
     void* ws = nullptr;
@@ -353,6 +354,8 @@ struct cpv_attn_part {
     const long long* zc;
     int nchunk, rows;
     int zbits;            // zc holds Z_c 2^zbits
+    const int64_t* pos;   // when set, the chunks in play are ceil((pos[pos_sel] + t) / 128)
+    int pos_sel, t;       // (device memory; nchunk is then the grid's, an upper bound)
 };
 // o = fmaf(p[c * cs], f[c], o) for c = 0 .. n-1 in order from +0 (the
 // attention's fold over its chunk partials, n >= 1): each batch of loads goes
@@ -385,4 +388,5 @@ __device__ __forceinline__ float cpv_fold_chain(const float* p, int64_t cs, cons
 }
 cpv_status cpv_attn_partials(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                              int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
-                             cpv_attn_part* part);
+                             cpv_attn_part* part, const int64_t* pos = nullptr, int pos_sel = 0,
+                             int nchunk_grid = 0, int64_t kv_rows = 0);

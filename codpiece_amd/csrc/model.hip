@@ -19,6 +19,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <array>
 #include <map>
 #include <string>
 #include <vector>
@@ -128,10 +129,16 @@ struct PrepArgs {
     const int32_t* pos_off;   // [T] position of token t = rope_pos0 + pos_off[t] (a tree's depths), or null: + t
     int H, Hkv, hd, n_rot, write;
     float eps;
+    const int64_t* pos;       // when set (device memory, read at run time): rope_pos0 = pos[0] + rope_off,
+    int pos_kv, rope_off;     // kv_row0 = pos[pos_kv]
 };
+
+__device__ __forceinline__ int64_t prep_rope0(const PrepArgs& a) { return a.pos ? a.pos[0] + a.rope_off : a.rope_pos0; }
+__device__ __forceinline__ int64_t prep_kv0(const PrepArgs& a) { return a.pos ? a.pos[a.pos_kv] : a.kv_row0; }
 
 __global__ __launch_bounds__(128) void qk_prep_kernel(PrepArgs a)
 {
+    const int64_t rope0 = prep_rope0(a), kv0 = prep_kv0(a);   // (read first: off the critical path)
     const int t = blockIdx.x, hh = blockIdx.y, i = threadIdx.x;
     const bool is_q = hh < a.H;
     const int kh = hh - a.H;
@@ -170,7 +177,7 @@ __global__ __launch_bounds__(128) void qk_prep_kernel(PrepArgs a)
     const int half = a.n_rot / 2;
     if (i < a.n_rot) {
         const int p = i < half ? i : i - half;
-        const float* cs = a.rope + (a.rope_pos0 + (a.pos_off ? a.pos_off[t] : t)) * a.n_rot + 2 * p;
+        const float* cs = a.rope + (rope0 + (a.pos_off ? a.pos_off[t] : t)) * a.n_rot + 2 * p;
         const float c = cs[0], s = cs[1];
         const float x0 = s_v[p], x1 = s_v[p + half];
         if (i < half) {
@@ -184,7 +191,7 @@ __global__ __launch_bounds__(128) void qk_prep_kernel(PrepArgs a)
     if (is_q) {
         a.qout[((int64_t)t * a.H + hh) * a.hd + i] = out;
     } else if (a.write) {
-        const int64_t row = a.kv_row0 + t;
+        const int64_t row = kv0 + t;
         a.k_cache[row * a.Hkv * a.hd + (int64_t)kh * a.hd + i] = cpv_f2h(out);
         const float vv = a.vv[(int64_t)t * a.ks + (int64_t)kh * a.hd + i];
         a.v_cache_t[((int64_t)kh * a.hd + i) * a.v_stride + row] = cpv_f2h(vv);
@@ -490,17 +497,20 @@ __global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
         __shared__ float s_f[4][FOLD_MAX];
         __shared__ double s_z[4][FOLD_MAX];
         __shared__ float s_m[4][2], s_inv[4];
-        const int hd = a.hd, nch = a.part.nchunk, rows = a.part.rows, H = n / hd;
+        const int hd = a.hd, rows = a.part.rows, H = n / hd;
+        const int nchg = a.part.nchunk;                       // the grid's chunks: an upper bound
         const int lh = t / hd, tl = t - lh * hd;             // head within the unit, thread within the head
         const int h = ec / hd, rr = m * H + h;                // (clamped: a thread past n reads a valid head)
         const int wph = hd / 64;                              // waves per head
+        // every grid chunk's max and sum are read while the count of chunks in
+        // play comes from device memory; those past it are never used
         float M = -INFINITY;
-        for (int c = tl; c < nch; c += hd) {
-            const float mc = a.part.mc[(int64_t)c * rows + rr];
-            s_f[lh][c] = mc;
+        for (int c = tl; c < nchg; c += hd) {
+            s_f[lh][c] = a.part.mc[(int64_t)c * rows + rr];
             s_z[lh][c] = ldexp((double)a.part.zc[(int64_t)c * rows + rr], -a.part.zbits);
-            M = fmaxf(M, mc);
         }
+        const int nch = a.part.pos ? (int)((a.part.pos[a.part.pos_sel] + a.part.t + 127) / 128) : nchg;
+        for (int c = tl; c < nch; c += hd) M = fmaxf(M, s_f[lh][c]);
         M = cpv_wave_reduce(M, cpv_op_max());
         if (lane == 0) s_m[lh][wave - lh * wph] = M;
         __syncthreads();
@@ -603,6 +613,7 @@ struct PrepKeptArgs {
 __global__ __launch_bounds__(128) void qk_prep_kept_kernel(PrepKeptArgs ka)
 {
     const PrepArgs& a = ka.p;
+    const int64_t rope0 = prep_rope0(a), kv0 = prep_kv0(a);   // (read first: off the critical path)
     const int t = blockIdx.x, hh = blockIdx.y, i = threadIdx.x;
     const bool is_q = hh < a.H;
     const int kh = hh - a.H;
@@ -657,7 +668,7 @@ __global__ __launch_bounds__(128) void qk_prep_kept_kernel(PrepKeptArgs ka)
     const int half = a.n_rot / 2;
     if (i < a.n_rot) {
         const int p = i < half ? i : i - half;
-        const float* cs = a.rope + (a.rope_pos0 + (a.pos_off ? a.pos_off[t] : t)) * a.n_rot + 2 * p;
+        const float* cs = a.rope + (rope0 + (a.pos_off ? a.pos_off[t] : t)) * a.n_rot + 2 * p;
         const float c = cs[0], sn = cs[1];
         const float x0 = s_v[p], x1 = s_v[p + half];
         if (i < half) {
@@ -671,7 +682,7 @@ __global__ __launch_bounds__(128) void qk_prep_kept_kernel(PrepKeptArgs ka)
     if (is_q) {
         a.qout[((int64_t)t * a.H + hh) * a.hd + i] = out;
     } else if (a.write) {
-        const int64_t row = a.kv_row0 + t;
+        const int64_t row = kv0 + t;
         a.k_cache[row * a.Hkv * a.hd + (int64_t)kh * a.hd + i] = cpv_f2h(out);
         a.v_cache_t[((int64_t)kh * a.hd + i) * a.v_stride + row] = cpv_f2h(vv);
     }
@@ -731,6 +742,23 @@ struct cpv_session {
     cpv_weight* cand_head = nullptr;      // the draft head's rows cand_host
     int32_t* cand_idx = nullptr;          // [max_batch] a link's argmax within the shortlist
     std::vector<void*> allocs;
+    // round replay: the n_past and mtp_past of the call in flight in device
+    // memory (the kernels that place rows read them there), and the rounds
+    // captured as graphs, by shape (t, depth and the attention grids' chunk
+    // counts), valid while the context's workspaces stay where they were
+    int64_t* pos_dev = nullptr;           // [2]
+    bool eager_only = false;              // set by a launch of the round that takes host positions
+    bool replay = true;
+    struct RoundGraph {
+        int key[4];
+        uint64_t ws_gen, used;
+        hipGraphExec_t exec;
+    };
+    std::vector<RoundGraph> graphs;
+    std::vector<std::array<int, 4>> warm;  // shapes run eagerly since the workspaces last moved
+    uint64_t warm_gen = 0, clock = 0;
+    int64_t n_captured = 0, n_replayed = 0;
+    std::vector<std::array<int, 4>> unreplayable;
 };
 
 static cpv_status dev_alloc(cpv_ctx* ctx, std::vector<void*>& list, size_t bytes, void** out)
@@ -913,6 +941,7 @@ extern "C" void cpv_session_free(cpv_session* s)
 {
     if (!s) return;
     (void)hipStreamSynchronize(s->model->ctx->stream);
+    for (auto& g : s->graphs) (void)hipGraphExecDestroy(g.exec);
     for (void* p : s->allocs) (void)hipFree(p);
     if (s->cand_dev) (void)hipFree(s->cand_dev);
     if (s->cand_head) cpv_weight_free(s->cand_head);
@@ -978,6 +1007,7 @@ extern "C" cpv_status cpv_session_create(cpv_model* m, int64_t n_ctx, int32_t ma
     A((size_t)16 * T * 4, (void**)&s->chain);
     A((size_t)16 * T * 4, (void**)&s->conf);
     A((size_t)2 * CPV_TREE_MAX * 4, (void**)&s->tree_dev);
+    A(2 * sizeof(int64_t), (void**)&s->pos_dev);
     A((size_t)T * 4, (void**)&s->cand_idx);
     A((size_t)2 * hp.n_layer * sizeof(uint16_t*), (void**)&s->caches_dev);
     if (st == CPV_OK) {
@@ -1055,6 +1085,21 @@ extern "C" cpv_status cpv_session_set_attn_tap(cpv_session* s, float* tap_dev, i
     return CPV_OK;
 }
 
+extern "C" cpv_status cpv_session_set_replay(cpv_session* s, int on)
+{
+    if (!s) return CPV_EINVAL;
+    s->replay = on != 0;
+    return CPV_OK;
+}
+
+extern "C" cpv_status cpv_session_replay_stats(const cpv_session* s, int64_t* captured, int64_t* replayed)
+{
+    if (!s || !captured || !replayed) return CPV_EINVAL;
+    *captured = s->n_captured;
+    *replayed = s->n_replayed;
+    return CPV_OK;
+}
+
 extern "C" cpv_status cpv_session_get_pos(const cpv_session* s, int64_t* n_past, int64_t* mtp_past)
 {
     if (!s) return CPV_EINVAL;
@@ -1129,9 +1174,33 @@ struct Tree {
     const int32_t* depth;
 };
 
+// the session's positions into its device copy, for the call's kernels
+__global__ void set_pos_kernel(int64_t* __restrict__ pos, int64_t n_past, int64_t mtp_past)
+{
+    if (threadIdx.x == 0) {
+        pos[0] = n_past;
+        pos[1] = mtp_past;
+    }
+}
+
+cpv_status set_pos_dev(cpv_session* s)
+{
+    cpv_ctx* ctx = s->model->ctx;
+    set_pos_kernel<<<1, 64, 0, ctx->stream>>>(s->pos_dev, s->n_past, s->mtp_past);
+    CPV_HIP(ctx, hipGetLastError());
+    return CPV_OK;
+}
+
+// the device position a block reads: KV rows from pos[kv] (0: n_past, 1:
+// mtp_past), rope positions pos[0] + rope_off (the host values rope_pos0,
+// kv_row0 and attn_past of the same call size the grids)
+struct PosSel {
+    int kv, rope_off;
+};
+
 cpv_status block_unfused(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_pos0, int64_t kv_row0,
                  int64_t attn_past, uint16_t* kc, uint16_t* vt, int64_t v_stride, bool write,
-                 const Tree* tree = nullptr)
+                 const Tree* tree, PosSel ps)
 {
     const int32_t* parent = tree ? tree->parent : nullptr;
     cpv_model* m = s->model;
@@ -1180,6 +1249,10 @@ cpv_status block_unfused(cpv_session* s, const LayerW& L, float* x, int T, int64
     pa.n_rot = hp.n_rot;
     pa.write = write ? 1 : 0;
     pa.eps = hp.rms_eps;
+    pa.pos = s->pos_dev;
+    pa.pos_kv = ps.kv;
+    pa.rope_off = ps.rope_off;
+    s->eager_only = true;   // (the attention below takes host positions)
     qk_prep_kernel<<<dim3((unsigned)T, (unsigned)(H + Hkv)), (unsigned)hd, 0, ctx->stream>>>(pa);
     CPV_HIP(ctx, hipGetLastError());
     const float kq_scale = 1.0f / sqrtf((float)hd);
@@ -1236,7 +1309,7 @@ bool fusable(const cpv_model* m, const LayerW& L)
 // wo GEMM, residual+norm+quant, gate|up GEMM, SwiGLU+quant, down GEMM.
 cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_pos0, int64_t kv_row0,
                  int64_t attn_past, uint16_t* kc, uint16_t* vt, int64_t v_stride, bool write, const cpv_gout* pend,
-                 int pend_src, cpv_gout* out, const Tree* tree = nullptr)
+                 int pend_src, cpv_gout* out, PosSel ps, const Tree* tree = nullptr)
 {
     const int32_t* parent = tree ? tree->parent : nullptr;
     cpv_model* m = s->model;
@@ -1247,7 +1320,7 @@ cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_
     out->acc = nullptr;
     if (!fusable(m, L)) {
         if (pend && (st = apply_kept(s, x, T, *pend, pend_src))) return st;
-        return block_unfused(s, L, x, T, rope_pos0, kv_row0, attn_past, kc, vt, v_stride, write, tree);
+        return block_unfused(s, L, x, T, rope_pos0, kv_row0, attn_past, kc, vt, v_stride, write, tree, ps);
     }
     // attention norm (after the pending residual term) and the q|k|v input
     RowArgs r{};
@@ -1285,6 +1358,9 @@ cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_
     pa.n_rot = hp.n_rot;
     pa.write = write ? 1 : 0;
     pa.eps = hp.rms_eps;
+    pa.pos = s->pos_dev;
+    pa.pos_kv = ps.kv;
+    pa.rope_off = ps.rope_off;
     pk.g = g;
     pk.gate_out = s->qg;
     qk_prep_kept_kernel<<<dim3((unsigned)T, (unsigned)(H + Hkv)), (unsigned)hd, 0, ctx->stream>>>(pk);
@@ -1298,15 +1374,19 @@ cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_
     r2.n = (int)(H * hd);
     r2.quant = 1;
     cpv_attn_part part{};
-    const int64_t nch = (attn_past + T + 127) / 128;         // the attention's 128-row chunks
-    const bool fold = !s->tap && hd % 64 == 0 && 256 % hd == 0 && nch <= FOLD_MAX &&
+    // the attention's 128-row chunks, and the grid's: a multiple of 8, so that
+    // one grid serves every position of a 1024-row range (a replayed round)
+    const int64_t nch = (attn_past + T + 127) / 128, nch_grid = (nch + 7) / 8 * 8;
+    const bool fold = !s->tap && hd % 64 == 0 && 256 % hd == 0 && nch_grid <= FOLD_MAX &&
                       cpv_attn_partials(ctx, s->q, kc, vt, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd, kq_scale,
-                                        &part) == CPV_OK;
+                                        &part, s->pos_dev, ps.kv, (int)nch_grid,
+                                        ps.kv == 0 ? s->n_ctx : s->mtp_ctx) == CPV_OK;
     if (fold) {
         r2.src = SRC_GATE_FOLD;
         r2.part = part;
         r2.hd = (int)hd;
     } else {
+        s->eager_only = true;   // (host positions)
         if ((st = cpv_attn_launch(ctx, s->q, kc, vt, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd,
                                   kq_scale, s->att)))
             return st;
@@ -1397,12 +1477,13 @@ extern "C" cpv_status cpv_prefill(cpv_session* s, const int32_t* tokens_dev, int
     cpv_status st;
     s->tap_off = 0;
     s->tree_base = -1;
+    if ((st = set_pos_dev(s)) != CPV_OK) return st;
     CPV_HIP(ctx, hipMemcpyAsync(s->tok, tokens_dev, (size_t)t * 4, hipMemcpyDeviceToDevice, ctx->stream));
     if ((st = cpv_get_rows(ctx, m->tok_embd, s->tok, t, s->x))) return st;
     cpv_gout pend{}, nxt{};
     for (int il = 0; il < m->hp.n_layer; il++) {
         if ((st = block(s, m->layers[il], s->x, t, s->n_past, s->n_past, s->n_past, s->kc[il], s->vt[il], s->v_stride,
-                        true, pend.acc ? &pend : nullptr, SRC_ADD, &nxt)))
+                        true, pend.acc ? &pend : nullptr, SRC_ADD, &nxt, PosSel{0, 0})))
             return st;
         pend = nxt;
     }
@@ -1460,6 +1541,149 @@ extern "C" cpv_status cpv_verify_step(cpv_session* s, const int32_t* tokens_dev,
     return cpv_verify_step_cands(s, tokens_dev, t, depth, noise_dev, nullptr, 0, out);
 }
 
+namespace {
+
+// the round's launches after its tokens are in s->tok and its positions in
+// s->pos_dev: the trunk, the LM head and its argmax, the MTP chain
+cpv_status round_body(cpv_session* s, int t, int depth, const float* noise_dev, bool shortlist, int n_cand)
+{
+    cpv_model* m = s->model;
+    cpv_ctx* ctx = m->ctx;
+    const cpv_hparams& hp = m->hp;
+    const int64_t E = hp.n_embd, V = hp.n_vocab;
+    cpv_status st;
+    if ((st = cpv_get_rows(ctx, m->tok_embd, s->tok, t, s->x))) return st;
+    cpv_gout pend{}, nxt{};
+    for (int il = 0; il < hp.n_layer; il++) {
+        if ((st = block(s, m->layers[il], s->x, t, s->n_past, s->n_past, s->n_past, s->kc[il], s->vt[il], s->v_stride,
+                        true, pend.acc ? &pend : nullptr, SRC_ADD, &nxt, PosSel{0, 0})))
+            return st;
+        pend = nxt;
+    }
+    // LM head and in-graph argmax (qwen35.rs:2788-2821)
+    if ((st = norm_head(s, s->x, t, pend.acc ? &pend : nullptr, m->output_norm, s->h, m->output, s->logits)))
+        return st;
+    if ((st = cpv_argmax_rows(ctx, s->logits, noise_dev, t, V, s->preds))) return st;
+    // fused MTP draft chain (qwen35.rs:2840-2962)
+    if (depth > 0) {
+        const LayerW& ML = m->layers[hp.n_layer];
+        const float* h_src = s->h;
+        const int32_t* tok_src = s->preds;
+        for (int step = 0; step < depth; step++) {
+            if ((st = cpv_get_rows(ctx, m->mtp_embed, tok_src, t, s->e))) return st;
+            if ((st = rmsnorm(ctx, s->e, E, m->enorm, s->cat, 2 * E, t, (int)E, hp.rms_eps))) return st;
+            if ((st = rmsnorm(ctx, h_src, E, m->hnorm, s->cat + E, 2 * E, t, (int)E, hp.rms_eps))) return st;
+            cpv_act act;
+            if ((st = cpv_quant_act(ctx, m->eh_proj->type, s->cat, t, 2 * E, next_act(s), &act))) return st;
+            cpv_gout eh;
+            if ((st = cpv_qgemm_keep(ctx, m->eh_proj, &act, &eh))) return st;
+            // positions rope_base + i + 1, rows mtp_past + i; only link 0 writes (:1858-1866, :2898-2906)
+            if ((st = block(s, ML, s->dsa, t, s->n_past + 1, s->mtp_past, s->mtp_past, s->kc[hp.n_layer],
+                            s->vt[hp.n_layer], s->mtp_v_stride, step == 0, &eh, SRC_SET, &nxt, PosSel{1, 1})))
+                return st;
+            // h_next = rms(d, shared_head_norm or output_norm), then the draft head,
+            // over the shortlist when one is given (qwen35.rs:2925-2931)
+            if ((st = norm_head(s, s->dsa, t, nxt.acc ? &nxt : nullptr, m->mtp_head_norm, s->hn,
+                                shortlist ? s->cand_head : m->mtp_head, s->mtp_logits)))
+                return st;
+            int32_t* ids = s->chain + (size_t)step * t;
+            if ((st = cpv_argmax_peak_rows(ctx, s->mtp_logits, nullptr, t, shortlist ? n_cand : V,
+                                           shortlist ? s->cand_idx : ids, s->conf + (size_t)step * t)))
+                return st;
+            if (shortlist) {
+                // drafts are candidates; the next link embeds the argmax itself, as the
+                // graph does (tok_src = ids, qwen35.rs:2958; the ids map back on the host, :1904-1910)
+                map_cands_kernel<<<(unsigned)((t + 255) / 256), 256, 0, ctx->stream>>>(s->cand_idx, s->cand_dev, t, ids);
+                CPV_HIP(ctx, hipGetLastError());
+            }
+            // the next link feeds on this link's prediction and hidden
+            CPV_HIP(ctx, hipMemcpyAsync(s->hsrc, s->hn, (size_t)t * E * 4, hipMemcpyDeviceToDevice, ctx->stream));
+            h_src = s->hsrc;
+            tok_src = shortlist ? s->cand_idx : ids;
+        }
+    }
+    return CPV_OK;
+}
+
+// the attention grid's chunk count for `rows` cache rows (as block() sizes it)
+int chunk_bucket(int64_t rows) { return (int)(((rows + 127) / 128 + 7) / 8 * 8); }
+
+// A greedy round of shape key replayed from its graph (*done set).  A shape's
+// first round runs eagerly (so that every workspace it uses has its size);
+// its second is captured, instantiated and launched.  A capture that fails,
+// or a round with a launch that takes host positions, leaves the shape to
+// eager rounds.  Graphs hold workspace addresses: a move of any workspace
+// (ws_gen) retires them.
+cpv_status replay_round(cpv_session* s, const std::array<int, 4>& key, bool* done)
+{
+    cpv_ctx* ctx = s->model->ctx;
+    *done = false;
+    if (s->warm_gen != ctx->ws_gen) {
+        s->warm.clear();
+        s->warm_gen = ctx->ws_gen;
+    }
+    auto same = [&](const int* k) { return std::equal(key.begin(), key.end(), k); };
+    for (auto& g : s->graphs)
+        if (same(g.key) && g.ws_gen == ctx->ws_gen) {
+            CPV_HIP(ctx, hipGraphLaunch(g.exec, ctx->stream));
+            g.used = ++s->clock;
+            s->n_replayed++;
+            *done = true;
+            return CPV_OK;
+        }
+    if (std::find(s->unreplayable.begin(), s->unreplayable.end(), key) != s->unreplayable.end()) return CPV_OK;
+    if (std::find(s->warm.begin(), s->warm.end(), key) == s->warm.end()) {
+        s->warm.push_back(key);
+        return CPV_OK;
+    }
+    // captured on a stream of its own (nothing runs while capturing), replayed on the caller's
+    const uint64_t gen0 = ctx->ws_gen;
+    const hipStream_t home = ctx->stream;
+    if ((!ctx->cap_stream && hipStreamCreateWithFlags(&ctx->cap_stream, hipStreamNonBlocking) != hipSuccess) ||
+        hipStreamBeginCapture(ctx->cap_stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+        (void)hipGetLastError();
+        s->unreplayable.push_back(key);
+        return CPV_OK;
+    }
+    ctx->stream = ctx->cap_stream;
+    s->eager_only = false;
+    const cpv_status st = round_body(s, key[0], key[1], nullptr, false, 0);
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(ctx->cap_stream, &graph);
+    ctx->stream = home;
+    hipGraphExec_t exec = nullptr;
+    const bool ok = st == CPV_OK && e == hipSuccess && graph && !s->eager_only && ctx->ws_gen == gen0 &&
+                    hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess;
+    if (graph) (void)hipGraphDestroy(graph);
+    (void)hipGetLastError();
+    if (!ok) {   // (nothing was launched: the round runs eagerly)
+        s->unreplayable.push_back(key);
+        return CPV_OK;
+    }
+    constexpr size_t MAX_GRAPHS = 8;
+    if (s->graphs.size() >= MAX_GRAPHS) {
+        size_t lru = 0;
+        for (size_t i = 1; i < s->graphs.size(); i++)
+            if (s->graphs[i].used < s->graphs[lru].used) lru = i;
+        CPV_HIP(ctx, hipStreamSynchronize(ctx->stream));   // (it may still be running)
+        (void)hipGraphExecDestroy(s->graphs[lru].exec);
+        s->graphs.erase(s->graphs.begin() + (long)lru);
+    }
+    cpv_session::RoundGraph g;
+    std::copy(key.begin(), key.end(), g.key);
+    g.ws_gen = gen0;
+    g.used = ++s->clock;
+    g.exec = exec;
+    s->graphs.push_back(g);
+    CPV_HIP(ctx, hipGraphLaunch(exec, ctx->stream));
+    s->n_captured++;
+    s->n_replayed++;
+    *done = true;
+    return CPV_OK;
+}
+
+}  // namespace
+
 extern "C" cpv_status cpv_verify_step_cands(cpv_session* s, const int32_t* tokens_dev, int t, int depth,
                                             const float* noise_dev, const int32_t* cands_host, int n_cand,
                                             cpv_round_out* out)
@@ -1483,57 +1707,15 @@ extern "C" cpv_status cpv_verify_step_cands(cpv_session* s, const int32_t* token
     cpv_status st;
     s->tap_off = 0;
     s->tree_base = -1;
+    if ((st = set_pos_dev(s)) != CPV_OK) return st;
     CPV_HIP(ctx, hipMemcpyAsync(s->tok, tokens_dev, (size_t)t * 4, hipMemcpyDeviceToDevice, ctx->stream));
-    if ((st = cpv_get_rows(ctx, m->tok_embd, s->tok, t, s->x))) return st;
-    cpv_gout pend{}, nxt{};
-    for (int il = 0; il < hp.n_layer; il++) {
-        if ((st = block(s, m->layers[il], s->x, t, s->n_past, s->n_past, s->n_past, s->kc[il], s->vt[il], s->v_stride,
-                        true, pend.acc ? &pend : nullptr, SRC_ADD, &nxt)))
-            return st;
-        pend = nxt;
+    // greedy rounds without a shortlist, a tap or the profiler replay a graph of their shape
+    bool done = false;
+    if (s->replay && !shortlist && !noise_dev && !s->tap && !ctx->prof) {
+        const std::array<int, 4> key{t, depth, chunk_bucket(s->n_past + t), depth > 0 ? chunk_bucket(s->mtp_past + t) : 0};
+        if ((st = replay_round(s, key, &done)) != CPV_OK) return st;
     }
-    // LM head and in-graph argmax (qwen35.rs:2788-2821)
-    if ((st = norm_head(s, s->x, t, pend.acc ? &pend : nullptr, m->output_norm, s->h, m->output, s->logits)))
-        return st;
-    if ((st = cpv_argmax_rows(ctx, s->logits, noise_dev, t, V, s->preds))) return st;
-    // fused MTP draft chain (qwen35.rs:2840-2962)
-    if (depth > 0) {
-        const LayerW& ML = m->layers[hp.n_layer];
-        const float* h_src = s->h;
-        const int32_t* tok_src = s->preds;
-        for (int step = 0; step < depth; step++) {
-            if ((st = cpv_get_rows(ctx, m->mtp_embed, tok_src, t, s->e))) return st;
-            if ((st = rmsnorm(ctx, s->e, E, m->enorm, s->cat, 2 * E, t, (int)E, hp.rms_eps))) return st;
-            if ((st = rmsnorm(ctx, h_src, E, m->hnorm, s->cat + E, 2 * E, t, (int)E, hp.rms_eps))) return st;
-            cpv_act act;
-            if ((st = cpv_quant_act(ctx, m->eh_proj->type, s->cat, t, 2 * E, next_act(s), &act))) return st;
-            cpv_gout eh;
-            if ((st = cpv_qgemm_keep(ctx, m->eh_proj, &act, &eh))) return st;
-            // positions rope_base + i + 1, rows mtp_past + i; only link 0 writes (:1858-1866, :2898-2906)
-            if ((st = block(s, ML, s->dsa, t, s->n_past + 1, s->mtp_past, s->mtp_past, s->kc[hp.n_layer],
-                            s->vt[hp.n_layer], s->mtp_v_stride, step == 0, &eh, SRC_SET, &nxt)))
-                return st;
-            // h_next = rms(d, shared_head_norm or output_norm), then the draft head,
-            // over the shortlist when one is given (qwen35.rs:2925-2931)
-            if ((st = norm_head(s, s->dsa, t, nxt.acc ? &nxt : nullptr, m->mtp_head_norm, s->hn,
-                                shortlist ? s->cand_head : m->mtp_head, s->mtp_logits)))
-                return st;
-            int32_t* ids = s->chain + (size_t)step * t;
-            if ((st = cpv_argmax_peak_rows(ctx, s->mtp_logits, nullptr, t, shortlist ? n_cand : V,
-                                           shortlist ? s->cand_idx : ids, s->conf + (size_t)step * t)))
-                return st;
-            if (shortlist) {
-                // drafts are candidates; the next link embeds the argmax itself, as the
-                // graph does (tok_src = ids, qwen35.rs:2958; the ids map back on the host, :1904-1910)
-                map_cands_kernel<<<(unsigned)((t + 255) / 256), 256, 0, ctx->stream>>>(s->cand_idx, s->cand_dev, t, ids);
-                CPV_HIP(ctx, hipGetLastError());
-            }
-            // the next link feeds on this link's prediction and hidden
-            CPV_HIP(ctx, hipMemcpyAsync(s->hsrc, s->hn, (size_t)t * E * 4, hipMemcpyDeviceToDevice, ctx->stream));
-            h_src = s->hsrc;
-            tok_src = shortlist ? s->cand_idx : ids;
-        }
-    }
+    if (!done && (st = round_body(s, t, depth, noise_dev, shortlist, n_cand)) != CPV_OK) return st;
     s->n_past += t;
     out->n_past = s->n_past;
     out->preds_dev = s->preds;
@@ -1636,12 +1818,13 @@ extern "C" cpv_status cpv_verify_tree(cpv_session* s, const int32_t* tokens_dev,
     tree_setup_kernel<<<1, CPV_TREE_MAX, 0, ctx->stream>>>(ts, s->tree_dev);
     CPV_HIP(ctx, hipGetLastError());
     const Tree tree{s->tree_dev, s->tree_dev + CPV_TREE_MAX};
+    if ((st = set_pos_dev(s)) != CPV_OK) return st;
     CPV_HIP(ctx, hipMemcpyAsync(s->tok, tokens_dev, (size_t)t * 4, hipMemcpyDeviceToDevice, ctx->stream));
     if ((st = cpv_get_rows(ctx, m->tok_embd, s->tok, t, s->x))) return st;
     cpv_gout pend{}, nxt{};
     for (int il = 0; il < hp.n_layer; il++) {
         if ((st = block(s, m->layers[il], s->x, t, s->n_past, s->n_past, s->n_past, s->kc[il], s->vt[il], s->v_stride,
-                        true, pend.acc ? &pend : nullptr, SRC_ADD, &nxt, &tree)))
+                        true, pend.acc ? &pend : nullptr, SRC_ADD, &nxt, PosSel{0, 0}, &tree)))
             return st;
         pend = nxt;
     }

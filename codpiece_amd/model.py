@@ -105,6 +105,17 @@ class Session:
             self.ctx._check(self.ctx.lib.cpv_session_set_attn_tap(self.h, ctypes.c_void_p(tap.data_ptr()),
                                                                   tap.numel()))
 
+    def set_replay(self, on):
+        """Replay greedy rounds from per-shape HIP graphs (on by default)."""
+        self.ctx._check(self.ctx.lib.cpv_session_set_replay(self.h, 1 if on else 0))
+
+    @property
+    def replay_stats(self):
+        """(rounds captured as graphs, rounds replayed) since the session was made."""
+        c, r = ctypes.c_int64(), ctypes.c_int64()
+        self.ctx._check(self.ctx.lib.cpv_session_replay_stats(self.h, ctypes.byref(c), ctypes.byref(r)))
+        return c.value, r.value
+
     @property
     def n_past(self):
         return self.pos[0]

@@ -264,6 +264,18 @@ cpv_status  cpv_session_get_pos(const cpv_session* s, int64_t* n_past, int64_t* 
  * at offset 0 with each call; blocks past capacity_floats are dropped.
  * NULL clears it. */
 cpv_status  cpv_session_set_attn_tap(cpv_session* s, float* tap_dev, int64_t capacity_floats);
+/* Round replay, the counterpart of the reference's per-shape graph reuse
+ * (qwen35.rs:1740-1748: one built graph kept per shape; the graph uid of
+ * patches/ggml-codpiece.patch:1-15).  On (the default), a cpv_verify_step
+ * round without noise, shortlist, tap or profiling replays a HIP graph of its
+ * shape -- t, depth and the attention grids' 1024-row position ranges -- which
+ * the session captures on the shape's second round; the round's positions and
+ * tokens are set on the stream before the replay, and the results are the
+ * eager round's bit for bit.  Off, every round launches its kernels. */
+cpv_status  cpv_session_set_replay(cpv_session* s, int on);
+/* No counterpart in the reference: rounds captured as graphs and rounds
+ * replayed (a captured round counts in both) since the session was made. */
+cpv_status  cpv_session_replay_stats(const cpv_session* s, int64_t* captured, int64_t* replayed);
 
 /* Trunk only over t prompt tokens (step_greedy's bulk prefill, main.rs:776-781):
  * writes the KV cache and advances n_past by t. */
