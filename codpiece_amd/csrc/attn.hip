@@ -12,9 +12,11 @@
 //     s = (float)(sum_d qf kf * 2^(Eq+Ek-28)), the sum exact -- here on the
 //     int8 MFMA with two signed 8-bit limbs per operand; w = s * scale.
 //  2. per chunk c of 128 cache rows (absolute rows), over its visible rows:
-//     m_c = max w, e = expf(w - m_c), p = f16(e), P_c = fma chain of p v in
-//     row order, Z_c = sum rint(e 2^54) exactly.
-//  3. M = max m_c, f_c = expf(m_c - M); in chunk order Zt += (Z_c 2^-54) f_c
+//     m_c = max w, e = expf(w - m_c), the weight p = rint(e 2^22) and each
+//     value vq = rint(f16(v) 2^14), both integers; S_c = sum p vq and
+//     Z_c = sum p, exact -- here on the int8 MFMA (3 signed 8-bit limbs of p,
+//     4 of vq); P_c = (float)S_c * 2^-36.
+//  3. M = max m_c, f_c = expf(m_c - M); in chunk order Zt += (Z_c 2^-22) f_c
 //     (binary64) and O = fma(P_c, f_c, O) (f32); out = O * (float)(1 / Zt).
 //
 // Kernels: chunk (grid: chunk x KV head x 32-row query block; scores on the
@@ -22,9 +24,11 @@
 // (one block per query row).  Scratch in the context workspace: P [chunks][T*H][D]
 // f32, m [chunks][T*H] f32, Z [chunks][T*H] int64.
 //
-// Layout.  K is [n_ctx][h_kv * d]; V is the transposed cache [h_kv * d][v_stride]
-// (the reference's non-FA V layout, qwen35.rs:580-586): the KV axis is
-// contiguous, the reduction axis of P V.
+// Layout.  K is [n_ctx][h_kv * d] f16.  V: a session's cache holds vq's limbs,
+// [h_kv * d][v_stride / 16][4][16] (written once per row, read by P V with no
+// conversion); the API's cache (cpv_attn) is the transposed f16 cache
+// [h_kv * d][v_stride] (the reference's non-FA V layout, qwen35.rs:580-586),
+// converted in the kernel.  Either way the KV axis is the reduction axis of P V.
 #include <math.h>
 
 #include "cpv_internal.h"
@@ -34,7 +38,10 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int CHUNK = 128;          // cache rows per chunk (the unit of the contract)
-constexpr int ZBITS = 54;           // 62 - ceil_log2(CHUNK + 1)
+constexpr int PBITS = 22;           // a weight e in (0, 1] as p = rint(e 2^22): PL limbs
+constexpr int PL = 3;
+constexpr int VBITS = CPV_ATTN_VBITS;   // an f16 value v as vq = rint(v 2^14): |vq| < 2^30, VLIMBS limbs
+constexpr int VLIMBS = CPV_ATTN_VLIMBS;
 constexpr int QB = 32;              // query rows per scores workgroup
 constexpr int E_EMPTY = -100000;    // exponent of an all-zero vector
 
@@ -93,7 +100,22 @@ struct ChunkArgs {
     const int64_t* pos;       // when set, n_past is pos[pos_sel] (device memory, read at run
     int pos_sel;              // time) and the grid may hold chunks past the end, which exit
     int64_t kv_rows;          // rows the K cache holds (loads stay below it; v_stride for V)
+    const int8_t* vl;         // the V cache's limbs (VL kernels): [Hkv*D][v_stride / 16][VLIMBS][16]
 };
+
+// an integer as L signed 8-bit limbs, x = sum l_i 256^i with l_i in
+// [-128, 127] below the top limb (which takes the rest)
+template <int L>
+__device__ __forceinline__ void balanced_limbs(int x, int8_t* l)
+{
+#pragma unroll
+    for (int i = 0; i < L - 1; i++) {
+        const int li = ((x + 128) & 255) - 128;
+        l[i] = (int8_t)li;
+        x = (x - li) >> 8;
+    }
+    l[L - 1] = (int8_t)x;
+}
 
 // pack 16 limbs of one kind into 4 dwords and store them as one 16-byte LDS write
 __device__ __forceinline__ void store16(int8_t* dst, const int8_t* v)
@@ -125,22 +147,23 @@ __device__ __forceinline__ int row_limbs(const float* v, int8_t* hi, int8_t* lo)
 // one 128-row chunk of the cache against 32 query rows of one KV head
 constexpr int CT = 512;             // threads of a chunk workgroup (8 waves)
 
-template <int D>
+// VL: V comes from the cache's limb planes (a.vl); else from the f16 cache
+// (a.vt), converted here
+template <int D, bool VL>
 __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
 {
     constexpr int TPR = D / 16;                // threads per row when converting (16 values each)
     constexpr int RPP = CT / TPR;              // rows per pass
-    // rows padded by 16 bytes (limbs, scores) and 4 floats (weights): the
-    // MFMA operand reads, the score writes and the transposed weight writes
-    // then fall on distinct LDS banks.  The weights take the K limbs' place
-    // once the scores are done.
+    // rows padded by 16 bytes (limbs) and 4 floats (scores): the MFMA operand
+    // reads and the score writes then fall on distinct LDS banks.  The
+    // weights' limbs take the K limbs' place once the scores are done.
     __shared__ __align__(16) int8_t s_qh[QB][D + 16], s_ql[QB][D + 16];
     __shared__ __align__(16) int8_t s_kbuf[2][CHUNK][D + 16];
     __shared__ __align__(16) float s_w[QB][CHUNK + 4];     // scores
-    static_assert(sizeof(float) * CHUNK * (QB + 4) <= sizeof(s_kbuf), "weights fit the K limbs' space");
+    static_assert(PL * QB * (CHUNK + 16) <= sizeof(s_kbuf), "the weights' limbs fit the K limbs' space");
     int8_t(*s_kh)[D + 16] = s_kbuf[0];
     int8_t(*s_kl)[D + 16] = s_kbuf[1];
-    float(*s_pt)[QB + 4] = (float(*)[QB + 4]) & s_kbuf[0][0][0];   // the f16-rounded weights (as f32), row-minor
+    int8_t(*s_p)[QB][CHUNK + 16] = (int8_t(*)[QB][CHUNK + 16]) & s_kbuf[0][0][0];   // [PL][query row][cache row]
     __shared__ int s_eq[QB], s_ek[CHUNK];
     __shared__ unsigned long long s_anc[QB];
     __shared__ uint64_t s_etab[32];                     // the expf table
@@ -223,15 +246,38 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
         store16(&s_kl[r][sub * 16], lo);
         if (sub == 0) s_ek[r] = e;
     }
-    // ---- the first V groups of this thread's P_c lane (d, chunk rows 8g..8g+7),
-    // in flight through the scores and the softmax; the loop below keeps four
-    // groups ahead.  Groups past the chunk's end re-read its last group.
-    constexpr int WPR = D / 64;                // waves per 8-row group of P_c
-    const int dv = (wave % WPR) * 64 + lane;
-    const uint16_t* vrow = a.vt + ((int64_t)kh * D + dv) * a.v_stride + j0;
-    const int gl = (nj - 1) >> 3;
-    uint4 vq0 = *(const uint4*)(vrow + 8 * min(0, gl)), vq1 = *(const uint4*)(vrow + 8 * min(1, gl)),
-          vq2 = *(const uint4*)(vrow + 8 * min(2, gl)), vq3 = *(const uint4*)(vrow + 8 * min(3, gl));
+    // ---- this wave's V operands, in flight through the scores and the
+    // softmax: d-block cb (16 columns), the chunk's rows in two 64-row steps;
+    // lane (c16, g4) holds column 16 cb + c16 and rows 64 ks + 16 g4 .. +15,
+    // the B operands of the P V MFMAs, as the VLIMBS signed 8-bit limbs of
+    // vq = rint(v 2^VBITS).  Segments past the cache's end (wholly: v_stride
+    // is a multiple of 16, or of 8 for halves) read its last one; those rows
+    // carry weight 0.
+    constexpr int NCB = D / 16;                 // d-blocks
+    static_assert((CT / 64) % NCB == 0, "waves per d-block");
+    const int cb = wave % NCB, c16 = lane & 15, g4 = lane >> 4;
+    const int dcol = cb * 16 + c16;
+    v4i vb[2][VLIMBS];
+    uint4 vraw[2][2];
+    if constexpr (VL) {
+        // (a segment's limbs lie together: one 64-byte read)
+        const int8_t* vbase = a.vl + ((int64_t)kh * D + dcol) * a.v_stride * VLIMBS;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            const int64_t sj = j0 + ks * 64 + g4 * 16, sjc = sj < a.v_stride ? sj : a.v_stride - 16;
+#pragma unroll
+            for (int l = 0; l < VLIMBS; l++) vb[ks][l] = *(const v4i*)(vbase + sjc * VLIMBS + 16 * l);
+        }
+    } else {
+        const uint16_t* vrow = a.vt + ((int64_t)kh * D + dcol) * a.v_stride;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int64_t sj = j0 + ks * 64 + g4 * 16 + 8 * h, sjc = sj < a.v_stride ? sj : a.v_stride - 8;
+                vraw[ks][h] = *(const uint4*)(vrow + sjc);
+            }
+    }
     __syncthreads();
 
     // ---- scores: 2 x 8 blocks of 16 x 16 (query rows x cache rows), 2 per wave
@@ -270,28 +316,45 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     }
     __syncthreads();
 
-    // ---- the chunk's softmax: SPR threads per query row, EPT cache rows
-    // each (rows part, part + SPR, ...: consecutive lanes, consecutive rows)
+    // ---- the chunk's softmax: SPR threads per query row, 8 cache rows each
+    // (4 part + 64 i + k: 16-byte reads of the scores, one dword per limb
+    // written); the weights in fixed point, p = rint(e 2^PBITS), as PL signed
+    // 8-bit limbs, and Z_c = sum p
     {
-        constexpr int SPR = CT / QB, EPT = CHUNK / SPR;
+        constexpr int SPR = CT / QB;
+        static_assert(CHUNK == 8 * SPR, "8 cache rows per thread");
         const int r = tid / SPR, part = tid % SPR;
         const int lr = blockIdx.z * QB + r;
+        float w[8];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const float4 w4 = *(const float4*)&s_w[r][4 * part + 64 * i];
+            w[4 * i] = w4.x;
+            w[4 * i + 1] = w4.y;
+            w[4 * i + 2] = w4.z;
+            w[4 * i + 3] = w4.w;
+        }
         float m = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < EPT; i++) m = fmaxf(m, s_w[r][part + SPR * i]);
+        for (int i = 0; i < 8; i++) m = fmaxf(m, w[i]);
         m = cpv_group_reduce<SPR>(m, cpv_op_max());
-        long long z = 0;
+        int z = 0;
 #pragma unroll
-        for (int i = 0; i < EPT; i++) {
-            const int jl = part + SPR * i;
-            const float w = s_w[r][jl];
-            float p = 0.0f;
-            if (w != -INFINITY) {
-                const float e = cpv_expf_t(w - m, s_etab);
-                p = cpv_h2f(cpv_f2h(e));
-                z += (long long)rint(ldexp((double)e, ZBITS));
+        for (int i = 0; i < 2; i++) {
+            uint32_t pk[PL] = {};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float wv = w[4 * i + k];
+                int q = 0;
+                if (wv != -INFINITY) q = (int)rintf(ldexpf(cpv_expf_t(wv - m, s_etab), PBITS));
+                z += q;
+                int8_t l[PL];
+                balanced_limbs<PL>(q, l);
+#pragma unroll
+                for (int p = 0; p < PL; p++) pk[p] |= (uint32_t)(uint8_t)l[p] << (8 * k);
             }
-            s_pt[jl][r] = p;
+#pragma unroll
+            for (int p = 0; p < PL; p++) *(uint32_t*)&s_p[p][r][4 * part + 64 * i] = pk[p];
         }
         z = cpv_group_reduce<SPR>(z, cpv_op_add());
         if (part == 0 && lr < LR) {
@@ -301,78 +364,60 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
             a.zc[row] = z;
         }
     }
+    // (the f16 cache's values into limbs meanwhile)
+    if constexpr (!VL) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            uint32_t pk[VLIMBS][4] = {};
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t wd[4] = {vraw[ks][h].x, vraw[ks][h].y, vraw[ks][h].z, vraw[ks][h].w};
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float v = cpv_h2f((uint16_t)(wd[e >> 1] >> (16 * (e & 1))));
+                    int8_t l[VLIMBS];
+                    balanced_limbs<VLIMBS>((int)rintf(ldexpf(v, VBITS)), l);
+                    const int k = 8 * h + e;
+#pragma unroll
+                    for (int p = 0; p < VLIMBS; p++) pk[p][k >> 2] |= (uint32_t)(uint8_t)l[p] << (8 * (k & 3));
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < VLIMBS; p++) vb[ks][p] = v4i{(int)pk[p][0], (int)pk[p][1], (int)pk[p][2], (int)pk[p][3]};
+        }
+    }
     __syncthreads();
 
-    // ---- P_c: RPW query rows x 64 d per wave (lane = d), fma chain over the
-    // chunk's rows in order.  In the last group, rows past the chunk's end have
-    // p = 0 (their score is -inf) and get v = 0, so they add exact zeros and
-    // leave the chain as it is over the chunk's own rows; later groups are
-    // skipped.
-    constexpr int RPW = QB * WPR * 64 / CT;    // query rows per wave
-    static_assert(RPW == 2 || RPW == 4 || RPW == 8, "P_c rows per wave");
-    const int r0 = (wave / WPR) * RPW;
-    if (blockIdx.z * QB + r0 < LR) {
-        float acc[RPW];
+    // ---- P_c on the int8 MFMA: for row block rb (16 query rows) and this
+    // wave's d-block, the limb products p_a v_b go to accumulator a + b
+    // (weight 2^(8 (a + b))); S = sum of them exactly in int64 (|S| < 2^59);
+    // P_c = (float)S * 2^-(PBITS + VBITS).  A lane holds D rows 4 g4 .. +3 of
+    // column c16.
+    for (int rb = wave / NCB; rb < QB / 16; rb += CT / 64 / NCB) {
+        if (blockIdx.z * QB + rb * 16 >= LR) break;   // (wave-uniform) past the query rows
+        v4i acc[PL + VLIMBS - 1];
 #pragma unroll
-        for (int i = 0; i < RPW; i++) acc[i] = 0.0f;
-        // rows 8g..8g+7 with their v in vw
-        auto rows8 = [&](int g, uint4 vq) {
-            uint32_t vw[4] = {vq.x, vq.y, vq.z, vq.w};
+        for (int q = 0; q < PL + VLIMBS - 1; q++) acc[q] = v4i{0, 0, 0, 0};
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int j = 8 * g + 2 * k;
-                vw[k] = j + 1 < nj ? vw[k] : (j < nj ? (vw[k] & 0xffffu) : 0u);
-            }
+        for (int ks = 0; ks < 2; ks++) {
+            v4i pa[PL];
 #pragma unroll
-            for (int jj = 0; jj < 8; jj++) {
-                const int jl = 8 * g + jj;
-                const float v = cpv_h2f((uint16_t)(vw[jj >> 1] >> (16 * (jj & 1))));
-                float pv[RPW];
-                if constexpr (RPW == 2) {
-                    const float2 p0 = *(const float2*)&s_pt[jl][r0];
-                    pv[0] = p0.x;
-                    pv[1] = p0.y;
-                } else {
+            for (int p = 0; p < PL; p++) pa[p] = *(const v4i*)&s_p[p][rb * 16 + c16][ks * 64 + g4 * 16];
 #pragma unroll
-                    for (int i = 0; i < RPW; i += 4) {
-                        const float4 p0 = *(const float4*)&s_pt[jl][r0 + i];
-                        pv[i] = p0.x;
-                        pv[i + 1] = p0.y;
-                        pv[i + 2] = p0.z;
-                        pv[i + 3] = p0.w;
-                    }
-                }
+            for (int p = 0; p < PL; p++)
 #pragma unroll
-                for (int i = 0; i < RPW; i++) acc[i] = fmaf(pv[i], v, acc[i]);
-            }
-        };
-        if (nj == CHUNK) {
-            // a whole chunk: each group's registers then take the group four ahead
-            auto group = [&](int g, uint4& vq) {
-                const uint4 cur = vq;
-                vq = *(const uint4*)(vrow + 8 * min(g + 4, gl));
-                rows8(g, cur);
-            };
-#pragma unroll
-            for (int g = 0; g < CHUNK / 8; g += 4) {
-                group(g, vq0);
-                group(g + 1, vq1);
-                group(g + 2, vq2);
-                group(g + 3, vq3);
-            }
-        } else {
-            // the short last chunk: its groups only
-            for (int g = 0; g <= gl; g++) rows8(g, *(const uint4*)(vrow + 8 * g));
+                for (int l = 0; l < VLIMBS; l++)
+                    acc[p + l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa[p], vb[ks][l], acc[p + l], 0, 0, 0);
         }
-        // finish every chain here (otherwise they are sunk into the stores below)
 #pragma unroll
-        for (int i = 0; i < RPW; i++) asm volatile("" : "+v"(acc[i]));
-#pragma unroll
-        for (int i = 0; i < RPW; i++) {
-            const int lr = blockIdx.z * QB + r0 + i;
+        for (int i = 0; i < 4; i++) {
+            const int lr = blockIdx.z * QB + rb * 16 + 4 * g4 + i;
             if (lr >= LR) break;
+            int64_t S = 0;
+#pragma unroll
+            for (int q = 0; q < PL + VLIMBS - 1; q++) S += (int64_t)acc[q][i] * ((int64_t)1 << (8 * q));
             const int t = lr / G, h = kh * G + lr % G;
-            a.P[(((int64_t)c * a.T + t) * a.H + h) * D + dv] = acc[i];
+            a.P[(((int64_t)c * a.T + t) * a.H + h) * D + dcol] = ldexpf((float)S, -(PBITS + VBITS));
         }
     }
 }
@@ -385,7 +430,7 @@ __global__ __launch_bounds__(D) void attn_fold_kernel(const float* __restrict__ 
                                                       const long long* __restrict__ zc, int nchunk, int rows,
                                                       float* __restrict__ out)
 {
-    extern __shared__ double s_dyn[];          // [nchunk] Z_c 2^-ZBITS, then [nchunk] factors f_c
+    extern __shared__ double s_dyn[];          // [nchunk] Z_c 2^-PBITS, then [nchunk] factors f_c
     double* s_z = s_dyn;
     float* s_f = (float*)(s_dyn + nchunk);
     __shared__ float s_red[D / 64];
@@ -395,7 +440,7 @@ __global__ __launch_bounds__(D) void attn_fold_kernel(const float* __restrict__ 
     for (int c = d; c < nchunk; c += D) {
         const float m = mc[(int64_t)c * rows + row];
         s_f[c] = m;
-        s_z[c] = ldexp((double)zc[(int64_t)c * rows + row], -ZBITS);
+        s_z[c] = ldexp((double)zc[(int64_t)c * rows + row], -PBITS);
         M = fmaxf(M, m);
     }
     M = cpv_wave_reduce(M, cpv_op_max());
@@ -428,7 +473,7 @@ template <int D>
 cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                       int64_t n_past, const int32_t* parent, int T, int H, int Hkv, float scale, float* out,
                       cpv_attn_part* part = nullptr, const int64_t* pos = nullptr, int pos_sel = 0,
-                      int nchunk_grid = 0, int64_t kv_rows = 0)
+                      int nchunk_grid = 0, int64_t kv_rows = 0, const int8_t* vl = nullptr)
 {
     const int64_t n = n_past + T;
     const int G = H / Hkv, LR = G * T, rows = T * H;
@@ -460,8 +505,12 @@ cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const ui
     ca.pos = pos;
     ca.pos_sel = pos_sel;
     ca.kv_rows = pos ? kv_rows : n;
-    attn_chunk_kernel<D><<<dim3((unsigned)(nchunk * Hkv), 1u, (unsigned)((LR + QB - 1) / QB)), CT, 0,
-                           ctx->stream>>>(ca);
+    ca.vl = vl;
+    if (vl && (v_stride % 16 || ((uintptr_t)vl & 15)))
+        return cpv_fail(ctx, CPV_EINVAL, "attention: limb planes need 16-byte aligned rows");
+    const dim3 cgrid((unsigned)(nchunk * Hkv), 1u, (unsigned)((LR + QB - 1) / QB));
+    if (vl) attn_chunk_kernel<D, true><<<cgrid, CT, 0, ctx->stream>>>(ca);
+    else attn_chunk_kernel<D, false><<<cgrid, CT, 0, ctx->stream>>>(ca);
     if (out)
         attn_fold_kernel<D><<<(unsigned)rows, D, (size_t)nchunk * 12, ctx->stream>>>(ca.P, ca.mc, ca.zc, nchunk,
                                                                                   rows, out);
@@ -472,7 +521,7 @@ cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const ui
         part->zc = ca.zc;
         part->nchunk = nchunk;
         part->rows = rows;
-        part->zbits = ZBITS;
+        part->zbits = PBITS;
         part->pos = pos;
         part->pos_sel = pos_sel;
         part->t = T;
@@ -491,9 +540,12 @@ bool attn_one_block(int64_t n_past, int t, int h)
 
 template <int D>
 cpv_status attn_run(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
-                    int64_t n_past, const int32_t* parent, int t, int h, int h_kv, float scale, float* out)
+                    int64_t n_past, const int32_t* parent, int t, int h, int h_kv, float scale, float* out,
+                    const int8_t* vl)
 {
-    if (parent) return attn_block<D>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out);
+    if (parent)
+        return attn_block<D>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out, nullptr, nullptr, 0, 0,
+                             0, vl);
     // a long chain runs in token blocks to bound the scratch: node t of a chain sees
     // the rows <= n_past + t, which is what a block starting at t0 sees with n_past + t0
     const int64_t n = n_past + t;
@@ -504,7 +556,7 @@ cpv_status attn_run(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint
     for (int t0 = 0; t0 < t; t0 += (int)tb) {
         const int tn = t - t0 < (int)tb ? t - t0 : (int)tb;
         cpv_status st = attn_block<D>(ctx, q + (int64_t)t0 * h * D, kc, vt, v_stride, n_past + t0, nullptr, tn, h,
-                                      h_kv, scale, out + (int64_t)t0 * h * D);
+                                      h_kv, scale, out + (int64_t)t0 * h * D, nullptr, nullptr, 0, 0, 0, vl);
         if (st != CPV_OK) return st;
     }
     return CPV_OK;
@@ -514,11 +566,11 @@ cpv_status attn_run(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint
 
 cpv_status cpv_attn_launch(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                            int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
-                           float* out)
+                           float* out, const int8_t* vl)
 {
     auto go = [=]() {
-        return d == 128 ? attn_run<128>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out)
-                        : attn_run<64>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out);
+        return d == 128 ? attn_run<128>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out, vl)
+                        : attn_run<64>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out, vl);
     };
     const int ev = cpv_prof_mark(ctx);
     const cpv_status st = go();
@@ -532,7 +584,8 @@ cpv_status cpv_attn_launch(cpv_ctx* ctx, const float* q, const uint16_t* kc, con
 
 cpv_status cpv_attn_partials(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                              int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
-                             cpv_attn_part* part, const int64_t* pos, int pos_sel, int nchunk_grid, int64_t kv_rows)
+                             cpv_attn_part* part, const int64_t* pos, int pos_sel, int nchunk_grid, int64_t kv_rows,
+                             const int8_t* vl)
 {
     const int64_t grid_past = pos && (int64_t)nchunk_grid * CHUNK - t > n_past ? (int64_t)nchunk_grid * CHUNK - t : n_past;
     if ((d != 64 && d != 128) || (parent && t > 64) ||
@@ -540,9 +593,9 @@ cpv_status cpv_attn_partials(cpv_ctx* ctx, const float* q, const uint16_t* kc, c
         return CPV_EUNSUPPORTED;   // (no message: the caller takes the unfused path)
     auto go = [=]() {
         return d == 128 ? attn_block<128>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, nullptr, part,
-                                          pos, pos_sel, nchunk_grid, kv_rows)
+                                          pos, pos_sel, nchunk_grid, kv_rows, vl)
                         : attn_block<64>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, nullptr, part,
-                                         pos, pos_sel, nchunk_grid, kv_rows);
+                                         pos, pos_sel, nchunk_grid, kv_rows, vl);
     };
     const int ev = cpv_prof_mark(ctx);
     const cpv_status st = go();

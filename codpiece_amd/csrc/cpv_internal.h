@@ -339,9 +339,16 @@ cpv_status cpv_argmax_peak_rows(cpv_ctx* ctx, const float* x, const float* noise
 
 // internal launchers
 cpv_status cpv_repack_launch(cpv_ctx* ctx, cpv_weight* w, const void* aos_dev);
+// the V cache of a session as limbs: vq = rint(f16(v) 2^CPV_ATTN_VBITS)
+// (|vq| < 2^30) as CPV_ATTN_VLIMBS signed 8-bit limbs, laid out
+// [Hkv*D][v_stride / 16][limb][16 rows] (v_stride a multiple of 16): the
+// limbs of 16 consecutive rows of one column are 64 contiguous bytes, which
+// attention's P V reads straight into the int8 MFMA
+constexpr int CPV_ATTN_VBITS = 14;
+constexpr int CPV_ATTN_VLIMBS = 4;
 cpv_status cpv_attn_launch(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                            int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
-                           float* out);
+                           float* out, const int8_t* vl = nullptr);
 cpv_status cpv_qgemm_launch(cpv_ctx* ctx, const cpv_weight* w, const float* x, int64_t m, float* y);
 
 // the attention's chunk partials for a consumer that folds them itself (chains
@@ -389,4 +396,4 @@ __device__ __forceinline__ float cpv_fold_chain(const float* p, int64_t cs, cons
 cpv_status cpv_attn_partials(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                              int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
                              cpv_attn_part* part, const int64_t* pos = nullptr, int pos_sel = 0,
-                             int nchunk_grid = 0, int64_t kv_rows = 0);
+                             int nchunk_grid = 0, int64_t kv_rows = 0, const int8_t* vl = nullptr);

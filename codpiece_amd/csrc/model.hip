@@ -123,7 +123,7 @@ struct PrepArgs {
     const float* rope;     // [n_pos][n_rot/2][2]
     float* qout;           // [T][H][hd]
     uint16_t* k_cache;     // [n_ctx][Hkv*hd]
-    uint16_t* v_cache_t;   // [Hkv*hd][v_stride]
+    int8_t* v_limbs;       // the V cache's limbs [Hkv*hd][v_stride / 16][CPV_ATTN_VLIMBS][16]
     int64_t v_stride;
     int64_t rope_pos0, kv_row0;
     const int32_t* pos_off;   // [T] position of token t = rope_pos0 + pos_off[t] (a tree's depths), or null: + t
@@ -135,6 +135,27 @@ struct PrepArgs {
 
 __device__ __forceinline__ int64_t prep_rope0(const PrepArgs& a) { return a.pos ? a.pos[0] + a.rope_off : a.rope_pos0; }
 __device__ __forceinline__ int64_t prep_kv0(const PrepArgs& a) { return a.pos ? a.pos[a.pos_kv] : a.kv_row0; }
+
+// value vv of cache row `row`, column kh*hd + i, into the V cache: rounded to
+// f16 (the cache's precision), then vq = rint(v 2^CPV_ATTN_VBITS) as signed
+// 8-bit limbs, one per plane
+__device__ __forceinline__ int8_t* v_limb_at(int8_t* v, int64_t col, int64_t v_stride, int64_t row)
+{
+    return v + (col * v_stride + (row & ~(int64_t)15)) * CPV_ATTN_VLIMBS + (row & 15);   // limb l at + 16 l
+}
+
+__device__ __forceinline__ void write_v_limbs(const PrepArgs& a, int kh, int i, int64_t row, float vv)
+{
+    int x = (int)rintf(ldexpf(cpv_h2f(cpv_f2h(vv)), CPV_ATTN_VBITS));
+    int8_t* dst = v_limb_at(a.v_limbs, (int64_t)kh * a.hd + i, a.v_stride, row);
+#pragma unroll
+    for (int l = 0; l < CPV_ATTN_VLIMBS - 1; l++) {
+        const int li = ((x + 128) & 255) - 128;
+        dst[16 * l] = (int8_t)li;
+        x = (x - li) >> 8;
+    }
+    dst[16 * (CPV_ATTN_VLIMBS - 1)] = (int8_t)x;
+}
 
 __global__ __launch_bounds__(128) void qk_prep_kernel(PrepArgs a)
 {
@@ -194,7 +215,7 @@ __global__ __launch_bounds__(128) void qk_prep_kernel(PrepArgs a)
         const int64_t row = kv0 + t;
         a.k_cache[row * a.Hkv * a.hd + (int64_t)kh * a.hd + i] = cpv_f2h(out);
         const float vv = a.vv[(int64_t)t * a.ks + (int64_t)kh * a.hd + i];
-        a.v_cache_t[((int64_t)kh * a.hd + i) * a.v_stride + row] = cpv_f2h(vv);
+        write_v_limbs(a, kh, i, row, vv);
     }
 }
 
@@ -684,7 +705,7 @@ __global__ __launch_bounds__(128) void qk_prep_kept_kernel(PrepKeptArgs ka)
     } else if (a.write) {
         const int64_t row = kv0 + t;
         a.k_cache[row * a.Hkv * a.hd + (int64_t)kh * a.hd + i] = cpv_f2h(out);
-        a.v_cache_t[((int64_t)kh * a.hd + i) * a.v_stride + row] = cpv_f2h(vv);
+        write_v_limbs(a, kh, i, row, vv);
     }
 }
 
@@ -718,7 +739,8 @@ struct cpv_session {
     int64_t n_ctx = 0, mtp_ctx = 0, v_stride = 0, mtp_v_stride = 0;
     int64_t n_past = 0, mtp_past = 0;
     int max_batch = 0;
-    std::vector<uint16_t*> kc, vt;        // per layer; the last pair is the MTP cache
+    std::vector<uint16_t*> kc;            // per layer; the last is the MTP cache
+    std::vector<int8_t*> vt;              // V caches as limb planes (cpv_attn_launch), likewise
     float* rope = nullptr;                // [n_ctx + 2][n_rot/2][2]
     // activations, max_batch rows
     float *x, *xn, *qg, *kk, *vv, *q, *att, *gated, *o, *up, *gt, *act, *h, *logits, *e, *cat, *d, *dsa;
@@ -733,7 +755,7 @@ struct cpv_session {
     float* tap = nullptr;                 // attention outputs of each call, when set
     int64_t tap_cap = 0, tap_off = 0;
     int32_t* tree_dev = nullptr;          // the last tree verify: parent [64], then depth [64]
-    uint16_t** caches_dev = nullptr;      // the trunk's K caches [n_layer], then its V caches [n_layer]
+    void** caches_dev = nullptr;          // the trunk's K caches [n_layer], then its V caches [n_layer]
     std::vector<int32_t> tree_parent;     // (host copy, to check a committed path)
     int64_t tree_base = -1;               // n_past before that verify; -1 when no tree is pending
     std::vector<int32_t> cand_host;       // the draft head's shortlist (host copy of cand_dev)
@@ -960,8 +982,8 @@ extern "C" cpv_status cpv_session_create(cpv_model* m, int64_t n_ctx, int32_t ma
     s->model = m;
     s->n_ctx = n_ctx;
     s->mtp_ctx = n_ctx < 16384 ? n_ctx : 16384;       // mtp_ctx_cap (qwen35.rs:366-373)
-    s->v_stride = (n_ctx + 7) / 8 * 8;
-    s->mtp_v_stride = (s->mtp_ctx + 7) / 8 * 8;
+    s->v_stride = (n_ctx + 15) / 16 * 16;          // (16-byte limb segments)
+    s->mtp_v_stride = (s->mtp_ctx + 15) / 16 * 16;
     s->max_batch = max_batch;
     const int64_t E = hp.n_embd, hd = hp.head_dim, H = hp.n_head, Hkv = hp.n_head_kv, F = hp.n_ff, V = hp.n_vocab;
     const int64_t T = max_batch;
@@ -976,8 +998,9 @@ extern "C" cpv_status cpv_session_create(cpv_model* m, int64_t n_ctx, int32_t ma
         const bool mtp = (int)il == hp.n_layer;
         const int64_t rows = mtp ? s->mtp_ctx : n_ctx, vs = mtp ? s->mtp_v_stride : s->v_stride;
         A((size_t)rows * Hkv * hd * 2, (void**)&s->kc[il]);
-        A((size_t)Hkv * hd * vs * 2, (void**)&s->vt[il]);
-        if (st == CPV_OK) CPV_HIP(ctx, hipMemsetAsync(s->vt[il], 0, (size_t)Hkv * hd * vs * 2, ctx->stream));
+        A((size_t)CPV_ATTN_VLIMBS * Hkv * hd * vs, (void**)&s->vt[il]);
+        if (st == CPV_OK)
+            CPV_HIP(ctx, hipMemsetAsync(s->vt[il], 0, (size_t)CPV_ATTN_VLIMBS * Hkv * hd * vs, ctx->stream));
     }
     A((size_t)T * E * 4, (void**)&s->x);
     A((size_t)T * 2 * E * 4, (void**)&s->xn);
@@ -1009,15 +1032,15 @@ extern "C" cpv_status cpv_session_create(cpv_model* m, int64_t n_ctx, int32_t ma
     A((size_t)2 * CPV_TREE_MAX * 4, (void**)&s->tree_dev);
     A(2 * sizeof(int64_t), (void**)&s->pos_dev);
     A((size_t)T * 4, (void**)&s->cand_idx);
-    A((size_t)2 * hp.n_layer * sizeof(uint16_t*), (void**)&s->caches_dev);
+    A((size_t)2 * hp.n_layer * sizeof(void*), (void**)&s->caches_dev);
     if (st == CPV_OK) {
-        std::vector<uint16_t*> cp(2 * hp.n_layer);
+        std::vector<void*> cp(2 * hp.n_layer);
         for (int il = 0; il < hp.n_layer; il++) {
             cp[il] = s->kc[il];
             cp[hp.n_layer + il] = s->vt[il];
         }
         // (synchronous: the host vector goes away on return)
-        hipError_t e = hipMemcpy(s->caches_dev, cp.data(), cp.size() * sizeof(uint16_t*), hipMemcpyHostToDevice);
+        hipError_t e = hipMemcpy(s->caches_dev, cp.data(), cp.size() * sizeof(void*), hipMemcpyHostToDevice);
         if (e != hipSuccess) st = cpv_hip_fail(ctx, e, "hipMemcpy");
     }
     const int64_t kmax = (2 * E > F ? 2 * E : F) > H * hd ? (2 * E > F ? 2 * E : F) : H * hd;
@@ -1199,7 +1222,7 @@ struct PosSel {
 };
 
 cpv_status block_unfused(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_pos0, int64_t kv_row0,
-                 int64_t attn_past, uint16_t* kc, uint16_t* vt, int64_t v_stride, bool write,
+                 int64_t attn_past, uint16_t* kc, int8_t* vt, int64_t v_stride, bool write,
                  const Tree* tree, PosSel ps)
 {
     const int32_t* parent = tree ? tree->parent : nullptr;
@@ -1238,7 +1261,7 @@ cpv_status block_unfused(cpv_session* s, const LayerW& L, float* x, int T, int64
     pa.rope = s->rope;
     pa.qout = s->q;
     pa.k_cache = kc;
-    pa.v_cache_t = vt;
+    pa.v_limbs = vt;
     pa.v_stride = v_stride;
     pa.rope_pos0 = rope_pos0;
     pa.kv_row0 = kv_row0;
@@ -1256,8 +1279,8 @@ cpv_status block_unfused(cpv_session* s, const LayerW& L, float* x, int T, int64
     qk_prep_kernel<<<dim3((unsigned)T, (unsigned)(H + Hkv)), (unsigned)hd, 0, ctx->stream>>>(pa);
     CPV_HIP(ctx, hipGetLastError());
     const float kq_scale = 1.0f / sqrtf((float)hd);
-    if ((st = cpv_attn_launch(ctx, s->q, kc, vt, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd, kq_scale,
-                              s->att)))
+    if ((st = cpv_attn_launch(ctx, s->q, kc, nullptr, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd,
+                              kq_scale, s->att, vt)))
         return st;
     if (s->tap) {
         const int64_t n = (int64_t)T * H * hd;
@@ -1308,7 +1331,7 @@ bool fusable(const cpv_model* m, const LayerW& L)
 // Launches per block: norm+quant, q|k|v GEMM, prep, attention (2), gate+quant,
 // wo GEMM, residual+norm+quant, gate|up GEMM, SwiGLU+quant, down GEMM.
 cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_pos0, int64_t kv_row0,
-                 int64_t attn_past, uint16_t* kc, uint16_t* vt, int64_t v_stride, bool write, const cpv_gout* pend,
+                 int64_t attn_past, uint16_t* kc, int8_t* vt, int64_t v_stride, bool write, const cpv_gout* pend,
                  int pend_src, cpv_gout* out, PosSel ps, const Tree* tree = nullptr)
 {
     const int32_t* parent = tree ? tree->parent : nullptr;
@@ -1347,7 +1370,7 @@ cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_
     pa.rope = s->rope;
     pa.qout = s->q;
     pa.k_cache = kc;
-    pa.v_cache_t = vt;
+    pa.v_limbs = vt;
     pa.v_stride = v_stride;
     pa.rope_pos0 = rope_pos0;
     pa.kv_row0 = kv_row0;
@@ -1378,17 +1401,17 @@ cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_
     // one grid serves every position of a 1024-row range (a replayed round)
     const int64_t nch = (attn_past + T + 127) / 128, nch_grid = (nch + 7) / 8 * 8;
     const bool fold = !s->tap && hd % 64 == 0 && 256 % hd == 0 && nch_grid <= FOLD_MAX &&
-                      cpv_attn_partials(ctx, s->q, kc, vt, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd, kq_scale,
-                                        &part, s->pos_dev, ps.kv, (int)nch_grid,
-                                        ps.kv == 0 ? s->n_ctx : s->mtp_ctx) == CPV_OK;
+                      cpv_attn_partials(ctx, s->q, kc, nullptr, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd,
+                                        kq_scale, &part, s->pos_dev, ps.kv, (int)nch_grid,
+                                        ps.kv == 0 ? s->n_ctx : s->mtp_ctx, vt) == CPV_OK;
     if (fold) {
         r2.src = SRC_GATE_FOLD;
         r2.part = part;
         r2.hd = (int)hd;
     } else {
         s->eager_only = true;   // (host positions)
-        if ((st = cpv_attn_launch(ctx, s->q, kc, vt, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd,
-                                  kq_scale, s->att)))
+        if ((st = cpv_attn_launch(ctx, s->q, kc, nullptr, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd,
+                                  kq_scale, s->att, vt)))
             return st;
         if (s->tap) {
             const int64_t n = (int64_t)T * H * hd;
@@ -1751,14 +1774,14 @@ __global__ void tree_setup_kernel(TreeSetup ts, int32_t* __restrict__ tree)
 }
 
 struct CompactArgs {
-    uint16_t* const* caches;   // K caches [n_layer], then V caches [n_layer]
+    void* const* caches;       // K caches [n_layer], then V caches (limbs) [n_layer]
     int64_t base, v_stride;
     int n_layer, width, n;     // width: h_kv * head_dim halves per row
     int8_t path[CPV_TREE_MAX];
 };
 
 // rows base + path[j] -> base + j of every trunk K cache (16-byte pieces of a
-// row) and columns likewise of every V cache (one V row per thread).  Since
+// row) and columns likewise of every V cache (one limb of one column per thread).  Since
 // path[j] >= j, writing row j never touches a source of a later j: each thread
 // moves its slice in order, eight rows at a time (all eight read before any is
 // written).
@@ -1767,7 +1790,7 @@ __global__ __launch_bounds__(256) void compact_kernel(CompactArgs a)
     const int layer = blockIdx.y;
     const int g = blockIdx.x * 256 + threadIdx.x, npiece = a.width / 8;
     if (g < npiece) {
-        uint16_t* kc = a.caches[layer];
+        uint16_t* kc = (uint16_t*)a.caches[layer];
         for (int j0 = 0; j0 < a.n; j0 += 8) {
             uint4 v[8];
 #pragma unroll
@@ -1777,16 +1800,17 @@ __global__ __launch_bounds__(256) void compact_kernel(CompactArgs a)
             for (int q = 0; q < 8; q++)
                 if (j0 + q < a.n) *(uint4*)(kc + (a.base + j0 + q) * a.width + g * 8) = v[q];
         }
-    } else if (g < npiece + a.width) {
-        uint16_t* vrow = a.caches[a.n_layer + layer] + (int64_t)(g - npiece) * a.v_stride + a.base;
+    } else if (g < npiece + CPV_ATTN_VLIMBS * a.width) {
+        const int vr = g - npiece, limb = vr / a.width, col = vr - limb * a.width;
+        int8_t* vc = (int8_t*)a.caches[a.n_layer + layer] + 16 * limb;
         for (int j0 = 0; j0 < a.n; j0 += 8) {
-            uint16_t v[8];
+            int8_t v[8];
 #pragma unroll
             for (int q = 0; q < 8; q++)
-                if (j0 + q < a.n) v[q] = vrow[a.path[j0 + q]];
+                if (j0 + q < a.n) v[q] = *v_limb_at(vc, col, a.v_stride, a.base + a.path[j0 + q]);
 #pragma unroll
             for (int q = 0; q < 8; q++)
-                if (j0 + q < a.n) vrow[j0 + q] = v[q];
+                if (j0 + q < a.n) *v_limb_at(vc, col, a.v_stride, a.base + j0 + q) = v[q];
         }
     }
 }
@@ -1868,7 +1892,7 @@ extern "C" cpv_status cpv_session_commit_branch(cpv_session* s, const int32_t* p
         a.n_layer = hp.n_layer;
         a.width = (int)(hp.n_head_kv * hp.head_dim);
         a.n = n;
-        const int threads = a.width / 8 + a.width;
+        const int threads = a.width / 8 + CPV_ATTN_VLIMBS * a.width;
         compact_kernel<<<dim3((unsigned)((threads + 255) / 256), (unsigned)hp.n_layer), 256, 0, ctx->stream>>>(a);
         CPV_HIP(ctx, hipGetLastError());
     }

@@ -115,7 +115,10 @@ void     cpvo_rope_neox(float* x, int n_rot, const float* cs_row);
  * cpvo_attn_f64 the same attention in binary64 (q rounded to f16), the
  * accuracy reference. */
 #define CPVO_ATTN_CHUNK 128
-#define CPVO_ATTN_ZBITS 54   /* 62 - ceil_log2(CHUNK + 1): a chunk's sum stays below 2^62 */
+#define CPVO_ATTN_PBITS 22   /* a row's weight e in (0, 1] as rint(e 2^22) */
+#define CPVO_ATTN_VBITS 14   /* an f16 value v as rint(v 2^14): |vq| < 2^30 */
+/* vq of an f16 cache value (f16_tab must be initialised: any cpvo_attn call does it) */
+int64_t  cpvo_attn_vq(uint16_t h);
 void     cpvo_attn(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n_past,
                    const int32_t* parent, int T, int H, int Hkv, int D, float scale,
                    float* out);

@@ -185,13 +185,26 @@ void cpvo_attn_f64(const float* q, const uint16_t* kc, const uint16_t* vc, int64
  *     w_j = s_j * scale (f32).
  *  2. Chunks of CPVO_ATTN_CHUNK consecutive cache rows (absolute row index).
  *     For each chunk c with a visible row: m_c = max of its visible w;
- *     e_j = expf(w_j - m_c) (the glibc expf restatement); p_j = f16(e_j);
- *     P_c[d] = fmaf(p_j, v_jd, P_c[d]) over its visible rows in increasing
- *     order from +0; Z_c = sum rint(e_j * 2^CPVO_ATTN_ZBITS), exact in int64.
+ *     e_j = expf(w_j - m_c) (the glibc expf restatement); its weight in
+ *     fixed point p_j = rint(e_j * 2^CPVO_ATTN_PBITS) (an integer in
+ *     [0, 2^22]); every f16 cache value v in fixed point at one scale for the
+ *     whole cache, vq = rint(v * 2^CPVO_ATTN_VBITS) (|vq| < 2^30, exact for
+ *     |v| >= 2^-4, within 2^-15 below); the integer sums over its visible
+ *     rows S_c[d] = sum p_j vq_jd (exact in int64, |S| < 2^59) and
+ *     Z_c = sum p_j; P_c[d] = (float)S_c[d] * 2^-(PBITS + VBITS) (one
+ *     rounding: (float) of the integer, then an exact scaling).
  *  3. M = max m_c; f_c = expf(m_c - M); over the chunks in increasing order
- *     Zt = Zt + (Z_c * 2^-ZBITS) * f_c in binary64 from 0, and
+ *     Zt = Zt + (Z_c * 2^-PBITS) * f_c in binary64 from 0, and
  *     O[d] = fmaf(P_c[d], f_c, O[d]) in f32 from +0; out[d] = O[d] * (float)(1 / Zt).
+ * Every sum of step 2 is an exact integer sum, so the same bits come out of
+ * any order: the device forms it on the int8 MFMA (p and vq as signed 8-bit
+ * limbs), from a cache that stores vq's limbs.
  * The f64 attention above is the accuracy reference this is tested against. */
+int64_t cpvo_attn_vq(uint16_t h)
+{
+    return (int64_t)rintf(ldexpf(f16_tab[h], CPVO_ATTN_VBITS));
+}
+
 static int64_t ipow_exp(const uint16_t* h, int n)
 {
     float mx = 0.0f;
@@ -221,6 +234,7 @@ void cpvo_attn(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n
         float* P = malloc(sizeof(float) * (size_t)nchunk * D);
         float* mc = malloc(sizeof(float) * (size_t)nchunk);
         int64_t* Zc = malloc(sizeof(int64_t) * (size_t)nchunk);
+        int64_t* S = malloc(sizeof(int64_t) * (size_t)D);
 #pragma omp for schedule(dynamic)
         for (int th = 0; th < T * H; th++) {
             const int t = th / H, h = th % H, kh = h / g;
@@ -256,14 +270,15 @@ void cpvo_attn(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n
                 for (int d = 0; d < D; d++) P[c * D + d] = 0.0f;
                 if (m == -INFINITY) continue;
                 if (m > M) M = m;
+                for (int d = 0; d < D; d++) S[d] = 0;
                 for (int64_t r = r0; r < r1; r++) {
                     if (w[r] == -INFINITY) continue;
-                    const float e = cpvo_expf(w[r] - m);
-                    const float p = f16_tab[cpvo_fp32_to_fp16(e)];
-                    Zc[c] += (int64_t)rint(ldexp((double)e, CPVO_ATTN_ZBITS));
+                    const int64_t p = (int64_t)rintf(ldexpf(cpvo_expf(w[r] - m), CPVO_ATTN_PBITS));
+                    Zc[c] += p;
                     const uint16_t* vr = vc + r * row + (int64_t)kh * D;
-                    for (int d = 0; d < D; d++) P[c * D + d] = fmaf(p, f16_tab[vr[d]], P[c * D + d]);
+                    for (int d = 0; d < D; d++) S[d] += p * cpvo_attn_vq(vr[d]);
                 }
+                for (int d = 0; d < D; d++) P[c * D + d] = ldexpf((float)S[d], -(CPVO_ATTN_PBITS + CPVO_ATTN_VBITS));
             }
             /* 3: fold the chunks in order, normalise once */
             float* o = out + ((int64_t)t * H + h) * D;
@@ -272,12 +287,12 @@ void cpvo_attn(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t n
             for (int64_t c = 0; c < nchunk; c++) {
                 if (mc[c] == -INFINITY) continue;
                 const float f = cpvo_expf(mc[c] - M);
-                Zt = Zt + ldexp((double)Zc[c], -CPVO_ATTN_ZBITS) * (double)f;
+                Zt = Zt + ldexp((double)Zc[c], -CPVO_ATTN_PBITS) * (double)f;
                 for (int d = 0; d < D; d++) o[d] = fmaf(P[c * D + d], f, o[d]);
             }
             const float inv = (float)(1.0 / Zt);
             for (int d = 0; d < D; d++) o[d] = o[d] * inv;
         }
-        free(w); free(vis); free(q16); free(qf); free(P); free(mc); free(Zc);
+        free(w); free(vis); free(q16); free(qf); free(P); free(mc); free(Zc); free(S);
     }
 }

@@ -108,10 +108,12 @@ def test_attention_f64_matches_dense_masked_softmax():
 
 
 @pytest.mark.parametrize("n_past,qmul", [(0, 1.0), (1, 3.0), (300, 1.0), (700, 3.0), (4096, 1.0)])
-def test_exact_contract_is_attention_up_to_f16_probabilities(n_past, qmul):
-    # the contract rounds every probability to f16 (relative error <= 2^-11,
-    # as ggml's f16 vec_dot_type does) and the scores to 15-bit fixed point:
-    # |exact - f64| <= 2^-10 * max|v| bounds both (sum of p is 1)
+def test_exact_contract_is_attention_up_to_its_fixed_points(n_past, qmul):
+    # the contract rounds the scores to 15-bit fixed point, each weight to a
+    # multiple of 2^-22 and each value to a multiple of 2^-14 (so within
+    # 2^-15, a weighted mean of which stays within 2^-15):
+    # |exact - f64| <= 2^-12 * max|v| + 2^-15 bounds them together (measured:
+    # 3e-6 max|v| at qmul 1, 6e-5 max|v| at qmul 3)
     rng = np.random.default_rng(n_past + 7)
     H, Hkv, D = 8, 2, 64
     T = len(TREE)
@@ -120,17 +122,18 @@ def test_exact_contract_is_attention_up_to_f16_probabilities(n_past, qmul):
     scale = np.float32(1) / np.sqrt(np.float32(D))
     a = cpvo.attn(q, k, v, n_past, TREE, scale)
     b = cpvo.attn(q, k, v, n_past, TREE, scale, f64=True)
-    bound = 2.0 ** -10 * np.abs(cpvo.f16_bits_to_f32(v)).max()
+    bound = 2.0 ** -12 * np.abs(cpvo.f16_bits_to_f32(v)).max() + 2.0 ** -15
     assert np.abs(a - b).max() <= bound
 
 
 @pytest.mark.parametrize("n_past", [0, 127, 128, 700, 2047])
 def test_exact_contract_uniform_weights_closed_form(n_past):
-    # q = 0: every visible score is 0, so in every chunk m = 0, e = 1, p = 1,
-    # Z_c = (rows) 2^ZBITS and the chunk factors are 1; with v = 1 each chunk's
-    # fma chain is its row count and the fold their sum, so
+    # q = 0: every visible score is 0, so in every chunk m = 0, e = 1,
+    # p = 2^22, Z_c = (rows) 2^22 and the chunk factors are 1; with v = 1
+    # (vq = 2^14) each chunk's P_c is its row count and the fold their sum, so
     # out = (float)n * (float)(1/n) exactly.  A dropped or repeated row or
-    # chunk, a wrong factor or a missing normalisation breaks the equality.
+    # chunk, a wrong factor, scale or limb weight, or a missing normalisation
+    # breaks the equality.
     rng = np.random.default_rng(n_past)
     H, Hkv, D, T = 4, 2, 32, 3
     n = n_past + T
@@ -175,6 +178,8 @@ def test_single_visible_row_returns_its_value():
     k, v = _cache(rng, 1, Hkv, D)
     q = rng.normal(size=(1, H, D)).astype(np.float32)
     out = cpvo.attn(q, k, v, 0, None, 0.3)
+    # weight 1 on the one row: the value at the contract's 2^-14 fixed point
     vv = cpvo.f16_bits_to_f32(v)[0]
-    assert np.array_equal(out[0, :D], vv) and np.array_equal(out[0, D:], vv)
+    want = (np.rint(vv.astype(np.float64) * 2.0 ** 14) * 2.0 ** -14).astype(np.float32)
+    assert np.array_equal(out[0, :D], want) and np.array_equal(out[0, D:], want)
 
