@@ -437,7 +437,11 @@ __global__ __launch_bounds__((64 * gemm_waves<TYPE, MC>())) void qgemm_kernel(Ge
     const float* dr = a.da + (int64_t)(a.m0 + m_ea) * nrow;
     float ev0 = dr[lane < nrow ? lane : 0], ev1 = dr[lane + 64 < nrow ? lane + 64 : 0];
 
-    // then two items of weights in flight
+    // then the weights: Q4_K and Q8_0 start with one item in flight and ask
+    // for the next when the current one has arrived (a launch's first
+    // requests then sit behind fewer bytes); Q6_K's longer units keep two in
+    // flight from the start
+    constexpr bool LEAN = TYPE != CPV_Q6_K;
     v4i bufA[F::PIECES], bufB[F::PIECES];
     uint16_t dA = 0, dB = 0;
     int eA = 0, eB = 0;
@@ -448,8 +452,10 @@ __global__ __launch_bounds__((64 * gemm_waves<TYPE, MC>())) void qgemm_kernel(Ge
     cur.tile = divmod_pos(cur.it, U, a.rU, &cur.u);
     Pos nl = step(cur);
     load(cur, bufA, dA, eA);
-    load(nl, bufB, dB, eB);
-    nl = step(nl);
+    if constexpr (!LEAN) {
+        load(nl, bufB, dB, eB);
+        nl = step(nl);
+    }
 
 #pragma unroll
     for (int q = 0; q < BC; q++) {
@@ -549,15 +555,29 @@ __global__ __launch_bounds__((64 * gemm_waves<TYPE, MC>())) void qgemm_kernel(Ge
         };
         for (int it = i0; it < i1; it += 2) {
             if (cur.tile != tile) { flush(); tile = cur.tile; }
-            unit(bufA, dA, eA, slot(cur.u));
-            load(nl, bufA, dA, eA);
-            nl = step(nl);
+            if constexpr (LEAN) {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                load(nl, bufB, dB, eB);
+                nl = step(nl);
+                unit(bufA, dA, eA, slot(cur.u));
+            } else {
+                unit(bufA, dA, eA, slot(cur.u));
+                load(nl, bufA, dA, eA);
+                nl = step(nl);
+            }
             if (it + 1 >= i1) break;
             cur = step(cur);
             if (cur.tile != tile) { flush(); tile = cur.tile; }
-            unit(bufB, dB, eB, slot(cur.u));
-            load(nl, bufB, dB, eB);
-            nl = step(nl);
+            if constexpr (LEAN) {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                load(nl, bufA, dA, eA);
+                nl = step(nl);
+                unit(bufB, dB, eB, slot(cur.u));
+            } else {
+                unit(bufB, dB, eB, slot(cur.u));
+                load(nl, bufB, dB, eB);
+                nl = step(nl);
+            }
             cur = step(cur);
         }
         flush();
