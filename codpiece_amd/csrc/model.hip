@@ -22,6 +22,7 @@
 #include <array>
 #include <map>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "cpv_internal.h"
@@ -263,10 +264,10 @@ __global__ void swiglu_kernel(const float* __restrict__ g, const float* __restri
 // kernels it replaces (add_kernel, rmsnorm_kernel, gate_mul_kernel,
 // swiglu_kernel, quant_q8k_kernel / quant_q80_kernel).  Row lengths are
 // multiples of 4.
-constexpr int RB = 1024;     // threads per row block
-constexpr int RW = RB / 64;  // waves
-constexpr int RUU = 3;       // units per wave: rows up to 3 * 16 * 256 = 12288 elements
-constexpr int RQ = RUU * 4;  // register slots per thread
+constexpr int RB = 1024;     // most threads per row block
+constexpr int RW = RB / 64;  // most waves
+constexpr int RUU = 3;       // most units per wave: rows up to 3 * 16 * 256 = 12288 elements
+constexpr int RQ = RUU * 4;  // most register slots per thread
 
 enum { SRC_X = 0, SRC_ADD = 1, SRC_SET = 2, SRC_GATE = 3, SRC_SWIGLU = 4, SRC_GATE_FOLD = 5 };
 constexpr int FOLD_MAX = 512;   // attention chunks a SRC_GATE_FOLD row kernel folds (contexts to 64k)
@@ -296,41 +297,37 @@ struct RowLds {
     long long red_s[RW];
 };
 
-__device__ float row_max(float v, float* slot)
+__device__ float row_max(float v, float* slot, int nw)
 {
     const int tid = threadIdx.x;
     v = cpv_wave_reduce(v, cpv_op_max());
     if ((tid & 63) == 0) slot[tid >> 6] = v;
     __syncthreads();
     float r = slot[0];
-    for (int i = 1; i < RW; i++) r = fmaxf(r, slot[i]);
+    for (int i = 1; i < nw; i++) r = fmaxf(r, slot[i]);
     return r;
 }
 
-__device__ long long row_sum(long long v, long long* slot)
+__device__ long long row_sum(long long v, long long* slot, int nw)
 {
     const int tid = threadIdx.x;
     v = cpv_wave_reduce(v, cpv_op_add());
     if ((tid & 63) == 0) slot[tid >> 6] = v;
     __syncthreads();
     long long r = 0;
-    for (int i = 0; i < RW; i++) r += slot[i];
+    for (int i = 0; i < nw; i++) r += slot[i];
     return r;
 }
 
-__device__ __forceinline__ float take(const cpv_gout& g, int m, int64_t n, int ea)
-{
-    double* p = g.acc + (int64_t)m * g.n_pad + n;
-    const double S = *p;
-    *p = 0.0;
-    return cpv_gout_value(S, g.ew[n], ea, g.win);
-}
-
-template <int SRC>
+// NU units of 256 elements per wave, as many waves as the row's units need
+// (each load slot past the row still costs the CU's load path a cycle per
+// byte: with one block per row, that path bounds the kernel)
+template <int SRC, int NU>
 __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
 {
+    constexpr int RUU = NU, RQ = 4 * NU;
     __shared__ RowLds L;
-    const int m = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int m = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
     const int n = a.n, U = (n + 255) / 256;
     constexpr bool kept = SRC == SRC_ADD || SRC == SRC_SET;
     float* xr = a.x + (int64_t)m * a.xs;
@@ -339,7 +336,7 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
     bool ok[RUU];
 #pragma unroll
     for (int uu = 0; uu < RUU; uu++) {
-        const int u = wave + RW * uu, e = u * 256 + 4 * lane;
+        const int u = wave + nw * uu, e = u * 256 + 4 * lane;
         ok[uu] = u < U && e < n;
         e0[uu] = ok[uu] ? e : 0;
     }
@@ -364,8 +361,8 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
     }
     if (kept) {
         // its sums and row exponents are loaded before anything is stored (the
-        // stores below could alias them), then Ea, then y = the finalized sums,
-        // folded into x, the accumulator entries cleared
+        // stores further down could alias them), then Ea, then y = the
+        // finalized sums, folded into x
         double* acc = a.g.acc + (int64_t)m * a.g.n_pad;
         double S[RQ];
         int ew[RQ];
@@ -386,13 +383,24 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
         const float* dar = a.g.da + (int64_t)m * a.g.nda;
         float mx = fabsf(dar[tid < a.g.nda ? tid : 0]);
         if (tid >= a.g.nda) mx = 0.0f;
-        for (int i = tid + RB; i < a.g.nda; i += RB) mx = fmaxf(mx, fabsf(dar[i]));
-        const int ea = cpv_exp_of_max(row_max(mx, L.red_ea));
+        for (int i = tid + (int)blockDim.x; i < a.g.nda; i += blockDim.x) mx = fmaxf(mx, fabsf(dar[i]));
+        const int ea = cpv_exp_of_max(row_max(mx, L.red_ea, nw));
 #pragma unroll
         for (int j = 0; j < RQ; j++) {
             const float gv = cpv_gout_value(S[j], ew[j], ea, a.g.win);
             v[j] = SRC == SRC_ADD ? gv + v[j] : gv;
         }
+    }
+#pragma unroll
+    for (int uu = 0; uu < RUU; uu++)
+        if (!ok[uu])
+#pragma unroll
+            for (int k = 0; k < 4; k++) v[uu * 4 + k] = 0.0f;
+    // the new x and the cleared accumulator entries are stored after the
+    // norm's block reductions: a barrier waits for the stores issued before it
+    auto store_kept = [&]() {
+        if (!kept) return;
+        double* acc = a.g.acc + (int64_t)m * a.g.n_pad;
 #pragma unroll
         for (int uu = 0; uu < RUU; uu++)
             if (ok[uu]) {
@@ -400,18 +408,14 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
                 *(double2*)(acc + e0[uu]) = make_double2(0.0, 0.0);
                 *(double2*)(acc + e0[uu] + 2) = make_double2(0.0, 0.0);
             }
-    }
-#pragma unroll
-    for (int uu = 0; uu < RUU; uu++)
-        if (!ok[uu])
-#pragma unroll
-            for (int k = 0; k < 4; k++) v[uu * 4 + k] = 0.0f;
+    };
+    if (!a.norm) store_kept();
     if (a.norm) {
         // exact fixed-point sum of the f32 squares, then ggml's f32 tail
         float am = 0.0f;
 #pragma unroll
         for (int j = 0; j < RQ; j++) am = fmaxf(am, fabsf(v[j]));
-        am = row_max(am, L.red_am);
+        am = row_max(am, L.red_am, nw);
         double sum = 0.0;
         if (am > 0.0f) {
             int e;
@@ -420,10 +424,11 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
             long long S = 0;
 #pragma unroll
             for (int j = 0; j < RQ; j++) S += cpv_fixed_floor(v[j] * v[j], g2);
-            sum = ldexp((double)row_sum(S, L.red_s), g2);
+            sum = ldexp((double)row_sum(S, L.red_s, nw), g2);
         }
         const float mean = (float)(sum / (double)n);
         const float scale = 1.0f / sqrtf(mean + a.eps);
+        store_kept();
 #pragma unroll
         for (int uu = 0; uu < RUU; uu++)
 #pragma unroll
@@ -448,7 +453,7 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
     int32_t* bs32 = const_cast<int32_t*>(a.act.bs32);
 #pragma unroll
     for (int uu = 0; uu < RUU; uu++) {
-        const int u = wave + RW * uu;
+        const int u = wave + nw * uu;
         if (u >= U) break;                                  // wave-uniform
         const float* x = v + uu * 4;
         uint32_t* qw = (uint32_t*)(qa + (int64_t)m * Kp + (int64_t)u * 256) + lane;
@@ -651,15 +656,14 @@ __global__ __launch_bounds__(128) void qk_prep_kept_kernel(PrepKeptArgs ka)
     if (a.hd > 64) mx = fmaxf(mx, s_am[1]);
     const int ea = cpv_exp_of_max(mx);
     __syncthreads();
+    // this thread's two values: q and its gate, or k and v (their accumulator
+    // entries are cleared at the end, after the block's barriers)
     const int64_t qoff = (int64_t)2 * a.H * a.hd;
-    float x, vv = 0.0f;
-    if (is_q) {
-        x = take(ka.g, t, (int64_t)hh * 2 * a.hd + i, ea);
-        ka.gate_out[((int64_t)t * a.H + hh) * a.hd + i] = take(ka.g, t, (int64_t)hh * 2 * a.hd + a.hd + i, ea);
-    } else {
-        x = take(ka.g, t, qoff + (int64_t)kh * a.hd + i, ea);
-        vv = take(ka.g, t, qoff + (int64_t)a.Hkv * a.hd + (int64_t)kh * a.hd + i, ea);
-    }
+    const int64_t n0 = is_q ? (int64_t)hh * 2 * a.hd + i : qoff + (int64_t)kh * a.hd + i;
+    const int64_t n1 = is_q ? n0 + a.hd : n0 + (int64_t)a.Hkv * a.hd;
+    double* acc = ka.g.acc + (int64_t)t * ka.g.n_pad;
+    const float x = cpv_gout_value(acc[n0], ka.g.ew[n0], ea, ka.g.win);
+    const float x1 = cpv_gout_value(acc[n1], ka.g.ew[n1], ea, ka.g.win);
     const float* w = is_q ? a.q_norm : a.k_norm;
     float am = fabsf(x);
     am = cpv_wave_reduce(am, cpv_op_max());
@@ -702,11 +706,14 @@ __global__ __launch_bounds__(128) void qk_prep_kept_kernel(PrepKeptArgs ka)
     }
     if (is_q) {
         a.qout[((int64_t)t * a.H + hh) * a.hd + i] = out;
+        ka.gate_out[((int64_t)t * a.H + hh) * a.hd + i] = x1;
     } else if (a.write) {
         const int64_t row = kv0 + t;
         a.k_cache[row * a.Hkv * a.hd + (int64_t)kh * a.hd + i] = cpv_f2h(out);
-        write_v_limbs(a, kh, i, row, vv);
+        write_v_limbs(a, kh, i, row, x1);
     }
+    acc[n0] = 0.0;
+    acc[n1] = 0.0;
 }
 
 unsigned grid_for(int64_t n) { return (unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096); }
@@ -1160,10 +1167,20 @@ cpv_status row_launch(cpv_ctx* ctx, const RowArgs& a, int T)
             return cpv_fail(ctx, CPV_EUNSUPPORTED, "row kernel: rows of %d need 16-byte aligned rows of a multiple of 4",
                             a.n);
     }
+    // row_kernel: the fewest units per wave that 16 waves cover, and the waves that many units need
+    const int U = (a.n + 255) / 256, nu = (U + RW - 1) / RW, nt = 64 * ((U + nu - 1) / nu);
+    if (a.src <= SRC_SET && nu > RUU)
+        return cpv_fail(ctx, CPV_EUNSUPPORTED, "row kernel: rows of %d exceed %d elements", a.n, RQ * RB);
+    auto rows = [&](auto src) {
+        constexpr int S = decltype(src)::value;
+        if (nu == 1) row_kernel<S, 1><<<(unsigned)T, (unsigned)nt, 0, ctx->stream>>>(a);
+        else if (nu == 2) row_kernel<S, 2><<<(unsigned)T, (unsigned)nt, 0, ctx->stream>>>(a);
+        else row_kernel<S, 3><<<(unsigned)T, (unsigned)nt, 0, ctx->stream>>>(a);
+    };
     switch (a.src) {
-    case SRC_X: row_kernel<SRC_X><<<(unsigned)T, RB, 0, ctx->stream>>>(a); break;
-    case SRC_ADD: row_kernel<SRC_ADD><<<(unsigned)T, RB, 0, ctx->stream>>>(a); break;
-    case SRC_SET: row_kernel<SRC_SET><<<(unsigned)T, RB, 0, ctx->stream>>>(a); break;
+    case SRC_X: rows(std::integral_constant<int, SRC_X>()); break;
+    case SRC_ADD: rows(std::integral_constant<int, SRC_ADD>()); break;
+    case SRC_SET: rows(std::integral_constant<int, SRC_SET>()); break;
     case SRC_GATE: unit_kernel<SRC_GATE><<<ugrid, 256, 0, ctx->stream>>>(a); break;
     case SRC_GATE_FOLD:
         if (a.hd % 64 || 256 % a.hd || a.n % a.hd || a.part.nchunk > FOLD_MAX)
