@@ -24,11 +24,13 @@
 // (one block per query row).  Scratch in the context workspace: P [chunks][T*H][D]
 // f32, m [chunks][T*H] f32, Z [chunks][T*H] int64.
 //
-// Layout.  K is [n_ctx][h_kv * d] f16.  V: a session's cache holds vq's limbs,
-// [h_kv * d][v_stride / 16][4][16] (written once per row, read by P V with no
-// conversion); the API's cache (cpv_attn) is the transposed f16 cache
-// [h_kv * d][v_stride] (the reference's non-FA V layout, qwen35.rs:580-586),
-// converted in the kernel.  Either way the KV axis is the reduction axis of P V.
+// Layout.  A session's caches hold limbs, written once per row and read by
+// the MFMAs with no conversion: K as each row's hi and lo limbs per KV head
+// with the heads' exponents (cpv_k_row_bytes), V as vq's limbs,
+// [h_kv * d][v_stride / 16][4][16].  The API's caches (cpv_attn) are f16:
+// K [n_ctx][h_kv * d] and the transposed V [h_kv * d][v_stride] (the
+// reference's non-FA V layout, qwen35.rs:580-586), converted in the kernel.
+// Either way the KV axis is the reduction axis of P V.
 #include <math.h>
 
 #include "cpv_internal.h"
@@ -43,7 +45,7 @@ constexpr int PL = 3;
 constexpr int VBITS = CPV_ATTN_VBITS;   // an f16 value v as vq = rint(v 2^14): |vq| < 2^30, VLIMBS limbs
 constexpr int VLIMBS = CPV_ATTN_VLIMBS;
 constexpr int QB = 32;              // query rows per scores workgroup
-constexpr int E_EMPTY = -100000;    // exponent of an all-zero vector
+constexpr int E_EMPTY = CPV_E_EMPTY;   // exponent of an all-zero vector
 
 __device__ __forceinline__ int ceil_log2_dev(int64_t v)
 {
@@ -75,17 +77,6 @@ __device__ __forceinline__ uint64_t ancestors(const int32_t* parent, int t)
     return m;
 }
 
-// 15-bit fixed point of an f16 value at exponent e, split into two signed
-// 8-bit limbs: f = 256 hi + lo, lo in [-128, 127], |hi| <= 64
-__device__ __forceinline__ void limbs(float v, int e, int8_t* hi, int8_t* lo)
-{
-    int f = 0;
-    if (e != E_EMPTY) f = (int)rintf(ldexpf(v, 14 - e));
-    const int h = (f + 128) >> 8;
-    *hi = (int8_t)h;
-    *lo = (int8_t)(f - 256 * h);
-}
-
 struct ChunkArgs {
     const float* q;           // [T][H][D]
     const uint16_t* kc;       // [n_ctx][Hkv*D]
@@ -100,7 +91,9 @@ struct ChunkArgs {
     const int64_t* pos;       // when set, n_past is pos[pos_sel] (device memory, read at run
     int pos_sel;              // time) and the grid may hold chunks past the end, which exit
     int64_t kv_rows;          // rows the K cache holds (loads stay below it; v_stride for V)
-    const int8_t* vl;         // the V cache's limbs (VL kernels): [Hkv*D][v_stride / 16][VLIMBS][16]
+    const int8_t* vl;         // the session's V cache as limbs (LC kernels): [Hkv*D][v_stride / 16][VLIMBS][16]
+    const int8_t* kl;         // the session's K cache as limbs (LC kernels): rows of k_row bytes
+    int64_t k_row;
 };
 
 // an integer as L signed 8-bit limbs, x = sum l_i 256^i with l_i in
@@ -140,16 +133,16 @@ __device__ __forceinline__ int row_limbs(const float* v, int8_t* hi, int8_t* lo)
     int e = E_EMPTY;
     if (mx > 0.0f) frexpf(mx, &e);
 #pragma unroll
-    for (int i = 0; i < 16; i++) limbs(v[i], e, &hi[i], &lo[i]);
+    for (int i = 0; i < 16; i++) cpv_k_limbs(v[i], e, &hi[i], &lo[i]);
     return e;
 }
 
 // one 128-row chunk of the cache against 32 query rows of one KV head
 constexpr int CT = 512;             // threads of a chunk workgroup (8 waves)
 
-// VL: V comes from the cache's limb planes (a.vl); else from the f16 cache
-// (a.vt), converted here
-template <int D, bool VL>
+// LC: K and V come from a session's limb caches (a.kl, a.vl); else from the
+// API's f16 caches (a.kc, a.vt), converted here
+template <int D, bool LC>
 __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
 {
     constexpr int TPR = D / 16;                // threads per row when converting (16 values each)
@@ -194,13 +187,23 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
         for (int i = 0; i < 4; i++) qv[i] = ((const float4*)src)[i];
     }
     // (rows clamped to the cache's: the chunk's end is known once n_past is)
+    // LC: kv[p] = 16 hi limbs, 16 lo limbs of the row's head, ekv[p] its exponent
     uint4 kv[KP][2];
+    int ekv[KP];
 #pragma unroll
     for (int p = 0; p < KP; p++) {
         const int64_t row = j0 + rq + p * RPP, rc = row < a.kv_rows ? row : a.kv_rows - 1;
-        const uint16_t* src = a.kc + rc * (int64_t)a.Hkv * D + (int64_t)kh * D + sub * 16;
-        kv[p][0] = *(const uint4*)src;
-        kv[p][1] = *(const uint4*)(src + 8);
+        if constexpr (LC) {
+            const int8_t* kr = a.kl + rc * a.k_row;
+            const int8_t* src = kr + (int64_t)kh * 2 * D + sub * 16;
+            kv[p][0] = *(const uint4*)src;
+            kv[p][1] = *(const uint4*)(src + D);
+            ekv[p] = *(const int*)(kr + (int64_t)a.Hkv * 2 * D + 4 * kh);
+        } else {
+            const uint16_t* src = a.kc + rc * (int64_t)a.Hkv * D + (int64_t)kh * D + sub * 16;
+            kv[p][0] = *(const uint4*)src;
+            kv[p][1] = *(const uint4*)(src + 8);
+        }
     }
     const int64_t n_past = a.pos ? a.pos[a.pos_sel] : a.n_past, n_all = n_past + a.T;
     if (j0 >= n_all) return;                   // a chunk past the end (the whole workgroup, before any barrier)
@@ -229,6 +232,14 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     for (int p = 0; p < KP; p++) {
         const int r = rq + p * RPP;
         if (r >= CHUNK) break;                 // (threads past the chunk when d = 64)
+        if constexpr (LC) {
+            // the cache's limbs as they are; rows past the chunk's end as an all-zero row
+            const bool in = r < nj;
+            *(uint4*)&s_kh[r][sub * 16] = in ? kv[p][0] : uint4{0, 0, 0, 0};
+            *(uint4*)&s_kl[r][sub * 16] = in ? kv[p][1] : uint4{0, 0, 0, 0};
+            if (sub == 0) s_ek[r] = in ? ekv[p] : E_EMPTY;
+            continue;
+        }
         const uint32_t wds[8] = {kv[p][0].x, kv[p][0].y, kv[p][0].z, kv[p][0].w,
                                  kv[p][1].x, kv[p][1].y, kv[p][1].z, kv[p][1].w};
         int8_t hi[16], lo[16];
@@ -259,7 +270,7 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     const int dcol = cb * 16 + c16;
     v4i vb[2][VLIMBS];
     uint4 vraw[2][2];
-    if constexpr (VL) {
+    if constexpr (LC) {
         // (a segment's limbs lie together: one 64-byte read)
         const int8_t* vbase = a.vl + ((int64_t)kh * D + dcol) * a.v_stride * VLIMBS;
 #pragma unroll
@@ -365,7 +376,7 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
         }
     }
     // (the f16 cache's values into limbs meanwhile)
-    if constexpr (!VL) {
+    if constexpr (!LC) {
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
             uint32_t pk[VLIMBS][4] = {};
@@ -473,8 +484,11 @@ template <int D>
 cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                       int64_t n_past, const int32_t* parent, int T, int H, int Hkv, float scale, float* out,
                       cpv_attn_part* part = nullptr, const int64_t* pos = nullptr, int pos_sel = 0,
-                      int nchunk_grid = 0, int64_t kv_rows = 0, const int8_t* vl = nullptr)
+                      int nchunk_grid = 0, int64_t kv_rows = 0, const int8_t* vl = nullptr,
+                      const int8_t* kl = nullptr)
 {
+    if ((vl != nullptr) != (kl != nullptr))
+        return cpv_fail(ctx, CPV_EINVAL, "attention: a session's K and V limb caches go together");
     const int64_t n = n_past + T;
     const int G = H / Hkv, LR = G * T, rows = T * H;
     int nchunk = (int)((n + CHUNK - 1) / CHUNK);
@@ -506,8 +520,10 @@ cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const ui
     ca.pos_sel = pos_sel;
     ca.kv_rows = pos ? kv_rows : n;
     ca.vl = vl;
-    if (vl && (v_stride % 16 || ((uintptr_t)vl & 15)))
-        return cpv_fail(ctx, CPV_EINVAL, "attention: limb planes need 16-byte aligned rows");
+    ca.kl = kl;
+    ca.k_row = cpv_k_row_bytes(Hkv, D);
+    if (vl && (v_stride % 16 || ((uintptr_t)vl & 15) || ((uintptr_t)kl & 15)))
+        return cpv_fail(ctx, CPV_EINVAL, "attention: limb caches need 16-byte aligned rows");
     const dim3 cgrid((unsigned)(nchunk * Hkv), 1u, (unsigned)((LR + QB - 1) / QB));
     if (vl) attn_chunk_kernel<D, true><<<cgrid, CT, 0, ctx->stream>>>(ca);
     else attn_chunk_kernel<D, false><<<cgrid, CT, 0, ctx->stream>>>(ca);
@@ -541,11 +557,11 @@ bool attn_one_block(int64_t n_past, int t, int h)
 template <int D>
 cpv_status attn_run(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                     int64_t n_past, const int32_t* parent, int t, int h, int h_kv, float scale, float* out,
-                    const int8_t* vl)
+                    const int8_t* vl, const int8_t* kl)
 {
     if (parent)
         return attn_block<D>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out, nullptr, nullptr, 0, 0,
-                             0, vl);
+                             0, vl, kl);
     // a long chain runs in token blocks to bound the scratch: node t of a chain sees
     // the rows <= n_past + t, which is what a block starting at t0 sees with n_past + t0
     const int64_t n = n_past + t;
@@ -556,7 +572,7 @@ cpv_status attn_run(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint
     for (int t0 = 0; t0 < t; t0 += (int)tb) {
         const int tn = t - t0 < (int)tb ? t - t0 : (int)tb;
         cpv_status st = attn_block<D>(ctx, q + (int64_t)t0 * h * D, kc, vt, v_stride, n_past + t0, nullptr, tn, h,
-                                      h_kv, scale, out + (int64_t)t0 * h * D, nullptr, nullptr, 0, 0, 0, vl);
+                                      h_kv, scale, out + (int64_t)t0 * h * D, nullptr, nullptr, 0, 0, 0, vl, kl);
         if (st != CPV_OK) return st;
     }
     return CPV_OK;
@@ -566,11 +582,11 @@ cpv_status attn_run(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint
 
 cpv_status cpv_attn_launch(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                            int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
-                           float* out, const int8_t* vl)
+                           float* out, const int8_t* vl, const int8_t* kl)
 {
     auto go = [=]() {
-        return d == 128 ? attn_run<128>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out, vl)
-                        : attn_run<64>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out, vl);
+        return d == 128 ? attn_run<128>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out, vl, kl)
+                        : attn_run<64>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, out, vl, kl);
     };
     const int ev = cpv_prof_mark(ctx);
     const cpv_status st = go();
@@ -585,7 +601,7 @@ cpv_status cpv_attn_launch(cpv_ctx* ctx, const float* q, const uint16_t* kc, con
 cpv_status cpv_attn_partials(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                              int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
                              cpv_attn_part* part, const int64_t* pos, int pos_sel, int nchunk_grid, int64_t kv_rows,
-                             const int8_t* vl)
+                             const int8_t* vl, const int8_t* kl)
 {
     const int64_t grid_past = pos && (int64_t)nchunk_grid * CHUNK - t > n_past ? (int64_t)nchunk_grid * CHUNK - t : n_past;
     if ((d != 64 && d != 128) || (parent && t > 64) ||
@@ -593,9 +609,9 @@ cpv_status cpv_attn_partials(cpv_ctx* ctx, const float* q, const uint16_t* kc, c
         return CPV_EUNSUPPORTED;   // (no message: the caller takes the unfused path)
     auto go = [=]() {
         return d == 128 ? attn_block<128>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, nullptr, part,
-                                          pos, pos_sel, nchunk_grid, kv_rows, vl)
+                                          pos, pos_sel, nchunk_grid, kv_rows, vl, kl)
                         : attn_block<64>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, nullptr, part,
-                                         pos, pos_sel, nchunk_grid, kv_rows, vl);
+                                         pos, pos_sel, nchunk_grid, kv_rows, vl, kl);
     };
     const int ev = cpv_prof_mark(ctx);
     const cpv_status st = go();

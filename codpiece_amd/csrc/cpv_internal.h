@@ -346,9 +346,31 @@ cpv_status cpv_repack_launch(cpv_ctx* ctx, cpv_weight* w, const void* aos_dev);
 // attention's P V reads straight into the int8 MFMA
 constexpr int CPV_ATTN_VBITS = 14;
 constexpr int CPV_ATTN_VLIMBS = 4;
+
+// the K cache of a session as limbs: per row and KV head, each f16 value kf
+// as the 15-bit fixed point rint(kf 2^(14 - e)), e the frexp exponent of the
+// head's largest |kf| (CPV_E_EMPTY for an all-zero head), split into two
+// signed 8-bit limbs f = 256 hi + lo (lo in [-128, 127]): d hi bytes, then d
+// lo bytes per head; after the h_kv heads their exponents (int32), padded to
+// 16 bytes.  Attention's scores take the limbs straight into the int8 MFMA.
+__host__ __device__ __forceinline__ int64_t cpv_k_row_bytes(int h_kv, int d)
+{
+    return (int64_t)h_kv * 2 * d + ((int64_t)h_kv * 4 + 15) / 16 * 16;
+}
+__device__ __forceinline__ void cpv_k_limbs(float kf, int e, int8_t* hi, int8_t* lo)
+{
+    int f = 0;
+    if (e != CPV_E_EMPTY) f = (int)rintf(ldexpf(kf, 14 - e));
+    const int h = (f + 128) >> 8;
+    *hi = (int8_t)h;
+    *lo = (int8_t)(f - 256 * h);
+}
+
+// attention over the API's caches (kc f16 [n_ctx][h_kv*d], vt f16 transposed)
+// or a session's (vl and kl set: the limb caches above; kc and vt unused)
 cpv_status cpv_attn_launch(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                            int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
-                           float* out, const int8_t* vl = nullptr);
+                           float* out, const int8_t* vl = nullptr, const int8_t* kl = nullptr);
 cpv_status cpv_qgemm_launch(cpv_ctx* ctx, const cpv_weight* w, const float* x, int64_t m, float* y);
 
 // the attention's chunk partials for a consumer that folds them itself (chains
@@ -396,4 +418,5 @@ __device__ __forceinline__ float cpv_fold_chain(const float* p, int64_t cs, cons
 cpv_status cpv_attn_partials(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                              int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
                              cpv_attn_part* part, const int64_t* pos = nullptr, int pos_sel = 0,
-                             int nchunk_grid = 0, int64_t kv_rows = 0, const int8_t* vl = nullptr);
+                             int nchunk_grid = 0, int64_t kv_rows = 0, const int8_t* vl = nullptr,
+                             const int8_t* kl = nullptr);

@@ -112,8 +112,8 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__
 }
 
 // Per token t and head: q/k RMS norm over the head, NEOX rope at position
-// rope_pos0 + t, then q to qout, k (f16) to k_cache row kv_row0 + t and v (f16)
-// to column kv_row0 + t of the transposed V cache.  Grid (T, H + Hkv), block hd.
+// rope_pos0 + t, then q to qout, and k and v (each rounded to f16) as limbs to
+// row kv_row0 + t of the session's K and V caches.  Grid (T, H + Hkv), block hd.
 struct PrepArgs {
     const float* qg;       // [T] rows of qs floats: [H][2*hd] query | output gate per head
     const float* kk;       // [T] rows of ks floats: [Hkv*hd]
@@ -123,7 +123,7 @@ struct PrepArgs {
     const float* k_norm;   // [hd]
     const float* rope;     // [n_pos][n_rot/2][2]
     float* qout;           // [T][H][hd]
-    uint16_t* k_cache;     // [n_ctx][Hkv*hd]
+    int8_t* k_limbs;       // the K cache's limbs: rows of cpv_k_row_bytes(Hkv, hd)
     int8_t* v_limbs;       // the V cache's limbs [Hkv*hd][v_stride / 16][CPV_ATTN_VLIMBS][16]
     int64_t v_stride;
     int64_t rope_pos0, kv_row0;
@@ -158,6 +158,27 @@ __device__ __forceinline__ void write_v_limbs(const PrepArgs& a, int kh, int i, 
     dst[16 * (CPV_ATTN_VLIMBS - 1)] = (int8_t)x;
 }
 
+// key kk (element i of KV head kh, one thread each: the whole block) of cache
+// row `row` into the K cache: rounded to f16, then the head's exponent and
+// each element's two limbs (cpv_k_limbs)
+__device__ __forceinline__ void write_k_limbs(const PrepArgs& a, int kh, int i, int64_t row, float kk, float* s_km)
+{
+    const float kf = cpv_h2f(cpv_f2h(kk));
+    float km = cpv_wave_reduce(fabsf(kf), cpv_op_max());
+    if ((i & 63) == 0) s_km[i >> 6] = km;
+    __syncthreads();
+    km = s_km[0];
+    if (a.hd > 64) km = fmaxf(km, s_km[1]);
+    const int e = cpv_exp_of_max(km);
+    int8_t hi, lo;
+    cpv_k_limbs(kf, e, &hi, &lo);
+    const int64_t krow = cpv_k_row_bytes(a.Hkv, a.hd);
+    int8_t* kr = a.k_limbs + row * krow;
+    kr[(int64_t)kh * 2 * a.hd + i] = hi;
+    kr[(int64_t)kh * 2 * a.hd + a.hd + i] = lo;
+    if (i == 0) *(int32_t*)(kr + (int64_t)a.Hkv * 2 * a.hd + 4 * kh) = e;
+}
+
 __global__ __launch_bounds__(128) void qk_prep_kernel(PrepArgs a)
 {
     const int64_t rope0 = prep_rope0(a), kv0 = prep_kv0(a);   // (read first: off the critical path)
@@ -167,7 +188,7 @@ __global__ __launch_bounds__(128) void qk_prep_kernel(PrepArgs a)
     const float* src = is_q ? a.qg + (int64_t)t * a.qs + (int64_t)hh * 2 * a.hd : a.kk + (int64_t)t * a.ks + (int64_t)kh * a.hd;
     const float* w = is_q ? a.q_norm : a.k_norm;
     __shared__ float s_v[128];
-    __shared__ float s_am[2];
+    __shared__ float s_am[2], s_km[2];
     __shared__ long long s_s[2];
     const float x = src[i];
     // rms over the head (n = hd <= 128: two waves at most)
@@ -212,10 +233,10 @@ __global__ __launch_bounds__(128) void qk_prep_kernel(PrepArgs a)
     }
     if (is_q) {
         a.qout[((int64_t)t * a.H + hh) * a.hd + i] = out;
-    } else if (a.write) {
+    } else if (a.write) {   // (block-uniform)
         const int64_t row = kv0 + t;
-        a.k_cache[row * a.Hkv * a.hd + (int64_t)kh * a.hd + i] = cpv_f2h(out);
         const float vv = a.vv[(int64_t)t * a.ks + (int64_t)kh * a.hd + i];
+        write_k_limbs(a, kh, i, row, out, s_km);
         write_v_limbs(a, kh, i, row, vv);
     }
 }
@@ -644,7 +665,7 @@ __global__ __launch_bounds__(128) void qk_prep_kept_kernel(PrepKeptArgs ka)
     const bool is_q = hh < a.H;
     const int kh = hh - a.H;
     __shared__ float s_v[128];
-    __shared__ float s_am[2];
+    __shared__ float s_am[2], s_km[2];
     __shared__ long long s_s[2];
     // Ea of this token's activation row
     float mx = 0.0f;
@@ -707,9 +728,9 @@ __global__ __launch_bounds__(128) void qk_prep_kept_kernel(PrepKeptArgs ka)
     if (is_q) {
         a.qout[((int64_t)t * a.H + hh) * a.hd + i] = out;
         ka.gate_out[((int64_t)t * a.H + hh) * a.hd + i] = x1;
-    } else if (a.write) {
+    } else if (a.write) {   // (block-uniform)
         const int64_t row = kv0 + t;
-        a.k_cache[row * a.Hkv * a.hd + (int64_t)kh * a.hd + i] = cpv_f2h(out);
+        write_k_limbs(a, kh, i, row, out, s_km);
         write_v_limbs(a, kh, i, row, x1);
     }
     acc[n0] = 0.0;
@@ -746,7 +767,7 @@ struct cpv_session {
     int64_t n_ctx = 0, mtp_ctx = 0, v_stride = 0, mtp_v_stride = 0;
     int64_t n_past = 0, mtp_past = 0;
     int max_batch = 0;
-    std::vector<uint16_t*> kc;            // per layer; the last is the MTP cache
+    std::vector<int8_t*> kc;              // K caches as limbs, per layer; the last is the MTP cache
     std::vector<int8_t*> vt;              // V caches as limb planes (cpv_attn_launch), likewise
     float* rope = nullptr;                // [n_ctx + 2][n_rot/2][2]
     // activations, max_batch rows
@@ -1004,7 +1025,7 @@ extern "C" cpv_status cpv_session_create(cpv_model* m, int64_t n_ctx, int32_t ma
     for (size_t il = 0; il < layers; il++) {
         const bool mtp = (int)il == hp.n_layer;
         const int64_t rows = mtp ? s->mtp_ctx : n_ctx, vs = mtp ? s->mtp_v_stride : s->v_stride;
-        A((size_t)rows * Hkv * hd * 2, (void**)&s->kc[il]);
+        A((size_t)rows * cpv_k_row_bytes((int)Hkv, (int)hd), (void**)&s->kc[il]);
         A((size_t)CPV_ATTN_VLIMBS * Hkv * hd * vs, (void**)&s->vt[il]);
         if (st == CPV_OK)
             CPV_HIP(ctx, hipMemsetAsync(s->vt[il], 0, (size_t)CPV_ATTN_VLIMBS * Hkv * hd * vs, ctx->stream));
@@ -1239,7 +1260,7 @@ struct PosSel {
 };
 
 cpv_status block_unfused(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_pos0, int64_t kv_row0,
-                 int64_t attn_past, uint16_t* kc, int8_t* vt, int64_t v_stride, bool write,
+                 int64_t attn_past, int8_t* kc, int8_t* vt, int64_t v_stride, bool write,
                  const Tree* tree, PosSel ps)
 {
     const int32_t* parent = tree ? tree->parent : nullptr;
@@ -1277,7 +1298,7 @@ cpv_status block_unfused(cpv_session* s, const LayerW& L, float* x, int T, int64
     pa.k_norm = L.k_norm;
     pa.rope = s->rope;
     pa.qout = s->q;
-    pa.k_cache = kc;
+    pa.k_limbs = kc;
     pa.v_limbs = vt;
     pa.v_stride = v_stride;
     pa.rope_pos0 = rope_pos0;
@@ -1296,8 +1317,8 @@ cpv_status block_unfused(cpv_session* s, const LayerW& L, float* x, int T, int64
     qk_prep_kernel<<<dim3((unsigned)T, (unsigned)(H + Hkv)), (unsigned)hd, 0, ctx->stream>>>(pa);
     CPV_HIP(ctx, hipGetLastError());
     const float kq_scale = 1.0f / sqrtf((float)hd);
-    if ((st = cpv_attn_launch(ctx, s->q, kc, nullptr, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd,
-                              kq_scale, s->att, vt)))
+    if ((st = cpv_attn_launch(ctx, s->q, nullptr, nullptr, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd,
+                              kq_scale, s->att, vt, kc)))
         return st;
     if (s->tap) {
         const int64_t n = (int64_t)T * H * hd;
@@ -1348,7 +1369,7 @@ bool fusable(const cpv_model* m, const LayerW& L)
 // Launches per block: norm+quant, q|k|v GEMM, prep, attention (2), gate+quant,
 // wo GEMM, residual+norm+quant, gate|up GEMM, SwiGLU+quant, down GEMM.
 cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_pos0, int64_t kv_row0,
-                 int64_t attn_past, uint16_t* kc, int8_t* vt, int64_t v_stride, bool write, const cpv_gout* pend,
+                 int64_t attn_past, int8_t* kc, int8_t* vt, int64_t v_stride, bool write, const cpv_gout* pend,
                  int pend_src, cpv_gout* out, PosSel ps, const Tree* tree = nullptr)
 {
     const int32_t* parent = tree ? tree->parent : nullptr;
@@ -1386,7 +1407,7 @@ cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_
     pa.k_norm = L.k_norm;
     pa.rope = s->rope;
     pa.qout = s->q;
-    pa.k_cache = kc;
+    pa.k_limbs = kc;
     pa.v_limbs = vt;
     pa.v_stride = v_stride;
     pa.rope_pos0 = rope_pos0;
@@ -1418,17 +1439,17 @@ cpv_status block(cpv_session* s, const LayerW& L, float* x, int T, int64_t rope_
     // one grid serves every position of a 1024-row range (a replayed round)
     const int64_t nch = (attn_past + T + 127) / 128, nch_grid = (nch + 7) / 8 * 8;
     const bool fold = !s->tap && hd % 64 == 0 && 256 % hd == 0 && nch_grid <= FOLD_MAX &&
-                      cpv_attn_partials(ctx, s->q, kc, nullptr, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd,
+                      cpv_attn_partials(ctx, s->q, nullptr, nullptr, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd,
                                         kq_scale, &part, s->pos_dev, ps.kv, (int)nch_grid,
-                                        ps.kv == 0 ? s->n_ctx : s->mtp_ctx, vt) == CPV_OK;
+                                        ps.kv == 0 ? s->n_ctx : s->mtp_ctx, vt, kc) == CPV_OK;
     if (fold) {
         r2.src = SRC_GATE_FOLD;
         r2.part = part;
         r2.hd = (int)hd;
     } else {
         s->eager_only = true;   // (host positions)
-        if ((st = cpv_attn_launch(ctx, s->q, kc, nullptr, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd,
-                                  kq_scale, s->att, vt)))
+        if ((st = cpv_attn_launch(ctx, s->q, nullptr, nullptr, v_stride, attn_past, parent, T, (int)H, (int)Hkv, (int)hd,
+                                  kq_scale, s->att, vt, kc)))
             return st;
         if (s->tap) {
             const int64_t n = (int64_t)T * H * hd;
@@ -1791,9 +1812,9 @@ __global__ void tree_setup_kernel(TreeSetup ts, int32_t* __restrict__ tree)
 }
 
 struct CompactArgs {
-    void* const* caches;       // K caches [n_layer], then V caches (limbs) [n_layer]
+    void* const* caches;       // K caches [n_layer], then V caches [n_layer] (limbs)
     int64_t base, v_stride;
-    int n_layer, width, n;     // width: h_kv * head_dim halves per row
+    int n_layer, kpieces, width, n;   // kpieces: 16-byte pieces of a K row; width: h_kv * head_dim
     int8_t path[CPV_TREE_MAX];
 };
 
@@ -1805,17 +1826,17 @@ struct CompactArgs {
 __global__ __launch_bounds__(256) void compact_kernel(CompactArgs a)
 {
     const int layer = blockIdx.y;
-    const int g = blockIdx.x * 256 + threadIdx.x, npiece = a.width / 8;
+    const int g = blockIdx.x * 256 + threadIdx.x, npiece = a.kpieces;
     if (g < npiece) {
-        uint16_t* kc = (uint16_t*)a.caches[layer];
+        uint4* kc = (uint4*)a.caches[layer];
         for (int j0 = 0; j0 < a.n; j0 += 8) {
             uint4 v[8];
 #pragma unroll
             for (int q = 0; q < 8; q++)
-                if (j0 + q < a.n) v[q] = *(const uint4*)(kc + (a.base + a.path[j0 + q]) * a.width + g * 8);
+                if (j0 + q < a.n) v[q] = kc[(a.base + a.path[j0 + q]) * npiece + g];
 #pragma unroll
             for (int q = 0; q < 8; q++)
-                if (j0 + q < a.n) *(uint4*)(kc + (a.base + j0 + q) * a.width + g * 8) = v[q];
+                if (j0 + q < a.n) kc[(a.base + j0 + q) * npiece + g] = v[q];
         }
     } else if (g < npiece + CPV_ATTN_VLIMBS * a.width) {
         const int vr = g - npiece, limb = vr / a.width, col = vr - limb * a.width;
@@ -1907,9 +1928,10 @@ extern "C" cpv_status cpv_session_commit_branch(cpv_session* s, const int32_t* p
         a.base = s->tree_base;
         a.v_stride = s->v_stride;
         a.n_layer = hp.n_layer;
+        a.kpieces = (int)(cpv_k_row_bytes((int)hp.n_head_kv, (int)hp.head_dim) / 16);
         a.width = (int)(hp.n_head_kv * hp.head_dim);
         a.n = n;
-        const int threads = a.width / 8 + CPV_ATTN_VLIMBS * a.width;
+        const int threads = a.kpieces + CPV_ATTN_VLIMBS * a.width;
         compact_kernel<<<dim3((unsigned)((threads + 255) / 256), (unsigned)hp.n_layer), 256, 0, ctx->stream>>>(a);
         CPV_HIP(ctx, hipGetLastError());
     }

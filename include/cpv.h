@@ -248,9 +248,11 @@ cpv_status  cpv_gguf_scan(const char* path, cpv_gguf_info* info, char* errbuf, i
 cpv_status  cpv_gguf_hparams(const char* path, cpv_hparams* hp, char* errbuf, int errlen);
 cpv_status  cpv_model_load_gguf(cpv_ctx* ctx, const char* path, cpv_model** out);
 
-/* Session::new_spec (qwen35.rs:528-649): f16 K caches [n_ctx][h_kv*d] and
- * transposed V caches per layer, plus the MTP cache (min(n_ctx, 16384)
- * rows); max_batch bounds t of every call. */
+/* Session::new_spec (qwen35.rs:528-649): a K and a V cache per layer, plus
+ * the MTP cache (min(n_ctx, 16384) rows); max_batch bounds t of every call.
+ * The caches hold each row's values rounded to f16 as the integer limbs the
+ * attention's MFMAs take (written once per row; the same scores and outputs
+ * as over f16 caches). */
 cpv_status  cpv_session_create(cpv_model* m, int64_t n_ctx, int32_t max_batch, cpv_session** out);
 void        cpv_session_free(cpv_session* s);
 /* n_past / mtp_past, the round bookkeeping of engine.rs:2533-2540: a caller
