@@ -607,18 +607,22 @@ cpv_status cpv_attn_partials(cpv_ctx* ctx, const float* q, const uint16_t* kc, c
     if ((d != 64 && d != 128) || (parent && t > 64) ||
         !(d == 128 ? attn_one_block<128>(grid_past, t, h) : attn_one_block<64>(grid_past, t, h)))
         return CPV_EUNSUPPORTED;   // (no message: the caller takes the unfused path)
-    auto go = [=]() {
-        return d == 128 ? attn_block<128>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, nullptr, part,
+    // (a profile replay runs after the caller's frame is gone: its partials'
+    // description goes to a scratch copy, not to *part)
+    auto go = [=](bool replay) {
+        cpv_attn_part scratch{};
+        cpv_attn_part* pt = replay ? &scratch : part;
+        return d == 128 ? attn_block<128>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, nullptr, pt,
                                           pos, pos_sel, nchunk_grid, kv_rows, vl, kl)
-                        : attn_block<64>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, nullptr, part,
+                        : attn_block<64>(ctx, q, kc, vt, v_stride, n_past, parent, t, h, h_kv, scale, nullptr, pt,
                                          pos, pos_sel, nchunk_grid, kv_rows, vl, kl);
     };
     const int ev = cpv_prof_mark(ctx);
-    const cpv_status st = go();
+    const cpv_status st = go(false);
     if (st == CPV_OK && ev >= 0) {  // algorithmic bytes: K and V rows once, q in (the fold is the consumer's)
         const double bytes = 2.0 * 2.0 * (double)(n_past + t) * h_kv * d + 4.0 * t * h * d;
         cpv_prof_add(ctx, ev, CPV_PROF_ATTN, bytes);
-        cpv_prof_keep(ctx, CPV_PROF_ATTN, bytes, [go]() { (void)go(); });
+        cpv_prof_keep(ctx, CPV_PROF_ATTN, bytes, [go]() { (void)go(true); });
     }
     return st;
 }
