@@ -136,6 +136,21 @@ def tensor_specs(hp):
     return specs
 
 
+def round_bytes(hp, n_kv, n_kv_mtp, depth, t):
+    """Algorithmic bytes of one round: every weight the round streams once,
+    the K and V rows it attends to as f16, and t rows of f32 activations in
+    and out of each GEMM (small): (verify only, verify + depth MTP links)."""
+    E, H, Hkv, hd, F = hp["n_embd"], hp["n_head"], hp["n_head_kv"], hp["head_dim"], hp["n_ff"]
+    layer = sum(row_bytes(q, k) * n for q, k, n in ((Q4_K, E, 2 * H * hd + 2 * Hkv * hd), (Q4_K, H * hd, E),
+                                                    (Q4_K, E, 2 * F), (Q4_K, F, E)))
+    acts = 4 * t * (E + (2 * H * hd + 2 * Hkv * hd) + H * hd + E + E + 2 * F + F + E)
+    head = row_bytes(Q6_K, E) * hp["n_vocab"] + 4 * t * hp["n_vocab"]
+    kv = lambda n: 2 * 2 * n * Hkv * hd
+    verify = hp["n_layer"] * (layer + acts + kv(n_kv)) + head
+    link = layer + acts + kv(n_kv_mtp) + row_bytes(Q4_K, 2 * E) * E + head
+    return verify, verify + depth * link
+
+
 def build_model(torch, ctx, hp, seed):
     from codpiece_amd.model import Model, make_hparams
     m = Model(ctx, make_hparams(**hp))
@@ -656,6 +671,16 @@ def main():
         vo.append(a.elapsed_time(b))
         sess.set_pos(n_past, mtp_past)
     vo.sort()
+    # the round's algorithmic bytes over its device time (the verify rows attend
+    # to n_past + t rows; the MTP links to their own cache, mtp_past + t)
+    t_round = 1 + args.depth
+    vb, rb = round_bytes(hp, n_past + t_round, mtp_past + t_round, args.depth, t_round)
+    vo_s, round_s = vo[len(vo) // 2] * 1e-3, dev_ms[len(dev_ms) // 2] * 1e-3
+    round_stats = {"verify_only_GB": round(vb / 1e9, 3), "verify_only_GB_s": round(vb / vo_s / 1e9, 1),
+                   "verify_only_frac": round(vb / vo_s / 1e9 / HBM_PEAK_GBS, 4),
+                   "round_GB": round(rb / 1e9, 3), "round_GB_s": round(rb / round_s / 1e9, 1),
+                   "round_frac": round(rb / round_s / 1e9 / HBM_PEAK_GBS, 4)}
+    print(f"[bench] round bytes: {round_stats}", file=sys.stderr, flush=True)
 
     # full rounds with the draft head over an 8192-token shortlist, rewound afterwards
     cands = np.arange(8192, dtype=np.int32)
@@ -745,6 +770,7 @@ def main():
         "cpu_baseline": cpu,
         "detail": {
             "round_device_us_median": round(dev_ms[len(dev_ms) // 2] * 1e3, 1),
+            "round_bytes": round_stats,
             "verify_only_device_us_median": round(vo[len(vo) // 2] * 1e3, 1),
             "round_shortlist_8192_device_us_median": round(sl[len(sl) // 2] * 1e3, 1),
             "tree_verify_16_device_us_median": round(tv[len(tv) // 2] * 1e3, 1),
