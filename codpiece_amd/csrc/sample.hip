@@ -48,12 +48,19 @@ constexpr int BAND = 16384;            // sorted band held in LDS as u64 keys
 constexpr int HIST_MAX = 4096;         // penalty window input limit (4 per thread)
 constexpr int VMAX = 262144;           // ids fit the low 18 bits of a key
 // a band in candidate order: a block radix sort of 16 keys per thread, each
-// key (desc_key, id) packed into 50 bits; its storage overlays the key buffer
-using band_sort_t = rocprim::block_radix_sort<unsigned long long, SB, BAND / SB>;
+// key (desc_key, id) packed into 50 bits, 5 bits per pass with match ranking
+// (377 µs per B = 1 acceptance call against 391 with rocPRIM's default 8);
+// its storage overlays the key buffer.  Bands of up to SMALL_BAND keys sort
+// with 4 keys per thread.
+using band_sort_t = rocprim::block_radix_sort<unsigned long long, SB, BAND / SB, rocprim::empty_type, 1, 1, 5,
+                                              rocprim::block_radix_rank_algorithm::match>;
+constexpr int SMALL_BAND = 4096;
+using small_sort_t = rocprim::block_radix_sort<unsigned long long, SB, SMALL_BAND / SB>;
 constexpr int KEY_BITS = 50;
 constexpr size_t SAMPLE_LDS_KEYS =
     (((size_t)BAND * 8 > sizeof(band_sort_t::storage_type) ? (size_t)BAND * 8 : sizeof(band_sort_t::storage_type)) +
      255) & ~(size_t)255;
+static_assert(sizeof(small_sort_t::storage_type) <= SAMPLE_LDS_KEYS, "the small sort fits the key buffer");
 
 // ------------------------------------------------------------ block scratch
 struct FMap { uint32_t d0, d1; };      // S -> S + (S even ? d0 : d1)
@@ -460,6 +467,47 @@ __device__ __forceinline__ unsigned long long cand_key(float l, int i)
     return ((unsigned long long)desc_key(l) << 32) | (uint32_t)i;
 }
 
+// the band's cnt keys (keys[0..cnt), any order) sorted in LDS, IPT per
+// thread, and written out as ids and logits at sid/sl[pos...]; sm->last gets
+// the last key
+template <class Sort, int IPT>
+__device__ __forceinline__ void sort_emit(const float* lg, int cnt, int pos, int32_t* sid, float* sl,
+                                          unsigned long long* keys, Small* sm)
+{
+    const int tid = threadIdx.x;
+    unsigned long long k[IPT];
+#pragma unroll
+    for (int q = 0; q < IPT; q++) {
+        const int t = tid * IPT + q;
+        const unsigned long long key = t < cnt ? keys[t] : ~0ull;
+        k[q] = key == ~0ull ? (1ull << KEY_BITS) - 1 : ((key >> 32) << 18) | (key & 0x3ffffull);
+    }
+    __syncthreads();                           // the key buffer becomes the sort's storage
+    Sort().sort_to_striped(k, *reinterpret_cast<typename Sort::storage_type*>(keys), 0, KEY_BITS);
+    // thread t now holds positions t, t + SB, ... of the band (striped: the
+    // stores coalesce); every logit load goes out before the first store
+    // (padding keys read id 0).  The positions are formed anew here: values
+    // kept across the sort were spilled and reloaded one store at a time.
+    int tb = tid;
+    asm volatile("" : "+v"(tb));
+    float lv[IPT];
+#pragma unroll
+    for (int q = 0; q < IPT; q++) {
+        const int t = tb + q * SB;
+        lv[q] = lg[t < cnt ? (int)(k[q] & 0x3ffffull) : 0];
+    }
+#pragma unroll
+    for (int q = 0; q < IPT; q++) {
+        const int t = tb + q * SB;
+        if (t < cnt) {
+            sid[pos + t] = (int)(k[q] & 0x3ffffull);
+            sl[pos + t] = lv[q];
+            if (t == cnt - 1) sm->last = ((k[q] >> 18) << 32) | (k[q] & 0x3ffffull);
+        }
+    }
+    __syncthreads();
+}
+
 // The next band of the candidate order after key *last (all keys when
 // have_last is false): at most BAND keys, ending early at a histogram bin
 // boundary once `want` are in.  Writes ids and logits to sid/sl[pos...],
@@ -535,38 +583,8 @@ __device__ __noinline__ int emit_band(const float* lg, int V, bool have_last, un
     });
     __syncthreads();
     const int cnt = sm->iv[3];
-    constexpr int IPT = BAND / SB;
-    unsigned long long k[IPT];
-#pragma unroll
-    for (int q = 0; q < IPT; q++) {
-        const int t = tid * IPT + q;
-        const unsigned long long key = t < cnt ? keys[t] : ~0ull;
-        k[q] = key == ~0ull ? (1ull << KEY_BITS) - 1 : ((key >> 32) << 18) | (key & 0x3ffffull);
-    }
-    __syncthreads();                           // the key buffer becomes the sort's storage
-    band_sort_t().sort_to_striped(k, *reinterpret_cast<band_sort_t::storage_type*>(keys), 0, KEY_BITS);
-    // thread t now holds positions t, t + SB, ... of the band (striped: the
-    // stores coalesce); every logit load goes out before the first store
-    // (padding keys read id 0).  The positions are formed anew here: values
-    // kept across the sort were spilled and reloaded one store at a time.
-    int tb = tid;
-    asm volatile("" : "+v"(tb));
-    float lv[IPT];
-#pragma unroll
-    for (int q = 0; q < IPT; q++) {
-        const int t = tb + q * SB;
-        lv[q] = lg[t < cnt ? (int)(k[q] & 0x3ffffull) : 0];
-    }
-#pragma unroll
-    for (int q = 0; q < IPT; q++) {
-        const int t = tb + q * SB;
-        if (t < cnt) {
-            sid[pos + t] = (int)(k[q] & 0x3ffffull);
-            sl[pos + t] = lv[q];
-            if (t == cnt - 1) sm->last = ((k[q] >> 18) << 32) | (k[q] & 0x3ffffull);
-        }
-    }
-    __syncthreads();
+    if (cnt <= SMALL_BAND) sort_emit<small_sort_t, SMALL_BAND / SB>(lg, cnt, pos, sid, sl, keys, sm);
+    else sort_emit<band_sort_t, BAND / SB>(lg, cnt, pos, sid, sl, keys, sm);
     *last_io = sm->last;
     __syncthreads();
     return cnt;
@@ -581,6 +599,9 @@ struct DistState {
     int cnt;                    // size of the first band
     unsigned long long last;    // its last key
     float pmax[EXP_SPLIT];      // fmaxf over each part of the row
+    double psum[EXP_SPLIT];     // each part's exponentials summed in binary64 (a forecast only)
+    FMap pmap[EXP_SPLIT];       // each part's fold steps composed in binade peb
+    int peb[EXP_SPLIT];         // the binade the forecast puts the fold in at the part's start
 };
 
 struct DistArgs {
@@ -713,15 +734,59 @@ __global__ __launch_bounds__(256) void exp_kernel(DistArgs a)
     float* pr = a.pr + (size_t)row * V;
     int i0, i1;
     exp_part(V, part, &i0, &i1);
+    double ps = 0.0;             // (the part's sum, for the fold's forecast)
     if (vec4_ok(lg, V) && vec4_ok(pr, V)) {
         const float4* l4 = (const float4*)lg;
         float4* p4 = (float4*)pr;
         for (int j = (i0 >> 2) + tid; j < (i1 >> 2); j += 256) {
             const float4 v = l4[j];
-            p4[j] = make_float4(cpv_expf(v.x - mx), cpv_expf(v.y - mx), cpv_expf(v.z - mx), cpv_expf(v.w - mx));
+            const float4 e = make_float4(cpv_expf(v.x - mx), cpv_expf(v.y - mx), cpv_expf(v.z - mx), cpv_expf(v.w - mx));
+            p4[j] = e;
+            ps += ((double)e.x + (double)e.y) + ((double)e.z + (double)e.w);
         }
     } else {
-        for (int i = i0 + tid; i < i1; i += 256) pr[i] = cpv_expf(lg[i] - mx);
+        for (int i = i0 + tid; i < i1; i += 256) {
+            pr[i] = cpv_expf(lg[i] - mx);
+            ps += (double)pr[i];
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o);
+    __shared__ double s_ps[4];
+    if ((tid & 63) == 0) s_ps[tid >> 6] = ps;
+    __syncthreads();
+    if (tid == 0) a.st[row].psum[part] = (s_ps[0] + s_ps[1]) + (s_ps[2] + s_ps[3]);
+}
+
+// The index-order fold's steps over each part, composed ahead (EXP_SPLIT
+// workgroups per row, after exp_kernel): the binary64 sums of the parts
+// before it forecast the binade the fold is in when it reaches the part;
+// the part's per-element maps S -> S + d[S & 1] in that binade (fmap_of),
+// composed in index order, are its whole step there.  The fold takes the
+// step only when it does reach the part in that binade and the step keeps
+// it below the binade's top (so no element left it); else it folds the
+// part element by element (dist_kernel).  The forecast sets only the speed.
+__global__ __launch_bounds__(256) void fmap_kernel(DistArgs a)
+{
+    const int part = blockIdx.x, row = blockIdx.y, V = a.V, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    DistState& st = a.st[row];
+    double before = 0.0;
+    for (int q = 0; q < part; q++) before += st.psum[q];
+    const int eb = f_eb((float)before);
+    const float* pr = a.pr + (size_t)row * V;
+    int i0, i1;
+    exp_part(V, part, &i0, &i1);
+    // thread t composes the contiguous run [i0 + t c, i0 + (t + 1) c)
+    const int c = (i1 - i0 + 255) / 256, b0 = i0 + tid * c, b1 = b0 + c < i1 ? b0 + c : i1;
+    FMap m = {0u, 0u};
+    for (int i = b0; i < b1; i++) m = fcomp(m, fmap_of(pr[i], eb));
+    m = wave_scan_maps(m);                     // lane 63: the wave's runs in order
+    __shared__ FMap s_w[4];
+    if (lane == 63) s_w[wave] = m;
+    __syncthreads();
+    if (tid == 0) {
+        const FMap t = fcomp(fcomp(s_w[0], s_w[1]), fcomp(s_w[2], s_w[3]));
+        st.pmap[part] = t;
+        st.peb[part] = eb;
     }
 }
 
@@ -815,7 +880,27 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
                         strided(V, [&](int i) { return lg[i]; }, [&](int i, float l) { pr[i] = cpv_expf(l - mx); });
                         __syncthreads();
                     }
-                    sum1 = block_fold([&](int i) { return pr[i]; }, V, 0.0f, 0.0f, F_NONE, sm, FOLD_SEQ).sum;
+                    if (a.pre_exp) {
+                        // part by part: the composed step where it applies, else element by element
+                        const DistState& st = a.st[row];
+                        for (int part = 0; part < EXP_SPLIT; part++) {
+                            int i0, i1;
+                            exp_part(V, part, &i0, &i1);
+                            if (i1 <= i0) continue;
+                            const int eb = f_eb(sum1);
+                            if (part > 0 && eb == st.peb[part]) {
+                                const uint32_t S0 = f_S(sum1), S = S0 + fsel(st.pmap[part], S0);
+                                if (S < FTOP) {
+                                    sum1 = f_make(eb, S);
+                                    continue;
+                                }
+                            }
+                            sum1 = block_fold([&](int i) { return pr[i0 + i]; }, i1 - i0, sum1, 0.0f, F_NONE, sm,
+                                              part == 0 ? FOLD_SEQ : 0).sum;
+                        }
+                    } else {
+                        sum1 = block_fold([&](int i) { return pr[i]; }, V, 0.0f, 0.0f, F_NONE, sm, FOLD_SEQ).sum;
+                    }
                     if (a.phase == 1) {
                         if (tid == 0) a.st[row].sum1 = sum1;
                         return;
@@ -1153,6 +1238,7 @@ cpv_status dist_launch(cpv_ctx* ctx, DistArgs& a, int rows)
     if (a.pre_exp) {
         rowmax_part_kernel<<<dim3(EXP_SPLIT, (unsigned)rows), 256, 0, ctx->stream>>>(a);
         exp_kernel<<<dim3(EXP_SPLIT, (unsigned)rows), 256, 0, ctx->stream>>>(a);
+        fmap_kernel<<<dim3(EXP_SPLIT, (unsigned)rows), 256, 0, ctx->stream>>>(a);
     }
     if (a.pre_exp && 2 * rows <= ctx->cu_count) {
         a.phase = 1;
