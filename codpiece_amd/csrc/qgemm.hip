@@ -595,6 +595,289 @@ __global__ __launch_bounds__((64 * gemm_waves<TYPE, MC>())) void qgemm_kernel(Ge
     }
 }
 
+// ---------------------------------------------------------------- Q4_K, 9-16 rows
+// The items, staging, tile sums and accumulator of qgemm_kernel for Q4_K
+// weights and 9 to 16 activation rows, with the integer dots on
+// v_mfma_i32_16x16x32_i8: one MFMA per (16-row block rb of the tile,
+// 32-element sub-block s of the unit) takes all 16 activation rows at once,
+// 32 MFMAs per item where the 4x4x4 shape needs 256 (the same layout as
+// qgemm_wide_kernel: A row and B column = lane % 16, codes 8 (lane / 16) ..
+// + 7 of the sub-block per lane, D rows 4 (lane / 16) + i of column lane %
+// 16).  Lane (c, g) = (lane % 16, lane / 16) thus holds the dots of
+// activation rows 4g..4g+3 with weight rows 16 rb + c, rb = 0..3: it decodes
+// the scales of those four weight rows (their headers come from the lanes
+// that loaded them) and runs the sub-block scale products, the min term
+// (packed 8-bit dot products against the split code sums) and the binary64
+// terms of its 16 (activation row, weight row) pairs in place.  The terms are
+// those of gemm_unit, so the accumulator entries are the same bits.
+constexpr int R16 = 16;   // activation rows of one launch (rows M..15 repeat row M-1 and are never stored)
+
+__host__ __device__ inline size_t q4k16_lds(int M, int nu, int nt)
+{
+    const size_t codes = (size_t)M * ((size_t)nu * 256 + 16);
+    const size_t aux = (size_t)nu * R16 * (16 + 8);   // [unit][row] packed code sums, then [unit][row] f64 scales
+    const size_t acc = (size_t)nt * M * 64 * 8;
+    return ((codes + 15) & ~(size_t)15) + aux + acc + 16;
+}
+
+__global__ __launch_bounds__(512) void qgemm_q4k16_kernel(GemmArgs a)
+{
+    constexpr int NW = 8, NT = 64 * NW;
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int s_ea[R16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c16 = lane & 15, g4 = lane >> 4;
+    const int M = a.M, U = a.U;
+    const int64_t Kp = (int64_t)U * 256;
+
+    const int b = blockIdx.x;
+    const int I0 = b * a.iq + (b < a.ir ? b : a.ir), I1 = I0 + a.iq + (b < a.ir ? 1 : 0);
+    int us, ul;
+    const int t0 = divmod_pos(I0, U, a.rU, &us), nu = I1 - I0 < U ? I1 - I0 : U;
+    const int nt = I1 > I0 ? divmod_pos(I1 - 1, U, a.rU, &ul) - t0 + 1 : 0;
+    const int cstride = nu * 256 + 16;
+    uint8_t* s_codes = smem;
+    int4* s_bsp = (int4*)(smem + ((M * cstride + 15) & ~15));        // [nu][R16]
+    double* s_dam = (double*)(s_bsp + nu * R16);                      // [nu][R16]
+    double* s_acc = s_dam + nu * R16;                                  // [nt][M][64]
+    uint8_t* s_trash = (uint8_t*)(s_acc + nt * M * 64);
+
+    const int n = I1 - I0;
+    const int i0 = I0 + wave * n / NW, i1 = I0 + (wave + 1) * n / NW;
+    struct Pos { int it, tile, u; };
+    const int ilast = i0 < i1 ? i1 - 1 : 0;
+    auto step = [&](Pos p) {
+        if (p.it < ilast) {
+            p.it++;
+            if (++p.u == U) { p.u = 0; p.tile++; }
+        }
+        return p;
+    };
+    // an item's weights in the MFMA's layout: per (rb, chunk pr) the 8 qs
+    // bytes 32 pr + 8 g .. of row 16 rb + c (the low nibbles are sub-block
+    // 2 pr, the high ones 2 pr + 1); and the header and exponent of row `lane`
+    struct Buf { uint2 w[16]; uint4 h; int er; };
+    auto load = [&](const Pos& p, Buf& B) {
+        const uint8_t* slab = a.w + (int64_t)p.it * 9 * 1024;
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            const int rb = q >> 2, pr = q & 3;
+            B.w[q] = *(const uint2*)(slab + (2 * pr + (g4 >> 1)) * 1024 + (16 * rb + c16) * 16 + 8 * (g4 & 1));
+        }
+        B.h = *(const uint4*)(slab + 8 * 1024 + lane * 16);
+        B.er = a.ew[p.tile * 64 + lane];
+    };
+
+    // ---- staging, as in qgemm_kernel: activation codes (rows of nu * 256 +
+    // 16 bytes), then per (unit, row) the code sums packed for the min term and
+    // the scale times 2^(win - Ea) in binary64 (the product gemm_unit forms)
+    constexpr int BC = 4;
+    const int ncode = M * nu * 16, naux = nu * M;
+    const float rc = __builtin_amdgcn_rcpf((float)(nu * 16)), rm = __builtin_amdgcn_rcpf((float)M);
+    auto code_src = [&](int i) {
+        int c;
+        const int m = divmod_small(i, nu * 16, rc, &c), j = c >> 4;
+        const int u = us + j < U ? us + j : us + j - U;
+        return (const v4i*)(a.qa + (int64_t)(a.m0 + m) * Kp + u * 256 + (c & 15) * 16);
+    };
+    auto code_dst = [&](int i) {
+        int c;
+        const int m = divmod_small(i, nu * 16, rc, &c);
+        return (v4i*)(s_codes + m * cstride + c * 16);
+    };
+    // aux entry e = (unit slot j, row m): e = j * M + m
+    auto aux_unit = [&](int e, int* m) {
+        const int j = divmod_small(e, M, rm, m);
+        return us + j < U ? us + j : us + j - U;
+    };
+    v4i cv[BC];
+#pragma unroll
+    for (int q = 0; q < BC; q++) cv[q] = *code_src(tid + q * NT < ncode ? tid + q * NT : 0);
+    int am;
+    const int au = aux_unit(tid < naux ? tid : 0, &am);
+    const int32_t* bsrc = a.bs + ((int64_t)(a.m0 + am) * U + au) * 8;
+    const v4i bs0 = *(const v4i*)bsrc, bs1 = *(const v4i*)(bsrc + 4);
+    const float dav = a.da[(int64_t)(a.m0 + am) * U + au];
+    const int m_ea = wave < M ? wave : 0;
+    const float* dr = a.da + (int64_t)(a.m0 + m_ea) * U;
+    float ev0 = dr[lane < U ? lane : 0], ev1 = dr[lane + 64 < U ? lane + 64 : 0];
+
+    // the first item's weights (one in flight; the next is asked for when it has arrived)
+    Buf bufA, bufB;
+    Pos cur;
+    cur.it = i0 < i1 ? i0 : 0;
+    cur.tile = divmod_pos(cur.it, U, a.rU, &cur.u);
+    Pos nl = step(cur);
+    load(cur, bufA);
+
+#pragma unroll
+    for (int q = 0; q < BC; q++) {
+        const int i = tid + q * NT;
+        *(i < ncode ? code_dst(i) : (v4i*)s_trash) = cv[q];
+    }
+    for (int i = tid + BC * NT; i < ncode; i += NT) *code_dst(i) = *code_src(i);
+    for (int i = tid; i < nt * M * 64; i += NT) s_acc[i] = 0.0;
+    for (int r = wave; r < M; r += NW) {
+        const float* drr = a.da + (int64_t)(a.m0 + r) * U;
+        float mx = 0.0f;
+        int ib = lane;
+        if (r == wave) {
+            mx = fmaxf(lane < U ? fabsf(ev0) : 0.0f, lane + 64 < U ? fabsf(ev1) : 0.0f);
+            ib = lane + 128;
+        }
+        for (int i = ib; i < U; i += 64) mx = fmaxf(mx, fabsf(drr[i]));
+        mx = cpv_wave_reduce(mx, cpv_op_max());
+        if (lane == 0) {
+            int e = CPV_E_EMPTY;
+            if (mx > 0.0f) frexpf(mx, &e);
+            s_ea[r] = e;
+        }
+    }
+    __syncthreads();
+    {
+        // a code sum s (|s| <= 32 * 127) as 64 bh + bl, bh = s >> 6 and bl in
+        // [0, 63]: both fit a signed byte, as do the 6-bit mins, so
+        // imin = 64 dot(mn, bh) + dot(mn, bl) over packed bytes
+        auto packb = [](int x0, int x1, int x2, int x3) {
+            return (int)(((uint32_t)x0 & 255u) | (((uint32_t)x1 & 255u) << 8) | (((uint32_t)x2 & 255u) << 16) |
+                         ((uint32_t)x3 << 24));
+        };
+        auto put = [&](int e, v4i b0, v4i b1, float dv) {
+            int m;
+            const int j = divmod_small(e, M, rm, &m);
+            s_bsp[j * R16 + m] = int4{packb(b0[0] >> 6, b0[1] >> 6, b0[2] >> 6, b0[3] >> 6),
+                                      packb(b1[0] >> 6, b1[1] >> 6, b1[2] >> 6, b1[3] >> 6),
+                                      packb(b0[0] & 63, b0[1] & 63, b0[2] & 63, b0[3] & 63),
+                                      packb(b1[0] & 63, b1[1] & 63, b1[2] & 63, b1[3] & 63)};
+            const int ex = s_ea[m];
+            s_dam[j * R16 + m] = ex == CPV_E_EMPTY ? 0.0 : (double)dv * ldexp(1.0, a.win - ex);
+        };
+        if (tid < naux) put(tid, bs0, bs1, dav);
+        for (int e = tid + NT; e < naux; e += NT) {   // (more than NT entries: long rows)
+            int m;
+            const int u = aux_unit(e, &m);
+            const int32_t* src = a.bs + ((int64_t)(a.m0 + m) * U + u) * 8;
+            put(e, *(const v4i*)src, *(const v4i*)(src + 4), a.da[(int64_t)(a.m0 + m) * U + u]);
+        }
+    }
+    __syncthreads();
+
+    if (i0 < i1) {
+        double S[4][4];   // [rb][i]: activation row 4 g + i, weight row 16 rb + c
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) S[rb][i] = 0.0;
+        int tile = cur.tile;
+        auto flush = [&]() {
+            double* acc = s_acc + ((tile - t0) * M) * 64 + c16;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = 4 * g4 + i;
+                if (m < M) {
+#pragma unroll
+                    for (int rb = 0; rb < 4; rb++)
+                        __hip_atomic_fetch_add(acc + m * 64 + 16 * rb, S[rb][i], __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+#pragma unroll
+                for (int rb = 0; rb < 4; rb++) S[rb][i] = 0.0;
+            }
+        };
+        auto slot = [&](int u) { return u >= us ? u - us : u - us + U; };
+        // the A operand's row (rows past M repeat row M - 1) and the lane's
+        // activation rows for the aux reads
+        const uint8_t* arow = s_codes + (c16 < M ? c16 : M - 1) * cstride + 8 * g4;
+        int mrow[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) mrow[i] = 4 * g4 + i < M ? 4 * g4 + i : M - 1;
+        auto unit = [&](const Buf& B, int j) {
+            // the headers of weight rows 16 rb + c from lanes 16 rb + c
+            uint32_t sc[4][2], mn[4][2];
+            double dws[4], dms[4];
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++) {
+                const int src = (16 * rb + c16) * 4;
+                const uint32_t hx = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)B.h.x);
+                const uint32_t hy = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)B.h.y);
+                const uint32_t hz = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)B.h.z);
+                const uint32_t hw = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)B.h.w);
+                const int er = __builtin_amdgcn_ds_bpermute(src, B.er);
+                dws[rb] = ldexp((double)h2f(hx & 0xffffu), -er);
+                dms[rb] = ldexp((double)h2f(hx >> 16), -er);
+                sc[rb][0] = hy & 0x3f3f3f3fu;
+                mn[rb][0] = hz & 0x3f3f3f3fu;
+                sc[rb][1] = (hw & 0x0f0f0f0fu) | (((hy >> 6) & 0x03030303u) << 4);
+                mn[rb][1] = ((hw >> 4) & 0x0f0f0f0fu) | (((hz >> 6) & 0x03030303u) << 4);
+            }
+            int isum[4][4];
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) isum[rb][i] = 0;
+            const uint8_t* ab = arow + j * 256;
+#pragma unroll
+            for (int pr = 0; pr < 4; pr++) {
+                const int64_t A0 = *(const int64_t*)(ab + 64 * pr), A1 = *(const int64_t*)(ab + 64 * pr + 32);
+#pragma unroll
+                for (int rb = 0; rb < 4; rb++) {
+                    const uint2 w = B.w[rb * 4 + pr];
+                    const int64_t blo = (int64_t)(((uint64_t)(w.y & 0x0f0f0f0fu) << 32) | (w.x & 0x0f0f0f0fu));
+                    const int64_t bhi =
+                        (int64_t)(((uint64_t)((w.y >> 4) & 0x0f0f0f0fu) << 32) | ((w.x >> 4) & 0x0f0f0f0fu));
+                    const v4i D0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(A0, blo, v4i{0, 0, 0, 0}, 0, 0, 0);
+                    const v4i D1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(A1, bhi, v4i{0, 0, 0, 0}, 0, 0, 0);
+                    const uint32_t scw = sc[rb][pr >> 1];
+                    const int sce = byte_of(scw, (2 * pr) & 3), sco = byte_of(scw, (2 * pr + 1) & 3);
+#pragma unroll
+                    for (int i = 0; i < 4; i++)   // 6-bit scales times |dots| <= 32*15*127: 24-bit products
+                        isum[rb][i] += __mul24(sce, D0[i]) + __mul24(sco, D1[i]);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int4 p = s_bsp[j * R16 + mrow[i]];
+                const double da = s_dam[j * R16 + mrow[i]];
+#pragma unroll
+                for (int rb = 0; rb < 4; rb++) {
+                    const int hi = __builtin_amdgcn_sdot4((int)mn[rb][1], p.y,
+                                                          __builtin_amdgcn_sdot4((int)mn[rb][0], p.x, 0, false), false);
+                    const int lo = __builtin_amdgcn_sdot4((int)mn[rb][1], p.w,
+                                                          __builtin_amdgcn_sdot4((int)mn[rb][0], p.z, 0, false), false);
+                    const int imin = hi * 64 + lo;
+                    S[rb][i] += rint(dws[rb] * da * (double)isum[rb][i]) - rint(dms[rb] * da * (double)imin);
+                }
+            }
+        };
+        for (int it = i0; it < i1; it += 2) {
+            if (cur.tile != tile) { flush(); tile = cur.tile; }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            load(nl, bufB);
+            nl = step(nl);
+            unit(bufA, slot(cur.u));
+            if (it + 1 >= i1) break;
+            cur = step(cur);
+            if (cur.tile != tile) { flush(); tile = cur.tile; }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            load(nl, bufA);
+            nl = step(nl);
+            unit(bufB, slot(cur.u));
+            cur = step(cur);
+        }
+        flush();
+    }
+    __syncthreads();
+    const float rM = __builtin_amdgcn_rcpf((float)M);
+    for (int i = tid; i < nt * M * 64; i += NT) {
+        int m;
+        const int t = divmod_small(i >> 6, M, rM, &m), l = i & 63;
+        const int tile = t0 + t;
+        double* g = a.gsum + (int64_t)(a.m0 + m) * a.n_pad + (int64_t)tile * 64 + l;
+        if (tile * U >= I0 && (tile + 1) * U <= I1) *g = s_acc[i];
+        else unsafeAtomicAdd(g, s_acc[i]);
+    }
+}
+
 // y = the accumulated split-K sums scaled by 2^(Ew + Ea - win); leaves the
 // accumulator zero.  One block per 256 outputs of one activation row; Ea(m)
 // is recomputed from the row's scales.
@@ -625,10 +908,13 @@ __global__ __launch_bounds__(256) void qgemm_finalize_kernel(double* __restrict_
 template <int TYPE, int MC>
 cpv_status launch_mc(cpv_ctx* ctx, const GemmArgs& a, float* y, int64_t N, int64_t k, double wbytes)
 {
-    const size_t lds = gemm_lds<TYPE>(a.M, a.nu_max, a.nt_max);
+    // Q4_K above 8 rows: the 16x16x32 kernel
+    constexpr bool R16K = TYPE == CPV_Q4_K && MC == R16;
+    const size_t lds = R16K ? q4k16_lds(a.M, a.nu_max, a.nt_max) : gemm_lds<TYPE>(a.M, a.nu_max, a.nt_max);
     const unsigned grid = (unsigned)ctx->cu_count;
     auto go = [=]() {
-        qgemm_kernel<TYPE, MC><<<grid, 64 * gemm_waves<TYPE, MC>(), lds, ctx->stream>>>(a);
+        if constexpr (R16K) qgemm_q4k16_kernel<<<grid, 512, lds, ctx->stream>>>(a);
+        else qgemm_kernel<TYPE, MC><<<grid, 64 * gemm_waves<TYPE, MC>(), lds, ctx->stream>>>(a);
         if (y)   // else the sums stay in the accumulator for a fused consumer
             qgemm_finalize_kernel<<<dim3((unsigned)((N + 255) / 256), (unsigned)a.M), 256, 0, ctx->stream>>>(
                 a.gsum, a.n_pad, a.ew, a.da, a.U * Fmt<TYPE>::DA, a.m0, a.win, y, N);
@@ -661,7 +947,11 @@ cpv_status launch_type(cpv_ctx* ctx, const GemmArgs& a, float* y, int64_t N, int
 }
 
 template <int TYPE>
-size_t lds_of(int M, int nu, int nt) { return gemm_lds<TYPE>(M, nu, nt); }
+size_t lds_of(int M, int nu, int nt)
+{
+    if (TYPE == CPV_Q4_K && M > 8) return q4k16_lds(M, nu, nt);
+    return gemm_lds<TYPE>(M, nu, nt);
+}
 
 static int isum_bits(int type) { return type == CPV_Q8_0 ? 20 : type == CPV_Q4_K ? 25 : 28; }
 

@@ -4,7 +4,8 @@ Bar: bit-exact.  The GEMM contract sums exact integers, so the HIP kernel must
 reproduce the oracle's f32 outputs bit for bit at every shape, including the
 27B-class verify shapes (K, N) in {(5120, 7168), (5120, 5120), (5120, 17408),
 (17408, 5120)} with M in {1, 5, 8, 16}; up to 16 rows share one pass over
-the weights (12 and 24 rows check the partial and split launches).
+the weights (12 and 24 rows check the partial and split launches; Q4_K above
+8 rows runs on the 16x16x32 MFMA kernel).
 """
 import numpy as np
 import pytest
@@ -76,7 +77,9 @@ def test_qgemm_lm_head_q6_k(ctx, m):
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
 
 
-def test_qgemm_extreme_scales_and_zero_rows(ctx):
+@pytest.mark.parametrize("m", [4, 9, 16])
+def test_qgemm_extreme_scales_and_zero_rows(ctx, m):
+    # 4 rows: the 4x4x4 kernel; 9 and 16: the 16x16x32 one
     t = cpvo.Q4_K
     n, k = 32, 1024
     rng = np.random.default_rng(3)
@@ -84,7 +87,7 @@ def test_qgemm_extreme_scales_and_zero_rows(ctx):
     wf[5] = 0.0                                   # an all-zero weight row
     wf[7] *= 1e3                                  # a row with huge scales
     wq = cpvo.quantize(t, wf)
-    x = rng.normal(0, 1, size=(4, k)).astype(np.float32)
+    x = rng.normal(0, 1, size=(m, k)).astype(np.float32)
     x[1] = 0.0                                    # an all-zero activation row
     x[2] *= 1e-6
     w = ctx.upload_weight(t, wq, n, k)
