@@ -57,10 +57,21 @@ using band_sort_t = rocprim::block_radix_sort<unsigned long long, SB, BAND / SB,
 constexpr int SMALL_BAND = 4096;
 using small_sort_t = rocprim::block_radix_sort<unsigned long long, SB, SMALL_BAND / SB>;
 constexpr int KEY_BITS = 50;
+// a first band split at histogram-bin boundaries into parts that workgroups
+// of their own sort: bin b (keys from offset o_b of the band on) joins part
+// o_b / PSPAN, so a part spans at most PSPAN keys plus its last bin, and
+// holds at most SMALL_BAND keys while no bin exceeds PSPAN
+constexpr int PSPAN = 2048;
+constexpr int MAXP = BAND / PSPAN;
 constexpr size_t SAMPLE_LDS_KEYS =
     (((size_t)BAND * 8 > sizeof(band_sort_t::storage_type) ? (size_t)BAND * 8 : sizeof(band_sort_t::storage_type)) +
      255) & ~(size_t)255;
 static_assert(sizeof(small_sort_t::storage_type) <= SAMPLE_LDS_KEYS, "the small sort fits the key buffer");
+// band_part_kernel's key buffer: one part (two workgroups share a CU)
+constexpr size_t PART_LDS_KEYS =
+    (((size_t)SMALL_BAND * 8 > sizeof(small_sort_t::storage_type) ? (size_t)SMALL_BAND * 8
+                                                                   : sizeof(small_sort_t::storage_type)) +
+     255) & ~(size_t)255;
 
 // ------------------------------------------------------------ block scratch
 struct FMap { uint32_t d0, d1; };      // S -> S + (S even ? d0 : d1)
@@ -73,6 +84,9 @@ struct Small {
     int wi[SWV];
     int iv[8];
     unsigned long long last;           // the last key of a band
+    int poff[8], pend[8], pfill[8];    // a partitioned band: each part's offset, end and fill
+    float pf1[8], pf2[8];              // each part's estimated sums of exp(l - max) and exp((l - max) / T)
+    unsigned long long wmax[SWV], wmin[SWV];
 };
 
 // for (i = tid; i < n; i += SB) use(i, load(i)), with BU loads in flight:
@@ -472,7 +486,7 @@ __device__ __forceinline__ unsigned long long cand_key(float l, int i)
 // the last key
 template <class Sort, int IPT>
 __device__ __forceinline__ void sort_emit(const float* lg, int cnt, int pos, int32_t* sid, float* sl,
-                                          unsigned long long* keys, Small* sm)
+                                          unsigned long long* keys, Small* sm, int (&oid)[IPT], float (&olv)[IPT])
 {
     const int tid = threadIdx.x;
     unsigned long long k[IPT];
@@ -504,30 +518,67 @@ __device__ __forceinline__ void sort_emit(const float* lg, int cnt, int pos, int
             sl[pos + t] = lv[q];
             if (t == cnt - 1) sm->last = ((k[q] >> 18) << 32) | (k[q] & 0x3ffffull);
         }
+        oid[q] = (int)(k[q] & 0x3ffffull);
+        olv[q] = lv[q];
     }
     __syncthreads();
 }
+template <class Sort, int IPT>
+__device__ __forceinline__ void sort_emit(const float* lg, int cnt, int pos, int32_t* sid, float* sl,
+                                          unsigned long long* keys, Small* sm)
+{
+    int oid[IPT];
+    float olv[IPT];
+    sort_emit<Sort, IPT>(lg, cnt, pos, sid, sl, keys, sm, oid, olv);
+}
+
+// the split top-p build's state per row: the row maximum in EXP_SPLIT
+// parts, then what its first launch leaves for the second
+constexpr int EXP_SPLIT = 32;
+struct DistState {
+    float sum1;                 // the index-order sum of exp(l - max)
+    int cnt;                    // size of the first band
+    unsigned long long last;    // its last key
+    float pmax[EXP_SPLIT];      // fmaxf over each part of the row
+    double psum[EXP_SPLIT];     // each part's exponentials summed in binary64 (a forecast only)
+    FMap pmap[EXP_SPLIT];       // each part's fold steps composed in binade peb
+    int peb[EXP_SPLIT];         // the binade the forecast puts the fold in at the part's start
+    int np;                     // the first band in parts (band_part_kernel sorts them), or 0
+    int boff[MAXP], bcnt[MAXP]; // each part's offset in the band and size
+    unsigned long long first;   // the band's first key
+    float bf1[MAXP], bf2[MAXP]; // each part's estimated sums of exp(l - max) and exp((l - max) / T)
+    FMap m1[MAXP], m2[MAXP];    // each part's top-p fold (pr / sum1) and final-sum (exp(l / T - mx2)) steps
+    int eb1[MAXP], eb2[MAXP];   // composed in these binades
+};
 
 // The next band of the candidate order after key *last (all keys when
 // have_last is false): at most BAND keys, ending early at a histogram bin
-// boundary once `want` are in.  Writes ids and logits to sid/sl[pos...],
-// advances *last and returns the band size.
-__device__ __noinline__ int emit_band(const float* lg, int V, bool have_last, unsigned long long* last_io, int want,
-                         int pos, int32_t* sid, float* sl, unsigned long long* keys, Small* sm)
+// boundary once `want` are in.  band_select leaves the last level's
+// histogram in the key buffer and describes the band: the keys after *last
+// and up to hi, which share `prefix` on the bits `fixed` and lie in bins
+// first..j of the level at shift sh; tot = 0: no key is left.
+struct BandSel {
+    unsigned long long prefix, fixed, hi;
+    int sh, nb, first, j;
+    uint32_t tot;
+};
+
+__device__ BandSel band_select(const float* lg, int V, bool have_last, unsigned long long last, int want,
+                               unsigned long long* keys, Small* sm)
 {
     const int tid = threadIdx.x;
-    const unsigned long long last = *last_io;
     uint32_t* hist = (uint32_t*)keys;
-    unsigned long long prefix = 0, fixed = 0, hi = ~0ull;
+    BandSel b{};
+    b.hi = ~0ull;
     // bit fields of the key: desc_key in 63..32 (12 + 12 + 8), id in 17..0 (9 + 9)
     const int SH[5] = {52, 40, 32, 9, 0};
     const int WD[5] = {12, 12, 8, 9, 9};
-    bool found = false;
-    for (int lev = 0; lev < 5 && !found; lev++) {
+    for (int lev = 0; lev < 5; lev++) {
         const int sh = SH[lev], nb = 1 << WD[lev];
         __syncthreads();
-        for (int b = tid; b < nb; b += SB) hist[b] = 0;
+        for (int q = tid; q < nb; q += SB) hist[q] = 0;
         __syncthreads();
+        const unsigned long long prefix = b.prefix, fixed = b.fixed;
         row_pass(lg, V, [&](int i, float l) {
             const unsigned long long key = cand_key(l, i);
             if ((have_last && key <= last) || (key & fixed) != prefix) return;
@@ -537,8 +588,8 @@ __device__ __noinline__ int emit_band(const float* lg, int V, bool have_last, un
         uint32_t c[4], s = 0;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const int b = tid * 4 + q;
-            c[q] = b < nb ? hist[b] : 0u;
+            const int bq = tid * 4 + q;
+            c[q] = bq < nb ? hist[bq] : 0u;
             s += c[q];
         }
         uint32_t tot;
@@ -549,12 +600,12 @@ __device__ __noinline__ int emit_band(const float* lg, int V, bool have_last, un
         int my_cap = -1, my_want = 0x7fffffff, my_first = 0x7fffffff;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const int b = tid * 4 + q;
-            if (b < nb) {
+            const int bq = tid * 4 + q;
+            if (bq < nb) {
                 run += c[q];
-                if (run <= (uint32_t)BAND) my_cap = b;
-                if (run >= (uint32_t)want && my_want == 0x7fffffff) my_want = b;
-                if (c[q] && my_first == 0x7fffffff) my_first = b;
+                if (run <= (uint32_t)BAND) my_cap = bq;
+                if (run >= (uint32_t)want && my_want == 0x7fffffff) my_want = bq;
+                if (c[q] && my_first == 0x7fffffff) my_first = bq;
             }
         }
         if (my_cap >= 0) atomicMax(&sm->iv[0], my_cap);
@@ -562,17 +613,31 @@ __device__ __noinline__ int emit_band(const float* lg, int V, bool have_last, un
         if (my_first != 0x7fffffff) atomicMin(&sm->iv[2], my_first);
         __syncthreads();
         const int jcap = sm->iv[0], jwant = sm->iv[1], first = sm->iv[2];
-        if (tot == 0) return 0;
+        b.tot = tot;
+        if (tot == 0) return b;
         if (jcap >= first) {
-            const int j = jwant < jcap ? jwant : jcap;
-            hi = prefix | ((unsigned long long)j << sh) | ((1ull << sh) - 1ull);
-            found = true;
-        } else {
-            // the first non-empty bin alone holds more than a band: refine it
-            prefix |= (unsigned long long)first << sh;
-            fixed |= (unsigned long long)(nb - 1) << sh;
+            b.j = jwant < jcap ? jwant : jcap;
+            b.hi = prefix | ((unsigned long long)b.j << sh) | ((1ull << sh) - 1ull);
+            b.sh = sh;
+            b.nb = nb;
+            b.first = first;
+            return b;
         }
+        // the first non-empty bin alone holds more than a band: refine it
+        b.prefix |= (unsigned long long)first << sh;
+        b.fixed |= (unsigned long long)(nb - 1) << sh;
     }
+    return b;   // (not reached: the last level's bins hold one key each)
+}
+
+// the band's keys gathered into the key buffer, sorted and written out at
+// sid/sl[pos...]; *last_io advances to the band's last key
+__device__ int band_sort_emit(const float* lg, int V, bool have_last, BandSel b,
+                              unsigned long long* last_io, int pos, int32_t* sid, float* sl,
+                              unsigned long long* keys, Small* sm)
+{
+    const int tid = threadIdx.x;
+    const unsigned long long last = *last_io, hi = b.hi;
     __syncthreads();
     if (tid == 0) sm->iv[3] = 0;
     __syncthreads();
@@ -590,19 +655,128 @@ __device__ __noinline__ int emit_band(const float* lg, int V, bool have_last, un
     return cnt;
 }
 
+// Writes ids and logits to sid/sl[pos...], advances *last and returns the
+// band size.
+__device__ __noinline__ int emit_band(const float* lg, int V, bool have_last, unsigned long long* last_io, int want,
+                                      int pos, int32_t* sid, float* sl, unsigned long long* keys, Small* sm)
+{
+    const BandSel b = band_select(lg, V, have_last, *last_io, want, keys, sm);
+    if (b.tot == 0) return 0;
+    return band_sort_emit(lg, V, have_last, b, last_io, pos, sid, sl, keys, sm);
+}
+
+// The first band for workgroups of its own to sort (the split top-p build):
+// its keys gathered into bkeys, part by part (parts of whole bins of a
+// histogram over the band's key range, each sorted by band_part_kernel).  Returns the band size and sets *last to its
+// last key and *np to the number of parts; or -1 (np = 0) when a part would
+// exceed SMALL_BAND keys, for the caller to emit the band itself.
+__device__ __noinline__ int emit_band_parts(const float* lg, int V, float mx, float T, unsigned long long* last,
+                                            unsigned long long* bkeys, DistState* st, int* np,
+                                            unsigned long long* keys, Small* sm)
+{
+    const int tid = threadIdx.x;
+    *np = 0;
+    const BandSel b = band_select(lg, V, false, 0ull, BAND, keys, sm);
+    if (b.tot == 0) return 0;
+    // the band's keys lie in [klo, hi]: a histogram of its own over that
+    // range, 4096 bins of 2^bs keys (the selection's bins are too coarse to
+    // part: near a band's edge one holds thousands of keys)
+    const unsigned long long klo = b.prefix | ((unsigned long long)b.first << b.sh), hi = b.hi;
+    const unsigned long long span = hi - klo;
+    const int bs = span >> 12 ? 64 - __clzll((long long)span) - 12 : 0;   // span >> bs < 4096
+    uint32_t* hist = (uint32_t*)keys;
+    uint8_t* part_of = (uint8_t*)keys + 4 * 4096;   // (after the histogram)
+    __syncthreads();
+    for (int q = tid; q < 4096; q += SB) hist[q] = 0;
+    __syncthreads();
+    row_pass(lg, V, [&](int i, float l) {
+        const unsigned long long key = cand_key(l, i);
+        if (key > hi || key < klo) return;
+        atomicAdd(&hist[(int)((key - klo) >> bs)], 1u);
+    });
+    __syncthreads();
+    // part of each bin (its offset in the band / PSPAN), each part's range
+    uint32_t c[4], s = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        c[q] = hist[tid * 4 + q];
+        s += c[q];
+    }
+    uint32_t tot;
+    uint32_t off = block_excl_scan(s, sm, &tot);
+    if (tid < MAXP) {
+        sm->poff[tid] = 0x7fffffff;
+        sm->pend[tid] = 0;
+        sm->pfill[tid] = 0;
+        sm->pf1[tid] = 0.0f;
+        sm->pf2[tid] = 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int bq = tid * 4 + q;
+        if (c[q]) {
+            const int k = (int)(off / PSPAN);
+            part_of[bq] = (uint8_t)k;
+            atomicMin(&sm->poff[k], (int)off);
+            atomicMax(&sm->pend[k], (int)(off + c[q]));
+            // the part's sums estimated from the bin's largest logit (they set
+            // the binades the parts' fold steps are composed in: speed only)
+            const uint32_t ord = ~(uint32_t)((klo + ((unsigned long long)bq << bs)) >> 32);
+            const float lb = __uint_as_float((ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord);
+            atomicAdd(&sm->pf1[k], (float)c[q] * __expf(lb - mx));
+            atomicAdd(&sm->pf2[k], (float)c[q] * __expf((lb - mx) / T));
+        }
+        off += c[q];
+    }
+    __syncthreads();
+    bool fits = true;
+    for (int k = 0; k < MAXP; k++)
+        if (sm->pend[k] - (sm->poff[k] < sm->pend[k] ? sm->poff[k] : sm->pend[k]) > SMALL_BAND) fits = false;
+    if (!fits) return -1;
+    unsigned long long kmx = 0ull, kmn = ~0ull;   // (the band is not empty)
+    row_pass(lg, V, [&](int i, float l) {
+        const unsigned long long key = cand_key(l, i);
+        if (key > hi || key < klo) return;
+        const int k = part_of[(int)((key - klo) >> bs)];
+        bkeys[sm->poff[k] + atomicAdd(&sm->pfill[k], 1)] = key;
+        kmx = key > kmx ? key : kmx;
+        kmn = key < kmn ? key : kmn;
+    });
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long y = __shfl_xor(kmx, o), z = __shfl_xor(kmn, o);
+        kmx = y > kmx ? y : kmx;
+        kmn = z < kmn ? z : kmn;
+    }
+    if ((tid & 63) == 0) {
+        sm->wmax[tid >> 6] = kmx;
+        sm->wmin[tid >> 6] = kmn;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        unsigned long long m = sm->wmax[0], n = sm->wmin[0];
+        for (int w = 1; w < SWV; w++) {
+            m = sm->wmax[w] > m ? sm->wmax[w] : m;
+            n = sm->wmin[w] < n ? sm->wmin[w] : n;
+        }
+        sm->last = m;
+        st->first = n;
+    }
+    __syncthreads();
+    if (tid < MAXP) {
+        const bool used = sm->pend[tid] > 0;
+        st->boff[tid] = used ? sm->poff[tid] : 0;
+        st->bcnt[tid] = used ? sm->pend[tid] - sm->poff[tid] : 0;
+        st->bf1[tid] = sm->pf1[tid];
+        st->bf2[tid] = sm->pf2[tid];
+    }
+    *last = sm->last;
+    *np = MAXP;
+    __syncthreads();
+    return (int)tot;
+}
+
 // ------------------------------------------------------------ distributions
-// the split top-p build's state per row: the row maximum in EXP_SPLIT
-// parts, then what its first launch leaves for the second
-constexpr int EXP_SPLIT = 32;
-struct DistState {
-    float sum1;                 // the index-order sum of exp(l - max)
-    int cnt;                    // size of the first band
-    unsigned long long last;    // its last key
-    float pmax[EXP_SPLIT];      // fmaxf over each part of the row
-    double psum[EXP_SPLIT];     // each part's exponentials summed in binary64 (a forecast only)
-    FMap pmap[EXP_SPLIT];       // each part's fold steps composed in binade peb
-    int peb[EXP_SPLIT];         // the binade the forecast puts the fold in at the part's start
-};
 
 struct DistArgs {
     const float* p_logits;      // spec: [B][k+1][V]; direct: [rows][V]
@@ -621,6 +795,9 @@ struct DistArgs {
     int phase;                  // 0: the whole build; top-p split: 1 (two workgroups per row), then 2
     int pre_exp;                // top-p: pr already holds expf(l - max) (exp_kernel)
     DistState* st;              // [rows] (phases 1 and 2)
+    unsigned long long* bkeys;  // [rows][BAND] the first band's keys, part by part (phase 1)
+    float* e2;                  // [rows][BAND] exp(l / T - mx2) of the first band's candidates (band parts)
+    int parts;                  // phase 1 leaves the first band in parts (band_part_kernel follows)
 };
 
 // Penalties (lib.rs:233-266): a dense copy of the row in which every token
@@ -906,17 +1083,59 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
                         return;
                     }
                 }
-                cnt = emit_band(lg, V, false, &last, BAND, 0, sid, sl, keys, sm);
                 if (a.phase == 1) {
+                    // the band's keys in parts for band_part_kernel to sort,
+                    // or the band sorted here
+                    DistState& st = a.st[row];
+                    int np = 0;
+                    cnt = -1;
+                    if (a.parts) {
+                        float mxr = -INFINITY;
+                        for (int q = 0; q < EXP_SPLIT; q++) mxr = fmaxf(mxr, st.pmax[q]);
+                        cnt = emit_band_parts(lg, V, mxr, P.temp, &last, a.bkeys + (size_t)row * BAND, &st, &np, keys,
+                                              sm);
+                    }
+                    if (cnt < 0) cnt = emit_band(lg, V, false, &last, BAND, 0, sid, sl, keys, sm);
                     if (tid == 0) {
-                        a.st[row].cnt = cnt;
-                        a.st[row].last = last;
+                        st.cnt = cnt;
+                        st.last = last;
+                        st.np = np;
                     }
                     return;
                 }
+                cnt = emit_band(lg, V, false, &last, BAND, 0, sid, sl, keys, sm);
             }
             float s = 0.0f;
             int ifirst = -1;
+            if (a.phase == 2 && a.st[row].np > 0 && cnt > 0) {
+                // the first band in parts: each part's composed step where it
+                // applies and leaves the sum below top_p (the fold's values
+                // only grow, so no element of the part meets the predicate),
+                // else the part element by element
+                const DistState& st = a.st[row];
+                for (int p = 0; p < st.np; p++) {
+                    const int pc = st.bcnt[p], po = st.boff[p];
+                    if (pc <= 0) continue;
+                    const int eb = f_eb(s);
+                    if (eb == st.eb1[p]) {
+                        const uint32_t S0 = f_S(s), S = S0 + fsel(st.m1[p], S0);
+                        if (S < FTOP && !(f_make(eb, S) >= P.top_p)) {
+                            s = f_make(eb, S);
+                            continue;
+                        }
+                    }
+                    const int32_t* band = sid + po;
+                    const FoldRes r = block_fold([&](int i) { return pr[band[i]] / sum1; }, pc, s, P.top_p, F_GE, sm);
+                    if (r.idx >= 0) {
+                        ifirst = po + r.idx;
+                        break;
+                    }
+                    s = r.sum;
+                }
+                emitted = cnt;
+                if (ifirst < 0 && emitted < V) cnt = emit_band(lg, V, true, &last, BAND, emitted, sid, sl, keys, sm);
+                else cnt = 0;
+            }
             while (cnt > 0) {
                 const int32_t* band = sid + emitted;
                 const FoldRes r = block_fold([&](int i) { return pr[band[i]] / sum1; }, cnt, s, P.top_p, F_GE, sm);
@@ -974,12 +1193,113 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
     const float T = P.temp;
     const float mx2 = (top_k || min_p || top_p ? sl[0] : mx) / T;
     __syncthreads();
+    if (top_p && a.phase == 2 && a.st[row].np > 0 && n <= a.st[row].cnt) {
+        // the survivors lie in the first band: its parts' e2 and composed
+        // steps (band_part_kernel), the steps where they apply, whole parts
+        // below n; the rest element by element
+        const DistState& st = a.st[row];
+        const float* e2 = a.e2 + (size_t)row * BAND;
+        float s2 = 0.0f;
+        for (int p = 0; p < st.np; p++) {
+            const int pc = st.bcnt[p], po = st.boff[p];
+            if (pc <= 0 || po >= n) continue;
+            const int len = n - po < pc ? n - po : pc;
+            const int eb = f_eb(s2);
+            if (len == pc && eb == st.eb2[p]) {
+                const uint32_t S0 = f_S(s2), S = S0 + fsel(st.m2[p], S0);
+                if (S < FTOP) {
+                    s2 = f_make(eb, S);
+                    continue;
+                }
+            }
+            s2 = block_fold([&](int i) { return e2[po + i]; }, len, s2, 0.0f, F_NONE, sm, po == 0 ? FOLD_SEQ : 0).sum;
+        }
+        __syncthreads();
+        strided(n, [&](int i) { return e2[i]; }, [&](int i, float e) { pr[i] = e / s2; });
+        if (tid == 0) a.hdr[row] = n;
+        return;
+    }
     strided(n, [&](int i) { return sl[i]; }, [&](int i, float l) { pr[i] = cpv_expf(l / T - mx2); });
     __syncthreads();
     const float s2 = block_fold([&](int i) { return pr[i]; }, n, 0.0f, 0.0f, F_NONE, sm, FOLD_SEQ).sum;
     __syncthreads();
     strided(n, [&](int i) { return pr[i]; }, [&](int i, float e) { pr[i] = e / s2; });
     if (tid == 0) a.hdr[row] = n;
+}
+
+// The split top-p build's first band, part by part (after phase 1, before
+// phase 2): workgroup (p, row) sorts part p's keys, whole histogram bins of
+// the band in order, and writes their ids and logits at the part's offset.
+// It then composes the part's steps of the two folds phase 2 runs over the
+// band in candidate order: the top-p fold of pr[id] / sum1 and the final
+// softmax sum of e2 = exp(l / T - mx2) (mx2 = the first candidate's l / T;
+// the e2 are kept for phase 2), each in the binade its estimated sums put the
+// fold in at the part's start.  Phase 2 takes a part's step only where it
+// applies (the fmap_kernel rule), else folds the part element by element.
+__global__ __launch_bounds__(SB) void band_part_kernel(DistArgs a)
+{
+    extern __shared__ __align__(16) unsigned char sdyn[];
+    unsigned long long* keys = (unsigned long long*)sdyn;
+    Small* sm;
+    const int p = blockIdx.x, row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    DistState& st = a.st[row];
+    if (p >= st.np) return;
+    sm = (Small*)(sdyn + PART_LDS_KEYS);
+    const int cnt = st.bcnt[p], off = st.boff[p];
+    if (cnt <= 0) return;
+    const unsigned long long* src = a.bkeys + (size_t)row * BAND + off;
+    for (int t = tid; t < cnt; t += SB) keys[t] = src[t];
+    __syncthreads();
+    const size_t ro = (size_t)row * a.V;
+    const float* lg = row_logits(a, row);
+    constexpr int IPT = SMALL_BAND / SB;
+    int id[IPT];
+    float lv[IPT];
+    sort_emit<small_sort_t, IPT>(lg, cnt, off, a.sid + ro, a.sl + ro, keys, sm, id, lv);
+    // this thread's positions tid + q SB: their terms (0 past the part)
+    const float sum1 = st.sum1, T = a.prm.temp;
+    const float mx2 = lg[(int)(st.first & 0x3ffffull)] / T;
+    const float* pr = a.pr + ro;
+    float* e2 = a.e2 + (size_t)row * BAND;
+    float t1[IPT], t2[IPT];
+#pragma unroll
+    for (int q = 0; q < IPT; q++) {
+        const int t = tid + q * SB;
+        t1[q] = t < cnt ? pr[id[q]] / sum1 : 0.0f;
+        t2[q] = t < cnt ? cpv_expf(lv[q] / T - mx2) : 0.0f;
+        if (t < cnt) e2[off + t] = t2[q];
+    }
+    double f1 = 0.0, f2 = 0.0;
+    for (int q = 0; q < p; q++) {
+        f1 += (double)st.bf1[q];
+        f2 += (double)st.bf2[q];
+    }
+    const int eb1 = f_eb((float)(f1 / (double)sum1)), eb2 = f_eb((float)f2);
+    // the maps composed in position order: each stride of SB positions over
+    // the waves in order, then the strides in order
+    FMap c1 = {0u, 0u}, c2 = {0u, 0u};
+#pragma unroll
+    for (int q = 0; q < IPT; q++) {
+        const FMap w1 = wave_scan_maps(fmap_of(t1[q], eb1)), w2 = wave_scan_maps(fmap_of(t2[q], eb2));
+        __syncthreads();
+        if (lane == 63) {
+            sm->wtot[wave] = w1;
+            sm->wi[wave] = (int)w2.d0;
+            sm->scan[wave] = w2.d1;
+        }
+        __syncthreads();
+        if (tid == 0)
+            for (int w = 0; w < SWV; w++) {
+                c1 = fcomp(c1, sm->wtot[w]);
+                c2 = fcomp(c2, FMap{(uint32_t)sm->wi[w], sm->scan[w]});
+            }
+    }
+    if (tid == 0) {
+        st.m1[p] = c1;
+        st.m2[p] = c2;
+        st.eb1[p] = eb1;
+        st.eb2[p] = eb2;
+    }
 }
 
 // ------------------------------------------------------------ acceptance
@@ -1189,6 +1509,8 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 struct DistBufs {
     int32_t* hdr;
     DistState* st;
+    unsigned long long* bkeys;
+    float* e2;
     int32_t* sid;
     float* sl;
     float* pr;
@@ -1199,7 +1521,8 @@ struct DistBufs {
 size_t dist_bytes(int rows, int V, bool pen)
 {
     const size_t rv = align256((size_t)rows * V * 4);
-    return align256((size_t)rows * 4) + align256((size_t)rows * sizeof(DistState)) + 3 * rv + (pen ? rv : 0);
+    return align256((size_t)rows * 4) + align256((size_t)rows * sizeof(DistState)) +
+           align256((size_t)rows * BAND * 8) + align256((size_t)rows * BAND * 4) + 3 * rv + (pen ? rv : 0);
 }
 
 DistBufs dist_carve(void* ws, int rows, int V, bool pen)
@@ -1211,6 +1534,10 @@ DistBufs dist_carve(void* ws, int rows, int V, bool pen)
     p += align256((size_t)rows * 4);
     d.st = (DistState*)p;
     p += align256((size_t)rows * sizeof(DistState));
+    d.bkeys = (unsigned long long*)p;
+    p += align256((size_t)rows * BAND * 8);
+    d.e2 = (float*)p;
+    p += align256((size_t)rows * BAND * 4);
     d.sid = (int32_t*)p;
     p += rv;
     d.sl = (float*)p;
@@ -1241,8 +1568,12 @@ cpv_status dist_launch(cpv_ctx* ctx, DistArgs& a, int rows)
         fmap_kernel<<<dim3(EXP_SPLIT, (unsigned)rows), 256, 0, ctx->stream>>>(a);
     }
     if (a.pre_exp && 2 * rows <= ctx->cu_count) {
+        // the first band in parts while the part workgroups fit the CUs two to a CU
+        a.parts = rows * MAXP <= 2 * ctx->cu_count;
         a.phase = 1;
         dist_kernel<<<(unsigned)(2 * rows), SB, lds, ctx->stream>>>(a);
+        if (a.parts)
+            band_part_kernel<<<dim3(MAXP, (unsigned)rows), SB, PART_LDS_KEYS + sizeof(Small), ctx->stream>>>(a);
         a.phase = 2;
         dist_kernel<<<(unsigned)rows, SB, lds, ctx->stream>>>(a);
     } else {
@@ -1285,6 +1616,8 @@ extern "C" cpv_status cpv_distribution(cpv_ctx* ctx, const float* logits_dev, in
     a.pr = probs_dev;
     a.hdr = n_dev;
     a.st = d.st;
+    a.bkeys = d.bkeys;
+    a.e2 = d.e2;
     return dist_launch(ctx, a, rows);
 }
 
@@ -1343,6 +1676,8 @@ extern "C" cpv_status cpv_spec_accept(cpv_ctx* ctx, const float* p_logits_dev, c
     a.pr = d.pr;
     a.hdr = d.hdr;
     a.st = d.st;
+    a.bkeys = d.bkeys;
+    a.e2 = d.e2;
     if ((st = dist_launch(ctx, a, rows))) return st;
     DecideArgs c{};
     c.draft = draft_dev;

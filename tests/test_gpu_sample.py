@@ -117,6 +117,20 @@ def test_distribution_equal_logits_order_by_id(ctx):
         check_dist(ctx, logits, p)
 
 
+def test_distribution_top_p_band_parts_and_fallback(ctx):
+    # the split top-p build sorts its first band in parts of whole histogram
+    # bins (a part spans at most 2048 keys plus its last bin, and may hold
+    # 4096); tied logits share a bin: row 0 ties 5000 top logits, more than a
+    # part may hold, so its band is sorted in one workgroup; row 1 ties 1500
+    print("case dist band parts", flush=True)
+    rng = np.random.default_rng(5)
+    logits = rng.normal(0, 1, size=(3, V27)).astype(np.float32)
+    logits[0, rng.choice(V27, 5000, replace=False)] = 5.0
+    logits[1, rng.choice(V27, 1500, replace=False)] = 5.0
+    for p in [cpvo.SamplerParams(temp=0.7, top_p=0.95), cpvo.SamplerParams(temp=1.0, top_p=0.3)]:
+        check_dist(ctx, logits, p)
+
+
 def short_exp_logits():
     """Logits l <= 0 whose expf is a float with at most 3 significant bits,
     from 1 down to 2^-40: their sums round on exact ties all the time."""
