@@ -314,7 +314,7 @@ struct RowArgs {
 
 // each block-wide reduction has its own LDS slots, so one barrier suffices
 struct RowLds {
-    float red_ea[RW], red_am[RW];
+    float red_am[RW];
     long long red_s[RW];
 };
 
@@ -401,11 +401,12 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
             ew[uu * 4 + 2] = ev.z;
             ew[uu * 4 + 3] = ev.w;
         }
+        // Ea: every wave reduces the row's few scales itself (no block barrier)
         const float* dar = a.g.da + (int64_t)m * a.g.nda;
-        float mx = fabsf(dar[tid < a.g.nda ? tid : 0]);
-        if (tid >= a.g.nda) mx = 0.0f;
-        for (int i = tid + (int)blockDim.x; i < a.g.nda; i += blockDim.x) mx = fmaxf(mx, fabsf(dar[i]));
-        const int ea = cpv_exp_of_max(row_max(mx, L.red_ea, nw));
+        float mx = fabsf(dar[lane < a.g.nda ? lane : 0]);
+        if (lane >= a.g.nda) mx = 0.0f;
+        for (int i = lane + 64; i < a.g.nda; i += 64) mx = fmaxf(mx, fabsf(dar[i]));
+        const int ea = cpv_exp_of_max(cpv_wave_reduce(mx, cpv_op_max()));
 #pragma unroll
         for (int j = 0; j < RQ; j++) {
             const float gv = cpv_gout_value(S[j], ew[j], ea, a.g.win);
@@ -589,14 +590,10 @@ __global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
         double* acc = a.g.acc + (int64_t)m * a.g.n_pad;
         const double S0 = acc[ec], S1 = acc[n + ec];
         const int e0 = a.g.ew[ec], e1 = a.g.ew[n + ec];
+        // Ea: every wave reduces the row's few scales itself (no block barrier)
         float mx = 0.0f;
-        for (int i = t; i < a.g.nda; i += 256) mx = fmaxf(mx, fabsf(a.g.da[(int64_t)m * a.g.nda + i]));
-        mx = cpv_wave_reduce(mx, cpv_op_max());
-        if (lane == 0) s_ax[wave] = mx;
-        __syncthreads();
-        mx = fmaxf(fmaxf(s_ax[0], s_ax[1]), fmaxf(s_ax[2], s_ax[3]));
-        __syncthreads();
-        const int ea = cpv_exp_of_max(mx);
+        for (int i = lane; i < a.g.nda; i += 64) mx = fmaxf(mx, fabsf(a.g.da[(int64_t)m * a.g.nda + i]));
+        const int ea = cpv_exp_of_max(cpv_wave_reduce(mx, cpv_op_max()));
         if (e < n) {
             const float gv = cpv_gout_value(S0, e0, ea, a.g.win), uv = cpv_gout_value(S1, e1, ea, a.g.win);
             acc[e] = 0.0;
@@ -667,16 +664,11 @@ __global__ __launch_bounds__(128) void qk_prep_kept_kernel(PrepKeptArgs ka)
     __shared__ float s_v[128];
     __shared__ float s_am[2], s_km[2];
     __shared__ long long s_s[2];
-    // Ea of this token's activation row
+    // Ea of this token's activation row: every wave reduces its few scales
+    // itself (no block barrier)
     float mx = 0.0f;
-    for (int c = i; c < ka.g.nda; c += a.hd) mx = fmaxf(mx, fabsf(ka.g.da[(int64_t)t * ka.g.nda + c]));
-    mx = cpv_wave_reduce(mx, cpv_op_max());
-    if ((i & 63) == 0) s_am[i >> 6] = mx;
-    __syncthreads();
-    mx = s_am[0];
-    if (a.hd > 64) mx = fmaxf(mx, s_am[1]);
-    const int ea = cpv_exp_of_max(mx);
-    __syncthreads();
+    for (int c = i & 63; c < ka.g.nda; c += 64) mx = fmaxf(mx, fabsf(ka.g.da[(int64_t)t * ka.g.nda + c]));
+    const int ea = cpv_exp_of_max(cpv_wave_reduce(mx, cpv_op_max()));
     // this thread's two values: q and its gate, or k and v (their accumulator
     // entries are cleared at the end, after the block's barriers)
     const int64_t qoff = (int64_t)2 * a.H * a.hd;
