@@ -550,10 +550,27 @@ __global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
         const int lh = t / hd, tl = t - lh * hd;             // head within the unit, thread within the head
         const int h = ec / hd, rr = m * H + h;                // (clamped: a thread past n reads a valid head)
         const int wph = hd / 64;                              // waves per head
-        // every grid chunk's max and sum are read while the count of chunks in
-        // play comes from device memory; those past it are never used
+        // every grid chunk's max and sum are read (this thread's first ones
+        // first) while the count of chunks in play comes from device memory;
+        // those past it are never used.  The element's partials of the first
+        // FB grid chunks go out next, into registers, so that the fma chain
+        // waits on no load for them (loads complete in order: the first max
+        // and sum do not wait for them)
+        constexpr int FB = 48;
+        const int c0 = tl < nchg ? tl : 0;
+        const float mc0 = a.part.mc[(int64_t)c0 * rows + rr];
+        const int64_t zc0 = a.part.zc[(int64_t)c0 * rows + rr];
+        const float* pr = a.part.P + (int64_t)rr * hd + (ec - h * hd);
+        const int64_t pcs = (int64_t)rows * hd;
+        float pv[FB];
+#pragma unroll
+        for (int i = 0; i < FB; i++) pv[i] = pr[(int64_t)(i < nchg ? i : nchg - 1) * pcs];
         float M = -INFINITY;
-        for (int c = tl; c < nchg; c += hd) {
+        if (tl < nchg) {
+            s_f[lh][tl] = mc0;
+            s_z[lh][tl] = ldexp((double)zc0, -a.part.zbits);
+        }
+        for (int c = tl + hd; c < nchg; c += hd) {
             s_f[lh][c] = a.part.mc[(int64_t)c * rows + rr];
             s_z[lh][c] = ldexp((double)a.part.zc[(int64_t)c * rows + rr], -a.part.zbits);
         }
@@ -574,9 +591,12 @@ __global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
             for (int c = 0; c < nch; c++) Zt = Zt + s_z[lh][c] * (double)s_f[lh][c];
             s_inv[lh] = (float)(1.0 / Zt);
         }
-        // the element's fma chain over the chunks
-        const float* pr = a.part.P + (int64_t)rr * hd + (ec - h * hd);
-        const float o = cpv_fold_chain(pr, (int64_t)rows * hd, s_f[lh], nch);
+        // the element's fma chain over the chunks, in chunk order
+        float o = 0.0f;
+#pragma unroll
+        for (int i = 0; i < FB; i++)
+            if (i < nch) o = fmaf(pv[i], s_f[lh][i], o);
+        if (nch > FB) o = cpv_fold_chain_from(pr, pcs, s_f[lh], nch, FB, o);
         __syncthreads();
         const float at = o * s_inv[lh];
         const float gv = a.gate[(int64_t)m * n + ec];

@@ -81,3 +81,30 @@ def test_replayed_rounds_equal_eager_rounds(model):
     assert b.replay_stats == (0, 0)
     for s in (a, b, other):
         s.free()
+
+
+def test_long_context_gate_fold_equals_unfused_attention(model):
+    # The gate kernel folds the attention's chunk partials itself, the first
+    # 48 chunks from registers and the rest from memory.  At 6600 + 5 rows
+    # (52 chunks) a round must equal, bit for bit, the same round through
+    # the attention's own fold kernel (an attention tap selects that path).
+    from codpiece_amd.model import Session
+    ctx, gm, w = model
+    a, b = Session(gm, 8192, max_batch=512), Session(gm, 8192, max_batch=512)
+    b.set_attn_tap(torch.zeros(16, device="cuda"))   # (too small to hold a copy: only the path changes)
+    rng = np.random.default_rng(21)
+    prompt = rng.integers(0, V, size=6600).tolist()
+    for s in (a, b):
+        for c in range(0, len(prompt), 512):
+            s.prefill(prompt[c:c + 512])
+    for r in range(2):
+        toks = rng.integers(0, V, size=5).tolist()
+        print(f"case long-context round {r} n_past={a.pos[0]}", flush=True)
+        oa = a.step_fused_cached(toks, 4, want_logits=True)
+        ob = b.step_fused_cached(toks, 4, want_logits=True)
+        assert oa.preds == ob.preds and oa.chain == ob.chain, r
+        assert _eq(oa.logits.cpu().numpy(), ob.logits.cpu().numpy()), r
+        assert _eq(oa.hidden.cpu().numpy(), ob.hidden.cpu().numpy()), r
+    assert a.pos == b.pos and a.pos[0] > 48 * 128
+    for s in (a, b):
+        s.free()
