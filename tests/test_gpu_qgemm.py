@@ -52,7 +52,7 @@ def run_case(ctx, t, n, k, m, seed=0, xscale=1.0):
 
 @pytest.mark.parametrize("tname", list(TYPES))
 @pytest.mark.parametrize("n,k", [(64, 256), (48, 512), (1000, 768), (33, 1024), (160, 4096)])
-@pytest.mark.parametrize("m", [1, 3, 5, 12, 16, 24])
+@pytest.mark.parametrize("m", [1, 3, 5, 9, 12, 13, 16, 24])
 def test_qgemm_bit_exact_small(ctx, tname, n, k, m):
     t = TYPES[tname]
     y, ref = run_case(ctx, t, n, k, m)
