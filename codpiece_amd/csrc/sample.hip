@@ -254,36 +254,80 @@ __device__ __forceinline__ bool fpred(int mode, float v, float thr)
     return mode == F_GE ? v >= thr : v > thr;
 }
 
+// one thread: t = t + x(i) for i < n in order; with a predicate, up to its
+// first hit (*hit = that index, t = the prefix there).  The prefixes only
+// grow, so the predicate is tested once per 16 elements, on the last prefix,
+// and inside those 16 only when it holds there.  Elements past n enter as 0,
+// which leaves a sum unchanged.
+template <class X>
+__device__ __forceinline__ float head_fold(X x_at, int n, float t, float thr, int pmode, int* hit)
+{
+    if (pmode == F_NONE) {
+#pragma unroll 16
+        for (int i = 0; i < n; i++) t = t + x_at(i);
+        return t;
+    }
+    for (int i0 = 0; i0 < n; i0 += 16) {
+        float v[16], tq[16];
+#pragma unroll
+        for (int q = 0; q < 16; q++) v[q] = x_at(i0 + q < n ? i0 + q : n - 1);
+        float u = t;
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            u = u + (i0 + q < n ? v[q] : 0.0f);
+            tq[q] = u;
+        }
+        if (fpred(pmode, u, thr)) {
+#pragma unroll
+            for (int q = 15; q >= 0; q--)
+                if (fpred(pmode, tq[q], thr)) { *hit = i0 + q; t = tq[q]; }
+            return t;
+        }
+        t = u;
+    }
+    *hit = -1;
+    return t;
+}
+
 // Sequential f32 fold s = s + x(i), i = 0..n-1, of non-negative finite x,
 // bit-identical to the loop, with an optional monotone predicate on the
 // running value (F_GE: s_i >= thr, F_GT: s_i > thr) whose first hit ends the
 // fold.  Called by every thread of the block with the same arguments.  With
-// seq > 0 (no predicate; x_at a plain load, so that the loop can issue its
-// loads ahead) one thread adds the first seq elements itself, in order: a sum
-// leaves a binade every time it doubles and each exit costs a block pass, so
-// a fold from 0 over values of one size, or over values sorted largest first
-// from 1, meets most of its exits in its first few hundred elements.
+// seq > 0 one thread adds the first seq elements itself, in order, with the
+// predicate on its prefixes (head_fold): a sum leaves a binade every time it doubles and
+// each exit costs a block pass, so a fold from 0 over values of one size, or
+// over values sorted largest first from 1, meets most of its exits in its
+// first few hundred elements.  That thread reads head[i] (LDS, staged by the
+// caller) when head is given, else x_at(i) (then a plain load, so that the
+// loop can issue its loads ahead).  With ck, thread 0 stores the running sum
+// after the first seq elements in ck[0] and after each window w of SB * FIPT
+// elements in ck[1 + w] (fold_search starts from them).
 template <class X>
-__device__ FoldRes block_fold(X x_at, int n, float s, float thr, int pmode, Small* sm, int seq = 0)
+__device__ FoldRes block_fold(X x_at, int n, float s, float thr, int pmode, Small* sm, int seq = 0,
+                              const float* head = nullptr, float* ck = nullptr)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     __syncthreads();
     if (tid < 4) (&sm->slot[0][0])[tid] = ~0ull;
     int start0 = 0;
-    if (seq > 0 && pmode == F_NONE) {
+    if (seq > 0) {
         start0 = seq < n ? seq : n;
         if (tid == 0) {
-            float t = s;
-#pragma unroll 16
-            for (int i = 0; i < start0; i++) t = t + x_at(i);
+            int hit = -1;
+            const float t = head ? head_fold([&](int i) { return head[i]; }, start0, s, thr, pmode, &hit)
+                                 : head_fold(x_at, start0, s, thr, pmode, &hit);
             sm->wf[0] = t;
+            sm->iv[5] = hit;
         }
         __syncthreads();
         s = sm->wf[0];
+        const int hit = sm->iv[5];
+        if (hit >= 0) return {s, hit};
     }
+    if (ck && tid == 0) ck[0] = s;
     __syncthreads();
-    int it = 0;
-    for (int start = start0; start < n; start += SB * FIPT) {
+    int it = 0, win = 0;
+    for (int start = start0; start < n; start += SB * FIPT, win++) {
         const int base = start + tid * FIPT;
         float xv[FIPT];
 #pragma unroll
@@ -355,6 +399,7 @@ __device__ FoldRes block_fold(X x_at, int n, float s, float thr, int pmode, Smal
             if (pr != ~0ull) return {__uint_as_float((uint32_t)pr), (int)(pr >> 32)};
             if (cr == ~0ull) {
                 s = f_make(eb, S0 + fsel(tot, S0));
+                if (ck && tid == 0) ck[1 + win] = s;
                 break;
             }
             const int ci = (int)(cr >> 32);
@@ -438,15 +483,27 @@ __device__ int block_count(Pred pred, int n, Small* sm)
     return (int)tot;
 }
 
-// smallest i < n with pred(i), or -1
+// smallest i < n with pred(i), or -1 (pred evaluated BU indices at a time,
+// at clamped indices, so that its loads are issued together)
 template <class Pred>
 __device__ int block_first(Pred pred, int n, Small* sm)
 {
     __syncthreads();
     if (threadIdx.x == 0) sm->iv[7] = 0x7fffffff;
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += SB)
-        if (pred(i)) { atomicMin(&sm->iv[7], i); break; }
+    int mine = 0x7fffffff;
+    for (int i0 = threadIdx.x; i0 < n && mine == 0x7fffffff; i0 += SB * BU) {
+        bool h[BU];
+#pragma unroll
+        for (int q = 0; q < BU; q++) {
+            const int i = i0 + q * SB;
+            h[q] = pred(i < n ? i : n - 1) && i < n;
+        }
+#pragma unroll
+        for (int q = BU - 1; q >= 0; q--)
+            if (h[q]) mine = i0 + q * SB;
+    }
+    if (mine != 0x7fffffff) atomicMin(&sm->iv[7], mine);
     __syncthreads();
     const int r = sm->iv[7];
     return r == 0x7fffffff ? -1 : r;
@@ -460,11 +517,69 @@ __device__ int block_last(Pred pred, int n, Small* sm)
     if (threadIdx.x == 0) sm->iv[6] = -1;
     __syncthreads();
     int mine = -1;
-    for (int i = threadIdx.x; i < n; i += SB)
-        if (pred(i)) mine = i;
+    for (int i0 = threadIdx.x; i0 < n; i0 += SB * BU) {
+        bool h[BU];
+#pragma unroll
+        for (int q = 0; q < BU; q++) {
+            const int i = i0 + q * SB;
+            h[q] = pred(i < n ? i : n - 1) && i < n;
+        }
+#pragma unroll
+        for (int q = 0; q < BU; q++)
+            if (h[q]) mine = i0 + q * SB;
+    }
     if (mine >= 0) atomicMax(&sm->iv[6], mine);
     __syncthreads();
     return sm->iv[6];
+}
+
+// Folds from 0 over values in candidate order (largest first) meet most of
+// their binade exits in the first elements: those go to the fold's
+// one-thread head, staged in LDS by the whole block first (the values may
+// gather, and one thread's loads from memory would wait one by one).  A
+// draw's two folds over the same values share the staging, and the search
+// starts at the last checkpoint of the total's fold below the target.
+struct FoldLds {
+    float head[FOLD_SEQ];
+    float ck[40];   // ck[0] after the head, ck[1 + w] after window w
+};
+static_assert((VMAX + SB * FIPT - 1) / (SB * FIPT) + 1 <= 40, "a checkpoint per fold window");
+
+template <class X>
+__device__ void stage_head(X x_at, int n, FoldLds* fl)
+{
+    const int ns = n < FOLD_SEQ ? n : FOLD_SEQ;
+    __syncthreads();
+    for (int i = threadIdx.x; i < ns; i += SB) fl->head[i] = x_at(i);
+    __syncthreads();
+}
+
+// the fold of x over n elements from 0, staged head first, with checkpoints
+template <class X>
+__device__ float staged_total(X x_at, int n, FoldLds* fl, Small* sm)
+{
+    stage_head(x_at, n, fl);
+    return block_fold(x_at, n, 0.0f, 0.0f, F_NONE, sm, FOLD_SEQ, fl->head, fl->ck).sum;
+}
+
+// the first prefix of the same fold meeting the predicate, from the last
+// checkpoint that does not (the prefixes are monotone: the values are >= 0
+// and f32 addition rounds monotonically)
+template <class X>
+__device__ FoldRes fold_search(X x_at, int n, float thr, int pmode, FoldLds* fl, Small* sm)
+{
+    __syncthreads();
+    const int ns = n < FOLD_SEQ ? n : FOLD_SEQ;
+    const int nw = (n - ns + SB * FIPT - 1) / (SB * FIPT);
+    int j = -1;
+    for (int c = 0; c <= nw && !fpred(pmode, fl->ck[c], thr); c++) j = c;
+    if (j < 0) return block_fold(x_at, n, 0.0f, thr, pmode, sm, FOLD_SEQ, fl->head);
+    const int p0 = ns + j * SB * FIPT;
+    const float c0 = fl->ck[j];
+    if (p0 >= n) return {c0, -1};
+    FoldRes r = block_fold([&](int i) { return x_at(p0 + i); }, n - p0, c0, thr, pmode, sm);
+    if (r.idx >= 0) r.idx += p0;
+    return r;
 }
 
 // ------------------------------------------------------------ candidate order
@@ -974,6 +1089,7 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
     extern __shared__ __align__(16) unsigned char sdyn[];
     unsigned long long* keys = (unsigned long long*)sdyn;
     Small* sm = (Small*)(sdyn + SAMPLE_LDS_KEYS);
+    FoldLds* fl = (FoldLds*)(sdyn + SAMPLE_LDS_KEYS + sizeof(Small));
     // the split top-p build: after rowmax_part_kernel and exp_kernel, in
     // phase 1 workgroup 2 r sums row r's exponentials in index order while
     // workgroup 2 r + 1 emits its first band (the two need nothing from each
@@ -1072,11 +1188,15 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
                                     continue;
                                 }
                             }
-                            sum1 = block_fold([&](int i) { return pr[i0 + i]; }, i1 - i0, sum1, 0.0f, F_NONE, sm,
-                                              part == 0 ? FOLD_SEQ : 0).sum;
+                            auto pv = [&](int i) { return pr[i0 + i]; };
+                            if (part == 0) stage_head(pv, i1 - i0, fl);
+                            sum1 = block_fold(pv, i1 - i0, sum1, 0.0f, F_NONE, sm, part == 0 ? FOLD_SEQ : 0,
+                                              fl->head).sum;
                         }
                     } else {
-                        sum1 = block_fold([&](int i) { return pr[i]; }, V, 0.0f, 0.0f, F_NONE, sm, FOLD_SEQ).sum;
+                        auto pv = [&](int i) { return pr[i]; };
+                        stage_head(pv, V, fl);
+                        sum1 = block_fold(pv, V, 0.0f, 0.0f, F_NONE, sm, FOLD_SEQ, fl->head).sum;
                     }
                     if (a.phase == 1) {
                         if (tid == 0) a.st[row].sum1 = sum1;
@@ -1125,7 +1245,10 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
                         }
                     }
                     const int32_t* band = sid + po;
-                    const FoldRes r = block_fold([&](int i) { return pr[band[i]] / sum1; }, pc, s, P.top_p, F_GE, sm);
+                    auto bv = [&](int i) { return pr[band[i]] / sum1; };
+                    const int seq = s == 0.0f ? FOLD_SEQ : 0;
+                    if (seq) stage_head(bv, pc, fl);
+                    const FoldRes r = block_fold(bv, pc, s, P.top_p, F_GE, sm, seq, fl->head);
                     if (r.idx >= 0) {
                         ifirst = po + r.idx;
                         break;
@@ -1138,7 +1261,10 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
             }
             while (cnt > 0) {
                 const int32_t* band = sid + emitted;
-                const FoldRes r = block_fold([&](int i) { return pr[band[i]] / sum1; }, cnt, s, P.top_p, F_GE, sm);
+                auto bv = [&](int i) { return pr[band[i]] / sum1; };
+                const int seq = s == 0.0f ? FOLD_SEQ : 0;
+                if (seq) stage_head(bv, cnt, fl);
+                const FoldRes r = block_fold(bv, cnt, s, P.top_p, F_GE, sm, seq, fl->head);
                 if (r.idx >= 0) ifirst = emitted + r.idx;
                 emitted += cnt;
                 if (r.idx >= 0) break;
@@ -1166,8 +1292,12 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
             const float l0 = sl[0];
             strided(n, [&](int i) { return sl[i]; }, [&](int i, float l) { pr[i] = cpv_expf(l - l0); });
             __syncthreads();
-            const float sA = block_fold([&](int i) { return pr[i]; }, n, 0.0f, 0.0f, F_NONE, sm).sum;
-            const FoldRes r = block_fold([&](int i) { return pr[i] / sA; }, n, 0.0f, P.top_p, F_GE, sm);
+            auto pv = [&](int i) { return pr[i]; };
+            stage_head(pv, n, fl);
+            const float sA = block_fold(pv, n, 0.0f, 0.0f, F_NONE, sm, FOLD_SEQ, fl->head).sum;
+            auto qv = [&](int i) { return pr[i] / sA; };
+            stage_head(qv, n, fl);
+            const FoldRes r = block_fold(qv, n, 0.0f, P.top_p, F_GE, sm, FOLD_SEQ, fl->head);
             if (r.idx >= 0) {
                 const int keep = r.idx + 1 > P.min_keep ? r.idx + 1 : P.min_keep;
                 if (keep <= n) n = keep;
@@ -1212,7 +1342,9 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
                     continue;
                 }
             }
-            s2 = block_fold([&](int i) { return e2[po + i]; }, len, s2, 0.0f, F_NONE, sm, po == 0 ? FOLD_SEQ : 0).sum;
+            auto ev = [&](int i) { return e2[po + i]; };
+            if (po == 0) stage_head(ev, len, fl);
+            s2 = block_fold(ev, len, s2, 0.0f, F_NONE, sm, po == 0 ? FOLD_SEQ : 0, fl->head).sum;
         }
         __syncthreads();
         strided(n, [&](int i) { return e2[i]; }, [&](int i, float e) { pr[i] = e / s2; });
@@ -1221,7 +1353,9 @@ __global__ __launch_bounds__(SB) void dist_kernel(DistArgs a)
     }
     strided(n, [&](int i) { return sl[i]; }, [&](int i, float l) { pr[i] = cpv_expf(l / T - mx2); });
     __syncthreads();
-    const float s2 = block_fold([&](int i) { return pr[i]; }, n, 0.0f, 0.0f, F_NONE, sm, FOLD_SEQ).sum;
+    auto pv2 = [&](int i) { return pr[i]; };
+    stage_head(pv2, n, fl);
+    const float s2 = block_fold(pv2, n, 0.0f, 0.0f, F_NONE, sm, FOLD_SEQ, fl->head).sum;
     __syncthreads();
     strided(n, [&](int i) { return pr[i]; }, [&](int i, float e) { pr[i] = e / s2; });
     if (tid == 0) a.hdr[row] = n;
@@ -1353,41 +1487,48 @@ __device__ __forceinline__ Row dist_row(const DecideArgs& a, int row)
 
 // Dist::draw (lib.rs:395-404): the first candidate whose cumulative
 // probability exceeds r, else the last
-__device__ int dist_draw(const Row& d, float r, Small* sm)
+__device__ int dist_draw(const Row& d, float r, Small* sm, FoldLds* fl)
 {
-    const FoldRes f = block_fold([&](int i) { return d.pr[i]; }, d.n, 0.0f, r, F_GT, sm);
+    auto pv = [&](int i) { return d.pr[i]; };
+    stage_head(pv, d.n, fl);
+    const FoldRes f = block_fold(pv, d.n, 0.0f, r, F_GT, sm, FOLD_SEQ, fl->head);
     return f.idx >= 0 ? d.sid[f.idx] : d.sid[d.n - 1];
 }
 
 // Dist::draw_excluding (lib.rs:408-436).  Adding 0 leaves an f32 sum
 // unchanged, so skipping x is folding it as 0.
-__device__ int dist_draw_excluding(const Row& d, int x, float r, Small* sm)
+__device__ int dist_draw_excluding(const Row& d, int x, float r, Small* sm, FoldLds* fl)
 {
     auto val = [&](int i) { return d.sid[i] == x ? 0.0f : d.pr[i]; };
-    const float total = block_fold(val, d.n, 0.0f, 0.0f, F_NONE, sm).sum;
-    if (total <= 0.0f) return dist_draw(d, r, sm);
+    const float total = staged_total(val, d.n, fl, sm);
+    if (total <= 0.0f) return dist_draw(d, r, sm, fl);
     const float target = r * total;
-    const FoldRes f = block_fold(val, d.n, 0.0f, target, F_GT, sm);
+    const FoldRes f = fold_search(val, d.n, target, F_GT, fl, sm);
     if (f.idx >= 0) return d.sid[f.idx];
     if (d.sid[d.n - 1] != x || d.n < 2) return d.sid[d.n - 1];
     return d.sid[d.n - 2];
 }
 
 // the general rule's residual max(0, p - q) over p's candidates in p's order
-__device__ int dist_draw_residual(const Row& p, const Row& q, float* qd, int V, float r, Small* sm)
+__device__ int dist_draw_residual(const Row& p, const Row& q, float* qd, int V, float r, Small* sm, FoldLds* fl)
 {
-    for (int i = threadIdx.x; i < V; i += SB) qd[i] = 0.0f;
+    if ((V & 3) == 0 && ((uintptr_t)qd & 15) == 0) {
+        for (int i = threadIdx.x; i < V / 4; i += SB) ((float4*)qd)[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    } else {
+        for (int i = threadIdx.x; i < V; i += SB) qd[i] = 0.0f;
+    }
     __syncthreads();
-    for (int i = threadIdx.x; i < q.n; i += SB) qd[q.sid[i]] = q.pr[i];
+    strided(q.n, [&](int i) { return make_int2(q.sid[i], __float_as_int(q.pr[i])); },
+            [&](int, int2 e) { qd[e.x] = __int_as_float(e.y); });
     __syncthreads();
     auto val = [&](int i) {
         const float d = p.pr[i] - qd[p.sid[i]];
         return d > 0.0f ? d : 0.0f;
     };
-    const float total = block_fold(val, p.n, 0.0f, 0.0f, F_NONE, sm).sum;
-    if (total <= 0.0f) return dist_draw(p, r, sm);
+    const float total = staged_total(val, p.n, fl, sm);
+    if (total <= 0.0f) return dist_draw(p, r, sm, fl);
     const float target = r * total;
-    const FoldRes f = block_fold(val, p.n, 0.0f, target, F_GT, sm);
+    const FoldRes f = fold_search(val, p.n, target, F_GT, fl, sm);
     if (f.idx >= 0) return p.sid[f.idx];
     const int l = block_last([&](int i) { return p.pr[i] - qd[p.sid[i]] > 0.0f; }, p.n, sm);
     return l >= 0 ? p.sid[l] : p.sid[p.n - 1];
@@ -1419,7 +1560,9 @@ __device__ __forceinline__ float uniform(const DecideArgs& a, int b, int j, int 
 __global__ __launch_bounds__(SB) void decide_kernel(DecideArgs a)
 {
     __shared__ Small sm_s;
+    __shared__ FoldLds fl_s;
     Small* sm = &sm_s;
+    FoldLds* fl = &fl_s;
     const int b = blockIdx.x, tid = threadIdx.x, K1 = a.k + 1, V = a.V;
     int n_keep = 0, rep = 0;
     bool have_rep = false;
@@ -1437,13 +1580,16 @@ __global__ __launch_bounds__(SB) void decide_kernel(DecideArgs a)
             const float px = pos >= 0 ? d.pr[pos] : 0.0f;
             if (!a.has_q) {
                 keep = u0 < px;
-                if (!keep) { rep = dist_draw_excluding(d, x, u1, sm); have_rep = true; }
+                if (!keep) { rep = dist_draw_excluding(d, x, u1, sm, fl); have_rep = true; }
             } else {
                 const Row q = dist_row(a, a.nrow_p + b * a.k + j);
                 const int qpos = block_first([&](int i) { return q.sid[i] == x; }, q.n, sm);
                 const float qx = qpos >= 0 ? q.pr[qpos] : 0.0f;
                 keep = u0 * qx < px;
-                if (!keep) { rep = dist_draw_residual(d, q, a.qdense + (size_t)b * V, V, u1, sm); have_rep = true; }
+                if (!keep) {
+                    rep = dist_draw_residual(d, q, a.qdense + (size_t)b * V, V, u1, sm, fl);
+                    have_rep = true;
+                }
             }
         }
         if (!keep) break;
@@ -1456,7 +1602,7 @@ __global__ __launch_bounds__(SB) void decide_kernel(DecideArgs a)
     } else {
         const Row d = dist_row(a, b * K1 + n_keep);
         if (a.mode == CPV_ACCEPT_GUMBEL) next = coupled_argmax(a, d, a.noise + ((size_t)b * K1 + n_keep) * V, sm);
-        else next = dist_draw(d, uniform(a, b, n_keep, 0), sm);
+        else next = dist_draw(d, uniform(a, b, n_keep, 0), sm, fl);
     }
     if (tid == 0) {
         a.out_tok[(size_t)b * K1 + n_keep] = next;
@@ -1552,7 +1698,7 @@ DistBufs dist_carve(void* ws, int rows, int V, bool pen)
 
 cpv_status dist_launch(cpv_ctx* ctx, DistArgs& a, int rows)
 {
-    const size_t lds = SAMPLE_LDS_KEYS + sizeof(Small);
+    const size_t lds = SAMPLE_LDS_KEYS + sizeof(Small) + sizeof(FoldLds);
     if (lds > ctx->lds_max) return cpv_fail(ctx, CPV_EUNSUPPORTED, "sampler: needs %zu bytes of LDS", lds);
     const int e0 = cpv_prof_mark(ctx);
     // top-p without penalties: the maximum and the exponentials over

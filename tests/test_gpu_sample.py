@@ -276,6 +276,27 @@ def test_reject_general_rule_with_draft_logits(ctx):
             same(got, ref)
 
 
+def test_reject_draws_deep_in_long_candidate_lists(ctx):
+    # near-flat target logits keep ~144k candidates at top-p 0.95, so the
+    # replacement draws' cumulative searches end anywhere from the first
+    # elements to the last of 18 fold windows (replacement uniforms from
+    # 0.001 to 0.999); random drafts are rejected, and with the draft
+    # distribution about half the residual terms are 0
+    print("case accept reject long lists", flush=True)
+    k, B = 4, 4
+    rng = np.random.default_rng(17)
+    pl = rng.normal(0, 0.05, size=(B, k + 1, V27)).astype(np.float32)
+    q = (pl[:, :k] + rng.normal(0, 0.05, size=(B, k, V27))).astype(np.float32)
+    draft = rng.integers(0, V27, size=(B, k)).astype(np.int32)
+    p = cpvo.SamplerParams(temp=0.7, top_p=0.95)
+    u = rng.random(size=(B, k + 1, 2)).astype(np.float32)
+    u[:, :, 1] = np.array([0.001, 0.3, 0.6, 0.999], dtype=np.float32)[:, None]
+    for ql in (None, q):
+        got = accept(ctx, pl, draft, p, cpvo.ACCEPT_REJECT, u=u, q=ql)
+        ref = cpvo.spec_accept(pl, draft, p, cpvo.ACCEPT_REJECT, u=u, q_logits=ql)
+        same(got, ref)
+
+
 def test_reject_penalty_window_grows_with_drafts(ctx):
     print("case accept reject penalties", flush=True)
     k, B, V = 4, 6, 5000
