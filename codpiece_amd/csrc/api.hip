@@ -733,15 +733,18 @@ __global__ __launch_bounds__(64) void argmax_fin_kernel(const unsigned long long
 }
 
 // softmax peak: each slice's sum of expf(x - max) in binary64 (max from the
-// argmax keys), then the row's slices added in order
+// argmax keys), then the row's slices added in order.  Every block reduces
+// the row's argmax keys itself; block 0 stores the row's argmax index, as
+// argmax_fin_kernel would
 __global__ __launch_bounds__(256) void peak_part_kernel(const float* __restrict__ x, int64_t n, int64_t chunk,
                                                         const unsigned long long* __restrict__ part,
-                                                        double* __restrict__ psum)
+                                                        double* __restrict__ psum, int32_t* __restrict__ idx_out)
 {
     __shared__ double s_d[4];
     const int64_t row = blockIdx.y, i0 = (int64_t)blockIdx.x * chunk;
     const int64_t i1 = i0 + chunk < n ? i0 + chunk : n;
     const unsigned long long k = cpv_wave_reduce(part[row * AM_NB + (threadIdx.x & 63)], cpv_op_umax());
+    if (blockIdx.x == 0 && threadIdx.x == 0) idx_out[row] = k ? (int32_t)(0xffffffffu - (uint32_t)k) : 0;
     const float mx = k ? am_value(k) : -INFINITY;
     const float* xr = x + row * n;
     double sum = 0.0;
@@ -780,10 +783,11 @@ cpv_status cpv_argmax_peak_rows(cpv_ctx* ctx, const float* x, const float* noise
     const int64_t chunk = (n + AM_NB - 1) / AM_NB;
     const dim3 grid(AM_NB, (unsigned)rows);
     argmax_part_kernel<<<grid, 256, 0, ctx->stream>>>(x, noise, n, chunk, part);
-    argmax_fin_kernel<<<(unsigned)rows, 64, 0, ctx->stream>>>(part, idx_out);
     if (peak_out) {
-        peak_part_kernel<<<grid, 256, 0, ctx->stream>>>(x, n, chunk, part, psum);
+        peak_part_kernel<<<grid, 256, 0, ctx->stream>>>(x, n, chunk, part, psum, idx_out);
         peak_fin_kernel<<<(unsigned)((rows + 63) / 64), 64, 0, ctx->stream>>>(psum, rows, peak_out);
+    } else {
+        argmax_fin_kernel<<<(unsigned)rows, 64, 0, ctx->stream>>>(part, idx_out);
     }
     CPV_HIP(ctx, hipGetLastError());
     return CPV_OK;

@@ -290,7 +290,7 @@ constexpr int RW = RB / 64;  // most waves
 constexpr int RUU = 3;       // most units per wave: rows up to 3 * 16 * 256 = 12288 elements
 constexpr int RQ = RUU * 4;  // most register slots per thread
 
-enum { SRC_X = 0, SRC_ADD = 1, SRC_SET = 2, SRC_GATE = 3, SRC_SWIGLU = 4, SRC_GATE_FOLD = 5 };
+enum { SRC_X = 0, SRC_ADD = 1, SRC_SET = 2, SRC_GATE = 3, SRC_SWIGLU = 4, SRC_GATE_FOLD = 5, SRC_CAT = 6 };
 constexpr int FOLD_MAX = 512;   // attention chunks a SRC_GATE_FOLD row kernel folds (contexts to 64k)
 
 struct RowArgs {
@@ -310,12 +310,18 @@ struct RowArgs {
     int64_t ys;
     int quant;             // quantize the row into act (0: no)
     cpv_act act;
+    // SRC_CAT: the row is [x row | x2 row], nseg elements each, each half
+    // RMS-normalized on its own (weights w and w2), as two rmsnorm_kernel rows
+    const float* x2;
+    int64_t xs2;
+    const float* w2;
+    int nseg;
 };
 
 // each block-wide reduction has its own LDS slots, so one barrier suffices
 struct RowLds {
-    float red_am[RW];
-    long long red_s[RW];
+    float red_am[RW], red_am2[RW];
+    long long red_s[RW], red_s2[RW];
 };
 
 __device__ float row_max(float v, float* slot, int nw)
@@ -366,11 +372,15 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
     // kept result's sums and row exponents, and the scales that give Ea
     float v[RQ], wv[RQ];
     const float* wsrc = a.w ? a.w : xr;
+    // SRC_CAT: a unit lies in one half (nseg is a multiple of 256)
+    auto in_hi = [&](int uu) { return SRC == SRC_CAT && e0[uu] >= a.nseg; };
 #pragma unroll
     for (int uu = 0; uu < RUU; uu++) {
-        const float4 xv = *(const float4*)(xr + e0[uu]);
-        const float4 ww = *(const float4*)(wsrc + e0[uu]);
-        const bool use_x = SRC == SRC_X || SRC == SRC_ADD;
+        const float* xp = in_hi(uu) ? a.x2 + (int64_t)m * a.xs2 + (e0[uu] - a.nseg) : xr + e0[uu];
+        const float* wp = in_hi(uu) ? a.w2 + (e0[uu] - a.nseg) : wsrc + e0[uu];
+        const float4 xv = *(const float4*)xp;
+        const float4 ww = *(const float4*)wp;
+        const bool use_x = SRC == SRC_X || SRC == SRC_ADD || SRC == SRC_CAT;
         v[uu * 4 + 0] = use_x ? xv.x : 0.0f;
         v[uu * 4 + 1] = use_x ? xv.y : 0.0f;
         v[uu * 4 + 2] = use_x ? xv.z : 0.0f;
@@ -433,30 +443,41 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
     };
     if (!a.norm) store_kept();
     if (a.norm) {
-        // exact fixed-point sum of the f32 squares, then ggml's f32 tail
-        float am = 0.0f;
+        // exact fixed-point sum of the f32 squares, then ggml's f32 tail, over
+        // the row (or over each half of a SRC_CAT row: hi selects the half)
+        auto norm_scale = [&](bool hi, int len, float* red_am, long long* red_s) {
+            float am = 0.0f;
 #pragma unroll
-        for (int j = 0; j < RQ; j++) am = fmaxf(am, fabsf(v[j]));
-        am = row_max(am, L.red_am, nw);
-        double sum = 0.0;
-        if (am > 0.0f) {
-            int e;
-            frexpf(am, &e);
-            const int g2 = 2 * e - (62 - ceil_log2_dev(n + 1));
-            long long S = 0;
+            for (int uu = 0; uu < RUU; uu++)
+                if (in_hi(uu) == hi)
 #pragma unroll
-            for (int j = 0; j < RQ; j++) S += cpv_fixed_floor(v[j] * v[j], g2);
-            sum = ldexp((double)row_sum(S, L.red_s, nw), g2);
-        }
-        const float mean = (float)(sum / (double)n);
-        const float scale = 1.0f / sqrtf(mean + a.eps);
+                    for (int k = 0; k < 4; k++) am = fmaxf(am, fabsf(v[uu * 4 + k]));
+            am = row_max(am, red_am, nw);
+            double sum = 0.0;
+            if (am > 0.0f) {
+                int e;
+                frexpf(am, &e);
+                const int g2 = 2 * e - (62 - ceil_log2_dev(len + 1));
+                long long S = 0;
+#pragma unroll
+                for (int uu = 0; uu < RUU; uu++)
+                    if (in_hi(uu) == hi)
+#pragma unroll
+                        for (int k = 0; k < 4; k++) S += cpv_fixed_floor(v[uu * 4 + k] * v[uu * 4 + k], g2);
+                sum = ldexp((double)row_sum(S, red_s, nw), g2);
+            }
+            const float mean = (float)(sum / (double)len);
+            return 1.0f / sqrtf(mean + a.eps);
+        };
+        const float scale = norm_scale(false, SRC == SRC_CAT ? a.nseg : n, L.red_am, L.red_s);
+        const float scale2 = SRC == SRC_CAT ? norm_scale(true, n - a.nseg, L.red_am2, L.red_s2) : scale;
         store_kept();
 #pragma unroll
         for (int uu = 0; uu < RUU; uu++)
 #pragma unroll
             for (int k = 0; k < 4; k++) {
                 const int j = uu * 4 + k;
-                const float tv = v[j] * scale;
+                const float tv = v[j] * (in_hi(uu) ? scale2 : scale);
                 v[j] = ok[uu] ? (a.w ? tv * wv[j] : tv) : 0.0f;   // padding stays 0
             }
     }
@@ -784,7 +805,7 @@ struct cpv_session {
     float* rope = nullptr;                // [n_ctx + 2][n_rot/2][2]
     // activations, max_batch rows
     float *x, *xn, *qg, *kk, *vv, *q, *att, *gated, *o, *up, *gt, *act, *h, *logits, *e, *cat, *d, *dsa;
-    float *mtp_logits, *hn, *hsrc;
+    float *mtp_logits, *hn;
     float *qkv, *gu;                      // outputs of the stacked q|k|v and gate|up GEMMs
     int32_t *tok, *preds, *chain;
     float* conf;
@@ -1060,7 +1081,6 @@ extern "C" cpv_status cpv_session_create(cpv_model* m, int64_t n_ctx, int32_t ma
     A((size_t)T * V * 4, (void**)&s->logits);
     A((size_t)T * V * 4, (void**)&s->mtp_logits);
     A((size_t)T * E * 4, (void**)&s->hn);
-    A((size_t)T * E * 4, (void**)&s->hsrc);
     A((size_t)T * E * 4, (void**)&s->e);
     A((size_t)T * 2 * E * 4, (void**)&s->cat);
     A((size_t)T * E * 4, (void**)&s->d);
@@ -1191,18 +1211,22 @@ cpv_status rmsnorm(cpv_ctx* ctx, const float* x, int64_t xs, const float* w, flo
 cpv_status row_launch(cpv_ctx* ctx, const RowArgs& a, int T)
 {
     const dim3 ugrid((unsigned)((a.n + 255) / 256), (unsigned)T);
-    if (a.src <= SRC_SET) {
+    const bool rowk = a.src <= SRC_SET || a.src == SRC_CAT;
+    if (rowk) {
         // row_kernel: 16-byte accesses of every row it reads or writes
         auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-        const bool kept = a.src != SRC_X;
+        const bool kept = a.src == SRC_ADD || a.src == SRC_SET;
         if (a.n % 4 || a.xs % 4 || !a.x || !al(a.x) || (a.w && !al(a.w)) || (a.y && (a.ys % 4 || !al(a.y))) ||
             (kept && (!al(a.g.acc) || a.g.n_pad % 4 || !al(a.g.ew))))
             return cpv_fail(ctx, CPV_EUNSUPPORTED, "row kernel: rows of %d need 16-byte aligned rows of a multiple of 4",
                             a.n);
+        if (a.src == SRC_CAT && (a.nseg % 256 || a.n != 2 * a.nseg || !a.w || !a.w2 || !al(a.w2) || !a.x2 ||
+                                 !al(a.x2) || a.xs2 % 4))
+            return cpv_fail(ctx, CPV_EUNSUPPORTED, "row kernel: halves of %d need whole units and both weights", a.nseg);
     }
     // row_kernel: the fewest units per wave that 16 waves cover, and the waves that many units need
     const int U = (a.n + 255) / 256, nu = (U + RW - 1) / RW, nt = 64 * ((U + nu - 1) / nu);
-    if (a.src <= SRC_SET && nu > RUU)
+    if (rowk && nu > RUU)
         return cpv_fail(ctx, CPV_EUNSUPPORTED, "row kernel: rows of %d exceed %d elements", a.n, RQ * RB);
     auto rows = [&](auto src) {
         constexpr int S = decltype(src)::value;
@@ -1214,6 +1238,7 @@ cpv_status row_launch(cpv_ctx* ctx, const RowArgs& a, int T)
     case SRC_X: rows(std::integral_constant<int, SRC_X>()); break;
     case SRC_ADD: rows(std::integral_constant<int, SRC_ADD>()); break;
     case SRC_SET: rows(std::integral_constant<int, SRC_SET>()); break;
+    case SRC_CAT: rows(std::integral_constant<int, SRC_CAT>()); break;
     case SRC_GATE: unit_kernel<SRC_GATE><<<ugrid, 256, 0, ctx->stream>>>(a); break;
     case SRC_GATE_FOLD:
         if (a.hd % 64 || 256 % a.hd || a.n % a.hd || a.part.nchunk > FOLD_MAX)
@@ -1644,10 +1669,30 @@ cpv_status round_body(cpv_session* s, int t, int depth, const float* noise_dev, 
         const int32_t* tok_src = s->preds;
         for (int step = 0; step < depth; step++) {
             if ((st = cpv_get_rows(ctx, m->mtp_embed, tok_src, t, s->e))) return st;
-            if ((st = rmsnorm(ctx, s->e, E, m->enorm, s->cat, 2 * E, t, (int)E, hp.rms_eps))) return st;
-            if ((st = rmsnorm(ctx, h_src, E, m->hnorm, s->cat + E, 2 * E, t, (int)E, hp.rms_eps))) return st;
             cpv_act act;
-            if ((st = cpv_quant_act(ctx, m->eh_proj->type, s->cat, t, 2 * E, next_act(s), &act))) return st;
+            if (2 * E <= (int64_t)RQ * RB && E % 256 == 0) {
+                // concat(enorm(e), hnorm(h)) normalized and quantized in one row kernel
+                RowArgs rc{};
+                rc.src = SRC_CAT;
+                rc.x = s->e;
+                rc.xs = E;
+                rc.x2 = h_src;
+                rc.xs2 = E;
+                rc.nseg = (int)E;
+                rc.n = (int)(2 * E);
+                rc.w = m->enorm;
+                rc.w2 = m->hnorm;
+                rc.norm = 1;
+                rc.eps = hp.rms_eps;
+                rc.quant = 1;
+                cpv_act_layout(m->eh_proj->type, t, 2 * E, next_act(s), &rc.act);
+                if ((st = row_launch(ctx, rc, t))) return st;
+                act = rc.act;
+            } else {
+                if ((st = rmsnorm(ctx, s->e, E, m->enorm, s->cat, 2 * E, t, (int)E, hp.rms_eps))) return st;
+                if ((st = rmsnorm(ctx, h_src, E, m->hnorm, s->cat + E, 2 * E, t, (int)E, hp.rms_eps))) return st;
+                if ((st = cpv_quant_act(ctx, m->eh_proj->type, s->cat, t, 2 * E, next_act(s), &act))) return st;
+            }
             cpv_gout eh;
             if ((st = cpv_qgemm_keep(ctx, m->eh_proj, &act, &eh))) return st;
             // positions rope_base + i + 1, rows mtp_past + i; only link 0 writes (:1858-1866, :2898-2906)
@@ -1669,9 +1714,9 @@ cpv_status round_body(cpv_session* s, int t, int depth, const float* noise_dev, 
                 map_cands_kernel<<<(unsigned)((t + 255) / 256), 256, 0, ctx->stream>>>(s->cand_idx, s->cand_dev, t, ids);
                 CPV_HIP(ctx, hipGetLastError());
             }
-            // the next link feeds on this link's prediction and hidden
-            CPV_HIP(ctx, hipMemcpyAsync(s->hsrc, s->hn, (size_t)t * E * 4, hipMemcpyDeviceToDevice, ctx->stream));
-            h_src = s->hsrc;
+            // the next link feeds on this link's prediction and hidden (read by its
+            // hnorm before its own head overwrites hn)
+            h_src = s->hn;
             tok_src = shortlist ? s->cand_idx : ids;
         }
     }
