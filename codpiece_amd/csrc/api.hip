@@ -724,6 +724,40 @@ __global__ __launch_bounds__(256) void argmax_part_kernel(const float* __restric
     if (threadIdx.x == 0) part[row * AM_NB + blockIdx.x] = best;
 }
 
+// argmax_part_kernel over a GEMM result kept in the accumulator: each entry
+// is finalized as qgemm_finalize_kernel does (and the accumulator cleared),
+// stored to y, then keyed; Ea of the row comes from a wave reduction per wave
+__global__ __launch_bounds__(256) void argmax_kept_part_kernel(cpv_gout g, const float* __restrict__ nz, int64_t chunk,
+                                                               float* __restrict__ y,
+                                                               unsigned long long* __restrict__ part)
+{
+    __shared__ unsigned long long s_k[4];
+    const int64_t n = g.n, row = blockIdx.y, i0 = (int64_t)blockIdx.x * chunk;
+    const int64_t i1 = i0 + chunk < n ? i0 + chunk : n;
+    const int lane = threadIdx.x & 63;
+    const float* dar = g.da + row * g.nda;
+    float mx = 0.0f;
+    for (int i = lane; i < g.nda; i += 64) mx = fmaxf(mx, fabsf(dar[i]));
+    const int ea = cpv_exp_of_max(cpv_wave_reduce(mx, cpv_op_max()));
+    double* acc = g.acc + row * g.n_pad;
+    float* yr = y + row * n;
+    const float* nr = nz ? nz + row * n : nullptr;
+    unsigned long long best = 0;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) {
+        const double S = acc[i];
+        acc[i] = 0.0;
+        const float x = cpv_gout_value(S, g.ew[i], ea, g.win);
+        yr[i] = x;
+        const float v = nr ? x + nr[i] : x;
+        if (v > -INFINITY) {
+            const unsigned long long k = am_key(v, i);
+            best = k > best ? k : best;
+        }
+    }
+    best = block_max_u64(best, s_k);
+    if (threadIdx.x == 0) part[row * AM_NB + blockIdx.x] = best;
+}
+
 __global__ __launch_bounds__(64) void argmax_fin_kernel(const unsigned long long* __restrict__ part,
                                                         int32_t* __restrict__ out)
 {
@@ -765,7 +799,7 @@ __global__ void peak_fin_kernel(const double* __restrict__ psum, int64_t rows, f
 }
 
 cpv_status cpv_argmax_peak_rows(cpv_ctx* ctx, const float* x, const float* noise, int64_t rows, int64_t n,
-                                int32_t* idx_out, float* peak_out)
+                                int32_t* idx_out, float* peak_out, const cpv_gout* kept)
 {
     const size_t need = (size_t)rows * AM_NB * 16;
     if (need > ctx->red_bytes) {
@@ -782,7 +816,8 @@ cpv_status cpv_argmax_peak_rows(cpv_ctx* ctx, const float* x, const float* noise
     double* psum = (double*)(part + rows * AM_NB);
     const int64_t chunk = (n + AM_NB - 1) / AM_NB;
     const dim3 grid(AM_NB, (unsigned)rows);
-    argmax_part_kernel<<<grid, 256, 0, ctx->stream>>>(x, noise, n, chunk, part);
+    if (kept) argmax_kept_part_kernel<<<grid, 256, 0, ctx->stream>>>(*kept, noise, chunk, const_cast<float*>(x), part);
+    else argmax_part_kernel<<<grid, 256, 0, ctx->stream>>>(x, noise, n, chunk, part);
     if (peak_out) {
         peak_part_kernel<<<grid, 256, 0, ctx->stream>>>(x, n, chunk, part, psum, idx_out);
         peak_fin_kernel<<<(unsigned)((rows + 63) / 64), 64, 0, ctx->stream>>>(psum, rows, peak_out);

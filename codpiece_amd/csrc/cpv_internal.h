@@ -333,9 +333,11 @@ cpv_status cpv_weight_concat(cpv_ctx* ctx, cpv_weight* const* parts, int np, cpv
 
 // Row argmax (first maximum, as cpv_argmax_rows) and, when peak_out is not
 // null, the softmax peak expf(0) * (float)(1 / sum_i expf(x_i - max)) of each
-// row (the sum in binary64), in two passes over 64 slices per row.
+// row (the sum in binary64), in two passes over 64 slices per row.  With
+// kept, the rows are first finalized from that kept GEMM result (n = kept->n)
+// into x, in the first pass.
 cpv_status cpv_argmax_peak_rows(cpv_ctx* ctx, const float* x, const float* noise, int64_t rows, int64_t n,
-                                int32_t* idx_out, float* peak_out);
+                                int32_t* idx_out, float* peak_out, const cpv_gout* kept = nullptr);
 
 // internal launchers
 cpv_status cpv_repack_launch(cpv_ctx* ctx, cpv_weight* w, const void* aos_dev);

@@ -1536,9 +1536,13 @@ cpv_status project(cpv_session* s, const cpv_weight* w, const float* x, int T, f
 
 // x (+ a kept result) -> RMS norm with w -> y (f32) and the input of head w_head,
 // whose logits go to logits
+// rms(x) with weight w into y, then the head's logits; with keep, the head's
+// result stays in the accumulator (*keep, for cpv_argmax_peak_rows to
+// finalize), else keep->acc is null and the logits are stored
 cpv_status norm_head(cpv_session* s, float* x, int T, const cpv_gout* pend, const float* w, float* y,
-                     const cpv_weight* w_head, float* logits)
+                     const cpv_weight* w_head, float* logits, cpv_gout* keep = nullptr)
 {
+    if (keep) keep->acc = nullptr;
     cpv_model* m = s->model;
     const cpv_hparams& hp = m->hp;
     if (hp.n_embd > (int64_t)RQ * RB) {     // rows too long for row_kernel (never with a kept result)
@@ -1560,6 +1564,7 @@ cpv_status norm_head(cpv_session* s, float* x, int T, const cpv_gout* pend, cons
     cpv_act_layout(w_head->type, T, hp.n_embd, next_act(s), &r.act);
     cpv_status st = row_launch(m->ctx, r, T);
     if (st != CPV_OK) return st;
+    if (keep) return cpv_qgemm_keep(m->ctx, w_head, &r.act, keep);
     return cpv_qgemm_act(m->ctx, w_head, &r.act, logits);
 }
 
@@ -1659,9 +1664,11 @@ cpv_status round_body(cpv_session* s, int t, int depth, const float* noise_dev, 
         pend = nxt;
     }
     // LM head and in-graph argmax (qwen35.rs:2788-2821)
-    if ((st = norm_head(s, s->x, t, pend.acc ? &pend : nullptr, m->output_norm, s->h, m->output, s->logits)))
+    cpv_gout hk;
+    if ((st = norm_head(s, s->x, t, pend.acc ? &pend : nullptr, m->output_norm, s->h, m->output, s->logits, &hk)))
         return st;
-    if ((st = cpv_argmax_rows(ctx, s->logits, noise_dev, t, V, s->preds))) return st;
+    if ((st = cpv_argmax_peak_rows(ctx, s->logits, noise_dev, t, V, s->preds, nullptr, hk.acc ? &hk : nullptr)))
+        return st;
     // fused MTP draft chain (qwen35.rs:2840-2962)
     if (depth > 0) {
         const LayerW& ML = m->layers[hp.n_layer];
@@ -1701,12 +1708,14 @@ cpv_status round_body(cpv_session* s, int t, int depth, const float* noise_dev, 
                 return st;
             // h_next = rms(d, shared_head_norm or output_norm), then the draft head,
             // over the shortlist when one is given (qwen35.rs:2925-2931)
+            cpv_gout mk;
             if ((st = norm_head(s, s->dsa, t, nxt.acc ? &nxt : nullptr, m->mtp_head_norm, s->hn,
-                                shortlist ? s->cand_head : m->mtp_head, s->mtp_logits)))
+                                shortlist ? s->cand_head : m->mtp_head, s->mtp_logits, &mk)))
                 return st;
             int32_t* ids = s->chain + (size_t)step * t;
             if ((st = cpv_argmax_peak_rows(ctx, s->mtp_logits, nullptr, t, shortlist ? n_cand : V,
-                                           shortlist ? s->cand_idx : ids, s->conf + (size_t)step * t)))
+                                           shortlist ? s->cand_idx : ids, s->conf + (size_t)step * t,
+                                           mk.acc ? &mk : nullptr)))
                 return st;
             if (shortlist) {
                 // drafts are candidates; the next link embeds the argmax itself, as the
@@ -1947,9 +1956,11 @@ extern "C" cpv_status cpv_verify_tree(cpv_session* s, const int32_t* tokens_dev,
             return st;
         pend = nxt;
     }
-    if ((st = norm_head(s, s->x, t, pend.acc ? &pend : nullptr, m->output_norm, s->h, m->output, s->logits)))
+    cpv_gout hk;
+    if ((st = norm_head(s, s->x, t, pend.acc ? &pend : nullptr, m->output_norm, s->h, m->output, s->logits, &hk)))
         return st;
-    if ((st = cpv_argmax_rows(ctx, s->logits, noise_dev, t, V, s->preds))) return st;
+    if ((st = cpv_argmax_peak_rows(ctx, s->logits, noise_dev, t, V, s->preds, nullptr, hk.acc ? &hk : nullptr)))
+        return st;
     s->tree_parent.assign(parent_host, parent_host + t);
     s->tree_base = s->n_past;
     s->n_past += t;
