@@ -246,9 +246,27 @@ __device__ __forceinline__ void gemm_unit(const v4i* pcu, uint16_t d6, int er, i
         }
     } else if constexpr (TYPE == CPV_Q6_K) {
         const double dws = ldexp((double)h2f(d6), -er);
+        // isum = sum_g sc_g * (dot_g - 32 * codesum_g); below 8 rows as
+        // sum_g sc_g * dot_g less 32 sum_g sc_g * codesum_g, the code-sum term
+        // first (the same integer: |terms| < 2^29; at 8 rows the registers
+        // for it would spill)
+        constexpr bool HOIST = MC < 8;
         int isum[MC];
 #pragma unroll
-        for (int m = 0; m < MC; m++) isum[m] = 0;
+        for (int m = 0; m < MC; m++) {
+            isum[m] = 0;
+            if constexpr (!HOIST) continue;
+            const v4i* bs = (const v4i*)(s_bs + (mrow[m] * U + u) * 16);
+            int t = 0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const v4i b = bs[q];
+                const uint32_t scw = (uint32_t)pcu[12][q];
+#pragma unroll
+                for (int e = 0; e < 4; e++) t += __mul24((int)(int8_t)byte_of(scw, e), b[e]);
+            }
+            isum[m] = -32 * t;
+        }
 #pragma unroll
         for (int hf = 0; hf < 2; hf++) {
 #pragma unroll
@@ -282,10 +300,14 @@ __device__ __forceinline__ void gemm_unit(const v4i* pcu, uint16_t d6, int er, i
                 const int sc1 = (int)(int8_t)byte_of((uint32_t)pcu[12][(g0 + 1) >> 2], (g0 + 1) & 3);
 #pragma unroll
                 for (int m = 0; m < MC; m++) {
-                    // int8 scales times |dot - 32 * code sum| < 2^18: 24-bit products
-                    const int32_t* bs = s_bs + (mrow[m] * U + u) * 16 + g0;
-                    isum[m] += __mul24(sc0, D0[m >> 2][m & 3] - 32 * bs[0]) +
-                               __mul24(sc1, D1[m >> 2][m & 3] - 32 * bs[1]);
+                    // int8 scales times |dot| and |dot - 32 * code sum| < 2^18: 24-bit products
+                    if constexpr (HOIST) {
+                        isum[m] += __mul24(sc0, D0[m >> 2][m & 3]) + __mul24(sc1, D1[m >> 2][m & 3]);
+                    } else {
+                        const int32_t* bs = s_bs + (mrow[m] * U + u) * 16 + g0;
+                        isum[m] += __mul24(sc0, D0[m >> 2][m & 3] - 32 * bs[0]) +
+                                   __mul24(sc1, D1[m >> 2][m & 3] - 32 * bs[1]);
+                    }
                 }
             }
         }
