@@ -85,6 +85,12 @@ class Session:
         self.h = h
         self.max_batch = max_batch
         self._tok = torch.empty(max_batch, dtype=torch.int32, device=self.ctx.torch_device)
+        # pinned host staging: the tokens go up and a round's ids and
+        # confidences come down asynchronously, with one wait per round
+        self._tok_h = torch.empty(max_batch, dtype=torch.int32, pin_memory=True)
+        self._ids_h = torch.empty(0, dtype=torch.int32, pin_memory=True)
+        self._conf_h = torch.empty(0, dtype=torch.float32, pin_memory=True)
+        self._tok_ev = None
 
     @property
     def pos(self):
@@ -125,9 +131,41 @@ class Session:
         return self.pos[1]
 
     def _tokens(self, tokens):
+        # the staging buffer is rewritten once the previous call's copy out of
+        # it has run (calls that do not wait for their results, such as
+        # prefill chunks, may still have it queued)
         t = len(tokens)
-        self._tok[:t].copy_(torch.as_tensor(np.asarray(tokens, dtype=np.int32)))
+        if self._tok_ev is not None:
+            self._tok_ev.synchronize()
+        self._tok_h[:t].numpy()[:] = np.asarray(tokens, dtype=np.int32)
+        with torch.cuda.stream(self.ctx.stream):
+            self._tok[:t].copy_(self._tok_h[:t], non_blocking=True)
+            self._tok_ev = torch.cuda.Event()
+            self._tok_ev.record(self.ctx.stream)
         return t
+
+    def _fetch_round(self, out, t, depth):
+        """The round's preds [t], chain [depth][t] and confidences [depth][t]
+        copied down on the stream, then one wait."""
+        n_ids = (1 + depth) * t
+        if self._ids_h.numel() < n_ids:
+            self._ids_h = torch.empty(n_ids, dtype=torch.int32, pin_memory=True)
+        if self._conf_h.numel() < max(depth * t, 1):
+            self._conf_h = torch.empty(max(depth * t, 1), dtype=torch.float32, pin_memory=True)
+        dev = self.ctx.torch_device
+        with torch.cuda.stream(self.ctx.stream):
+            self._ids_h[:t].copy_(_device_view(out.preds_dev, t, torch.int32, dev), non_blocking=True)
+            if depth:
+                self._ids_h[t:n_ids].copy_(_device_view(out.chain_dev, depth * t, torch.int32, dev),
+                                           non_blocking=True)
+                self._conf_h[:depth * t].copy_(_device_view(out.conf_dev, depth * t, torch.float32, dev),
+                                               non_blocking=True)
+        self.ctx.stream.synchronize()
+        ids = self._ids_h[:n_ids].tolist()
+        preds = ids[:t]
+        chain = [ids[t + l * t:t + (l + 1) * t] for l in range(depth)]
+        conf = self._conf_h[:depth * t].view(depth, t).tolist() if depth else []
+        return preds, chain, conf
 
     def prefill(self, tokens):
         t = self._tokens(tokens)
@@ -151,13 +189,7 @@ class Session:
                 self.h, ctypes.c_void_p(self._tok.data_ptr()), t, depth, nz,
                 c.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), int(c.size), ctypes.byref(out)))
         V, E = self.model.hp.n_vocab, self.model.hp.n_embd
-        preds = _device_view(out.preds_dev, t, torch.int32, self.ctx.torch_device).cpu().tolist()
-        chain = []
-        conf = []
-        if depth:
-            ch = _device_view(out.chain_dev, depth * t, torch.int32, self.ctx.torch_device).cpu().view(depth, t)
-            cf = _device_view(out.conf_dev, depth * t, torch.float32, self.ctx.torch_device).cpu().view(depth, t)
-            chain, conf = ch.tolist(), cf.tolist()
+        preds, chain, conf = self._fetch_round(out, t, depth)
         logits = hidden = None
         if want_logits:
             logits = _device_view(out.logits_dev, t * V, torch.float32, self.ctx.torch_device).view(t, V).clone()
