@@ -68,11 +68,12 @@ def test_qgemm_bit_exact_verify_shapes(ctx, tname, k, n, m):
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), np.abs(y - ref).max()
 
 
-@pytest.mark.parametrize("m", [5, 16])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 16])
 def test_qgemm_lm_head_q6_k(ctx, m):
     # the output projection of the 27B-class layout: Q6_K, K = 5120, a slice of
     # the 151,936 vocabulary rows (full vocab is covered by the e2e test); 16
-    # rows are a draft tree's
+    # rows are a draft tree's; below 8 rows the code-sum term is summed ahead
+    # of the group loop, at 8 inside it
     y, ref = run_case(ctx, cpvo.Q6_K, 4096, 5120, m)
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
 
