@@ -462,8 +462,10 @@ __global__ __launch_bounds__((64 * gemm_waves<TYPE, MC>())) void qgemm_kernel(Ge
     // then the weights: Q4_K and Q8_0 start with one item in flight and ask
     // for the next when the current one has arrived (a launch's first
     // requests then sit behind fewer bytes); Q6_K's longer units keep two in
-    // flight from the start
-    constexpr bool LEAN = TYPE != CPV_Q6_K;
+    // flight from the start below 4 rows and at 8 (the head: 104 us at one
+    // row either way; 4-7 rows lean, 118 -> 110 us at 5; 8 rows two in
+    // flight, 184 against 243 us)
+    constexpr bool LEAN = TYPE != CPV_Q6_K || (MC >= 4 && MC < 8);
     v4i bufA[F::PIECES], bufB[F::PIECES];
     uint16_t dA = 0, dB = 0;
     int eA = 0, eB = 0;
