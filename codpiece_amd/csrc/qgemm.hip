@@ -686,7 +686,10 @@ __global__ __launch_bounds__(512) void qgemm_q4k16_kernel(GemmArgs a)
 #pragma unroll
         for (int q = 0; q < 16; q++) {
             const int rb = q >> 2, pr = q & 3;
-            B.w[q] = *(const uint2*)(slab + (2 * pr + (g4 >> 1)) * 1024 + (16 * rb + c16) * 16 + 8 * (g4 & 1));
+            // (non-temporal: 95 -> 92 us per layer at 16 rows)
+            const unsigned long long wq = __builtin_nontemporal_load(
+                (const unsigned long long*)(slab + (2 * pr + (g4 >> 1)) * 1024 + (16 * rb + c16) * 16 + 8 * (g4 & 1)));
+            B.w[q] = make_uint2((uint32_t)wq, (uint32_t)(wq >> 32));
         }
         B.h = *(const uint4*)(slab + 8 * 1024 + lane * 16);
         B.er = a.ew[p.tile * 64 + lane];
