@@ -62,6 +62,14 @@ class RoundOut(ctypes.Structure):
     ]
 
 
+class DraftOut(ctypes.Structure):
+    """cpv_draft_out: one standalone draft link (Qwen35::mtp_draft, qwen35.rs:2086-2192)."""
+    _fields_ = [
+        ("logits_dev", ctypes.c_void_p), ("hidden_dev", ctypes.c_void_p), ("draft_dev", ctypes.c_void_p),
+        ("keep_dev", ctypes.c_void_p),
+    ]
+
+
 class GgufInfo(ctypes.Structure):
     """cpv_gguf_info: what GgufFile::open reads (crates/codpiece-gguf/src/lib.rs:345-458)."""
     _fields_ = [
@@ -126,6 +134,8 @@ SIGNATURES = {
     "cpv_verify_step": (_INT, [_P, _P, _INT, _INT, _P, ctypes.POINTER(RoundOut)]),
     "cpv_verify_step_cands": (_INT, [_P, _P, _INT, _INT, _P, ctypes.POINTER(ctypes.c_int32), _INT,
                                      ctypes.POINTER(RoundOut)]),
+    "cpv_mtp_draft": (_INT, [_P, _P, _I32, _I64, _F32, ctypes.POINTER(DraftOut)]),
+    "cpv_redraft_gate": (_INT, [_P, _P, _I64, _I64, _F32, _P, _P]),
     "cpv_verify_tree": (_INT, [_P, _P, ctypes.POINTER(ctypes.c_int32), _INT, _P, ctypes.POINTER(RoundOut)]),
     "cpv_session_commit_branch": (_INT, [_P, ctypes.POINTER(ctypes.c_int32), _INT]),
 }

@@ -79,9 +79,10 @@ extern "C" cpv_status cpv_init(int device, cpv_ctx** out)
     }
     c->stream = c->own_stream;
     if (cpv_noalloc_setup(c) != CPV_OK) {
-        (void)hipStreamDestroy(c->own_stream);
-        delete c;
-        return CPV_EDEVICE;
+        // only cpv_qgemm_noalloc uses the scratch, and it reports CPV_EDEVICE
+        // itself while ctx->scratch is null; the rest of the library works
+        c->scratch = nullptr;
+        (void)hipGetLastError();
     }
     *out = c;
     return CPV_OK;
@@ -798,10 +799,48 @@ __global__ void peak_fin_kernel(const double* __restrict__ psum, int64_t rows, f
     out[row] = 1.0f * (float)(1.0 / tot);
 }
 
-cpv_status cpv_argmax_peak_rows(cpv_ctx* ctx, const float* x, const float* noise, int64_t rows, int64_t n,
-                                int32_t* idx_out, float* peak_out, const cpv_gout* kept)
+// the re-draft gate's bound pass: each slice's S = sum of e_i = expf(x_i -
+// max) and W = sum of e_i (n - i), both in binary64 (max from the argmax
+// keys).  W bounds the rounding of the index-order f32 sum: every prefix of
+// that sum rounds with a relative error of at most 2^-24, and e_i is in the
+// n - i prefixes from i on.  Block 0 stores the row's argmax index.
+__global__ __launch_bounds__(256) void gate_part_kernel(const float* __restrict__ x, int64_t n, int64_t chunk,
+                                                        const unsigned long long* __restrict__ part,
+                                                        double* __restrict__ sw, int32_t* __restrict__ idx_out)
 {
-    const size_t need = (size_t)rows * AM_NB * 16;
+    __shared__ double s_d[4][2];
+    const int64_t row = blockIdx.y, i0 = (int64_t)blockIdx.x * chunk;
+    const int64_t i1 = i0 + chunk < n ? i0 + chunk : n;
+    const unsigned long long k = cpv_wave_reduce(part[row * AM_NB + (threadIdx.x & 63)], cpv_op_umax());
+    if (blockIdx.x == 0 && threadIdx.x == 0) idx_out[row] = k ? (int32_t)(0xffffffffu - (uint32_t)k) : 0;
+    const float mx = k ? am_value(k) : -INFINITY;
+    const float* xr = x + row * n;
+    double S = 0.0, W = 0.0;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) {
+        const double e = (double)cpv_expf(xr[i] - mx);
+        S += e;
+        W += e * (double)(n - i);
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        S += __shfl_xor(S, off);
+        W += __shfl_xor(W, off);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        s_d[threadIdx.x >> 6][0] = S;
+        s_d[threadIdx.x >> 6][1] = W;
+    }
+    __syncthreads();
+    if (threadIdx.x < 2) {
+        const int c = threadIdx.x;
+        sw[(row * AM_NB + blockIdx.x) * 2 + c] = (s_d[0][c] + s_d[1][c]) + (s_d[2][c] + s_d[3][c]);
+    }
+}
+
+// the reduction buffer for `rows` rows: argmax keys [rows][AM_NB], then
+// binary64 pairs [rows][AM_NB][2] (the peak's sums use the first half)
+static cpv_status reduce_buffer(cpv_ctx* ctx, int64_t rows, unsigned long long** keys, double** sums)
+{
+    const size_t need = (size_t)rows * AM_NB * 24;
     if (need > ctx->red_bytes) {
         CPV_HIP(ctx, hipStreamSynchronize(ctx->stream));
         if (ctx->red) (void)hipFree(ctx->red);
@@ -812,8 +851,40 @@ cpv_status cpv_argmax_peak_rows(cpv_ctx* ctx, const float* x, const float* noise
         ctx->red_bytes = bs;
         ctx->ws_gen++;
     }
-    unsigned long long* part = (unsigned long long*)ctx->red;
-    double* psum = (double*)(part + rows * AM_NB);
+    *keys = (unsigned long long*)ctx->red;
+    *sums = (double*)(*keys + rows * AM_NB);
+    return CPV_OK;
+}
+
+cpv_status cpv_argmax_gate_rows(cpv_ctx* ctx, const float* x, int64_t rows, int64_t n, int32_t* idx_out, float p_min,
+                                int32_t* keep_out, const cpv_gout* kept)
+{
+    unsigned long long* part;
+    double* sw;
+    cpv_status st = reduce_buffer(ctx, rows, &part, &sw);
+    if (st != CPV_OK) return st;
+    const int64_t chunk = (n + AM_NB - 1) / AM_NB;
+    const dim3 grid(AM_NB, (unsigned)rows);
+    if (kept) argmax_kept_part_kernel<<<grid, 256, 0, ctx->stream>>>(*kept, nullptr, chunk, const_cast<float*>(x), part);
+    else argmax_part_kernel<<<grid, 256, 0, ctx->stream>>>(x, nullptr, n, chunk, part);
+    CPV_HIP(ctx, hipGetLastError());
+    if (!(p_min > 0.0f)) {
+        argmax_fin_kernel<<<(unsigned)rows, 64, 0, ctx->stream>>>(part, idx_out);
+        CPV_HIP(ctx, hipGetLastError());
+        return keep_out ? cpv_gate_fin_launch(ctx, x, rows, n, idx_out, nullptr, 0, p_min, keep_out) : CPV_OK;
+    }
+    gate_part_kernel<<<grid, 256, 0, ctx->stream>>>(x, n, chunk, part, sw, idx_out);
+    CPV_HIP(ctx, hipGetLastError());
+    return cpv_gate_fin_launch(ctx, x, rows, n, idx_out, sw, AM_NB, p_min, keep_out);
+}
+
+cpv_status cpv_argmax_peak_rows(cpv_ctx* ctx, const float* x, const float* noise, int64_t rows, int64_t n,
+                                int32_t* idx_out, float* peak_out, const cpv_gout* kept)
+{
+    unsigned long long* part;
+    double* psum;
+    cpv_status st = reduce_buffer(ctx, rows, &part, &psum);
+    if (st != CPV_OK) return st;
     const int64_t chunk = (n + AM_NB - 1) / AM_NB;
     const dim3 grid(AM_NB, (unsigned)rows);
     if (kept) argmax_kept_part_kernel<<<grid, 256, 0, ctx->stream>>>(*kept, noise, chunk, const_cast<float*>(x), part);
@@ -826,6 +897,15 @@ cpv_status cpv_argmax_peak_rows(cpv_ctx* ctx, const float* x, const float* noise
     }
     CPV_HIP(ctx, hipGetLastError());
     return CPV_OK;
+}
+
+extern "C" cpv_status cpv_redraft_gate(cpv_ctx* ctx, const float* logits_dev, int64_t rows, int64_t v,
+                                       float p_min, int32_t* argmax_dev, int32_t* keep_dev)
+{
+    if (!ctx || !logits_dev || !argmax_dev || !keep_dev || rows < 0 || rows > 65535 || v <= 0 || v > 262144)
+        return cpv_fail(ctx, CPV_EINVAL, "redraft_gate: bad arguments");
+    if (rows == 0) return CPV_OK;
+    return cpv_argmax_gate_rows(ctx, logits_dev, rows, v, argmax_dev, p_min, keep_dev, nullptr);
 }
 
 extern "C" cpv_status cpv_argmax_rows(cpv_ctx* ctx, const float* x_dev, const float* noise_dev, int64_t rows,

@@ -339,6 +339,19 @@ cpv_status cpv_weight_concat(cpv_ctx* ctx, cpv_weight* const* parts, int np, cpv
 cpv_status cpv_argmax_peak_rows(cpv_ctx* ctx, const float* x, const float* noise, int64_t rows, int64_t n,
                                 int32_t* idx_out, float* peak_out, const cpv_gout* kept = nullptr);
 
+// Row argmax (first maximum) and the re-draft gate of each row: keep_out[r] =
+// 0 when p_min > 0 and 1 / lse < p_min, else 1, with lse the index-order f32
+// sum of expf(x_i - max) (engine.rs:2598-2606), decided exactly: a binary64
+// bound pass settles rows whose 1 / lse is clear of p_min by more than the f32
+// sum's rounding can move it, and the others run the sequential fold.  keep_out
+// may be null when p_min <= 0.  With kept, as cpv_argmax_peak_rows.
+cpv_status cpv_argmax_gate_rows(cpv_ctx* ctx, const float* x, int64_t rows, int64_t n, int32_t* idx_out, float p_min,
+                                int32_t* keep_out, const cpv_gout* kept = nullptr);
+// the gate's decision from the bound pass's pairs sw [rows][nb][2] (sw null:
+// every row keeps), the argmax idx giving each row's max (sample.hip)
+cpv_status cpv_gate_fin_launch(cpv_ctx* ctx, const float* x, int64_t rows, int64_t n, const int32_t* idx,
+                               const double* sw, int nb, float p_min, int32_t* keep_out);
+
 // internal launchers
 cpv_status cpv_repack_launch(cpv_ctx* ctx, cpv_weight* w, const void* aos_dev);
 // the V cache of a session as limbs: vq = rint(f16(v) 2^CPV_ATTN_VBITS)

@@ -824,6 +824,7 @@ struct cpv_session {
     int64_t cand_cap = 0;
     cpv_weight* cand_head = nullptr;      // the draft head's rows cand_host
     int32_t* cand_idx = nullptr;          // [max_batch] a link's argmax within the shortlist
+    int32_t* draft_io = nullptr;          // cpv_mtp_draft: the token in, then the draft and its gate out
     std::vector<void*> allocs;
     // round replay: the n_past and mtp_past of the call in flight in device
     // memory (the kernels that place rows read them there), and the rounds
@@ -1092,6 +1093,7 @@ extern "C" cpv_status cpv_session_create(cpv_model* m, int64_t n_ctx, int32_t ma
     A((size_t)2 * CPV_TREE_MAX * 4, (void**)&s->tree_dev);
     A(2 * sizeof(int64_t), (void**)&s->pos_dev);
     A((size_t)T * 4, (void**)&s->cand_idx);
+    A(4 * sizeof(int32_t), (void**)&s->draft_io);
     A((size_t)2 * hp.n_layer * sizeof(void*), (void**)&s->caches_dev);
     if (st == CPV_OK) {
         std::vector<void*> cp(2 * hp.n_layer);
@@ -1637,6 +1639,89 @@ cpv_status set_cands(cpv_session* s, const int32_t* cands, int n)
 }
 
 }  // namespace
+
+namespace {
+
+// a standalone draft link's inputs: its rope position and MTP row into the
+// session's device positions, its token into draft_io[0]
+__global__ void draft_setup_kernel(int64_t* __restrict__ pos, int64_t rope_pos, int64_t mtp_row,
+                                   int32_t* __restrict__ io, int32_t token)
+{
+    if (threadIdx.x == 0) {
+        pos[0] = rope_pos;
+        pos[1] = mtp_row;
+        io[0] = token;
+    }
+}
+
+}  // namespace
+
+extern "C" cpv_status cpv_mtp_draft(cpv_session* s, const float* hidden_dev, int32_t token, int64_t pos, float p_min,
+                                    cpv_draft_out* out)
+{
+    if (!s || !hidden_dev || !out) return cpv_fail(s ? s->model->ctx : nullptr, CPV_EINVAL, "mtp_draft: null argument");
+    cpv_model* m = s->model;
+    cpv_ctx* ctx = m->ctx;
+    const cpv_hparams& hp = m->hp;
+    const int64_t E = hp.n_embd, V = hp.n_vocab;
+    if (!hp.has_mtp) return cpv_fail(ctx, CPV_EINVAL, "mtp_draft: the model has no MTP head");
+    if (token < 0 || token >= V) return cpv_fail(ctx, CPV_EINVAL, "mtp_draft: token %d outside the vocabulary", token);
+    // the rope table covers positions 0 .. n_ctx + 1
+    if (pos < 0 || pos > s->n_ctx + 1) return cpv_fail(ctx, CPV_EINVAL, "mtp_draft: position %lld out of range", (long long)pos);
+    // the reference writes row mtp_past with no check (qwen35.rs:2177-2181);
+    // here a full MTP cache is an error
+    if (s->mtp_past + 1 > s->mtp_ctx)
+        return cpv_fail(ctx, CPV_EINVAL, "mtp_draft: the MTP cache is full (%lld rows)", (long long)s->mtp_ctx);
+    cpv_status st;
+    s->tap_off = 0;
+    draft_setup_kernel<<<1, 64, 0, ctx->stream>>>(s->pos_dev, pos, s->mtp_past, s->draft_io, token);
+    CPV_HIP(ctx, hipGetLastError());
+    if ((st = cpv_get_rows(ctx, m->mtp_embed, s->draft_io, 1, s->e))) return st;
+    cpv_act act;
+    if (2 * E <= (int64_t)RQ * RB && E % 256 == 0) {
+        RowArgs rc{};
+        rc.src = SRC_CAT;
+        rc.x = s->e;
+        rc.xs = E;
+        rc.x2 = hidden_dev;
+        rc.xs2 = E;
+        rc.nseg = (int)E;
+        rc.n = (int)(2 * E);
+        rc.w = m->enorm;
+        rc.w2 = m->hnorm;
+        rc.norm = 1;
+        rc.eps = hp.rms_eps;
+        rc.quant = 1;
+        cpv_act_layout(m->eh_proj->type, 1, 2 * E, next_act(s), &rc.act);
+        if ((st = row_launch(ctx, rc, 1))) return st;
+        act = rc.act;
+    } else {
+        if ((st = rmsnorm(ctx, s->e, E, m->enorm, s->cat, 2 * E, 1, (int)E, hp.rms_eps))) return st;
+        if ((st = rmsnorm(ctx, hidden_dev, E, m->hnorm, s->cat + E, 2 * E, 1, (int)E, hp.rms_eps))) return st;
+        if ((st = cpv_quant_act(ctx, m->eh_proj->type, s->cat, 1, 2 * E, next_act(s), &act))) return st;
+    }
+    cpv_gout eh, nxt;
+    if ((st = cpv_qgemm_keep(ctx, m->eh_proj, &act, &eh))) return st;
+    // the MTP layer: K/V written at row mtp_past, rows 0..mtp_past attended
+    // (mtp_graph.rs:179-195 via build_attn_block), rope position pos
+    if ((st = block(s, m->layers[hp.n_layer], s->dsa, 1, pos, s->mtp_past, s->mtp_past, s->kc[hp.n_layer],
+                    s->vt[hp.n_layer], s->mtp_v_stride, true, &eh, SRC_SET, &nxt, PosSel{1, 0})))
+        return st;
+    // h_out = rms(cur, shared_head_norm or output_norm), then the head (mtp_graph.rs:218-245)
+    cpv_gout mk;
+    if ((st = norm_head(s, s->dsa, 1, nxt.acc ? &nxt : nullptr, m->mtp_head_norm, s->hn, m->mtp_head, s->mtp_logits,
+                        &mk)))
+        return st;
+    if ((st = cpv_argmax_gate_rows(ctx, s->mtp_logits, 1, V, s->draft_io + 1, p_min, s->draft_io + 2,
+                                   mk.acc ? &mk : nullptr)))
+        return st;
+    s->mtp_past += 1;
+    out->logits_dev = s->mtp_logits;
+    out->hidden_dev = s->hn;
+    out->draft_dev = s->draft_io + 1;
+    out->keep_dev = s->draft_io + 2;
+    return CPV_OK;
+}
 
 extern "C" cpv_status cpv_verify_step(cpv_session* s, const int32_t* tokens_dev, int t, int depth,
                                       const float* noise_dev, cpv_round_out* out)

@@ -1731,7 +1731,69 @@ cpv_status dist_launch(cpv_ctx* ctx, DistArgs& a, int rows)
     return CPV_OK;
 }
 
+// The re-draft gate's decision for row blockIdx.x: 1 / lse < p_min, lse the
+// index-order f32 sum of e_i = expf(x_i - max) (engine.rs:2598-2606; the CLI
+// spec path's softmax_prob at the argmax, crates/codpiece-cli/src/main.rs:
+// 946-954, is the same value).  The bound pass gives S = sum e_i and W =
+// sum e_i (n - i) in binary64.  The f32 loop's k-th add rounds its prefix by
+// at most 2^-24 relative and carries the earlier errors with factors (1 +
+// 2^-24) at most n times, so |lse - S| <= 2^-24 (1 + 2^-24)^n W, and for n <=
+// 2^18 (a factor below 1.016), B = 0x1.1p-24 W + 2^-40 S covers it (the
+// 2^-40 S for the binary64 sums themselves, each term of which passes
+// through fewer than 2^7 adds).  1 / lse then lies in [1 / (S + B), 1 / (S - B)]: below
+// p (1 - 2^-23) it rounds to an f32 below p_min, and from p_min up it rounds
+// to p_min or above.  Rows in between run the sequential fold (block_fold
+// over the same e_i, bit-identical to the loop).  A sum that is not finite and
+// at least 1 (a NaN, or no finite logit) makes 1 / lse a NaN or 0 in the
+// reference; it keeps the draft on NaN, as a NaN compares false.
+__global__ __launch_bounds__(SB) void gate_fin_kernel(const float* __restrict__ x, int n,
+                                                      const int32_t* __restrict__ idx, const double* __restrict__ sw,
+                                                      int nb, float p_min, int32_t* __restrict__ keep)
+{
+    __shared__ Small sm;
+    __shared__ int s_dec;
+    const int64_t row = blockIdx.x;
+    const float* xr = x + row * (int64_t)n;
+    if (threadIdx.x == 0) {
+        int dec = 1;
+        if (sw && p_min > 0.0f) {
+            double S = 0.0, W = 0.0;
+            for (int b = 0; b < nb; b++) {
+                S += sw[(row * nb + b) * 2];
+                W += sw[(row * nb + b) * 2 + 1];
+            }
+            if (S >= 1.0 && S < 1e30) {
+                const double B = 0x1.1p-24 * W + 0x1p-40 * S;
+                const double rmax = 1.0 / (S - B), rmin = 1.0 / (S + B);
+                const double p = (double)p_min;
+                if (rmax * (1.0 + 0x1p-40) < p * (1.0 - 0x1p-23)) dec = 0;
+                else if (rmin * (1.0 - 0x1p-40) >= p) dec = 1;
+                else dec = 2;
+            }
+        }
+        s_dec = dec;
+    }
+    __syncthreads();
+    int dec = s_dec;
+    if (dec == 2) {
+        const float m = xr[idx[row]];
+        const FoldRes r = block_fold([&](int i) { return cpv_expf(xr[i] - m); }, n, 0.0f, 0.0f, F_NONE, &sm, FOLD_SEQ);
+        const float g = 1.0f / r.sum;
+        dec = g < p_min ? 0 : 1;
+    }
+    if (threadIdx.x == 0) keep[row] = dec;
+}
+
 }  // namespace
+
+cpv_status cpv_gate_fin_launch(cpv_ctx* ctx, const float* x, int64_t rows, int64_t n, const int32_t* idx,
+                               const double* sw, int nb, float p_min, int32_t* keep_out)
+{
+    if (n > VMAX) return cpv_fail(ctx, CPV_EUNSUPPORTED, "redraft gate: rows longer than %d", VMAX);
+    gate_fin_kernel<<<(unsigned)rows, SB, 0, ctx->stream>>>(x, (int)n, idx, sw, nb, p_min, keep_out);
+    CPV_HIP(ctx, hipGetLastError());
+    return CPV_OK;
+}
 
 extern "C" cpv_status cpv_distribution(cpv_ctx* ctx, const float* logits_dev, int rows, int v,
                                        const cpv_sampler_params* params, const int32_t* hist_dev, int hist_len,

@@ -17,7 +17,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import CpvError, Hparams, RoundOut
+from ._lib import CpvError, DraftOut, Hparams, RoundOut
 
 
 def make_hparams(n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, n_rot=None,
@@ -75,6 +75,19 @@ class FusedOut:
     conf: list = field(default_factory=list)    # [depth][t]
     logits: object = None                       # torch [t][V] on the device, when wanted
     hidden: object = None                       # torch [t][E] on the device, when wanted
+
+
+@dataclass
+class DraftResult:
+    """One standalone draft link: the draft (argmax), the gate's verdict, the
+    link's hidden row as a device pointer for the next link (session memory,
+    valid until the session's next call), and, when asked, copies of the
+    logits and hidden."""
+    draft: int
+    keep: bool
+    hidden_ptr: int
+    logits: object = None
+    hidden: object = None
 
 
 class Session:
@@ -170,6 +183,36 @@ class Session:
     def prefill(self, tokens):
         t = self._tokens(tokens)
         self.ctx._check(self.ctx.lib.cpv_prefill(self.h, ctypes.c_void_p(self._tok.data_ptr()), t))
+
+    def mtp_draft(self, hidden, token, pos, p_min=0.0, want=False):
+        """Qwen35::mtp_draft (qwen35.rs:2086-2192): one draft link from the
+        hidden row `hidden` (a cuda tensor of n_embd floats, or the device
+        pointer of a previous link's hidden_ptr) and `token` at rope position
+        `pos`; mtp_past advances by 1.  The gate is the re-draft's softmax-peak
+        test at p_min (engine.rs:2598-2606; 0 = no gate)."""
+        if isinstance(hidden, torch.Tensor):
+            assert hidden.is_cuda and hidden.dtype == torch.float32 and hidden.numel() == self.model.hp.n_embd
+            hidden = hidden.contiguous()
+            hp = hidden.data_ptr()
+        else:
+            hp = int(hidden)
+        out = DraftOut()
+        self.ctx._check(self.ctx.lib.cpv_mtp_draft(self.h, ctypes.c_void_p(hp), int(token), int(pos), float(p_min),
+                                                   ctypes.byref(out)))
+        if self._ids_h.numel() < 2:
+            self._ids_h = torch.empty(16, dtype=torch.int32, pin_memory=True)
+        dev = self.ctx.torch_device
+        with torch.cuda.stream(self.ctx.stream):
+            self._ids_h[:1].copy_(_device_view(out.draft_dev, 1, torch.int32, dev), non_blocking=True)
+            self._ids_h[1:2].copy_(_device_view(out.keep_dev, 1, torch.int32, dev), non_blocking=True)
+        self.ctx.stream.synchronize()
+        d, k = self._ids_h[:2].tolist()
+        logits = hid = None
+        if want:
+            V, E = self.model.hp.n_vocab, self.model.hp.n_embd
+            logits = _device_view(out.logits_dev, V, torch.float32, dev).clone()
+            hid = _device_view(out.hidden_dev, E, torch.float32, dev).clone()
+        return DraftResult(int(d), bool(k), int(out.hidden_dev), logits, hid)
 
     def step_fused_cached(self, tokens, depth, want_logits=False, noise=None, cands=None):
         """Verify `tokens` and chain `depth` drafts; greedy in-graph argmax,
@@ -268,6 +311,8 @@ class FusedStats:
     rounds: int
     prefill_s: float = 0.0
     decode_s: float = 0.0
+    redraft_rounds: int = 0     # rounds after which the drafts were re-drafted (sampled loop)
+    redraft_links: int = 0      # standalone draft links run (each advances mtp_past)
 
 
 def fused_generate(session, prompt, n_gen, depth, tail=64, bulk=512, timer=None, drafter=None):
@@ -327,8 +372,107 @@ def _penalties_on(p):
     return p.penalty_last_n > 0 and (p.penalty_repeat != 1.0 or p.penalty_freq != 0.0 or p.penalty_present != 0.0)
 
 
+def redraft(session, hidden, token, n_links, p_min, give_back=False):
+    """Draft links from `hidden` and `token` at rope position n_past, chained
+    on the drafts and the links' own hiddens, until n_links or the gate stops
+    one (engine.rs:2584-2625; the CLI spec path, crates/codpiece-cli/src/
+    main.rs:1052-1089, also gives the stopped link's MTP row back).  Returns
+    (drafts, links run)."""
+    drafts = []
+    pos = session.pos[0]
+    h, tok = hidden, token
+    links = 0
+    for _ in range(n_links):
+        r = session.mtp_draft(h, tok, pos, p_min)
+        links += 1
+        if not r.keep:
+            if give_back:
+                n_past, mtp_past = session.pos
+                session.set_pos(n_past, mtp_past - 1)
+            break
+        drafts.append(r.draft)
+        tok, h = r.draft, r.hidden_ptr
+        pos += 1
+    return drafts, links
+
+
+def spec_generate(session, prompt, n_gen, n_spec=1, p_min=0.75, tail=64, bulk=512):
+    """cmd_spec (crates/codpiece-cli/src/main.rs:956-1180) without the context
+    oracle (--oracle 0, its default) and without EOS: the prompt through the
+    trunk (bulk prefill, then the last `tail` tokens as a verify-only round
+    for the last row's argmax and hidden), then rounds of: up to n_spec
+    standalone draft links from the last committed token and hidden, stopped
+    (and the link's MTP row given back) at the first below p_min; a
+    verify-only round of [last] + drafts; greedy acceptance; the rejected
+    drafts rewound from n_past and mtp_past.  Returns (committed, FusedStats)."""
+    import time
+    t0 = time.perf_counter()
+    split = max(0, len(prompt) - tail)
+    bulk = min(bulk, getattr(session, "max_batch", bulk))
+    for c in range(0, split, bulk):
+        session.prefill(prompt[c:min(split, c + bulk)])
+    out = session.step_fused_cached(prompt[split:], 0, want_logits=True)
+    at = len(out.preds) - 1
+    committed = [out.preds[at]]
+    hidden = out.hidden[at]
+    t1 = time.perf_counter()
+    accepted = proposed = rounds = links = 0
+    while len(committed) < n_gen:
+        last = committed[-1]
+        drafts, nl = redraft(session, hidden, last, n_spec, p_min, give_back=True)
+        links += nl
+        batch = [last] + drafts
+        out = session.step_fused_cached(batch, 0, want_logits=True)
+        rounds += 1
+        proposed += len(drafts)
+        keep = 0
+        while keep < len(drafts) and out.preds[keep] == drafts[keep]:
+            keep += 1
+        accepted += keep
+        done = False
+        for d in drafts[:keep]:
+            committed.append(d)
+            if len(committed) >= n_gen:
+                done = True
+                break
+        if done:
+            break
+        committed.append(out.preds[keep])
+        hidden = out.hidden[keep]
+        extra = len(drafts) - keep
+        if extra:
+            n_past, mtp_past = session.pos
+            session.set_pos(n_past - extra, mtp_past - extra)
+    t2 = time.perf_counter()
+    return committed, FusedStats(accepted, proposed, rounds, t1 - t0, t2 - t1, 0, links)
+
+
+def mtp_probe(session, prompt, n_gen, tail=64, bulk=512):
+    """cmd_mtp_probe (crates/codpiece-cli/src/main.rs:1205-1293) without EOS:
+    plain greedy decoding one token per verify-only step, with one standalone
+    draft link per step predicting the token after next.  Returns (the greedy
+    stream, hits, total): how often the link's draft was the next token."""
+    split = max(0, len(prompt) - tail)
+    bulk = min(bulk, getattr(session, "max_batch", bulk))
+    for c in range(0, split, bulk):
+        session.prefill(prompt[c:min(split, c + bulk)])
+    out = session.step_fused_cached(prompt[split:], 0, want_logits=True)
+    at = len(out.preds) - 1
+    nxt, hidden = out.preds[at], out.hidden[at]
+    stream, drafted, hits, total = [nxt], None, 0, 0
+    for _ in range(n_gen):
+        if drafted is not None:
+            total += 1
+            hits += int(drafted == nxt)
+        drafted = session.mtp_draft(hidden, nxt, session.pos[0]).draft
+        out = session.step_fused_cached([nxt], 0, want_logits=True)
+        nxt, hidden = out.preds[0], out.hidden[0]
+        stream.append(nxt)
+    return stream, hits, total
+
+
 def sampled_generate(session, prompt, n_gen, depth, params, mode=_lib.ACCEPT_REJECT, seed=0, tail=64, bulk=512,
-                     noise=None, chain_pmin=0.0, drafter=None):
+                     noise=None, chain_pmin=0.0, drafter=None, redraft_depth=3, redraft_pmin=0.75):
     """The engine's sampled speculative loop for one request (crates/codpiece-
     server/src/engine.rs), at a fixed draft depth, without EOS, stop strings,
     JSON or forced tokens:
@@ -347,7 +491,15 @@ def sampled_generate(session, prompt, n_gen, depth, params, mode=_lib.ACCEPT_REJ
       * the next drafts are the chain at n_keep, cut at the first link whose
         confidence is below chain_pmin (:2508-2517), and dropped when the next
         token is not the trunk's argmax there (:2527-2529); the rejected rows
-        are rewound (:2533-2540).
+        are rewound (:2533-2540);
+      * when no draft is left, up to redraft_depth standalone draft links run
+        from the trunk's hidden at n_keep and the next token, at rope position
+        n_past, each kept while its softmax peak is at least redraft_pmin
+        (the post-commit re-draft, :2584-2625; the engine's defaults,
+        CODPIECE_REDRAFT = 3 and CODPIECE_REDRAFT_PMIN = 0.75, :2162-2185),
+        cut to `depth`.  Every link run advances mtp_past, the stopped one
+        included.  redraft_depth 0 turns it off; an external drafter (the
+        engine's DFlash mode) has none.
     Randomness is explicit: the reference's sequential xoshiro stream becomes
     Philox4x64-10 uniforms by role, round r (the tail round is 0) using key
     (seed + r, 0) with counter (0, j, role, 0).  In GUMBEL mode noise(r, rows)
@@ -389,7 +541,7 @@ def sampled_generate(session, prompt, n_gen, depth, params, mode=_lib.ACCEPT_REJ
     if drafter is not None:
         drafts = list(drafter(committed, drafts))
     t1 = time.perf_counter()
-    accepted = proposed = rounds = 0
+    accepted = proposed = rounds = re_rounds = re_links = 0
     while len(committed) < n_gen:
         rounds += 1
         batch = [nxt] + drafts
@@ -422,9 +574,14 @@ def sampled_generate(session, prompt, n_gen, depth, params, mode=_lib.ACCEPT_REJ
         over = len(batch) - (keep + 1)
         n_past, mtp_past = session.pos
         session.set_pos(n_past - over, mtp_past + keep + 1)
+        if not drafts and redraft_depth > 0 and drafter is None:
+            drafts, nl = redraft(session, out.hidden[keep], nxt, redraft_depth, redraft_pmin)
+            drafts = drafts[:depth]
+            re_rounds += 1
+            re_links += nl
     t2 = time.perf_counter()
-    return committed, FusedStats(accepted, proposed, rounds, t1 - t0, t2 - t1)
+    return committed, FusedStats(accepted, proposed, rounds, t1 - t0, t2 - t1, re_rounds, re_links)
 
 
-__all__ = ["Model", "Session", "FusedOut", "FusedStats", "make_hparams", "fused_generate", "sampled_generate",
-           "CpvError"]
+__all__ = ["Model", "Session", "FusedOut", "FusedStats", "DraftResult", "make_hparams", "fused_generate",
+           "sampled_generate", "spec_generate", "mtp_probe", "redraft", "CpvError"]

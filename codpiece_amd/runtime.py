@@ -119,6 +119,17 @@ class Context:
         self._check(self.lib.cpv_argmax_rows(self.h, _ptr(x), _ptr(noise), rows, n, _ptr(out)))
         return out
 
+    def redraft_gate(self, logits, p_min):
+        """cpv_redraft_gate over logits [rows][v]: (argmax [rows], keep [rows])
+        int32 device tensors; keep = 0 where the softmax peak 1 / lse is below
+        p_min (lse the index-order f32 sum, engine.rs:2598-2606)."""
+        logits = logits.contiguous()
+        rows, v = logits.shape
+        am = torch.empty(rows, dtype=torch.int32, device=logits.device)
+        keep = torch.empty(rows, dtype=torch.int32, device=logits.device)
+        self._check(self.lib.cpv_redraft_gate(self.h, _ptr(logits), rows, v, float(p_min), _ptr(am), _ptr(keep)))
+        return am, keep
+
     def attn(self, q, k_cache, v_cache_t, n_past, parent, h_kv, scale, out=None):
         """q [t][h][d] f32; k_cache [n_ctx][h_kv*d] and v_cache_t [h_kv*d][v_stride], 16-bit tensors."""
         t, h, d = q.shape

@@ -312,6 +312,37 @@ cpv_status  cpv_verify_step_cands(cpv_session* s, const int32_t* tokens_dev, int
                                   const float* noise_dev, const int32_t* cands_host, int n_cand,
                                   cpv_round_out* out);
 
+/* One standalone draft link: Qwen35::mtp_draft (qwen35.rs:2086-2192), whose
+ * graph is build_mtp_impl (mtp_graph.rs:123-249).  From the trunk's normed
+ * hidden row hidden_dev [n_embd] (a row of cpv_round_out.hidden_dev, or the
+ * previous link's hidden_dev) and `token`, the token at the position after
+ * that row: rms(embed(token)) * enorm ; rms(hidden) * hnorm, eh_proj, the MTP
+ * layer at rope position `pos` with its K/V written at MTP row mtp_past and
+ * rows 0..mtp_past attended, then rms with the head norm (the next link's
+ * hidden) and the draft head.  mtp_past advances by 1, as in the reference
+ * (:2189).  Also on the device: the draft, argmax of the logits with the first
+ * maximum winning (the host argmax, qwen35.rs:3659-3669), and the confidence
+ * gate of the engine's re-draft (crates/codpiece-server/src/engine.rs:
+ * 2598-2606) and of the CLI spec path (crates/codpiece-cli/src/main.rs:
+ * 1066-1069): keep = 0 when p_min > 0 and 1 / lse < p_min, lse the f32 sum in
+ * index order of exp(l - max), decided exactly; else keep = 1.  Outputs are
+ * session-owned device memory, valid until the session's next call.
+ * 0 <= pos <= n_ctx + 1; a full MTP cache (mtp_past = min(n_ctx, 16384)) is
+ * an error, where the reference would write past it. */
+typedef struct {
+    float*   logits_dev;    /* [n_vocab] the draft head's logits */
+    float*   hidden_dev;    /* [n_embd] the link's hidden for the next link */
+    int32_t* draft_dev;     /* [1] argmax of logits_dev */
+    int32_t* keep_dev;      /* [1] the gate: 1 = keep the draft, 0 = stop */
+} cpv_draft_out;
+cpv_status  cpv_mtp_draft(cpv_session* s, const float* hidden_dev, int32_t token, int64_t pos, float p_min,
+                          cpv_draft_out* out);
+
+/* The argmax and the re-draft gate of cpv_mtp_draft for `rows` logit rows
+ * [rows][v] (v <= 262144): argmax_dev [rows], keep_dev [rows] as above. */
+cpv_status  cpv_redraft_gate(cpv_ctx* ctx, const float* logits_dev, int64_t rows, int64_t v, float p_min,
+                             int32_t* argmax_dev, int32_t* keep_dev);
+
 /* ---- draft trees ----------------------------------------------------------
  * No counterpart in the reference: its rounds verify a linear draft and rewind
  * the rejected tail (crates/codpiece-server/src/engine.rs:2533-2540,

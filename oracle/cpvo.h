@@ -154,6 +154,12 @@ float    cpvo_dist_peak(const float* probs, int n);
 int32_t  cpvo_sample_coupled(const cpvo_sampler_params* p, const float* logits, int V,
                              const int32_t* hist, int n_hist, const float* noise_t);
 int32_t  cpvo_argmax(const float* x, int64_t n);
+/* The draft gate of the engine's post-commit re-draft (crates/codpiece-server/
+ * src/engine.rs:2598-2606) and of the CLI spec path (softmax_prob at the
+ * argmax, crates/codpiece-cli/src/main.rs:946-954, 1066-1069): 1 / lse with
+ * lse = sum over i, in index order, of exp(l_i - max) in f32 (max the f32::max
+ * fold from -inf).  The caller compares it with p_min. */
+float    cpvo_softmax_peak_seq(const float* l, int64_t n);
 
 /* ---- acceptance (crates/codpiece-server/src/engine.rs:2326-2461) -------- */
 enum { CPVO_ACCEPT_GREEDY = 0, CPVO_ACCEPT_REJECT = 1, CPVO_ACCEPT_GUMBEL = 2 };
@@ -230,6 +236,16 @@ int           cpvo_verify_step(cpvo_session* s, const int32_t* tok, int t, int d
 int           cpvo_verify_step_cands(cpvo_session* s, const int32_t* tok, int t, int depth, const float* noise,
                                      const int32_t* cands, int n_cand, int32_t* preds, int32_t* chain, float* conf,
                                      float* logits_out, float* hidden_out);
+/* Qwen35::mtp_draft (qwen35.rs:2086-2192), the graph of build_mtp_impl
+ * (mtp_graph.rs:123-249): one draft link from the trunk's normed hidden row
+ * `hidden` [E] and `token`, the token at the position after it, placed at rope
+ * position `pos`: rms(embed(token)) * enorm ; rms(hidden) * hnorm, eh_proj,
+ * the MTP layer's attention (its K/V written at MTP row mtp_past, attending
+ * rows 0..mtp_past) and FFN, then rms with the head norm (hidden_out [E]) and
+ * the draft head (logits_out [V]).  mtp_past advances by 1.  Returns -1 (and
+ * does nothing) when the MTP cache is full or pos is past the rope table. */
+int           cpvo_mtp_draft(cpvo_session* s, const float* hidden, int32_t token, int64_t pos, float* logits_out,
+                             float* hidden_out);
 /* cmd_fused: returns the number of committed tokens; stats = {accepted, proposed, rounds} */
 int           cpvo_fused_generate(cpvo_session* s, const int32_t* prompt, int n_prompt, int n_gen, int depth,
                                   int tail, int bulk, int32_t* committed, int64_t* stats);

@@ -91,6 +91,7 @@ def lib():
             "cpvo_dist_peak": (f32, [P, ctypes.c_int]),
             "cpvo_sample_coupled": (i32, [P, P, ctypes.c_int, P, ctypes.c_int, P]),
             "cpvo_argmax": (i32, [P, i64]),
+            "cpvo_softmax_peak_seq": (f32, [P, i64]),
             "cpvo_spec_accept": (ctypes.c_int, [P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                                 P, ctypes.c_int, P, P, P, ctypes.c_int, P, P]),
             "cpvo_spec_accept_rng": (ctypes.c_int, [P, P, ctypes.c_int, ctypes.c_int, P, P, P,
@@ -112,6 +113,7 @@ def lib():
             "cpvo_verify_step": (ctypes.c_int, [P, P, ctypes.c_int, ctypes.c_int, P, P, P, P, P, P]),
             "cpvo_verify_step_cands": (ctypes.c_int, [P, P, ctypes.c_int, ctypes.c_int, P, P, ctypes.c_int, P, P, P,
                                                       P, P]),
+            "cpvo_mtp_draft": (ctypes.c_int, [P, P, i32, i64, P, P]),
             "cpvo_fused_generate": (ctypes.c_int, [P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                                    ctypes.c_int, ctypes.c_int, P, P]),
         }
@@ -357,6 +359,13 @@ def argmax(x):
     return lib().cpvo_argmax(_p(x), x.size)
 
 
+def softmax_peak_seq(x):
+    """1 / (index-order f32 sum of exp(x - max)): the re-draft gate's value
+    (engine.rs:2598-2606)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return float(lib().cpvo_softmax_peak_seq(_p(x), x.size))
+
+
 def spec_accept(p_logits, draft, params, mode, u=None, q_logits=None, noise_t=None, hist=None):
     """Acceptance for B sequences: returns (tokens [B][k+1], n_accept [B])."""
     p_logits = np.ascontiguousarray(p_logits, dtype=np.float32)
@@ -483,6 +492,16 @@ class Session:
         assert lib().cpvo_verify_step_cands(self.h, _p(t), T, depth, _p(nz), _p(c), 0 if c is None else c.size,
                                             _p(preds), _p(chain), _p(conf), _p(logits), _p(hidden)) == 0
         return preds, chain[:depth], conf[:depth], logits, hidden
+
+    def mtp_draft(self, hidden, token, pos):
+        """One standalone draft link (Qwen35::mtp_draft): (logits [V], hidden
+        [E]); mtp_past advances by 1."""
+        V, E = self.model.hp.n_vocab, self.model.hp.n_embd
+        h = np.ascontiguousarray(hidden, dtype=np.float32).ravel()
+        assert h.size == E
+        logits, hout = np.empty(V, np.float32), np.empty(E, np.float32)
+        assert lib().cpvo_mtp_draft(self.h, _p(h), int(token), int(pos), _p(logits), _p(hout)) == 0
+        return logits, hout
 
     def fused_generate(self, prompt, n_gen, depth, tail=64, bulk=512):
         p = np.ascontiguousarray(prompt, dtype=np.int32)

@@ -412,6 +412,36 @@ int cpvo_verify_step_cands(cpvo_session* s, const int32_t* tok, int T, int depth
     return 0;
 }
 
+/* Qwen35::mtp_draft (qwen35.rs:2086-2192) on the graph of build_mtp_impl
+ * (mtp_graph.rs:123-249): the link of the round's chain for one row, except
+ * that its K/V row is written at mtp_past (row_ids, :2177-2181), it attends
+ * rows 0..mtp_past (the mask, :2163-2174), its rope position is the caller's
+ * `pos` (:2161), and mtp_past advances by 1 (:2189). */
+int cpvo_mtp_draft(cpvo_session* s, const float* hidden, int32_t token, int64_t pos, float* logits_out,
+                   float* hidden_out)
+{
+    const cpvo_model* m = s->m;
+    const cpvo_hparams* hp = &m->hp;
+    const int64_t E = hp->n_embd;
+    if (!hp->has_mtp || s->mtp_past + 1 > s->mtp_ctx || pos < 0 || pos > s->n_ctx + 1) return -1;
+    if (token < 0 || token >= hp->n_vocab) return -1;
+    float* e = malloc(sizeof(float) * (size_t)E);
+    float* cat = malloc(sizeof(float) * (size_t)(2 * E));
+    float* d = malloc(sizeof(float) * (size_t)E);
+    embed(mtp_embed_w(m), &token, 1, e);
+    const int64_t eo = g_fault == 3 ? E : 0;
+    rms_rows(e, 1, (int)E, E, g_fault == 6 ? m->hnorm : m->enorm, hp->rms_eps, cat + eo, 2 * E);
+    rms_rows(hidden, 1, (int)E, E, g_fault == 6 ? m->enorm : m->hnorm, hp->rms_eps, cat + E - eo, 2 * E);
+    mm(&m->eh_proj, cat, 1, d);
+    block(s, &m->L[hp->n_layer], d, 1, pos, s->mtp_past, s->mtp_past, s->kc[hp->n_layer], s->vc[hp->n_layer], 1);
+    rms_rows(d, 1, (int)E, E, mtp_head_norm(m), hp->rms_eps, hidden_out, E);
+    mm(mtp_head_w(m), hidden_out, 1, logits_out);
+    if (g_fault == 4) memcpy(hidden_out, d, sizeof(float) * (size_t)E);
+    s->mtp_past += 1;
+    free(e); free(cat); free(d);
+    return 0;
+}
+
 /* cmd_fused (crates/codpiece-cli/src/main.rs:643-931) at a fixed depth, no
  * EOS (the seeded model has no tokenizer): bulk prefill through the trunk,
  * the last `tail` prompt tokens through a round, then rounds of

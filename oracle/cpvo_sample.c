@@ -230,6 +230,15 @@ int32_t cpvo_argmax(const float* x, int64_t n)
     return (int32_t)bi;
 }
 
+float cpvo_softmax_peak_seq(const float* l, int64_t n)      /* engine.rs:2598-2606 */
+{
+    float m = -INFINITY;
+    for (int64_t i = 0; i < n; i++) m = fmaxf(m, l[i]);
+    float lse = 0.0f;
+    for (int64_t i = 0; i < n; i++) lse += cpvo_expf(l[i] - m);
+    return 1.0f / lse;
+}
+
 static int32_t argmax_plus(const float* x, const float* nz, int V)
 {
     int32_t bi = 0;

@@ -72,6 +72,15 @@ class OracleSession:
         p, ch, cf, lg, hd = self.s.step_fused_cached(tokens, depth, want_logits, _host(noise))
         return FusedOut(p.tolist(), ch.tolist(), cf.tolist(), lg, hd)
 
+    def mtp_draft(self, hidden, token, pos, p_min=0.0, want=False):
+        """The oracle's standalone draft link (cpvo_mtp_draft) with its argmax
+        and the re-draft gate (cpvo_softmax_peak_seq): the same contract as
+        Session.mtp_draft; hidden_ptr is the link's hidden row itself."""
+        from codpiece_amd.model import DraftResult
+        logits, hout = self.s.mtp_draft(_host(hidden), token, pos)
+        keep = not (p_min > 0 and cpvo.softmax_peak_seq(logits) < p_min)
+        return DraftResult(cpvo.argmax(logits), keep, hout, logits, hout)
+
     def accept_round(self, out, drafts, params, mode, noise=None, hist=None, key=0):
         """The oracle's acceptance (cpvo_spec_accept) with the device's Philox
         uniforms for `key`: the same contract as Session.accept_round."""

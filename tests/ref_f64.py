@@ -262,6 +262,33 @@ class RefSession:
     def _head_name(self):
         return "output.weight" if self.m.has("output.weight") else "token_embd.weight"
 
+    def _mtp_names(self):
+        nl = self.hp["n_layer"]
+        nx = f"blk.{nl}.nextn."
+        m = self.m
+        emb = nx + "embed_tokens.weight" if m.has(nx + "embed_tokens.weight") else "token_embd.weight"
+        hn = nx + "shared_head_norm.weight" if m.has(nx + "shared_head_norm.weight") else "output_norm.weight"
+        head = nx + "shared_head_head.weight" if m.has(nx + "shared_head_head.weight") else self._head_name()
+        return nx, emb, hn, head
+
+    def draft(self, hidden, token, pos):
+        """Qwen35::mtp_draft (qwen35.rs:2086-2192) on the graph of
+        build_mtp_impl (mtp_graph.rs:123-249): (logits [V], hidden [E]) of one
+        link; its K/V at MTP row mtp_past (row_ids, :2177-2181), rows
+        0..mtp_past visible (:2163-2174), rope position pos; mtp_past + 1."""
+        hp, m = self.hp, self.m
+        nx, emb, hn, head = self._mtp_names()
+        assert self.mtp_past + 1 <= self.mtp_ctx
+        e = m.rows(emb, [int(token)])
+        cat = np.concatenate([rms(e, m.vec(nx + "enorm.weight"), hp["rms_eps"]),
+                              rms(np.asarray(hidden, np.float64).reshape(1, -1), m.vec(nx + "hnorm.weight"),
+                                  hp["rms_eps"])], axis=1)
+        d = m.mm(nx + "eh_proj.weight", cat)
+        d = self._block(hp["n_layer"], d, pos, self.mtp_past, self.mtp_past, True)
+        hs = rms(d, m.vec(hn), hp["rms_eps"])
+        self.mtp_past += 1
+        return m.mm(head, hs)[0], hs[0]
+
     def step(self, tokens, depth):
         """(preds, chain [depth][T], conf [depth][T], logits [T][V], hidden [T][E])"""
         hp, m = self.hp, self.m

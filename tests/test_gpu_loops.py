@@ -6,7 +6,10 @@ and cpv_spec_accept reproduces cpvo_spec_accept for the same uniforms, so the
 same host loop (codpiece_amd.model) driven over the device session and over
 the oracle session must commit the same tokens with the same counts and end at
 the same positions: rejection at T = 0.7 / top-p 0.95 (the config-5 sampled
-leg's setting), gumbel coupling with and without filters, and penalties.  The
+leg's setting), gumbel coupling with and without filters, and penalties, each
+with the post-commit re-draft off, at the engine's defaults, at a p_min that
+keeps some links, and ungated.  The CLI spec path (standalone draft links then
+a verify-only round) likewise.  The
 uniforms are Philox4x64-10 by role (key seed + round); the gumbel noise is
 generated once on the host and handed to both.
 
@@ -68,19 +71,69 @@ CASES = [
 ]
 
 
+def mixed_pmin(models):
+    """A re-draft gate threshold near the median softmax peak of this model's
+    draft links (from the oracle), so that re-drafts keep some links and stop
+    at others."""
+    _, _, om = models
+    s = cpvo.Session(om, 64)
+    prompt = np.random.default_rng(12).integers(0, V, size=8).tolist()
+    _, _, _, _, H = s.step_fused_cached(prompt, 0, want_logits=True)
+    peaks = []
+    for i in range(8):
+        lg, _ = s.mtp_draft(H[i], prompt[(i + 3) % 8], s.pos[0])
+        peaks.append(cpvo.softmax_peak_seq(lg))
+    s.free()
+    return float(np.median(peaks))
+
+
+# the post-commit re-draft (engine.rs:2584-2625): off, the engine's defaults
+# (depth 3, p_min 0.75), a p_min that keeps some links, ungated
+REDRAFTS = [("redraft_off", 0, 0.75), ("redraft_default", 3, 0.75), ("redraft_mixed", 3, None),
+            ("redraft_ungated", 3, 0.0)]
+
+
+@pytest.mark.parametrize("rd", REDRAFTS, ids=[r[0] for r in REDRAFTS])
 @pytest.mark.parametrize("name,mode,pk", CASES, ids=[c[0] for c in CASES])
-def test_sampled_loop_equals_the_oracle_loop(models, name, mode, pk):
+def test_sampled_loop_equals_the_oracle_loop(models, name, mode, pk, rd):
     from codpiece_amd.model import sampled_generate
     from codpiece_amd.runtime import SamplerParams
+    _, rdepth, pmin = rd
+    if pmin is None:
+        pmin = mixed_pmin(models)
     g, o = sessions(models)
     prompt = np.random.default_rng(21).integers(0, V, size=96).tolist()
     noise = gumbel_noise(5, pk["temp"])
-    print(f"case {name}", flush=True)
-    toks, st = sampled_generate(g, prompt, 24, 3, SamplerParams(**pk), mode, seed=13, tail=32, bulk=64, noise=noise)
+    print(f"case {name} {rd[0]}", flush=True)
+    toks, st = sampled_generate(g, prompt, 24, 3, SamplerParams(**pk), mode, seed=13, tail=32, bulk=64, noise=noise,
+                                redraft_depth=rdepth, redraft_pmin=pmin)
     otoks, ost = sampled_generate(mf.OracleSession(o), prompt, 24, 3, cpvo.SamplerParams(**pk), mode, seed=13,
-                                  tail=32, bulk=64, noise=noise)
+                                  tail=32, bulk=64, noise=noise, redraft_depth=rdepth, redraft_pmin=pmin)
     assert toks == otoks
     assert (st.accepted, st.proposed, st.rounds) == (ost.accepted, ost.proposed, ost.rounds)
+    assert (st.redraft_rounds, st.redraft_links) == (ost.redraft_rounds, ost.redraft_links)
+    if rdepth and name != "gumbel_plain":      # (plain gumbel commits the graph's argmax: never divergent)
+        assert st.redraft_rounds > 0
+    assert g.pos == o.pos
+    g.free()
+    o.free()
+
+
+@pytest.mark.parametrize("n_spec,p_min", [(1, 0.75), (3, None), (3, 0.0)])
+def test_spec_path_equals_the_oracle(models, n_spec, p_min):
+    """The CLI spec path (crates/codpiece-cli/src/main.rs:1040-1160): standalone
+    draft links, a verify-only round, greedy acceptance, both positions rewound."""
+    from codpiece_amd.model import spec_generate
+    if p_min is None:
+        p_min = mixed_pmin(models)
+    g, o = sessions(models)
+    prompt = np.random.default_rng(23).integers(0, V, size=80).tolist()
+    print(f"case spec n_spec={n_spec} p_min={p_min}", flush=True)
+    toks, st = spec_generate(g, prompt, 24, n_spec, p_min, tail=16, bulk=64)
+    otoks, ost = spec_generate(mf.OracleSession(o), prompt, 24, n_spec, p_min, tail=16, bulk=64)
+    assert toks == otoks
+    assert (st.accepted, st.proposed, st.rounds, st.redraft_links) == (ost.accepted, ost.proposed, ost.rounds,
+                                                                         ost.redraft_links)
     assert g.pos == o.pos
     g.free()
     o.free()
