@@ -30,7 +30,9 @@ Beside the line's required fields, `detail` holds:
     (main.rs:549-629);
   * oracle_drafts: the fused loop with drafts from the plain greedy stream
     (acceptance 1.0), accepted tok/s when every draft is right;
-  * sampled_T0.7_top_p0.95: the sampled loop's leg;
+  * greedy_run and sampled_T0.7_top_p0.95: the workload's two full runs,
+    512 new tokens each (greedy, and T = 0.7 / top-p 0.95 with the engine's
+    post-commit re-draft), from a fresh prefill;
   * gemm: the Q4_K and Q8_0 GEMMs at the four verify shapes x M in
     {1, 5, 8, 16}, weights rotated over >= 512 MB;
   * attention_tree16: tree attention at context 8192 and 32768;
@@ -78,6 +80,8 @@ def parse():
     ap.add_argument("--attn", type=int, default=1, help="0 skips the tree attention microbench")
     ap.add_argument("--legs", type=int, default=1,
                     help="0 skips the step-cost sweep, the oracle-drafts and the T = 0.7 legs")
+    ap.add_argument("--run-tokens", type=int, default=512,
+                    help="new tokens of the workload's greedy and T = 0.7 runs (the legs)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--sampler", type=int, default=1, help="0 skips the acceptance-sampler microbench")
     ap.add_argument("--sampler-only", action="store_true", help="run only the acceptance-sampler microbench")
@@ -521,9 +525,22 @@ def oracle_drafts_leg(sess, prompt, depth, chunk, n_gen=64):
             "stream_equals_plain_greedy": toks == plain}
 
 
-def sampled_leg(sess, prompt, depth, chunk, seed, n_gen=64):
-    """The T = 0.7 / top-p 0.95 leg: the sampled speculative loop (rejection
-    rule on the device with Philox uniforms, MTP drafts) at the workload."""
+def greedy_leg(sess, prompt, depth, chunk, n_gen=512):
+    """The workload's greedy run at its full length: the fused loop
+    (main.rs:843-929) from a fresh prefill of the prompt, n_gen tokens."""
+    from codpiece_amd.model import fused_generate
+    sess.set_pos(0, 0)
+    toks, st = fused_generate(sess, prompt, n_gen, depth, tail=64, bulk=chunk)
+    return {"tokens": len(toks), "rounds": st.rounds, "acceptance": round(st.accepted / max(1, st.proposed), 4),
+            "tokens_per_round": round((len(toks) - 1) / max(1, st.rounds), 3), "prefill_s": round(st.prefill_s, 3),
+            "decode_s": round(st.decode_s, 4), "tok_s": round((len(toks) - 1) / st.decode_s, 2)}
+
+
+def sampled_leg(sess, prompt, depth, chunk, seed, n_gen=512):
+    """The workload's T = 0.7 / top-p 0.95 run at its full length: the engine's
+    sampled speculative loop (rejection rule on the device with Philox
+    uniforms, MTP chain drafts, the post-commit re-draft at the engine's
+    defaults: 3 links, softmax-peak gate 0.75), n_gen tokens."""
     from codpiece_amd import _lib
     from codpiece_amd.model import sampled_generate
     from codpiece_amd.runtime import SamplerParams
@@ -531,8 +548,9 @@ def sampled_leg(sess, prompt, depth, chunk, seed, n_gen=64):
     toks, st = sampled_generate(sess, prompt, n_gen, depth, SamplerParams(temp=0.7, top_p=0.95),
                                 _lib.ACCEPT_REJECT, seed=seed, tail=64, bulk=chunk)
     return {"tokens": len(toks), "rounds": st.rounds, "acceptance": round(st.accepted / max(1, st.proposed), 4),
-            "tokens_per_round": round((len(toks) - 1) / max(1, st.rounds), 3),
-            "decode_s": round(st.decode_s, 4), "tok_s": round((len(toks) - 1) / st.decode_s, 2)}
+            "tokens_per_round": round((len(toks) - 1) / max(1, st.rounds), 3), "prefill_s": round(st.prefill_s, 3),
+            "decode_s": round(st.decode_s, 4), "tok_s": round((len(toks) - 1) / st.decode_s, 2),
+            "redraft_rounds": st.redraft_rounds, "redraft_links": st.redraft_links}
 
 
 def prefill_gemm_stats(ctx, prof, hp, rows):
@@ -737,12 +755,14 @@ def main():
         with open(tpath) as f:
             traffic = json.load(f).get(dom)
 
-    oracle_drafts = sampled = None
+    oracle_drafts = sampled = greedy = None
     if args.legs:
         oracle_drafts = oracle_drafts_leg(sess, prompt, args.depth, chunk)
         print(f"[bench] oracle drafts: {oracle_drafts}", file=sys.stderr, flush=True)
-        sampled = sampled_leg(sess, prompt, args.depth, chunk, args.seed)
-        print(f"[bench] T=0.7 leg: {sampled}", file=sys.stderr, flush=True)
+        greedy = greedy_leg(sess, prompt, args.depth, chunk, args.run_tokens)
+        print(f"[bench] greedy run: {greedy}", file=sys.stderr, flush=True)
+        sampled = sampled_leg(sess, prompt, args.depth, chunk, args.seed, args.run_tokens)
+        print(f"[bench] T=0.7 run: {sampled}", file=sys.stderr, flush=True)
     gemm = gemm_bench(torch, ctx, args.seed) if args.gemm else None
     attn = attn_bench(torch, ctx, args.seed) if args.attn else None
     sampler = sampler_bench(torch, ctx, args.seed) if args.sampler else None
@@ -791,6 +811,7 @@ def main():
             "acceptance_sampler": sampler,
             "step_cost_us": step_cost,
             "oracle_drafts": oracle_drafts,
+            "greedy_run": greedy,
             "sampled_T0.7_top_p0.95": sampled,
             "gemm": gemm,
             "attention_tree16": attn,
