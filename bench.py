@@ -749,11 +749,14 @@ def main():
     rep_ms, rep_bytes = replay[dom]
     achieved = rep_bytes / (rep_ms * 1e-3) / 1e9
 
-    traffic = None
+    # HBM bytes per launch by class, from rocprofv3 FETCH_SIZE / WRITE_SIZE
+    # passes at this workload's shape (profiles/traffic_hbm_27b_q4k_ctx4096.md)
+    traffic_table = {}
     tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get(dom)
+            traffic_table = json.load(f)
+    traffic = traffic_table.get(dom)
 
     oracle_drafts = sampled = greedy = None
     if args.legs:
@@ -802,7 +805,8 @@ def main():
                                    "GB_per_launch": round(v[2] / v[0] / 1e9, 5),
                                    "us_per_launch_replayed": round(replay[k][0] * 1e3, 2),
                                    "GB_s_replayed": round(replay[k][1] / (replay[k][0] * 1e-3) / 1e9, 1),
-                                   "us_per_launch_event_bracketed": round(v[1] / v[0] * 1e3, 2)}
+                                   "us_per_launch_event_bracketed": round(v[1] / v[0] * 1e3, 2),
+                                   "hbm_bytes_per_launch": traffic_table.get(k)}
                                for k, v in prof.items() if v[0]},
             "profiled_rounds": args.profile_rounds,
             "prefill": {"tokens": args.prompt, "chunk": chunk, "wall_s": round(prefill_wall, 3),
