@@ -115,7 +115,7 @@ SIGNATURES = {
     "cpv_argmax_rows": (_INT, [_P, _P, _P, _I64, _I64, _P]),
     "cpv_distribution": (_INT, [_P, _P, _INT, _INT, ctypes.POINTER(SamplerParams), _P, _INT, _P, _P, _P]),
     "cpv_spec_accept": (_INT, [_P, _P, _P, _P, _INT, _INT, _INT, ctypes.POINTER(SamplerParams), _INT,
-                               _P, ctypes.c_uint64, _P, _P, _INT, _P, _P]),
+                               _P, ctypes.c_uint64, ctypes.c_uint64, _P, _P, _INT, _P, _P]),
     "cpv_model_create": (_INT, [_P, ctypes.POINTER(Hparams), ctypes.POINTER(_P)]),
     "cpv_model_set_tensor": (_INT, [_P, ctypes.c_char_p, _INT, _P, _INT, _I64, _I64]),
     "cpv_model_ready": (_INT, [_P]),

@@ -223,12 +223,26 @@ extern "C" cpv_status cpv_profile_stop(cpv_ctx* ctx, cpv_prof_stat* out)
     return CPV_OK;
 }
 
+bool cpv_capturing(cpv_ctx* ctx)
+{
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+cpv_status cpv_refuse_growth(cpv_ctx* ctx, const char* what, size_t bytes)
+{
+    ctx->grow_refused = true;
+    return cpv_fail(ctx, CPV_EUNSUPPORTED, "%s: growing to %zu bytes while the stream is being captured "
+                                           "(run the call once outside the capture first)", what, bytes);
+}
+
 cpv_status cpv_workspace(cpv_ctx* ctx, size_t bytes, void** out)
 {
     if (bytes <= ctx->ws_bytes) {
         *out = ctx->ws;
         return CPV_OK;
     }
+    if (cpv_capturing(ctx)) return cpv_refuse_growth(ctx, "workspace", bytes);
     if (ctx->ws) {
         CPV_HIP(ctx, hipStreamSynchronize(ctx->stream));
         CPV_HIP(ctx, hipFree(ctx->ws));
@@ -842,6 +856,7 @@ static cpv_status reduce_buffer(cpv_ctx* ctx, int64_t rows, unsigned long long**
 {
     const size_t need = (size_t)rows * AM_NB * 24;
     if (need > ctx->red_bytes) {
+        if (cpv_capturing(ctx)) return cpv_refuse_growth(ctx, "reduction buffer", need);
         CPV_HIP(ctx, hipStreamSynchronize(ctx->stream));
         if (ctx->red) (void)hipFree(ctx->red);
         ctx->red = nullptr;

@@ -30,6 +30,8 @@ struct cpv_ctx {
     size_t red_bytes = 0;
     // this device's address of the file-scope scratch of cpv_qgemm_noalloc
     void* scratch = nullptr;
+    // set when a buffer was not grown because the stream was being captured
+    bool grow_refused = false;
     // kernel timing (cpv_profile_start / _stop): event pairs around launches,
     // and each launch kept for cpv_profile_replay
     struct prof_rec { int cls, ev0, ev1; double bytes; };
@@ -81,6 +83,13 @@ cpv_status cpv_noalloc_setup(cpv_ctx* ctx);
 // grow the context workspace to at least `bytes` (synchronises the stream
 // before freeing an old buffer the queued work may still use)
 cpv_status cpv_workspace(cpv_ctx* ctx, size_t bytes, void** out);
+
+// Whether ctx->stream is being captured into a graph.  A buffer that would
+// have to grow then is not grown (a capture may record no synchronisation,
+// allocation or memset): the call fails with CPV_EUNSUPPORTED and sets
+// ctx->grow_refused, and a round being captured runs eagerly instead.
+bool cpv_capturing(cpv_ctx* ctx);
+cpv_status cpv_refuse_growth(cpv_ctx* ctx, const char* what, size_t bytes);
 
 // bytes per block / elements per block of a GGUF type
 int64_t cpv_type_block(int type);

@@ -188,7 +188,7 @@ bool open_file(const char* path, File* g, std::string* err)
         if (!r.num(&magic)) break;
         if (magic != MAGIC) {
             char b[64];
-            snprintf(b, sizeof b, "bad magic 0x%08x (not a GGUF file)", magic);
+            snprintf(b, sizeof b, "not a GGUF file: it starts with 0x%08x where the magic 0x%08x belongs", magic, MAGIC);
             *err = b;
             break;
         }
@@ -198,7 +198,8 @@ bool open_file(const char* path, File* g, std::string* err)
         uint64_t nt, nk;
         if (!r.len(&nt) || !r.len(&nk)) break;
         if (nt > MAX_TENSORS || nk > MAX_KVS) {
-            *err = "implausible counts: " + std::to_string(nt) + " tensors, " + std::to_string(nk) + " kvs";
+            *err = "header lists " + std::to_string(nt) + " tensors and " + std::to_string(nk) +
+                   " metadata entries, more than this reader accepts (2^20 of each)";
             break;
         }
         bool bad = false;
@@ -256,8 +257,8 @@ bool open_file(const char* path, File* g, std::string* err)
             if (t.bytes >= 0) {
                 const uint64_t end = t.offset + (uint64_t)t.bytes;
                 if (end < t.offset || end > data_len) {
-                    *err = "tensor " + t.name + " [" + std::to_string(t.offset) + ".." + std::to_string(end) +
-                           "] exceeds the data section (" + std::to_string(data_len) + " bytes)";
+                    *err = "tensor " + t.name + " would end at byte " + std::to_string(end) +
+                           " of a data section that holds " + std::to_string(data_len);
                     bad = true;
                     break;
                 }

@@ -1859,6 +1859,7 @@ cpv_status replay_round(cpv_session* s, const std::array<int, 4>& key, bool* don
     }
     ctx->stream = ctx->cap_stream;
     s->eager_only = false;
+    ctx->grow_refused = false;
     const cpv_status st = round_body(s, key[0], key[1], nullptr, false, 0);
     hipGraph_t graph = nullptr;
     const hipError_t e = hipStreamEndCapture(ctx->cap_stream, &graph);
@@ -1869,7 +1870,14 @@ cpv_status replay_round(cpv_session* s, const std::array<int, 4>& key, bool* don
     if (graph) (void)hipGraphDestroy(graph);
     (void)hipGetLastError();
     if (!ok) {   // (nothing was launched: the round runs eagerly)
-        s->unreplayable.push_back(key);
+        if (ctx->grow_refused) {
+            // a buffer had to grow: the eager round grows it, and the shape
+            // is warmed again before its next capture
+            ctx->grow_refused = false;
+            s->warm.erase(std::remove(s->warm.begin(), s->warm.end(), key), s->warm.end());
+        } else {
+            s->unreplayable.push_back(key);
+        }
         return CPV_OK;
     }
     constexpr size_t MAX_GRAPHS = 8;

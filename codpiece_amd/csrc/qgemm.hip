@@ -988,6 +988,7 @@ static cpv_status gemm_accumulator(cpv_ctx* ctx, int64_t rows, int64_t n_pad, do
 {
     const size_t need = (size_t)rows * n_pad * sizeof(double);
     if (need > ctx->gsum_bytes) {
+        if (cpv_capturing(ctx)) return cpv_refuse_growth(ctx, "GEMM accumulator", need);
         CPV_HIP(ctx, hipStreamSynchronize(ctx->stream));
         if (ctx->gsum) (void)hipFree(ctx->gsum);
         ctx->gsum = nullptr;

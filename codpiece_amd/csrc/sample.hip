@@ -1437,11 +1437,11 @@ __global__ __launch_bounds__(SB) void band_part_kernel(DistArgs a)
 }
 
 // ------------------------------------------------------------ acceptance
-// Philox4x64-10 (Salmon, Moraes, Dror, Shaw, SC'11): counter (c0, c1, c2, 0),
+// Philox4x64-10 (Salmon, Moraes, Dror, Shaw, SC'11): counter (c0, c1, c2, c3),
 // key (seed, 0); the uniform is the top 24 bits of the first output word.
-__device__ float philox_u01(uint64_t seed, uint64_t c0, uint64_t c1, uint64_t c2)
+__device__ float philox_u01(uint64_t seed, uint64_t c0, uint64_t c1, uint64_t c2, uint64_t c3)
 {
-    uint64_t x0 = c0, x1 = c1, x2 = c2, x3 = 0, k0 = seed, k1 = 0;
+    uint64_t x0 = c0, x1 = c1, x2 = c2, x3 = c3, k0 = seed, k1 = 0;
     for (int r = 0; r < 10; r++) {
         const uint64_t lo0 = 0xD2E7470EE14C6C93ull * x0, hi0 = __umul64hi(0xD2E7470EE14C6C93ull, x0);
         const uint64_t lo1 = 0xCA5A826395121157ull * x2, hi1 = __umul64hi(0xCA5A826395121157ull, x2);
@@ -1459,7 +1459,7 @@ __device__ float philox_u01(uint64_t seed, uint64_t c0, uint64_t c1, uint64_t c2
 struct DecideArgs {
     const int32_t* draft;       // [B][k]
     const float* u;             // [B][k+1][2] or NULL (Philox)
-    uint64_t seed;
+    uint64_t seed, round;
     const float* noise;         // [B][k+1][V] (GUMBEL)
     int B, k, V, mode, has_q, nrow_p;
     float T, inv_t;
@@ -1552,7 +1552,7 @@ __device__ int coupled_argmax(const DecideArgs& a, const Row& d, const float* no
 __device__ __forceinline__ float uniform(const DecideArgs& a, int b, int j, int r)
 {
     if (a.u) return a.u[((size_t)b * (a.k + 1) + j) * 2 + r];
-    return philox_u01(a.seed, (uint64_t)b, (uint64_t)j, (uint64_t)r);
+    return philox_u01(a.seed, (uint64_t)b, (uint64_t)j, (uint64_t)r, a.round);
 }
 
 // engine.rs:2326-2461 for one sequence: walk the drafts, stop at the first
@@ -1832,8 +1832,9 @@ extern "C" cpv_status cpv_distribution(cpv_ctx* ctx, const float* logits_dev, in
 extern "C" cpv_status cpv_spec_accept(cpv_ctx* ctx, const float* p_logits_dev, const float* q_logits_dev,
                                       const int32_t* draft_dev, int b, int k, int v,
                                       const cpv_sampler_params* params, int mode, const float* u_dev,
-                                      uint64_t philox_seed, const float* noise_dev, const int32_t* hist_dev,
-                                      int hist_len, int32_t* out_tok_dev, int32_t* out_n_dev)
+                                      uint64_t philox_seed, uint64_t philox_round, const float* noise_dev,
+                                      const int32_t* hist_dev, int hist_len, int32_t* out_tok_dev,
+                                      int32_t* out_n_dev)
 {
     if (!ctx) return CPV_EINVAL;
     if (!p_logits_dev || (k > 0 && !draft_dev) || !out_tok_dev || !out_n_dev || b < 1 || k < 0 || k > 15 || v < 1 ||
@@ -1891,6 +1892,7 @@ extern "C" cpv_status cpv_spec_accept(cpv_ctx* ctx, const float* p_logits_dev, c
     c.draft = draft_dev;
     c.u = u_dev;
     c.seed = philox_seed;
+    c.round = philox_round;
     c.noise = noise_dev;
     c.B = b;
     c.k = k;

@@ -257,11 +257,12 @@ class Session:
             hidden = _device_view(out.hidden_dev, t * E, torch.float32, self.ctx.torch_device).view(t, E).clone()
         return FusedOut(preds, [], [], logits, hidden)
 
-    def accept_round(self, out, drafts, params, mode, noise=None, hist=None, key=0):
+    def accept_round(self, out, drafts, params, mode, noise=None, hist=None, key=0, round=0):
         """Decide a verified round on the device (cpv_spec_accept over the
         round's logits, out.logits [t][V] with t = len(drafts) + 1): returns
         (the accepted drafts then the next token, the number accepted).
-        Uniforms are Philox4x64-10 with key (key, 0), counter (0, j, role, 0);
+        Uniforms are Philox4x64-10 with key (key, 0), counter (0, j, role,
+        round);
         `noise` ([t][V], T-scaled gumbel) for the gumbel mode; `hist` the
         penalty window, oldest first."""
         t, V = out.logits.shape
@@ -270,7 +271,7 @@ class Session:
         h = None if not hist else torch.tensor(list(hist), dtype=torch.int32, device=dev).view(1, -1)
         nz = None if noise is None else _as_device(noise, dev).view(1, t, V)
         tok, n = self.ctx.spec_accept(out.logits.view(1, t, V), dr, params, mode, noise=nz, hist=h,
-                                      philox_seed=int(key))
+                                      philox_seed=int(key), philox_round=int(round))
         n = int(n.cpu()[0])
         return tok[0, :n + 1].cpu().tolist(), n
 
@@ -323,6 +324,11 @@ def fused_generate(session, prompt, n_gen, depth, tail=64, bulk=512, timer=None,
     engine's verify-only rounds take DFlash drafts, engine.rs:2291-2293); the
     chain is still computed at `depth`.  depth 0 with no drafter is plain
     greedy decoding, one token per round.
+    When n_gen is reached inside a round's accepted drafts the loop ends
+    there, before the round's rewind, as the reference's does (`break
+    'outer`, main.rs:883-887): the session's n_past then still counts that
+    round's unused rows, so a caller that reuses the session sets its
+    positions first.
     Returns (committed tokens, FusedStats)."""
     import time
     t0 = time.perf_counter()
@@ -502,12 +508,14 @@ def sampled_generate(session, prompt, n_gen, depth, params, mode=_lib.ACCEPT_REJ
         engine's DFlash mode) has none.
     Randomness is explicit: the reference's sequential xoshiro stream becomes
     Philox4x64-10 uniforms by role, round r (the tail round is 0) using key
-    (seed + r, 0) with counter (0, j, role, 0).  In GUMBEL mode noise(r, rows)
+    (seed, 0) with counter (0, j, role, r).  In GUMBEL mode noise(r, rows)
     supplies round r's T-scaled gumbel noise [rows][V] (the engine's noise
     thread, :2080-2118): the verify argmaxes logits + noise in the graph, and
     the acceptance couples on the same noise.  drafter(committed, drafts), when
     given, replaces each round's drafts after those rules (an external
-    drafter, as fused_generate takes).  Returns (committed tokens,
+    drafter, as fused_generate takes).  As in fused_generate (and the
+    engine's `break 'outer`), a run that ends inside a round's accepted
+    drafts leaves that round unrewound.  Returns (committed tokens,
     FusedStats)."""
     import time
     if mode == _lib.ACCEPT_GUMBEL and noise is None:
@@ -548,7 +556,7 @@ def sampled_generate(session, prompt, n_gen, depth, params, mode=_lib.ACCEPT_REJ
         nz = noise(rounds, len(batch)) if mode == _lib.ACCEPT_GUMBEL else None
         out = session.step_fused_cached(batch, depth, want_logits=True, noise=nz)
         proposed += len(drafts)
-        toks, keep = session.accept_round(out, drafts, params, mode, noise=nz, hist=hist(), key=seed + rounds)
+        toks, keep = session.accept_round(out, drafts, params, mode, noise=nz, hist=hist(), key=seed, round=rounds)
         accepted += keep
         done = False
         for d in drafts[:keep]:

@@ -153,7 +153,7 @@ class Context:
         return ids, probs, n
 
     def spec_accept(self, p_logits, draft, params, mode, u=None, q_logits=None, noise=None, hist=None,
-                    philox_seed=0, out_tok=None, out_n=None):
+                    philox_seed=0, philox_round=0, out_tok=None, out_n=None):
         b, k1, v = p_logits.shape
         k = k1 - 1
         if out_tok is None:
@@ -163,7 +163,7 @@ class Context:
         hl = 0 if hist is None else hist.shape[1]
         self._check(self.lib.cpv_spec_accept(
             self.h, _ptr(p_logits), _ptr(q_logits), _ptr(draft.to(torch.int32).contiguous()), b, k, v,
-            ctypes.byref(params), mode, _ptr(u), philox_seed, _ptr(noise),
+            ctypes.byref(params), mode, _ptr(u), philox_seed, philox_round, _ptr(noise),
             _ptr(None if hist is None else hist.to(torch.int32).contiguous()), hl, _ptr(out_tok), _ptr(out_n)))
         return out_tok, out_n
 

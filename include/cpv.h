@@ -179,7 +179,9 @@ cpv_status  cpv_distribution(cpv_ctx* ctx, const float* logits_dev, int rows, in
  *   u_dev         f32 [b][k+1][2] uniforms by role (r0 = accept roll, or the
  *                 bonus draw at j = k; r1 = residual draw), or NULL to draw
  *                 them from Philox4x64-10 with key (philox_seed, 0) and
- *                 counter (b, j, r, 0), taking (x >> 40) / 2^24.
+ *                 counter (b, j, r, philox_round), taking (x >> 40) / 2^24
+ *                 (a request keeps its seed; each of its rounds takes its
+ *                 own philox_round).
  *   noise_dev     f32 [b][k+1][v], T-scaled gumbel noise (GUMBEL mode only)
  *   hist_dev      int32 [b][hist_len] penalty window, oldest first, -1 empty
  *                 (only read when a penalty is active)
@@ -190,8 +192,9 @@ cpv_status  cpv_distribution(cpv_ctx* ctx, const float* logits_dev, int rows, in
 cpv_status  cpv_spec_accept(cpv_ctx* ctx, const float* p_logits_dev, const float* q_logits_dev,
                             const int32_t* draft_dev, int b, int k, int v,
                             const cpv_sampler_params* params, int mode, const float* u_dev,
-                            uint64_t philox_seed, const float* noise_dev, const int32_t* hist_dev,
-                            int hist_len, int32_t* out_tok_dev, int32_t* out_n_dev);
+                            uint64_t philox_seed, uint64_t philox_round, const float* noise_dev,
+                            const int32_t* hist_dev, int hist_len, int32_t* out_tok_dev,
+                            int32_t* out_n_dev);
 
 /* ---- model and verify round ------------------------------------------------- */
 typedef struct cpv_model cpv_model;

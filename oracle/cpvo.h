@@ -63,8 +63,8 @@ int64_t  cpvo_expf_vs_libm(float lo, float hi, int64_t stride);
 /* ---- RNGs --------------------------------------------------------------- */
 void     cpvo_philox4x64(const uint64_t ctr[4], const uint64_t key[2], uint64_t out[4]);
 float    cpvo_u01(uint64_t x);                       /* (x >> 40) / 2^24, as next_f32 */
-/* u[b][j][r] = cpvo_u01(philox((b, j, r, 0), (seed, 0))[0]) for j in [0,k], r in {0,1} */
-void     cpvo_philox_uniforms(uint64_t seed, int B, int k, float* u);
+/* u[b][j][r] = cpvo_u01(philox((b, j, r, round), (seed, 0))[0]) for j in [0,k], r in {0,1} */
+void     cpvo_philox_uniforms(uint64_t seed, uint64_t round, int B, int k, float* u);
 /* xoshiro256++ seeded by splitmix64 (crates/codpiece-sample/src/lib.rs:88-130) */
 void     cpvo_rng_seed(uint64_t seed, uint64_t s[4]);
 uint64_t cpvo_rng_next_u64(uint64_t s[4]);

@@ -64,7 +64,7 @@ def lib():
             "cpvo_expf_vs_libm": (i64, [f32, f32, i64]),
             "cpvo_exp_table": (None, [P]),
             "cpvo_philox4x64": (None, [P, P, P]),
-            "cpvo_philox_uniforms": (None, [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, P]),
+            "cpvo_philox_uniforms": (None, [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int, ctypes.c_int, P]),
             "cpvo_rng_seed": (None, [ctypes.c_uint64, P]),
             "cpvo_rng_next_u64": (ctypes.c_uint64, [P]),
             "cpvo_rng_next_f32": (f32, [P]),
@@ -168,9 +168,10 @@ def philox4x64(ctr, key):
     return out
 
 
-def philox_uniforms(seed, B, k):
+def philox_uniforms(seed, B, k, round=0):
+    """u[b][j][r] from Philox4x64-10, counter (b, j, r, round), key (seed, 0)."""
     u = np.empty((B, k + 1, 2), dtype=np.float32)
-    lib().cpvo_philox_uniforms(seed, B, k, _p(u))
+    lib().cpvo_philox_uniforms(seed, round, B, k, _p(u))
     return u
 
 

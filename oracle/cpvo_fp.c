@@ -181,13 +181,13 @@ float cpvo_u01(uint64_t x)
     return (float)(x >> 40) / (float)(1u << 24);
 }
 
-void cpvo_philox_uniforms(uint64_t seed, int B, int k, float* u)
+void cpvo_philox_uniforms(uint64_t seed, uint64_t round, int B, int k, float* u)
 {
     uint64_t key[2] = {seed, 0};
     for (int b = 0; b < B; b++)
         for (int j = 0; j <= k; j++)
             for (int r = 0; r < 2; r++) {
-                uint64_t ctr[4] = {(uint64_t)b, (uint64_t)j, (uint64_t)r, 0}, out[4];
+                uint64_t ctr[4] = {(uint64_t)b, (uint64_t)j, (uint64_t)r, round}, out[4];
                 cpvo_philox4x64(ctr, key, out);
                 u[((int64_t)b * (k + 1) + j) * 2 + r] = cpvo_u01(out[0]);
             }

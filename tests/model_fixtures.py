@@ -81,11 +81,11 @@ class OracleSession:
         keep = not (p_min > 0 and cpvo.softmax_peak_seq(logits) < p_min)
         return DraftResult(cpvo.argmax(logits), keep, hout, logits, hout)
 
-    def accept_round(self, out, drafts, params, mode, noise=None, hist=None, key=0):
+    def accept_round(self, out, drafts, params, mode, noise=None, hist=None, key=0, round=0):
         """The oracle's acceptance (cpvo_spec_accept) with the device's Philox
-        uniforms for `key`: the same contract as Session.accept_round."""
+        uniforms for `key` and `round`: the same contract as Session.accept_round."""
         t, V = out.logits.shape
-        u = cpvo.philox_uniforms(int(key), 1, t - 1)
+        u = cpvo.philox_uniforms(int(key), 1, t - 1, round=int(round))
         nz = None if noise is None else _host(noise).reshape(1, t, V)
         h = None if not hist else np.asarray(list(hist), dtype=np.int32).reshape(1, -1)
         tok, n = cpvo.spec_accept(np.asarray(out.logits).reshape(1, t, V), np.asarray(drafts, np.int32).reshape(1, t - 1),

@@ -1,11 +1,12 @@
 """GPU parity of tree-masked GQA attention against the oracle.
 
-Bar: bit-exact.  Both sides implement the exact-window attention contract
-(fixed-point scores with exact integer sums, an exact softmax normaliser, f16
-probabilities and fixed-order f32 accumulation), so the device result does
-not depend on its grid, KV split or the number of query rows per call.  The
-contract itself is held within 2^-10 max|v| of binary64 attention by the
-oracle's own tests.
+Bar: bit-exact.  Both sides implement the chunked attention contract:
+fixed-point scores with exact integer sums; per 128-row chunk the weights
+p = rint(expf(w - m_c) 2^22) and the values vq = rint(f16(v) 2^14), whose
+products and normaliser are summed exactly in integers; then a fold over the
+chunks in chunk order.  So the device result does not depend on its grid or
+on the number of query rows per call.  The contract itself is held within
+2^-12 max|v| + 2^-15 of binary64 attention by the oracle's own tests.
 """
 import numpy as np
 import pytest

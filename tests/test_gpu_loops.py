@@ -10,7 +10,7 @@ leg's setting), gumbel coupling with and without filters, and penalties, each
 with the post-commit re-draft off, at the engine's defaults, at a p_min that
 keeps some links, and ungated.  The CLI spec path (standalone draft links then
 a verify-only round) likewise.  The
-uniforms are Philox4x64-10 by role (key seed + round); the gumbel noise is
+uniforms are Philox4x64-10 by role (key seed, round in the counter); the gumbel noise is
 generated once on the host and handed to both.
 
 The losslessness gate (scripts/final-verify.sh:15-30): with drafts taken from

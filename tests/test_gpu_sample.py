@@ -201,10 +201,10 @@ def drafts_for(rng, pl, k, p_argmax=0.7):
     return d
 
 
-def accept(ctx, pl, draft, p, mode, seed=None, u=None, q=None, noise=None, hist=None):
+def accept(ctx, pl, draft, p, mode, seed=None, u=None, q=None, noise=None, hist=None, rnd=0):
     t = lambda a, dt=np.float32: None if a is None else torch.from_numpy(np.ascontiguousarray(a, dtype=dt)).cuda()
     tok, n = ctx.spec_accept(t(pl), t(draft, np.int32), dev_params(p), mode, u=t(u), q_logits=t(q),
-                             noise=t(noise), hist=t(hist, np.int32), philox_seed=seed or 0)
+                             noise=t(noise), hist=t(hist, np.int32), philox_seed=seed or 0, philox_round=rnd)
     torch.cuda.synchronize()
     return tok.cpu().numpy(), n.cpu().numpy()
 
@@ -237,6 +237,9 @@ def test_headline_acceptance(ctx, B):
          cpvo.spec_accept(pl, draft, p, cpvo.ACCEPT_REJECT, u=u, q_logits=ql))
     same(accept(ctx, pl, draft, p, cpvo.ACCEPT_REJECT, seed=seed),
          cpvo.spec_accept(pl, draft, p, cpvo.ACCEPT_REJECT, u=u))
+    # a later round of the same request: the round in the counter's last word
+    same(accept(ctx, pl, draft, p, cpvo.ACCEPT_REJECT, seed=seed, rnd=37),
+         cpvo.spec_accept(pl, draft, p, cpvo.ACCEPT_REJECT, u=cpvo.philox_uniforms(seed, B, k, round=37)))
     g = cpvo.SamplerParams()
     same(accept(ctx, pl, draft, g, cpvo.ACCEPT_GREEDY), cpvo.spec_accept(pl, draft, g, cpvo.ACCEPT_GREEDY))
 

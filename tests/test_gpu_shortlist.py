@@ -70,6 +70,33 @@ def test_shortlist_rounds_equal_oracle(models):
     o.free()
 
 
+def test_permuted_shortlist_feeds_the_index_to_the_next_link(models):
+    # the same candidate set in identity and in permuted order: the first
+    # link's drafts agree, the second link embeds the shortlist index
+    # (qwen35.rs:2958) and differs; each order equals the oracle's round
+    from codpiece_amd.model import Session
+    ctx, gm, om = models
+    V = K_MODEL["n_vocab"]
+    n = 512
+    ident = list(range(n))
+    perm = np.random.default_rng(23).permutation(n).tolist()
+    prompt = np.random.default_rng(24).integers(0, V, size=40).tolist()
+    rounds = []
+    for cands in (ident, perm):
+        g, o = Session(gm, 256), cpvo.Session(om, 256)
+        g.prefill(prompt[:35])
+        o.prefill(prompt[:35])
+        a = g.step_fused_cached(prompt[35:], 2, want_logits=True, cands=cands)
+        b = o.step_fused_cached(prompt[35:], 2, want_logits=True, cands=cands)
+        same_round(a, b)
+        rounds.append(a)
+        g.free()
+        o.free()
+    a0, a1 = rounds
+    assert a0.preds == a1.preds and a0.chain[0] == a1.chain[0]
+    assert a0.chain[1] != a1.chain[1] or a0.conf[1] != a1.conf[1]
+
+
 def test_shortlist_of_the_argmax_rows_matches_the_full_head_first_link(models):
     # with every id a candidate, in order, link 0 equals the full head's draft
     from codpiece_amd.model import Session

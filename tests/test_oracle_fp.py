@@ -84,6 +84,12 @@ def test_uniforms_are_24_bit_and_role_addressed():
     assert np.array_equal(u, u2[:3])
     x = cpvo.philox4x64((2, 3, 1, 0), (1234, 0))
     assert u[2, 3, 1] == np.float32(int(x[0]) >> 40) / np.float32(2**24)
+    # the round is the counter's last word: round r of seed s is not round 0
+    # of another seed (a request keeps one key for all of its rounds)
+    u7 = cpvo.philox_uniforms(1234, 3, 4, round=7)
+    x7 = cpvo.philox4x64((2, 3, 1, 7), (1234, 0))
+    assert u7[2, 3, 1] == np.float32(int(x7[0]) >> 40) / np.float32(2**24)
+    assert not np.array_equal(u7, u) and not np.array_equal(u7, cpvo.philox_uniforms(1234 + 7, 3, 4))
 
 
 def test_splitmix_seeding_known_answer():

@@ -126,6 +126,30 @@ def test_exact_contract_is_attention_up_to_its_fixed_points(n_past, qmul):
     assert np.abs(a - b).max() <= bound
 
 
+@pytest.mark.parametrize("vscale,rel", [(1e-3, 4e-3), (2.0 ** -10, 4e-3), (2.0 ** -6, 4e-4), (1.0, 2e-5)])
+def test_exact_contract_with_small_values_is_absolute_in_v(vscale, rel):
+    # vq = rint(f16(v) 2^14) rounds each value within 2^-15 absolute, not
+    # relative: for values far below 2^-4 the bound 2^-12 max|v| + 2^-15 is
+    # its absolute term, and the error relative to max|v| grows as the
+    # values shrink (measured: 0.17% of max|v| for V ~ N(0, 1e-3), 0.013%
+    # at 2^-6, 4e-6 at unit scale).  Each case holds the bound and its
+    # measured relative size (with margin).
+    rng = np.random.default_rng(int(1 / vscale) if vscale < 1 else 5)
+    H, Hkv, D = 8, 2, 64
+    T = len(TREE)
+    n = 300 + T
+    k = cpvo.f32_to_f16_bits(rng.normal(size=(n, Hkv * D)).astype(np.float32))
+    v = cpvo.f32_to_f16_bits((vscale * rng.normal(size=(n, Hkv * D))).astype(np.float32))
+    q = rng.normal(size=(T, H, D)).astype(np.float32)
+    scale = np.float32(1) / np.sqrt(np.float32(D))
+    a = cpvo.attn(q, k, v, 300, TREE, scale)
+    b = cpvo.attn(q, k, v, 300, TREE, scale, f64=True)
+    vmax = np.abs(cpvo.f16_bits_to_f32(v)).max()
+    err = np.abs(a - b).max()
+    assert err <= 2.0 ** -12 * vmax + 2.0 ** -15
+    assert err / vmax <= rel
+
+
 @pytest.mark.parametrize("n_past", [0, 127, 128, 700, 2047])
 def test_exact_contract_uniform_weights_closed_form(n_past):
     # q = 0: every visible score is 0, so in every chunk m = 0, e = 1,

@@ -6,7 +6,7 @@ independent restatement of the engine's loop written here from
 crates/codpiece-server/src/engine.rs:1958-2039 and 2212-2625 with the
 codpiece-sample primitives (Sampler::distribution, Dist::prob_of / draw /
 draw_excluding, sample_coupled), draft by draft, on the same uniforms by role
-(Philox4x64-10, key seed + round, counter (0, j, role)) and the same gumbel
+(Philox4x64-10, key seed, counter (0, j, role, round)) and the same gumbel
 noise.  Rejection, gumbel coupling with and without filters, and penalties;
 with the post-commit re-draft (:2584-2625: standalone draft links from the
 kept row's hidden, gated by the softmax peak, computed here as a numpy
@@ -84,7 +84,7 @@ def engine_restatement(osess, prompt, n_gen, depth, params, mode, seed, tail, bu
         nz = noise(rounds, len(batch)) if mode == GUMBEL else None
         P, C, CF, L, H = osess.step_fused_cached(batch, depth, want_logits=True, noise=nz)
         prop += k
-        u = cpvo.philox_uniforms(seed + rounds, 1, k)[0]
+        u = cpvo.philox_uniforms(seed, 1, k, round=rounds)[0]
         n_keep, repl = 0, None
         for j, d in enumerate(drafts):
             if mode == GUMBEL:
