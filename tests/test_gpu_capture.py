@@ -41,8 +41,9 @@ def test_buffer_growth_is_refused_inside_a_capture():
     x1 = rng.normal(0, 1, size=(5, 1024)).astype(np.float32)
     ctx.qgemm(w1, torch.from_numpy(x1).cuda())
     torch.cuda.synchronize()
-    # a larger one needs both to grow
-    n, k, m = 8192, 4096, 16
+    # a tall one needs the split-K accumulator to grow past its first 16 MiB
+    # (16 rows x 151,936 outputs x 8 bytes = 19.4 MB)
+    n, k, m = 151936, 256, 16
     q2 = cpvo.quantize(cpvo.Q4_K, rng.normal(0, 0.02, size=(n, k)).astype(np.float32))
     w2 = ctx.upload_weight(cpvo.Q4_K, q2, n, k)
     x2 = torch.from_numpy(rng.normal(0, 1, size=(m, k)).astype(np.float32)).cuda()
