@@ -54,15 +54,6 @@ __device__ __forceinline__ int ceil_log2_dev(int64_t v)
     return b;
 }
 
-// visibility of cache row j for node t: context rows, then the node's
-// ancestors and itself (tree, bit mask anc) or every node up to t (chain)
-__device__ __forceinline__ bool visible(int64_t j, int64_t n_past, int t, bool tree, uint64_t anc)
-{
-    if (j < n_past) return true;
-    const int64_t node = j - n_past;
-    return tree ? ((anc >> node) & 1ull) != 0 : node <= t;
-}
-
 // node t and its ancestors; a link that does not point to an earlier node
 // ends the walk (so a malformed array cannot loop)
 __device__ __forceinline__ uint64_t ancestors(const int32_t* parent, int t)
@@ -159,19 +150,35 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     int8_t(*s_p)[QB][CHUNK + 16] = (int8_t(*)[QB][CHUNK + 16]) & s_kbuf[0][0][0];   // [PL][query row][cache row]
     __shared__ int s_eq[QB], s_ek[CHUNK];
     __shared__ unsigned long long s_anc[QB];
+    __shared__ int s_vis[QB], s_orow[QB];      // (per query row; set with its limbs)
     __shared__ uint64_t s_etab[32];                     // the expf table
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid < 32) {
         constexpr uint64_t etab[32] = CPV_EXP2F_TAB;
         s_etab[tid] = etab[tid];
     }
-    // KV head fastest: the last blocks dispatched are the heads' last chunk,
-    // the only one that can be short, and a short chunk costs little below
-    const int c = blockIdx.x / a.Hkv, kh = blockIdx.x % a.Hkv;
+    // KV head fastest, chunks last to first: the first blocks dispatched are
+    // those past the end (which exit at once) and the short last chunk (which
+    // costs little below), so the blocks that a full grid places on a CU
+    // beside another are full chunks beside those
+    const int c = (int)(gridDim.x / a.Hkv) - 1 - (int)(blockIdx.x / a.Hkv), kh = blockIdx.x % a.Hkv;
     const int64_t j0 = (int64_t)c * CHUNK;
     const int G = a.H / a.Hkv, LR = G * a.T;
     const int sub = tid % TPR;
     const bool tree = a.parent != nullptr;
+
+    // The grid's last 8 chunks may lie past the end or hold the short last
+    // one (a replayed round's grid serves a 1024-row range).  There n_past is
+    // read first: a chunk past the end exits before any load, and a bounded
+    // chunk's loads stay below row n (the rows past it read row n - 1 again).
+    const bool tail = a.pos != nullptr && c >= (int)(gridDim.x / a.Hkv) - 8;
+    const bool bounded = a.pos == nullptr || tail;
+    int64_t n_past = a.n_past;
+    if (tail) {
+        n_past = a.pos[a.pos_sel];
+        if (j0 >= n_past + a.T) return;        // (the whole workgroup, before any barrier)
+    }
+    const int64_t lim = bounded ? n_past + a.T : a.kv_rows;   // (a.kv_rows = n without positions)
 
     // ---- q and K go out first, at clamped (in-bounds) rows, with no branch
     // around a load (a branch makes the compiler wait for every load at the join)
@@ -186,13 +193,13 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
 #pragma unroll
         for (int i = 0; i < 4; i++) qv[i] = ((const float4*)src)[i];
     }
-    // (rows clamped to the cache's: the chunk's end is known once n_past is)
+    // (elsewhere rows clamped to the cache's: the chunk's end is known once n_past is)
     // LC: kv[p] = 16 hi limbs, 16 lo limbs of the row's head, ekv[p] its exponent
     uint4 kv[KP][2];
     int ekv[KP];
 #pragma unroll
     for (int p = 0; p < KP; p++) {
-        const int64_t row = j0 + rq + p * RPP, rc = row < a.kv_rows ? row : a.kv_rows - 1;
+        const int64_t row = j0 + rq + p * RPP, rc = row < lim ? row : lim - 1;
         if constexpr (LC) {
             const int8_t* kr = a.kl + rc * a.k_row;
             const int8_t* src = kr + (int64_t)kh * 2 * D + sub * 16;
@@ -205,7 +212,8 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
             kv[p][1] = *(const uint4*)(src + 8);
         }
     }
-    const int64_t n_past = a.pos ? a.pos[a.pos_sel] : a.n_past, n_all = n_past + a.T;
+    if (a.pos && !tail) n_past = a.pos[a.pos_sel];
+    const int64_t n_all = n_past + a.T;
     if (j0 >= n_all) return;                   // a chunk past the end (the whole workgroup, before any barrier)
     const int nj = (int)(n_all - j0 < CHUNK ? n_all - j0 : CHUNK);
     // ---- query rows lr = blockIdx.z * 32 + r: token t = lr / G, head kh * G + lr % G
@@ -223,8 +231,15 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
         store16(&s_qh[rq][sub * 16], hi);
         store16(&s_ql[rq][sub * 16], lo);
         if (sub == 0) {
+            // the row's visible cache rows in this chunk: the first s_vis of
+            // them (the context, and for a chain its nodes up to t), then for
+            // a tree the ancestors' bits of s_anc; nothing for a row past LR
+            const int t = lrc / G;
+            const int64_t vis = (tree ? n_past : n_past + t + 1) - j0;
             s_eq[rq] = e;
-            s_anc[rq] = (tree && qok) ? ancestors(a.parent, lrq / G) : 0ull;
+            s_vis[rq] = !qok ? 0 : vis < 0 ? 0 : vis < nj ? (int)vis : nj;
+            s_anc[rq] = (tree && qok) ? ancestors(a.parent, t) : 0ull;
+            s_orow[rq] = t * a.H + kh * G + lrc % G;
         }
     }
     // ---- the chunk's cache rows of this KV head
@@ -262,20 +277,23 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     // lane (c16, g4) holds column 16 cb + c16 and rows 64 ks + 16 g4 .. +15,
     // the B operands of the P V MFMAs, as the VLIMBS signed 8-bit limbs of
     // vq = rint(v 2^VBITS).  Segments past the cache's end (wholly: v_stride
-    // is a multiple of 16, or of 8 for halves) read its last one; those rows
+    // is a multiple of 16, or of 8 for halves) read its last one, and in a
+    // bounded chunk those past n read the one holding row n - 1; those rows
     // carry weight 0.
     constexpr int NCB = D / 16;                 // d-blocks
     static_assert((CT / 64) % NCB == 0, "waves per d-block");
     const int cb = wave % NCB, c16 = lane & 15, g4 = lane >> 4;
     const int dcol = cb * 16 + c16;
     v4i vb[2][VLIMBS];
+    const int64_t vlast16 = bounded ? (lim - 1) & ~(int64_t)15 : a.v_stride - 16;
+    const int64_t vlast8 = bounded ? (lim - 1) & ~(int64_t)7 : a.v_stride - 8;
     uint4 vraw[2][2];
     if constexpr (LC) {
         // (a segment's limbs lie together: one 64-byte read)
         const int8_t* vbase = a.vl + ((int64_t)kh * D + dcol) * a.v_stride * VLIMBS;
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
-            const int64_t sj = j0 + ks * 64 + g4 * 16, sjc = sj < a.v_stride ? sj : a.v_stride - 16;
+            const int64_t sj = j0 + ks * 64 + g4 * 16, sjc = sj <= vlast16 ? sj : vlast16;
 #pragma unroll
             for (int l = 0; l < VLIMBS; l++) vb[ks][l] = *(const v4i*)(vbase + sjc * VLIMBS + 16 * l);
         }
@@ -285,14 +303,18 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
         for (int ks = 0; ks < 2; ks++)
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                const int64_t sj = j0 + ks * 64 + g4 * 16 + 8 * h, sjc = sj < a.v_stride ? sj : a.v_stride - 8;
+                const int64_t sj = j0 + ks * 64 + g4 * 16 + 8 * h, sjc = sj <= vlast8 ? sj : vlast8;
                 vraw[ks][h] = *(const uint4*)(vrow + sjc);
             }
     }
     __syncthreads();
 
-    // ---- scores: 2 x 8 blocks of 16 x 16 (query rows x cache rows), 2 per wave
-    for (int blk = wave; blk < 2 * (CHUNK / 16); blk += CT / 64) {
+    // ---- scores: 2 x 8 blocks of 16 x 16 (query rows x cache rows), 2 per
+    // wave; a chunk of at most 64 rows (the short last one) has only its
+    // first half, and the softmax and P V below skip the second
+    const bool half = nj <= CHUNK / 2;
+    const int nblk = half ? CHUNK / 16 : 2 * (CHUNK / 16);
+    for (int blk = wave; blk < nblk; blk += CT / 64) {
         const int qb = blk & 1, jb = blk >> 1;
         v4i hh = {0, 0, 0, 0}, mix = {0, 0, 0, 0}, ll = {0, 0, 0, 0};
         const int ar = qb * 16 + (lane & 15), bc = jb * 16 + (lane & 15), kg = (lane >> 4) * 16;
@@ -306,23 +328,20 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
             mix = __builtin_amdgcn_mfma_i32_16x16x64_i8(qlv, khv, mix, 0, 0, 0);
             ll = __builtin_amdgcn_mfma_i32_16x16x64_i8(qlv, klv, ll, 0, 0, 0);
         }
-        // lane holds query rows 4 (lane/16) + i of the block, cache row bc
+        // lane holds query rows 4 (lane/16) + i of the block, cache row bc.
+        // S = hh 2^16 + mix 2^8 + ll is exact in binary64 (|S| < 2^37), the
+        // score one rounding of S 2^(eq+ek-28): 0 when either row is all
+        // zero, as its limbs are (and blocks past the chunk's end kept S = 0)
         const int ek = s_ek[bc];
+        const int64_t node = j0 + bc - n_past;   // (a tree node when in [0, 64))
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int r = qb * 16 + 4 * (lane >> 4) + i;
-            const int lr = blockIdx.z * QB + r;
-            float w = -INFINITY;
-            if (lr < LR && bc < nj && visible(j0 + bc, n_past, lr / G, tree, s_anc[r])) {
-                const int eq = s_eq[r];
-                float sc = 0.0f;
-                if (eq != E_EMPTY && ek != E_EMPTY) {
-                    const int64_t S = (int64_t)hh[i] * 65536 + (int64_t)mix[i] * 256 + (int64_t)ll[i];
-                    sc = (float)ldexp((double)S, eq + ek - 28);
-                }
-                w = sc * a.scale;
-            }
-            s_w[r][bc] = w;
+            bool vis = bc < s_vis[r];
+            if (tree) vis = vis || ((uint64_t)node < 64 && ((s_anc[r] >> node) & 1ull));
+            const double S = __builtin_fma((double)hh[i], 65536.0, (double)(mix[i] * 256 + ll[i]));
+            const float sc = (float)ldexp(S, s_eq[r] + ek - 28);
+            s_w[r][bc] = vis ? sc * a.scale : -INFINITY;
         }
     }
     __syncthreads();
@@ -339,7 +358,8 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
         float w[8];
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const float4 w4 = *(const float4*)&s_w[r][4 * part + 64 * i];
+            const float4 w4 = i == 0 || !half ? *(const float4*)&s_w[r][4 * part + 64 * i]
+                                              : float4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
             w[4 * i] = w4.x;
             w[4 * i + 1] = w4.y;
             w[4 * i + 2] = w4.z;
@@ -352,12 +372,13 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
         int z = 0;
 #pragma unroll
         for (int i = 0; i < 2; i++) {
+            if (i == 1 && half) break;
             uint32_t pk[PL] = {};
 #pragma unroll
             for (int k = 0; k < 4; k++) {
                 const float wv = w[4 * i + k];
-                int q = 0;
-                if (wv != -INFINITY) q = (int)rintf(ldexpf(cpv_expf_t(wv - m, s_etab), PBITS));
+                const int qe = (int)rintf(ldexpf(cpv_expf_sel(wv - m, s_etab), PBITS));   // (every lane)
+                const int q = wv != -INFINITY ? qe : 0;
                 z += q;
                 int8_t l[PL];
                 balanced_limbs<PL>(q, l);
@@ -369,8 +390,7 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
         }
         z = cpv_group_reduce<SPR>(z, cpv_op_add());
         if (part == 0 && lr < LR) {
-            const int t = lr / G, h = kh * G + lr % G;
-            const int64_t row = (int64_t)c * a.T * a.H + (int64_t)t * a.H + h;
+            const int64_t row = (int64_t)c * a.T * a.H + s_orow[r];
             a.mc[row] = m;
             a.zc[row] = z;
         }
@@ -411,6 +431,7 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
         for (int q = 0; q < PL + VLIMBS - 1; q++) acc[q] = v4i{0, 0, 0, 0};
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
+            if (ks == 1 && half) break;
             v4i pa[PL];
 #pragma unroll
             for (int p = 0; p < PL; p++) pa[p] = *(const v4i*)&s_p[p][rb * 16 + c16][ks * 64 + g4 * 16];
@@ -427,8 +448,7 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
             int64_t S = 0;
 #pragma unroll
             for (int q = 0; q < PL + VLIMBS - 1; q++) S += (int64_t)acc[q][i] * ((int64_t)1 << (8 * q));
-            const int t = lr / G, h = kh * G + lr % G;
-            a.P[(((int64_t)c * a.T + t) * a.H + h) * D + dcol] = ldexpf((float)S, -(PBITS + VBITS));
+            a.P[((int64_t)c * a.T * a.H + s_orow[rb * 16 + 4 * g4 + i]) * D + dcol] = ldexpf((float)S, -(PBITS + VBITS));
         }
     }
 }

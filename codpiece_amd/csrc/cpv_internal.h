@@ -143,11 +143,8 @@ __host__ __device__ __forceinline__ uint16_t cpv_f2h(float f)
 // wherever the reference applies exp on the verify path (sigmoid, SiLU, the
 // sampler), so results match the CPU bit for bit.  cpv_expf_t takes the table
 // from the caller (a copy in LDS keeps global loads out of a kernel's phase).
-__host__ __device__ __forceinline__ float cpv_expf_t(float x, const uint64_t* tab)
+__host__ __device__ __forceinline__ float cpv_expf_core(float x, const uint64_t* tab)
 {
-    if (x != x) return x + x;
-    if (x > 0x1.62e42ep6f) return __builtin_huge_valf();
-    if (x < -0x1.9fe368p6f) return 0.0f;
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
     const double c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
@@ -163,6 +160,23 @@ __host__ __device__ __forceinline__ float cpv_expf_t(float x, const uint64_t* ta
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     return (float)(y * s);
+}
+__host__ __device__ __forceinline__ float cpv_expf_t(float x, const uint64_t* tab)
+{
+    if (x != x) return x + x;
+    if (x > 0x1.62e42ep6f) return __builtin_huge_valf();
+    if (x < -0x1.9fe368p6f) return 0.0f;
+    return cpv_expf_core(x, tab);
+}
+// the same values with no branches: the main path on x clamped to its range
+// (NaN to the low end), kept there by an empty asm statement the compiler
+// cannot sink into a branch, then the special cases selected
+__device__ __forceinline__ float cpv_expf_sel(float x, const uint64_t* tab)
+{
+    constexpr float lo = -0x1.9fe368p6f, hi = 0x1.62e42ep6f;
+    float y = cpv_expf_core(fminf(fmaxf(x, lo), hi), tab);
+    __asm__ volatile("" : "+v"(y));
+    return x != x ? x + x : x > hi ? __builtin_huge_valf() : x < lo ? 0.0f : y;
 }
 __host__ __device__ __forceinline__ float cpv_expf(float x)
 {
