@@ -88,34 +88,39 @@ struct ChunkArgs {
 };
 
 // an integer as L signed 8-bit limbs, x = sum l_i 256^i with l_i in
-// [-128, 127] below the top limb (which takes the rest)
+// [-128, 127] below the top limb (which takes the rest), as the bytes of one
+// dword: byte i of x + K (K = 128 in each lower byte) is l_i + 128 below the
+// top, the top limb itself last, so XOR with K leaves each l_i
 template <int L>
-__device__ __forceinline__ void balanced_limbs(int x, int8_t* l)
+__device__ __forceinline__ uint32_t packed_limbs(int x)
 {
-#pragma unroll
-    for (int i = 0; i < L - 1; i++) {
-        const int li = ((x + 128) & 255) - 128;
-        l[i] = (int8_t)li;
-        x = (x - li) >> 8;
-    }
-    l[L - 1] = (int8_t)x;
+    constexpr uint32_t K = 0x80808080u >> (8 * (5 - L));
+    return ((uint32_t)x + K) ^ K;
 }
 
-// pack 16 limbs of one kind into 4 dwords and store them as one 16-byte LDS write
-__device__ __forceinline__ void store16(int8_t* dst, const int8_t* v)
+// out[p] = byte p of w[0], w[1], w[2], w[3] (w[0]'s lowest), p < L: four
+// values' limb p side by side, as the MFMA operands take them
+// (v_perm_b32 picks bytes 0-3 from its second source, 4-7 from its first)
+template <int L>
+__device__ __forceinline__ void limb_transpose(const uint32_t* w, uint32_t* out)
 {
-    uint32_t w[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-        w[i] = (uint32_t)(uint8_t)v[4 * i] | ((uint32_t)(uint8_t)v[4 * i + 1] << 8) |
-               ((uint32_t)(uint8_t)v[4 * i + 2] << 16) | ((uint32_t)(uint8_t)v[4 * i + 3] << 24);
-    *(uint4*)dst = uint4{w[0], w[1], w[2], w[3]};
+    const uint32_t a01 = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);   // w0.0 w1.0 w0.1 w1.1
+    const uint32_t a23 = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);
+    out[0] = __builtin_amdgcn_perm(a23, a01, 0x05040100u);
+    out[1] = __builtin_amdgcn_perm(a23, a01, 0x07060302u);
+    if constexpr (L > 2) {
+        const uint32_t b01 = __builtin_amdgcn_perm(w[1], w[0], 0x07030602u);   // w0.2 w1.2 w0.3 w1.3
+        const uint32_t b23 = __builtin_amdgcn_perm(w[3], w[2], 0x07030602u);
+        out[2] = __builtin_amdgcn_perm(b23, b01, 0x05040100u);
+        if constexpr (L > 3) out[3] = __builtin_amdgcn_perm(b23, b01, 0x07060302u);
+    }
 }
 
 // the limbs of 16 f16-exact values at the exponent of the largest |value| of
-// their row (a row spans TPR consecutive lanes)
+// their row (a row spans TPR consecutive lanes): lo[j] and hi[j] hold values
+// 4j .. 4j + 3
 template <int TPR>
-__device__ __forceinline__ int row_limbs(const float* v, int8_t* hi, int8_t* lo)
+__device__ __forceinline__ int row_limbs(const float* v, uint32_t* hi, uint32_t* lo)
 {
     float mx = 0.0f;
 #pragma unroll
@@ -124,7 +129,14 @@ __device__ __forceinline__ int row_limbs(const float* v, int8_t* hi, int8_t* lo)
     int e = E_EMPTY;
     if (mx > 0.0f) frexpf(mx, &e);
 #pragma unroll
-    for (int i = 0; i < 16; i++) cpv_k_limbs(v[i], e, &hi[i], &lo[i]);
+    for (int j = 0; j < 4; j++) {
+        uint32_t w[4], t[2];
+#pragma unroll
+        for (int k = 0; k < 4; k++) w[k] = packed_limbs<2>(cpv_k_fixed(v[4 * j + k], e));
+        limb_transpose<2>(w, t);
+        lo[j] = t[0];
+        hi[j] = t[1];
+    }
     return e;
 }
 
@@ -226,10 +238,10 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
             v[4 * i + 2] = qok ? cpv_h2f(cpv_f2h(qv[i].z)) : 0.0f;
             v[4 * i + 3] = qok ? cpv_h2f(cpv_f2h(qv[i].w)) : 0.0f;
         }
-        int8_t hi[16], lo[16];
+        uint32_t hi[4], lo[4];
         const int e = row_limbs<TPR>(v, hi, lo);
-        store16(&s_qh[rq][sub * 16], hi);
-        store16(&s_ql[rq][sub * 16], lo);
+        *(uint4*)&s_qh[rq][sub * 16] = uint4{hi[0], hi[1], hi[2], hi[3]};
+        *(uint4*)&s_ql[rq][sub * 16] = uint4{lo[0], lo[1], lo[2], lo[3]};
         if (sub == 0) {
             // the row's visible cache rows in this chunk: the first s_vis of
             // them (the context, and for a chain its nodes up to t), then for
@@ -257,19 +269,16 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
         }
         const uint32_t wds[8] = {kv[p][0].x, kv[p][0].y, kv[p][0].z, kv[p][0].w,
                                  kv[p][1].x, kv[p][1].y, kv[p][1].z, kv[p][1].w};
-        int8_t hi[16], lo[16];
+        uint32_t hi[4] = {0, 0, 0, 0}, lo[4] = {0, 0, 0, 0};   // (what row_limbs gives an all-zero row)
         int e = E_EMPTY;
         if (r < nj) {                          // the same for the TPR lanes of a row
             float v[16];
 #pragma unroll
             for (int i = 0; i < 16; i++) v[i] = cpv_h2f((uint16_t)(wds[i >> 1] >> (16 * (i & 1))));
             e = row_limbs<TPR>(v, hi, lo);
-        } else {                               // what row_limbs gives an all-zero row
-#pragma unroll
-            for (int i = 0; i < 16; i++) hi[i] = lo[i] = 0;
         }
-        store16(&s_kh[r][sub * 16], hi);
-        store16(&s_kl[r][sub * 16], lo);
+        *(uint4*)&s_kh[r][sub * 16] = uint4{hi[0], hi[1], hi[2], hi[3]};
+        *(uint4*)&s_kl[r][sub * 16] = uint4{lo[0], lo[1], lo[2], lo[3]};
         if (sub == 0) s_ek[r] = e;
     }
     // ---- this wave's V operands, in flight through the scores and the
@@ -373,18 +382,16 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             if (i == 1 && half) break;
-            uint32_t pk[PL] = {};
+            uint32_t wq[4], pk[PL];
 #pragma unroll
             for (int k = 0; k < 4; k++) {
                 const float wv = w[4 * i + k];
                 const int qe = (int)rintf(ldexpf(cpv_expf_sel(wv - m, s_etab), PBITS));   // (every lane)
                 const int q = wv != -INFINITY ? qe : 0;
                 z += q;
-                int8_t l[PL];
-                balanced_limbs<PL>(q, l);
-#pragma unroll
-                for (int p = 0; p < PL; p++) pk[p] |= (uint32_t)(uint8_t)l[p] << (8 * k);
+                wq[k] = packed_limbs<PL>(q);
             }
+            limb_transpose<PL>(wq, pk);
 #pragma unroll
             for (int p = 0; p < PL; p++) *(uint32_t*)&s_p[p][r][4 * part + 64 * i] = pk[p];
         }
@@ -399,19 +406,19 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     if constexpr (!LC) {
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
-            uint32_t pk[VLIMBS][4] = {};
+            uint32_t pk[VLIMBS][4];
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const uint32_t wd[4] = {vraw[ks][h].x, vraw[ks][h].y, vraw[ks][h].z, vraw[ks][h].w};
+            for (int j = 0; j < 4; j++) {      // values 4j .. 4j + 3 of the segment: half j / 2 of the raw read
+                const uint4 raw = vraw[ks][j >> 1];
+                const uint32_t wd[2] = {(j & 1) ? raw.z : raw.x, (j & 1) ? raw.w : raw.y};
+                uint32_t w[4], t[VLIMBS];
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float v = cpv_h2f((uint16_t)(wd[e >> 1] >> (16 * (e & 1))));
-                    int8_t l[VLIMBS];
-                    balanced_limbs<VLIMBS>((int)rintf(ldexpf(v, VBITS)), l);
-                    const int k = 8 * h + e;
+                for (int k = 0; k < 4; k++)
+                    w[k] = packed_limbs<VLIMBS>(
+                        (int)rintf(ldexpf(cpv_h2f((uint16_t)(wd[k >> 1] >> (16 * (k & 1)))), VBITS)));
+                limb_transpose<VLIMBS>(w, t);
 #pragma unroll
-                    for (int p = 0; p < VLIMBS; p++) pk[p][k >> 2] |= (uint32_t)(uint8_t)l[p] << (8 * (k & 3));
-                }
+                for (int p = 0; p < VLIMBS; p++) pk[p][j] = t[p];
             }
 #pragma unroll
             for (int p = 0; p < VLIMBS; p++) vb[ks][p] = v4i{(int)pk[p][0], (int)pk[p][1], (int)pk[p][2], (int)pk[p][3]};

@@ -395,10 +395,13 @@ __host__ __device__ __forceinline__ int64_t cpv_k_row_bytes(int h_kv, int d)
 {
     return (int64_t)h_kv * 2 * d + ((int64_t)h_kv * 4 + 15) / 16 * 16;
 }
+__device__ __forceinline__ int cpv_k_fixed(float kf, int e)
+{
+    return e != CPV_E_EMPTY ? (int)rintf(ldexpf(kf, 14 - e)) : 0;
+}
 __device__ __forceinline__ void cpv_k_limbs(float kf, int e, int8_t* hi, int8_t* lo)
 {
-    int f = 0;
-    if (e != CPV_E_EMPTY) f = (int)rintf(ldexpf(kf, 14 - e));
+    const int f = cpv_k_fixed(kf, e);
     const int h = (f + 128) >> 8;
     *hi = (int8_t)h;
     *lo = (int8_t)(f - 256 * h);
