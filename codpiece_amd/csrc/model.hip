@@ -324,14 +324,20 @@ struct RowLds {
     long long red_s[RW], red_s2[RW];
 };
 
+// (the RW slots are read at once, those past the block's nw waves masked:
+// a loop to nw would wait on each read in turn)
 __device__ float row_max(float v, float* slot, int nw)
 {
     const int tid = threadIdx.x;
     v = cpv_wave_reduce(v, cpv_op_max());
     if ((tid & 63) == 0) slot[tid >> 6] = v;
     __syncthreads();
-    float r = slot[0];
-    for (int i = 1; i < nw; i++) r = fmaxf(r, slot[i]);
+    float sv[RW];
+#pragma unroll
+    for (int i = 0; i < RW; i++) sv[i] = slot[i];
+    float r = sv[0];
+#pragma unroll
+    for (int i = 1; i < RW; i++) r = i < nw ? fmaxf(r, sv[i]) : r;
     return r;
 }
 
@@ -341,8 +347,12 @@ __device__ long long row_sum(long long v, long long* slot, int nw)
     v = cpv_wave_reduce(v, cpv_op_add());
     if ((tid & 63) == 0) slot[tid >> 6] = v;
     __syncthreads();
+    long long sv[RW];
+#pragma unroll
+    for (int i = 0; i < RW; i++) sv[i] = slot[i];
     long long r = 0;
-    for (int i = 0; i < nw; i++) r += slot[i];
+#pragma unroll
+    for (int i = 0; i < RW; i++) r += i < nw ? sv[i] : 0;
     return r;
 }
 
@@ -579,6 +589,7 @@ __global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
         // and sum do not wait for them)
         constexpr int FB = 48;
         const int c0 = tl < nchg ? tl : 0;
+        const float gv = a.gate[(int64_t)m * n + ec];           // (the gate goes out first too)
         const float mc0 = a.part.mc[(int64_t)c0 * rows + rr];
         const int64_t zc0 = a.part.zc[(int64_t)c0 * rows + rr];
         const float* pr = a.part.P + (int64_t)rr * hd + (ec - h * hd);
@@ -620,7 +631,6 @@ __global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
         if (nch > FB) o = cpv_fold_chain_from(pr, pcs, s_f[lh], nch, FB, o);
         __syncthreads();
         const float at = o * s_inv[lh];
-        const float gv = a.gate[(int64_t)m * n + ec];
         const float sig = 1.0f / (1.0f + cpv_expf(-gv));
         val = e < n ? at * sig : 0.0f;
     } else if (SRC == SRC_GATE) {
