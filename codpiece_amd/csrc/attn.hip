@@ -44,7 +44,8 @@ constexpr int PBITS = 22;           // a weight e in (0, 1] as p = rint(e 2^22):
 constexpr int PL = 3;
 constexpr int VBITS = CPV_ATTN_VBITS;   // an f16 value v as vq = rint(v 2^14): |vq| < 2^30, VLIMBS limbs
 constexpr int VLIMBS = CPV_ATTN_VLIMBS;
-constexpr int QB = 32;              // query rows per scores workgroup
+constexpr int QB_CHAIN = 32;        // query rows per chunk workgroup: chains and prefill
+constexpr int QB_WIDE = 48;         //   and when a KV head has more than 32 (a 16-node tree's 80: 48 + 32)
 constexpr int E_EMPTY = CPV_E_EMPTY;   // exponent of an all-zero vector
 
 __device__ __forceinline__ int ceil_log2_dev(int64_t v)
@@ -140,26 +141,30 @@ __device__ __forceinline__ int row_limbs(const float* v, uint32_t* hi, uint32_t*
     return e;
 }
 
-// one 128-row chunk of the cache against 32 query rows of one KV head
+// one 128-row chunk of the cache against QB query rows of one KV head
 constexpr int CT = 512;             // threads of a chunk workgroup (8 waves)
 
 // LC: K and V come from a session's limb caches (a.kl, a.vl); else from the
-// API's f16 caches (a.kc, a.vt), converted here
-template <int D, bool LC>
+// API's f16 caches (a.kc, a.vt), converted here.  QB: query rows per
+// workgroup, a multiple of 16 (MFMA row blocks)
+template <int D, bool LC, int QB>
 __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
 {
+    static_assert(QB % 16 == 0, "16-row query blocks");
+    constexpr int QBB = QB / 16;               // query row blocks
     constexpr int TPR = D / 16;                // threads per row when converting (16 values each)
     constexpr int RPP = CT / TPR;              // rows per pass
+    constexpr int QP = (QB + RPP - 1) / RPP;   // query conversion passes
     // rows padded by 16 bytes (limbs) and 4 floats (scores): the MFMA operand
     // reads and the score writes then fall on distinct LDS banks.  The
     // weights' limbs take the K limbs' place once the scores are done.
+    constexpr int KBUF = 2 * CHUNK * (D + 16), PBUF = PL * QB * (CHUNK + 16);
     __shared__ __align__(16) int8_t s_qh[QB][D + 16], s_ql[QB][D + 16];
-    __shared__ __align__(16) int8_t s_kbuf[2][CHUNK][D + 16];
+    __shared__ __align__(16) int8_t s_kbuf[KBUF > PBUF ? KBUF : PBUF];
     __shared__ __align__(16) float s_w[QB][CHUNK + 4];     // scores
-    static_assert(PL * QB * (CHUNK + 16) <= sizeof(s_kbuf), "the weights' limbs fit the K limbs' space");
-    int8_t(*s_kh)[D + 16] = s_kbuf[0];
-    int8_t(*s_kl)[D + 16] = s_kbuf[1];
-    int8_t(*s_p)[QB][CHUNK + 16] = (int8_t(*)[QB][CHUNK + 16]) & s_kbuf[0][0][0];   // [PL][query row][cache row]
+    int8_t(*s_kh)[D + 16] = (int8_t(*)[D + 16]) & s_kbuf[0];
+    int8_t(*s_kl)[D + 16] = (int8_t(*)[D + 16]) & s_kbuf[CHUNK * (D + 16)];
+    int8_t(*s_p)[QB][CHUNK + 16] = (int8_t(*)[QB][CHUNK + 16]) & s_kbuf[0];   // [PL][query row][cache row]
     __shared__ int s_eq[QB], s_ek[CHUNK];
     __shared__ unsigned long long s_anc[QB];
     __shared__ int s_vis[QB], s_orow[QB];      // (per query row; set with its limbs)
@@ -195,15 +200,15 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     // ---- q and K go out first, at clamped (in-bounds) rows, with no branch
     // around a load (a branch makes the compiler wait for every load at the join)
     constexpr int KP = CHUNK / RPP > 0 ? CHUNK / RPP : 1;   // K passes
-    const int rq = tid / TPR;                  // query row converted by this thread (if < QB)
-    const int lrq = blockIdx.z * QB + rq;
-    const bool qok = rq < QB && lrq < LR;
-    const int lrc = qok ? lrq : 0;
-    float4 qv[4];
-    {
+    const int rq = tid / TPR;                  // query row converted by this thread in pass 0
+    float4 qv[QP][4];
+#pragma unroll
+    for (int qp = 0; qp < QP; qp++) {          // (rows past QB or LR read row 0)
+        const int lrq = blockIdx.z * QB + rq + qp * RPP;
+        const int lrc = rq + qp * RPP < QB && lrq < LR ? lrq : 0;
         const float* src = a.q + ((int64_t)(lrc / G) * a.H + kh * G + lrc % G) * D + sub * 16;
 #pragma unroll
-        for (int i = 0; i < 4; i++) qv[i] = ((const float4*)src)[i];
+        for (int i = 0; i < 4; i++) qv[qp][i] = ((const float4*)src)[i];
     }
     // (elsewhere rows clamped to the cache's: the chunk's end is known once n_past is)
     // LC: kv[p] = 16 hi limbs, 16 lo limbs of the row's head, ekv[p] its exponent
@@ -228,30 +233,36 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     const int64_t n_all = n_past + a.T;
     if (j0 >= n_all) return;                   // a chunk past the end (the whole workgroup, before any barrier)
     const int nj = (int)(n_all - j0 < CHUNK ? n_all - j0 : CHUNK);
-    // ---- query rows lr = blockIdx.z * 32 + r: token t = lr / G, head kh * G + lr % G
-    if (rq < QB) {
+    // ---- query rows lr = blockIdx.z * QB + r: token t = lr / G, head kh * G + lr % G
+#pragma unroll
+    for (int qp = 0; qp < QP; qp++) {
+        const int r = rq + qp * RPP;
+        if (r >= QB) break;                    // (threads past the block's rows in the last pass)
+        const int lrq = blockIdx.z * QB + r;
+        const bool qok = lrq < LR;
+        const int lrc = qok ? lrq : 0;
         float v[16];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            v[4 * i + 0] = qok ? cpv_h2f(cpv_f2h(qv[i].x)) : 0.0f;
-            v[4 * i + 1] = qok ? cpv_h2f(cpv_f2h(qv[i].y)) : 0.0f;
-            v[4 * i + 2] = qok ? cpv_h2f(cpv_f2h(qv[i].z)) : 0.0f;
-            v[4 * i + 3] = qok ? cpv_h2f(cpv_f2h(qv[i].w)) : 0.0f;
+            v[4 * i + 0] = qok ? cpv_h2f(cpv_f2h(qv[qp][i].x)) : 0.0f;
+            v[4 * i + 1] = qok ? cpv_h2f(cpv_f2h(qv[qp][i].y)) : 0.0f;
+            v[4 * i + 2] = qok ? cpv_h2f(cpv_f2h(qv[qp][i].z)) : 0.0f;
+            v[4 * i + 3] = qok ? cpv_h2f(cpv_f2h(qv[qp][i].w)) : 0.0f;
         }
         uint32_t hi[4], lo[4];
         const int e = row_limbs<TPR>(v, hi, lo);
-        *(uint4*)&s_qh[rq][sub * 16] = uint4{hi[0], hi[1], hi[2], hi[3]};
-        *(uint4*)&s_ql[rq][sub * 16] = uint4{lo[0], lo[1], lo[2], lo[3]};
+        *(uint4*)&s_qh[r][sub * 16] = uint4{hi[0], hi[1], hi[2], hi[3]};
+        *(uint4*)&s_ql[r][sub * 16] = uint4{lo[0], lo[1], lo[2], lo[3]};
         if (sub == 0) {
             // the row's visible cache rows in this chunk: the first s_vis of
             // them (the context, and for a chain its nodes up to t), then for
             // a tree the ancestors' bits of s_anc; nothing for a row past LR
             const int t = lrc / G;
             const int64_t vis = (tree ? n_past : n_past + t + 1) - j0;
-            s_eq[rq] = e;
-            s_vis[rq] = !qok ? 0 : vis < 0 ? 0 : vis < nj ? (int)vis : nj;
-            s_anc[rq] = (tree && qok) ? ancestors(a.parent, t) : 0ull;
-            s_orow[rq] = t * a.H + kh * G + lrc % G;
+            s_eq[r] = e;
+            s_vis[r] = !qok ? 0 : vis < 0 ? 0 : vis < nj ? (int)vis : nj;
+            s_anc[r] = (tree && qok) ? ancestors(a.parent, t) : 0ull;
+            s_orow[r] = t * a.H + kh * G + lrc % G;
         }
     }
     // ---- the chunk's cache rows of this KV head
@@ -318,13 +329,13 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     }
     __syncthreads();
 
-    // ---- scores: 2 x 8 blocks of 16 x 16 (query rows x cache rows), 2 per
-    // wave; a chunk of at most 64 rows (the short last one) has only its
-    // first half, and the softmax and P V below skip the second
+    // ---- scores: QBB x 8 blocks of 16 x 16 (query rows x cache rows); a
+    // chunk of at most 64 rows (the short last one) has only its first half,
+    // and the softmax and P V below skip the second
     const bool half = nj <= CHUNK / 2;
-    const int nblk = half ? CHUNK / 16 : 2 * (CHUNK / 16);
+    const int nblk = half ? QBB * (CHUNK / 32) : QBB * (CHUNK / 16);
     for (int blk = wave; blk < nblk; blk += CT / 64) {
-        const int qb = blk & 1, jb = blk >> 1;
+        const int qb = blk % QBB, jb = blk / QBB;
         v4i hh = {0, 0, 0, 0}, mix = {0, 0, 0, 0}, ll = {0, 0, 0, 0};
         const int ar = qb * 16 + (lane & 15), bc = jb * 16 + (lane & 15), kg = (lane >> 4) * 16;
 #pragma unroll
@@ -357,12 +368,14 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
 
     // ---- the chunk's softmax: SPR threads per query row, 8 cache rows each
     // (4 part + 64 i + k: 16-byte reads of the scores, one dword per limb
-    // written); the weights in fixed point, p = rint(e 2^PBITS), as PL signed
-    // 8-bit limbs, and Z_c = sum p
-    {
-        constexpr int SPR = CT / QB;
-        static_assert(CHUNK == 8 * SPR, "8 cache rows per thread");
-        const int r = tid / SPR, part = tid % SPR;
+    // written), CT / SPR rows per pass; the weights in fixed point,
+    // p = rint(e 2^PBITS), as PL signed 8-bit limbs, and Z_c = sum p
+    constexpr int SPR = CHUNK / 8, SRP = CT / SPR;
+    static_assert(QB % SRP == 0 || QB % SRP == SRP / 2, "softmax passes of whole row groups");
+#pragma unroll
+    for (int r0 = 0; r0 < QB; r0 += SRP) {
+        const int r = r0 + tid / SPR, part = tid % SPR;
+        if (r >= QB) break;                    // (a half pass: whole waves past the rows)
         const int lr = blockIdx.z * QB + r;
         float w[8];
 #pragma unroll
@@ -551,9 +564,23 @@ cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const ui
     ca.k_row = cpv_k_row_bytes(Hkv, D);
     if (vl && (v_stride % 16 || ((uintptr_t)vl & 15) || ((uintptr_t)kl & 15)))
         return cpv_fail(ctx, CPV_EINVAL, "attention: limb caches need 16-byte aligned rows");
+    // a KV head's rows past 32 in blocks of 48 once there are 512 (chunk, KV
+    // head) units or more (a 16-node tree's 80 rows in two workgroups per
+    // chunk, not three): each stages and converts the chunk's K and V once for
+    // more rows, and two still fit a CU.  With fewer units the 32-row blocks'
+    // extra workgroups take no more passes over the CUs, and their shorter
+    // chains win (the 16-node tree at 4101 rows: 9.59 against 9.71 ms; at
+    // 32768 over the API's caches: 200 against 182 us)
+    const bool wide = LR > QB_CHAIN && (int64_t)nchunk * Hkv >= 512;
+    const int QB = wide ? QB_WIDE : QB_CHAIN;
     const dim3 cgrid((unsigned)(nchunk * Hkv), 1u, (unsigned)((LR + QB - 1) / QB));
-    if (vl) attn_chunk_kernel<D, true><<<cgrid, CT, 0, ctx->stream>>>(ca);
-    else attn_chunk_kernel<D, false><<<cgrid, CT, 0, ctx->stream>>>(ca);
+    if (wide) {
+        if (vl) attn_chunk_kernel<D, true, QB_WIDE><<<cgrid, CT, 0, ctx->stream>>>(ca);
+        else attn_chunk_kernel<D, false, QB_WIDE><<<cgrid, CT, 0, ctx->stream>>>(ca);
+    } else {
+        if (vl) attn_chunk_kernel<D, true, QB_CHAIN><<<cgrid, CT, 0, ctx->stream>>>(ca);
+        else attn_chunk_kernel<D, false, QB_CHAIN><<<cgrid, CT, 0, ctx->stream>>>(ca);
+    }
     if (out)
         attn_fold_kernel<D><<<(unsigned)rows, D, (size_t)nchunk * 12, ctx->stream>>>(ca.P, ca.mc, ca.zc, nchunk,
                                                                                   rows, out);

@@ -299,3 +299,40 @@ def test_wide_rows_round_is_bit_exact():
     gm.free()
     om.free()
     ctx.close()
+
+
+def test_wide_query_blocks_at_long_context(models):
+    # From 512 (chunk, KV head) units on, a KV head's query rows past 32 run
+    # in 48-row blocks over the session's limb caches; the config-1 model (2
+    # KV heads) gets there at 32768 cached rows.  Each verify row depends only
+    # on its own token and the rows before it, so the first 8 rows of a
+    # 16-row verify (64 query rows per KV head: 48-row blocks) equal an 8-row
+    # verify (32 rows: one 32-row block) bit for bit, and a 16-node tree with
+    # linear parents (48-row blocks, ancestor masks) equals the 16-row chain.
+    from codpiece_amd.model import Session
+    ctx, gm, om = models
+    n = 32768
+    s = Session(gm, n + 64, max_batch=512)
+    rng = np.random.default_rng(21)
+    prompt = rng.integers(0, V, size=n).tolist()
+    print("case prefill 32768 rows", flush=True)
+    for c in range(0, n, 512):
+        s.prefill(prompt[c:c + 512])
+    s.set_pos(n, 0)
+    toks = rng.integers(0, V, size=16).tolist()
+    print("case 16-row chain", flush=True)
+    a = s.step_fused_cached(toks, 0, want_logits=True)
+    la, ha = a.logits.cpu().numpy(), a.hidden.cpu().numpy()
+    s.set_pos(n, 0)
+    print("case 8-row chain", flush=True)
+    b = s.step_fused_cached(toks[:8], 0, want_logits=True)
+    assert b.preds == a.preds[:8]
+    assert np.array_equal(b.logits.cpu().numpy().view(np.uint32), la[:8].view(np.uint32))
+    assert np.array_equal(b.hidden.cpu().numpy().view(np.uint32), ha[:8].view(np.uint32))
+    s.set_pos(n, 0)
+    print("case 16-node linear tree", flush=True)
+    t = s.verify_tree(toks, [-1] + list(range(15)), want_logits=True)
+    assert t.preds == a.preds
+    assert np.array_equal(t.logits.cpu().numpy().view(np.uint32), la.view(np.uint32))
+    assert np.array_equal(t.hidden.cpu().numpy().view(np.uint32), ha.view(np.uint32))
+    s.free()
