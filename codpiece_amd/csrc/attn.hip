@@ -510,7 +510,7 @@ __global__ __launch_bounds__(D) void attn_fold_kernel(const float* __restrict__ 
         s_inv = (float)(1.0 / Zt);
     }
     const float* pr = P + (int64_t)row * D + d;
-    const float o = cpv_fold_chain(pr, (int64_t)rows * D, s_f, nchunk);
+    const float o = cpv_fold_chain<32>(pr, (int64_t)rows * D, s_f, nchunk);   // (32 partials in flight per step)
     __syncthreads();
     out[(int64_t)row * D + d] = o * s_inv;
 }

@@ -432,10 +432,10 @@ struct cpv_attn_part {
 // out, at clamped in-bounds indexes and without a branch, one batch ahead of
 // the chain that consumes it
 // (from chunk c0 on, after the fold o of the chunks before it)
+template <int B = 16>
 __device__ __forceinline__ float cpv_fold_chain_from(const float* p, int64_t cs, const float* f, int n, int c0,
                                                      float o)
 {
-    constexpr int B = 16;
     float cur[B];
 #pragma unroll
     for (int i = 0; i < B; i++) cur[i] = p[(int64_t)(c0 + i < n ? c0 + i : n - 1) * cs];
@@ -457,9 +457,10 @@ __device__ __forceinline__ float cpv_fold_chain_from(const float* p, int64_t cs,
         if (c + i < n) o = fmaf(cur[i], f[c + i], o);
     return o;
 }
+template <int B = 16>
 __device__ __forceinline__ float cpv_fold_chain(const float* p, int64_t cs, const float* f, int n)
 {
-    return cpv_fold_chain_from(p, cs, f, n, 0, 0.0f);
+    return cpv_fold_chain_from<B>(p, cs, f, n, 0, 0.0f);
 }
 cpv_status cpv_attn_partials(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                              int64_t n_past, const int32_t* parent, int t, int h, int h_kv, int d, float scale,
