@@ -592,6 +592,10 @@ __global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
         const float gv = a.gate[(int64_t)m * n + ec];           // (the gate goes out first too)
         const float mc0 = a.part.mc[(int64_t)c0 * rows + rr];
         const int64_t zc0 = a.part.zc[(int64_t)c0 * rows + rr];
+        const int nch = a.part.pos ? (int)((a.part.pos[a.part.pos_sel] + a.part.t + 127) / 128) : nchg;
+        // (the compiler would otherwise issue the partials' loads first, and
+        // the first max and the chunk count would wait for all of them)
+        asm volatile("" ::: "memory");
         const float* pr = a.part.P + (int64_t)rr * hd + (ec - h * hd);
         const int64_t pcs = (int64_t)rows * hd;
         float pv[FB];
@@ -606,7 +610,6 @@ __global__ __launch_bounds__(256) void unit_kernel(RowArgs a)
             s_f[lh][c] = a.part.mc[(int64_t)c * rows + rr];
             s_z[lh][c] = ldexp((double)a.part.zc[(int64_t)c * rows + rr], -a.part.zbits);
         }
-        const int nch = a.part.pos ? (int)((a.part.pos[a.part.pos_sel] + a.part.t + 127) / 128) : nchg;
         for (int c = tl; c < nch; c += hd) M = fmaxf(M, s_f[lh][c]);
         M = cpv_wave_reduce(M, cpv_op_max());
         if (lane == 0) s_m[lh][wave - lh * wph] = M;
