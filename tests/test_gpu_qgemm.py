@@ -78,10 +78,11 @@ def test_qgemm_lm_head_q6_k(ctx, m):
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("tname", ["q4_k", "q6_k"])
 @pytest.mark.parametrize("m", [4, 9, 16])
-def test_qgemm_extreme_scales_and_zero_rows(ctx, m):
-    # 4 rows: the 4x4x4 kernel; 9 and 16: the 16x16x32 one
-    t = cpvo.Q4_K
+def test_qgemm_extreme_scales_and_zero_rows(ctx, tname, m):
+    # 4 rows: the 4x4x4 kernel; 9 and 16: the 16x16x32 ones
+    t = TYPES[tname]
     n, k = 32, 1024
     rng = np.random.default_rng(3)
     wf = rng.normal(0, 0.02, size=(n, k)).astype(np.float32)
