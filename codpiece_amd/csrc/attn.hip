@@ -329,39 +329,50 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     }
     __syncthreads();
 
-    // ---- scores: QBB x 8 blocks of 16 x 16 (query rows x cache rows); a
-    // chunk of at most 64 rows (the short last one) has only its first half,
-    // and the softmax and P V below skip the second
+    // ---- scores: QBB x 8 blocks of 16 x 16 (query rows x cache rows); wave
+    // w takes blocks w + 8 b, b < QBB, side by side, so that their MFMA
+    // chains interleave.  A block past the chunk's end meets all-zero K rows
+    // (S = 0) and is written as -inf, as every invisible score is; a chunk of
+    // at most 64 rows (the short last one) has only its first half read
+    // below, and the softmax and P V skip the second
     const bool half = nj <= CHUNK / 2;
-    const int nblk = half ? QBB * (CHUNK / 32) : QBB * (CHUNK / 16);
-    for (int blk = wave; blk < nblk; blk += CT / 64) {
-        const int qb = blk % QBB, jb = blk / QBB;
-        v4i hh = {0, 0, 0, 0}, mix = {0, 0, 0, 0}, ll = {0, 0, 0, 0};
-        const int ar = qb * 16 + (lane & 15), bc = jb * 16 + (lane & 15), kg = (lane >> 4) * 16;
+    {
+        const int kg = (lane >> 4) * 16;
+        v4i hh[QBB], mix[QBB], ll[QBB];
 #pragma unroll
-        for (int ks = 0; ks < D / 64; ks++) {
-            if (jb * 16 >= nj) break;          // a block past the chunk's end: every score is -inf
-            const v4i qhv = *(const v4i*)&s_qh[ar][ks * 64 + kg], qlv = *(const v4i*)&s_ql[ar][ks * 64 + kg];
-            const v4i khv = *(const v4i*)&s_kh[bc][ks * 64 + kg], klv = *(const v4i*)&s_kl[bc][ks * 64 + kg];
-            hh = __builtin_amdgcn_mfma_i32_16x16x64_i8(qhv, khv, hh, 0, 0, 0);
-            mix = __builtin_amdgcn_mfma_i32_16x16x64_i8(qhv, klv, mix, 0, 0, 0);
-            mix = __builtin_amdgcn_mfma_i32_16x16x64_i8(qlv, khv, mix, 0, 0, 0);
-            ll = __builtin_amdgcn_mfma_i32_16x16x64_i8(qlv, klv, ll, 0, 0, 0);
-        }
-        // lane holds query rows 4 (lane/16) + i of the block, cache row bc.
-        // S = hh 2^16 + mix 2^8 + ll is exact in binary64 (|S| < 2^37), the
-        // score one rounding of S 2^(eq+ek-28): 0 when either row is all
-        // zero, as its limbs are (and blocks past the chunk's end kept S = 0)
-        const int ek = s_ek[bc];
-        const int64_t node = j0 + bc - n_past;   // (a tree node when in [0, 64))
+        for (int b = 0; b < QBB; b++) hh[b] = mix[b] = ll[b] = v4i{0, 0, 0, 0};
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = qb * 16 + 4 * (lane >> 4) + i;
-            bool vis = bc < s_vis[r];
-            if (tree) vis = vis || ((uint64_t)node < 64 && ((s_anc[r] >> node) & 1ull));
-            const double S = __builtin_fma((double)hh[i], 65536.0, (double)(mix[i] * 256 + ll[i]));
-            const float sc = (float)ldexp(S, s_eq[r] + ek - 28);
-            s_w[r][bc] = vis ? sc * a.scale : -INFINITY;
+        for (int ks = 0; ks < D / 64; ks++)
+#pragma unroll
+            for (int b = 0; b < QBB; b++) {
+                const int blk = wave + (CT / 64) * b, qb = blk % QBB, jb = blk / QBB;
+                const int ar = qb * 16 + (lane & 15), bc = jb * 16 + (lane & 15);
+                const v4i qhv = *(const v4i*)&s_qh[ar][ks * 64 + kg], qlv = *(const v4i*)&s_ql[ar][ks * 64 + kg];
+                const v4i khv = *(const v4i*)&s_kh[bc][ks * 64 + kg], klv = *(const v4i*)&s_kl[bc][ks * 64 + kg];
+                hh[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qhv, khv, hh[b], 0, 0, 0);
+                mix[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qhv, klv, mix[b], 0, 0, 0);
+                mix[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qlv, khv, mix[b], 0, 0, 0);
+                ll[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qlv, klv, ll[b], 0, 0, 0);
+            }
+#pragma unroll
+        for (int b = 0; b < QBB; b++) {
+            const int blk = wave + (CT / 64) * b, qb = blk % QBB, jb = blk / QBB;
+            const int bc = jb * 16 + (lane & 15);
+            // lane holds query rows 4 (lane/16) + i of the block, cache row bc.
+            // S = hh 2^16 + mix 2^8 + ll is exact in binary64 (|S| < 2^37), the
+            // score one rounding of S 2^(eq+ek-28): 0 when either row is all
+            // zero, as its limbs are
+            const int ek = s_ek[bc];
+            const int64_t node = j0 + bc - n_past;   // (a tree node when in [0, 64))
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = qb * 16 + 4 * (lane >> 4) + i;
+                bool vis = bc < s_vis[r];
+                if (tree) vis = vis || ((uint64_t)node < 64 && ((s_anc[r] >> node) & 1ull));
+                const double S = __builtin_fma((double)hh[b][i], 65536.0, (double)(mix[b][i] * 256 + ll[b][i]));
+                const float sc = (float)ldexp(S, s_eq[r] + ek - 28);
+                s_w[r][bc] = vis ? sc * a.scale : -INFINITY;
+            }
         }
     }
     __syncthreads();
