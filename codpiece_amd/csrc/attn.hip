@@ -26,8 +26,9 @@
 //
 // Layout.  A session's caches hold limbs, written once per row and read by
 // the MFMAs with no conversion: K as each row's hi and lo limbs per KV head
-// with the heads' exponents (cpv_k_row_bytes), V as vq's limbs,
-// [h_kv * d][v_stride / 16][4][16].  The API's caches (cpv_attn) are f16:
+// (cpv_k_row_bytes), then the heads' exponents as a plane [h_kv][v_stride]
+// (a chunk's 128 exponents of one head in 512 contiguous bytes), V as vq's
+// limbs, [h_kv * d][v_stride / 16][4][16].  The API's caches (cpv_attn) are f16:
 // K [n_ctx][h_kv * d] and the transposed V [h_kv * d][v_stride] (the
 // reference's non-FA V layout, qwen35.rs:580-586), converted in the kernel.
 // Either way the KV axis is the reduction axis of P V.
@@ -84,8 +85,8 @@ struct ChunkArgs {
     int pos_sel;              // time) and the grid may hold chunks past the end, which exit
     int64_t kv_rows;          // rows the K cache holds (loads stay below it; v_stride for V)
     const int8_t* vl;         // the session's V cache as limbs (LC kernels): [Hkv*D][v_stride / 16][VLIMBS][16]
-    const int8_t* kl;         // the session's K cache as limbs (LC kernels): rows of k_row bytes
-    int64_t k_row;
+    const int8_t* kl;         // the session's K cache as limbs (LC kernels): rows of k_row bytes, then
+    int64_t k_row;            // the exponent plane [Hkv][v_stride] (cpv_k_exps)
 };
 
 // an integer as L signed 8-bit limbs, x = sum l_i 256^i with l_i in
@@ -218,11 +219,10 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     for (int p = 0; p < KP; p++) {
         const int64_t row = j0 + rq + p * RPP, rc = row < lim ? row : lim - 1;
         if constexpr (LC) {
-            const int8_t* kr = a.kl + rc * a.k_row;
-            const int8_t* src = kr + (int64_t)kh * 2 * D + sub * 16;
+            const int8_t* src = a.kl + rc * a.k_row + (int64_t)kh * 2 * D + sub * 16;
             kv[p][0] = *(const uint4*)src;
             kv[p][1] = *(const uint4*)(src + D);
-            ekv[p] = *(const int*)(kr + (int64_t)a.Hkv * 2 * D + 4 * kh);
+            ekv[p] = *(const int32_t*)(a.kl + a.v_stride * a.k_row + 4 * ((int64_t)kh * a.v_stride + rc));
         } else {
             const uint16_t* src = a.kc + rc * (int64_t)a.Hkv * D + (int64_t)kh * D + sub * 16;
             kv[p][0] = *(const uint4*)src;

@@ -389,11 +389,22 @@ constexpr int CPV_ATTN_VLIMBS = 4;
 // as the 15-bit fixed point rint(kf 2^(14 - e)), e the frexp exponent of the
 // head's largest |kf| (CPV_E_EMPTY for an all-zero head), split into two
 // signed 8-bit limbs f = 256 hi + lo (lo in [-128, 127]): d hi bytes, then d
-// lo bytes per head; after the h_kv heads their exponents (int32), padded to
-// 16 bytes.  Attention's scores take the limbs straight into the int8 MFMA.
+// lo bytes per head, rows of cpv_k_row_bytes; then, after v_stride rows (the
+// V cache's stride, at least the row count), the exponents as an int32 plane
+// [h_kv][v_stride], so that a chunk's exponents of one head are contiguous.
+// Attention's scores take the limbs straight into the int8 MFMA.
 __host__ __device__ __forceinline__ int64_t cpv_k_row_bytes(int h_kv, int d)
 {
-    return (int64_t)h_kv * 2 * d + ((int64_t)h_kv * 4 + 15) / 16 * 16;
+    return (int64_t)h_kv * 2 * d;
+}
+__host__ __device__ __forceinline__ int64_t cpv_k_cache_bytes(int h_kv, int d, int64_t v_stride)
+{
+    return v_stride * cpv_k_row_bytes(h_kv, d) + (int64_t)h_kv * v_stride * 4;
+}
+template <class T>
+__host__ __device__ __forceinline__ T* cpv_k_exps(T* kc, int h_kv, int d, int64_t v_stride)
+{
+    return (T*)((int8_t*)kc + v_stride * cpv_k_row_bytes(h_kv, d));
 }
 __device__ __forceinline__ int cpv_k_fixed(float kf, int e)
 {

@@ -123,7 +123,7 @@ struct PrepArgs {
     const float* k_norm;   // [hd]
     const float* rope;     // [n_pos][n_rot/2][2]
     float* qout;           // [T][H][hd]
-    int8_t* k_limbs;       // the K cache's limbs: rows of cpv_k_row_bytes(Hkv, hd)
+    int8_t* k_limbs;       // the K cache's limbs: rows of cpv_k_row_bytes(Hkv, hd), then the exponent plane
     int8_t* v_limbs;       // the V cache's limbs [Hkv*hd][v_stride / 16][CPV_ATTN_VLIMBS][16]
     int64_t v_stride;
     int64_t rope_pos0, kv_row0;
@@ -176,7 +176,7 @@ __device__ __forceinline__ void write_k_limbs(const PrepArgs& a, int kh, int i, 
     int8_t* kr = a.k_limbs + row * krow;
     kr[(int64_t)kh * 2 * a.hd + i] = hi;
     kr[(int64_t)kh * 2 * a.hd + a.hd + i] = lo;
-    if (i == 0) *(int32_t*)(kr + (int64_t)a.Hkv * 2 * a.hd + 4 * kh) = e;
+    if (i == 0) cpv_k_exps((int32_t*)a.k_limbs, a.Hkv, a.hd, a.v_stride)[(int64_t)kh * a.v_stride + row] = e;
 }
 
 __global__ __launch_bounds__(128) void qk_prep_kernel(PrepArgs a)
@@ -1072,7 +1072,8 @@ extern "C" cpv_status cpv_session_create(cpv_model* m, int64_t n_ctx, int32_t ma
     for (size_t il = 0; il < layers; il++) {
         const bool mtp = (int)il == hp.n_layer;
         const int64_t rows = mtp ? s->mtp_ctx : n_ctx, vs = mtp ? s->mtp_v_stride : s->v_stride;
-        A((size_t)rows * cpv_k_row_bytes((int)Hkv, (int)hd), (void**)&s->kc[il]);
+        (void)rows;
+        A((size_t)cpv_k_cache_bytes((int)Hkv, (int)hd, vs), (void**)&s->kc[il]);
         A((size_t)CPV_ATTN_VLIMBS * Hkv * hd * vs, (void**)&s->vt[il]);
         if (st == CPV_OK)
             CPV_HIP(ctx, hipMemsetAsync(s->vt[il], 0, (size_t)CPV_ATTN_VLIMBS * Hkv * hd * vs, ctx->stream));
@@ -1987,11 +1988,13 @@ struct CompactArgs {
     void* const* caches;       // K caches [n_layer], then V caches [n_layer] (limbs)
     int64_t base, v_stride;
     int n_layer, kpieces, width, n;   // kpieces: 16-byte pieces of a K row; width: h_kv * head_dim
+    int h_kv;
     int8_t path[CPV_TREE_MAX];
 };
 
 // rows base + path[j] -> base + j of every trunk K cache (16-byte pieces of a
-// row) and columns likewise of every V cache (one limb of one column per thread).  Since
+// row, then one KV head's exponents per thread) and columns likewise of every
+// V cache (one limb of one column per thread).  Since
 // path[j] >= j, writing row j never touches a source of a later j: each thread
 // moves its slice in order, eight rows at a time (all eight read before any is
 // written).
@@ -2010,7 +2013,21 @@ __global__ __launch_bounds__(256) void compact_kernel(CompactArgs a)
             for (int q = 0; q < 8; q++)
                 if (j0 + q < a.n) kc[(a.base + j0 + q) * npiece + g] = v[q];
         }
-    } else if (g < npiece + CPV_ATTN_VLIMBS * a.width) {
+    } else if (g >= npiece + CPV_ATTN_VLIMBS * a.width) {
+        const int kh = g - npiece - CPV_ATTN_VLIMBS * a.width;
+        if (kh < a.h_kv) {
+            int32_t* ke = (int32_t*)((int8_t*)a.caches[layer] + a.v_stride * (int64_t)npiece * 16) + kh * a.v_stride;
+            for (int j0 = 0; j0 < a.n; j0 += 8) {
+                int32_t v[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++)
+                    if (j0 + q < a.n) v[q] = ke[a.base + a.path[j0 + q]];
+#pragma unroll
+                for (int q = 0; q < 8; q++)
+                    if (j0 + q < a.n) ke[a.base + j0 + q] = v[q];
+            }
+        }
+    } else {
         const int vr = g - npiece, limb = vr / a.width, col = vr - limb * a.width;
         int8_t* vc = (int8_t*)a.caches[a.n_layer + layer] + 16 * limb;
         for (int j0 = 0; j0 < a.n; j0 += 8) {
@@ -2104,8 +2121,9 @@ extern "C" cpv_status cpv_session_commit_branch(cpv_session* s, const int32_t* p
         a.n_layer = hp.n_layer;
         a.kpieces = (int)(cpv_k_row_bytes((int)hp.n_head_kv, (int)hp.head_dim) / 16);
         a.width = (int)(hp.n_head_kv * hp.head_dim);
+        a.h_kv = (int)hp.n_head_kv;
         a.n = n;
-        const int threads = a.kpieces + CPV_ATTN_VLIMBS * a.width;
+        const int threads = a.kpieces + CPV_ATTN_VLIMBS * a.width + a.h_kv;
         compact_kernel<<<dim3((unsigned)((threads + 255) / 256), (unsigned)hp.n_layer), 256, 0, ctx->stream>>>(a);
         CPV_HIP(ctx, hipGetLastError());
     }
