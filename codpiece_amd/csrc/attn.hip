@@ -75,7 +75,8 @@ struct ChunkArgs {
     const uint16_t* kc;       // [n_ctx][Hkv*D]
     const uint16_t* vt;       // [Hkv*D][v_stride]
     const int32_t* parent;    // [T] or null
-    float* P;                 // [chunks][T*H][D]
+    float* P;                 // partial of chunk c, query row r: P + c p_cs + r p_rs, D floats
+    int64_t p_cs, p_rs;       //   ([chunks][T*H][D] for a consumer's fold, [T*H][chunks][D] for attn_fold_kernel)
     float* mc;                // [chunks][T*H]
     long long* zc;            // [chunks][T*H]
     int64_t n_past, n, v_stride;   // n = n_past + T rows in play
@@ -157,15 +158,27 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     constexpr int RPP = CT / TPR;              // rows per pass
     constexpr int QP = (QB + RPP - 1) / RPP;   // query conversion passes
     // rows padded by 16 bytes (limbs) and 4 floats (scores): the MFMA operand
-    // reads and the score writes then fall on distinct LDS banks.  The
-    // weights' limbs take the K limbs' place once the scores are done.
+    // reads and the score writes then fall on distinct LDS banks.  One buffer
+    // holds the phases in turn: the K limbs at 0 and the query limbs after
+    // them until the score MFMAs are done; the weights' limbs at 0 once the
+    // scores are done.  The scores lie after the query limbs, or, for more
+    // than 32 query rows (OVL), at PBUF over both (a barrier after the score
+    // MFMAs): 52 KB a workgroup at 48 rows and d = 128, so that two share a
+    // CU (at 78 KB one ran per CU).
+    constexpr bool OVL = QB > QB_CHAIN;
     constexpr int KBUF = 2 * CHUNK * (D + 16), PBUF = PL * QB * (CHUNK + 16);
-    __shared__ __align__(16) int8_t s_qh[QB][D + 16], s_ql[QB][D + 16];
-    __shared__ __align__(16) int8_t s_kbuf[KBUF > PBUF ? KBUF : PBUF];
-    __shared__ __align__(16) float s_w[QB][CHUNK + 4];     // scores
-    int8_t(*s_kh)[D + 16] = (int8_t(*)[D + 16]) & s_kbuf[0];
-    int8_t(*s_kl)[D + 16] = (int8_t(*)[D + 16]) & s_kbuf[CHUNK * (D + 16)];
-    int8_t(*s_p)[QB][CHUNK + 16] = (int8_t(*)[QB][CHUNK + 16]) & s_kbuf[0];   // [PL][query row][cache row]
+    constexpr int QS = 2 * QB * (D + 16), WS = QB * (CHUNK + 4) * (int)sizeof(float);
+    constexpr int KQ = (KBUF > PBUF ? KBUF : PBUF) + QS;
+    constexpr int WOFF = OVL ? PBUF : KQ;
+    constexpr int UBUF = KQ > WOFF + WS ? KQ : WOFF + WS;
+    static_assert(PBUF % 16 == 0 && KBUF % 16 == 0, "16-byte aligned phases");
+    __shared__ __align__(16) int8_t s_buf[UBUF];
+    int8_t(*s_kh)[D + 16] = (int8_t(*)[D + 16]) & s_buf[0];
+    int8_t(*s_kl)[D + 16] = (int8_t(*)[D + 16]) & s_buf[CHUNK * (D + 16)];
+    int8_t(*s_qh)[D + 16] = (int8_t(*)[D + 16]) & s_buf[KQ - QS];
+    int8_t(*s_ql)[D + 16] = (int8_t(*)[D + 16]) & s_buf[KQ - QS + QB * (D + 16)];
+    float(*s_w)[CHUNK + 4] = (float(*)[CHUNK + 4]) & s_buf[WOFF];                // scores
+    int8_t(*s_p)[QB][CHUNK + 16] = (int8_t(*)[QB][CHUNK + 16]) & s_buf[0];      // [PL][query row][cache row]
     __shared__ int s_eq[QB], s_ek[CHUNK];
     __shared__ unsigned long long s_anc[QB];
     __shared__ int s_vis[QB], s_orow[QB];      // (per query row; set with its limbs)
@@ -354,6 +367,7 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
                 mix[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qlv, khv, mix[b], 0, 0, 0);
                 ll[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qlv, klv, ll[b], 0, 0, 0);
             }
+        if constexpr (OVL) __syncthreads();   // (the scores overwrite the q and K limbs)
 #pragma unroll
         for (int b = 0; b < QBB; b++) {
             const int blk = wave + (CT / 64) * b, qb = blk % QBB, jb = blk / QBB;
@@ -479,7 +493,8 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
             int64_t S = 0;
 #pragma unroll
             for (int q = 0; q < PL + VLIMBS - 1; q++) S += (int64_t)acc[q][i] * ((int64_t)1 << (8 * q));
-            a.P[((int64_t)c * a.T * a.H + s_orow[rb * 16 + 4 * g4 + i]) * D + dcol] = ldexpf((float)S, -(PBITS + VBITS));
+            a.P[(int64_t)c * a.p_cs + (int64_t)s_orow[rb * 16 + 4 * g4 + i] * a.p_rs + dcol] =
+                ldexpf((float)S, -(PBITS + VBITS));
         }
     }
 }
@@ -487,19 +502,22 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
 // one query row: the chunks folded in order, then the normalisation.  The
 // chunk maxima, sums and factors are staged in LDS; empty chunks (no visible
 // row) carry factor 0 and zero partials, which leave both folds unchanged.
+// Threads 0 .. D-1 fold one column each; a third wave's first lane sums Z
+// meanwhile (a serial binary64 chain, off the folds' path).
 template <int D>
-__global__ __launch_bounds__(D) void attn_fold_kernel(const float* __restrict__ P, const float* __restrict__ mc,
-                                                      const long long* __restrict__ zc, int nchunk, int rows,
-                                                      float* __restrict__ out)
+__global__ __launch_bounds__(D + 64) void attn_fold_kernel(const float* __restrict__ P, const float* __restrict__ mc,
+                                                           const long long* __restrict__ zc, int nchunk, int rows,
+                                                           float* __restrict__ out)
 {
+    constexpr int NT = D + 64, NW = NT / 64;
     extern __shared__ double s_dyn[];          // [nchunk] Z_c 2^-PBITS, then [nchunk] factors f_c
     double* s_z = s_dyn;
     float* s_f = (float*)(s_dyn + nchunk);
-    __shared__ float s_red[D / 64];
+    __shared__ float s_red[NW];
     __shared__ float s_inv;
     const int row = blockIdx.x, d = threadIdx.x, lane = d & 63, wave = d >> 6;
     float M = -INFINITY;
-    for (int c = d; c < nchunk; c += D) {
+    for (int c = d; c < nchunk; c += NT) {
         const float m = mc[(int64_t)c * rows + row];
         s_f[c] = m;
         s_z[c] = ldexp((double)zc[(int64_t)c * rows + row], -PBITS);
@@ -509,21 +527,23 @@ __global__ __launch_bounds__(D) void attn_fold_kernel(const float* __restrict__ 
     if (lane == 0) s_red[wave] = M;
     __syncthreads();
     M = s_red[0];
-    for (int i = 1; i < D / 64; i++) M = fmaxf(M, s_red[i]);
-    for (int c = d; c < nchunk; c += D) {
+    for (int i = 1; i < NW; i++) M = fmaxf(M, s_red[i]);
+    for (int c = d; c < nchunk; c += NT) {
         const float m = s_f[c];
         s_f[c] = m == -INFINITY ? 0.0f : cpv_expf(m - M);
     }
     __syncthreads();
-    if (d == 0) {
+    float o = 0.0f;
+    if (d < D) {                               // (wave-uniform)
+        // (a row's partials lie together: [rows][nchunk][D])
+        o = cpv_fold_chain<32>(P + (int64_t)row * nchunk * D + d, D, s_f, nchunk);
+    } else if (d == D) {
         double Zt = 0.0;
         for (int c = 0; c < nchunk; c++) Zt = Zt + s_z[c] * (double)s_f[c];
         s_inv = (float)(1.0 / Zt);
     }
-    const float* pr = P + (int64_t)row * D + d;
-    const float o = cpv_fold_chain<32>(pr, (int64_t)rows * D, s_f, nchunk);   // (32 partials in flight per step)
     __syncthreads();
-    out[(int64_t)row * D + d] = o * s_inv;
+    if (d < D) out[(int64_t)row * D + d] = o * s_inv;
 }
 
 // one call over T query tokens (the scratch holds T*H rows per chunk); with
@@ -558,6 +578,8 @@ cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const ui
     ca.vt = vt;
     ca.parent = parent;
     ca.P = (float*)ws;
+    ca.p_cs = out ? D : (int64_t)rows * D;
+    ca.p_rs = out ? (int64_t)nchunk * D : D;
     ca.mc = (float*)((uint8_t*)ws + P_b);
     ca.zc = (long long*)((uint8_t*)ws + P_b + m_b);
     ca.n_past = n_past;
@@ -593,7 +615,7 @@ cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const ui
         else attn_chunk_kernel<D, false, QB_CHAIN><<<cgrid, CT, 0, ctx->stream>>>(ca);
     }
     if (out)
-        attn_fold_kernel<D><<<(unsigned)rows, D, (size_t)nchunk * 12, ctx->stream>>>(ca.P, ca.mc, ca.zc, nchunk,
+        attn_fold_kernel<D><<<(unsigned)rows, D + 64, (size_t)nchunk * 12, ctx->stream>>>(ca.P, ca.mc, ca.zc, nchunk,
                                                                                   rows, out);
     CPV_HIP(ctx, hipGetLastError());
     if (part) {
