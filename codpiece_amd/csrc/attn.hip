@@ -46,7 +46,8 @@ constexpr int PL = 3;
 constexpr int VBITS = CPV_ATTN_VBITS;   // an f16 value v as vq = rint(v 2^14): |vq| < 2^30, VLIMBS limbs
 constexpr int VLIMBS = CPV_ATTN_VLIMBS;
 constexpr int QB_CHAIN = 32;        // query rows per chunk workgroup: chains and prefill
-constexpr int QB_WIDE = 48;         //   and when a KV head has more than 32 (a 16-node tree's 80: 48 + 32)
+constexpr int QB_WIDE = 48;         //   and when a KV head has more than 80
+constexpr int QB_TREE = 80;         //   and when it has 49 to 80 (a 16-node tree's 5 x 16)
 constexpr int E_EMPTY = CPV_E_EMPTY;   // exponent of an all-zero vector
 
 __device__ __forceinline__ int ceil_log2_dev(int64_t v)
@@ -164,10 +165,13 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     // scores are done.  The scores lie after the query limbs, or, for more
     // than 32 query rows (OVL), at PBUF over both (a barrier after the score
     // MFMAs): 52 KB a workgroup at 48 rows and d = 128, so that two share a
-    // CU (at 78 KB one ran per CU).
+    // CU (at 78 KB one ran per CU).  Past 48 rows the scores wait in
+    // registers and go through the LDS and the softmax WR rows at a time.
     constexpr bool OVL = QB > QB_CHAIN;
+    constexpr int WR = QB > QB_WIDE ? QB_WIDE : QB, NH = (QB + WR - 1) / WR;
+    static_assert(WR % 16 == 0, "score halves of whole row blocks");
     constexpr int KBUF = 2 * CHUNK * (D + 16), PBUF = PL * QB * (CHUNK + 16);
-    constexpr int QS = 2 * QB * (D + 16), WS = QB * (CHUNK + 4) * (int)sizeof(float);
+    constexpr int QS = 2 * QB * (D + 16), WS = WR * (CHUNK + 4) * (int)sizeof(float);
     constexpr int KQ = (KBUF > PBUF ? KBUF : PBUF) + QS;
     constexpr int WOFF = OVL ? PBUF : KQ;
     constexpr int UBUF = KQ > WOFF + WS ? KQ : WOFF + WS;
@@ -349,6 +353,7 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     // at most 64 rows (the short last one) has only its first half read
     // below, and the softmax and P V skip the second
     const bool half = nj <= CHUNK / 2;
+    float scv[NH > 1 ? QBB : 1][4];            // this lane's scores (masked), past 48 rows
     {
         const int kg = (lane >> 4) * 16;
         v4i hh[QBB], mix[QBB], ll[QBB];
@@ -385,27 +390,45 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
                 if (tree) vis = vis || ((uint64_t)node < 64 && ((s_anc[r] >> node) & 1ull));
                 const double S = __builtin_fma((double)hh[b][i], 65536.0, (double)(mix[b][i] * 256 + ll[b][i]));
                 const float sc = (float)ldexp(S, s_eq[r] + ek - 28);
-                s_w[r][bc] = vis ? sc * a.scale : -INFINITY;
+                const float wv = vis ? sc * a.scale : -INFINITY;
+                if constexpr (NH == 1) s_w[r][bc] = wv;
+                else scv[b][i] = wv;
             }
         }
     }
-    __syncthreads();
 
     // ---- the chunk's softmax: SPR threads per query row, 8 cache rows each
     // (4 part + 64 i + k: 16-byte reads of the scores, one dword per limb
     // written), CT / SPR rows per pass; the weights in fixed point,
-    // p = rint(e 2^PBITS), as PL signed 8-bit limbs, and Z_c = sum p
+    // p = rint(e 2^PBITS), as PL signed 8-bit limbs, and Z_c = sum p.  The
+    // scores of rows h WR .. (h + 1) WR - 1 go to the LDS first (the blocks
+    // of a wave's b are whole in one of them: wave-uniform).
     constexpr int SPR = CHUNK / 8, SRP = CT / SPR;
-    static_assert(QB % SRP == 0 || QB % SRP == SRP / 2, "softmax passes of whole row groups");
+    static_assert(WR % (SRP / 2) == 0 && QB % (SRP / 2) == 0, "softmax passes of whole waves");
 #pragma unroll
-    for (int r0 = 0; r0 < QB; r0 += SRP) {
+    for (int h = 0; h < NH; h++) {
+    if constexpr (NH > 1) {
+        if (h > 0) __syncthreads();            // (the previous rows' scores are read)
+#pragma unroll
+        for (int b = 0; b < QBB; b++) {
+            const int blk = wave + (CT / 64) * b, qb = blk % QBB, jb = blk / QBB;
+            if (qb * 16 / WR != h) continue;
+            const int bc = jb * 16 + (lane & 15);
+#pragma unroll
+            for (int i = 0; i < 4; i++) s_w[qb * 16 + 4 * (lane >> 4) + i - h * WR][bc] = scv[b][i];
+        }
+    }
+    __syncthreads();
+    const int rend = (h + 1) * WR < QB ? (h + 1) * WR : QB;
+#pragma unroll
+    for (int r0 = h * WR; r0 < rend; r0 += SRP) {
         const int r = r0 + tid / SPR, part = tid % SPR;
-        if (r >= QB) break;                    // (a half pass: whole waves past the rows)
+        if (r >= rend) break;                  // (a half pass: whole waves past the rows)
         const int lr = blockIdx.z * QB + r;
         float w[8];
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const float4 w4 = i == 0 || !half ? *(const float4*)&s_w[r][4 * part + 64 * i]
+            const float4 w4 = i == 0 || !half ? *(const float4*)&s_w[r - h * WR][4 * part + 64 * i]
                                               : float4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
             w[4 * i] = w4.x;
             w[4 * i + 1] = w4.y;
@@ -439,6 +462,7 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
             a.mc[row] = m;
             a.zc[row] = z;
         }
+    }
     }
     // (the f16 cache's values into limbs meanwhile)
     if constexpr (!LC) {
@@ -604,10 +628,16 @@ cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const ui
     // extra workgroups take no more passes over the CUs, and their shorter
     // chains win (the 16-node tree at 4101 rows: 9.59 against 9.71 ms; at
     // 32768 over the API's caches: 200 against 182 us)
+    // Over the API's f16 caches, 49 to 80 rows (a 16-node tree's) go in one
+    // 80-row block: the chunk's K and V are loaded and converted to limbs
+    // once for all of them, not once per 48-row block.
     const bool wide = LR > QB_CHAIN && (int64_t)nchunk * Hkv >= 512;
-    const int QB = wide ? QB_WIDE : QB_CHAIN;
+    const bool tree_blk = wide && !vl && LR > QB_WIDE && LR <= QB_TREE;
+    const int QB = tree_blk ? QB_TREE : wide ? QB_WIDE : QB_CHAIN;
     const dim3 cgrid((unsigned)(nchunk * Hkv), 1u, (unsigned)((LR + QB - 1) / QB));
-    if (wide) {
+    if (tree_blk) {
+        attn_chunk_kernel<D, false, QB_TREE><<<cgrid, CT, 0, ctx->stream>>>(ca);
+    } else if (wide) {
         if (vl) attn_chunk_kernel<D, true, QB_WIDE><<<cgrid, CT, 0, ctx->stream>>>(ca);
         else attn_chunk_kernel<D, false, QB_WIDE><<<cgrid, CT, 0, ctx->stream>>>(ca);
     } else {

@@ -72,6 +72,19 @@ def test_tree_verify_config(ctx, n_ctx):
     close(*run(ctx, 16, 40, 8, 128, n_ctx, TREE16, seed=n_ctx))
 
 
+@pytest.mark.parametrize("t,parent", [(13, TREE16[:13]), (11, None)])
+def test_80_row_block_with_padding_rows(ctx, t, parent):
+    # over the API's caches, 49 to 80 query rows per KV head run as one
+    # 80-row block from 512 (chunk, KV head) units on: 65 and 55 rows here,
+    # the rest of the block padding
+    close(*run(ctx, t, 40, 8, 128, 8192, parent, seed=t))
+
+
+def test_80_row_block_d64(ctx):
+    # d = 64, 2 KV heads: 257 chunks x 2 = 514 units, 64 query rows per KV head
+    close(*run(ctx, 16, 8, 2, 64, 32768, TREE16, seed=64))
+
+
 def test_tree_with_linear_parents_equals_chain(ctx):
     a, _ = run(ctx, 8, 8, 2, 64, 200, None, seed=3)
     b, _ = run(ctx, 8, 8, 2, 64, 200, list(range(-1, 7)), seed=3)
