@@ -89,6 +89,7 @@ struct ChunkArgs {
     const int8_t* vl;         // the session's V cache as limbs (LC kernels): [Hkv*D][v_stride / 16][VLIMBS][16]
     const int8_t* kl;         // the session's K cache as limbs (LC kernels): rows of k_row bytes, then
     int64_t k_row;            // the exponent plane [Hkv][v_stride] (cpv_k_exps)
+    int fwd;                  // chunks in dispatch order first to last (no pos)
 };
 
 // an integer as L signed 8-bit limbs, x = sum l_i 256^i with l_i in
@@ -195,8 +196,11 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     // KV head fastest, chunks last to first: the first blocks dispatched are
     // those past the end (which exit at once) and the short last chunk (which
     // costs little below), so the blocks that a full grid places on a CU
-    // beside another are full chunks beside those
-    const int c = (int)(gridDim.x / a.Hkv) - 1 - (int)(blockIdx.x / a.Hkv), kh = blockIdx.x % a.Hkv;
+    // beside another are full chunks beside those.  A grid of more blocks
+    // than two a CU (fwd) runs first to last: the short chunk then comes in
+    // the last round, not a full one.
+    const int cq = (int)(blockIdx.x / a.Hkv), kh = blockIdx.x % a.Hkv;
+    const int c = a.fwd ? cq : (int)(gridDim.x / a.Hkv) - 1 - cq;
     const int64_t j0 = (int64_t)c * CHUNK;
     const int G = a.H / a.Hkv, LR = G * a.T;
     const int sub = tid % TPR;
@@ -635,6 +639,7 @@ cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const ui
     const bool tree_blk = wide && !vl && LR > QB_WIDE && LR <= QB_TREE;
     const int QB = tree_blk ? QB_TREE : wide ? QB_WIDE : QB_CHAIN;
     const dim3 cgrid((unsigned)(nchunk * Hkv), 1u, (unsigned)((LR + QB - 1) / QB));
+    ca.fwd = !pos && (int64_t)cgrid.x * cgrid.z > 2 * (int64_t)ctx->cu_count;
     if (tree_blk) {
         attn_chunk_kernel<D, false, QB_TREE><<<cgrid, CT, 0, ctx->stream>>>(ca);
     } else if (wide) {
