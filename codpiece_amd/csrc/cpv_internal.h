@@ -109,20 +109,19 @@ __host__ __device__ __forceinline__ float cpv_h2f(uint16_t h)
 {
     return (float)__builtin_bit_cast(_Float16, h);
 }
-__host__ __device__ __forceinline__ uint16_t cpv_f2h(float f)
+// f32 -> f16, round to nearest even (subnormals kept, overflow to inf), NaN
+// as the quiet NaN 0x7e00 with the input's sign: v_cvt_f16_f32 under the
+// default mode, which equals the bit-level rounding rule for every f32 input
+// but NaN payloads (compared over all 2^32 inputs on gfx950).  The empty asm
+// keeps the compiler from folding a product into the conversion
+// (v_mad_mixlo_f16 rounds a * b once, where the contract rounds it to f32
+// first).
+__device__ __forceinline__ uint16_t cpv_f2h(float f)
 {
-    // every case is computed and selected (no branches: the conversion runs
-    // per element in divergent-free inner loops)
+    asm volatile("" : "+v"(f));
+    const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)f);
     const uint32_t x = __builtin_bit_cast(uint32_t, f);
-    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
-    // below 2^-14: subnormal or zero, exact scaling by 2^24 then RNE
-    const uint32_t sub = (uint32_t)rintf(__builtin_bit_cast(float, ax < 0x38800000u ? ax : 0u) * 16777216.0f);
-    // normal: round the 13 dropped bits, ties to even
-    const uint32_t nrm = ((ax + 0x0fffu + ((ax >> 13) & 1u)) - 0x38000000u) >> 13;
-    uint32_t r = ax < 0x38800000u ? sub : nrm;
-    r = ax >= 0x477ff000u ? 0x7c00u : r;                // |f| >= 65520 (and inf) rounds to inf
-    r = ax > 0x7f800000u ? 0x7e00u : r;                 // NaN
-    return (uint16_t)(sign | r);
+    return (x & 0x7fffffffu) > 0x7f800000u ? (uint16_t)(((x >> 16) & 0x8000u) | 0x7e00u) : h;
 }
 
 // 2^(i/32) in binary64, stored minus i << 47
