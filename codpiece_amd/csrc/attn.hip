@@ -72,7 +72,9 @@ __device__ __forceinline__ uint64_t ancestors(const int32_t* parent, int t)
 }
 
 struct ChunkArgs {
-    const float* q;           // [T][H][D]
+    const float* q;           // [T][H][D] (LC kernels)
+    const int8_t* qlim;       // the same rows (t * H + h) as limbs (the others): [T*H][2][D], the D hi
+    const int32_t* qexp;      //   limbs then the D lo; [T*H] the rows' exponents
     const uint16_t* kc;       // [n_ctx][Hkv*D]
     const uint16_t* vt;       // [Hkv*D][v_stride]
     const int32_t* parent;    // [T] or null
@@ -143,6 +145,36 @@ __device__ __forceinline__ int row_limbs(const float* v, uint32_t* hi, uint32_t*
         hi[j] = t[1];
     }
     return e;
+}
+
+// The query rows as the chunk kernels take them (once per call, not once per
+// chunk): each element rounded to f16, the row's exponent, the two limbs.
+// TPR lanes per row, 16 values each.
+template <int D>
+__global__ __launch_bounds__(256) void q_limbs_kernel(const float* __restrict__ q, int rows, int8_t* __restrict__ qlim,
+                                                      int32_t* __restrict__ qexp)
+{
+    constexpr int TPR = D / 16;
+    const int g = blockIdx.x * 256 + threadIdx.x, row = g / TPR, sub = g % TPR;
+    const int rc = row < rows ? row : rows - 1;   // (the row's lanes reduce together: all active)
+    const float4* src = (const float4*)(q + (int64_t)rc * D + sub * 16);
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 x = src[i];
+        v[4 * i + 0] = cpv_h2f(cpv_f2h(x.x));
+        v[4 * i + 1] = cpv_h2f(cpv_f2h(x.y));
+        v[4 * i + 2] = cpv_h2f(cpv_f2h(x.z));
+        v[4 * i + 3] = cpv_h2f(cpv_f2h(x.w));
+    }
+    uint32_t hi[4], lo[4];
+    const int e = row_limbs<TPR>(v, hi, lo);
+    if (row < rows) {
+        int8_t* dst = qlim + (int64_t)row * 2 * D + sub * 16;
+        *(uint4*)dst = uint4{hi[0], hi[1], hi[2], hi[3]};
+        *(uint4*)(dst + D) = uint4{lo[0], lo[1], lo[2], lo[3]};
+        if (sub == 0) qexp[row] = e;
+    }
 }
 
 // one 128-row chunk of the cache against QB query rows of one KV head
@@ -223,14 +255,26 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     // around a load (a branch makes the compiler wait for every load at the join)
     constexpr int KP = CHUNK / RPP > 0 ? CHUNK / RPP : 1;   // K passes
     const int rq = tid / TPR;                  // query row converted by this thread in pass 0
-    float4 qv[QP][4];
+    // (LC: the f32 rows, made into limbs below; else their limbs as made by
+    // q_limbs_kernel, once per call)
+    float4 qv[LC ? QP : 1][4];
+    uint4 qlv[LC ? 1 : QP][2];
+    int qev[LC ? 1 : QP];
 #pragma unroll
     for (int qp = 0; qp < QP; qp++) {          // (rows past QB or LR read row 0)
         const int lrq = blockIdx.z * QB + rq + qp * RPP;
         const int lrc = rq + qp * RPP < QB && lrq < LR ? lrq : 0;
-        const float* src = a.q + ((int64_t)(lrc / G) * a.H + kh * G + lrc % G) * D + sub * 16;
+        const int64_t qrow = (int64_t)(lrc / G) * a.H + kh * G + lrc % G;
+        if constexpr (LC) {
+            const float* src = a.q + qrow * D + sub * 16;
 #pragma unroll
-        for (int i = 0; i < 4; i++) qv[qp][i] = ((const float4*)src)[i];
+            for (int i = 0; i < 4; i++) qv[qp][i] = ((const float4*)src)[i];
+        } else {
+            const int8_t* src = a.qlim + qrow * 2 * D + sub * 16;
+            qlv[qp][0] = *(const uint4*)src;
+            qlv[qp][1] = *(const uint4*)(src + D);
+            qev[qp] = a.qexp[qrow];
+        }
     }
     // (elsewhere rows clamped to the cache's: the chunk's end is known once n_past is)
     // LC: kv[p] = 16 hi limbs, 16 lo limbs of the row's head, ekv[p] its exponent
@@ -262,18 +306,26 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
         const int lrq = blockIdx.z * QB + r;
         const bool qok = lrq < LR;
         const int lrc = qok ? lrq : 0;
-        float v[16];
+        // (a row past LR: all-zero limbs, as an all-zero row has)
+        int e;
+        if constexpr (LC) {
+            float v[16];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            v[4 * i + 0] = qok ? cpv_h2f(cpv_f2h(qv[qp][i].x)) : 0.0f;
-            v[4 * i + 1] = qok ? cpv_h2f(cpv_f2h(qv[qp][i].y)) : 0.0f;
-            v[4 * i + 2] = qok ? cpv_h2f(cpv_f2h(qv[qp][i].z)) : 0.0f;
-            v[4 * i + 3] = qok ? cpv_h2f(cpv_f2h(qv[qp][i].w)) : 0.0f;
+            for (int i = 0; i < 4; i++) {
+                v[4 * i + 0] = qok ? cpv_h2f(cpv_f2h(qv[qp][i].x)) : 0.0f;
+                v[4 * i + 1] = qok ? cpv_h2f(cpv_f2h(qv[qp][i].y)) : 0.0f;
+                v[4 * i + 2] = qok ? cpv_h2f(cpv_f2h(qv[qp][i].z)) : 0.0f;
+                v[4 * i + 3] = qok ? cpv_h2f(cpv_f2h(qv[qp][i].w)) : 0.0f;
+            }
+            uint32_t hi[4], lo[4];
+            e = row_limbs<TPR>(v, hi, lo);
+            *(uint4*)&s_qh[r][sub * 16] = uint4{hi[0], hi[1], hi[2], hi[3]};
+            *(uint4*)&s_ql[r][sub * 16] = uint4{lo[0], lo[1], lo[2], lo[3]};
+        } else {
+            *(uint4*)&s_qh[r][sub * 16] = qok ? qlv[qp][0] : uint4{0, 0, 0, 0};
+            *(uint4*)&s_ql[r][sub * 16] = qok ? qlv[qp][1] : uint4{0, 0, 0, 0};
+            e = qok ? qev[qp] : E_EMPTY;
         }
-        uint32_t hi[4], lo[4];
-        const int e = row_limbs<TPR>(v, hi, lo);
-        *(uint4*)&s_qh[r][sub * 16] = uint4{hi[0], hi[1], hi[2], hi[3]};
-        *(uint4*)&s_ql[r][sub * 16] = uint4{lo[0], lo[1], lo[2], lo[3]};
         if (sub == 0) {
             // the row's visible cache rows in this chunk: the first s_vis of
             // them (the context, and for a chain its nodes up to t), then for
@@ -579,6 +631,9 @@ __global__ __launch_bounds__(D + 64) void attn_fold_kernel(const float* __restri
 // that folds them itself
 // With pos set (partials only), the grid and the scratch are sized for
 // nchunk_grid chunks, at least the call's, and n_past is read on the device.
+// Over the API's caches the queries are made into limbs first
+// (q_limbs_kernel, once per call); a session's LC kernels convert their own
+// (about as fast at a verify's few rows, with no launch of its own).
 template <int D>
 cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const uint16_t* vt, int64_t v_stride,
                       int64_t n_past, const int32_t* parent, int T, int H, int Hkv, float scale, float* out,
@@ -596,12 +651,22 @@ cpv_status attn_block(cpv_ctx* ctx, const float* q, const uint16_t* kc, const ui
     if (pos && nchunk_grid > nchunk) nchunk = nchunk_grid;
     const size_t P_b = ((size_t)nchunk * rows * D * 4 + 255) & ~(size_t)255;
     const size_t m_b = ((size_t)nchunk * rows * 4 + 255) & ~(size_t)255;
-    const size_t z_b = (size_t)nchunk * rows * 8;
+    const size_t z_b = ((size_t)nchunk * rows * 8 + 255) & ~(size_t)255;
+    const size_t ql_b = vl ? 0 : (((size_t)rows * 2 * D + 255) & ~(size_t)255) + (size_t)rows * 4;
     void* ws = nullptr;
-    cpv_status st = cpv_workspace(ctx, P_b + m_b + z_b, &ws);
+    cpv_status st = cpv_workspace(ctx, P_b + m_b + z_b + ql_b, &ws);
     if (st != CPV_OK) return st;
     ChunkArgs ca;
     ca.q = q;
+    ca.qlim = nullptr;
+    ca.qexp = nullptr;
+    if (!vl) {
+        int8_t* ql = (int8_t*)ws + P_b + m_b + z_b;
+        int32_t* qe = (int32_t*)(ql + (((size_t)rows * 2 * D + 255) & ~(size_t)255));
+        q_limbs_kernel<D><<<(unsigned)(((int64_t)rows * (D / 16) + 255) / 256), 256, 0, ctx->stream>>>(q, rows, ql, qe);
+        ca.qlim = ql;
+        ca.qexp = qe;
+    }
     ca.kc = kc;
     ca.vt = vt;
     ca.parent = parent;
