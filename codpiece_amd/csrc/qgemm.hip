@@ -1110,7 +1110,7 @@ static cpv_status qgemm_into(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* a
         if ((st = cpv_qgemm_wide(ctx, w, act, a.gsum, a.win)) != CPV_OK) return st;
         if (y)
             qgemm_finalize_kernel<<<dim3((unsigned)((w->n + 255) / 256), (unsigned)m), 256, 0, ctx->stream>>>(
-                a.gsum, a.n_pad, a.ew, a.da, U, 0, a.win, y, w->n);
+                a.gsum, a.n_pad, a.ew, a.da, kq ? U : 8 * U, 0, a.win, y, w->n);
         CPV_HIP(ctx, hipGetLastError());
         return CPV_OK;
     }

@@ -224,16 +224,147 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(3))) void qg
         }
 }
 
+// The same for Q8_0 weights and activations (ggml's Q8_0 vec_dot_type).
+// Per (activation row m, weight row n, 32-element block j) the dot is one
+// 16x16x32 MFMA's entry, and the block's term is rounded on its own:
+//     term = rint(dw_j * da_j * 2^-g * dot)          (binary64, exact product)
+// eight terms per 256-element unit where Q4_K has two, so this kernel is
+// bound by its binary64 VALU work.  A unit's 17 pieces: 16 of codes (block j
+// in pieces 2j, 2j + 1), then the 8 block scales (f16).
+__global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_wide_q80_kernel(WideArgs a)
+{
+    __shared__ __align__(16) uint8_t s_codes[2][WBM][WROW];
+    __shared__ double s_dad[2][WBM][8];  // da_j * 2^(win - Ea) per staged row and block
+    __shared__ double s_sm[WBM];         // 2^(win - Ea(m)), 0 for an all-zero row
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int U = a.U, M = a.M, NDA = 8 * a.U;
+    const int64_t Kp = (int64_t)U * 256;
+
+    const int nb = gridDim.x, b0 = blockIdx.x;
+    const int L = (nb & 7) == 0 ? (b0 & 7) * (nb >> 3) + (b0 >> 3) : b0;
+    const int mb = L % a.mblocks, r0 = L / a.mblocks;
+    const int ks = r0 % a.ksplit, tile = r0 / a.ksplit;
+    const int u0 = ks * a.upk, u1 = min(U, u0 + a.upk);
+    const int rbase = mb * WBM;
+
+    for (int r = wave; r < WBM; r += WT / 64) {
+        const int mr = a.m0 + min(rbase + r, M - 1);
+        float mx = 0.0f;
+        for (int c = lane; c < NDA; c += 64) mx = fmaxf(mx, fabsf(a.da[(int64_t)mr * NDA + c]));
+        mx = cpv_wave_reduce(mx, cpv_op_max());
+        if (lane == 0) {
+            int e = CPV_E_EMPTY;
+            if (mx > 0.0f) frexpf(mx, &e);
+            s_sm[r] = e == CPV_E_EMPTY ? 0.0 : ldexp(1.0, a.win - e);
+        }
+    }
+
+    const int8_t* qbase = a.qa + (int64_t)(a.m0 + rbase) * Kp;
+    int soff[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int p = tid + q * WT, r = p >> 4;
+        soff[q] = (min(rbase + r, M - 1) - rbase) * (int)Kp + (p & 15) * 16;
+    }
+    // scales: thread tid stages blocks 2 (tid & 3), +1 of row tid >> 2
+    const int srow = tid >> 2, sblk = 2 * (tid & 3);
+    const float* sda = a.da + (int64_t)(a.m0 + min(rbase + srow, M - 1)) * NDA + sblk;
+    auto stage_load = [&](int u, v4i* cv, float2& dv) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) cv[q] = *(const v4i*)(qbase + soff[q] + u * 256);
+        dv = *(const float2*)(sda + 8 * u);
+    };
+    auto stage_store = [&](int buf, const v4i* cv, float2 dv) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int p = tid + q * WT;
+            *(v4i*)&s_codes[buf][p >> 4][(p & 15) * 16] = cv[q];
+        }
+        s_dad[buf][srow][sblk] = (double)dv.x * s_sm[srow];
+        s_dad[buf][srow][sblk + 1] = (double)dv.y * s_sm[srow];
+    };
+
+    // this lane's weight row and k slot: 8 codes of block j (bytes 8 (kq & 1)
+    // .. of piece 2j + (kq >> 1)), and the row's 8 block scales
+    const int nl = lane & 15, kq = lane >> 4;
+    const int nrow = wave * 16 + nl;
+    const uint8_t* wrow = a.w + (int64_t)tile * U * 17 * 1024 + nrow * 16;
+    struct Wt { v2i q[8]; v4i s; };
+    auto wload = [&](int u, Wt& t) {
+        const uint8_t* p = wrow + (int64_t)u * 17 * 1024;
+#pragma unroll
+        for (int j = 0; j < 8; j++) t.q[j] = *(const v2i*)(p + (2 * j + (kq >> 1)) * 1024 + 8 * (kq & 1));
+        t.s = *(const v4i*)(p + 16 * 1024);
+    };
+    const int er = a.ew[(int64_t)tile * 64 + nrow];
+
+    double S[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) S[mt][i] = 0.0;
+
+    Wt wc, wn;
+    v4i cv[4];
+    float2 dv;
+    wload(u0, wc);
+    stage_load(u0, cv, dv);
+    __syncthreads();                    // s_sm
+    stage_store(0, cv, dv);
+    __syncthreads();
+
+    for (int u = u0; u < u1; u++) {
+        const int buf = (u - u0) & 1;
+        const int un = u + 1 < u1 ? u + 1 : u;
+        wload(un, wn);
+        stage_load(un, cv, dv);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t hw = (uint32_t)wc.s[j >> 1];
+            const double dwj = ldexp((double)cpv_h2f((uint16_t)((j & 1) ? hw >> 16 : hw & 0xffffu)), -er);
+            const int64_t bq = pack2((uint32_t)wc.q[j][0], (uint32_t)wc.q[j][1]);
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++) {
+                const int64_t av = *(const int64_t*)&s_codes[buf][mt * 16 + nl][8 * kq + 32 * j];
+                const v4i d = mfma16(av, bq, v4i{0, 0, 0, 0});
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    S[mt][i] += rint(dwj * s_dad[buf][mt * 16 + 4 * kq + i][j] * (double)d[i]);   // |dot| <= 32*127*127
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        stage_store(buf ^ 1, cv, dv);
+        __syncthreads();
+        wc = wn;
+    }
+
+    double* g = a.gsum + (int64_t)tile * 64 + nrow;
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = rbase + mt * 16 + 4 * kq + i;
+            if (m < M) {
+                double* p = g + (int64_t)(a.m0 + m) * a.n_pad;
+                if (a.ksplit == 1) *p = S[mt][i];
+                else unsafeAtomicAdd(p, S[mt][i]);
+            }
+        }
+}
+
 }  // namespace
 
 bool cpv_qgemm_wide_ok(const cpv_weight* w, int64_t m)
 {
-    return w->type == CPV_Q4_K && m >= CPV_WIDE_MIN_ROWS;
+    return (w->type == CPV_Q4_K || w->type == CPV_Q8_0) && m >= CPV_WIDE_MIN_ROWS;
 }
 
 cpv_status cpv_qgemm_wide(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, double* gsum, int win)
 {
-    if (w->type != CPV_Q4_K || !act->kq || act->U != (int)w->units || act->m < 1 || act->m > INT32_MAX / 2)
+    const bool q80 = w->type == CPV_Q8_0;
+    if ((w->type != CPV_Q4_K && !q80) || act->kq == q80 || act->U != (int)w->units || act->m < 1 ||
+        act->m > INT32_MAX / 2)
         return cpv_fail(ctx, CPV_EINVAL, "qgemm_wide: weight or activation format not supported");
     if ((int64_t)WBM * act->U * 256 > INT32_MAX)   // the staging offsets within a row block are 32-bit
         return cpv_fail(ctx, CPV_EUNSUPPORTED, "qgemm_wide: k=%lld too long", (long long)w->k);
@@ -259,14 +390,18 @@ cpv_status cpv_qgemm_wide(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act,
     const int64_t grid = blocks * a.ksplit;
     if (grid > INT32_MAX) return cpv_fail(ctx, CPV_EUNSUPPORTED, "qgemm_wide: grid of %lld", (long long)grid);
     const int ev = cpv_prof_mark(ctx);
-    auto go = [=]() { qgemm_wide_kernel<<<(unsigned)grid, WT, 0, ctx->stream>>>(a); };
+    auto go = [=]() {
+        if (q80) qgemm_wide_q80_kernel<<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
+        else qgemm_wide_kernel<<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
+    };
     go();
     CPV_HIP(ctx, hipGetLastError());
     if (ev >= 0) {  // algorithmic bytes: the weight, f32 activations in, f32 outputs
-        const double bytes = (double)w->n * (double)(w->k / 256) * 144.0 + 4.0 * a.M * (double)w->k +
-                             4.0 * a.M * (double)w->n;
-        cpv_prof_add(ctx, ev, CPV_PROF_Q4_K_WIDE, bytes);
-        cpv_prof_keep(ctx, CPV_PROF_Q4_K_WIDE, bytes, go);
+        const double bytes = (double)w->n * (q80 ? (double)(w->k / 32) * 34.0 : (double)(w->k / 256) * 144.0) +
+                             4.0 * a.M * (double)w->k + 4.0 * a.M * (double)w->n;
+        const int cls = q80 ? CPV_PROF_Q8_0_WIDE : CPV_PROF_Q4_K_WIDE;
+        cpv_prof_add(ctx, ev, cls, bytes);
+        cpv_prof_keep(ctx, cls, bytes, go);
     }
     return CPV_OK;
 }

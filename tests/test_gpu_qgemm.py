@@ -5,7 +5,8 @@ reproduce the oracle's f32 outputs bit for bit at every shape, including the
 27B-class verify shapes (K, N) in {(5120, 7168), (5120, 5120), (5120, 17408),
 (17408, 5120)} with M in {1, 5, 8, 16}; up to 16 rows share one pass over
 the weights (12 and 24 rows check the partial and split launches; Q4_K above
-8 rows runs on the 16x16x32 MFMA kernel).
+8 rows runs on the 16x16x32 MFMA kernel).  From 32 rows on, Q4_K and Q8_0
+run on the wide (prefill) kernels, held to the same bar.
 """
 import numpy as np
 import pytest
@@ -99,29 +100,40 @@ def test_qgemm_extreme_scales_and_zero_rows(ctx, tname, m):
     assert np.all(y[1] == 0) and np.all(y[:, 5] == 0)
 
 
-# ---- the wide Q4_K kernel (32 rows and more: the prompt prefill)
+# ---- the wide Q4_K and Q8_0 kernels (32 rows and more: the prompt prefill)
 
+@pytest.mark.parametrize("tname", ["q4_k", "q8_0"])
 @pytest.mark.parametrize("n,k", [(64, 256), (1000, 768), (33, 1024), (160, 4096)])
 @pytest.mark.parametrize("m", [32, 37, 64, 100, 256])
-def test_qgemm_wide_bit_exact_small(ctx, n, k, m):
-    y, ref = run_case(ctx, cpvo.Q4_K, n, k, m)
+def test_qgemm_wide_bit_exact_small(ctx, tname, n, k, m):
+    y, ref = run_case(ctx, TYPES[tname], n, k, m)
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), np.abs(y - ref).max()
 
 
+@pytest.mark.parametrize("m", [32, 100])
+def test_qgemm_wide_q8_0_partial_unit(ctx, m):
+    # K = 800: 25 blocks of 32, so the last 256-element unit holds one block
+    y, ref = run_case(ctx, cpvo.Q8_0, 40, 800, m)
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), np.abs(y - ref).max()
+
+
+@pytest.mark.parametrize("tname", ["q4_k", "q8_0"])
 @pytest.mark.parametrize("k,n", [(5120, 7168), (5120, 5120), (5120, 17408), (17408, 5120)])
 @pytest.mark.parametrize("m", [64, 256])
-def test_qgemm_wide_bit_exact_prefill_shapes(ctx, k, n, m):
-    y, ref = run_case(ctx, cpvo.Q4_K, n, k, m)
+def test_qgemm_wide_bit_exact_prefill_shapes(ctx, tname, k, n, m):
+    y, ref = run_case(ctx, TYPES[tname], n, k, m)
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), np.abs(y - ref).max()
 
 
-def test_qgemm_wide_rows_match_the_skinny_kernel(ctx):
+@pytest.mark.parametrize("tname", ["q4_k", "q8_0"])
+def test_qgemm_wide_rows_match_the_skinny_kernel(ctx, tname):
     # a row's outputs do not depend on the rows batched with it: the wide
     # launch over 96 rows against the skinny kernel on 8-row slices
+    t = TYPES[tname]
     n, k = 5120, 17408
-    wq = weights(cpvo.Q4_K, n, k)
+    wq = weights(t, n, k)
     x = torch.from_numpy(np.random.default_rng(11).normal(0, 1, size=(96, k)).astype(np.float32)).cuda()
-    w = ctx.upload_weight(cpvo.Q4_K, wq, n, k)
+    w = ctx.upload_weight(t, wq, n, k)
     yw = ctx.qgemm(w, x).cpu().numpy()
     for r in range(0, 96, 8):
         ys = ctx.qgemm(w, x[r:r + 8].contiguous()).cpu().numpy()
@@ -129,8 +141,9 @@ def test_qgemm_wide_rows_match_the_skinny_kernel(ctx):
     w.free()
 
 
-def test_qgemm_wide_extreme_scales_and_zero_rows(ctx):
-    t = cpvo.Q4_K
+@pytest.mark.parametrize("tname", ["q4_k", "q8_0"])
+def test_qgemm_wide_extreme_scales_and_zero_rows(ctx, tname):
+    t = TYPES[tname]
     n, k = 96, 1280
     rng = np.random.default_rng(4)
     wf = rng.normal(0, 0.02, size=(n, k)).astype(np.float32)
