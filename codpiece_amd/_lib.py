@@ -78,8 +78,10 @@ class GgufInfo(ctypes.Structure):
     ]
 
 
-PROF_Q4_K, PROF_Q6_K, PROF_Q8_0, PROF_ATTN, PROF_SAMPLE, PROF_Q4_K_WIDE, PROF_Q8_0_WIDE, PROF_CLASSES = range(8)
-PROF_NAMES = ("qgemm_q4_k", "qgemm_q6_k", "qgemm_q8_0", "attention", "sampler", "qgemm_q4_k_wide", "qgemm_q8_0_wide")
+(PROF_Q4_K, PROF_Q6_K, PROF_Q8_0, PROF_ATTN, PROF_SAMPLE, PROF_Q4_K_WIDE, PROF_Q8_0_WIDE, PROF_Q6_K_WIDE,
+ PROF_CLASSES) = range(9)
+PROF_NAMES = ("qgemm_q4_k", "qgemm_q6_k", "qgemm_q8_0", "attention", "sampler", "qgemm_q4_k_wide", "qgemm_q8_0_wide",
+              "qgemm_q6_k_wide")
 
 
 class ProfStat(ctypes.Structure):

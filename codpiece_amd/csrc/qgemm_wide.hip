@@ -1,4 +1,5 @@
-// qgemm_wide.hip — the Q4_K GEMM for many activation rows (prompt prefill).
+// qgemm_wide.hip — the GEMMs for many activation rows (prompt prefill): Q4_K
+// first, then Q8_0 and Q6_K (below) on the same mapping.
 //
 // The prefill pushes a chunk of the prompt through the trunk as one batch of
 // rows (engine.rs:1922-1953, step_greedy -> run_general, qwen35.rs:1125-1302),
@@ -353,17 +354,180 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qg
         }
 }
 
+// The same for Q6_K weights (Q8_K activations).  Per (activation row m,
+// weight row n, unit) the integer isum = sum_g sc_g * dot_g over the 16
+// groups of 16 codes (q - 32), then one binary64 term rint(A * isum) as the
+// contract has it.  Per 32-element chunk c (half h = c / 4, quarter s = c %
+// 4) a lane's 8 codes are the low (s < 2) or high nibbles of ql bytes 64 h +
+// 32 (s & 1) + 8 kq .., with qh bits 2 s, 2 s + 1 of bytes 32 h + 8 kq ..
+// above them; the chunk's two groups go through two MFMAs whose B operands
+// hold the codes in the group's k slots (kq < 2, kq >= 2) and zeros in the
+// other's.  A unit's pieces: ql 0-7, qh 8-11, the 16 group scales 12; the
+// unit's d (f16) lies in a region of its own after the tiles.
+__global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_wide_q6k_kernel(WideArgs a)
+{
+    __shared__ __align__(16) uint8_t s_codes[2][WBM][WROW];
+    __shared__ double s_dad[2][WBM];    // da * 2^(win - Ea) per staged row
+    __shared__ double s_sm[WBM];        // 2^(win - Ea(m)), 0 for an all-zero row
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int U = a.U, M = a.M;
+    const int64_t Kp = (int64_t)U * 256;
+
+    const int nb = gridDim.x, b0 = blockIdx.x;
+    const int L = (nb & 7) == 0 ? (b0 & 7) * (nb >> 3) + (b0 >> 3) : b0;
+    const int mb = L % a.mblocks, r0 = L / a.mblocks;
+    const int ks = r0 % a.ksplit, tile = r0 / a.ksplit;
+    const int u0 = ks * a.upk, u1 = min(U, u0 + a.upk);
+    const int rbase = mb * WBM;
+
+    for (int r = wave; r < WBM; r += WT / 64) {
+        const int mr = a.m0 + min(rbase + r, M - 1);
+        float mx = 0.0f;
+        for (int u = lane; u < U; u += 64) mx = fmaxf(mx, fabsf(a.da[(int64_t)mr * U + u]));
+        mx = cpv_wave_reduce(mx, cpv_op_max());
+        if (lane == 0) {
+            int e = CPV_E_EMPTY;
+            if (mx > 0.0f) frexpf(mx, &e);
+            s_sm[r] = e == CPV_E_EMPTY ? 0.0 : ldexp(1.0, a.win - e);
+        }
+    }
+
+    const int8_t* qbase = a.qa + (int64_t)(a.m0 + rbase) * Kp;
+    int soff[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int p = tid + q * WT, r = p >> 4;
+        soff[q] = (min(rbase + r, M - 1) - rbase) * (int)Kp + (p & 15) * 16;
+    }
+    const float* sda = a.da + (int64_t)(a.m0 + min(rbase + (tid & 63), M - 1)) * U;
+    auto stage_load = [&](int u, v4i* cv, float& dv) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) cv[q] = *(const v4i*)(qbase + soff[q] + u * 256);
+        dv = sda[u];
+    };
+    auto stage_store = [&](int buf, const v4i* cv, float dv) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int p = tid + q * WT;
+            *(v4i*)&s_codes[buf][p >> 4][(p & 15) * 16] = cv[q];
+        }
+        if (tid < WBM) s_dad[buf][tid] = (double)dv * s_sm[tid];
+    };
+
+    const int nl = lane & 15, kq = lane >> 4;
+    const int nrow = wave * 16 + nl;
+    const uint8_t* wrow = a.w + (int64_t)tile * U * 13 * 1024 + nrow * 16;
+    const uint16_t* drow = (const uint16_t*)(a.w + (int64_t)(a.n_pad / 64) * U * 13 * 1024) + (int64_t)tile * U * 64 + nrow;
+    struct Wt { v2i ql[2][2]; v2i qh[2]; v4i s; uint32_t d; };
+    auto wload = [&](int u, Wt& t) {
+        const uint8_t* p = wrow + (int64_t)u * 13 * 1024 + 8 * (kq & 1);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+#pragma unroll
+            for (int s1 = 0; s1 < 2; s1++) t.ql[h][s1] = *(const v2i*)(p + (4 * h + 2 * s1 + (kq >> 1)) * 1024);
+            t.qh[h] = *(const v2i*)(p + (8 + 2 * h + (kq >> 1)) * 1024);
+        }
+        t.s = *(const v4i*)(wrow + (int64_t)u * 13 * 1024 + 12 * 1024);
+        t.d = drow[(int64_t)u * 64];
+    };
+    const int er = a.ew[(int64_t)tile * 64 + nrow];
+    // the 4 codes of a dword as signed bytes q - 32 (q in 0..63: q ^ 32,
+    // with bits 6 and 7 set where q < 32)
+    auto centered = [](uint32_t q) {
+        const uint32_t t = q ^ 0x20202020u;
+        return t | (((t >> 5) & 0x01010101u) * 0xc0u);
+    };
+
+    double S[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) S[mt][i] = 0.0;
+
+    Wt wc, wn;
+    v4i cv[4];
+    float dv;
+    wload(u0, wc);
+    stage_load(u0, cv, dv);
+    __syncthreads();                    // s_sm
+    stage_store(0, cv, dv);
+    __syncthreads();
+
+    for (int u = u0; u < u1; u++) {
+        const int buf = (u - u0) & 1;
+        const int un = u + 1 < u1 ? u + 1 : u;
+        wload(un, wn);
+        stage_load(un, cv, dv);
+        const double dws = ldexp((double)cpv_h2f((uint16_t)wc.d), -er);
+        int isum[4][4];
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) isum[mt][i] = 0;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const int h = c >> 2, sq = c & 3;
+            uint32_t cw[2];
+#pragma unroll
+            for (int x = 0; x < 2; x++) {
+                const uint32_t lo = ((uint32_t)wc.ql[h][sq & 1][x] >> (4 * (sq >> 1))) & 0x0f0f0f0fu;
+                const uint32_t hi = (((uint32_t)wc.qh[h][x] >> (2 * sq)) & 0x03030303u) << 4;
+                cw[x] = centered(lo | hi);
+            }
+            const int64_t bc = pack2(cw[0], cw[1]);
+            const int64_t b0v = kq < 2 ? bc : 0, b1v = kq < 2 ? 0 : bc;   // group 2c, group 2c + 1
+            const uint32_t sw = (uint32_t)wc.s[c >> 1];
+            const int sc0 = (int)(int8_t)(sw >> (16 * (c & 1))), sc1 = (int)(int8_t)(sw >> (16 * (c & 1) + 8));
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++) {
+                const int64_t av = *(const int64_t*)&s_codes[buf][mt * 16 + nl][8 * kq + 32 * c];
+                const v4i d0 = mfma16(av, b0v, v4i{0, 0, 0, 0});
+                const v4i d1 = mfma16(av, b1v, v4i{0, 0, 0, 0});
+#pragma unroll
+                for (int i = 0; i < 4; i++) isum[mt][i] += sc0 * d0[i] + sc1 * d1[i];   // |isum| < 2^28
+            }
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++)
+                asm volatile("" : "+v"(isum[mt][0]), "+v"(isum[mt][1]), "+v"(isum[mt][2]), "+v"(isum[mt][3]));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++) {
+            const double* dd = &s_dad[buf][mt * 16 + 4 * kq];
+#pragma unroll
+            for (int i = 0; i < 4; i++) S[mt][i] += rint(dws * dd[i] * (double)isum[mt][i]);
+        }
+        stage_store(buf ^ 1, cv, dv);
+        __syncthreads();
+        wc = wn;
+    }
+
+    double* g = a.gsum + (int64_t)tile * 64 + nrow;
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = rbase + mt * 16 + 4 * kq + i;
+            if (m < M) {
+                double* p = g + (int64_t)(a.m0 + m) * a.n_pad;
+                if (a.ksplit == 1) *p = S[mt][i];
+                else unsafeAtomicAdd(p, S[mt][i]);
+            }
+        }
+}
+
 }  // namespace
 
 bool cpv_qgemm_wide_ok(const cpv_weight* w, int64_t m)
 {
-    return (w->type == CPV_Q4_K || w->type == CPV_Q8_0) && m >= CPV_WIDE_MIN_ROWS;
+    return (w->type == CPV_Q4_K || w->type == CPV_Q6_K || w->type == CPV_Q8_0) && m >= CPV_WIDE_MIN_ROWS;
 }
 
 cpv_status cpv_qgemm_wide(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, double* gsum, int win)
 {
-    const bool q80 = w->type == CPV_Q8_0;
-    if ((w->type != CPV_Q4_K && !q80) || act->kq == q80 || act->U != (int)w->units || act->m < 1 ||
+    const bool q80 = w->type == CPV_Q8_0, q6k = w->type == CPV_Q6_K;
+    if ((w->type != CPV_Q4_K && !q80 && !q6k) || act->kq == q80 || act->U != (int)w->units || act->m < 1 ||
         act->m > INT32_MAX / 2)
         return cpv_fail(ctx, CPV_EINVAL, "qgemm_wide: weight or activation format not supported");
     if ((int64_t)WBM * act->U * 256 > INT32_MAX)   // the staging offsets within a row block are 32-bit
@@ -392,14 +556,15 @@ cpv_status cpv_qgemm_wide(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act,
     const int ev = cpv_prof_mark(ctx);
     auto go = [=]() {
         if (q80) qgemm_wide_q80_kernel<<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
+        else if (q6k) qgemm_wide_q6k_kernel<<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
         else qgemm_wide_kernel<<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
     };
     go();
     CPV_HIP(ctx, hipGetLastError());
     if (ev >= 0) {  // algorithmic bytes: the weight, f32 activations in, f32 outputs
-        const double bytes = (double)w->n * (q80 ? (double)(w->k / 32) * 34.0 : (double)(w->k / 256) * 144.0) +
-                             4.0 * a.M * (double)w->k + 4.0 * a.M * (double)w->n;
-        const int cls = q80 ? CPV_PROF_Q8_0_WIDE : CPV_PROF_Q4_K_WIDE;
+        const double wrow_b = q80 ? (double)(w->k / 32) * 34.0 : (double)(w->k / 256) * (q6k ? 210.0 : 144.0);
+        const double bytes = (double)w->n * wrow_b + 4.0 * a.M * (double)w->k + 4.0 * a.M * (double)w->n;
+        const int cls = q80 ? CPV_PROF_Q8_0_WIDE : q6k ? CPV_PROF_Q6_K_WIDE : CPV_PROF_Q4_K_WIDE;
         cpv_prof_add(ctx, ev, cls, bytes);
         cpv_prof_keep(ctx, cls, bytes, go);
     }

@@ -383,7 +383,7 @@ cpv_status  cpv_session_commit_branch(cpv_session* s, const int32_t* path_host, 
  * rows read once).  The events add a little time between launches: time
  * throughput without them. */
 enum { CPV_PROF_Q4_K = 0, CPV_PROF_Q6_K = 1, CPV_PROF_Q8_0 = 2, CPV_PROF_ATTN = 3, CPV_PROF_SAMPLE = 4,
-       CPV_PROF_Q4_K_WIDE = 5, CPV_PROF_Q8_0_WIDE = 6, CPV_PROF_CLASSES = 7 };
+       CPV_PROF_Q4_K_WIDE = 5, CPV_PROF_Q8_0_WIDE = 6, CPV_PROF_Q6_K_WIDE = 7, CPV_PROF_CLASSES = 8 };
 typedef struct { int64_t launches; double ms; double bytes; } cpv_prof_stat;
 cpv_status  cpv_profile_start(cpv_ctx* ctx);
 cpv_status  cpv_profile_stop(cpv_ctx* ctx, cpv_prof_stat* out /* [CPV_PROF_CLASSES] */);

@@ -5,8 +5,8 @@ reproduce the oracle's f32 outputs bit for bit at every shape, including the
 27B-class verify shapes (K, N) in {(5120, 7168), (5120, 5120), (5120, 17408),
 (17408, 5120)} with M in {1, 5, 8, 16}; up to 16 rows share one pass over
 the weights (12 and 24 rows check the partial and split launches; Q4_K above
-8 rows runs on the 16x16x32 MFMA kernel).  From 32 rows on, Q4_K and Q8_0
-run on the wide (prefill) kernels, held to the same bar.
+8 rows runs on the 16x16x32 MFMA kernel).  From 32 rows on, every type runs
+on its wide (prefill) kernel, held to the same bar.
 """
 import numpy as np
 import pytest
@@ -100,9 +100,9 @@ def test_qgemm_extreme_scales_and_zero_rows(ctx, tname, m):
     assert np.all(y[1] == 0) and np.all(y[:, 5] == 0)
 
 
-# ---- the wide Q4_K and Q8_0 kernels (32 rows and more: the prompt prefill)
+# ---- the wide kernels (32 rows and more: the prompt prefill)
 
-@pytest.mark.parametrize("tname", ["q4_k", "q8_0"])
+@pytest.mark.parametrize("tname", ["q4_k", "q6_k", "q8_0"])
 @pytest.mark.parametrize("n,k", [(64, 256), (1000, 768), (33, 1024), (160, 4096)])
 @pytest.mark.parametrize("m", [32, 37, 64, 100, 256])
 def test_qgemm_wide_bit_exact_small(ctx, tname, n, k, m):
@@ -117,7 +117,7 @@ def test_qgemm_wide_q8_0_partial_unit(ctx, m):
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), np.abs(y - ref).max()
 
 
-@pytest.mark.parametrize("tname", ["q4_k", "q8_0"])
+@pytest.mark.parametrize("tname", ["q4_k", "q6_k", "q8_0"])
 @pytest.mark.parametrize("k,n", [(5120, 7168), (5120, 5120), (5120, 17408), (17408, 5120)])
 @pytest.mark.parametrize("m", [64, 256])
 def test_qgemm_wide_bit_exact_prefill_shapes(ctx, tname, k, n, m):
@@ -125,7 +125,7 @@ def test_qgemm_wide_bit_exact_prefill_shapes(ctx, tname, k, n, m):
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), np.abs(y - ref).max()
 
 
-@pytest.mark.parametrize("tname", ["q4_k", "q8_0"])
+@pytest.mark.parametrize("tname", ["q4_k", "q6_k", "q8_0"])
 def test_qgemm_wide_rows_match_the_skinny_kernel(ctx, tname):
     # a row's outputs do not depend on the rows batched with it: the wide
     # launch over 96 rows against the skinny kernel on 8-row slices
@@ -141,7 +141,7 @@ def test_qgemm_wide_rows_match_the_skinny_kernel(ctx, tname):
     w.free()
 
 
-@pytest.mark.parametrize("tname", ["q4_k", "q8_0"])
+@pytest.mark.parametrize("tname", ["q4_k", "q6_k", "q8_0"])
 def test_qgemm_wide_extreme_scales_and_zero_rows(ctx, tname):
     t = TYPES[tname]
     n, k = 96, 1280
