@@ -301,10 +301,10 @@ void cpv_act_layout(int type, int64_t m, int64_t k, void* buf, cpv_act* out);
 cpv_status cpv_quant_act(cpv_ctx* ctx, int type, const float* x, int64_t m, int64_t k, void* buf, cpv_act* out);
 cpv_status cpv_qgemm_act(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, float* y);
 
-// The Q4_K GEMM for many activation rows (qgemm_wide.hip): the same
-// accumulator sums as cpv_qgemm_act's skinny kernel, on the 16x16x32 int8
-// MFMA, for all act->m rows in one launch; cpv_qgemm_act takes it from
-// CPV_WIDE_MIN_ROWS rows on.
+// The GEMMs for many activation rows (qgemm_wide.hip): the same accumulator
+// sums as cpv_qgemm_act's skinny kernels, on the 16x16x32 int8 MFMA, for all
+// act->m rows in one launch; cpv_qgemm_act takes them from CPV_WIDE_MIN_ROWS
+// rows on (Q6_K from 9).
 constexpr int CPV_WIDE_MIN_ROWS = 32;
 bool cpv_qgemm_wide_ok(const cpv_weight* w, int64_t m);
 cpv_status cpv_qgemm_wide(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, double* gsum, int win);

@@ -232,10 +232,12 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(3))) void qg
 // eight terms per 256-element unit where Q4_K has two, so this kernel is
 // bound by its binary64 VALU work.  A unit's 17 pieces: 16 of codes (block j
 // in pieces 2j, 2j + 1), then the 8 block scales (f16).
+// NMT: 16-row blocks of the 64 that hold rows (fewer when M <= 48)
+template <int NMT>
 __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_wide_q80_kernel(WideArgs a)
 {
-    __shared__ __align__(16) uint8_t s_codes[2][WBM][WROW];
-    __shared__ double s_dad[2][WBM][8];  // da_j * 2^(win - Ea) per staged row and block
+    __shared__ __align__(16) uint8_t s_codes[2][16 * NMT][WROW];
+    __shared__ double s_dad[2][16 * NMT][8];   // da_j * 2^(win - Ea) per staged row and block
     __shared__ double s_sm[WBM];         // 2^(win - Ea(m)), 0 for an all-zero row
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -273,17 +275,19 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qg
     const float* sda = a.da + (int64_t)(a.m0 + min(rbase + srow, M - 1)) * NDA + sblk;
     auto stage_load = [&](int u, v4i* cv, float2& dv) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) cv[q] = *(const v4i*)(qbase + soff[q] + u * 256);
+        for (int q = 0; q < NMT; q++) cv[q] = *(const v4i*)(qbase + soff[q] + u * 256);
         dv = *(const float2*)(sda + 8 * u);
     };
     auto stage_store = [&](int buf, const v4i* cv, float2 dv) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
+        for (int q = 0; q < NMT; q++) {
             const int p = tid + q * WT;
             *(v4i*)&s_codes[buf][p >> 4][(p & 15) * 16] = cv[q];
         }
-        s_dad[buf][srow][sblk] = (double)dv.x * s_sm[srow];
-        s_dad[buf][srow][sblk + 1] = (double)dv.y * s_sm[srow];
+        if (srow < 16 * NMT) {
+            s_dad[buf][srow][sblk] = (double)dv.x * s_sm[srow];
+            s_dad[buf][srow][sblk + 1] = (double)dv.y * s_sm[srow];
+        }
     };
 
     // this lane's weight row and k slot: 8 codes of block j (bytes 8 (kq & 1)
@@ -300,14 +304,14 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qg
     };
     const int er = a.ew[(int64_t)tile * 64 + nrow];
 
-    double S[4][4];
+    double S[NMT][4];
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
+    for (int mt = 0; mt < NMT; mt++)
 #pragma unroll
         for (int i = 0; i < 4; i++) S[mt][i] = 0.0;
 
     Wt wc, wn;
-    v4i cv[4];
+    v4i cv[NMT];
     float2 dv;
     wload(u0, wc);
     stage_load(u0, cv, dv);
@@ -326,7 +330,7 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qg
             const double dwj = ldexp((double)cpv_h2f((uint16_t)((j & 1) ? hw >> 16 : hw & 0xffffu)), -er);
             const int64_t bq = pack2((uint32_t)wc.q[j][0], (uint32_t)wc.q[j][1]);
 #pragma unroll
-            for (int mt = 0; mt < 4; mt++) {
+            for (int mt = 0; mt < NMT; mt++) {
                 const int64_t av = *(const int64_t*)&s_codes[buf][mt * 16 + nl][8 * kq + 32 * j];
                 const v4i d = mfma16(av, bq, v4i{0, 0, 0, 0});
 #pragma unroll
@@ -342,7 +346,7 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qg
 
     double* g = a.gsum + (int64_t)tile * 64 + nrow;
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
+    for (int mt = 0; mt < NMT; mt++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int m = rbase + mt * 16 + 4 * kq + i;
@@ -364,10 +368,12 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qg
 // hold the codes in the group's k slots (kq < 2, kq >= 2) and zeros in the
 // other's.  A unit's pieces: ql 0-7, qh 8-11, the 16 group scales 12; the
 // unit's d (f16) lies in a region of its own after the tiles.
+// NMT: 16-row blocks of the 64 that hold rows (fewer when M <= 48)
+template <int NMT>
 __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_wide_q6k_kernel(WideArgs a)
 {
-    __shared__ __align__(16) uint8_t s_codes[2][WBM][WROW];
-    __shared__ double s_dad[2][WBM];    // da * 2^(win - Ea) per staged row
+    __shared__ __align__(16) uint8_t s_codes[2][16 * NMT][WROW];
+    __shared__ double s_dad[2][16 * NMT];   // da * 2^(win - Ea) per staged row
     __shared__ double s_sm[WBM];        // 2^(win - Ea(m)), 0 for an all-zero row
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -403,16 +409,16 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qg
     const float* sda = a.da + (int64_t)(a.m0 + min(rbase + (tid & 63), M - 1)) * U;
     auto stage_load = [&](int u, v4i* cv, float& dv) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) cv[q] = *(const v4i*)(qbase + soff[q] + u * 256);
+        for (int q = 0; q < NMT; q++) cv[q] = *(const v4i*)(qbase + soff[q] + u * 256);
         dv = sda[u];
     };
     auto stage_store = [&](int buf, const v4i* cv, float dv) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
+        for (int q = 0; q < NMT; q++) {
             const int p = tid + q * WT;
             *(v4i*)&s_codes[buf][p >> 4][(p & 15) * 16] = cv[q];
         }
-        if (tid < WBM) s_dad[buf][tid] = (double)dv * s_sm[tid];
+        if (tid < 16 * NMT) s_dad[buf][tid] = (double)dv * s_sm[tid];
     };
 
     const int nl = lane & 15, kq = lane >> 4;
@@ -439,14 +445,14 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qg
         return t | (((t >> 5) & 0x01010101u) * 0xc0u);
     };
 
-    double S[4][4];
+    double S[NMT][4];
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
+    for (int mt = 0; mt < NMT; mt++)
 #pragma unroll
         for (int i = 0; i < 4; i++) S[mt][i] = 0.0;
 
     Wt wc, wn;
-    v4i cv[4];
+    v4i cv[NMT];
     float dv;
     wload(u0, wc);
     stage_load(u0, cv, dv);
@@ -460,9 +466,9 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qg
         wload(un, wn);
         stage_load(un, cv, dv);
         const double dws = ldexp((double)cpv_h2f((uint16_t)wc.d), -er);
-        int isum[4][4];
+        int isum[NMT][4];
 #pragma unroll
-        for (int mt = 0; mt < 4; mt++)
+        for (int mt = 0; mt < NMT; mt++)
 #pragma unroll
             for (int i = 0; i < 4; i++) isum[mt][i] = 0;
 #pragma unroll
@@ -480,7 +486,7 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qg
             const uint32_t sw = (uint32_t)wc.s[c >> 1];
             const int sc0 = (int)(int8_t)(sw >> (16 * (c & 1))), sc1 = (int)(int8_t)(sw >> (16 * (c & 1) + 8));
 #pragma unroll
-            for (int mt = 0; mt < 4; mt++) {
+            for (int mt = 0; mt < NMT; mt++) {
                 const int64_t av = *(const int64_t*)&s_codes[buf][mt * 16 + nl][8 * kq + 32 * c];
                 const v4i d0 = mfma16(av, b0v, v4i{0, 0, 0, 0});
                 const v4i d1 = mfma16(av, b1v, v4i{0, 0, 0, 0});
@@ -488,12 +494,12 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qg
                 for (int i = 0; i < 4; i++) isum[mt][i] += sc0 * d0[i] + sc1 * d1[i];   // |isum| < 2^28
             }
 #pragma unroll
-            for (int mt = 0; mt < 4; mt++)
+            for (int mt = 0; mt < NMT; mt++)
                 asm volatile("" : "+v"(isum[mt][0]), "+v"(isum[mt][1]), "+v"(isum[mt][2]), "+v"(isum[mt][3]));
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int mt = 0; mt < 4; mt++) {
+        for (int mt = 0; mt < NMT; mt++) {
             const double* dd = &s_dad[buf][mt * 16 + 4 * kq];
 #pragma unroll
             for (int i = 0; i < 4; i++) S[mt][i] += rint(dws * dd[i] * (double)isum[mt][i]);
@@ -505,7 +511,7 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qg
 
     double* g = a.gsum + (int64_t)tile * 64 + nrow;
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
+    for (int mt = 0; mt < NMT; mt++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int m = rbase + mt * 16 + 4 * kq + i;
@@ -521,7 +527,11 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qg
 
 bool cpv_qgemm_wide_ok(const cpv_weight* w, int64_t m)
 {
-    return (w->type == CPV_Q4_K || w->type == CPV_Q6_K || w->type == CPV_Q8_0) && m >= CPV_WIDE_MIN_ROWS;
+    // (Q6_K from 9 rows: one 16-row block streams the weights once where the
+    // skinny kernel takes them in 8-row passes; Q8_0's 16-row block was no
+    // faster than its skinny kernel's one pass)
+    return ((w->type == CPV_Q4_K || w->type == CPV_Q8_0) && m >= CPV_WIDE_MIN_ROWS) ||
+           (w->type == CPV_Q6_K && m > 8);
 }
 
 cpv_status cpv_qgemm_wide(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, double* gsum, int win)
@@ -555,8 +565,12 @@ cpv_status cpv_qgemm_wide(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act,
     if (grid > INT32_MAX) return cpv_fail(ctx, CPV_EUNSUPPORTED, "qgemm_wide: grid of %lld", (long long)grid);
     const int ev = cpv_prof_mark(ctx);
     auto go = [=]() {
-        if (q80) qgemm_wide_q80_kernel<<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
-        else if (q6k) qgemm_wide_q6k_kernel<<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
+        if (q80 && a.M <= 16) qgemm_wide_q80_kernel<1><<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
+        else if (q80 && a.M <= 32) qgemm_wide_q80_kernel<2><<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
+        else if (q80) qgemm_wide_q80_kernel<4><<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
+        else if (q6k && a.M <= 16) qgemm_wide_q6k_kernel<1><<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
+        else if (q6k && a.M <= 32) qgemm_wide_q6k_kernel<2><<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
+        else if (q6k) qgemm_wide_q6k_kernel<4><<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
         else qgemm_wide_kernel<<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
     };
     go();
