@@ -1118,7 +1118,7 @@ static cpv_status qgemm_into(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* a
     for (int64_t m0 = 0; m0 < m;) {
         // rows per launch: up to 16 (Q6_K: 8, whose 16-row pass measured slower
         // than two 8-row ones: 397 vs 333 us for the 151,936-row head; above 8
-        // rows Q6_K takes the wide kernel), as many as LDS holds
+        // rows Q6_K and Q8_0 take the wide kernels), as many as LDS holds
         const int cap = w->type == CPV_Q6_K ? 8 : 16;
         int M = (int)((m - m0) < cap ? (m - m0) : cap);
         while (M > 1 && lds(M) > lds_cap) M--;

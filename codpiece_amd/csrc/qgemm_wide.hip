@@ -237,7 +237,7 @@ template <int NMT>
 __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_wide_q80_kernel(WideArgs a)
 {
     __shared__ __align__(16) uint8_t s_codes[2][16 * NMT][WROW];
-    __shared__ double s_dad[2][16 * NMT][8];   // da_j * 2^(win - Ea) per staged row and block
+    __shared__ double s_dad[2][16 * NMT + 1][8];   // da_j * 2^(win - Ea) per staged row and block (+ a dump row)
     __shared__ double s_sm[WBM];         // 2^(win - Ea(m)), 0 for an all-zero row
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -284,10 +284,11 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qg
             const int p = tid + q * WT;
             *(v4i*)&s_codes[buf][p >> 4][(p & 15) * 16] = cv[q];
         }
-        if (srow < 16 * NMT) {
-            s_dad[buf][srow][sblk] = (double)dv.x * s_sm[srow];
-            s_dad[buf][srow][sblk + 1] = (double)dv.y * s_sm[srow];
-        }
+        // (rows past the blocks write the dump row: a branch here made the
+        // compiler hold every load across it, 256 VGPRs and spills)
+        const int sr = srow < 16 * NMT ? srow : 16 * NMT;
+        s_dad[buf][sr][sblk] = (double)dv.x * s_sm[srow];
+        s_dad[buf][sr][sblk + 1] = (double)dv.y * s_sm[srow];
     };
 
     // this lane's weight row and k slot: 8 codes of block j (bytes 8 (kq & 1)
@@ -527,11 +528,10 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(2))) void qg
 
 bool cpv_qgemm_wide_ok(const cpv_weight* w, int64_t m)
 {
-    // (Q6_K from 9 rows: one 16-row block streams the weights once where the
-    // skinny kernel takes them in 8-row passes; Q8_0's 16-row block was no
-    // faster than its skinny kernel's one pass)
-    return ((w->type == CPV_Q4_K || w->type == CPV_Q8_0) && m >= CPV_WIDE_MIN_ROWS) ||
-           (w->type == CPV_Q6_K && m > 8);
+    // (Q6_K and Q8_0 from 9 rows: one 16-row block streams the weights once
+    // where Q6_K's skinny kernel takes them in 8-row passes and Q8_0's runs
+    // one wave per SIMD; Q4_K has its own 16-row kernel)
+    return (w->type == CPV_Q4_K && m >= CPV_WIDE_MIN_ROWS) || ((w->type == CPV_Q6_K || w->type == CPV_Q8_0) && m > 8);
 }
 
 cpv_status cpv_qgemm_wide(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, double* gsum, int win)
