@@ -1,0 +1,79 @@
+"""The built library's kernels: no register spills and no scratch beyond the
+known users.  Reads the gfx950 code objects that the build embedded in
+codpiece_amd/libcpv.so (clang offload bundles) and their AMDGPU metadata
+notes.  A spill is a regression to catch on the CPU: a branch around a
+staging store once cost a wide GEMM 256 VGPRs and 1 KB of scratch per lane,
+9x its time, with every parity test still green."""
+import os
+import struct
+
+import pytest
+
+msgpack = pytest.importorskip("msgpack")
+
+LIB = os.path.join(os.path.dirname(__file__), "..", "codpiece_amd", "libcpv.so")
+MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
+
+# scratch in bytes per lane: private arrays indexed at run time (the branch
+# commit's row copy, the acceptance walk's staging) and the sampler's spills
+SCRATCH_OK = {"compact_kernel": 144, "decide_kernel": 56, "dist_kernel": 168}
+# VGPRs spilled to scratch: the sampler's one-workgroup-per-row build runs
+# 1024 threads (128 VGPRs each); its spills are known and bounded here.
+# (SGPR spills go to VGPR lanes, not to memory, and are not counted.)
+SPILL_OK = {"dist_kernel": 86}
+
+
+def kernels():
+    data = open(LIB, "rb").read()
+    out = []
+    pos = data.find(MAGIC)
+    while pos >= 0:
+        n = struct.unpack_from("<Q", data, pos + 24)[0]
+        off = pos + 32
+        for _ in range(n):
+            eo, es, tl = struct.unpack_from("<QQQ", data, off)
+            triple = data[off + 24:off + 24 + tl].decode()
+            off += 24 + tl
+            if "gfx950" not in triple or not es:
+                continue
+            elf = data[pos + eo:pos + eo + es]
+            shoff = struct.unpack_from("<Q", elf, 0x28)[0]
+            shentsize, shnum = struct.unpack_from("<HH", elf, 0x3A)
+            for k in range(shnum):
+                sh = shoff + k * shentsize
+                if struct.unpack_from("<I", elf, sh + 4)[0] != 7:      # SHT_NOTE
+                    continue
+                so, ss = struct.unpack_from("<QQ", elf, sh + 0x18)
+                note, p = elf[so:so + ss], 0
+                while p + 12 <= len(note):
+                    namesz, descsz, ntype = struct.unpack_from("<III", note, p)
+                    name = note[p + 12:p + 12 + namesz]
+                    d0 = p + 12 + ((namesz + 3) & ~3)
+                    desc = note[d0:d0 + descsz]
+                    p = d0 + ((descsz + 3) & ~3)
+                    if name.startswith(b"AMDGPU") and ntype == 32:
+                        for kd in msgpack.unpackb(desc, raw=False).get("amdhsa.kernels", []):
+                            out.append(kd)
+        pos = data.find(MAGIC, pos + 1)
+    return out
+
+
+def short(name):
+    for key in set(SCRATCH_OK) | set(SPILL_OK):
+        if key in name:
+            return key
+    return name
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="libcpv.so not built")
+def test_no_spills_or_unexpected_scratch():
+    ks = kernels()
+    assert len(ks) > 50, len(ks)                       # every translation unit's code object was read
+    bad = []
+    for kd in ks:
+        name = short(kd[".name"])
+        spill = kd.get(".vgpr_spill_count", 0)
+        scratch = kd.get(".private_segment_fixed_size", 0)
+        if spill > SPILL_OK.get(name, 0) or scratch > SCRATCH_OK.get(name, 0):
+            bad.append((kd[".name"], spill, scratch, kd.get(".vgpr_count")))
+    assert not bad, bad
