@@ -392,8 +392,9 @@ def sampler_bench(torch, ctx, seed, reps=20):
 def gemm_bench(torch, ctx, seed, rotate_bytes=512e6):
     """The verify GEMM at its shapes: Q4_K and Q8_0 weights (random blocks
     with plausible scales) x f32 activations ~N(0, 1) of M rows, for each of
-    GEMM_SHAPES and M in {1, 5, 8, 16}, and at 256 rows (a prefill chunk's,
-    on the wide kernels: `TOP_s` is its int8 rate).  Each shape's weights are uploaded in
+    GEMM_SHAPES and M in {1, 5, 8, 16}, and at 256 rows (a prefill chunk's:
+    `TOP_s` is its int8 rate); `kernel` "wide" marks the launches the library
+    gave its wide kernels (Q8_0 from 9 rows, Q4_K from 32).  Each shape's weights are uploaded in
     enough copies to cover `rotate_bytes` (more than the 256 MB last-level
     cache), and consecutive calls rotate through them, so every call streams
     its weights from HBM.  `us` is the GEMM kernels' time per call (the
@@ -417,7 +418,6 @@ def gemm_bench(torch, ctx, seed, rotate_bytes=512e6):
                 del raw
             res = {"weights_MB": round(wbytes / 1e6, 2), "copies_rotated": copies}
             for M in (1, 5, 8, 16, 256):
-                mcls = cls + "_wide" if M >= 32 else cls
                 x = torch.randn(M, k, device=dev, generator=gen)
                 y = torch.empty(M, n, device=dev)
                 for w in ws[:2]:
@@ -426,6 +426,8 @@ def gemm_bench(torch, ctx, seed, rotate_bytes=512e6):
                 for w in ws:
                     ctx.qgemm(w, x, y)
                 prof = ctx.profile_stop()
+                # (the skinny or the wide kernel's class, as the library chose by rows)
+                mcls = cls if prof[cls][0] > 0 else cls + "_wide"
                 launches = prof[mcls][0]
                 ms, b = ctx.profile_replay(mcls, reps=3)
                 per = launches / copies
@@ -440,6 +442,8 @@ def gemm_bench(torch, ctx, seed, rotate_bytes=512e6):
                 res[f"M={M}"] = {"us": round(us, 2), "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
                                  "MB": round(b * per / 1e6, 2), "launches": per,
                                  "us_call": round(e0.elapsed_time(e1) * 1e3 / copies, 2)}
+                if mcls != cls:
+                    res[f"M={M}"]["kernel"] = "wide"
                 if M >= 32:
                     res[f"M={M}"]["TOP_s"] = round(2.0 * M * n * k / (us * 1e-6) / 1e12, 1)
             out[f"{name} {k}x{n}"] = res
