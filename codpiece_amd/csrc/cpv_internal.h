@@ -303,9 +303,8 @@ cpv_status cpv_qgemm_act(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, 
 
 // The GEMMs for many activation rows (qgemm_wide.hip): the same accumulator
 // sums as cpv_qgemm_act's skinny kernels, on the 16x16x32 int8 MFMA, for all
-// act->m rows in one launch; cpv_qgemm_act takes them from CPV_WIDE_MIN_ROWS
-// rows on (Q6_K and Q8_0 from 9).
-constexpr int CPV_WIDE_MIN_ROWS = 32;
+// act->m rows in one launch; cpv_qgemm_act takes them above 16 rows for
+// Q4_K and above 8 for Q6_K and Q8_0 (cpv_qgemm_wide_ok).
 bool cpv_qgemm_wide_ok(const cpv_weight* w, int64_t m);
 cpv_status cpv_qgemm_wide(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, double* gsum, int win);
 

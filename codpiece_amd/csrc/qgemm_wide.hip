@@ -60,10 +60,12 @@ __device__ __forceinline__ v4i mfma16(int64_t a, int64_t b, v4i c)
 
 __device__ __forceinline__ int byte_at(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xffu); }
 
+// NMT: 16-row blocks of the 64 that hold rows (fewer when M <= 48)
+template <int NMT>
 __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(3))) void qgemm_wide_kernel(WideArgs a)
 {
-    __shared__ __align__(16) uint8_t s_codes[2][WBM][WROW];
-    __shared__ double s_dad[2][WBM];    // da * 2^(win - Ea) per staged row
+    __shared__ __align__(16) uint8_t s_codes[2][16 * NMT][WROW];
+    __shared__ double s_dad[2][16 * NMT + 1];   // da * 2^(win - Ea) per staged row (+ a dump slot)
     __shared__ double s_sm[WBM];        // 2^(win - Ea(m)), 0 for an all-zero row
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -105,16 +107,18 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(3))) void qg
     const float* sda = a.da + (int64_t)(a.m0 + min(rbase + (tid & 63), M - 1)) * U;
     auto stage_load = [&](int u, v4i* cv, float& dv) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) cv[q] = *(const v4i*)(qbase + soff[q] + u * 256);
+        for (int q = 0; q < NMT; q++) cv[q] = *(const v4i*)(qbase + soff[q] + u * 256);
         dv = sda[u];
     };
     auto stage_store = [&](int buf, const v4i* cv, float dv) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
+        for (int q = 0; q < NMT; q++) {
             const int p = tid + q * WT;
             *(v4i*)&s_codes[buf][p >> 4][(p & 15) * 16] = cv[q];
         }
-        if (tid < WBM) s_dad[buf][tid] = (double)dv * s_sm[tid];
+        // (threads past the rows write the dump slot: no branch around the store)
+        const int sr = tid < 16 * NMT ? tid : 16 * NMT;
+        s_dad[buf][sr] = (double)dv * s_sm[tid & (WBM - 1)];
     };
 
     // this lane's weight row and k slot: 8 codes (bytes 8 (kq & 1).. of piece
@@ -131,14 +135,14 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(3))) void qg
     };
     const int er = a.ew[(int64_t)tile * 64 + nrow];
 
-    double S[4][4];
+    double S[NMT][4];
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
+    for (int mt = 0; mt < NMT; mt++)
 #pragma unroll
         for (int i = 0; i < 4; i++) S[mt][i] = 0.0;
 
     Wt wc, wn;
-    v4i cv[4];
+    v4i cv[NMT];
     float dv;
     wload(u0, wc);
     stage_load(u0, cv, dv);
@@ -163,10 +167,10 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(3))) void qg
         const uint32_t mn_hi = ((hw >> 4) & 0x0f0f0f0fu) | (((hz >> 6) & 0x03030303u) << 4);
         // per sub-block j: its B operands (codes, mn_j in every byte) built here, then
         // the four 16-row blocks; the dots are scaled by sc_j as they come
-        int isum[4][4];
-        v4i dmin[4];
+        int isum[NMT][4];
+        v4i dmin[NMT];
 #pragma unroll
-        for (int mt = 0; mt < 4; mt++) {
+        for (int mt = 0; mt < NMT; mt++) {
             dmin[mt] = v4i{0, 0, 0, 0};
 #pragma unroll
             for (int i = 0; i < 4; i++) isum[mt][i] = 0;
@@ -181,7 +185,7 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(3))) void qg
             const int64_t bm = pack2(bb, bb);
             const int scj = byte_at(j < 4 ? sc_lo : sc_hi, j & 3);
 #pragma unroll
-            for (int mt = 0; mt < 4; mt++) {
+            for (int mt = 0; mt < NMT; mt++) {
                 const int64_t av = *(const int64_t*)&s_codes[buf][mt * 16 + nl][8 * kq + 32 * j];
                 const v4i d = mfma16(av, bq, v4i{0, 0, 0, 0});
                 dmin[mt] = mfma16(av, bm, dmin[mt]);
@@ -192,12 +196,12 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(3))) void qg
             // compiler sinks them and keeps all 32 MFMA results live, which
             // costs the registers of a second wave per SIMD)
 #pragma unroll
-            for (int mt = 0; mt < 4; mt++)
+            for (int mt = 0; mt < NMT; mt++)
                 asm volatile("" : "+v"(isum[mt][0]), "+v"(isum[mt][1]), "+v"(isum[mt][2]), "+v"(isum[mt][3]));
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int mt = 0; mt < 4; mt++) {
+        for (int mt = 0; mt < NMT; mt++) {
             const double* dd = &s_dad[buf][mt * 16 + 4 * kq];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -213,7 +217,7 @@ __global__ __launch_bounds__(WT) __attribute__((amdgpu_waves_per_eu(3))) void qg
     // the sums: stored when this workgroup covers all of K, else added
     double* g = a.gsum + (int64_t)tile * 64 + nrow;
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
+    for (int mt = 0; mt < NMT; mt++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int m = rbase + mt * 16 + 4 * kq + i;
@@ -530,8 +534,9 @@ bool cpv_qgemm_wide_ok(const cpv_weight* w, int64_t m)
 {
     // (Q6_K and Q8_0 from 9 rows: one 16-row block streams the weights once
     // where Q6_K's skinny kernel takes them in 8-row passes and Q8_0's runs
-    // one wave per SIMD; Q4_K has its own 16-row kernel)
-    return (w->type == CPV_Q4_K && m >= CPV_WIDE_MIN_ROWS) || ((w->type == CPV_Q6_K || w->type == CPV_Q8_0) && m > 8);
+    // one wave per SIMD; Q4_K from 17, past its own 16-row kernel: at 24
+    // rows 34 against 46 us, at 16 the 16-row kernel's 27 against 28 us)
+    return (w->type == CPV_Q4_K && m > 16) || ((w->type == CPV_Q6_K || w->type == CPV_Q8_0) && m > 8);
 }
 
 cpv_status cpv_qgemm_wide(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act, double* gsum, int win)
@@ -571,7 +576,9 @@ cpv_status cpv_qgemm_wide(cpv_ctx* ctx, const cpv_weight* w, const cpv_act* act,
         else if (q6k && a.M <= 16) qgemm_wide_q6k_kernel<1><<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
         else if (q6k && a.M <= 32) qgemm_wide_q6k_kernel<2><<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
         else if (q6k) qgemm_wide_q6k_kernel<4><<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
-        else qgemm_wide_kernel<<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
+        else if (a.M <= 16) qgemm_wide_kernel<1><<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
+        else if (a.M <= 32) qgemm_wide_kernel<2><<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
+        else qgemm_wide_kernel<4><<<(unsigned)grid, WT, 0, ctx->stream>>>(a);
     };
     go();
     CPV_HIP(ctx, hipGetLastError());

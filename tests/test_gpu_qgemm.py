@@ -5,8 +5,9 @@ reproduce the oracle's f32 outputs bit for bit at every shape, including the
 27B-class verify shapes (K, N) in {(5120, 7168), (5120, 5120), (5120, 17408),
 (17408, 5120)} with M in {1, 5, 8, 16}; up to 16 rows share one pass over
 the weights (12 and 24 rows check the partial and split launches; Q4_K above
-8 rows runs on the 16x16x32 MFMA kernel).  From 32 rows on, every type runs
-on its wide (prefill) kernel, held to the same bar.
+8 rows runs on the 16x16x32 MFMA kernel).  Above 16 rows (Q4_K) or 8 rows
+(Q6_K, Q8_0) every type runs on its wide (prefill) kernel, held to the same
+bar.
 """
 import numpy as np
 import pytest
@@ -100,7 +101,7 @@ def test_qgemm_extreme_scales_and_zero_rows(ctx, tname, m):
     assert np.all(y[1] == 0) and np.all(y[:, 5] == 0)
 
 
-# ---- the wide kernels (32 rows and more: the prompt prefill)
+# ---- the wide kernels (the prompt prefill's rows; here 32 and more)
 
 @pytest.mark.parametrize("tname", ["q4_k", "q6_k", "q8_0"])
 @pytest.mark.parametrize("n,k", [(64, 256), (1000, 768), (33, 1024), (160, 4096)])
