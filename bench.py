@@ -391,10 +391,11 @@ def sampler_bench(torch, ctx, seed, reps=20):
 
 def gemm_bench(torch, ctx, seed, rotate_bytes=512e6):
     """The verify GEMM at its shapes: Q4_K and Q8_0 weights (random blocks
-    with plausible scales) x f32 activations ~N(0, 1) of M rows, for each of
+    with plausible scales; Q6_K too, the head's and a Q4_K_M file's other
+    type) x f32 activations ~N(0, 1) of M rows, for each of
     GEMM_SHAPES and M in {1, 5, 8, 16}, and at 256 rows (a prefill chunk's:
     `TOP_s` is its int8 rate); `kernel` "wide" marks the launches the library
-    gave its wide kernels (Q8_0 from 9 rows, Q4_K from 32).  Each shape's weights are uploaded in
+    gave its wide kernels (Q6_K and Q8_0 from 9 rows, Q4_K from 17).  Each shape's weights are uploaded in
     enough copies to cover `rotate_bytes` (more than the 256 MB last-level
     cache), and consecutive calls rotate through them, so every call streams
     its weights from HBM.  `us` is the GEMM kernels' time per call (the
@@ -406,7 +407,7 @@ def gemm_bench(torch, ctx, seed, rotate_bytes=512e6):
     gen = torch.Generator(device=ctx.torch_device).manual_seed(seed + 11)
     dev = ctx.torch_device
     out = {}
-    for qt, name in ((Q4_K, "q4_k"), (Q8_0, "q8_0")):
+    for qt, name in ((Q4_K, "q4_k"), (Q8_0, "q8_0"), (Q6_K, "q6_k")):
         cls = "qgemm_" + name
         for k, n in GEMM_SHAPES:
             wbytes = n * row_bytes(qt, k)
