@@ -19,10 +19,13 @@
 //  3. M = max m_c, f_c = expf(m_c - M); in chunk order Zt += (Z_c 2^-22) f_c
 //     (binary64) and O = fma(P_c, f_c, O) (f32); out = O * (float)(1 / Zt).
 //
-// Kernels: chunk (grid: chunk x KV head x 32-row query block; scores on the
-// MFMA, then the chunk's softmax and its P_c in the same workgroup) and fold
-// (one block per query row).  Scratch in the context workspace: P [chunks][T*H][D]
-// f32, m [chunks][T*H] f32, Z [chunks][T*H] int64.
+// Kernels: chunk (grid: chunk x KV head x query block of 32, 48 or 80 rows;
+// scores on the MFMA, then the chunk's softmax and its P_c in the same
+// workgroup) and fold (one block per query row), and over the API's caches a
+// first launch that makes the query rows' limbs once.  Scratch in the context
+// workspace: P (per chunk and query row, D f32: [chunks][T*H][D] for a
+// consumer's fold, [T*H][chunks][D] for the fold here), m [chunks][T*H] f32,
+// Z [chunks][T*H] int64, the query limbs.
 //
 // Layout.  A session's caches hold limbs, written once per row and read by
 // the MFMAs with no conversion: K as each row's hi and lo limbs per KV head
@@ -45,9 +48,9 @@ constexpr int PBITS = 22;           // a weight e in (0, 1] as p = rint(e 2^22):
 constexpr int PL = 3;
 constexpr int VBITS = CPV_ATTN_VBITS;   // an f16 value v as vq = rint(v 2^14): |vq| < 2^30, VLIMBS limbs
 constexpr int VLIMBS = CPV_ATTN_VLIMBS;
-constexpr int QB_CHAIN = 32;        // query rows per chunk workgroup: chains and prefill
-constexpr int QB_WIDE = 48;         //   and when a KV head has more than 80
-constexpr int QB_TREE = 80;         //   and when it has 49 to 80 (a 16-node tree's 5 x 16)
+constexpr int QB_CHAIN = 32;        // query rows per chunk workgroup: chains, prefill, fewer than 512 units;
+constexpr int QB_WIDE = 48;         //   from 512 (chunk, KV head) units on, when a KV head has more than 32,
+constexpr int QB_TREE = 80;         //   or, over the API's caches, 49 to 80 (a 16-node tree's 5 x 16)
 constexpr int E_EMPTY = CPV_E_EMPTY;   // exponent of an all-zero vector
 
 __device__ __forceinline__ int ceil_log2_dev(int64_t v)
