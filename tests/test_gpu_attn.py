@@ -80,6 +80,16 @@ def test_80_row_block_with_padding_rows(ctx, t, parent):
     close(*run(ctx, t, 40, 8, 128, 8192, parent, seed=t))
 
 
+@pytest.mark.parametrize("t,n_ctx", [(8, 8192), (20, 8192), (16, 4096)])
+def test_query_block_shapes(ctx, t, n_ctx):
+    # 40 Q / 8 KV heads, random trees: 40 query rows per KV head in one
+    # 48-row block, 100 in 48 + 48 + 4, both from 512 units on; and 80 rows
+    # below 512 units (4096 rows: 264 units) in 32-row blocks
+    rng = np.random.default_rng(t + n_ctx)
+    parent = [-1] + [int(rng.integers(-1, i)) for i in range(1, t)]
+    close(*run(ctx, t, 40, 8, 128, n_ctx, parent, seed=t))
+
+
 def test_80_row_block_d64(ctx):
     # d = 64, 2 KV heads: 257 chunks x 2 = 514 units, 64 query rows per KV head
     close(*run(ctx, 16, 8, 2, 64, 32768, TREE16, seed=64))
