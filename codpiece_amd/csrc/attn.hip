@@ -551,7 +551,15 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
     // wave's d-block, the limb products p_a v_b go to accumulator a + b
     // (weight 2^(8 (a + b))); S = sum of them exactly in int64 (|S| < 2^59);
     // P_c = (float)S * 2^-(PBITS + VBITS).  A lane holds D rows 4 g4 .. +3 of
-    // column c16.
+    // column c16.  Where the wave's values of a 64-row step all have a zero
+    // top limb (|v| < 2^(8 (VLIMBS - 1) - 1 - VBITS), 512 for f16 values at
+    // 2^14), that limb's products are zero and their MFMAs are skipped.
+    bool vtop[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+        const v4i t = vb[ks][VLIMBS - 1];
+        vtop[ks] = __builtin_amdgcn_ballot_w64((t[0] | t[1] | t[2] | t[3]) != 0) != 0;   // (wave-uniform)
+    }
     for (int rb = wave / NCB; rb < QB / 16; rb += CT / 64 / NCB) {
         if (blockIdx.z * QB + rb * 16 >= LR) break;   // (wave-uniform) past the query rows
         v4i acc[PL + VLIMBS - 1];
@@ -566,8 +574,14 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
 #pragma unroll
             for (int p = 0; p < PL; p++)
 #pragma unroll
-                for (int l = 0; l < VLIMBS; l++)
+                for (int l = 0; l < VLIMBS - 1; l++)
                     acc[p + l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa[p], vb[ks][l], acc[p + l], 0, 0, 0);
+            if (vtop[ks]) {
+#pragma unroll
+                for (int p = 0; p < PL; p++)
+                    acc[p + VLIMBS - 1] =
+                        __builtin_amdgcn_mfma_i32_16x16x64_i8(pa[p], vb[ks][VLIMBS - 1], acc[p + VLIMBS - 1], 0, 0, 0);
+            }
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) {

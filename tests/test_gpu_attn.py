@@ -95,6 +95,30 @@ def test_80_row_block_d64(ctx):
     close(*run(ctx, 16, 8, 2, 64, 32768, TREE16, seed=64))
 
 
+@pytest.mark.parametrize("n_past", [300, 8192])
+def test_large_values_use_the_top_value_limb(ctx, n_past):
+    # values of magnitude 512 and up carry a nonzero top limb (|vq| >= 2^23):
+    # scattered rows and columns of them, so that some 64-row steps of a
+    # wave hold one and others do not, next to small ones
+    rng = np.random.default_rng(n_past + 1)
+    t, h, hkv, d = 16, 40, 8, 128
+    n_ctx = n_past + t
+    k, v, vt = make(rng, n_ctx, hkv, d)
+    big = cpvo.f32_to_f16_bits((rng.normal(size=(n_ctx, hkv * d)) * 3000).astype(np.float32))
+    rows = rng.random(n_ctx) < 0.05
+    cols = rng.random(hkv * d) < 0.3
+    mask = rows[:, None] & cols[None, :]
+    v = np.where(mask, big, v)
+    vt[:, :n_ctx] = v.T
+    q = rng.normal(size=(t, h, d)).astype(np.float32)
+    scale = np.float32(1) / np.sqrt(np.float32(d))
+    par = torch.tensor(TREE16, dtype=torch.int32, device="cuda")
+    got = ctx.attn(torch.from_numpy(q).cuda(), torch.from_numpy(k.view(np.int16)).cuda(),
+                   torch.from_numpy(vt.view(np.int16)).cuda(), n_past, par, hkv, float(scale)).cpu().numpy()
+    ref = cpvo.attn(q, k, v, n_past, TREE16, scale)
+    close(got, ref)
+
+
 def test_tree_with_linear_parents_equals_chain(ctx):
     a, _ = run(ctx, 8, 8, 2, 64, 200, None, seed=3)
     b, _ = run(ctx, 8, 8, 2, 64, 200, list(range(-1, 7)), seed=3)
