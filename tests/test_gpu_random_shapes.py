@@ -1,5 +1,6 @@
-"""GPU parity on randomly drawn shapes: attention over the API's f16 caches
-and the quantized GEMM, against the oracle.
+"""GPU parity on randomly drawn shapes: attention over the API's f16 caches,
+the quantized GEMM, the target distributions and speculative acceptance,
+against the oracle.
 
 Bar: bit-exact, as everywhere else.  The fixed-shape tests pin the model's
 shapes and the kernels' thresholds one by one; these draw the shapes the
@@ -12,7 +13,13 @@ kernels' dispatch has to get right together, each case from its own seed:
 - GEMM: Q8_0, Q4_K and Q6_K; K up to 6144 (multiples of the block, so Q8_0
   also takes partial 256-element units); N from 1 to 5120; M at the
   kernels' row thresholds (8/9, 16/17, 32/33, 48/49, 64/65, ...) or anywhere
-  up to 256; activation scales 1e-3 to 50; zero weight and activation rows.
+  up to 256; activation scales 1e-3 to 50; zero weight and activation rows;
+- sampler: vocabularies of 1 to 262144 ids; 1-8 rows or 40-140 short ones;
+  logits of spread 0.05-10, with spikes, ties and masked (-inf) ids; every
+  filter (temperature 0-1.5, top-k past V, top-p, min-p, min_keep 0 to
+  5000) and the penalties over a history with empty slots; acceptance for
+  1-16 sequences of 0-8 drafts by argmax match, rejection (the one-hot rule
+  and the draft distribution, uniforms given or from Philox) and gumbel.
 """
 import numpy as np
 import pytest
@@ -103,3 +110,118 @@ def test_qgemm_random_shape(ctx, seed):
     w.free()
     ref = cpvo.qgemm(ty, wq, x)
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), np.abs(y - ref).max()
+
+
+def dev_params(p):
+    from codpiece_amd.runtime import SamplerParams
+    return SamplerParams(p.temp, p.top_k, p.top_p, p.min_p, p.min_keep, p.penalty_repeat, p.penalty_freq,
+                         p.penalty_present, p.penalty_last_n)
+
+
+def rand_v(rng):
+    r = rng.random()
+    if r < 0.2:
+        return int(rng.integers(1, 64))
+    if r < 0.5:
+        return int(rng.integers(64, 20000))
+    if r < 0.8:
+        return 151936
+    return int(rng.integers(20000, 262145))
+
+
+def rand_logits(rng, shape):
+    x = rng.normal(0, float(rng.choice([0.05, 1.0, 3.0, 10.0])), size=shape).astype(np.float32)
+    flat = x.reshape(-1, shape[-1])
+    if rng.random() < 0.5:
+        for r in range(flat.shape[0]):
+            flat[r, rng.integers(shape[-1])] += np.float32(rng.choice([3.0, 8.0, 20.0]))
+    if rng.random() < 0.25:                    # ties
+        x = (np.round(x * 2) / 2).astype(np.float32)
+    if rng.random() < 0.15:                    # masked ids (id 0 stays)
+        x[rng.random(size=shape) < 0.3] = -np.inf
+        x.reshape(-1, shape[-1])[:, 0] = 0.0
+    return np.ascontiguousarray(x)
+
+
+def rand_params(rng, V, penalties=True):
+    pen = penalties and rng.random() < 0.3
+    return cpvo.SamplerParams(
+        temp=float(rng.choice([0.0, 0.3, 0.7, 1.0, 1.5])),
+        top_k=0 if rng.random() < 0.5 else int(rng.integers(1, V + 6)),
+        top_p=1.0 if rng.random() < 0.3 else float(rng.uniform(0.05, 1.0)),
+        min_p=0.0 if rng.random() < 0.6 else float(rng.uniform(0.0, 0.3)),
+        min_keep=int(rng.choice([1, 0, int(rng.integers(1, 5000))])),
+        penalty_repeat=float(rng.choice([0.7, 1.3])) if pen else 1.0,
+        penalty_freq=float(rng.uniform(0, 0.5)) if pen else 0.0,
+        penalty_present=float(rng.uniform(0, 0.5)) if pen else 0.0,
+        penalty_last_n=int(rng.integers(0, 200)) if pen else 64)
+
+
+def rand_hist(rng, rows, V):
+    h = rng.integers(0, min(V, 500), size=(rows, int(rng.integers(1, 300)))).astype(np.int32)
+    h[rng.random(size=h.shape) < 0.1] = -1     # empty slots
+    return h
+
+
+def dev(a, dt=np.float32):
+    return None if a is None else torch.from_numpy(np.ascontiguousarray(a, dtype=dt)).cuda()
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_distribution_random(ctx, seed):
+    rng = np.random.default_rng(11000 + seed)
+    V = rand_v(rng)
+    rows = int(rng.integers(1, 9)) if rng.random() < 0.85 else int(rng.integers(40, 141))
+    if rows > 20 and V > 20000:
+        V = 8192
+    logits = rand_logits(rng, (rows, V))
+    p = rand_params(rng, V)
+    hist = rand_hist(rng, rows, V) if p.penalty_repeat != 1.0 else None
+    print(f"case rows={rows} V={V} temp={p.temp} top_k={p.top_k} top_p={p.top_p:.3f} min_p={p.min_p:.3f} "
+          f"min_keep={p.min_keep} penalties={hist is not None}", flush=True)
+    ids, probs, n = ctx.distribution(dev(logits), dev_params(p), dev(hist, np.int32))
+    ids, probs, n = ids.cpu().numpy(), probs.cpu().numpy(), n.cpu().numpy()
+    for r in range(rows):
+        hr = None if hist is None else ([x for x in hist[r] if x >= 0][-p.penalty_last_n:] if p.penalty_last_n else [])
+        rid, rp, _ = cpvo.distribution(p, logits[r], hr)
+        assert n[r] == rid.size, (r, n[r], rid.size)
+        assert np.array_equal(ids[r, :n[r]], rid), r
+        assert np.array_equal(probs[r, :n[r]].view(np.uint32), rp.view(np.uint32)), r
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_acceptance_random(ctx, seed):
+    rng = np.random.default_rng(12000 + seed)
+    V, B, k = rand_v(rng), int(rng.integers(1, 17)), int(rng.integers(0, 9))
+    if B * (k + 1) * V > 4e7:
+        V = max(1, int(4e7 // (B * (k + 1))))
+    pl = rand_logits(rng, (B, k + 1, V))
+    mode = (cpvo.ACCEPT_GREEDY, cpvo.ACCEPT_REJECT, cpvo.ACCEPT_REJECT, cpvo.ACCEPT_GUMBEL)[seed % 4]
+    p = rand_params(rng, V, penalties=mode == cpvo.ACCEPT_REJECT)
+    if mode == cpvo.ACCEPT_GUMBEL and p.temp == 0.0:
+        p.temp = 0.7
+    draft = rng.integers(0, V, size=(B, k)).astype(np.int32)
+    take = rng.random(size=(B, k)) < 0.7
+    draft[take] = pl.argmax(axis=2)[:, :k][take]
+    q = None
+    if mode == cpvo.ACCEPT_REJECT and rng.random() < 0.5:
+        q = (pl[:, :k] + rng.normal(0, 1, size=(B, k, V))).astype(np.float32)
+    noise = None
+    if mode == cpvo.ACCEPT_GUMBEL:
+        g = rng.random(size=(B, k + 1, V)).astype(np.float32)
+        noise = (-np.log(-np.log(np.maximum(g, 1e-12)))).astype(np.float32) * np.float32(p.temp)
+    hist = rand_hist(rng, B, V) if (mode == cpvo.ACCEPT_REJECT and p.penalty_repeat != 1.0) else None
+    philox = rng.random() < 0.5
+    ps, pr = int(rng.integers(0, 1 << 30)), int(rng.integers(0, 1000))
+    u = cpvo.philox_uniforms(ps, B, k, round=pr) if philox else rng.random(size=(B, k + 1, 2)).astype(np.float32)
+    print(f"case B={B} k={k} V={V} mode={mode} temp={p.temp} top_k={p.top_k} top_p={p.top_p:.3f} "
+          f"min_p={p.min_p:.3f} q={q is not None} penalties={hist is not None} philox={philox}", flush=True)
+    tok, n = ctx.spec_accept(dev(pl), dev(draft, np.int32), dev_params(p), mode, u=None if philox else dev(u),
+                             q_logits=dev(q), noise=dev(noise), hist=dev(hist, np.int32),
+                             philox_seed=ps if philox else 0, philox_round=pr if philox else 0)
+    tok, n = tok.cpu().numpy(), n.cpu().numpy()
+    rt, rn = cpvo.spec_accept(pl, draft, p, mode, u=u if mode == cpvo.ACCEPT_REJECT else None, q_logits=q,
+                              noise_t=noise, hist=hist)
+    assert np.array_equal(n, rn), (n, rn)
+    for b in range(B):
+        assert np.array_equal(tok[b, :n[b] + 1], rt[b, :rn[b] + 1]), (b, tok[b], rt[b])
