@@ -19,13 +19,20 @@ kernels' dispatch has to get right together, each case from its own seed:
   filter (temperature 0-1.5, top-k past V, top-p, min-p, min_keep 0 to
   5000) and the penalties over a history with empty slots; acceptance for
   1-16 sequences of 0-8 drafts by argmax match, rejection (the one-hot rule
-  and the draft distribution, uniforms given or from Philox) and gumbel.
+  and the draft distribution, uniforms given or from Philox) and gumbel;
+- whole rounds on random small models: 1-3 layers, d_model 256-5120, head
+  dim 64 or 128, 1-20 query heads over 1-4 KV heads, FFN 256-3072, Q8_0 or
+  Q4_K linears with a Q8_0, Q4_K or Q6_K head, with or without the MTP
+  layer; prompts prefilled in random chunks, then three rounds of 1-16 rows
+  at depth 0-4, each rewound to a random accepted prefix.
 """
 import numpy as np
 import pytest
 import torch
 
 from oracle import cpvo
+
+import model_fixtures as mf
 
 pytestmark = pytest.mark.gpu
 
@@ -225,3 +232,61 @@ def test_acceptance_random(ctx, seed):
     assert np.array_equal(n, rn), (n, rn)
     for b in range(B):
         assert np.array_equal(tok[b, :n[b] + 1], rt[b, :rn[b] + 1]), (b, tok[b], rt[b])
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_rounds_on_random_models(ctx, seed):
+    from codpiece_amd.model import Model, Session, make_hparams
+    rng = np.random.default_rng(13000 + seed)
+    qt = (cpvo.Q8_0, cpvo.Q4_K)[seed % 2]
+    while True:
+        hd, hkv = int(rng.choice([64, 128])), int(rng.choice([1, 2, 4]))
+        H = hkv * int(rng.choice([1, 2, 4, 5]))
+        if qt == cpvo.Q8_0 or (H * hd) % 256 == 0:    # (wo's K is H * hd)
+            break
+    E, F = 256 * int(rng.choice([1, 2, 3, 4, 6, 8, 20])), 256 * int(rng.integers(1, 13))
+    while E * F > 5120 * 1536:
+        F = max(256, F // 512 * 256)
+    hp = dict(mf.TINY, n_layer=int(rng.integers(1, 4)), n_embd=E, n_head=H, n_head_kv=hkv, head_dim=hd, n_rot=hd,
+              rope_sections=[11, 11, 10, 0] if hd == 64 else [22, 22, 20, 0], n_ff=F,
+              n_vocab=int(rng.integers(300, 6000)), has_mtp=int(rng.random() < 0.8))
+    ht = (cpvo.Q8_0, cpvo.Q4_K, cpvo.Q6_K)[int(rng.integers(0, 3))]
+    print(f"case {hp} linears={qt} head={ht}", flush=True)
+    tensors = mf.make_tensors(hp, seed=int(rng.integers(0, 1 << 20)), qtype=qt, head_type=ht)
+    gm = Model(ctx, make_hparams(**hp))
+    mf.load_into(gm, tensors)
+    gm.ready()
+    om = cpvo.Model(hp)
+    mf.load_into(om, tensors)
+    g, o = Session(gm, 1024, max_batch=256), cpvo.Session(om, 1024)
+    try:
+        n_prompt = int(rng.integers(1, 400))
+        prompt = rng.integers(0, hp["n_vocab"], size=n_prompt + 64).tolist()
+        c = 0
+        while c < n_prompt:
+            step = min(n_prompt - c, int(rng.choice([1, 5, 17, 64, 256])))
+            g.prefill(prompt[c:c + step])
+            o.prefill(prompt[c:c + step])
+            c += step
+        for _ in range(3):
+            T = int(rng.integers(1, 17))
+            depth = int(rng.integers(0, 5)) if hp["has_mtp"] else 0
+            print(f"round n_past={g.pos[0]} T={T} depth={depth}", flush=True)
+            a = g.step_fused_cached(prompt[c:c + T], depth, want_logits=True)
+            b = o.step_fused_cached(prompt[c:c + T], depth, want_logits=True)
+            assert np.array_equal(a.logits.cpu().numpy().view(np.uint32), b[3].view(np.uint32))
+            assert np.array_equal(a.hidden.cpu().numpy().view(np.uint32), b[4].view(np.uint32))
+            assert a.preds == b[0].tolist() and a.chain == b[1].tolist()
+            # keep a random accepted prefix; a round without drafts writes no
+            # MTP rows, so only a drafting round moves the MTP position
+            keep = int(rng.integers(1, T + 1))
+            n_past, mtp_past = g.pos
+            m2 = mtp_past + keep if depth > 0 else mtp_past
+            g.set_pos(n_past - T + keep, m2)
+            o.set_pos(n_past - T + keep, m2)
+            c += keep
+    finally:
+        g.free()
+        o.free()
+        gm.free()
+        om.free()
