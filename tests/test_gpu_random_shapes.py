@@ -24,7 +24,9 @@ kernels' dispatch has to get right together, each case from its own seed:
   dim 64 or 128, 1-20 query heads over 1-4 KV heads, FFN 256-3072, Q8_0 or
   Q4_K linears with a Q8_0, Q4_K or Q6_K head, with or without the MTP
   layer; prompts prefilled in random chunks, then three rounds of 1-16 rows
-  at depth 0-4, each rewound to a random accepted prefix.
+  at depth 0-4, each rewound to a random accepted prefix; random draft
+  trees of 1-64 nodes on such models, every leaf's path against the
+  oracle's chain of it, then a committed branch and the round after it.
 """
 import numpy as np
 import pytest
@@ -234,11 +236,9 @@ def test_acceptance_random(ctx, seed):
         assert np.array_equal(tok[b, :n[b] + 1], rt[b, :rn[b] + 1]), (b, tok[b], rt[b])
 
 
-@pytest.mark.parametrize("seed", range(8))
-def test_rounds_on_random_models(ctx, seed):
-    from codpiece_amd.model import Model, Session, make_hparams
-    rng = np.random.default_rng(13000 + seed)
-    qt = (cpvo.Q8_0, cpvo.Q4_K)[seed % 2]
+def random_models(ctx, rng, qt):
+    """A random small layout with its weights: (device model, oracle model, hparams)."""
+    from codpiece_amd.model import Model, make_hparams
     while True:
         hd, hkv = int(rng.choice([64, 128])), int(rng.choice([1, 2, 4]))
         H = hkv * int(rng.choice([1, 2, 4, 5]))
@@ -258,6 +258,14 @@ def test_rounds_on_random_models(ctx, seed):
     gm.ready()
     om = cpvo.Model(hp)
     mf.load_into(om, tensors)
+    return gm, om, hp
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_rounds_on_random_models(ctx, seed):
+    from codpiece_amd.model import Session
+    rng = np.random.default_rng(13000 + seed)
+    gm, om, hp = random_models(ctx, rng, (cpvo.Q8_0, cpvo.Q4_K)[seed % 2])
     g, o = Session(gm, 1024, max_batch=256), cpvo.Session(om, 1024)
     try:
         n_prompt = int(rng.integers(1, 400))
@@ -285,6 +293,60 @@ def test_rounds_on_random_models(ctx, seed):
             g.set_pos(n_past - T + keep, m2)
             o.set_pos(n_past - T + keep, m2)
             c += keep
+    finally:
+        g.free()
+        o.free()
+        gm.free()
+        om.free()
+
+
+def path_to(parent, v):
+    p = []
+    while v >= 0:
+        p.append(v)
+        v = parent[v]
+    return p[::-1]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_trees_on_random_models(ctx, seed):
+    # every leaf's root-to-node path of a random tree (1-64 nodes) equals the
+    # oracle's chain verify of that path from the same context; then a random
+    # node's path is committed and the next round equals the one after the
+    # oracle's chain of that path
+    from codpiece_amd.model import Session
+    rng = np.random.default_rng(14000 + seed)
+    gm, om, hp = random_models(ctx, rng, (cpvo.Q8_0, cpvo.Q4_K)[seed % 2])
+    V = hp["n_vocab"]
+    t = int(rng.integers(1, 65))
+    parent = [-1] + [int(rng.integers(-1, j)) for j in range(1, t)]
+    n_prompt = int(rng.integers(1, 300))
+    prompt = rng.integers(0, V, size=n_prompt).tolist()
+    toks = rng.integers(0, V, size=t).tolist()
+    g, o = Session(gm, 1024, max_batch=256), cpvo.Session(om, 1024)
+    try:
+        g.prefill(prompt)
+        o.prefill(prompt)
+        print(f"tree of {t} after {n_prompt}", flush=True)
+        a = g.verify_tree(toks, parent, want_logits=True)
+        la, ha = a.logits.cpu().numpy(), a.hidden.cpu().numpy()
+        for leaf in [v for v in range(t) if v not in parent]:
+            path = path_to(parent, leaf)
+            o.set_pos(n_prompt, 0)
+            b = o.step_fused_cached([toks[v] for v in path], 0, want_logits=True)
+            assert np.array_equal(la[path].view(np.uint32), b[3].view(np.uint32)), ("logits", path)
+            assert np.array_equal(ha[path].view(np.uint32), b[4].view(np.uint32)), ("hidden", path)
+            assert [a.preds[v] for v in path] == b[0].tolist()
+        path = path_to(parent, int(rng.integers(0, t)))
+        g.commit_branch(path)
+        o.set_pos(n_prompt, 0)
+        o.step_fused_cached([toks[v] for v in path], 0)
+        assert g.pos[0] == o.pos[0] == n_prompt + len(path)
+        nxt = rng.integers(0, V, size=int(rng.integers(1, 9))).tolist()
+        a = g.step_fused_cached(nxt, 0, want_logits=True)
+        b = o.step_fused_cached(nxt, 0, want_logits=True)
+        assert np.array_equal(a.logits.cpu().numpy().view(np.uint32), b[3].view(np.uint32))
+        assert a.preds == b[0].tolist()
     finally:
         g.free()
         o.free()
