@@ -613,58 +613,20 @@ extern "C" cpv_status cpv_weight_info(const cpv_weight* w, int* type, int64_t* n
 }
 
 // ---------------------------------------------------------------- get_rows
-// Dequantize from the repacked layout with ggml's f32 formulas:
-//   Q8_0: q * d;  Q4_K: (d*sc)*q - (dmin*m);  Q6_K: d*sc*q, left to right.
+// Dequantize from the repacked layout with ggml's f32 formulas
+// (cpv_dequant4), four elements per thread
 template <int TYPE>
 __global__ void get_rows_kernel(const uint8_t* __restrict__ data, const int32_t* __restrict__ rows,
                                 int64_t nrows, int64_t n, int64_t k, int64_t U, float* __restrict__ out)
 {
-    constexpr int PIECES = TYPE == CPV_Q4_K ? 9 : TYPE == CPV_Q6_K ? 13 : 17;
     const int64_t r_out = blockIdx.y;
     if (r_out >= nrows) return;
     const int64_t row = rows[r_out];
-    const int64_t tiles = (n + 63) / 64;
-    for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < k; e += (int64_t)gridDim.x * blockDim.x) {
-        float v = 0.0f;
-        if (row >= 0 && row < n) {
-            const int64_t t = row / 64;
-            const int lane = (int)(row % 64);
-            const int64_t u = e / 256;
-            const int el = (int)(e % 256);
-            const uint8_t* slab = data + (t * U + u) * PIECES * 1024 + lane * 16;
-            auto byte_at = [&](int idx) { return slab[(idx / 16) * 1024 + idx % 16]; };   // block byte idx of the piece run
-            if (TYPE == CPV_Q4_K) {
-                const uint8_t* meta = slab + 8 * 1024;
-                const int j = el / 32, l = el % 32;
-                const int qsbyte = (j / 2) * 32 + l;
-                const uint8_t byte = byte_at(qsbyte);
-                const int code = (j & 1) ? (byte >> 4) : (byte & 15);
-                const uint8_t* s = meta + 4;
-                int sc, m;
-                if (j < 4) { sc = s[j] & 63; m = s[j + 4] & 63; }
-                else { sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4); m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
-                const float d = f16_to_f32((uint16_t)(meta[0] | (meta[1] << 8)));
-                const float dm = f16_to_f32((uint16_t)(meta[2] | (meta[3] << 8)));
-                const float d1 = d * (float)sc, m1 = dm * (float)m;
-                v = d1 * (float)code - m1;
-            } else if (TYPE == CPV_Q6_K) {
-                const int h = el / 128, l = el % 128, l32 = l % 32, quad = l / 32;
-                const uint8_t ql = byte_at(h * 64 + l32 + (quad & 1) * 32);
-                const uint8_t qh = byte_at(128 + h * 32 + l32);
-                const int lo = (quad < 2) ? (ql & 15) : (ql >> 4);
-                const int code = (lo | (((qh >> (2 * quad)) & 3) << 4)) - 32;
-                const int8_t sc = (int8_t)byte_at(192 + el / 16);
-                const uint8_t* dd = data + tiles * U * 13 * 1024 + ((t * U + u) * 64 + lane) * 2;
-                const float d = f16_to_f32((uint16_t)(dd[0] | (dd[1] << 8)));
-                v = d * (float)sc * (float)code;
-            } else {
-                const int blk = el / 32;
-                const int8_t code = (int8_t)byte_at(el);
-                const uint8_t* dd = slab + 16 * 1024 + blk * 2;
-                v = (float)code * f16_to_f32((uint16_t)(dd[0] | (dd[1] << 8)));
-            }
-        }
-        out[r_out * k + e] = v;
+    for (int64_t e = 4 * (blockIdx.x * (int64_t)blockDim.x + threadIdx.x); e < k; e += 4 * (int64_t)gridDim.x * blockDim.x) {
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (row >= 0 && row < n) cpv_dequant4<TYPE>(data, n, U, row, e, v);
+#pragma unroll
+        for (int i = 0; i < 4; i++) out[r_out * k + e + i] = v[i];
     }
 }
 
@@ -674,7 +636,8 @@ extern "C" cpv_status cpv_get_rows(cpv_ctx* ctx, const cpv_weight* w, const int3
     if (!ctx || !w || !rows_dev || !out_dev || n < 0) return cpv_fail(ctx, CPV_EINVAL, "get_rows: bad arguments");
     if (n == 0) return CPV_OK;
     if (n > 65535) return cpv_fail(ctx, CPV_EINVAL, "get_rows: at most 65535 rows per call");
-    dim3 grid((unsigned)((w->k + 255) / 256), (unsigned)n);
+    // (four elements per thread: rows are whole 32-element blocks)
+    dim3 grid((unsigned)((w->k + 1023) / 1024), (unsigned)n);
     const uint8_t* d = (const uint8_t*)w->data;
     switch (w->type) {
     case CPV_Q4_K: get_rows_kernel<CPV_Q4_K><<<grid, 256, 0, ctx->stream>>>(d, rows_dev, n, w->n, w->k, w->units, out_dev); break;
@@ -692,7 +655,7 @@ extern "C" cpv_status cpv_get_rows(cpv_ctx* ctx, const cpv_weight* w, const int3
 // (2^32 - 1 - index), so the integer maximum of the keys is the largest value
 // at its first index (-0 is keyed as +0, which compares equal); 0 = no winner.
 // Pass 2 reduces a row's keys.
-constexpr int AM_NB = 64;
+constexpr int AM_NB = CPV_AM_NB;
 
 __device__ __forceinline__ unsigned long long am_key(float v, int64_t i)
 {
@@ -778,22 +741,55 @@ __global__ __launch_bounds__(64) void argmax_fin_kernel(const unsigned long long
 {
     const int64_t row = blockIdx.x;
     const unsigned long long v = cpv_wave_reduce(part[row * AM_NB + threadIdx.x], cpv_op_umax());
-    if (threadIdx.x == 0) out[row] = v ? (int32_t)(0xffffffffu - (uint32_t)v) : 0;
+    if (threadIdx.x == 0) out[row] = cpv_am_index(v);
+}
+
+// An embedding table whose rows of the argmax winners a draft chain's next
+// link takes (data null: none): the blocks of a row write row tok of it to
+// out[row], four elements per thread, as get_rows_kernel does
+struct EmbArgs {
+    const uint8_t* data;
+    int type;
+    int64_t n, k, U;
+    float* out;
+};
+
+__device__ __forceinline__ void embed_share(const EmbArgs& e, int64_t row, int64_t tok)
+{
+    if (!e.data) return;
+    for (int64_t i = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x); i < e.k; i += 4 * (int64_t)gridDim.x * blockDim.x) {
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (tok >= 0 && tok < e.n) cpv_dequant4_t(e.type, e.data, e.n, e.U, tok, i, v);
+#pragma unroll
+        for (int k = 0; k < 4; k++) e.out[row * e.k + i + k] = v[k];
+    }
+}
+
+// argmax_fin_kernel's index, with the winners' embedding rows: every block
+// reduces its row's keys
+__global__ __launch_bounds__(256) void argmax_embed_kernel(const unsigned long long* __restrict__ part,
+                                                           int32_t* __restrict__ idx_out, EmbArgs emb)
+{
+    const int64_t row = blockIdx.y;
+    const int32_t tok = cpv_am_index(cpv_wave_reduce(part[row * AM_NB + (threadIdx.x & 63)], cpv_op_umax()));
+    if (blockIdx.x == 0 && threadIdx.x == 0) idx_out[row] = tok;
+    embed_share(emb, row, tok);
 }
 
 // softmax peak: each slice's sum of expf(x - max) in binary64 (max from the
 // argmax keys), then the row's slices added in order.  Every block reduces
 // the row's argmax keys itself; block 0 stores the row's argmax index, as
-// argmax_fin_kernel would
+// argmax_fin_kernel would, and the first blocks the winners' embedding rows
 __global__ __launch_bounds__(256) void peak_part_kernel(const float* __restrict__ x, int64_t n, int64_t chunk,
                                                         const unsigned long long* __restrict__ part,
-                                                        double* __restrict__ psum, int32_t* __restrict__ idx_out)
+                                                        double* __restrict__ psum, int32_t* __restrict__ idx_out,
+                                                        EmbArgs emb)
 {
     __shared__ double s_d[4];
     const int64_t row = blockIdx.y, i0 = (int64_t)blockIdx.x * chunk;
     const int64_t i1 = i0 + chunk < n ? i0 + chunk : n;
     const unsigned long long k = cpv_wave_reduce(part[row * AM_NB + (threadIdx.x & 63)], cpv_op_umax());
-    if (blockIdx.x == 0 && threadIdx.x == 0) idx_out[row] = k ? (int32_t)(0xffffffffu - (uint32_t)k) : 0;
+    if (blockIdx.x == 0 && threadIdx.x == 0) idx_out[row] = cpv_am_index(k);
     const float mx = k ? am_value(k) : -INFINITY;
     const float* xr = x + row * n;
     double sum = 0.0;
@@ -802,15 +798,14 @@ __global__ __launch_bounds__(256) void peak_part_kernel(const float* __restrict_
     if ((threadIdx.x & 63) == 0) s_d[threadIdx.x >> 6] = sum;
     __syncthreads();
     if (threadIdx.x == 0) psum[row * AM_NB + blockIdx.x] = (s_d[0] + s_d[1]) + (s_d[2] + s_d[3]);
+    embed_share(emb, row, cpv_am_index(k));
 }
 
 __global__ void peak_fin_kernel(const double* __restrict__ psum, int64_t rows, float* __restrict__ out)
 {
     const int64_t row = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (row >= rows) return;
-    double tot = 0.0;
-    for (int b = 0; b < AM_NB; b++) tot += psum[row * AM_NB + b];
-    out[row] = 1.0f * (float)(1.0 / tot);
+    out[row] = cpv_peak_of(psum + row * AM_NB);
 }
 
 // the re-draft gate's bound pass: each slice's S = sum of e_i = expf(x_i -
@@ -826,7 +821,7 @@ __global__ __launch_bounds__(256) void gate_part_kernel(const float* __restrict_
     const int64_t row = blockIdx.y, i0 = (int64_t)blockIdx.x * chunk;
     const int64_t i1 = i0 + chunk < n ? i0 + chunk : n;
     const unsigned long long k = cpv_wave_reduce(part[row * AM_NB + (threadIdx.x & 63)], cpv_op_umax());
-    if (blockIdx.x == 0 && threadIdx.x == 0) idx_out[row] = k ? (int32_t)(0xffffffffu - (uint32_t)k) : 0;
+    if (blockIdx.x == 0 && threadIdx.x == 0) idx_out[row] = cpv_am_index(k);
     const float mx = k ? am_value(k) : -INFINITY;
     const float* xr = x + row * n;
     double S = 0.0, W = 0.0;
@@ -894,7 +889,8 @@ cpv_status cpv_argmax_gate_rows(cpv_ctx* ctx, const float* x, int64_t rows, int6
 }
 
 cpv_status cpv_argmax_peak_rows(cpv_ctx* ctx, const float* x, const float* noise, int64_t rows, int64_t n,
-                                int32_t* idx_out, float* peak_out, const cpv_gout* kept)
+                                int32_t* idx_out, float* peak_out, const cpv_gout* kept, cpv_am_fin* fin,
+                                const cpv_weight* emb, float* emb_out)
 {
     unsigned long long* part;
     double* psum;
@@ -904,12 +900,18 @@ cpv_status cpv_argmax_peak_rows(cpv_ctx* ctx, const float* x, const float* noise
     const dim3 grid(AM_NB, (unsigned)rows);
     if (kept) argmax_kept_part_kernel<<<grid, 256, 0, ctx->stream>>>(*kept, noise, chunk, const_cast<float*>(x), part);
     else argmax_part_kernel<<<grid, 256, 0, ctx->stream>>>(x, noise, n, chunk, part);
+    EmbArgs ea{};
+    if (emb) ea = EmbArgs{(const uint8_t*)emb->data, emb->type, emb->n, emb->k, emb->units, emb_out};
     if (peak_out) {
-        peak_part_kernel<<<grid, 256, 0, ctx->stream>>>(x, n, chunk, part, psum, idx_out);
-        peak_fin_kernel<<<(unsigned)((rows + 63) / 64), 64, 0, ctx->stream>>>(psum, rows, peak_out);
+        peak_part_kernel<<<grid, 256, 0, ctx->stream>>>(x, n, chunk, part, psum, idx_out, ea);
+        if (!fin) peak_fin_kernel<<<(unsigned)((rows + 63) / 64), 64, 0, ctx->stream>>>(psum, rows, peak_out);
+    } else if (emb) {
+        argmax_embed_kernel<<<dim3((unsigned)((emb->k + 1023) / 1024), (unsigned)rows), 256, 0, ctx->stream>>>(part, idx_out,
+                                                                                                          ea);
     } else {
         argmax_fin_kernel<<<(unsigned)rows, 64, 0, ctx->stream>>>(part, idx_out);
     }
+    if (fin) fin->psum = peak_out ? psum : nullptr;
     CPV_HIP(ctx, hipGetLastError());
     return CPV_OK;
 }

@@ -357,8 +357,99 @@ cpv_status cpv_weight_concat(cpv_ctx* ctx, cpv_weight* const* parts, int np, cpv
 // row (the sum in binary64), in two passes over 64 slices per row.  With
 // kept, the rows are first finalized from that kept GEMM result (n = kept->n)
 // into x, in the first pass.
+// With emb, the pass that stores idx_out also stores emb_out[r] = row
+// idx_out[r] of that embedding table, as cpv_get_rows would.  With fin and
+// peak_out, the peak's last pass is left to the kernel that consumes it: fin
+// receives the peak's slice sums [rows][CPV_AM_NB] (cpv_peak_of's order),
+// valid until the next argmax call on the context.
+struct cpv_am_fin {
+    const double* psum;
+};
 cpv_status cpv_argmax_peak_rows(cpv_ctx* ctx, const float* x, const float* noise, int64_t rows, int64_t n,
-                                int32_t* idx_out, float* peak_out, const cpv_gout* kept = nullptr);
+                                int32_t* idx_out, float* peak_out, const cpv_gout* kept = nullptr,
+                                cpv_am_fin* fin = nullptr, const cpv_weight* emb = nullptr, float* emb_out = nullptr);
+constexpr int CPV_AM_NB = 64;   // slices per row of the argmax and peak passes
+// a row's argmax from its slice keys: key = (order-preserving value bits) << 32
+// | (2^32 - 1 - index), 0 for a slice with no value above -inf; no winner gives 0
+__device__ __forceinline__ int32_t cpv_am_index(unsigned long long best)
+{
+    return best ? (int32_t)(0xffffffffu - (uint32_t)best) : 0;
+}
+// the softmax peak from a row's slice sums, added in slice order
+__device__ __forceinline__ float cpv_peak_of(const double* psum_row)
+{
+    double tot = 0.0;
+    for (int b = 0; b < CPV_AM_NB; b++) tot += psum_row[b];
+    return 1.0f * (float)(1.0 / tot);
+}
+
+// elements e .. e+3 (e a multiple of 4) of weight row `row` (0 <= row < n),
+// dequantized from the repacked layout (64-row tiles of U units, PIECES KiB
+// per tile and unit, a row's 16 bytes per KiB; Q6_K's f16 scales after the
+// tiles) with ggml's f32 formulas:
+//   Q8_0: q * d;  Q4_K: (d*sc)*q - (dmin*m);  Q6_K: d*sc*q, left to right.
+// The four codes of each kind sit in one dword of a 16-byte piece.
+template <int TYPE>
+__device__ __forceinline__ void cpv_dequant4(const uint8_t* data, int64_t n, int64_t U, int64_t row, int64_t e,
+                                             float* out)
+{
+    constexpr int PIECES = TYPE == CPV_Q4_K ? 9 : TYPE == CPV_Q6_K ? 13 : 17;
+    const int64_t t = row / 64, u = e / 256;
+    const int lane = (int)(row % 64), el = (int)(e % 256);
+    const uint8_t* slab = data + (t * U + u) * PIECES * 1024 + lane * 16;
+    // the dword holding block bytes idx .. idx+3 of the piece run
+    auto dword_at = [&](int idx) { return *(const uint32_t*)(slab + (idx / 16) * 1024 + idx % 16); };
+    if constexpr (TYPE == CPV_Q4_K) {
+        const uint4 meta = *(const uint4*)(slab + 8 * 1024);   // d, dmin, then 12 bytes of scales and mins
+        const uint32_t sw[3] = {meta.y, meta.z, meta.w};
+        auto s = [&](int i) { return (int)((sw[i >> 2] >> (8 * (i & 3))) & 0xffu); };
+        const int j = el / 32, l = el % 32;
+        const uint32_t codes = dword_at((j / 2) * 32 + l);
+        int sc, m;
+        if (j < 4) {
+            sc = s(j) & 63;
+            m = s(j + 4) & 63;
+        } else {
+            sc = (s(j + 4) & 0xF) | ((s(j - 4) >> 6) << 4);
+            m = (s(j + 4) >> 4) | ((s(j) >> 6) << 4);
+        }
+        const float d = cpv_h2f((uint16_t)(meta.x & 0xffffu));
+        const float dm = cpv_h2f((uint16_t)(meta.x >> 16));
+        const float d1 = d * (float)sc, m1 = dm * (float)m;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t byte = (codes >> (8 * k)) & 0xffu;
+            const int code = (j & 1) ? (int)(byte >> 4) : (int)(byte & 15);
+            out[k] = d1 * (float)code - m1;
+        }
+    } else if constexpr (TYPE == CPV_Q6_K) {
+        const int h = el / 128, l = el % 128, l32 = l % 32, quad = l / 32;
+        const uint32_t ql = dword_at(h * 64 + l32 + (quad & 1) * 32);
+        const uint32_t qh = dword_at(128 + h * 32 + l32);
+        const int8_t sc = (int8_t)slab[((192 + el / 16) / 16) * 1024 + (192 + el / 16) % 16];
+        const float d = cpv_h2f(*(const uint16_t*)(data + ((n + 63) / 64) * U * 13 * 1024 + ((t * U + u) * 64 + lane) * 2));
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t qlb = (ql >> (8 * k)) & 0xffu, qhb = (qh >> (8 * k)) & 0xffu;
+            const int lo = (quad < 2) ? (int)(qlb & 15) : (int)(qlb >> 4);
+            const int code = (lo | (int)(((qhb >> (2 * quad)) & 3) << 4)) - 32;
+            out[k] = d * (float)sc * (float)code;
+        }
+    } else {
+        const uint32_t codes = dword_at(el);
+        const float d = cpv_h2f(*(const uint16_t*)(slab + 16 * 1024 + (el / 32) * 2));
+#pragma unroll
+        for (int k = 0; k < 4; k++) out[k] = (float)(int8_t)((codes >> (8 * k)) & 0xffu) * d;
+    }
+}
+// the same for a weight type known at run time (CPV_Q8_0, CPV_Q4_K or CPV_Q6_K)
+__device__ __forceinline__ void cpv_dequant4_t(int type, const uint8_t* data, int64_t n, int64_t U, int64_t row,
+                                               int64_t e, float* out)
+{
+    if (type == CPV_Q4_K) cpv_dequant4<CPV_Q4_K>(data, n, U, row, e, out);
+    else if (type == CPV_Q6_K) cpv_dequant4<CPV_Q6_K>(data, n, U, row, e, out);
+    else cpv_dequant4<CPV_Q8_0>(data, n, U, row, e, out);
+}
 
 // Row argmax (first maximum) and the re-draft gate of each row: keep_out[r] =
 // 0 when p_min > 0 and 1 / lse < p_min, else 1, with lse the index-order f32

@@ -316,6 +316,10 @@ struct RowArgs {
     int64_t xs2;
     const float* w2;
     int nseg;
+    // SRC_CAT with psum set: the block also stores conf_out[m], the softmax
+    // peak of the previous draft link from its slice sums [T][CPV_AM_NB]
+    const double* psum;
+    float* conf_out;
 };
 
 // each block-wide reduction has its own LDS slots, so one barrier suffices
@@ -384,6 +388,9 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
     const float* wsrc = a.w ? a.w : xr;
     // SRC_CAT: a unit lies in one half (nseg is a multiple of 256)
     auto in_hi = [&](int uu) { return SRC == SRC_CAT && e0[uu] >= a.nseg; };
+    // the previous link's slice sums, one per lane of the last wave
+    const bool peak = SRC == SRC_CAT && a.psum != nullptr && wave == nw - 1;
+    const double pv = peak ? a.psum[(int64_t)m * CPV_AM_NB + lane] : 0.0;
 #pragma unroll
     for (int uu = 0; uu < RUU; uu++) {
         const float* xp = in_hi(uu) ? a.x2 + (int64_t)m * a.xs2 + (e0[uu] - a.nseg) : xr + e0[uu];
@@ -497,6 +504,12 @@ __global__ __launch_bounds__(RB) void row_kernel(RowArgs a)
             if (ok[uu])
                 *(float4*)(a.y + (int64_t)m * a.ys + e0[uu]) =
                     make_float4(v[uu * 4], v[uu * 4 + 1], v[uu * 4 + 2], v[uu * 4 + 3]);
+    }
+    if (peak) {
+        // peak_fin_kernel's sum, in slice order
+        double tot = 0.0;
+        for (int b = 0; b < CPV_AM_NB; b++) tot += __shfl(pv, b);
+        if (lane == 0) a.conf_out[m] = 1.0f * (float)(1.0 / tot);
     }
     if (!a.quant) return;
     const int64_t Kp = (int64_t)U * 256;
@@ -1239,6 +1252,7 @@ cpv_status row_launch(cpv_ctx* ctx, const RowArgs& a, int T)
         if (a.src == SRC_CAT && (a.nseg % 256 || a.n != 2 * a.nseg || !a.w || !a.w2 || !al(a.w2) || !a.x2 ||
                                  !al(a.x2) || a.xs2 % 4))
             return cpv_fail(ctx, CPV_EUNSUPPORTED, "row kernel: halves of %d need whole units and both weights", a.nseg);
+        if (a.src == SRC_CAT && a.psum && !a.conf_out) return cpv_fail(ctx, CPV_EINVAL, "row kernel: a peak needs its output");
     }
     // row_kernel: the fewest units per wave that 16 waves cover, and the waves that many units need
     const int U = (a.n + 255) / 256, nu = (U + RW - 1) / RW, nt = 64 * ((U + nu - 1) / nu);
@@ -1766,22 +1780,32 @@ cpv_status round_body(cpv_session* s, int t, int depth, const float* noise_dev, 
     cpv_gout hk;
     if ((st = norm_head(s, s->x, t, pend.acc ? &pend : nullptr, m->output_norm, s->h, m->output, s->logits, &hk)))
         return st;
-    if ((st = cpv_argmax_peak_rows(ctx, s->logits, noise_dev, t, V, s->preds, nullptr, hk.acc ? &hk : nullptr)))
+    // with a draft chain, the argmax's last pass also writes the winners'
+    // embedding rows for link 0 (each link's peak pass those for the next
+    // one), and with the chain in row kernels each link's peak but the last
+    // is finished by the next link's row kernel
+    const bool cat = depth > 0 && 2 * E <= (int64_t)RQ * RB && E % 256 == 0;
+    cpv_am_fin pfin{};
+    if ((st = cpv_argmax_peak_rows(ctx, s->logits, noise_dev, t, V, s->preds, nullptr, hk.acc ? &hk : nullptr,
+                                   nullptr, depth > 0 ? m->mtp_embed : nullptr, s->e)))
         return st;
     // fused MTP draft chain (qwen35.rs:2840-2962)
     if (depth > 0) {
         const LayerW& ML = m->layers[hp.n_layer];
         const float* h_src = s->h;
-        const int32_t* tok_src = s->preds;
         for (int step = 0; step < depth; step++) {
-            if ((st = cpv_get_rows(ctx, m->mtp_embed, tok_src, t, s->e))) return st;
             cpv_act act;
-            if (2 * E <= (int64_t)RQ * RB && E % 256 == 0) {
-                // concat(enorm(e), hnorm(h)) normalized and quantized in one row kernel
+            if (cat) {
+                // concat(enorm(e), hnorm(h)) normalized and quantized in one row
+                // kernel, which also finishes the previous link's peak
                 RowArgs rc{};
                 rc.src = SRC_CAT;
                 rc.x = s->e;
                 rc.xs = E;
+                if (step > 0) {
+                    rc.psum = pfin.psum;
+                    rc.conf_out = s->conf + (size_t)(step - 1) * t;
+                }
                 rc.x2 = h_src;
                 rc.xs2 = E;
                 rc.nseg = (int)E;
@@ -1812,20 +1836,22 @@ cpv_status round_body(cpv_session* s, int t, int depth, const float* noise_dev, 
                                 shortlist ? s->cand_head : m->mtp_head, s->mtp_logits, &mk)))
                 return st;
             int32_t* ids = s->chain + (size_t)step * t;
+            const bool more = step + 1 < depth;
             if ((st = cpv_argmax_peak_rows(ctx, s->mtp_logits, nullptr, t, shortlist ? n_cand : V,
                                            shortlist ? s->cand_idx : ids, s->conf + (size_t)step * t,
-                                           mk.acc ? &mk : nullptr)))
+                                           mk.acc ? &mk : nullptr, cat && more ? &pfin : nullptr,
+                                           more ? m->mtp_embed : nullptr, s->e)))
                 return st;
             if (shortlist) {
-                // drafts are candidates; the next link embeds the argmax itself, as the
+                // drafts are candidates; the next link embeds the argmax itself (the
+                // index into the shortlist, embedded by the peak pass above), as the
                 // graph does (tok_src = ids, qwen35.rs:2958; the ids map back on the host, :1904-1910)
                 map_cands_kernel<<<(unsigned)((t + 255) / 256), 256, 0, ctx->stream>>>(s->cand_idx, s->cand_dev, t, ids);
                 CPV_HIP(ctx, hipGetLastError());
             }
-            // the next link feeds on this link's prediction and hidden (read by its
-            // hnorm before its own head overwrites hn)
+            // the next link feeds on this link's prediction (its embedding in e) and
+            // hidden (read by its hnorm before its own head overwrites hn)
             h_src = s->hn;
-            tok_src = shortlist ? s->cand_idx : ids;
         }
     }
     return CPV_OK;
