@@ -173,16 +173,21 @@ def test_qgemm_rejects_bad_shapes(ctx):
         ctx.upload_weight(cpvo.Q4_K, np.zeros(144, np.uint8), 1, 100)
 
 
-@pytest.mark.parametrize("tname", list(TYPES))
-def test_get_rows_matches_ggml_dequant(ctx, tname):
+@pytest.mark.parametrize("tname,k", [(t, k) for t in TYPES for k in (512, 5120)] + [("q8_0", 800)])
+def test_get_rows_matches_ggml_dequant(ctx, tname, k):
+    # four elements per thread; 800 = 25 Q8_0 blocks (a partial 256-element
+    # unit); ids outside the table give zero rows
     t = TYPES[tname]
-    n, k = 300, 512
+    n = 300
     wq = weights(t, n, k)
     w = ctx.upload_weight(t, wq, n, k)
-    rows = torch.tensor([0, 7, 299, 150, 7], dtype=torch.int32, device="cuda")
+    ids = [0, 7, 299, 150, 7, 64, 63]
+    rows = torch.tensor(ids + [-1, n], dtype=torch.int32, device="cuda")
     got = ctx.get_rows(w, rows).cpu().numpy()
-    ref = cpvo.dequantize(t, wq, k)[[0, 7, 299, 150, 7]]
-    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    w.free()
+    ref = cpvo.dequantize(t, wq, k)[ids]
+    assert np.array_equal(got[:len(ids)].view(np.uint32), ref.view(np.uint32))
+    assert not got[len(ids):].any()
 
 
 def test_argmax_first_maximum_and_noise(ctx):
