@@ -744,9 +744,9 @@ __global__ __launch_bounds__(64) void argmax_fin_kernel(const unsigned long long
     if (threadIdx.x == 0) out[row] = cpv_am_index(v);
 }
 
-// An embedding table whose rows of the argmax winners a draft chain's next
-// link takes (data null: none): the blocks of a row write row tok of it to
-// out[row], four elements per thread, as get_rows_kernel does
+// The embedding table of a draft chain's next link (data null: none): the
+// blocks of a row write the table's row tok, the row's argmax, to out[row],
+// four elements per thread, as get_rows_kernel does
 struct EmbArgs {
     const uint8_t* data;
     int type;
