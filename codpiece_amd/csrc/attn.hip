@@ -587,11 +587,23 @@ __global__ __launch_bounds__(CT) void attn_chunk_kernel(ChunkArgs a)
         for (int i = 0; i < 4; i++) {
             const int lr = blockIdx.z * QB + rb * 16 + 4 * g4 + i;
             if (lr >= LR) break;
-            int64_t S = 0;
+            float pc;
+            if (!vtop[0] && !vtop[1]) {
+                // (wave-uniform) no top value limb: |vq| < 2^23, so |S| < 2^22 2^23
+                // 128 < 2^52 and every step of the limb sum below is exact in
+                // binary64; one rounding to f32, as from the int64 sum
+                double Sd = (double)acc[PL + VLIMBS - 3][i];
 #pragma unroll
-            for (int q = 0; q < PL + VLIMBS - 1; q++) S += (int64_t)acc[q][i] * ((int64_t)1 << (8 * q));
+                for (int q = PL + VLIMBS - 4; q >= 0; q--) Sd = __builtin_fma(Sd, 256.0, (double)acc[q][i]);
+                pc = (float)Sd;
+            } else {
+                int64_t S = 0;
+#pragma unroll
+                for (int q = 0; q < PL + VLIMBS - 1; q++) S += (int64_t)acc[q][i] * ((int64_t)1 << (8 * q));
+                pc = (float)S;
+            }
             a.P[(int64_t)c * a.p_cs + (int64_t)s_orow[rb * 16 + 4 * g4 + i] * a.p_rs + dcol] =
-                ldexpf((float)S, -(PBITS + VBITS));
+                ldexpf(pc, -(PBITS + VBITS));
         }
     }
 }
