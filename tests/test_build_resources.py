@@ -77,3 +77,18 @@ def test_no_spills_or_unexpected_scratch():
         if spill > SPILL_OK.get(name, 0) or scratch > SCRATCH_OK.get(name, 0):
             bad.append((kd[".name"], spill, scratch, kd.get(".vgpr_count")))
     assert not bad, bad
+
+
+# kernels whose speed rests on two 512-thread workgroups sharing a CU: at most
+# 128 VGPRs (4 waves per SIMD in a 512-entry register file).  Packing the
+# attention's per-row metadata into one 16-byte LDS word once took the 80-row
+# block to 140 VGPRs, one workgroup per CU, and the 16-node tree at 32768
+# from 126 to 164 us, every parity test still green.
+TWO_PER_CU = ("attn_chunk_kernel",)
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="libcpv.so not built")
+def test_two_workgroups_per_cu_fit():
+    over = [(kd[".name"], kd.get(".vgpr_count")) for kd in kernels()
+            if any(k in kd[".name"] for k in TWO_PER_CU) and kd.get(".vgpr_count", 0) > 128]
+    assert not over, over
